@@ -1,0 +1,74 @@
+/*
+ * liboctex_amd.so entry points beyond the reference's cuvsOctex* C ABI.  None of them has a
+ * counterpart in the reference's C ABI:
+ *   - introspection of a search (the reference exposes the same to its bench and tests through the
+ *     C++-only detail::timed_batch / resident_search / memory_report, introspect.hpp:41-60);
+ *   - the stage entry points: one HIP kernel each, on caller-provided device buffers, so that the
+ *     parity tests call every kernel of the search path with controlled inputs (as the reference's
+ *     cpp/tests/test_search.cu launches its kernels directly).
+ * All return CUVS_SUCCESS / CUVS_ERROR with cuvsGetLastErrorText() set; `stream` is a hipStream_t
+ * (NULL: the null stream); the stage calls wait for their kernel before returning.
+ */
+#pragma once
+
+#include <cuvs/core/c_api.h>
+#include <cuvs/neighbors/octex.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/** Copy a buffer of the index's cached search plan ("queries", "Y", "qs", "seg", "cand", "dist",
+ * "nin", "si", "sd", "done", "seg2", "cand2", "dist2", "n2", "bi", "bd") to dst (host or device),
+ * at most `bytes`; *size receives the buffer's size.  The buffers hold the last batch searched. */
+cuvsError_t octexIndexCopyPlanBuffer(cuvsOctexIndex_t index, const char* name, void* dst, int64_t bytes,
+                                     int64_t* size);
+
+/** The cached plan's shape: {m, k, KO, lr, W, W2, rerank, wave_rerank, final_rerank, graph?}. */
+cuvsError_t octexIndexPlanInfo(cuvsOctexIndex_t index, int32_t* info);
+
+/* ---- stage entry points (fp16 arrays as raw 16-bit words) ---- */
+
+/** qc = q - mu, qh = fp16(qc) (search_kernels.cuh:57-69). */
+cuvsError_t octexStageCenter(const float* q, const float* mu, int64_t m, int32_t D, float* qc, void* qh,
+                             void* stream);
+/** Y [m, N] = qh [m, K] @ ucatT [N, K]^T + shift [N], fp16 (search.cu:305-320). */
+cuvsError_t octexStageProject(const void* qh, const void* ucatT, const void* shift, int32_t m, int32_t K,
+                              int32_t N, void* Y, void* stream);
+/** qs [m, S] = qc [m, D] @ basis [D, S] (search.cu:323-341, fp32). */
+cuvsError_t octexStageSketchQuery(const float* qc, const float* basis, int32_t m, int32_t D, int32_t S,
+                                  float* qs, void* stream);
+/** E8^b points p [n, 8b] and hashes h [n] of y [n, 8b] * inv_f (e8.cuh:44-85). */
+cuvsError_t octexStageE8(const float* y, int64_t n, int32_t b, float inv_f, float* p, int64_t* h,
+                         void* stream);
+/** probe_kernel (search_kernels.cuh:84-127): seg [m, C, 2]. */
+cuvsError_t octexStageProbe(const void* Y, int32_t m, int32_t C, int32_t L, int32_t B, const float* inv_f,
+                            const int32_t* off, int64_t T1, const int64_t* keys, int64_t Mmax,
+                            const int32_t* base, int32_t l, int32_t lr, int32_t logT, int32_t* seg,
+                            void* stream);
+/** gather_kernel (search_kernels.cuh:138-253): rows = 0 lists, 1 table rows; W a power of two. */
+cuvsError_t octexStageGather(int32_t rows, const int32_t* seg, int32_t nseg, int32_t m, const int32_t* lists,
+                             int64_t stride, const int32_t* table, int32_t table_len, const int8_t* code,
+                             const float* scale, const float* qs, int32_t S, int32_t W, int32_t* cand,
+                             float* dist, int32_t* nout, void* stream);
+/** rerank_keep_kernel (search_kernels.cuh:421-467). */
+cuvsError_t octexStageRerankKeep(const int32_t* cand, const float* dist, const int32_t* nin, int32_t m,
+                                 int32_t W, const void* vectors, int32_t D, const float* Q, int32_t R,
+                                 int32_t KO, int64_t* si, float* sd, int32_t fresh, void* stream);
+/** sketch_keep_kernel (search_kernels.cuh:471-508). */
+cuvsError_t octexStageSketchKeep(const int32_t* cand, const float* dist, const int32_t* nin, int32_t m,
+                                 int32_t W, int32_t KO, int64_t* si, float* sd, int32_t fresh, void* stream);
+/** pick_starts_kernel (search_kernels.cuh:571-631). */
+cuvsError_t octexStagePickStarts(const int64_t* si, int32_t m, int32_t KO, int64_t* done, int32_t E,
+                                 int32_t off, int32_t S, int32_t rowlen, int32_t* seg2, void* stream);
+/** final_rerank_kernel (search_kernels.cuh:634-669). */
+cuvsError_t octexStageFinalRerank(const int64_t* si, int32_t m, int32_t KO, int32_t R, const void* vectors,
+                                  int32_t D, const float* Q, int32_t k, int64_t* bi, float* bd, void* stream);
+/** take_k_kernel (search_kernels.cuh:672-685). */
+cuvsError_t octexStageTakeK(const int64_t* si, const float* sd, int32_t m, int32_t KO, int32_t k, int64_t* bi,
+                            float* bd, void* stream);
+
+#ifdef __cplusplus
+}
+#endif

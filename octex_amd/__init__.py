@@ -1,0 +1,12 @@
+"""octex for MI355X: approximate k-nearest-neighbor search by E8-lattice cell lists (cuvs::neighbors::octex),
+with every search step a hand-written HIP kernel for gfx950.
+
+    import octex_amd as octex
+    index = octex.load("index_dir")        # or octex.build(xb, "index_dir")
+    D, I = index.search(xq, k=10)          # (distances, neighbors), nearest first
+"""
+
+from .index import Index, build, load
+
+__version__ = "0.1.0"
+__all__ = ["Index", "build", "load", "__version__"]

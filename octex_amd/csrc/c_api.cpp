@@ -1,0 +1,427 @@
+// The cuvsOctex* C ABI (the reference: c/src/neighbors/octex.cpp:31-333) and the subset of the cuVS
+// core C API it needs (resources, stream, last error text; c/src/core/exceptions.hpp:17-33), on
+// DLPack tensors in HIP device memory (kDLROCM) or host memory (kDLCPU, kDLROCMHost).
+
+#include "common.hpp"
+#include "index_impl.hpp"
+#include "search.hpp"
+
+#include <cuvs/core/c_api.h>
+#include <cuvs/neighbors/octex.h>
+#include <cuvs/neighbors/octex.hpp>
+#include <octex_amd/octex_amd.h>
+
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <exception>
+#include <string>
+#include <type_traits>
+#include <vector>
+
+namespace {
+
+namespace octex = cuvs::neighbors::octex;
+
+thread_local std::string g_last_error;
+
+template <typename Fn>
+auto translate_exceptions(Fn func) -> cuvsError_t
+{
+  try {
+    func();
+    cuvsSetLastErrorText(nullptr);
+    return CUVS_SUCCESS;
+  } catch (std::exception const& e) {
+    cuvsSetLastErrorText(e.what());
+  } catch (...) {
+    cuvsSetLastErrorText("unknown exception");
+  }
+  return CUVS_ERROR;
+}
+
+auto as_res(cuvsResources_t res) -> raft::resources*
+{
+  OCTEX_EXPECTS(res != 0, "octex: the resources handle is NULL");
+  return reinterpret_cast<raft::resources*>(res);
+}
+
+auto to_cpp(cuvsOctexIndexParams const& p) -> octex::index_params
+{
+  octex::index_params out;
+  out.copies   = p.copies;
+  out.blocks   = p.blocks;
+  out.pca_dims = p.pca_dims;
+  if (p.spacings != nullptr && p.n_spacings > 0) out.spacings.assign(p.spacings, p.spacings + p.n_spacings);
+  out.list_len           = p.list_len;
+  out.min_cell           = p.min_cell;
+  out.log_buckets        = p.log_buckets;
+  out.sketch_width       = p.sketch_width;
+  out.table_len          = p.table_len;
+  out.reverse_edges      = p.reverse_edges;
+  out.exact_lists        = p.exact_lists;
+  out.list_probes        = p.list_probes;
+  out.member_lists       = p.member_lists;
+  out.exact_table_max    = p.exact_table_max;
+  out.table_passes       = p.table_passes;
+  out.table_sketch_order = p.table_sketch_order;
+  out.write_behind       = p.write_behind;
+  out.seed               = p.seed;
+  if (p.devices != nullptr && p.n_devices > 0) out.devices.assign(p.devices, p.devices + p.n_devices);
+  return out;
+}
+
+auto to_cpp(cuvsOctexLoadParams const& p) -> octex::load_params
+{
+  OCTEX_EXPECTS(p.placement == OCTEX_PLACEMENT_REPLICATE || p.placement == OCTEX_PLACEMENT_SHARD,
+                "octex: unknown placement");
+  OCTEX_EXPECTS(p.sketch == OCTEX_SKETCH_REPLICATE || p.sketch == OCTEX_SKETCH_SHARD ||
+                  p.sketch == OCTEX_SKETCH_HOST,
+                "octex: unknown sketch placement");
+  octex::load_params out;
+  if (p.devices != nullptr && p.n_devices > 0) out.devices.assign(p.devices, p.devices + p.n_devices);
+  out.mode            = static_cast<octex::placement>(static_cast<int>(p.placement));
+  out.vectors_on_host = p.vectors_on_host;
+  out.shard_vectors   = p.shard_vectors;
+  out.table_on_host   = p.table_on_host;
+  out.sketch          = static_cast<octex::sketch_placement>(static_cast<int>(p.sketch));
+  out.parts           = p.parts;
+  out.copies_per_part = p.copies_per_part;
+  out.copies_limit    = p.copies_limit;
+  out.list_limit      = p.list_limit;
+  return out;
+}
+
+auto to_cpp(cuvsOctexSearchParams const& p) -> octex::search_params
+{
+  octex::search_params out;
+  out.read            = p.read;
+  out.starts          = p.starts;
+  out.waves           = p.waves;
+  out.rerank          = p.rerank;
+  out.wave_rerank     = p.wave_rerank;
+  out.batch           = p.batch;
+  out.sketch_rank     = p.sketch_rank;
+  out.final_rerank    = p.final_rerank;
+  out.balanced_gather = p.balanced_gather;
+  out.fused_merge     = p.fused_merge;
+  out.use_graph       = p.use_graph;
+  return out;
+}
+
+auto as_index(cuvsOctexIndex const& index) -> octex::index*
+{
+  OCTEX_EXPECTS(index.addr != 0, "octex: the index is empty (load it first)");
+  return reinterpret_cast<octex::index*>(index.addr);
+}
+
+// ---- DLPack tensors (the reference: c/src/core/interop.hpp:25-97)
+
+auto host_compatible(DLTensor const& t) -> bool
+{
+  return t.device.device_type == kDLCPU || t.device.device_type == kDLROCMHost;
+}
+auto device_compatible(DLTensor const& t) -> bool
+{
+  return t.device.device_type == kDLROCM || t.device.device_type == kDLROCMHost;
+}
+
+template <typename T>
+auto dl_code() -> uint8_t
+{
+  if constexpr (std::is_floating_point_v<T> || std::is_same_v<T, __half>) return kDLFloat;
+  if constexpr (std::is_signed_v<T>) return kDLInt;
+  return kDLUInt;
+}
+
+template <typename T>
+auto dl_matrix(DLManagedTensor* m, bool device) -> T*
+{
+  OCTEX_EXPECTS(m != nullptr, "octex: a DLPack tensor is NULL");
+  DLTensor const& t = m->dl_tensor;
+  if (device)
+    OCTEX_EXPECTS(device_compatible(t), "octex: expected a tensor in device memory");
+  else
+    OCTEX_EXPECTS(host_compatible(t), "octex: expected a tensor in host memory");
+  OCTEX_EXPECTS(t.ndim == 2, "octex: the DLPack tensor has the wrong number of dimensions");
+  OCTEX_EXPECTS(t.dtype.code == dl_code<T>() && t.dtype.bits == 8 * sizeof(T) && t.dtype.lanes == 1,
+                "octex: the DLPack tensor has the wrong data type");
+  if (t.strides != nullptr) {
+    int64_t expect = 1;
+    for (int i = t.ndim - 1; i >= 0; --i) {
+      OCTEX_EXPECTS(t.shape[i] == 1 || t.strides[i] == expect, "octex: the DLPack tensor must be dense and row major");
+      expect *= t.shape[i];
+    }
+  }
+  return reinterpret_cast<T*>(static_cast<char*>(t.data) + t.byte_offset);
+}
+
+}  // namespace
+
+// ==================================================================== cuVS core
+
+extern "C" cuvsError_t cuvsResourcesCreate(cuvsResources_t* res)
+{
+  return translate_exceptions([=] {
+    OCTEX_EXPECTS(res != nullptr, "octex: NULL output pointer");
+    *res = reinterpret_cast<cuvsResources_t>(new raft::resources());
+  });
+}
+
+extern "C" cuvsError_t cuvsResourcesDestroy(cuvsResources_t res)
+{
+  return translate_exceptions([=] { delete reinterpret_cast<raft::resources*>(res); });
+}
+
+extern "C" cuvsError_t cuvsStreamSet(cuvsResources_t res, void* stream)
+{
+  return translate_exceptions([=] { as_res(res)->set_stream(static_cast<hipStream_t>(stream)); });
+}
+
+extern "C" cuvsError_t cuvsStreamGet(cuvsResources_t res, void** stream)
+{
+  return translate_exceptions([=] { *stream = static_cast<void*>(as_res(res)->get_stream()); });
+}
+
+extern "C" cuvsError_t cuvsStreamSync(cuvsResources_t res)
+{
+  return translate_exceptions([=] { OCTEX_HIP(hipStreamSynchronize(as_res(res)->get_stream())); });
+}
+
+extern "C" const char* cuvsGetLastErrorText(void) { return g_last_error.c_str(); }
+
+extern "C" void cuvsSetLastErrorText(const char* error) { g_last_error = error != nullptr ? error : ""; }
+
+// ==================================================================== cuvsOctex*
+
+extern "C" cuvsError_t cuvsOctexIndexParamsCreate(cuvsOctexIndexParams_t* params)
+{
+  return translate_exceptions([=] {
+    octex::index_params d;
+    *params = new cuvsOctexIndexParams{d.copies,        d.blocks,          d.pca_dims,     nullptr,
+                                       0,               d.list_len,        d.min_cell,     d.log_buckets,
+                                       d.sketch_width,  d.table_len,       d.reverse_edges, d.exact_lists,
+                                       d.list_probes,   d.member_lists,    d.exact_table_max,
+                                       d.table_passes,  d.table_sketch_order, d.write_behind, d.seed,
+                                       nullptr,         0};
+  });
+}
+
+extern "C" cuvsError_t cuvsOctexIndexParamsDestroy(cuvsOctexIndexParams_t params)
+{
+  return translate_exceptions([=] { delete params; });
+}
+
+extern "C" cuvsError_t cuvsOctexLoadParamsCreate(cuvsOctexLoadParams_t* params)
+{
+  return translate_exceptions([=] {
+    octex::load_params d;
+    *params = new cuvsOctexLoadParams{nullptr,
+                                      0,
+                                      static_cast<cuvsOctexPlacement>(static_cast<int>(d.mode)),
+                                      d.vectors_on_host,
+                                      d.shard_vectors,
+                                      d.table_on_host,
+                                      static_cast<cuvsOctexSketchPlacement>(static_cast<int>(d.sketch)),
+                                      d.parts,
+                                      d.copies_per_part,
+                                      d.copies_limit,
+                                      d.list_limit};
+  });
+}
+
+extern "C" cuvsError_t cuvsOctexLoadParamsDestroy(cuvsOctexLoadParams_t params)
+{
+  return translate_exceptions([=] { delete params; });
+}
+
+extern "C" cuvsError_t cuvsOctexSearchParamsCreate(cuvsOctexSearchParams_t* params)
+{
+  return translate_exceptions([=] {
+    octex::search_params d;
+    *params = new cuvsOctexSearchParams{d.read,        d.starts,       d.waves,           d.rerank,
+                                        d.wave_rerank, d.batch,        d.sketch_rank,     d.final_rerank,
+                                        d.balanced_gather, d.fused_merge, d.use_graph};
+  });
+}
+
+extern "C" cuvsError_t cuvsOctexSearchParamsDestroy(cuvsOctexSearchParams_t params)
+{
+  return translate_exceptions([=] { delete params; });
+}
+
+extern "C" cuvsError_t cuvsOctexIndexCreate(cuvsOctexIndex_t* index)
+{
+  return translate_exceptions([=] { *index = new cuvsOctexIndex{}; });
+}
+
+extern "C" cuvsError_t cuvsOctexIndexDestroy(cuvsOctexIndex_t index)
+{
+  return translate_exceptions([=] {
+    if (index == nullptr) return;
+    if (index->addr != 0) delete reinterpret_cast<octex::index*>(index->addr);
+    delete index;
+  });
+}
+
+extern "C" cuvsError_t cuvsOctexIndexGetSize(cuvsOctexIndex_t index, int64_t* size)
+{
+  return translate_exceptions([=] { *size = as_index(*index)->size(); });
+}
+
+extern "C" cuvsError_t cuvsOctexIndexGetDim(cuvsOctexIndex_t index, int64_t* dim)
+{
+  return translate_exceptions([=] { *dim = as_index(*index)->dim(); });
+}
+
+extern "C" cuvsError_t cuvsOctexIndexGetCopies(cuvsOctexIndex_t index, int32_t* copies)
+{
+  return translate_exceptions([=] { *copies = as_index(*index)->copies(); });
+}
+
+extern "C" cuvsError_t cuvsOctexIndexGetNumDevices(cuvsOctexIndex_t index, int32_t* n_devices)
+{
+  return translate_exceptions(
+    [=] { *n_devices = static_cast<int32_t>(as_index(*index)->devices().size()); });
+}
+
+extern "C" cuvsError_t cuvsOctexIndexGetDevices(cuvsOctexIndex_t index, int32_t* devices)
+{
+  return translate_exceptions([=] {
+    auto const& d = as_index(*index)->devices();
+    for (size_t i = 0; i < d.size(); ++i)
+      devices[i] = d[i];
+  });
+}
+
+extern "C" cuvsError_t cuvsOctexIndexGetDeviceBytes(cuvsOctexIndex_t index, int64_t* bytes)
+{
+  return translate_exceptions([=] {
+    auto b = as_index(*index)->device_bytes();
+    for (size_t i = 0; i < b.size(); ++i)
+      bytes[i] = b[i];
+  });
+}
+
+extern "C" cuvsError_t cuvsOctexBuild(cuvsResources_t res, cuvsOctexIndexParams_t params,
+                                      DLManagedTensor* dataset, const char* path)
+{
+  return translate_exceptions([=] {
+    OCTEX_EXPECTS(path != nullptr, "octex: the index directory is NULL");
+    OCTEX_EXPECTS(params != nullptr && dataset != nullptr, "octex: NULL parameters or dataset");
+    auto* r           = as_res(res);
+    const auto p      = to_cpp(*params);
+    auto const& t     = dataset->dl_tensor;
+    const bool dev    = t.device.device_type == kDLROCM;
+    const std::string dir(path);
+    auto run = [&](auto tag) {
+      using T    = decltype(tag);
+      T* data    = dl_matrix<T>(dataset, dev);
+      int64_t n  = t.shape[0], d = t.shape[1];
+      std::vector<T> host;
+      if (dev) {  // the build reads the dataset from the host
+        host.resize(static_cast<size_t>(n * d));
+        OCTEX_HIP(hipMemcpy(host.data(), data, sizeof(T) * host.size(), hipMemcpyDefault));
+        data = host.data();
+      }
+      octex::build(*r, p, raft::host_matrix_view<const T, int64_t, raft::row_major>(data, n, d), dir);
+    };
+    if (t.dtype.code == kDLFloat && t.dtype.bits == 32)
+      run(float{});
+    else if (t.dtype.code == kDLFloat && t.dtype.bits == 16)
+      run(__half{});
+    else
+      octex::detail::fail("octex: the dataset must be float32 or float16");
+  });
+}
+
+extern "C" cuvsError_t cuvsOctexLoad(cuvsResources_t res, const char* path, cuvsOctexLoadParams_t params,
+                                     cuvsOctexIndex_t index)
+{
+  return translate_exceptions([=] {
+    OCTEX_EXPECTS(index != nullptr, "octex: the index handle is NULL");
+    OCTEX_EXPECTS(index->addr == 0, "octex: the index handle already holds an index");
+    OCTEX_EXPECTS(path != nullptr, "octex: the index directory is NULL");
+    auto* r      = as_res(res);
+    const auto p = params != nullptr ? to_cpp(*params) : octex::load_params{};
+    index->addr  = reinterpret_cast<uintptr_t>(new octex::index(octex::load(*r, std::string(path), p)));
+  });
+}
+
+extern "C" cuvsError_t cuvsOctexSearch(cuvsResources_t res, cuvsOctexSearchParams_t params,
+                                       cuvsOctexIndex_t index, DLManagedTensor* queries,
+                                       DLManagedTensor* neighbors, DLManagedTensor* distances)
+{
+  return translate_exceptions([=] {
+    auto* r        = as_res(res);
+    OCTEX_EXPECTS(params != nullptr, "octex: the search parameters are NULL");
+    const auto p   = to_cpp(*params);
+    auto const& ix = *as_index(*index);
+    OCTEX_EXPECTS(queries != nullptr && neighbors != nullptr && distances != nullptr, "octex: NULL tensor");
+    const bool dev = queries->dl_tensor.device.device_type == kDLROCM;
+    auto* q        = dl_matrix<float>(queries, dev);
+    auto* nb       = dl_matrix<int64_t>(neighbors, dev);
+    auto* ds       = dl_matrix<float>(distances, dev);
+    const auto& qt = queries->dl_tensor;
+    const auto& nt = neighbors->dl_tensor;
+    const auto& dt = distances->dl_tensor;
+    OCTEX_EXPECTS(nt.shape[0] == qt.shape[0] && dt.shape[0] == qt.shape[0] && dt.shape[1] == nt.shape[1],
+                  "octex: output shapes");
+    octex::detail::search_impl(*r, p, ix, q, qt.shape[0], qt.shape[1], nb, ds, nt.shape[1], !dev, false);
+  });
+}
+
+// ==================================================================== introspection (octex_amd.h)
+
+extern "C" cuvsError_t octexIndexCopyPlanBuffer(cuvsOctexIndex_t index, const char* name, void* dst,
+                                                int64_t bytes, int64_t* size)
+{
+  return translate_exceptions([=] {
+    auto& ix = as_index(*index)->impl();
+    std::shared_ptr<octex::detail::plan> pl;
+    {
+      std::lock_guard<std::mutex> lock(ix.mu);
+      OCTEX_EXPECTS(!ix.plans.empty(), "octex: no search ran on this index yet");
+      pl = ix.plans.begin()->second;
+    }
+    std::string n(name != nullptr ? name : "");
+    octex::detail::dbuf const* b = nullptr;
+    if (n == "queries") b = &pl->qbuf;
+    else if (n == "qc") b = &pl->qc;
+    else if (n == "qh") b = &pl->qh;
+    else if (n == "Y") b = &pl->Y;
+    else if (n == "qs") b = &pl->qs;
+    else if (n == "seg") b = &pl->seg;
+    else if (n == "cand") b = &pl->cand;
+    else if (n == "dist") b = &pl->dist;
+    else if (n == "nin") b = &pl->nin;
+    else if (n == "si") b = &pl->si;
+    else if (n == "sd") b = &pl->sd;
+    else if (n == "done") b = &pl->done;
+    else if (n == "seg2") b = &pl->seg2;
+    else if (n == "cand2") b = &pl->cand2;
+    else if (n == "dist2") b = &pl->dist2;
+    else if (n == "n2") b = &pl->n2;
+    else if (n == "bi") b = &pl->bi;
+    else if (n == "bd") b = &pl->bd;
+    else octex::detail::fail("octex: unknown plan buffer %s", n.c_str());
+    if (size != nullptr) *size = static_cast<int64_t>(b->size);
+    if (dst != nullptr && bytes > 0) {
+      OCTEX_HIP(hipSetDevice(ix.device));
+      OCTEX_HIP(hipStreamSynchronize(ix.stream));
+      OCTEX_HIP(hipMemcpy(dst, b->ptr, std::min<size_t>(b->size, static_cast<size_t>(bytes)), hipMemcpyDefault));
+    }
+  });
+}
+
+extern "C" cuvsError_t octexIndexPlanInfo(cuvsOctexIndex_t index, int32_t* info)
+{
+  return translate_exceptions([=] {
+    auto& ix = as_index(*index)->impl();
+    std::lock_guard<std::mutex> lock(ix.mu);
+    OCTEX_EXPECTS(!ix.plans.empty(), "octex: no search ran on this index yet");
+    auto const& pl = *ix.plans.begin()->second;
+    int32_t v[] = {pl.m, pl.k, pl.KO, pl.lr, pl.W, pl.W2, pl.R1, pl.R2, pl.FR, pl.graph != nullptr ? 1 : 0};
+    std::memcpy(info, v, sizeof(v));
+  });
+}

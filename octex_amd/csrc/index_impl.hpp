@@ -1,0 +1,75 @@
+// State of a loaded octex index on one MI355X (the reference's index_impl + device_part,
+// detail/index_impl.hpp:115-177, for a single device).
+//
+// HBM layout (one allocation per array):
+//   lists    i32 [C, stride]        cell lists of all levels of every copy (stride = rows * l)
+//   keys     i64 [C, L, mmax]       cell ids per (copy, level) in (bucket, id) order
+//   offsets  i32 [C, L, 2^logT + 1] CSR of the buckets into keys
+//   base     i32 [C, L]             first cell row of every level
+//   ucatT    f16 [C * 8b, D]        projections of all copies, one row per projected coordinate
+//                                   (the transpose of the reference's ucat [D, C * 8b]) so that the
+//                                   MFMA A-operand loads are contiguous
+//   shift    f16 [C * 8b], inv_f f32 [L], mean f32 [D], basis f32 [D, S], scale f32 [S]
+//   sketch   i8  [N, S]             (or pinned host memory)
+//   vectors  f16 [N, D]             (or pinned host memory)
+//   table    i32 [N, table_len]     (or pinned host memory)
+#pragma once
+
+#include "common.hpp"
+
+#include <cuvs/neighbors/octex.hpp>
+
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+namespace cuvs::neighbors::octex::detail {
+
+struct plan;  // buffers and graph of one (batch, k, search parameters); search.cpp
+
+struct index_impl {
+  // meta.json
+  int64_t n = 0, dim = 0;
+  int copies = 0, blocks = 4, list_len = 0, log_buckets = 20, sketch_width = 0, table_len = 0;
+  std::vector<float> spacings;
+  std::string path;
+
+  load_params params;
+  std::vector<int> devices;  // the one GPU holding the index
+  int device         = 0;
+  hipStream_t stream = nullptr;
+
+  dbuf lists, keys, offsets, base, ucatT, shift, inv_f, mean, basis, scale;
+  dbuf sketch, vectors, table;
+  hbuf host_sketch, host_vectors, host_table;
+  int64_t stride = 0, mmax = 0, T1 = 0;
+  int64_t bytes  = 0;  // device bytes of the arrays
+
+  [[nodiscard]] auto levels() const -> int { return static_cast<int>(spacings.size()); }
+  [[nodiscard]] auto code() const -> const signed char*
+  {
+    return host_sketch.ptr != nullptr ? static_cast<const signed char*>(host_sketch.dptr)
+                                      : sketch.as<const signed char>();
+  }
+  [[nodiscard]] auto vecs() const -> const __half*
+  {
+    return host_vectors.ptr != nullptr ? static_cast<const __half*>(host_vectors.dptr)
+                                       : vectors.as<const __half>();
+  }
+  [[nodiscard]] auto rows() const -> const int*
+  {
+    return host_table.ptr != nullptr ? static_cast<const int*>(host_table.dptr) : table.as<const int>();
+  }
+
+  std::mutex mu;
+  std::map<std::string, std::shared_ptr<plan>> plans;
+
+  index_impl() = default;
+  index_impl(index_impl const&) = delete;
+  ~index_impl();
+};
+
+}  // namespace cuvs::neighbors::octex::detail

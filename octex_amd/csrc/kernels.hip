@@ -1,0 +1,1016 @@
+// octex search kernels for MI355X (gfx950, wave64).  One workgroup per query for every per-query
+// step, as the reference's kernels (cpp/src/neighbors/octex/detail/search_kernels.cuh), written for
+// 64-lane wavefronts: wave-aggregated LDS appends (ballot / popcount), 64-lane scans and butterflies.
+//
+// Arithmetic pins shared with the CPU oracle: E8 distances t = x - a, acc = fma(t, t, acc); the
+// sketch score u = fma(code, scale, -qs), d = fma(u, u, d) over Lr-lane chunks then an xor butterfly;
+// the exact distance over 64 lanes (pairs l, l + 64, ...), acc = fma(a, a, acc), fma(b, b, acc), then
+// an xor butterfly; selections by (distance bits, id).  Built with -ffp-contract=off so that no other
+// operation is contracted.
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace cuvs::neighbors::octex::detail {
+
+namespace {
+
+constexpr unsigned kIdHash = 2654435761u;
+constexpr uint64_t kEmpty  = ~0ULL;
+
+__constant__ long long kPrimes[8] = {1000003LL,
+                                     998244353LL,
+                                     1000000007LL,
+                                     2147483647LL,
+                                     1099511627791LL,
+                                     4398042316799LL,
+                                     70368744177643LL,
+                                     1125899906842597LL};  // e8.cuh:13-20
+constexpr unsigned long long kMix = 0x9E3779B97F4A7C15ULL;  // e8.cuh:21
+
+// ------------------------------------------------------------------ E8 (e8.cuh:24-85)
+
+/** Nearest point of D8: round every coordinate, then fix the parity at the worst-rounded one. */
+__device__ __forceinline__ void d8(const float (&x)[8], float (&f)[8])
+{
+  float s  = 0.f;
+  int im   = 0;
+  float em = -1.f, ei = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    f[i]     = rintf(x[i]);
+    s        = s + f[i];
+    float e  = x[i] - f[i];
+    float ae = fabsf(e);
+    if (ae > em) {
+      em = ae;
+      im = i;
+      ei = e;
+    }
+  }
+  if (fmodf(s, 2.f) != 0.f) {
+    const float step = ei >= 0.f ? 1.f : -1.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      if (i == im) f[i] = f[i] + step;
+  }
+}
+
+/** Nearest point of E8 = D8 u (D8 + 1/2): the nearer of the two cosets' points (ties: D8). */
+__device__ __forceinline__ void e8_point(const float (&x)[8], float (&p)[8])
+{
+  float a[8], c[8], xs[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++)
+    xs[i] = x[i] - 0.5f;
+  d8(x, a);
+  d8(xs, c);
+  float da = 0.f, dc = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    c[i]     = c[i] + 0.5f;
+    float ta = x[i] - a[i];
+    float tc = x[i] - c[i];
+    da       = fmaf(ta, ta, da);
+    dc       = fmaf(tc, tc, dc);
+  }
+  const bool useA = da <= dc;
+#pragma unroll
+  for (int i = 0; i < 8; i++)
+    p[i] = useA ? a[i] : c[i];
+}
+
+/** Block hash: sum of 2 p_i times the i-th prime (64-bit wraparound). */
+__device__ __forceinline__ unsigned long long block_hash(const float (&p)[8])
+{
+  unsigned long long hb = 0;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    long long p2 = static_cast<long long>(2.f * p[i]);
+    hb += static_cast<unsigned long long>(p2) * static_cast<unsigned long long>(kPrimes[i]);
+  }
+  return hb;
+}
+
+__device__ __forceinline__ long long finish_hash(unsigned long long h)
+{
+  long long hs = static_cast<long long>(h);
+  hs           = static_cast<long long>(static_cast<unsigned long long>(hs ^ (hs >> 31)) * kMix);
+  return hs ^ (hs >> 29);
+}
+
+/** 64-bit cell id of the E8^B point nearest to y * inv_f. */
+template <int B>
+__device__ __forceinline__ long long e8b_hash64(const float (&y)[8 * B], float inv_f)
+{
+  unsigned long long h = 0;
+#pragma unroll
+  for (int j = 0; j < B; j++) {
+    float x[8], p[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      x[i] = y[8 * j + i] * inv_f;
+    e8_point(x, p);
+    unsigned long long hb = block_hash(p);
+    h                     = (j == 0) ? hb : h * kMix + hb;
+  }
+  return finish_hash(h);
+}
+
+// ------------------------------------------------------------------ query preparation
+
+__global__ void center_kernel(const float* __restrict__ q, const float* __restrict__ mu,
+                              int64_t total, int D, float* __restrict__ qc, __half* __restrict__ qh)
+{
+  int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= total) return;
+  float v = q[t] - mu[t % D];
+  qc[t]   = v;
+  qh[t]   = __float2half(v);
+}
+
+__global__ void pad_rows_kernel(float* __restrict__ q, int from, int m, int D)
+{
+  int64_t t     = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  int64_t total = static_cast<int64_t>(m - from) * D;
+  if (t >= total) return;
+  q[static_cast<int64_t>(from) * D + t] = q[t % D];
+}
+
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+/** Four consecutive fp16 of row r (k..k+3) of a row-major [rows, K] matrix, zeros outside it. */
+__device__ __forceinline__ half4_t load_h4(const __half* __restrict__ a, int r, int rows, int K, int k,
+                                           bool vec)
+{
+  half4_t v = {0, 0, 0, 0};
+  if (r >= rows) return v;
+  const __half* p = a + static_cast<int64_t>(r) * K + k;
+  if (vec && k + 3 < K) {
+    uint2 u = *reinterpret_cast<const uint2*>(p);
+    v       = *reinterpret_cast<half4_t*>(&u);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      if (k + j < K) v[j] = static_cast<_Float16>(__half2float(p[j]));
+  }
+  return v;
+}
+
+/**
+ * Y [m, N] = qh [m, K] @ ucatT [N, K]^T + shift (search.cu:305-320 as one MFMA kernel): every wave
+ * computes a 16-query x 64-output tile with v_mfma_f32_16x16x16_f16 (A = 16 outputs x 16 k of
+ * ucatT, B = 16 k x 16 queries of qh), fp32 accumulation, the fp16 shift added in fp32 and one
+ * rounding to fp16.  Lane l holds D[4 (l / 16) + r][l % 16]: 4 consecutive outputs of one query,
+ * stored as one 8-byte write.
+ */
+__global__ __launch_bounds__(256) void project_kernel(const __half* __restrict__ qh,
+                                                      const __half* __restrict__ ucatT,
+                                                      const __half* __restrict__ shift, int m, int K,
+                                                      int N, __half* __restrict__ Y)
+{
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int q0   = (blockIdx.x * 4 + wid) * 16;
+  const int n0   = blockIdx.y * 64;
+  const bool vec = (K & 3) == 0;
+  const int kq   = (lane >> 4) * 4;
+  const int ql   = q0 + (lane & 15);
+  float4_t acc[4];
+#pragma unroll
+  for (int t = 0; t < 4; t++)
+    acc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (int k0 = 0; k0 < K; k0 += 16) {
+    half4_t b = load_h4(qh, ql, m, K, k0 + kq, vec);
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      half4_t a = load_h4(ucatT, n0 + t * 16 + (lane & 15), N, K, k0 + kq, vec);
+      acc[t]    = __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, acc[t], 0, 0, 0);
+    }
+  }
+  if (ql >= m) return;
+  __half* yrow = Y + static_cast<int64_t>(ql) * N;
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    const int nb = n0 + t * 16 + kq;
+    __half o[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+      o[r] = __float2half(acc[t][r] + (nb + r < N ? __half2float(shift[nb + r]) : 0.f));
+    if (nb + 3 < N && (N & 3) == 0) {
+      *reinterpret_cast<uint2*>(yrow + nb) = *reinterpret_cast<uint2*>(o);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+        if (nb + r < N) yrow[nb + r] = o[r];
+    }
+  }
+}
+
+/** qs [m, S] = qc [m, D] @ basis [D, S]: one thread per output, sequential fma over d. */
+__global__ void sketch_query_kernel(const float* __restrict__ qc, const float* __restrict__ basis,
+                                    int m, int D, int S, float* __restrict__ qs)
+{
+  int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= static_cast<int64_t>(m) * S) return;
+  int64_t q = t / S;
+  int s     = static_cast<int>(t % S);
+  const float* r = qc + q * D;
+  float acc      = 0.f;
+  for (int d = 0; d < D; d++)
+    acc = fmaf(r[d], basis[static_cast<int64_t>(d) * S + s], acc);
+  qs[t] = acc;
+}
+
+template <int B>
+__global__ void e8_kernel(const float* __restrict__ y, int64_t n, float inv_f, float* __restrict__ p,
+                          long long* __restrict__ h)
+{
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float yv[8 * B];
+#pragma unroll
+  for (int k = 0; k < 8 * B; k++)
+    yv[k] = y[i * 8 * B + k];
+#pragma unroll
+  for (int j = 0; j < B; j++) {
+    float x[8], pp[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+      x[k] = yv[8 * j + k] * inv_f;
+    e8_point(x, pp);
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+      p[i * 8 * B + 8 * j + k] = pp[k];
+  }
+  h[i] = e8b_hash64<B>(yv, inv_f);
+}
+
+// ------------------------------------------------------------------ probe (search_kernels.cuh:84-127)
+
+/**
+ * One lane per (query, copy): for levels fine to coarse, the cell id of y * inv_f[j], its bucket,
+ * and a scan of the bucket's keys; the first hit gives seg = ((base + p) * l, lr), none (0, 0).
+ */
+template <int B>
+__global__ __launch_bounds__(256) void probe_kernel(const __half* __restrict__ Y, int m, int C,
+                                                    int L, const float* __restrict__ inv_f,
+                                                    const int* __restrict__ off, int64_t T1,
+                                                    const long long* __restrict__ keys,
+                                                    int64_t Mmax, const int* __restrict__ base,
+                                                    int l, int lr, int logT, int2* __restrict__ seg)
+{
+  int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= static_cast<int64_t>(m) * C) return;
+  const int c = static_cast<int>(t % C);
+  float y[8 * B];
+  const uint4* yp = reinterpret_cast<const uint4*>(Y + t * 8 * B);
+#pragma unroll
+  for (int i = 0; i < B; i++) {
+    uint4 u        = yp[i];
+    const __half2* h = reinterpret_cast<const __half2*>(&u);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      float2 v            = __half22float2(h[j]);
+      y[8 * i + 2 * j]     = v.x;
+      y[8 * i + 2 * j + 1] = v.y;
+    }
+  }
+  int2 sg              = make_int2(0, 0);
+  const long long mask = (1LL << logT) - 1;
+  for (int j = 0; j < L; j++) {
+    long long h          = e8b_hash64<B>(y, inv_f[j]);
+    int bk               = static_cast<int>(h & mask);
+    const int* o         = off + (static_cast<int64_t>(c) * L + j) * T1 + bk;
+    const long long* kk  = keys + (static_cast<int64_t>(c) * L + j) * Mmax;
+    const int p0 = o[0], p1 = o[1];
+    int hit = -1;
+    for (int p = p0; p < p1; p++)
+      if (kk[p] == h) {
+        hit = p;
+        break;
+      }
+    if (hit >= 0) {
+      sg = make_int2((base[c * L + j] + hit) * l, lr);
+      break;
+    }
+  }
+  seg[t] = sg;
+}
+
+// ------------------------------------------------------------------ gather (search_kernels.cuh:138-253)
+
+__device__ __forceinline__ int hash_log_dev(int total, int log_cap)
+{
+  if (total <= 0) return kMinLogHash;
+  int want = static_cast<int>((3 * static_cast<int64_t>(total) + 1) / 2);
+  int e    = 32 - __clz(want - 1);  // smallest e with 2^e >= want (want >= 1)
+  if (want == 1) e = 0;
+  return e < kMinLogHash ? kMinLogHash : (e > log_cap ? log_cap : e);
+}
+
+/**
+ * Distinct ids of all segments of a query with their sketch scores.  The entries of all segments are
+ * split evenly over the workgroup (exclusive prefix of the segment lengths, binary search per entry);
+ * an LDS open-addressing set drops duplicates; new ids are appended to the query's candidate row by
+ * one atomic per wavefront.  Then Lr lanes per candidate read its sketch row (16 bytes each) and
+ * reduce the score by an xor butterfly.
+ *
+ * kRows = false: segment c = (first entry, length) in the lists of copy c (row stride `stride`).
+ * kRows = true:  segment = (row, length) of the neighbor table [N, table_len]; -1 entries skipped.
+ */
+template <bool kRows>
+__global__ __launch_bounds__(kGatherThreads) void gather_kernel(
+  const int2* __restrict__ seg, int nseg, const int* __restrict__ lists, int64_t stride,
+  const int* __restrict__ table, int table_len, const signed char* __restrict__ code,
+  const float* __restrict__ scale, const float* __restrict__ qs, int S, int W, int logW,
+  int* __restrict__ cand, float* __restrict__ dist, int* __restrict__ nout)
+{
+  const int q = blockIdx.x;
+  extern __shared__ int sm[];
+  float* qv = reinterpret_cast<float*>(sm);
+  float* sc = qv + S;
+  int* pre  = reinterpret_cast<int*>(sc + S);  // [nseg + 1] exclusive prefix
+  int* st   = pre + nseg + 1;                  // [nseg] segment starts
+  int* ht   = st + nseg;                       // hash set
+  __shared__ int cnt;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, nw = blockDim.x >> 6;
+  for (int i = tid; i < S; i += blockDim.x) {
+    qv[i] = qs[static_cast<int64_t>(q) * S + i];
+    sc[i] = scale[i];
+  }
+  if (tid == 0) cnt = 0;
+  if (wid == 0) {
+    int carry = 0;
+    for (int c0 = 0; c0 < nseg; c0 += 64) {
+      const int c = c0 + lane;
+      int2 sl     = c < nseg ? seg[static_cast<int64_t>(q) * nseg + c] : make_int2(0, 0);
+      int v       = sl.y;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        int u = __shfl_up(v, o);
+        if (lane >= o) v += u;
+      }
+      if (c < nseg) {
+        pre[c] = carry + v - sl.y;
+        st[c]  = sl.x;
+      }
+      carry += __shfl(v, 63);
+    }
+    if (lane == 0) pre[nseg] = carry;
+  }
+  __syncthreads();
+  const int total = pre[nseg];
+  const int HT    = 1 << hash_log_dev(total, logW);
+  for (int i = tid; i < HT; i += blockDim.x)
+    ht[i] = -1;
+  __syncthreads();
+  int* crow = cand + static_cast<int64_t>(q) * W;
+  for (int i0 = 0; i0 < total; i0 += blockDim.x) {
+    const int i = i0 + tid;
+    bool fresh  = false;
+    int v       = -1;
+    if (i < total) {
+      int lo = 0, hi = nseg - 1;
+      while (lo < hi) {
+        int mid = (lo + hi + 1) >> 1;
+        if (pre[mid] <= i)
+          lo = mid;
+        else
+          hi = mid - 1;
+      }
+      if constexpr (kRows) {
+        v = table[static_cast<int64_t>(st[lo]) * table_len + (i - pre[lo])];
+      } else {
+        v = lists[static_cast<int64_t>(lo) * stride + st[lo] + (i - pre[lo])];
+      }
+      if (v >= 0) {
+        unsigned s = (static_cast<unsigned>(v) * kIdHash) & (HT - 1);
+        for (int p = 0; p < HT; p++) {
+          int prev = atomicCAS(&ht[s], -1, v);
+          if (prev == -1) {
+            fresh = true;
+            break;
+          }
+          if (prev == v) break;
+          s = (s + 1) & (HT - 1);
+        }
+      }
+    }
+    const unsigned long long mask = __ballot(fresh);
+    if (mask != 0) {
+      const int leader = __ffsll(static_cast<long long>(mask)) - 1;
+      int at           = 0;
+      if (lane == leader) at = atomicAdd(&cnt, __popcll(mask));
+      at = __shfl(at, leader);
+      if (fresh) {
+        int slot = at + __popcll(mask & ((1ULL << lane) - 1ULL));
+        if (slot < W) crow[slot] = v;
+      }
+    }
+  }
+  __syncthreads();
+  const int n = min(cnt, W);
+  int Lr      = 1;  // lanes per candidate: the next power of two >= S / 16, at most 32
+  while (Lr < S / 16 && Lr < 32)
+    Lr <<= 1;
+  const int G = 64 / Lr, sub = lane & (Lr - 1);
+  float* drow = dist + static_cast<int64_t>(q) * W;
+  for (int j0 = wid * G; j0 < n; j0 += nw * G) {
+    const int j = j0 + lane / Lr;
+    float d     = 0.f;
+    if (j < n) {
+      const signed char* x = code + static_cast<int64_t>(crow[j]) * S;
+      for (int k = sub * 16; k < S; k += Lr * 16) {
+        int4 w                = *reinterpret_cast<const int4*>(x + k);
+        const signed char* bb = reinterpret_cast<const signed char*>(&w);
+#pragma unroll
+        for (int t = 0; t < 16; t++) {
+          float u = fmaf(static_cast<float>(bb[t]), sc[k + t], -qv[k + t]);
+          d       = fmaf(u, u, d);
+        }
+      }
+    }
+    for (int o = Lr >> 1; o; o >>= 1)
+      d += __shfl_xor(d, o);
+    if (j < n && sub == 0) drow[j] = d;
+  }
+  if (tid == 0) nout[q] = n;
+}
+
+// ------------------------------------------------------------------ selection and merges
+
+struct select_state {
+  unsigned prefix, kk, eq, idprefix, kk2;
+  int nsel, need_id;
+};
+
+/**
+ * Wave 0 finds the digit d of a 256-bin histogram where the running count reaches kk (1 <= kk <=
+ * the histogram's total); returns true in the one lane that holds d, with kk reduced to the count
+ * still to take inside bin d and binpop the population of bin d.
+ */
+__device__ __forceinline__ bool pick_digit(const unsigned* hist, unsigned& kk, unsigned& digit,
+                                           unsigned& binpop)
+{
+  const int lane = threadIdx.x & 63;
+  unsigned h[4], s = 0;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    h[j] = hist[4 * lane + j];
+    s += h[j];
+  }
+  unsigned incl = s;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    unsigned u = __shfl_up(incl, o);
+    if (lane >= o) incl += u;
+  }
+  const unsigned excl = incl - s;
+  const unsigned want = kk;
+  if (!(excl < want && want <= incl)) return false;
+  unsigned cum = excl;
+  int j        = 0;
+  for (; j < 3; j++) {
+    if (cum + h[j] >= want) break;
+    cum += h[j];
+  }
+  kk     = want - cum;
+  digit  = 4 * lane + j;
+  binpop = h[j];
+  return true;
+}
+
+/**
+ * The R smallest of n (distance, id) pairs of a query by (distance bits, id) (search_kernels.cuh
+ * :259-322 with a deterministic tie rule): a radix select over the distance bits finds the threshold
+ * T; when only some of the keys equal to T are taken, a second radix select over their ids takes the
+ * smallest ids.  Selected ids (and keys when skey is set) go to sid / skey in any order; nsel in st.
+ * All threads of the workgroup call it.
+ */
+__device__ void select_smallest(const unsigned* __restrict__ kd, const int* __restrict__ cid, int n,
+                                int R, int* sid, float* skey, unsigned* hist, select_state& st)
+{
+  const int tid = threadIdx.x, wid = tid >> 6;
+  if (tid == 0) {
+    st.prefix  = 0;
+    st.kk      = min(R, n);
+    st.nsel    = 0;
+    st.need_id = 0;
+    st.eq      = 0;
+  }
+  __syncthreads();
+  if (n <= R) {
+    for (int i = tid; i < n; i += blockDim.x) {
+      sid[i] = cid[i];
+      if (skey) skey[i] = __uint_as_float(kd[i]);
+    }
+    if (tid == 0) st.nsel = n;
+    __syncthreads();
+    return;
+  }
+  unsigned mask = 0;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int i = tid; i < 256; i += blockDim.x)
+      hist[i] = 0;
+    __syncthreads();
+    const unsigned pf = st.prefix;
+    for (int i = tid; i < n; i += blockDim.x) {
+      unsigned k = kd[i];
+      if ((k & mask) == pf) atomicAdd(&hist[(k >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (wid == 0) {
+      unsigned kk = st.kk, digit = 0, pop = 0;
+      if (pick_digit(hist, kk, digit, pop)) {
+        st.kk     = kk;
+        st.prefix = pf | (digit << shift);
+        st.eq     = pop;
+      }
+    }
+    mask |= 255u << shift;
+    __syncthreads();
+  }
+  const unsigned T = st.prefix;
+  if (st.kk < st.eq) {  // ties at T: the smallest ids among the keys equal to T
+    if (tid == 0) {
+      st.idprefix = 0;
+      st.kk2      = st.kk;
+      st.need_id  = 1;
+    }
+    __syncthreads();
+    unsigned imask = 0;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      for (int i = tid; i < 256; i += blockDim.x)
+        hist[i] = 0;
+      __syncthreads();
+      const unsigned pf = st.idprefix;
+      for (int i = tid; i < n; i += blockDim.x) {
+        unsigned id = static_cast<unsigned>(cid[i]);
+        if (kd[i] == T && (id & imask) == pf) atomicAdd(&hist[(id >> shift) & 255u], 1u);
+      }
+      __syncthreads();
+      if (wid == 0) {
+        unsigned kk = st.kk2, digit = 0, pop = 0;
+        if (pick_digit(hist, kk, digit, pop)) {
+          st.kk2      = kk;
+          st.idprefix = pf | (digit << shift);
+        }
+      }
+      imask |= 255u << shift;
+      __syncthreads();
+    }
+  }
+  const bool by_id   = st.need_id != 0;
+  const unsigned Tid = st.idprefix;
+  for (int i = tid; i < n; i += blockDim.x) {
+    unsigned k = kd[i];
+    bool take  = k < T || (k == T && (!by_id || static_cast<unsigned>(cid[i]) <= Tid));
+    if (take) {
+      int s  = atomicAdd(&st.nsel, 1);
+      sid[s] = cid[i];
+      if (skey) skey[s] = __uint_as_float(k);
+    }
+  }
+  __syncthreads();
+}
+
+/**
+ * Squared distances of the fp16 rows sid[0, ns) to the fp32 query sq (search_kernels.cuh:325-342):
+ * one wavefront per row, lane l takes the half2 pairs l, l + 64, ..., then a 64-lane xor butterfly.
+ */
+__device__ void exact_distances(const int* sid, int ns, const __half* __restrict__ vectors, int D,
+                                const float* sq, float* sd)
+{
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int P    = D / 2;
+  for (int j = wid; j < ns; j += nw) {
+    const __half2* x = reinterpret_cast<const __half2*>(vectors + static_cast<int64_t>(sid[j]) * D);
+    float acc        = 0.f;
+    for (int k = lane; k < P; k += 64) {
+      float2 v = __half22float2(x[k]);
+      float a  = v.x - sq[2 * k];
+      float b  = v.y - sq[2 * k + 1];
+      acc      = fmaf(a, a, acc);
+      acc      = fmaf(b, b, acc);
+    }
+#pragma unroll
+    for (int o = 32; o; o >>= 1)
+      acc += __shfl_xor(acc, o);
+    if (lane == 0) sd[j] = acc;
+  }
+  __syncthreads();
+}
+
+/** Ascending bitonic sort of P (a power of two) 64-bit keys in LDS. */
+__device__ void bitonic_sort(uint64_t* key, int P)
+{
+  for (int size = 2; size <= P; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = threadIdx.x; i < P; i += blockDim.x) {
+        int j = i ^ stride;
+        if (j > i) {
+          bool up    = (i & size) == 0;
+          uint64_t a = key[i], b = key[j];
+          if ((a > b) == up) {
+            key[i] = b;
+            key[j] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+__device__ __forceinline__ uint64_t dist_key(float d, long long id)
+{
+  return (static_cast<uint64_t>(__float_as_uint(d)) << 32) | static_cast<unsigned>(id);
+}
+
+/** The kept list (unless fresh) and ns new (distance, id) pairs as P keys (search_kernels.cuh:372-392). */
+__device__ void load_keys(uint64_t* key, int P, const long long* pb, const float* pd, int KO,
+                          bool fresh, const int* sid, const float* sdv, int ns)
+{
+  for (int i = threadIdx.x; i < P; i += blockDim.x) {
+    uint64_t k = kEmpty;
+    if (i < KO) {
+      if (!fresh && pb[i] >= 0) k = dist_key(pd[i], pb[i]);
+    } else if (i - KO < ns) {
+      k = dist_key(sdv[i - KO], sid[i - KO]);
+    }
+    key[i] = k;
+  }
+  __syncthreads();
+}
+
+/**
+ * The first KO distinct sorted keys to (pb, pd), padded with (-1, +inf) (search_kernels.cuh:396-415):
+ * wavefront 0 walks the keys 64 at a time and places every distinct key by a ballot prefix count.
+ */
+__device__ void store_keys(const uint64_t* key, int P, int KO, long long* pb, float* pd)
+{
+  if ((threadIdx.x >> 6) != 0) return;
+  const int lane = threadIdx.x & 63;
+  int at         = 0;
+  for (int i0 = 0; i0 < P && at < KO; i0 += 64) {
+    const int i      = i0 + lane;
+    const uint64_t k = i < P ? key[i] : kEmpty;
+    const bool keep  = k != kEmpty && (i == 0 || key[i - 1] != k);
+    const unsigned long long mask = __ballot(keep);
+    const int o = at + __popcll(mask & ((1ULL << lane) - 1ULL));
+    if (keep && o < KO) {
+      pb[o] = static_cast<long long>(static_cast<unsigned>(k & 0xffffffffULL));
+      pd[o] = __uint_as_float(static_cast<unsigned>(k >> 32));
+    }
+    at += __popcll(mask);
+  }
+  for (int o = min(at, KO) + lane; o < KO; o += 64) {
+    pb[o] = -1;
+    pd[o] = INFINITY;
+  }
+}
+
+/**
+ * Exact rerank of the R sketch-nearest candidates of a query, merged into its kept list of the best
+ * KO (search_kernels.cuh:421-467).  fresh: the kept list starts empty.
+ */
+__global__ __launch_bounds__(kKeepThreads) void rerank_keep_kernel(
+  const int* __restrict__ cand, const float* __restrict__ dist, const int* __restrict__ nin, int W,
+  const __half* __restrict__ vectors, int D, const float* __restrict__ Q, int R, int KO,
+  long long* __restrict__ bi, float* __restrict__ bd, bool fresh)
+{
+  const int q = blockIdx.x;
+  extern __shared__ float sq[];
+  __shared__ unsigned hist[256];
+  __shared__ select_state st;
+  __shared__ int sid[kMaxRerank];
+  __shared__ float sd[kMaxRerank];
+  __shared__ uint64_t key[kMaxKeepSort];
+  const int n = min(nin[q], W);
+  for (int i = threadIdx.x; i < D; i += blockDim.x)
+    sq[i] = Q[static_cast<int64_t>(q) * D + i];
+  select_smallest(reinterpret_cast<const unsigned*>(dist + static_cast<int64_t>(q) * W),
+                  cand + static_cast<int64_t>(q) * W, n, R, sid, nullptr, hist, st);
+  const int ns = st.nsel;
+  exact_distances(sid, ns, vectors, D, sq, sd);
+  long long* pb = bi + static_cast<int64_t>(q) * KO;
+  float* pd     = bd + static_cast<int64_t>(q) * KO;
+  int P         = 2;
+  while (P < KO + R)
+    P <<= 1;
+  load_keys(key, P, pb, pd, KO, fresh, sid, sd, ns);
+  bitonic_sort(key, P);
+  store_keys(key, P, KO, pb, pd);
+}
+
+/** The KO sketch-nearest candidates merged into the kept list by sketch distance (:471-508). */
+__global__ __launch_bounds__(512) void sketch_keep_kernel(const int* __restrict__ cand,
+                                                          const float* __restrict__ dist,
+                                                          const int* __restrict__ nin, int W, int KO,
+                                                          long long* __restrict__ si,
+                                                          float* __restrict__ sd, bool fresh)
+{
+  const int q = blockIdx.x;
+  __shared__ unsigned hist[256];
+  __shared__ select_state st;
+  __shared__ int sid[kMaxSketchKO];
+  __shared__ float sdv[kMaxSketchKO];
+  __shared__ uint64_t key[2 * kMaxSketchKO];
+  const int n = min(nin[q], W);
+  select_smallest(reinterpret_cast<const unsigned*>(dist + static_cast<int64_t>(q) * W),
+                  cand + static_cast<int64_t>(q) * W, n, KO, sid, sdv, hist, st);
+  const int ns  = st.nsel;
+  long long* pb = si + static_cast<int64_t>(q) * KO;
+  float* pd     = sd + static_cast<int64_t>(q) * KO;
+  int P         = 2;
+  while (P < KO + ns)
+    P <<= 1;
+  load_keys(key, P, pb, pd, KO, fresh, sid, sdv, ns);
+  bitonic_sort(key, P);
+  store_keys(key, P, KO, pb, pd);
+}
+
+/**
+ * Start points of a wave (search_kernels.cuh:571-631): the first S kept entries (best first) that no
+ * earlier wave expanded (done[:, :off]), written to done[:, off:off + S] and to the gather segments
+ * seg2 = (row, rowlen); (-1 / (0, 0)) when fewer remain.
+ */
+__global__ __launch_bounds__(256) void pick_starts_kernel(const long long* __restrict__ si, int KO,
+                                                          long long* __restrict__ done, int E,
+                                                          int off, int S, int rowlen,
+                                                          int2* __restrict__ seg2)
+{
+  const int q = blockIdx.x;
+  __shared__ int ht[kPickHash];
+  __shared__ unsigned char fresh[kMaxSketchKO];
+  const long long* ps = si + static_cast<int64_t>(q) * KO;
+  long long* pd       = done + static_cast<int64_t>(q) * E;
+  for (int i = threadIdx.x; i < kPickHash; i += blockDim.x)
+    ht[i] = -1;
+  __syncthreads();
+  for (int i = threadIdx.x; i < off; i += blockDim.x) {
+    long long v = pd[i];
+    if (v < 0) continue;
+    unsigned h = (static_cast<unsigned>(v) * kIdHash) & (kPickHash - 1);
+    for (int p = 0; p < kPickHash; p++) {
+      int prev = atomicCAS(&ht[h], -1, static_cast<int>(v));
+      if (prev == -1 || prev == static_cast<int>(v)) break;
+      h = (h + 1) & (kPickHash - 1);
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < KO; i += blockDim.x) {
+    long long v = ps[i];
+    bool f      = v >= 0;
+    if (f) {
+      unsigned h = (static_cast<unsigned>(v) * kIdHash) & (kPickHash - 1);
+      for (int p = 0; p < kPickHash; p++) {
+        int t = ht[h];
+        if (t == -1) break;
+        if (t == static_cast<int>(v)) {
+          f = false;
+          break;
+        }
+        h = (h + 1) & (kPickHash - 1);
+      }
+    }
+    fresh[i] = f;
+  }
+  __syncthreads();
+  if ((threadIdx.x >> 6) != 0) return;
+  const int lane = threadIdx.x & 63;
+  int at         = 0;
+  for (int i0 = 0; i0 < KO && at < S; i0 += 64) {
+    const int i     = i0 + lane;
+    const bool take = i < KO && fresh[i];
+    const unsigned long long mask = __ballot(take);
+    const int o = at + __popcll(mask & ((1ULL << lane) - 1ULL));
+    if (take && o < S) {
+      long long v                            = ps[i];
+      pd[off + o]                            = v;
+      seg2[static_cast<int64_t>(q) * S + o] = make_int2(static_cast<int>(v), rowlen);
+    }
+    at += __popcll(mask);
+  }
+  for (int o = min(at, S) + lane; o < S; o += 64) {
+    pd[off + o]                            = -1;
+    seg2[static_cast<int64_t>(q) * S + o] = make_int2(0, 0);
+  }
+}
+
+/** Exact rerank of the first R kept entries (sketch-rank mode) into the best k (:634-669). */
+__global__ __launch_bounds__(kKeepThreads) void final_rerank_kernel(
+  const long long* __restrict__ si, int KO, int R, const __half* __restrict__ vectors, int D,
+  const float* __restrict__ Q, int k, long long* __restrict__ bi, float* __restrict__ bd)
+{
+  const int q = blockIdx.x;
+  extern __shared__ float sq[];
+  __shared__ int sid[kMaxRerank];
+  __shared__ float sd[kMaxRerank];
+  __shared__ uint64_t key[kMaxRerank];
+  __shared__ int nsel;
+  const long long* ps = si + static_cast<int64_t>(q) * KO;
+  for (int i = threadIdx.x; i < D; i += blockDim.x)
+    sq[i] = Q[static_cast<int64_t>(q) * D + i];
+  if (threadIdx.x < 64) {  // the valid entries among the first R, in order (ballot compaction)
+    const int lane = threadIdx.x;
+    int at         = 0;
+    for (int i0 = 0; i0 < R; i0 += 64) {
+      const int i    = i0 + lane;
+      const bool ok  = i < R && ps[i] >= 0;
+      const unsigned long long mask = __ballot(ok);
+      if (ok) sid[at + __popcll(mask & ((1ULL << lane) - 1ULL))] = static_cast<int>(ps[i]);
+      at += __popcll(mask);
+    }
+    if (lane == 0) nsel = at;
+  }
+  __syncthreads();
+  const int ns = nsel;
+  exact_distances(sid, ns, vectors, D, sq, sd);
+  int P = 2;
+  while (P < R)
+    P <<= 1;
+  load_keys(key, P, nullptr, nullptr, 0, true, sid, sd, ns);
+  bitonic_sort(key, P);
+  store_keys(key, P, k, bi + static_cast<int64_t>(q) * k, bd + static_cast<int64_t>(q) * k);
+}
+
+__global__ void take_k_kernel(const long long* __restrict__ si, const float* __restrict__ sd, int KO,
+                              int k, int m, long long* __restrict__ bi, float* __restrict__ bd)
+{
+  int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= static_cast<int64_t>(m) * k) return;
+  int64_t q = t / k, j = t % k;
+  bi[t]     = si[q * KO + j];
+  bd[t]     = sd[q * KO + j];
+}
+
+}  // namespace
+
+// ================================================================== launchers
+
+void launch_center(const float* q, const float* mu, int64_t m, int D, float* qc, __half* qh,
+                   hipStream_t s)
+{
+  const int64_t total = m * D;
+  if (total == 0) return;
+  center_kernel<<<grid_for(total, 256), 256, 0, s>>>(q, mu, total, D, qc, qh);
+  OCTEX_HIP(hipGetLastError());
+}
+
+void launch_pad_rows(float* q, int from, int m, int D, hipStream_t s)
+{
+  const int64_t total = static_cast<int64_t>(m - from) * D;
+  if (total <= 0) return;
+  pad_rows_kernel<<<grid_for(total, 256), 256, 0, s>>>(q, from, m, D);
+  OCTEX_HIP(hipGetLastError());
+}
+
+void launch_project(const __half* qh, const __half* ucatT, const __half* shift, int m, int K, int N,
+                    __half* Y, hipStream_t s)
+{
+  if (m == 0 || N == 0) return;
+  OCTEX_EXPECTS(K >= 1, "octex: projection needs a positive dimension");
+  dim3 grid(static_cast<unsigned>((m + 63) / 64), static_cast<unsigned>((N + 63) / 64));
+  project_kernel<<<grid, 256, 0, s>>>(qh, ucatT, shift, m, K, N, Y);
+  OCTEX_HIP(hipGetLastError());
+}
+
+void launch_sketch_query(const float* qc, const float* basis, int m, int D, int S, float* qs,
+                         hipStream_t s)
+{
+  const int64_t total = static_cast<int64_t>(m) * S;
+  if (total == 0) return;
+  sketch_query_kernel<<<grid_for(total, 256), 256, 0, s>>>(qc, basis, m, D, S, qs);
+  OCTEX_HIP(hipGetLastError());
+}
+
+void launch_e8(const float* y, int64_t n, int b, float inv_f, float* p, long long* h, hipStream_t s)
+{
+  if (n == 0) return;
+  auto g = grid_for(n, 256);
+  switch (b) {
+    case 1: e8_kernel<1><<<g, 256, 0, s>>>(y, n, inv_f, p, h); break;
+    case 2: e8_kernel<2><<<g, 256, 0, s>>>(y, n, inv_f, p, h); break;
+    case 3: e8_kernel<3><<<g, 256, 0, s>>>(y, n, inv_f, p, h); break;
+    case 4: e8_kernel<4><<<g, 256, 0, s>>>(y, n, inv_f, p, h); break;
+    case 5: e8_kernel<5><<<g, 256, 0, s>>>(y, n, inv_f, p, h); break;
+    case 6: e8_kernel<6><<<g, 256, 0, s>>>(y, n, inv_f, p, h); break;
+    case 8: e8_kernel<8><<<g, 256, 0, s>>>(y, n, inv_f, p, h); break;
+    default: fail("octex: blocks must be 1-6 or 8");
+  }
+  OCTEX_HIP(hipGetLastError());
+}
+
+void launch_probe(const __half* Y, int m, int C, int L, int B, const float* inv_f, const int* off,
+                  int64_t T1, const long long* keys, int64_t Mmax, const int* base, int l, int lr,
+                  int logT, int2* seg, hipStream_t s)
+{
+  const int64_t tot = static_cast<int64_t>(m) * C;
+  if (tot == 0) return;
+  OCTEX_EXPECTS(T1 == (int64_t{1} << logT) + 1, "octex: offsets rows must hold 2^log_buckets + 1 entries");
+  auto g = grid_for(tot, 256);
+#define OCTEX_PROBE(b) \
+  probe_kernel<b><<<g, 256, 0, s>>>(Y, m, C, L, inv_f, off, T1, keys, Mmax, base, l, lr, logT, seg)
+  switch (B) {
+    case 1: OCTEX_PROBE(1); break;
+    case 2: OCTEX_PROBE(2); break;
+    case 3: OCTEX_PROBE(3); break;
+    case 4: OCTEX_PROBE(4); break;
+    case 5: OCTEX_PROBE(5); break;
+    case 6: OCTEX_PROBE(6); break;
+    case 8: OCTEX_PROBE(8); break;
+    default: fail("octex: blocks must be 1-6 or 8");
+  }
+#undef OCTEX_PROBE
+  OCTEX_HIP(hipGetLastError());
+}
+
+auto gather_smem(int W, int S, int nseg) -> size_t
+{
+  return static_cast<size_t>(W + 2 * S + 2 * nseg + 1) * sizeof(int);
+}
+
+void launch_gather(bool rows, const int2* seg, int nseg, int m, const int* lists, int64_t stride,
+                   const int* table, int table_len, const signed char* code, const float* scale,
+                   const float* qs, int S, int W, int logW, int* cand, float* dist, int* nout,
+                   hipStream_t s)
+{
+  if (m == 0) return;
+  OCTEX_EXPECTS(nseg >= 1, "octex: a gather needs at least one segment per query");
+  OCTEX_EXPECTS(W == (1 << logW) && W <= kMaxHash, "octex: hash set size");
+  OCTEX_EXPECTS(S % 16 == 0 && S >= 16 && S <= 512, "octex: sketch width: a multiple of 16, <= 512");
+  const size_t smem = gather_smem(W, S, nseg);
+  OCTEX_EXPECTS(smem <= 160 * 1024, "octex: gather needs %zu bytes of LDS (max 160 KiB)", smem);
+  if (rows) {
+    OCTEX_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gather_kernel<true>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
+    gather_kernel<true><<<m, kGatherThreads, smem, s>>>(seg, nseg, lists, stride, table, table_len, code,
+                                                        scale, qs, S, W, logW, cand, dist, nout);
+  } else {
+    OCTEX_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gather_kernel<false>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
+    gather_kernel<false><<<m, kGatherThreads, smem, s>>>(seg, nseg, lists, stride, table, table_len, code,
+                                                         scale, qs, S, W, logW, cand, dist, nout);
+  }
+  OCTEX_HIP(hipGetLastError());
+}
+
+void launch_rerank_keep(const int* cand, const float* dist, const int* nin, int m, int W,
+                        const __half* vectors, int D, const float* Q, int R, int KO, long long* si,
+                        float* sd, bool fresh, hipStream_t s)
+{
+  if (m == 0) return;
+  OCTEX_EXPECTS(R >= 1 && R <= kMaxRerank && KO + R <= kMaxKeepSort && KO >= 1,
+                "octex: rerank in [1, 512] and max(starts, k) + rerank <= 1024");
+  OCTEX_EXPECTS(D % 2 == 0, "octex: the dimension must be even");
+  rerank_keep_kernel<<<m, kKeepThreads, D * sizeof(float), s>>>(cand, dist, nin, W, vectors, D, Q, R,
+                                                                KO, si, sd, fresh);
+  OCTEX_HIP(hipGetLastError());
+}
+
+void launch_sketch_keep(const int* cand, const float* dist, const int* nin, int m, int W, int KO,
+                        long long* si, float* sd, bool fresh, hipStream_t s)
+{
+  if (m == 0) return;
+  OCTEX_EXPECTS(KO >= 1 && KO <= kMaxSketchKO, "octex: max(starts, k) must be <= 1024 with sketch_rank");
+  sketch_keep_kernel<<<m, 512, 0, s>>>(cand, dist, nin, W, KO, si, sd, fresh);
+  OCTEX_HIP(hipGetLastError());
+}
+
+void launch_pick_starts(const long long* si, int m, int KO, long long* done, int E, int off, int S,
+                        int rowlen, int2* seg2, hipStream_t s)
+{
+  if (m == 0) return;
+  OCTEX_EXPECTS(KO <= kMaxSketchKO && off <= kMaxExpanded && off + S <= E,
+                "octex: starts * (waves - 1) <= 6144");
+  pick_starts_kernel<<<m, 256, 0, s>>>(si, KO, done, E, off, S, rowlen, seg2);
+  OCTEX_HIP(hipGetLastError());
+}
+
+void launch_final_rerank(const long long* si, int m, int KO, int R, const __half* vectors, int D,
+                         const float* Q, int k, long long* bi, float* bd, hipStream_t s)
+{
+  if (m == 0) return;
+  OCTEX_EXPECTS(R >= k && R <= kMaxRerank && R <= KO,
+                "octex: final_rerank 0 (sketch order) or k <= final_rerank <= 512");
+  final_rerank_kernel<<<m, kKeepThreads, D * sizeof(float), s>>>(si, KO, R, vectors, D, Q, k, bi, bd);
+  OCTEX_HIP(hipGetLastError());
+}
+
+void launch_take_k(const long long* si, const float* sd, int m, int KO, int k, long long* bi,
+                   float* bd, hipStream_t s)
+{
+  const int64_t total = static_cast<int64_t>(m) * k;
+  if (total == 0) return;
+  take_k_kernel<<<grid_for(total, 256), 256, 0, s>>>(si, sd, KO, k, m, bi, bd);
+  OCTEX_HIP(hipGetLastError());
+}
+
+}  // namespace cuvs::neighbors::octex::detail

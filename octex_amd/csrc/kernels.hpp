@@ -1,0 +1,67 @@
+// Launchers of the octex search kernels for gfx950 (kernels.hip).  Every launcher checks the shapes
+// its grid assumes and throws an "octex: ..." error before a launch that would not fit.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace cuvs::neighbors::octex::detail {
+
+// limits of the per-query LDS structures (search_kernels.cuh:20-29)
+constexpr int kMinLogHash     = 11;     // smallest hash set: 2^11 slots
+constexpr int kMaxHash        = 32768;  // largest hash set (LDS)
+constexpr int kMaxRerank      = 512;    // exact rerank depth per round
+constexpr int kMaxKeepSort    = 1024;   // kept + reranked keys sorted together
+constexpr int kMaxSketchKO    = 1024;   // kept entries of the sketch merge
+constexpr int kPickHash       = 8192;   // hash set of the expanded start points
+constexpr int kMaxExpanded    = 6144;   // start points expanded by earlier waves
+constexpr int kGatherThreads  = 512;
+constexpr int kKeepThreads    = 256;
+
+/** log2 of the hash set of a query reading `total` entries: ceil(log2(1.5 total)) in [11, log_cap]. */
+inline auto hash_log_host(int total, int log_cap) -> int
+{
+  if (total <= 0) return kMinLogHash;
+  int64_t want = (3 * int64_t{total} + 1) / 2;
+  int e        = 0;
+  while ((int64_t{1} << e) < want)
+    e++;
+  return e < kMinLogHash ? kMinLogHash : (e > log_cap ? log_cap : e);
+}
+
+void launch_center(const float* q, const float* mu, int64_t m, int D, float* qc, __half* qh,
+                   hipStream_t s);
+void launch_pad_rows(float* q, int from, int m, int D, hipStream_t s);
+/** Y [m, N] = qh [m, K] @ ucatT [N, K]^T + shift [N] (fp16 MFMA, fp32 accumulate, fp16 out). */
+void launch_project(const __half* qh, const __half* ucatT, const __half* shift, int m, int K, int N,
+                    __half* Y, hipStream_t s);
+/** qs [m, S] = qc [m, D] @ basis [D, S] (fp32, sequential fma over d). */
+void launch_sketch_query(const float* qc, const float* basis, int m, int D, int S, float* qs,
+                         hipStream_t s);
+/** E8^b points and hashes of y [n, 8b] * inv_f (the E8 decode of the probe, for tests). */
+void launch_e8(const float* y, int64_t n, int b, float inv_f, float* p, long long* h, hipStream_t s);
+void launch_probe(const __half* Y, int m, int C, int L, int B, const float* inv_f, const int* off,
+                  int64_t T1, const long long* keys, int64_t Mmax, const int* base, int l, int lr,
+                  int logT, int2* seg, hipStream_t s);
+/** LDS bytes of a gather over `nseg` segments per query with hash sets up to W slots. */
+auto gather_smem(int W, int S, int nseg) -> size_t;
+void launch_gather(bool rows, const int2* seg, int nseg, int m, const int* lists, int64_t stride,
+                   const int* table, int table_len, const signed char* code, const float* scale,
+                   const float* qs, int S, int W, int logW, int* cand, float* dist, int* nout,
+                   hipStream_t s);
+void launch_rerank_keep(const int* cand, const float* dist, const int* nin, int m, int W,
+                        const __half* vectors, int D, const float* Q, int R, int KO, long long* si,
+                        float* sd, bool fresh, hipStream_t s);
+void launch_sketch_keep(const int* cand, const float* dist, const int* nin, int m, int W, int KO,
+                        long long* si, float* sd, bool fresh, hipStream_t s);
+void launch_pick_starts(const long long* si, int m, int KO, long long* done, int E, int off, int S,
+                        int rowlen, int2* seg2, hipStream_t s);
+void launch_final_rerank(const long long* si, int m, int KO, int R, const __half* vectors, int D,
+                         const float* Q, int k, long long* bi, float* bd, hipStream_t s);
+void launch_take_k(const long long* si, const float* sd, int m, int KO, int k, long long* bi,
+                   float* bd, hipStream_t s);
+
+}  // namespace cuvs::neighbors::octex::detail

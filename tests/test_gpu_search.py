@@ -1,0 +1,186 @@
+"""The whole search on the GPU through the cuvsOctex* C ABI, against the CPU oracle on the same index and queries.
+
+Parity: given the GPU's own projections Y and sketch queries qs (read back from the search plan), the oracle's
+search returns the same ids and bit-identical distances; against exact search, recall thresholds of the
+reference's tests (test_build.py:48-54, octex_c.cu:196).  Batch splitting / padding, graph replay, device tensors,
+sketch-rank mode and the parameter limits are covered too."""
+
+import numpy as np
+import pytest
+from conftest import exact_knn, recall
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def octex():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import octex_amd
+
+    return octex_amd
+
+
+PARAMS = dict(read=32, starts=64, waves=2, rerank=64, wave_rerank=64)
+
+
+def oracle_given_gpu_projections(index, oix, Q, k, **params):
+    """The oracle's search fed with the GPU plan's Y and qs of the last (single) batch."""
+    info = index.plan_info()
+    assert info["m"] == len(Q)
+    C, w, S = oix.copies, oix.width, oix.sketch_width
+    Y = index.plan_buffer("Y", np.uint16)[: len(Q) * C * w].reshape(len(Q), C * w)
+    qs = index.plan_buffer("qs", np.float32)[: len(Q) * S].reshape(len(Q), S)
+    D, I, tr = O.search(oix, Q, k=k, Y=Y, qs=qs, trace=True, **params)
+    return D, I, tr, Y, qs
+
+
+def assert_same_results(D, I, D2, I2):
+    """Identical ids and distances, except where distances tie (then the ids at the tie may swap)."""
+    assert np.array_equal(D, D2), "distances differ"
+    diff = I != I2
+    if diff.any():
+        for q, j in zip(*np.nonzero(diff)):
+            assert (D[q] == D[q, j]).sum() > 1, f"query {q} rank {j}: ids differ without a distance tie"
+
+
+def test_search_matches_oracle(octex, small_index):
+    index = octex.load(small_index["path"])
+    oix = O.Index(small_index["path"])
+    Q = small_index["Q"]
+    D, I = index.search(Q, k=10, **PARAMS)
+    Do, Io, tr, Y, qs = oracle_given_gpu_projections(index, oix, Q, 10, **PARAMS)
+    assert_same_results(D, I, Do, Io)
+    # stage by stage: probe segments, first-round candidate counts, the final kept list
+    seg = index.plan_buffer("seg", np.int32)[: len(Q) * oix.copies * 2].reshape(len(Q), oix.copies, 2)
+    assert np.array_equal(seg, tr["seg"])
+    nin = index.plan_buffer("nin", np.int32)[: len(Q)]
+    assert np.array_equal(nin, tr["n1"])
+    KO = max(PARAMS["starts"], 10)
+    sd = index.plan_buffer("sd", np.float32)[: len(Q) * KO].reshape(len(Q), KO)
+    assert np.array_equal(sd, tr["sd"])
+    # the projections themselves against the fp64 oracle: within one fp16 ulp
+    qc, qh = O.center(Q, oix.mean)
+    Yr, _ = O.project(qh, oix.ucat, oix.shift)
+    from test_gpu_stages import ulp_diff
+
+    assert ulp_diff(Y, Yr).max() <= 1
+    assert np.allclose(qs, O.sketch_query(qc, oix.basis), rtol=1e-5, atol=1e-4)
+
+
+def test_search_recall_and_distances(octex, small_index):
+    index = octex.load(small_index["path"])
+    Q = small_index["Q"]
+    D, I = index.search(Q, k=10, **PARAMS)
+    assert recall(I, small_index["gt"]) >= 0.95
+    Xh = small_index["X"].astype(np.float16).astype(np.float64)
+    exact = ((Xh[I] - Q[:, None, :].astype(np.float64)) ** 2).sum(-1)
+    assert np.allclose(D, exact, rtol=1e-3)
+    assert (np.diff(D, axis=1) >= 0).all()
+
+
+def test_batch_split_and_padding(octex, small_index):
+    """Results do not depend on the batch size: batches of 37 (last one padded) equal one batch."""
+    index = octex.load(small_index["path"])
+    Q = small_index["Q"]
+    D1, I1 = index.search(Q, k=10, batch=1000, **PARAMS)
+    D2, I2 = index.search(Q, k=10, batch=37, **PARAMS)
+    assert np.array_equal(I1, I2) and np.array_equal(D1, D2)
+
+
+def test_graph_equals_direct_launches(octex, small_index):
+    index = octex.load(small_index["path"])
+    Q = small_index["Q"]
+    D1, I1 = index.search(Q, k=10, **PARAMS)
+    assert index.plan_info()["graph"] == 1
+    D2, I2 = index.search(Q, k=10, use_graph=False, **PARAMS)
+    assert index.plan_info()["graph"] == 0
+    assert np.array_equal(I1, I2) and np.array_equal(D1, D2)
+    for _ in range(3):  # replays of one graph, with eager work in between
+        D3, I3 = index.search(Q, k=10, **PARAMS)
+        assert np.array_equal(I1, I3) and np.array_equal(D1, D3)
+
+
+def test_device_tensors(octex, small_index):
+    index = octex.load(small_index["path"])
+    Q = small_index["Q"]
+    D1, I1 = index.search(Q, k=10, **PARAMS)
+    D2, I2 = index.search(torch.from_numpy(Q).cuda(), k=10, **PARAMS)
+    assert D2.is_cuda and I2.dtype == torch.int64
+    assert np.array_equal(I1, I2.cpu().numpy()) and np.array_equal(D1, D2.cpu().numpy())
+
+
+def test_sketch_rank_matches_oracle(octex, small_index):
+    index = octex.load(small_index["path"])
+    oix = O.Index(small_index["path"])
+    Q = small_index["Q"]
+    p = dict(read=16, starts=96, waves=2, sketch_rank=True, final_rerank=48)
+    D, I = index.search(Q, k=10, **p)
+    Do, Io, _, _, _ = oracle_given_gpu_projections(index, oix, Q, 10, **p)
+    assert_same_results(D, I, Do, Io)
+    p0 = dict(p, final_rerank=0)  # sketch order, sketch distances out
+    D, I = index.search(Q, k=10, **p0)
+    Do, Io, _, _, _ = oracle_given_gpu_projections(index, oix, Q, 10, **p0)
+    assert_same_results(D, I, Do, Io)
+
+
+def test_waves_zero_and_k_above_starts(octex, small_index):
+    index = octex.load(small_index["path"])
+    oix = O.Index(small_index["path"])
+    Q = small_index["Q"][:50]
+    for p, k in ((dict(read=8, starts=32, waves=0), 10), (dict(read=32, starts=8, waves=1), 20)):
+        D, I = index.search(Q, k=k, **p)
+        Do, Io, _, _, _ = oracle_given_gpu_projections(index, oix, Q, k, **p)
+        assert_same_results(D, I, Do, Io)
+
+
+def test_wide_index_matches_oracle(octex, wide_index):
+    """Sketch width 96 (8 lanes per candidate, two of them idle), 3 blocks, dimension 96."""
+    index = octex.load(wide_index["path"])
+    oix = O.Index(wide_index["path"])
+    Q = wide_index["Q"]
+    D, I = index.search(Q, k=10, **PARAMS)
+    Do, Io, _, _, _ = oracle_given_gpu_projections(index, oix, Q, 10, **PARAMS)
+    assert_same_results(D, I, Do, Io)
+    gt, _ = exact_knn(wide_index["X"].astype(np.float16).astype(np.float32), Q)
+    assert recall(I, gt) >= 0.9
+
+
+def test_load_limits_match_oracle(octex, small_index):
+    index = octex.load(small_index["path"], copies_limit=5, list_limit=8)
+    assert index.copies == 5
+    oix = O.Index(small_index["path"], copies_limit=5, list_limit=8)
+    Q = small_index["Q"][:40]
+    D, I = index.search(Q, k=10, **PARAMS)
+    Do, Io, _, _, _ = oracle_given_gpu_projections(index, oix, Q, 10, **PARAMS)
+    assert_same_results(D, I, Do, Io)
+
+
+def test_placements_on_host(octex, small_index):
+    """Vectors, table and sketch in pinned host memory give the same results."""
+    Q = small_index["Q"][:40]
+    D1, I1 = octex.load(small_index["path"]).search(Q, k=10, **PARAMS)
+    index = octex.load(small_index["path"], vectors_on_host=True, table_on_host=True, sketch="host")
+    D2, I2 = index.search(Q, k=10, **PARAMS)
+    assert np.array_equal(I1, I2) and np.array_equal(D1, D2)
+
+
+def test_errors(octex, small_index):
+    from octex_amd._lib import OctexError
+
+    index = octex.load(small_index["path"])
+    Q = small_index["Q"][:4]
+    with pytest.raises(ValueError, match="dimension"):
+        index.search(Q[:, :10], k=10)
+    with pytest.raises(OctexError, match="max\\(starts, k\\) must be <= 512"):
+        index.search(Q, k=10, starts=600)
+    with pytest.raises(OctexError, match="read, starts >= 1"):
+        index.search(Q, k=10, read=0)
+    with pytest.raises(FileNotFoundError):
+        octex.load(small_index["path"] + "_missing")
+    assert index.size == 4000 and index.dim == 64 and index.copies == 16 and len(index.devices) == 1
+    assert index.device_bytes[0] > 0

@@ -1,0 +1,313 @@
+"""Every HIP kernel of the search path against the CPU oracle on the same inputs, through the stage entry points
+of liboctex_amd.so (include/octex_amd/octex_amd.h).  Bit-exact: E8 points and hashes, probe segments, candidate
+sets, sketch scores, selections, kept lists, start points.  The fp16 projection: within 1 fp16 ulp of the fp64
+value (its MFMA accumulation order is not the oracle's); the fp32 sketch query: 1e-5 relative."""
+
+import ctypes as ct
+
+import numpy as np
+import pytest
+from conftest import clustered
+from test_oracle import check_e8, e8_inputs
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def L():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from octex_amd import _lib
+
+    return _lib
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def P(t):
+    return ct.c_void_p(t.data_ptr())
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+def i32(v):
+    return ct.c_int32(int(v))
+
+
+def i64(v):
+    return ct.c_int64(int(v))
+
+
+# ---------------------------------------------------------------- E8 and projections
+
+
+@pytest.mark.parametrize("b", [4, 1, 3, 8])
+def test_e8_kernel_matches_oracle(L, b):
+    x = e8_inputs(n=20000 if b == 4 else 4000, b=b, seed=b)
+    inv_f = np.float32(1.0 / 2.5)
+    dx = dev(x)
+    dp = torch.empty_like(dx)
+    dh = torch.empty(x.shape[0], dtype=torch.int64, device="cuda")
+    L.call("octexStageE8", P(dx), i64(x.shape[0]), i32(b), ct.c_float(inv_f), P(dp), P(dh), None)
+    p, h = O.e8_batch(x, b, float(inv_f))
+    assert np.array_equal(host(dp), p)
+    assert np.array_equal(host(dh), h)
+    check_e8(x, host(dp), host(dh), b, inv_f)
+
+
+def test_e8_golden(L):
+    import os
+
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "e8.npz"))
+    dx = dev(g["y"])
+    dp = torch.empty_like(dx)
+    dh = torch.empty(g["y"].shape[0], dtype=torch.int64, device="cuda")
+    L.call("octexStageE8", P(dx), i64(g["y"].shape[0]), i32(g["b"]), ct.c_float(g["inv_f"]), P(dp), P(dh), None)
+    assert np.array_equal(host(dp), g["p"]) and np.array_equal(host(dh), g["h"])
+
+
+def test_center_kernel(L):
+    g = np.random.default_rng(0)
+    q = g.standard_normal((77, 96)).astype(np.float32)
+    mu = g.standard_normal(96).astype(np.float32)
+    dq, dmu = dev(q), dev(mu)
+    qc = torch.empty_like(dq)
+    qh = torch.empty(q.shape, dtype=torch.int16, device="cuda")
+    L.call("octexStageCenter", P(dq), P(dmu), i64(77), i32(96), P(qc), P(qh), None)
+    rc, rh = O.center(q, mu)
+    assert np.array_equal(host(qc), rc) and np.array_equal(host(qh).view(np.uint16), rh)
+
+
+def ulp_diff(a_bits, b_bits):
+    """Distance in fp16 units in the last place between two arrays of fp16 bit patterns."""
+    def ordered(h):
+        h = h.astype(np.int32)
+        return np.where(h & 0x8000, -(h & 0x7FFF), h & 0x7FFF)
+
+    return np.abs(ordered(a_bits) - ordered(b_bits))
+
+
+@pytest.mark.parametrize("m,K,N", [(300, 96, 6400 // 8), (1000, 128, 256), (65, 100, 72), (17, 34, 40), (130, 960, 96)])
+def test_projection_within_one_ulp(L, m, K, N):
+    g = np.random.default_rng(m + K + N)
+    qh = (g.standard_normal((m, K)) * 0.5).astype(np.float16)
+    ucat = (g.standard_normal((K, N)) / np.sqrt(K)).astype(np.float16)
+    shift = g.uniform(0, 2, N).astype(np.float16)
+    dY = torch.empty((m, N), dtype=torch.int16, device="cuda")
+    ucatT = np.ascontiguousarray(ucat.T)
+    L.call("octexStageProject", P(dev(qh.view(np.int16))), P(dev(ucatT.view(np.int16))), P(dev(shift.view(np.int16))),
+           i32(m), i32(K), i32(N), P(dY), None)
+    Y, Yd = O.project(qh.view(np.uint16), ucat.view(np.uint16), shift.view(np.uint16))
+    got = host(dY).view(np.uint16)
+    u = ulp_diff(got, Y)
+    assert u.max() <= 1, f"max ulp {u.max()}"
+    assert (u > 0).mean() < 0.02, f"ulp mismatch rate {(u > 0).mean()}"
+
+
+def test_sketch_query_kernel(L):
+    g = np.random.default_rng(1)
+    qc = g.standard_normal((500, 96)).astype(np.float32)
+    basis = g.standard_normal((96, 64)).astype(np.float32)
+    qs = torch.empty((500, 64), dtype=torch.float32, device="cuda")
+    L.call("octexStageSketchQuery", P(dev(qc)), P(dev(basis)), i32(500), i32(96), i32(64), P(qs), None)
+    ref = qc.astype(np.float64) @ basis.astype(np.float64)
+    assert np.allclose(host(qs), ref, rtol=1e-5, atol=1e-4)
+
+
+# ---------------------------------------------------------------- probe, gather
+
+
+@pytest.fixture(scope="module")
+def ix(small_index):
+    return O.Index(small_index["path"])
+
+
+@pytest.fixture(scope="module")
+def dix(L, ix):
+    """The oracle's index arrays on the device (the loader's layout)."""
+    return dict(
+        inv_f=dev(ix.inv_f), offsets=dev(ix.offsets), keys=dev(ix.keys), base=dev(ix.base), lists=dev(ix.lists),
+        sketch=dev(ix.sketch), scale=dev(ix.scale), vectors=dev(ix.vectors.view(np.int16)), table=dev(ix.table),
+    )
+
+
+def queries_Y(ix, X, extra_random=64, seed=0):
+    """Projections of database rows (cells exist) and of random points (mostly misses)."""
+    qc, qh = O.center(X, ix.mean)
+    Y, _ = O.project(qh, ix.ucat, ix.shift)
+    g = np.random.default_rng(seed)
+    R = O.f2h(g.standard_normal((extra_random, Y.shape[1])).astype(np.float32) * 3)
+    return np.concatenate([Y, R])
+
+
+def run_probe(L, ix, dix, Y, lr):
+    m, C = Y.shape[0], ix.copies
+    seg = torch.empty((m, C, 2), dtype=torch.int32, device="cuda")
+    L.call("octexStageProbe", P(dev(Y.view(np.int16))), i32(m), i32(C), i32(len(ix.spacings)), i32(ix.blocks),
+           P(dix["inv_f"]), P(dix["offsets"]), i64(ix.offsets.shape[2]), P(dix["keys"]), i64(ix.keys.shape[2]),
+           P(dix["base"]), i32(ix.list_len), i32(lr), i32(ix.log_buckets), P(seg), None)
+    return seg
+
+
+def test_probe_matches_oracle(L, ix, dix, small_index):
+    Y = queries_Y(ix, small_index["X"][:200])
+    for lr in (ix.list_len, 5):
+        seg = run_probe(L, ix, dix, Y, lr)
+        ref = O.probe(ix, Y, read=lr)
+        assert np.array_equal(host(seg), ref)
+    assert (ref[:200, :, 1] > 0).mean() > 0.9 and (ref[200:, :, 1] == 0).mean() > 0.5
+
+
+def gather_gpu(L, ix, dix, seg, qs, rows, W=4096):
+    m, nseg = seg.shape[0], seg.shape[1]
+    cand = torch.full((m, W), -5, dtype=torch.int32, device="cuda")
+    dist = torch.zeros((m, W), dtype=torch.float32, device="cuda")
+    nout = torch.zeros(m, dtype=torch.int32, device="cuda")
+    L.call("octexStageGather", i32(rows), P(seg), i32(nseg), i32(m), P(dix["lists"]), i64(ix.lists.shape[1]),
+           P(dix["table"]), i32(ix.table_len), P(dix["sketch"]), P(dix["scale"]), P(dev(qs)), i32(ix.sketch_width),
+           i32(W), P(cand), P(dist), P(nout), None)
+    return host(cand), host(dist), host(nout)
+
+
+def check_gather(ix, seg, qs, cand, dist, nout, rows):
+    for q in range(seg.shape[0]):
+        rc, rd = O.gather(ix, seg[q], qs[q], rows=rows)
+        n = nout[q]
+        assert n == len(rc)
+        order = np.argsort(cand[q, :n])
+        assert np.array_equal(cand[q, :n][order], rc), f"query {q}: candidate sets differ"
+        assert np.array_equal(dist[q, :n][order], rd), f"query {q}: sketch scores differ"
+
+
+def test_gather_lists_matches_oracle(L, ix, dix, small_index):
+    Y = queries_Y(ix, small_index["X"][:64], extra_random=8)
+    seg = run_probe(L, ix, dix, Y, ix.list_len)
+    qs = np.random.default_rng(2).standard_normal((Y.shape[0], ix.sketch_width)).astype(np.float32)
+    cand, dist, nout = gather_gpu(L, ix, dix, seg, qs, rows=0)
+    check_gather(ix, host(seg), qs, cand, dist, nout, rows=False)
+
+
+def test_gather_rows_matches_oracle(L, ix, dix):
+    g = np.random.default_rng(3)
+    m, S = 48, 64
+    seg2 = np.stack([g.integers(0, ix.n, (m, S)), np.full((m, S), ix.table_len)], -1).astype(np.int32)
+    seg2[:, -7:] = 0  # unused start points
+    seg2[0] = 0  # a query without starts
+    qs = g.standard_normal((m, ix.sketch_width)).astype(np.float32)
+    cand, dist, nout = gather_gpu(L, ix, dix, dev(seg2), qs, rows=1)
+    check_gather(ix, seg2, qs, cand, dist, nout, rows=True)
+    assert nout[0] == 0
+
+
+# ---------------------------------------------------------------- keep, pick, final
+
+
+def random_candidates(g, m, W, n_max, N, ties=True):
+    cand = np.full((m, W), -9, np.int32)
+    dist = np.zeros((m, W), np.float32)
+    nin = g.integers(1, n_max, m).astype(np.int32)
+    nin[0] = n_max
+    nin[1] = 3
+    for q in range(m):
+        n = nin[q]
+        cand[q, :n] = g.choice(N, n, replace=False)
+        dist[q, :n] = g.integers(0, 40, n) if ties else g.uniform(0, 100, n)
+    return cand, dist, nin
+
+
+@pytest.mark.parametrize("fresh", [True, False])
+def test_rerank_keep_matches_oracle(L, ix, dix, small_index, fresh):
+    g = np.random.default_rng(4 + fresh)
+    m, W, KO, R = 40, 2048, 64, 48
+    cand, dist, nin = random_candidates(g, m, W, 1500, ix.n)
+    Q = small_index["Q"][:m]
+    si = np.full((m, KO), -1, np.int64)
+    sd = np.full((m, KO), np.inf, np.float32)
+    if not fresh:
+        for q in range(m):
+            ids = g.choice(ix.n, 50, replace=False)
+            ex = np.array([O.exact_dist(ix.vectors[i], Q[q]) for i in ids], np.float32)
+            si[q], sd[q] = O.merge_keep(si[q], sd[q], ids.astype(np.int32), ex, True)
+    dsi, dsd = dev(si), dev(sd)
+    L.call("octexStageRerankKeep", P(dev(cand)), P(dev(dist)), P(dev(nin)), i32(m), i32(W), P(dix["vectors"]),
+           i32(ix.dim), P(dev(Q)), i32(R), i32(KO), P(dsi), P(dsd), i32(fresh), None)
+    for q in range(m):
+        ri, rd = O.rerank_keep(ix, cand[q, : nin[q]], dist[q, : nin[q]], Q[q], R, si[q], sd[q], fresh)
+        assert np.array_equal(host(dsi)[q], ri), f"query {q}"
+        assert np.array_equal(host(dsd)[q], rd), f"query {q}"
+
+
+@pytest.mark.parametrize("fresh", [True, False])
+def test_sketch_keep_matches_oracle(L, fresh):
+    g = np.random.default_rng(6 + fresh)
+    m, W, KO = 32, 4096, 200
+    cand, dist, nin = random_candidates(g, m, W, 3000, 100_000)
+    si = np.full((m, KO), -1, np.int64)
+    sd = np.full((m, KO), np.inf, np.float32)
+    if not fresh:
+        for q in range(m):
+            ids = g.choice(100_000, 150, replace=False).astype(np.int32)
+            si[q], sd[q] = O.merge_keep(si[q], sd[q], ids, g.integers(0, 40, 150).astype(np.float32), True)
+    dsi, dsd = dev(si), dev(sd)
+    L.call("octexStageSketchKeep", P(dev(cand)), P(dev(dist)), P(dev(nin)), i32(m), i32(W), i32(KO), P(dsi),
+           P(dsd), i32(fresh), None)
+    for q in range(m):
+        ri, rd = O.sketch_keep(cand[q, : nin[q]], dist[q, : nin[q]], si[q], sd[q], fresh)
+        assert np.array_equal(host(dsi)[q], ri) and np.array_equal(host(dsd)[q], rd), f"query {q}"
+
+
+def test_pick_starts_matches_oracle(L):
+    g = np.random.default_rng(8)
+    m, KO, S, waves = 30, 256, 64, 4
+    E = S * waves
+    si = np.stack([g.choice(50_000, KO, replace=False) for _ in range(m)]).astype(np.int64)
+    si[:, 200:] = -1
+    done = np.full((m, E), -3, np.int64)
+    for off in (0, S, 2 * S):
+        dd = dev(done)
+        seg2 = torch.zeros((m, S, 2), dtype=torch.int32, device="cuda")
+        L.call("octexStagePickStarts", P(dev(si)), i32(m), i32(KO), P(dd), i32(E), i32(off), i32(S), i32(40),
+               P(seg2), None)
+        for q in range(m):
+            rdone, rseg = O.pick_starts(si[q], done[q], off, S, 40)
+            assert np.array_equal(host(dd)[q, : off + S], rdone[: off + S]), f"query {q} off {off}"
+            assert np.array_equal(host(seg2)[q], rseg)
+        done = host(dd)
+        si = np.stack([np.concatenate([g.permutation(r[:200]), r[200:]]) for r in si])  # a new kept order
+
+
+def test_final_rerank_and_take_k(L, ix, dix, small_index):
+    g = np.random.default_rng(9)
+    m, KO, R, k = 25, 128, 64, 10
+    si = np.stack([g.choice(ix.n, KO, replace=False) for _ in range(m)]).astype(np.int64)
+    si[:, 40:50] = -1
+    Q = small_index["Q"][:m]
+    bi = torch.empty((m, k), dtype=torch.int64, device="cuda")
+    bd = torch.empty((m, k), dtype=torch.float32, device="cuda")
+    L.call("octexStageFinalRerank", P(dev(si)), i32(m), i32(KO), i32(R), P(dix["vectors"]), i32(ix.dim), P(dev(Q)),
+           i32(k), P(bi), P(bd), None)
+    for q in range(m):
+        ri, rd = O.final_rerank(ix, si[q], R, Q[q], k)
+        assert np.array_equal(host(bi)[q], ri) and np.array_equal(host(bd)[q], rd)
+    sd = g.uniform(0, 1, (m, KO)).astype(np.float32)
+    L.call("octexStageTakeK", P(dev(si)), P(dev(sd)), i32(m), i32(KO), i32(k), P(bi), P(bd), None)
+    assert np.array_equal(host(bi), si[:, :k]) and np.array_equal(host(bd), sd[:, :k])
+
+
+def test_stage_errors(L):
+    from octex_amd._lib import OctexError
+
+    with pytest.raises(OctexError, match="blocks must be 1-6 or 8"):
+        x = torch.zeros((4, 56), device="cuda")
+        L.call("octexStageE8", P(x), i64(4), i32(7), ct.c_float(1.0), P(x), P(x), None)
+    with pytest.raises(OctexError, match="rerank in \\[1, 512\\]"):
+        L.call("octexStageRerankKeep", P(x), P(x), P(x), i32(1), i32(2048), P(x), i32(64), P(x), i32(600), i32(10),
+               P(x), P(x), i32(1), None)

@@ -1,0 +1,324 @@
+"""The CPU oracle pinned against the reference's known-answer rules and against independent mathematics:
+IEEE fp16 (numpy), E8 lattice membership / optimality and the reference test's hash_ref (test_build.cu:79-176),
+fp64 scores, brute-force sets and selections, the keep / pick-starts rules (test_search.cu:347-504), recall
+against exact search, and the committed golden fixtures.  CPU only."""
+
+import json
+import os
+
+import numpy as np
+import pytest
+from conftest import clustered, exact_knn, recall
+
+from oracle import oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+# ---------------------------------------------------------------- fp16
+
+
+def test_fp16_matches_numpy_all_halves():
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    f = O.h2f(h)
+    ref = h.view(np.float16).astype(np.float32)
+    same = (f == ref) | (np.isnan(f) & np.isnan(ref))
+    assert same.all()
+
+
+def test_fp16_rounding_matches_numpy():
+    g = np.random.default_rng(0)
+    x = np.concatenate([
+        g.standard_normal(200_000).astype(np.float32) * 10,
+        g.standard_normal(50_000).astype(np.float32) * 1e-5,  # subnormal range
+        (g.integers(-4096, 4096, 50_000) + 0.5).astype(np.float32) / 2,  # exact ties
+        np.array([65504, 65520, 65519.99, 1e9, -1e9, 0.0, -0.0, 2**-25, 2**-24, 3 * 2**-26], np.float32),
+    ])
+    assert np.array_equal(O.f2h(x), x.astype(np.float16).view(np.uint16))
+
+
+# ---------------------------------------------------------------- E8 (test_build.cu:94-176)
+
+PRIMES = np.array([1000003, 998244353, 1000000007, 2147483647, 1099511627791, 4398042316799, 70368744177643,
+                   1125899906842597], dtype=np.uint64)
+MIX = np.uint64(0x9E3779B97F4A7C15)
+
+
+def hash_ref(p, b):
+    """The reference test's hash of decoded points (test_build.cu:79-92): lround(2 p) times the primes."""
+    with np.errstate(over="ignore"):
+        h = np.zeros(p.shape[0], np.uint64)
+        for j in range(b):
+            two_p = np.rint(2.0 * p[:, 8 * j : 8 * j + 8].astype(np.float64)).astype(np.int64).astype(np.uint64)
+            hb = (two_p * PRIMES[None, :]).sum(axis=1, dtype=np.uint64)
+            h = hb if j == 0 else h * MIX + hb
+        s = h.view(np.int64)
+        s = ((s ^ (s >> 31)).view(np.uint64) * MIX).view(np.int64)
+        return s ^ (s >> 29)
+
+
+def e8_roots():
+    roots = []
+    for i in range(8):
+        for j in range(i + 1, 8):
+            for si in (-1, 1):
+                for sj in (-1, 1):
+                    r = np.zeros(8)
+                    r[i], r[j] = si, sj
+                    roots.append(r)
+    for m in range(256):
+        if bin(m).count("1") % 2 == 0:
+            roots.append(np.array([-0.5 if (m >> k) & 1 else 0.5 for k in range(8)]))
+    return np.array(roots)
+
+
+def e8_inputs(n=20000, b=4, seed=7):
+    g = np.random.default_rng(seed)
+    x = g.uniform(-6, 6, (n, 8 * b)).astype(np.float32)
+    x[:500] = np.round(x[:500] * 2) * 0.5  # half-integer ties
+    x[500:800] = np.round(x[500:800])  # integer points
+    return x
+
+
+def check_e8(x, p, h, b, inv_f):
+    roots = e8_roots()
+    assert len(roots) == 240
+    xs = (x * np.float32(inv_f)).astype(np.float64)
+    pp = p.astype(np.float64)
+    for j in range(b):
+        blk = pp[:, 8 * j : 8 * j + 8]
+        fr = blk - np.floor(blk)
+        all_int = (fr == 0).all(1)
+        all_half = (fr == 0.5).all(1)
+        assert (all_int | all_half).all(), "not in D8 u (D8 + 1/2)"
+        assert (np.fmod(np.abs(blk.sum(1)), 2.0) == 0).all(), "odd coordinate sum"
+        r = xs[:, 8 * j : 8 * j + 8] - blk
+        d0 = (r**2).sum(1)
+        d1 = ((r[:, None, :] - roots[None, :, :]) ** 2).sum(2)
+        assert (d1 >= d0[:, None] - 1e-6).all(), "a root improves the decoded point"
+    assert np.array_equal(h, hash_ref(p, b)), "hash differs from hash_ref"
+
+
+def test_e8_invariants_and_hash_ref():
+    x = e8_inputs()
+    p, h = O.e8_batch(x, 4, 1.0 / 2.5)
+    check_e8(x, p, h, 4, 1.0 / 2.5)
+
+
+@pytest.mark.parametrize("b", [1, 2, 3, 8])
+def test_e8_blocks(b):
+    x = e8_inputs(n=3000, b=b, seed=b)
+    p, h = O.e8_batch(x, b, 0.5)
+    check_e8(x, p, h, b, 0.5)
+
+
+def test_e8_plausible_mistakes_fail():
+    """The checks above catch a wrong coset choice or a dropped parity fix (a planted mistake on the CPU)."""
+    x = e8_inputs(n=2000)
+    p, h = O.e8_batch(x, 4, 1.0)
+    bad = p.copy()
+    bad[:, :8] = np.round(x[:, :8])  # plain rounding: parity not fixed, coset never half
+    with pytest.raises(AssertionError):
+        check_e8(x, bad, hash_ref(bad, 4), 4, 1.0)
+    with pytest.raises(AssertionError):
+        check_e8(x, p, h ^ 1, 4, 1.0)
+
+
+def test_golden_e8():
+    g = np.load(os.path.join(GOLDEN, "e8.npz"))
+    p, h = O.e8_batch(g["y"], int(g["b"]), float(g["inv_f"]))
+    assert np.array_equal(p, g["p"]) and np.array_equal(h, g["h"])
+
+
+# ---------------------------------------------------------------- scores
+
+
+@pytest.mark.parametrize("S", [16, 48, 64, 96, 128, 512])
+def test_sketch_dist_formula(S):
+    g = np.random.default_rng(S)
+    code = g.integers(-127, 128, S).astype(np.int8)
+    scale = g.uniform(0.01, 0.1, S).astype(np.float32)
+    qs = g.standard_normal(S).astype(np.float32)
+    d = O.sketch_dist(code, scale, qs)
+    ref = ((code.astype(np.float64) * scale.astype(np.float64) - qs.astype(np.float64)) ** 2).sum()
+    assert abs(d - ref) <= 1e-5 * ref
+
+
+@pytest.mark.parametrize("D", [2, 64, 96, 128, 130, 960])
+def test_exact_dist_formula(D):
+    g = np.random.default_rng(D)
+    x = g.standard_normal(D).astype(np.float16)
+    q = g.standard_normal(D).astype(np.float32)
+    d = O.exact_dist(x.view(np.uint16), q)
+    ref = ((x.astype(np.float64) - q.astype(np.float64)) ** 2).sum()
+    assert abs(d - ref) <= 1e-5 * ref
+
+
+def test_golden_scores():
+    g = np.load(os.path.join(GOLDEN, "scores.npz"))
+    for code, scale, qs, d in zip(g["code"], g["scale"], g["qs"], g["sketch"]):
+        assert np.float32(O.sketch_dist(code, scale, qs)) == d
+    for x, q, d in zip(g["x"], g["q"], g["exact"]):
+        assert np.float32(O.exact_dist(x, q)) == d
+
+
+# ---------------------------------------------------------------- selection and merges
+
+
+def test_select_is_lexicographic():
+    g = np.random.default_rng(1)
+    cand = g.permutation(5000).astype(np.int32)
+    dist = g.integers(0, 50, 5000).astype(np.float32)  # many ties
+    for R in (1, 7, 128, 5000, 6000):
+        sid, sd = O.select(cand, dist, R)
+        order = np.lexsort((cand, dist))[: min(R, 5000)]
+        assert np.array_equal(sid, cand[order]) and np.array_equal(sd, dist[order])
+
+
+def keep_rule(si, sd, new_ids, new_d, KO, fresh):
+    """test_search.cu:347-375: sort (distance, id), take the first KO distinct, pad (-1, +inf)."""
+    pairs = [] if fresh else [(float(d), int(i)) for i, d in zip(si, sd) if i >= 0]
+    pairs += [(float(d), int(i)) for i, d in zip(new_ids, new_d)]
+    pairs = sorted(set(pairs))[:KO]
+    out_i = [i for _, i in pairs] + [-1] * (KO - len(pairs))
+    out_d = [d for d, _ in pairs] + [np.inf] * (KO - len(pairs))
+    return np.array(out_i), np.array(out_d, np.float32)
+
+
+def test_merge_keep_rule():
+    g = np.random.default_rng(2)
+    for fresh in (True, False):
+        KO = 64
+        si = g.choice(1000, KO, replace=False).astype(np.int64)
+        sd = g.uniform(0, 10, KO).astype(np.float32)
+        si[-5:] = -1
+        ids = g.integers(0, 1000, 100).astype(np.int32)
+        d = g.uniform(0, 10, 100).astype(np.float32)
+        d[:10] = 3.0  # distance ties
+        ids[10:20] = si[:10]  # the same ids again, with their own distances
+        d[10:20] = sd[:10]
+        oi, od = O.merge_keep(si, sd, ids, d, fresh)
+        ri, rd = keep_rule(si, sd, ids, d, KO, fresh)
+        assert np.array_equal(oi, ri) and np.array_equal(od, rd)
+
+
+def test_pick_starts_rule():
+    """test_search.cu:476-504: the first S kept entries not expanded before, -1 padded."""
+    g = np.random.default_rng(3)
+    KO, S, E = 200, 32, 96
+    si = g.choice(10_000, KO, replace=False).astype(np.int64)
+    si[150:] = -1
+    done = np.full(E, -7, np.int64)
+    done[:64] = g.choice(si[:150], 64, replace=False)
+    done_out, seg2 = O.pick_starts(si, done, 64, S, 48)
+    fresh = [v for v in si if v >= 0 and v not in set(done[:64].tolist())][:S]
+    fresh += [-1] * (S - len(fresh))
+    assert np.array_equal(done_out[64 : 64 + S], fresh)
+    assert np.array_equal(done_out[:64], done[:64])
+    exp = np.array([(v, 48) if v >= 0 else (0, 0) for v in fresh])
+    assert np.array_equal(seg2, exp)
+
+
+# ---------------------------------------------------------------- index-level stages
+
+
+def test_gather_is_the_union(small_index):
+    ix = O.Index(small_index["path"])
+    g = np.random.default_rng(4)
+    qs = g.standard_normal(ix.sketch_width).astype(np.float32)
+    # list segments of random cell rows of every copy
+    C = ix.copies
+    seg = np.zeros((C, 2), np.int32)
+    for c in range(C):
+        rows = ix.lists.shape[1] // ix.list_len
+        seg[c] = (g.integers(0, rows) * ix.list_len, g.integers(0, ix.list_len + 1))
+    seg[3] = (0, 0)
+    cand, dist = O.gather(ix, seg, qs)
+    union = set()
+    for c in range(C):
+        union |= set(ix.lists[c, seg[c, 0] : seg[c, 0] + seg[c, 1]].tolist())
+    assert set(cand.tolist()) == union and len(cand) == len(union)
+    ref = ((ix.sketch[cand].astype(np.float64) * ix.scale - qs) ** 2).sum(1)
+    assert np.allclose(dist, ref, rtol=1e-5)
+    # table rows, with -1 padding skipped
+    seg2 = np.stack([g.integers(0, ix.n, 40), np.full(40, ix.table_len)], 1).astype(np.int32)
+    seg2[5] = (0, 0)
+    cand2, _ = O.gather(ix, seg2, qs, rows=True)
+    rows = set(ix.table[seg2[seg2[:, 1] > 0, 0]].ravel().tolist()) - {-1}
+    assert set(cand2.tolist()) == rows
+
+
+def test_probe_construction(small_index):
+    """A query equal to a database row's own projection finds a cell in every copy (test_search.cu:86-170 shape):
+    seg = (row * l, lr) with the row's id in the segment at the coarsest level at the latest."""
+    ix = O.Index(small_index["path"])
+    X = small_index["X"][:20]
+    qc, qh = O.center(X, ix.mean)
+    Y, _ = O.project(qh, ix.ucat, ix.shift)
+    seg = O.probe(ix, Y, read=ix.list_len)
+    assert (seg[:, :, 1] == ix.list_len).mean() > 0.9
+    assert ((seg[:, :, 0] % ix.list_len) == 0).all()
+
+
+def test_search_recall(small_index):
+    ix = O.Index(small_index["path"])
+    D, I = O.search(ix, small_index["Q"], k=10, read=32, starts=64, waves=2)
+    assert recall(I, small_index["gt"]) >= 0.95
+    assert (np.diff(D, axis=1) >= 0).all()
+    Xh = small_index["X"].astype(np.float16).astype(np.float64)
+    exact = ((Xh[I] - small_index["Q"][:, None, :].astype(np.float64)) ** 2).sum(-1)
+    assert np.allclose(D, exact, rtol=1e-4)
+
+
+def test_search_sketch_rank(small_index):
+    ix = O.Index(small_index["path"])
+    D, I = O.search(ix, small_index["Q"], k=10, read=32, starts=64, waves=2, sketch_rank=True, final_rerank=64)
+    assert recall(I, small_index["gt"]) >= 0.8
+    assert (np.diff(D, axis=1) >= 0).all()
+
+
+def test_search_limits(small_index):
+    ix = O.Index(small_index["path"])
+    q = small_index["Q"][:2]
+    with pytest.raises(ValueError, match="max\\(starts, k\\) must be <= 512"):
+        O.search(ix, q, k=10, starts=600)
+    with pytest.raises(ValueError, match="rerank in \\[1, 512\\]"):
+        O.search(ix, q, k=10, rerank=0)
+    with pytest.raises(ValueError, match="starts \\* \\(waves - 1\\) <= 6144"):
+        O.search(ix, q, k=10, starts=512, waves=14, rerank=1, wave_rerank=1)
+
+
+def test_list_limit_and_copies_limit(small_index):
+    ix = O.Index(small_index["path"], list_limit=8, copies_limit=4)
+    full = O.Index(small_index["path"])
+    assert ix.copies == 4 and ix.list_len == 8
+    rows = full.lists.shape[1] // full.list_len
+    assert np.array_equal(ix.lists.reshape(4, rows, 8), full.lists[:4].reshape(4, rows, full.list_len)[:, :, :8])
+    D, I = O.search(ix, small_index["Q"][:10], k=10, read=32, starts=32, waves=1)
+    assert (I >= 0).all()
+
+
+def test_index_directory_format(small_index):
+    """The builder writes the files and shapes of the format-1 directory (design.md:27-54)."""
+    path = small_index["path"]
+    meta = json.load(open(os.path.join(path, "meta.json")))
+    assert meta["format"] == 1 and meta["metric"] == "sqeuclidean" and meta["files"] == {}
+    C, L, n, d = meta["copies"], len(meta["spacings"]), meta["n"], meta["dim"]
+    w = 8 * meta["blocks"]
+    shapes = dict(mean=(d,), proj=(C, d, w), shift=(C, w), base=(C, L), cells=(C, L), sketch_scale=(meta["sketch_width"],),
+                  sketch_basis=(d, meta["sketch_width"]), sketch=(n, meta["sketch_width"]), vectors=(n, d),
+                  table=(n, meta["table_len"]))
+    for name, shape in shapes.items():
+        assert np.load(os.path.join(path, name + ".npy"), mmap_mode="r").shape == shape, name
+    offs = np.load(os.path.join(path, "offsets.npy"))
+    keys = np.load(os.path.join(path, "keys.npy"))
+    cells = np.load(os.path.join(path, "cells.npy"))
+    assert offs.shape == (C, L, 2 ** meta["log_buckets"] + 1)
+    assert (offs[:, :, -1] == cells).all() and (np.diff(offs, axis=2) >= 0).all()
+    T = 2 ** meta["log_buckets"]
+    for c in range(C):
+        for j in range(L):
+            k = keys[c, j, : cells[c, j]]
+            b = k & (T - 1)
+            assert (np.diff(b) >= 0).all()  # (bucket, hash) order
+            assert np.array_equal(np.searchsorted(b, np.arange(T + 1)), offs[c, j])
