@@ -47,9 +47,10 @@ cuvsError_t octexStageProbe(const void* Y, int32_t m, int32_t C, int32_t L, int3
                             const int32_t* off, int64_t T1, const int64_t* keys, int64_t Mmax,
                             const int32_t* base, int32_t l, int32_t lr, int32_t logT, int32_t* seg,
                             void* stream);
-/** gather_kernel (search_kernels.cuh:138-253): rows = 0 lists, 1 table rows; W a power of two. */
+/** gather_kernel (search_kernels.cuh:138-253): rows = 0 lists, 1 table rows; W a power of two; ids at or
+ * above n are skipped like the -1 padding. */
 cuvsError_t octexStageGather(int32_t rows, const int32_t* seg, int32_t nseg, int32_t m, const int32_t* lists,
-                             int64_t stride, const int32_t* table, int32_t table_len, const int8_t* code,
+                             int64_t stride, const int32_t* table, int32_t table_len, int64_t n, const int8_t* code,
                              const float* scale, const float* qs, int32_t S, int32_t W, int32_t* cand,
                              float* dist, int32_t* nout, void* stream);
 /** rerank_keep_kernel (search_kernels.cuh:421-467). */

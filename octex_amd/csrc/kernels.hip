@@ -327,7 +327,7 @@ __device__ __forceinline__ int hash_log_dev(int total, int log_cap)
 template <bool kRows>
 __global__ __launch_bounds__(kGatherThreads) void gather_kernel(
   const int2* __restrict__ seg, int nseg, const int* __restrict__ lists, int64_t stride,
-  const int* __restrict__ table, int table_len, const signed char* __restrict__ code,
+  const int* __restrict__ table, int table_len, int64_t N, const signed char* __restrict__ code,
   const float* __restrict__ scale, const float* __restrict__ qs, int S, int W, int logW,
   int* __restrict__ cand, float* __restrict__ dist, int* __restrict__ nout)
 {
@@ -389,7 +389,7 @@ __global__ __launch_bounds__(kGatherThreads) void gather_kernel(
       } else {
         v = lists[static_cast<int64_t>(lo) * stride + st[lo] + (i - pre[lo])];
       }
-      if (v >= 0) {
+      if (v >= 0 && v < N) {  // -1: padding of a table row (search_kernels.cuh:213)
         unsigned s = (static_cast<unsigned>(v) * kIdHash) & (HT - 1);
         for (int p = 0; p < HT; p++) {
           int prev = atomicCAS(&ht[s], -1, v);
@@ -938,7 +938,7 @@ auto gather_smem(int W, int S, int nseg) -> size_t
 }
 
 void launch_gather(bool rows, const int2* seg, int nseg, int m, const int* lists, int64_t stride,
-                   const int* table, int table_len, const signed char* code, const float* scale,
+                   const int* table, int table_len, int64_t n, const signed char* code, const float* scale,
                    const float* qs, int S, int W, int logW, int* cand, float* dist, int* nout,
                    hipStream_t s)
 {
@@ -951,12 +951,12 @@ void launch_gather(bool rows, const int2* seg, int nseg, int m, const int* lists
   if (rows) {
     OCTEX_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gather_kernel<true>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
-    gather_kernel<true><<<m, kGatherThreads, smem, s>>>(seg, nseg, lists, stride, table, table_len, code,
+    gather_kernel<true><<<m, kGatherThreads, smem, s>>>(seg, nseg, lists, stride, table, table_len, n, code,
                                                         scale, qs, S, W, logW, cand, dist, nout);
   } else {
     OCTEX_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gather_kernel<false>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
-    gather_kernel<false><<<m, kGatherThreads, smem, s>>>(seg, nseg, lists, stride, table, table_len, code,
+    gather_kernel<false><<<m, kGatherThreads, smem, s>>>(seg, nseg, lists, stride, table, table_len, n, code,
                                                          scale, qs, S, W, logW, cand, dist, nout);
   }
   OCTEX_HIP(hipGetLastError());

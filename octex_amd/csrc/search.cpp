@@ -58,7 +58,7 @@ void first_round(index_impl const& ix, plan const& pl, hipStream_t s)
   launch_probe(pl.Y.as<__half>(), m, C, ix.levels(), ix.blocks, ix.inv_f.as<float>(), ix.offsets.as<int>(),
                ix.T1, ix.keys.as<long long>(), ix.mmax, ix.base.as<int>(), ix.list_len, pl.lr,
                ix.log_buckets, pl.seg.as<int2>(), s);
-  launch_gather(false, pl.seg.as<int2>(), C, m, ix.lists.as<int>(), ix.stride, nullptr, 0, ix.code(),
+  launch_gather(false, pl.seg.as<int2>(), C, m, ix.lists.as<int>(), ix.stride, nullptr, 0, ix.n, ix.code(),
                 ix.scale.as<float>(), pl.qs.as<float>(), S, pl.W, pl.logW, pl.cand.as<int>(),
                 pl.dist.as<float>(), pl.nin.as<int>(), s);
   if (pl.sp.sketch_rank)
@@ -78,7 +78,7 @@ void wave_round(index_impl const& ix, plan const& pl, hipStream_t s)
   for (int wv = 0; wv < nw; wv++) {
     launch_pick_starts(pl.si.as<long long>(), m, pl.KO, pl.done.as<long long>(), st * nw, wv * st, st,
                        ix.table_len, pl.seg2.as<int2>(), s);
-    launch_gather(true, pl.seg2.as<int2>(), st, m, nullptr, 0, ix.rows(), ix.table_len, ix.code(),
+    launch_gather(true, pl.seg2.as<int2>(), st, m, nullptr, 0, ix.rows(), ix.table_len, ix.n, ix.code(),
                   ix.scale.as<float>(), pl.qs.as<float>(), S, pl.W2, pl.logW2, pl.cand2.as<int>(),
                   pl.dist2.as<float>(), pl.n2.as<int>(), s);
     if (pl.sp.sketch_rank)

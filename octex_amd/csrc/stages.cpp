@@ -92,7 +92,7 @@ extern "C" cuvsError_t octexStageProbe(const void* Y, int32_t m, int32_t C, int3
 
 extern "C" cuvsError_t octexStageGather(int32_t rows, const int32_t* seg, int32_t nseg, int32_t m,
                                         const int32_t* lists, int64_t stride, const int32_t* table,
-                                        int32_t table_len, const int8_t* code, const float* scale, const float* qs,
+                                        int32_t table_len, int64_t n, const int8_t* code, const float* scale, const float* qs,
                                         int32_t S, int32_t W, int32_t* cand, float* dist, int32_t* nout,
                                         void* stream)
 {
@@ -104,7 +104,7 @@ extern "C" cuvsError_t octexStageGather(int32_t rows, const int32_t* seg, int32_
     else
       need(lists, "lists");
     OCTEX_EXPECTS(W >= (1 << kMinLogHash) && (W & (W - 1)) == 0, "octex: W must be a power of two >= 2048");
-    launch_gather(rows != 0, reinterpret_cast<const int2*>(seg), nseg, m, lists, stride, table, table_len,
+    launch_gather(rows != 0, reinterpret_cast<const int2*>(seg), nseg, m, lists, stride, table, table_len, n,
                   reinterpret_cast<const signed char*>(code), scale, qs, S, W, log2_ceil(W), cand, dist,
                   nout, s);
   });

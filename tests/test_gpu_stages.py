@@ -27,10 +27,12 @@ def L():
 
 
 def dev(a):
-    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    return torch.from_numpy(np.array(a, copy=True)).cuda()
 
 
 def P(t):
+    """The device address of a tensor; the caller keeps the tensor alive (a temporary would be freed, and its
+    block reused by the next allocation, before the kernel reads it)."""
     return ct.c_void_p(t.data_ptr())
 
 
@@ -103,8 +105,8 @@ def test_projection_within_one_ulp(L, m, K, N):
     shift = g.uniform(0, 2, N).astype(np.float16)
     dY = torch.empty((m, N), dtype=torch.int16, device="cuda")
     ucatT = np.ascontiguousarray(ucat.T)
-    L.call("octexStageProject", P(dev(qh.view(np.int16))), P(dev(ucatT.view(np.int16))), P(dev(shift.view(np.int16))),
-           i32(m), i32(K), i32(N), P(dY), None)
+    dqh, du, ds = dev(qh.view(np.int16)), dev(ucatT.view(np.int16)), dev(shift.view(np.int16))
+    L.call("octexStageProject", P(dqh), P(du), P(ds), i32(m), i32(K), i32(N), P(dY), None)
     Y, Yd = O.project(qh.view(np.uint16), ucat.view(np.uint16), shift.view(np.uint16))
     got = host(dY).view(np.uint16)
     u = ulp_diff(got, Y)
@@ -117,7 +119,8 @@ def test_sketch_query_kernel(L):
     qc = g.standard_normal((500, 96)).astype(np.float32)
     basis = g.standard_normal((96, 64)).astype(np.float32)
     qs = torch.empty((500, 64), dtype=torch.float32, device="cuda")
-    L.call("octexStageSketchQuery", P(dev(qc)), P(dev(basis)), i32(500), i32(96), i32(64), P(qs), None)
+    dqc, db = dev(qc), dev(basis)
+    L.call("octexStageSketchQuery", P(dqc), P(db), i32(500), i32(96), i32(64), P(qs), None)
     ref = qc.astype(np.float64) @ basis.astype(np.float64)
     assert np.allclose(host(qs), ref, rtol=1e-5, atol=1e-4)
 
@@ -151,7 +154,8 @@ def queries_Y(ix, X, extra_random=64, seed=0):
 def run_probe(L, ix, dix, Y, lr):
     m, C = Y.shape[0], ix.copies
     seg = torch.empty((m, C, 2), dtype=torch.int32, device="cuda")
-    L.call("octexStageProbe", P(dev(Y.view(np.int16))), i32(m), i32(C), i32(len(ix.spacings)), i32(ix.blocks),
+    dY = dev(Y.view(np.int16))
+    L.call("octexStageProbe", P(dY), i32(m), i32(C), i32(len(ix.spacings)), i32(ix.blocks),
            P(dix["inv_f"]), P(dix["offsets"]), i64(ix.offsets.shape[2]), P(dix["keys"]), i64(ix.keys.shape[2]),
            P(dix["base"]), i32(ix.list_len), i32(lr), i32(ix.log_buckets), P(seg), None)
     return seg
@@ -171,9 +175,10 @@ def gather_gpu(L, ix, dix, seg, qs, rows, W=4096):
     cand = torch.full((m, W), -5, dtype=torch.int32, device="cuda")
     dist = torch.zeros((m, W), dtype=torch.float32, device="cuda")
     nout = torch.zeros(m, dtype=torch.int32, device="cuda")
+    dqs = dev(qs)
     L.call("octexStageGather", i32(rows), P(seg), i32(nseg), i32(m), P(dix["lists"]), i64(ix.lists.shape[1]),
-           P(dix["table"]), i32(ix.table_len), P(dix["sketch"]), P(dix["scale"]), P(dev(qs)), i32(ix.sketch_width),
-           i32(W), P(cand), P(dist), P(nout), None)
+           P(dix["table"]), i32(ix.table_len), i64(ix.n), P(dix["sketch"]), P(dix["scale"]), P(dqs),
+           i32(ix.sketch_width), i32(W), P(cand), P(dist), P(nout), None)
     return host(cand), host(dist), host(nout)
 
 
@@ -202,7 +207,8 @@ def test_gather_rows_matches_oracle(L, ix, dix):
     seg2[:, -7:] = 0  # unused start points
     seg2[0] = 0  # a query without starts
     qs = g.standard_normal((m, ix.sketch_width)).astype(np.float32)
-    cand, dist, nout = gather_gpu(L, ix, dix, dev(seg2), qs, rows=1)
+    dseg2 = dev(seg2)
+    cand, dist, nout = gather_gpu(L, ix, dix, dseg2, qs, rows=1)
     check_gather(ix, seg2, qs, cand, dist, nout, rows=True)
     assert nout[0] == 0
 
@@ -237,8 +243,9 @@ def test_rerank_keep_matches_oracle(L, ix, dix, small_index, fresh):
             ex = np.array([O.exact_dist(ix.vectors[i], Q[q]) for i in ids], np.float32)
             si[q], sd[q] = O.merge_keep(si[q], sd[q], ids.astype(np.int32), ex, True)
     dsi, dsd = dev(si), dev(sd)
-    L.call("octexStageRerankKeep", P(dev(cand)), P(dev(dist)), P(dev(nin)), i32(m), i32(W), P(dix["vectors"]),
-           i32(ix.dim), P(dev(Q)), i32(R), i32(KO), P(dsi), P(dsd), i32(fresh), None)
+    dc, dd, dn, dQ = dev(cand), dev(dist), dev(nin), dev(Q)
+    L.call("octexStageRerankKeep", P(dc), P(dd), P(dn), i32(m), i32(W), P(dix["vectors"]), i32(ix.dim), P(dQ),
+           i32(R), i32(KO), P(dsi), P(dsd), i32(fresh), None)
     for q in range(m):
         ri, rd = O.rerank_keep(ix, cand[q, : nin[q]], dist[q, : nin[q]], Q[q], R, si[q], sd[q], fresh)
         assert np.array_equal(host(dsi)[q], ri), f"query {q}"
@@ -257,8 +264,8 @@ def test_sketch_keep_matches_oracle(L, fresh):
             ids = g.choice(100_000, 150, replace=False).astype(np.int32)
             si[q], sd[q] = O.merge_keep(si[q], sd[q], ids, g.integers(0, 40, 150).astype(np.float32), True)
     dsi, dsd = dev(si), dev(sd)
-    L.call("octexStageSketchKeep", P(dev(cand)), P(dev(dist)), P(dev(nin)), i32(m), i32(W), i32(KO), P(dsi),
-           P(dsd), i32(fresh), None)
+    dc, dd, dn = dev(cand), dev(dist), dev(nin)
+    L.call("octexStageSketchKeep", P(dc), P(dd), P(dn), i32(m), i32(W), i32(KO), P(dsi), P(dsd), i32(fresh), None)
     for q in range(m):
         ri, rd = O.sketch_keep(cand[q, : nin[q]], dist[q, : nin[q]], si[q], sd[q], fresh)
         assert np.array_equal(host(dsi)[q], ri) and np.array_equal(host(dsd)[q], rd), f"query {q}"
@@ -272,9 +279,9 @@ def test_pick_starts_matches_oracle(L):
     si[:, 200:] = -1
     done = np.full((m, E), -3, np.int64)
     for off in (0, S, 2 * S):
-        dd = dev(done)
+        dd, dsi = dev(done), dev(si)
         seg2 = torch.zeros((m, S, 2), dtype=torch.int32, device="cuda")
-        L.call("octexStagePickStarts", P(dev(si)), i32(m), i32(KO), P(dd), i32(E), i32(off), i32(S), i32(40),
+        L.call("octexStagePickStarts", P(dsi), i32(m), i32(KO), P(dd), i32(E), i32(off), i32(S), i32(40),
                P(seg2), None)
         for q in range(m):
             rdone, rseg = O.pick_starts(si[q], done[q], off, S, 40)
@@ -292,13 +299,15 @@ def test_final_rerank_and_take_k(L, ix, dix, small_index):
     Q = small_index["Q"][:m]
     bi = torch.empty((m, k), dtype=torch.int64, device="cuda")
     bd = torch.empty((m, k), dtype=torch.float32, device="cuda")
-    L.call("octexStageFinalRerank", P(dev(si)), i32(m), i32(KO), i32(R), P(dix["vectors"]), i32(ix.dim), P(dev(Q)),
+    dsi, dQ = dev(si), dev(Q)
+    L.call("octexStageFinalRerank", P(dsi), i32(m), i32(KO), i32(R), P(dix["vectors"]), i32(ix.dim), P(dQ),
            i32(k), P(bi), P(bd), None)
     for q in range(m):
         ri, rd = O.final_rerank(ix, si[q], R, Q[q], k)
         assert np.array_equal(host(bi)[q], ri) and np.array_equal(host(bd)[q], rd)
     sd = g.uniform(0, 1, (m, KO)).astype(np.float32)
-    L.call("octexStageTakeK", P(dev(si)), P(dev(sd)), i32(m), i32(KO), i32(k), P(bi), P(bd), None)
+    dsd = dev(sd)
+    L.call("octexStageTakeK", P(dsi), P(dsd), i32(m), i32(KO), i32(k), P(bi), P(bd), None)
     assert np.array_equal(host(bi), si[:, :k]) and np.array_equal(host(bd), sd[:, :k])
 
 
