@@ -1,0 +1,260 @@
+#!/usr/bin/env python3
+"""Benchmark of octex's batched search on one MI355X: queries/sec at recall@10 >= 0.99 (k = 10), with the achieved
+HBM bandwidth of the dominant kernel against the roofline and the CPU oracle's rate on the same index.
+
+Workload: 1M float32 vectors, d = 128, from a 1,000-component Gaussian mixture
+(centroids uniform in [0, 128], sigma 12), clipped to [0, 255] and rounded; 10,000 queries from the same mixture;
+k = 10, batch 10,000.  Seeded synthetic data (no datasets are downloaded).  The index is built on the GPU by this
+library's builder at the start of the run.
+
+Protocol (the reference's octex_bench.cu:223-242): queries resident in HBM, one capture run, warm-up, then `steps`
+timed searches of the whole batch bracketed by device synchronizations.  A short sweep over search parameters picks
+the fastest setting whose recall@10 against exact search is >= 0.99.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor figure
+
+CONFIGS = {
+    # configs[1] of BASELINE.json
+    "sift1m": dict(n=1_000_000, d=128, nq=10_000, clusters=1000, kind="sift", batch=10_000,
+                   index=dict(copies=200, list_len=32, sketch_width=64, table_len=64, min_cell=2, reverse_edges=False,
+                              seed=0)),
+    # a small stand-in for quick checks
+    "small": dict(n=100_000, d=128, nq=10_000, clusters=100, kind="sift", batch=10_000,
+                  index=dict(copies=64, list_len=32, sketch_width=64, table_len=64, min_cell=2, reverse_edges=False,
+                             seed=0, log_buckets=18)),
+}
+
+SWEEP = [  # ordered from cheaper to dearer
+    dict(read=16, starts=64, waves=1, rerank=64, wave_rerank=64),
+    dict(read=24, starts=64, waves=1, rerank=64, wave_rerank=64),
+    dict(read=32, starts=64, waves=2, rerank=64, wave_rerank=64),
+    dict(read=32, starts=128, waves=2, rerank=128, wave_rerank=128),
+    dict(read=32, starts=128, waves=3, rerank=128, wave_rerank=128),
+]
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def make_data(cfg):
+    """SIFT-like mixture: centroids U[0, 128]^d, sigma 12, clipped to [0, 255], rounded (data seed 0, queries 1)."""
+    d, C = cfg["d"], cfg["clusters"]
+    g = np.random.default_rng(0)
+    centers = g.uniform(0, 128, (C, d)).astype(np.float32)
+    X = np.empty((cfg["n"], d), np.float32)
+    step = 1 << 18
+    for r0 in range(0, cfg["n"], step):
+        m = min(step, cfg["n"] - r0)
+        a = g.integers(0, C, m)
+        X[r0 : r0 + m] = np.rint(np.clip(centers[a] + 12 * g.standard_normal((m, d), dtype=np.float32), 0, 255))
+    gq = np.random.default_rng(1)
+    a = gq.integers(0, C, cfg["nq"])
+    Q = np.rint(np.clip(centers[a] + 12 * gq.standard_normal((cfg["nq"], d), dtype=np.float32), 0, 255))
+    return X, Q.astype(np.float32)
+
+
+def ground_truth(X, Q, k, torch):
+    """Exact k nearest neighbors on the GPU (fp32; integer-valued data makes every distance exact)."""
+    Xd = torch.from_numpy(X).cuda()
+    Qd = torch.from_numpy(Q).cuda()
+    xn = (Xd * Xd).sum(1)
+    best_d = torch.full((len(Q), k), float("inf"), device="cuda")
+    best_i = torch.zeros((len(Q), k), dtype=torch.int64, device="cuda")
+    step = 1 << 17
+    for r0 in range(0, len(X), step):
+        dd = xn[None, r0 : r0 + step] - 2 * (Qd @ Xd[r0 : r0 + step].T)
+        v, i = torch.topk(dd, k, dim=1, largest=False)
+        cd = torch.cat([best_d, v], 1)
+        ci = torch.cat([best_i, i + r0], 1)
+        o = torch.argsort(cd, dim=1)[:, :k]
+        best_d, best_i = torch.gather(cd, 1, o), torch.gather(ci, 1, o)
+    del Xd
+    return best_i.cpu().numpy()
+
+
+def recall(I, gt, k=10):
+    I, gt = np.asarray(I)[:, :k], np.asarray(gt)[:, :k]
+    hits = sum(len(set(a) & set(b)) for a, b in zip(I.tolist(), gt.tolist()))
+    return hits / (k * len(I))
+
+
+def time_search(index, Qd, k, params, steps, warmup, torch):
+    for _ in range(warmup):
+        index.search(Qd, k=k, **params)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        index.search(Qd, k=k, **params)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def stage_bytes(name, wave, cnt, m, C, S, D, KO, table_len, starts, w):
+    """Algorithmic bytes of one launch: every distinct row read once at its natural size (no cache-line inflation)."""
+    if name == "gather_lists":
+        return m * C * 8 + cnt["entries1"] * 4 + cnt["distinct1"] * (S + 8) + m * (S * 4 + 4)
+    if name == "gather_rows":
+        return m * starts * 8 + cnt["starts2"][wave] * table_len * 4 + cnt["distinct2"][wave] * (S + 8) + m * (S * 4 + 4)
+    if name == "rerank_keep":
+        return cnt["distinct1"] * 8 + cnt["reranked1"] * 2 * D + m * (12 * KO + 4 * D + 4)
+    if name == "rerank_keep_wave":
+        return cnt["distinct2"][wave] * 8 + cnt["reranked2"][wave] * 2 * D + m * (24 * KO + 4 * D + 4)
+    if name == "probe":  # Y rows, one offsets pair and one key per (query, copy), the segment out
+        return m * C * (2 * w + 8 + 8 + 8)
+    if name == "project":
+        return m * D * 2 + C * w * D * 2 + m * C * w * 2
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="sift1m", choices=sorted(CONFIGS))
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU time of the CPU-baseline sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--params", default=None, help="JSON search parameters (skips the sweep)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build searches on one GPU; runs on several GPUs are not part of it", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import octex_amd
+
+    cfg = CONFIGS[args.config]
+    k = 10
+    t0 = time.time()
+    X, Q = make_data(cfg)
+    log(f"data {X.shape} queries {Q.shape} in {time.time() - t0:.1f} s")
+    t0 = time.time()
+    gt = ground_truth(X, Q, k, torch)
+    log(f"ground truth in {time.time() - t0:.1f} s")
+    index, build_s = octex_amd.build_in_memory(X, **cfg["index"])
+    log(f"index built in {build_s:.1f} s: {index}, {index.device_bytes[0] / 2**30:.1f} GiB")
+    Qd = torch.from_numpy(Q).cuda()
+
+    # the fastest sweep point at recall >= 0.99
+    sweep = [json.loads(args.params)] if args.params else SWEEP
+    chosen, points = None, []
+    for p in sweep:
+        p = dict(p, batch=cfg["batch"])
+        D_, I_ = index.search(Qd, k=k, **p)
+        r = recall(I_.cpu().numpy(), gt)
+        s = time_search(index, Qd, k, p, steps=3, warmup=1, torch=torch)
+        points.append(dict(params=p, recall=round(r, 5), qps=round(len(Q) / s)))
+        log(f"sweep {p}: recall {r:.4f}, {len(Q) / s:,.0f} QPS")
+        if r >= 0.99 and (chosen is None or len(Q) / s > chosen["qps"]):
+            chosen = points[-1]
+    if chosen is None:
+        chosen = max(points, key=lambda x: x["recall"])
+    params = chosen["params"]
+
+    # the timed region
+    sec = time_search(index, Qd, k, params, steps=args.steps, warmup=args.warmup, torch=torch)
+    qps = len(Q) / sec
+    D_, I_ = index.search(Qd, k=k, **params)
+    rec = recall(I_.cpu().numpy(), gt)
+    log(f"timed: {sec * 1e3:.3f} ms per batch of {len(Q)}, {qps:,.0f} QPS, recall {rec:.4f}")
+
+    # roofline of the dominant kernel: HIP events around every launch of one batch on the index's stream
+    stages, cnt = index.profile_batch(Qd, k=k, reps=5, **params)
+    info = index.plan_info()
+    C, S, D, w = index.copies, 64 if "sketch_width" not in cfg["index"] else cfg["index"]["sketch_width"], X.shape[1], 32
+    totals, per_launch, waves_seen = {}, [], {}
+    for name, ms in stages:
+        wv = waves_seen.get(name, 0)
+        waves_seen[name] = wv + 1
+        b = stage_bytes(name, wv, cnt, len(Q), C, S, D, info["KO"], 64, params["starts"], w)
+        per_launch.append(dict(stage=name, wave=wv, ms=round(ms, 4), bytes=b,
+                               gbs=round(b / (ms * 1e-3) / 1e9, 1) if b else None))
+        totals[name] = totals.get(name, 0.0) + ms
+    dominant = max(totals, key=totals.get)
+    dl = [x for x in per_launch if x["stage"] == dominant]
+    avg_ms = sum(x["ms"] for x in dl) / len(dl)
+    avg_bytes = sum(x["bytes"] for x in dl) / len(dl)
+    achieved = avg_bytes / (avg_ms * 1e-3) / 1e9
+    log("stages: " + ", ".join(f"{x['stage']}[{x['wave']}] {x['ms']:.3f} ms {x['gbs']} GB/s" for x in per_launch))
+
+    # CPU baseline: the oracle (C++ restatement of the search) on the same index, a bounded query sample
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import oracle as O
+
+        threads = min(16, os.cpu_count() or 1)
+        t0 = time.time()
+        oix = O.Index(index)
+        log(f"oracle index copied to the host in {time.time() - t0:.1f} s")
+        n_s = 64
+        t0 = time.time()
+        O.search(oix, Q[:n_s], k=k, threads=threads, **params)
+        first = time.time() - t0
+        n_s = int(min(len(Q), max(n_s, n_s * args.cpu_seconds / max(first, 1e-3))))
+        t0 = time.time()
+        Dc, Ic = O.search(oix, Q[:n_s], k=k, threads=threads, **params)
+        cs = time.time() - t0
+        cpu = dict(value=round(n_s / cs, 1), unit="queries/s", cores=threads, kind="port",
+                   sample=f"first {n_s} of the {len(Q)} queries, same index and parameters, {cs:.1f} s",
+                   recall=round(recall(Ic, gt[:n_s]), 4))
+        log(f"cpu baseline: {cpu}")
+
+    out = {
+        "metric": "queries/sec at recall@10>=0.99, k=10, 1 MI355X; achieved HBM GB/s",
+        "value": round(qps, 1),
+        "unit": "queries/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sec * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 rerank, int8 sketch, fp32 accumulate",
+        "data": "synthetic (seeded Gaussian mixture, BASELINE.json configs[1])",
+        "config": {
+            "workload": f"{args.config}: {X.shape[0]} x {X.shape[1]} SIFT-like mixture, {len(Q)} queries, k=10, "
+                        f"batch {cfg['batch']}",
+            "index": cfg["index"],
+            "search": params,
+            "recall@10": round(rec, 5),
+            "recall_target_met": rec >= 0.99,
+            "build_seconds": round(build_s, 1),
+            "index_gib": round(index.device_bytes[0] / 2**30, 2),
+            "sweep": points,
+            "stages": per_launch,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": dominant,
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "avg_launch_ms": round(avg_ms, 4),
+            "algorithmic_bytes_per_launch": int(avg_bytes),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -25,6 +25,36 @@ extern "C" {
 cuvsError_t octexIndexCopyPlanBuffer(cuvsOctexIndex_t index, const char* name, void* dst, int64_t bytes,
                                      int64_t* size);
 
+/**
+ * Build the index of a float32 / float16 dataset [n, dim] in the HBM of the current GPU (or
+ * params->devices[0]) and place it in the empty handle `index`, ready to search, without a round
+ * trip through files; with `path` non-NULL the format-1 directory is written as well.  *seconds
+ * (optional) receives the build time.  cuvsOctexBuild + cuvsOctexLoad in one step.
+ */
+cuvsError_t octexBuildInMemory(cuvsResources_t res, cuvsOctexIndexParams_t params, DLManagedTensor* dataset,
+                               const char* path, cuvsOctexIndex_t index, double* seconds);
+
+/**
+ * Profile one batch of queries [m <= batch, dim] (float32, host or device): a normal search, then the
+ * same batch launched kernel by kernel `reps` times with HIP events around every launch on the index's
+ * stream.  names (64 x 32 chars) and ms receive the stages in launch order with their average
+ * milliseconds, *nstages their count; counters (52 int64, optional): probe hits, list entries read,
+ * distinct first-round candidates, first-round reranked, then per wave (16 each) valid start points,
+ * distinct candidates and reranked entries, all summed over the batch's m rows.
+ */
+cuvsError_t octexIndexProfileBatch(cuvsOctexIndex_t index, cuvsOctexSearchParams_t params, DLManagedTensor* queries,
+                                   int64_t k, int32_t reps, char* names, double* ms, int32_t* nstages,
+                                   int64_t* counters);
+
+/**
+ * Copy an array of a loaded or built index to dst (host or device), at most `bytes`; *size receives
+ * its size: "lists" (of copy `copy`), "keys", "offsets", "base", "ucatT", "shift", "inv_f", "mean",
+ * "basis", "scale", "sketch", "vectors", "table", "spacings" (float32), and "meta" (11 int64: n, dim,
+ * copies, blocks, levels, list_len, log_buckets, sketch_width, table_len, mmax, T1).
+ */
+cuvsError_t octexIndexCopyArray(cuvsOctexIndex_t index, const char* name, int32_t copy, void* dst, int64_t bytes,
+                                int64_t* size);
+
 /** The cached plan's shape: {m, k, KO, lr, W, W2, rerank, wave_rerank, final_rerank, graph?}. */
 cuvsError_t octexIndexPlanInfo(cuvsOctexIndex_t index, int32_t* info);
 

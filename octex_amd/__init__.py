@@ -6,7 +6,7 @@ with every search step a hand-written HIP kernel for gfx950.
     D, I = index.search(xq, k=10)          # (distances, neighbors), nearest first
 """
 
-from .index import Index, build, load
+from .index import Index, build, build_in_memory, load
 
 __version__ = "0.1.0"
-__all__ = ["Index", "build", "load", "__version__"]
+__all__ = ["Index", "build", "build_in_memory", "load", "__version__"]

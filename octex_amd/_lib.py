@@ -116,7 +116,7 @@ EXPORTS = (
     "cuvsOctexIndexCreate", "cuvsOctexIndexDestroy", "cuvsOctexIndexGetSize", "cuvsOctexIndexGetDim",
     "cuvsOctexIndexGetCopies", "cuvsOctexIndexGetNumDevices", "cuvsOctexIndexGetDevices",
     "cuvsOctexIndexGetDeviceBytes", "cuvsOctexBuild", "cuvsOctexLoad", "cuvsOctexSearch",
-    "octexIndexCopyPlanBuffer", "octexIndexPlanInfo",
+    "octexIndexCopyPlanBuffer", "octexIndexPlanInfo", "octexBuildInMemory", "octexIndexProfileBatch", "octexIndexCopyArray",
     "octexStageCenter", "octexStageProject", "octexStageSketchQuery", "octexStageE8", "octexStageProbe",
     "octexStageGather", "octexStageRerankKeep", "octexStageSketchKeep", "octexStagePickStarts",
     "octexStageFinalRerank", "octexStageTakeK",

@@ -1,20 +1,713 @@
-// octex::build (octex.hpp:214-222): index construction into a format-1 directory.
-#include "common.hpp"
+// octex::build on one MI355X (the reference: build.cu:104-454, build_setup.cuh:40-175,
+// build_cells.cuh:451-613, build_table.cuh:557-843).  The index is built in HBM:
+//   - PCA of every max(1, n / 200000)-th row: fp64 scatter matrix on the GPU, cyclic Jacobi on the host;
+//   - per copy the seeded rotation of the top pca_dims directions (the reference's generator scheme),
+//     then per spacing the cells (GPU sort of the cell ids) and their member lists;
+//   - the int8 sketch of the top sketch_width directions;
+//   - the neighbor table searched by this library's own search over every base vector (first round,
+//     then 2 and 3 waves over the previous table), with reverse edges merged on the host.
+// build() writes the format-1 directory; build_and_load() keeps the index in HBM as well.
 
-#include <cuvs/neighbors/octex.hpp>
+#include "build_kernels.hpp"
+#include "build.hpp"
+#include "common.hpp"
+#include "index_impl.hpp"
+#include "meta.hpp"
+#include "npy.hpp"
+#include "search.hpp"
+
+#include <hip/hip_fp16.h>
+
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <filesystem>
+#include <fstream>
+#include <numeric>
+#include <random>
+#include <sstream>
+#include <thread>
 
 namespace cuvs::neighbors::octex {
 
-void build(raft::resources const&, index_params const&,
-           raft::host_matrix_view<const float, int64_t, raft::row_major>, std::string const&)
+namespace detail {
+
+namespace {
+
+auto seconds_since(std::chrono::steady_clock::time_point t) -> double
 {
-  detail::fail("octex: build is not available in this build of the library");
+  return std::chrono::duration<double>(std::chrono::steady_clock::now() - t).count();
 }
 
-void build(raft::resources const&, index_params const&,
-           raft::host_matrix_view<const half, int64_t, raft::row_major>, std::string const&)
+void build_log(const char* fmt, ...)
 {
-  detail::fail("octex: build is not available in this build of the library");
+  static const bool on = std::getenv("OCTEX_VERBOSE") != nullptr;
+  if (!on) return;
+  va_list ap;
+  va_start(ap, fmt);
+  std::vfprintf(stderr, fmt, ap);
+  va_end(ap);
+}
+
+template <typename F>
+void parallel_for(int64_t n, F&& f)
+{
+  const int threads = static_cast<int>(std::clamp<int64_t>(n / 4096, 1, 16));
+  if (threads == 1) {
+    f(0, n);
+    return;
+  }
+  std::vector<std::thread> th;
+  for (int t = 0; t < threads; t++)
+    th.emplace_back([&, t] { f(n * t / threads, n * (t + 1) / threads); });
+  for (auto& x : th)
+    x.join();
+}
+
+/** Symmetric eigen decomposition by cyclic Jacobi rotations: values descending, vectors as columns. */
+void jacobi(std::vector<double>& A, int d, std::vector<double>& vals, std::vector<double>& V)
+{
+  V.assign(static_cast<size_t>(d) * d, 0.0);
+  for (int i = 0; i < d; i++)
+    V[static_cast<size_t>(i) * d + i] = 1.0;
+  auto at = [&](int i, int j) -> double& { return A[static_cast<size_t>(i) * d + j]; };
+  for (int sweep = 0; sweep < 60; sweep++) {
+    double off = 0, tot = 0;
+    for (int i = 0; i < d; i++)
+      for (int j = 0; j < d; j++) {
+        double v = at(i, j) * at(i, j);
+        tot += v;
+        if (i != j) off += v;
+      }
+    if (off <= 1e-26 * tot) break;
+    for (int p = 0; p < d; p++)
+      for (int q = p + 1; q < d; q++) {
+        double apq = at(p, q);
+        if (std::fabs(apq) <= 1e-300) continue;
+        double theta = (at(q, q) - at(p, p)) / (2 * apq);
+        double t     = (theta >= 0 ? 1.0 : -1.0) / (std::fabs(theta) + std::sqrt(theta * theta + 1));
+        double c = 1 / std::sqrt(t * t + 1), s = t * c;
+        for (int r = 0; r < d; r++) {  // columns p, q
+          double arp = at(r, p), arq = at(r, q);
+          at(r, p)   = c * arp - s * arq;
+          at(r, q)   = s * arp + c * arq;
+        }
+        for (int r = 0; r < d; r++) {  // rows p, q
+          double apr = at(p, r), aqr = at(q, r);
+          at(p, r)   = c * apr - s * aqr;
+          at(q, r)   = s * apr + c * aqr;
+        }
+        for (int r = 0; r < d; r++) {
+          double vrp = V[static_cast<size_t>(r) * d + p], vrq = V[static_cast<size_t>(r) * d + q];
+          V[static_cast<size_t>(r) * d + p] = c * vrp - s * vrq;
+          V[static_cast<size_t>(r) * d + q] = s * vrp + c * vrq;
+        }
+      }
+  }
+  std::vector<int> order(d);
+  std::iota(order.begin(), order.end(), 0);
+  std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return at(a, a) > at(b, b); });
+  std::vector<double> V2(static_cast<size_t>(d) * d);
+  vals.resize(d);
+  for (int k = 0; k < d; k++) {
+    vals[k] = at(order[k], order[k]);
+    for (int r = 0; r < d; r++)
+      V2[static_cast<size_t>(r) * d + k] = V[static_cast<size_t>(r) * d + order[k]];
+  }
+  V.swap(V2);
+}
+
+auto splitmix64(uint64_t z) -> uint64_t  // build_setup.cuh:105-111
+{
+  z += 0x9E3779B97F4A7C15ULL;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+  return z ^ (z >> 31);
+}
+
+/**
+ * Projections [C, d, w] and shifts [C, w] (build_setup.cuh:119-175): copy c draws a Gaussian [p, w]
+ * matrix from mt19937_64(splitmix64(seed * 0x100000001B3 + c)), orthonormalizes its columns
+ * (Gram-Schmidt), rotates the top-p principal directions with it and divides by the mean projected
+ * standard deviation; its shift is uniform in [0, 2) from the same generator.
+ */
+void make_projections(std::vector<float> const& vectors, std::vector<double> const& values, int64_t samples,
+                      int64_t d, int p, int w, int copies, uint64_t seed, std::vector<float>& proj,
+                      std::vector<float>& shift)
+{
+  OCTEX_EXPECTS(p >= w, "octex: pca_dims must be at least 8 * blocks");
+  OCTEX_EXPECTS(p <= d, "octex: pca_dims exceeds the dimension");
+  proj.assign(static_cast<size_t>(copies) * d * w, 0.f);
+  shift.assign(static_cast<size_t>(copies) * w, 0.f);
+  std::vector<double> q(static_cast<size_t>(p) * w);
+  for (int c = 0; c < copies; c++) {
+    std::mt19937_64 gen(splitmix64(seed * 0x100000001B3ULL + static_cast<uint64_t>(c)));
+    std::normal_distribution<double> normal(0.0, 1.0);
+    std::uniform_real_distribution<double> uni(0.0, 2.0);
+    for (auto& v : q)
+      v = normal(gen);
+    for (int s = 0; s < w; s++) {
+      for (int t = 0; t < s; t++) {
+        double dot = 0;
+        for (int r = 0; r < p; r++)
+          dot += q[r * w + s] * q[r * w + t];
+        for (int r = 0; r < p; r++)
+          q[r * w + s] -= dot * q[r * w + t];
+      }
+      double nrm = 0;
+      for (int r = 0; r < p; r++)
+        nrm += q[r * w + s] * q[r * w + s];
+      nrm = std::sqrt(nrm);
+      for (int r = 0; r < p; r++)
+        q[r * w + s] /= nrm;
+    }
+    double sd = 0;
+    for (int s = 0; s < w; s++) {
+      double v = 0;
+      for (int r = 0; r < p; r++)
+        v += values[r] * q[r * w + s] * q[r * w + s];
+      sd += std::sqrt(v / static_cast<double>(std::max<int64_t>(samples - 1, 1)));
+    }
+    sd /= w;
+    float* u = proj.data() + static_cast<size_t>(c) * d * w;
+    for (int64_t k = 0; k < d; k++)
+      for (int s = 0; s < w; s++) {
+        double v = 0;
+        for (int r = 0; r < p; r++)
+          v += static_cast<double>(vectors[k * d + r]) * q[r * w + s];
+        u[k * w + s] = static_cast<float>(v / sd);
+      }
+    for (int s = 0; s < w; s++)
+      shift[static_cast<size_t>(c) * w + s] = static_cast<float>(uni(gen));
+  }
+}
+
+/** The rule of a merged table row (build_table.cuh:157-164): its first kf forward entries, up to kr
+ * reverse entries (lowest rank first, then lowest id), then its other forward entries; duplicates,
+ * -1 and the row itself dropped; the first kout kept, in that priority order. */
+struct reverse_rule {
+  int kin, kf, ks, kr, kout;
+};
+
+void merge_reverse(std::vector<int32_t> const& fwd, int64_t n, reverse_rule const& rr, std::vector<int32_t>& table)
+{
+  const int kin = rr.kin;
+  std::vector<int32_t> cnt(n + 1, 0);
+  parallel_for(n, [&](int64_t v0, int64_t v1) {
+    for (int64_t v = v0; v < v1; v++)
+      for (int r = 0; r < rr.ks; r++) {
+        int32_t u = fwd[v * kin + r];
+        if (u >= 0 && u != v) __atomic_fetch_add(&cnt[u + 1], 1, __ATOMIC_RELAXED);
+      }
+  });
+  std::vector<int64_t> off(n + 1, 0);
+  for (int64_t u = 0; u < n; u++)
+    off[u + 1] = off[u] + cnt[u + 1];
+  std::vector<uint64_t> ent(off[n]);
+  std::vector<int64_t> cur(off.begin(), off.end() - 1);
+  parallel_for(n, [&](int64_t v0, int64_t v1) {
+    for (int64_t v = v0; v < v1; v++)
+      for (int r = 0; r < rr.ks; r++) {
+        int32_t u = fwd[v * kin + r];
+        if (u >= 0 && u != v) {
+          int64_t at = __atomic_fetch_add(&cur[u], 1, __ATOMIC_RELAXED);
+          ent[at]    = (static_cast<uint64_t>(r) << 32) | static_cast<uint32_t>(v);
+        }
+      }
+  });
+  table.assign(static_cast<size_t>(n) * rr.kout, -1);
+  parallel_for(n, [&](int64_t u0, int64_t u1) {
+    std::vector<int32_t> pri;
+    for (int64_t u = u0; u < u1; u++) {
+      std::sort(ent.begin() + off[u], ent.begin() + off[u + 1]);
+      pri.clear();
+      for (int t = 0; t < rr.kf; t++)
+        pri.push_back(fwd[u * kin + t]);
+      for (int t = 0; t < rr.kr && off[u] + t < off[u + 1]; t++)
+        pri.push_back(static_cast<int32_t>(ent[off[u] + t] & 0xffffffffULL));
+      for (int t = rr.kf; t < kin; t++)
+        pri.push_back(fwd[u * kin + t]);
+      int o = 0;
+      int32_t* row = table.data() + u * rr.kout;
+      for (size_t i = 0; i < pri.size() && o < rr.kout; i++) {
+        int32_t v = pri[i];
+        if (v < 0 || v == u) continue;
+        bool dup = false;
+        for (int j = 0; j < o; j++)
+          dup |= row[j] == v;
+        if (!dup) row[o++] = v;
+      }
+    }
+  });
+}
+
+}  // namespace
+
+/** The neighbor rows [n, k] of an in-memory index, replacing its table (the reference's set_table). */
+void set_table(index_impl& ix, std::vector<int32_t> const& rows, int k)
+{
+  {
+    std::lock_guard<std::mutex> lock(ix.mu);
+    ix.plans.clear();
+  }
+  const size_t bytes = static_cast<size_t>(ix.n) * k * sizeof(int32_t);
+  if (ix.table.size != bytes) {
+    ix.bytes -= static_cast<int64_t>(ix.table.size);
+    ix.table = dbuf();
+    ix.table = dbuf(bytes);
+    ix.bytes += static_cast<int64_t>(bytes);
+  }
+  OCTEX_HIP(hipMemcpy(ix.table.ptr, rows.data(), bytes, hipMemcpyHostToDevice));
+  ix.table_len = k;
+}
+
+void drop_table(index_impl& ix)
+{
+  {
+    std::lock_guard<std::mutex> lock(ix.mu);
+    ix.plans.clear();
+  }
+  ix.bytes -= static_cast<int64_t>(ix.table.size);
+  ix.table     = dbuf();
+  ix.table_len = 0;
+}
+
+/**
+ * The searched neighbor table (build_table.cuh:557-843): forward rows of 3k/2 from a search of every
+ * base vector (the vector itself dropped), passes with 0, 2 and 3 waves over the previous table,
+ * reverse edges merged by the rule kf = k/4 forward first, then up to k - kf reverse entries.
+ */
+void searched_table(index_impl& ix, index const& idx, int k, bool reverse_edges, int passes, bool sketch_order,
+                    std::vector<int32_t>& table)
+{
+  const int64_t n = ix.n, d = ix.dim;
+  const int kin = k + k / 2, kq = kin + 1;
+  OCTEX_EXPECTS(k >= 1 && kq < n, "octex: table_len too large for the dataset");
+  const int kf = std::max(1, k / 4);
+  reverse_rule rr{kin, kf, kin, std::max(1, k - kf), k};
+  struct pass_t {
+    int waves, starts;
+  };
+  std::vector<pass_t> plan{{0, 64}, {2, 128}, {3, 128}};
+  plan.resize(std::clamp(passes, 1, 3));
+  for (auto& p : plan)
+    p.starts = std::max(p.starts, kin + 1);
+  search_params sp;
+  sp.read         = 64;
+  sp.batch        = 10000;
+  sp.sketch_rank  = true;
+  sp.final_rerank = sketch_order ? 0 : std::max(64, kin + 1);
+  std::vector<int32_t> fwd(static_cast<size_t>(n) * kin);
+  const int64_t chunk = std::min<int64_t>(n, int64_t{1} << 20);
+  dbuf qf(static_cast<size_t>(chunk) * d * sizeof(float));
+  dbuf nb(static_cast<size_t>(chunk) * kq * sizeof(int64_t)), nd(static_cast<size_t>(chunk) * kq * sizeof(float));
+  std::vector<int64_t> hnb(static_cast<size_t>(chunk) * kq);
+  raft::resources res;
+  res.set_stream(ix.stream);
+  for (size_t v = 0; v < plan.size(); v++) {
+    auto t0 = std::chrono::steady_clock::now();
+    if (plan[v].waves > 0) set_table(ix, table, k);
+    sp.starts = plan[v].starts;
+    sp.waves  = plan[v].waves;
+    for (int64_t r0 = 0; r0 < n; r0 += chunk) {
+      const int64_t m = std::min(chunk, n - r0);
+      half_to_float(ix.vectors.as<__half>() + r0 * d, m * d, qf.as<float>(), ix.stream);
+      search_impl(res, sp, idx, qf.as<float>(), m, d, nb.as<int64_t>(), nd.as<float>(), kq, false, false);
+      OCTEX_HIP(hipStreamSynchronize(ix.stream));
+      OCTEX_HIP(hipMemcpy(hnb.data(), nb.ptr, sizeof(int64_t) * m * kq, hipMemcpyDeviceToHost));
+      parallel_for(m, [&](int64_t i0, int64_t i1) {  // drop the vector itself, keep the first kin
+        for (int64_t i = i0; i < i1; i++) {
+          int32_t* o = fwd.data() + (r0 + i) * kin;
+          int t      = 0;
+          for (int j = 0; j < kq && t < kin; j++) {
+            int64_t u = hnb[i * kq + j];
+            if (u == r0 + i) continue;
+            o[t++] = u < 0 ? -1 : static_cast<int32_t>(u);
+          }
+          for (; t < kin; t++)
+            o[t] = -1;
+        }
+      });
+    }
+    if (plan[v].waves > 0) drop_table(ix);
+    if (reverse_edges) {
+      merge_reverse(fwd, n, rr, table);
+    } else {
+      table.assign(static_cast<size_t>(n) * k, -1);
+      parallel_for(n, [&](int64_t i0, int64_t i1) {
+        for (int64_t i = i0; i < i1; i++)
+          std::copy_n(fwd.data() + i * kin, k, table.data() + i * k);
+      });
+    }
+    build_log("table pass %zu (%d waves): %.2f s\n", v + 1, plan[v].waves, seconds_since(t0));
+  }
+}
+
+auto build_in_memory(index_params const& params, const __half* x, int64_t n, int64_t d, build_record& rec)
+  -> std::shared_ptr<index_impl>
+{
+  const auto t_all = std::chrono::steady_clock::now();
+  const int C = params.copies, b = params.blocks, w = 8 * b, l = params.list_len;
+  const int L     = static_cast<int>(params.spacings.size());
+  const int64_t T = int64_t{1} << params.log_buckets;
+  const int S     = params.sketch_width > 0
+                      ? static_cast<int>(std::min<int64_t>(params.sketch_width, d))
+                      : static_cast<int>(std::max<int64_t>(std::min<int64_t>(d / 16 * 16, 128), std::min<int64_t>(d, 16)));
+  const int k = params.table_len;
+  OCTEX_EXPECTS(C >= 1, "octex: at least one copy");
+  OCTEX_EXPECTS(n >= 2 && d >= 1, "octex: empty dataset");
+  OCTEX_EXPECTS(b >= 1 && b <= 8 && b != 7, "octex: blocks must be 1-6 or 8");
+  OCTEX_EXPECTS(L >= 1, "octex: at least one spacing");
+  OCTEX_EXPECTS(n >= l && l >= 1, "octex: fewer vectors than the list length");
+  OCTEX_EXPECTS(n < (int64_t{1} << 31), "octex: at most 2^31 - 1 vectors");
+  OCTEX_EXPECTS(params.log_buckets >= 1 && params.log_buckets <= 30, "octex: log_buckets in [1, 30]");
+  OCTEX_EXPECTS(d % 2 == 0, "octex: the dimension must be even");
+  OCTEX_EXPECTS(S % 16 == 0 && S <= 512, "octex: sketch width: a multiple of 16, <= 512");
+  OCTEX_EXPECTS(!params.exact_lists,
+                "octex: exact_lists is not supported by this builder (lists come from the cell members)");
+  int cur = 0;
+  OCTEX_HIP(hipGetDevice(&cur));
+  auto impl = std::make_shared<index_impl>();
+  auto& ix  = *impl;
+  ix.device = params.devices.empty() ? cur : params.devices.front();
+  ix.devices = {ix.device};
+  OCTEX_HIP(hipSetDevice(ix.device));
+  OCTEX_HIP(hipStreamCreateWithFlags(&ix.stream, hipStreamNonBlocking));
+  hipStream_t s = ix.stream;
+  ix.n = n, ix.dim = d, ix.copies = C, ix.blocks = b, ix.list_len = l, ix.log_buckets = params.log_buckets;
+  ix.sketch_width = S;
+  ix.spacings     = params.spacings;
+  auto t = std::chrono::steady_clock::now();
+  auto phase = [&](const char* name) {
+    rec.phases.emplace_back(name, seconds_since(t));
+    build_log("%s: %.2f s\n", name, rec.phases.back().second);
+    t = std::chrono::steady_clock::now();
+  };
+
+  // the fp16 vectors: the index's own, read by every step of the build
+  ix.vectors = dbuf(static_cast<size_t>(n) * d * sizeof(__half));
+  ix.bytes += static_cast<int64_t>(ix.vectors.size);
+  OCTEX_HIP(hipMemcpy(ix.vectors.ptr, x, ix.vectors.size, hipMemcpyHostToDevice));
+  const __half* xd = ix.vectors.as<__half>();
+
+  // PCA of a sample (build_setup.cuh:40-103)
+  const int64_t step = std::max<int64_t>(1, n / 200000), ns = (n + step - 1) / step;
+  std::vector<double> mu(d, 0.0);
+  for (int64_t i = 0; i < ns; i++)
+    for (int64_t j = 0; j < d; j++)
+      mu[j] += static_cast<double>(__half2float(x[i * step * d + j]));
+  rec.mean.resize(d);
+  for (int64_t j = 0; j < d; j++)
+    rec.mean[j] = static_cast<float>(mu[j] / static_cast<double>(ns));
+  ix.mean = dbuf(d * sizeof(float));
+  OCTEX_HIP(hipMemcpy(ix.mean.ptr, rec.mean.data(), d * sizeof(float), hipMemcpyHostToDevice));
+  std::vector<double> G(static_cast<size_t>(d) * d);
+  {
+    dbuf dG(G.size() * sizeof(double));
+    pca_scatter(xd, n, static_cast<int>(d), step, ns, ix.mean.as<float>(), dG.as<double>(), s);
+    OCTEX_HIP(hipMemcpy(G.data(), dG.ptr, dG.size, hipMemcpyDeviceToHost));
+  }
+  std::vector<double> vals, V;
+  jacobi(G, static_cast<int>(d), vals, V);
+  std::vector<float> pvec(static_cast<size_t>(d) * d);
+  for (size_t i = 0; i < pvec.size(); i++)
+    pvec[i] = static_cast<float>(V[i]);
+  const int p = std::min<int>(params.pca_dims, static_cast<int>(d));
+  make_projections(pvec, vals, ns, d, p, w, C, params.seed, rec.proj, rec.shift);
+  phase("setup");
+
+  // cells of every copy
+  ix.offsets = dbuf(static_cast<size_t>(C) * L * (T + 1) * sizeof(int32_t));
+  ix.bytes += static_cast<int64_t>(ix.offsets.size);
+  ix.T1 = T + 1;
+  rec.base.assign(static_cast<size_t>(C) * L, 0);
+  rec.cells.assign(static_cast<size_t>(C) * L, 0);
+  std::vector<std::vector<dbuf>> level_keys(C);
+  ix.copy_lists.resize(C);
+  ix.list_rows.resize(C);
+  {
+    cell_builder cb;
+    cb.reserve(n, w, s);
+    dbuf y(static_cast<size_t>(n) * w * sizeof(float)), U(static_cast<size_t>(d) * w * sizeof(float)),
+      sh(w * sizeof(float));
+    for (int c = 0; c < C; c++) {
+      OCTEX_HIP(hipMemcpy(U.ptr, rec.proj.data() + static_cast<size_t>(c) * d * w, U.size, hipMemcpyHostToDevice));
+      OCTEX_HIP(hipMemcpy(sh.ptr, rec.shift.data() + static_cast<size_t>(c) * w, sh.size, hipMemcpyHostToDevice));
+      project_rows(xd, n, static_cast<int>(d), ix.mean.as<float>(), U.as<float>(), sh.as<float>(), w, y.as<float>(), s);
+      std::vector<dbuf> level_lists(L);
+      level_keys[c].resize(L);
+      int64_t row = 0;
+      for (int j = 0; j < L; j++) {
+        const int mc = (params.min_cell > 1 && j < L - 1) ? params.min_cell : 1;
+        int* offs    = ix.offsets.as<int32_t>() + (static_cast<int64_t>(c) * L + j) * (T + 1);
+        int64_t M    = cb.level(y.as<float>(), b, params.spacings[j], mc, l, params.log_buckets, offs,
+                                level_keys[c][j], level_lists[j]);
+        rec.base[static_cast<size_t>(c) * L + j]  = static_cast<int32_t>(row);
+        rec.cells[static_cast<size_t>(c) * L + j] = M;
+        row += M;
+      }
+      OCTEX_EXPECTS(row * l < (int64_t{1} << 31), "octex: a copy holds more than 2^31 list entries");
+      ix.list_rows[c]     = row;
+      ix.copy_lists[c]    = dbuf(static_cast<size_t>(std::max<int64_t>(row * l, 1)) * sizeof(int32_t));
+      int64_t at          = 0;
+      for (int j = 0; j < L; j++) {
+        const int64_t M = rec.cells[static_cast<size_t>(c) * L + j];
+        if (M > 0)
+          OCTEX_HIP(hipMemcpyAsync(ix.copy_lists[c].as<int32_t>() + at * l, level_lists[j].ptr,
+                                   static_cast<size_t>(M) * l * sizeof(int32_t), hipMemcpyDeviceToDevice, s));
+        at += M;
+      }
+      OCTEX_HIP(hipStreamSynchronize(s));
+      ix.bytes += static_cast<int64_t>(ix.copy_lists[c].size);
+    }
+  }
+  // keys [C, L, mmax], zero padded; the per-copy list pointers
+  int64_t mmax = 1;
+  for (auto v : rec.cells)
+    mmax = std::max(mmax, v);
+  ix.mmax = mmax;
+  ix.keys = dbuf(static_cast<size_t>(C) * L * mmax * sizeof(int64_t));
+  ix.bytes += static_cast<int64_t>(ix.keys.size);
+  OCTEX_HIP(hipMemsetAsync(ix.keys.ptr, 0, ix.keys.size, s));
+  for (int c = 0; c < C; c++)
+    for (int j = 0; j < L; j++) {
+      const int64_t M = rec.cells[static_cast<size_t>(c) * L + j];
+      if (M > 0)
+        OCTEX_HIP(hipMemcpyAsync(ix.keys.as<int64_t>() + (static_cast<int64_t>(c) * L + j) * mmax,
+                                 level_keys[c][j].ptr, M * sizeof(int64_t), hipMemcpyDeviceToDevice, s));
+    }
+  OCTEX_HIP(hipStreamSynchronize(s));
+  level_keys.clear();
+  {
+    std::vector<long long> hp(C);
+    for (int c = 0; c < C; c++)
+      hp[c] = reinterpret_cast<long long>(ix.copy_lists[c].ptr);
+    ix.list_ptr = dbuf(hp.size() * sizeof(long long));
+    OCTEX_HIP(hipMemcpy(ix.list_ptr.ptr, hp.data(), ix.list_ptr.size, hipMemcpyHostToDevice));
+    ix.base = dbuf(rec.base.size() * sizeof(int32_t));
+    OCTEX_HIP(hipMemcpy(ix.base.ptr, rec.base.data(), ix.base.size, hipMemcpyHostToDevice));
+  }
+  // the search-side arrays of the loader (load.cu:385-402): fp16 ucatT and shift, inv_f of the JSON text
+  {
+    std::vector<__half> uc(static_cast<size_t>(C) * w * d), shh(static_cast<size_t>(C) * w);
+    for (int c = 0; c < C; c++)
+      for (int sI = 0; sI < w; sI++) {
+        for (int64_t k2 = 0; k2 < d; k2++)
+          uc[(static_cast<size_t>(c) * w + sI) * d + k2] = __float2half(rec.proj[(static_cast<size_t>(c) * d + k2) * w + sI]);
+        shh[static_cast<size_t>(c) * w + sI] = __float2half(rec.shift[static_cast<size_t>(c) * w + sI]);
+      }
+    std::vector<float> inv(L);
+    for (int j = 0; j < L; j++)
+      inv[j] = static_cast<float>(1.0 / std::strtod(json_float(params.spacings[j]).c_str(), nullptr));
+    ix.ucatT = dbuf(uc.size() * sizeof(__half));
+    ix.shift = dbuf(shh.size() * sizeof(__half));
+    ix.inv_f = dbuf(inv.size() * sizeof(float));
+    OCTEX_HIP(hipMemcpy(ix.ucatT.ptr, uc.data(), ix.ucatT.size, hipMemcpyHostToDevice));
+    OCTEX_HIP(hipMemcpy(ix.shift.ptr, shh.data(), ix.shift.size, hipMemcpyHostToDevice));
+    OCTEX_HIP(hipMemcpy(ix.inv_f.ptr, inv.data(), ix.inv_f.size, hipMemcpyHostToDevice));
+  }
+  phase("copies");
+
+  // sketch (build.cu:286-305)
+  rec.basis.resize(static_cast<size_t>(d) * S);
+  for (int64_t r = 0; r < d; r++)
+    for (int sI = 0; sI < S; sI++)
+      rec.basis[r * S + sI] = pvec[r * d + sI];
+  ix.basis  = dbuf(rec.basis.size() * sizeof(float));
+  ix.sketch = dbuf(static_cast<size_t>(n) * S);
+  ix.bytes += static_cast<int64_t>(ix.sketch.size);
+  OCTEX_HIP(hipMemcpy(ix.basis.ptr, rec.basis.data(), ix.basis.size, hipMemcpyHostToDevice));
+  make_sketch(xd, n, static_cast<int>(d), ix.mean.as<float>(), ix.basis.as<float>(), S, rec.scale,
+              ix.sketch.as<signed char>(), s);
+  ix.scale = dbuf(S * sizeof(float));
+  OCTEX_HIP(hipMemcpy(ix.scale.ptr, rec.scale.data(), ix.scale.size, hipMemcpyHostToDevice));
+  phase("sketch");
+
+  // neighbor table, searched by this library's search
+  if (k > 0) {
+    index idx(impl);
+    std::vector<int32_t> table;
+    searched_table(ix, idx, k, params.reverse_edges, params.table_passes, params.table_sketch_order, table);
+    set_table(ix, table, k);
+    phase("table");
+  }
+  OCTEX_HIP(hipSetDevice(cur));
+  rec.phases.emplace_back("total", seconds_since(t_all));
+  return impl;
+}
+
+namespace {
+
+/** Streams an .npy file: header first, then the data in pieces. */
+class npy_stream {
+ public:
+  npy_stream(std::string const& path, const char* descr, std::vector<int64_t> const& shape) : path_(path)
+  {
+    std::string sh = "(";
+    for (size_t i = 0; i < shape.size(); i++) {
+      sh += std::to_string(shape[i]);
+      if (shape.size() == 1 || i + 1 < shape.size()) sh += ",";
+      if (i + 1 < shape.size()) sh += " ";
+    }
+    sh += ")";
+    std::string hdr = std::string("{'descr': '") + descr + "', 'fortran_order': False, 'shape': " + sh + ", }";
+    const size_t total = 10 + hdr.size() + 1;
+    hdr.append((64 - total % 64) % 64, ' ');
+    hdr += '\n';
+    f_ = std::fopen(path.c_str(), "wb");
+    OCTEX_EXPECTS(f_ != nullptr, "octex: cannot write %s", path.c_str());
+    const char magic[8] = {'\x93', 'N', 'U', 'M', 'P', 'Y', '\x01', '\x00'};
+    const uint16_t hl   = static_cast<uint16_t>(hdr.size());
+    put(magic, 8);
+    put(&hl, 2);
+    put(hdr.data(), hdr.size());
+  }
+  void put(const void* p, size_t bytes)
+  {
+    OCTEX_EXPECTS(bytes == 0 || std::fwrite(p, 1, bytes, f_) == bytes, "octex: short write %s", path_.c_str());
+  }
+  void zeros(size_t bytes)
+  {
+    static const std::vector<char> z(1 << 20, 0);
+    while (bytes > 0) {
+      size_t m = std::min(bytes, z.size());
+      put(z.data(), m);
+      bytes -= m;
+    }
+  }
+  void put_device(const void* p, size_t bytes)
+  {
+    constexpr size_t kChunk = size_t{64} << 20;
+    std::vector<char> h(std::min(bytes, kChunk));
+    for (size_t o = 0; o < bytes; o += kChunk) {
+      size_t m = std::min(kChunk, bytes - o);
+      OCTEX_HIP(hipMemcpy(h.data(), static_cast<const char*>(p) + o, m, hipMemcpyDeviceToHost));
+      put(h.data(), m);
+    }
+  }
+  ~npy_stream()
+  {
+    if (f_ != nullptr) std::fclose(f_);
+  }
+  void close()
+  {
+    OCTEX_EXPECTS(std::fclose(f_) == 0, "octex: short write %s", path_.c_str());
+    f_ = nullptr;
+  }
+
+ private:
+  std::string path_;
+  FILE* f_ = nullptr;
+};
+
+}  // namespace
+
+void write_index(index_impl const& ix, build_record const& rec, index_params const& params, std::string const& path)
+{
+  namespace fs = std::filesystem;
+  fs::create_directories(path);
+  auto file = [&](const char* name) { return (fs::path(path) / name).string(); };
+  const int C = ix.copies, L = ix.levels(), w = 8 * ix.blocks, l = ix.list_len, S = ix.sketch_width;
+  const int64_t n = ix.n, d = ix.dim, T1 = ix.T1;
+  OCTEX_HIP(hipSetDevice(ix.device));
+  write_npy(file("mean.npy"), rec.mean.data(), {d});
+  write_npy(file("proj.npy"), rec.proj.data(), {C, d, w});
+  write_npy(file("shift.npy"), rec.shift.data(), {C, w});
+  write_npy(file("base.npy"), rec.base.data(), {C, L});
+  write_npy(file("cells.npy"), rec.cells.data(), {C, L});
+  {
+    npy_stream k(file("keys.npy"), "<i8", {C, L, ix.mmax});
+    k.put_device(ix.keys.ptr, ix.keys.size);
+    k.close();
+  }
+  {
+    npy_stream o(file("offsets.npy"), "<i4", {C, L, T1});
+    o.put_device(ix.offsets.ptr, ix.offsets.size);
+    o.close();
+  }
+  {
+    int64_t lmax = 0;
+    for (auto r : ix.list_rows)
+      lmax = std::max(lmax, r * l);
+    npy_stream ls(file("lists.npy"), "<i4", {C, lmax});
+    for (int c = 0; c < C; c++) {
+      const size_t bytes = static_cast<size_t>(ix.list_rows[c] * l) * sizeof(int32_t);
+      ls.put_device(ix.copy_lists[c].ptr, bytes);
+      ls.zeros(static_cast<size_t>(lmax) * sizeof(int32_t) - bytes);
+    }
+    ls.close();
+  }
+  write_npy(file("sketch_basis.npy"), rec.basis.data(), {d, int64_t{S}});
+  write_npy(file("sketch_scale.npy"), rec.scale.data(), {int64_t{S}});
+  {
+    npy_stream sk(file("sketch.npy"), "|i1", {n, int64_t{S}});
+    sk.put_device(ix.sketch.ptr, static_cast<size_t>(n) * S);
+    sk.close();
+  }
+  {
+    npy_stream v(file("vectors.npy"), "<f2", {n, d});
+    v.put_device(ix.vectors.ptr, static_cast<size_t>(n) * d * sizeof(__half));
+    v.close();
+  }
+  if (ix.table_len > 0) {
+    npy_stream t(file("table.npy"), "<i4", {n, int64_t{ix.table_len}});
+    t.put_device(ix.table.ptr, static_cast<size_t>(n) * ix.table_len * sizeof(int32_t));
+    t.close();
+  }
+  // meta.json last: a directory without it is incomplete (build.cu:67-98, 423-424)
+  std::ostringstream m;
+  m << "{\n \"format\": 1,\n \"n\": " << n << ",\n \"dim\": " << d << ",\n \"copies\": " << C
+    << ",\n \"blocks\": " << ix.blocks << ",\n \"spacings\": [";
+  for (int j = 0; j < L; j++)
+    m << (j ? ", " : "") << json_float(params.spacings[j]);
+  m << "],\n \"list_len\": " << l << ",\n \"log_buckets\": " << ix.log_buckets << ",\n \"sketch_width\": " << S
+    << ",\n \"table_len\": " << ix.table_len << ",\n \"metric\": \"sqeuclidean\",\n \"files\": {}";
+  if (!rec.phases.empty()) {
+    m << ",\n \"build_seconds\": {";
+    for (size_t i = 0; i < rec.phases.size(); i++) {
+      char buf[64];
+      std::snprintf(buf, sizeof(buf), "%.3f", rec.phases[i].second);
+      m << (i ? ", " : "") << "\"" << rec.phases[i].first << "\": " << buf;
+    }
+    m << "}";
+  }
+  m << "\n}\n";
+  std::ofstream(file("meta.json")) << m.str();
+}
+
+}  // namespace detail
+
+namespace {
+
+void build_half(index_params const& params, const __half* x, int64_t n, int64_t d, std::string const& path)
+{
+  detail::build_record rec;
+  auto impl = detail::build_in_memory(params, x, n, d, rec);
+  detail::write_index(*impl, rec, params, path);
+}
+
+}  // namespace
+
+void build(raft::resources const&, index_params const& params,
+           raft::host_matrix_view<const float, int64_t, raft::row_major> dataset, std::string const& path)
+{
+  const int64_t n = dataset.extent(0), d = dataset.extent(1);
+  std::vector<__half> xh(static_cast<size_t>(n) * d);
+  const float* src = dataset.data_handle();
+  detail::parallel_for(n * d, [&](int64_t i0, int64_t i1) {
+    for (int64_t i = i0; i < i1; i++)
+      xh[i] = __float2half(src[i]);
+  });
+  build_half(params, xh.data(), n, d, path);
+}
+
+void build(raft::resources const&, index_params const& params,
+           raft::host_matrix_view<const half, int64_t, raft::row_major> dataset, std::string const& path)
+{
+  build_half(params, dataset.data_handle(), dataset.extent(0), dataset.extent(1), path);
 }
 
 }  // namespace cuvs::neighbors::octex

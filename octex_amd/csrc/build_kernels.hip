@@ -1,0 +1,471 @@
+// Kernels of the octex index builder on MI355X (the reference: detail/build_cells.cuh,
+// build_setup.cuh, build_common.cuh).  Cells of a copy are found by sorting the 64-bit cell ids of all
+// rows (rocPRIM radix sort), their lists from the members of each cell sorted by their distance to the
+// cell center (a second radix sort on (cell, distance)), and the (bucket, id) order with CSR offsets.
+
+#include "build_kernels.hpp"
+#include "common.hpp"
+#include "e8_device.hpp"
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <rocprim/device/device_radix_sort.hpp>
+#include <rocprim/device/device_scan.hpp>
+
+#include <cstdint>
+
+namespace cuvs::neighbors::octex::detail {
+
+namespace {
+
+constexpr int kMaxW = 64;  // 8 * blocks
+
+/** A[i, :] = x[i * step, :] - mean (fp64), for the scatter matrix of the PCA sample. */
+__global__ void pca_sample_kernel(const __half* __restrict__ x, int64_t ns, int64_t step, int d,
+                                  const float* __restrict__ mean, double* __restrict__ A)
+{
+  int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= ns * d) return;
+  int64_t i = t / d;
+  int k     = static_cast<int>(t % d);
+  A[t]      = static_cast<double>(__half2float(x[i * step * d + k]) - mean[k]);
+}
+
+/** G = A^T A (fp64) by 16 x 16 output tiles, samples staged through LDS in chunks of 64 rows. */
+__global__ __launch_bounds__(256) void scatter_kernel(const double* __restrict__ A, int64_t ns, int d,
+                                                      double* __restrict__ G)
+{
+  __shared__ double ta[64][17], tb[64][17];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const int a0 = blockIdx.y * 16, b0 = blockIdx.x * 16;
+  double acc = 0;
+  for (int64_t r0 = 0; r0 < ns; r0 += 64) {
+    for (int t = threadIdx.x; t < 64 * 16; t += 256) {
+      int r = t >> 4, c = t & 15;
+      int64_t row = r0 + r;
+      ta[r][c]    = (row < ns && a0 + c < d) ? A[row * d + a0 + c] : 0.0;
+      tb[r][c]    = (row < ns && b0 + c < d) ? A[row * d + b0 + c] : 0.0;
+    }
+    __syncthreads();
+#pragma unroll 8
+    for (int r = 0; r < 64; r++)
+      acc = fma(ta[r][ty], tb[r][tx], acc);
+    __syncthreads();
+  }
+  if (a0 + ty < d && b0 + tx < d) G[static_cast<int64_t>(a0 + ty) * d + b0 + tx] = acc;
+}
+
+/** y [n, w] = (x - mean) @ U + shift (fp32): one thread per row, U [d, w] in LDS. */
+__global__ __launch_bounds__(256) void project_rows_kernel(const __half* __restrict__ x, int64_t n, int d,
+                                                           const float* __restrict__ mean,
+                                                           const float* __restrict__ U,
+                                                           const float* __restrict__ shift, int w,
+                                                           float* __restrict__ y)
+{
+  extern __shared__ float su[];
+  float* sm = su + d * w;
+  for (int t = threadIdx.x; t < d * w; t += blockDim.x)
+    su[t] = U[t];
+  for (int t = threadIdx.x; t < d; t += blockDim.x)
+    sm[t] = mean[t];
+  __syncthreads();
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float acc[kMaxW];
+  for (int s = 0; s < w; s++)
+    acc[s] = 0.f;
+  const __half* r = x + i * d;
+  for (int k = 0; k < d; k++) {
+    float v = __half2float(r[k]) - sm[k];
+    for (int s = 0; s < w; s++)
+      acc[s] = fmaf(v, su[k * w + s], acc[s]);
+  }
+  for (int s = 0; s < w; s++)
+    y[i * w + s] = acc[s] + shift[s];
+}
+
+/** keys[i] = cell id of y[i] / f (division, as build_cells.cuh:69-71), idx[i] = i. */
+template <int B>
+__global__ void cell_hash_kernel(const float* __restrict__ y, int64_t n, float f, long long* __restrict__ keys,
+                                 int* __restrict__ idx)
+{
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float x[8 * B];
+#pragma unroll
+  for (int k = 0; k < 8 * B; k++)
+    x[k] = y[i * 8 * B + k] / f;
+  keys[i] = e8b_hash64<B>(x, 1.0f);
+  idx[i]  = static_cast<int>(i);
+}
+
+/** flag[i] = 1 where a run of equal sorted keys starts. */
+__global__ void run_flag_kernel(const long long* __restrict__ k, int64_t n, int* __restrict__ flag)
+{
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  flag[i] = (i == 0 || k[i] != k[i - 1]) ? 1 : 0;
+}
+
+/** Runs from the inclusive scan rid of the flags: start and key of every run. */
+__global__ void run_start_kernel(const long long* __restrict__ k, const int* __restrict__ rid, int64_t n,
+                                 int* __restrict__ start, long long* __restrict__ ukey)
+{
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  if (i == 0 || k[i] != k[i - 1]) {
+    int r    = rid[i] - 1;
+    start[r] = static_cast<int>(i);
+    ukey[r]  = k[i];
+  }
+}
+
+/** pop[r] = start[r + 1] - start[r]; keep[r] = a list for run r. */
+__global__ void run_keep_kernel(const int* __restrict__ start, int runs, int64_t n, int min_cell,
+                                int* __restrict__ pop, int* __restrict__ keep)
+{
+  int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= runs) return;
+  int e   = r + 1 < runs ? start[r + 1] : static_cast<int>(n);
+  pop[r]  = e - start[r];
+  keep[r] = pop[r] >= min_cell ? 1 : 0;
+}
+
+/** The kept runs compacted: key, first row and population of cell kidx[r]. */
+__global__ void run_compact_kernel(const long long* __restrict__ ukey, const int* __restrict__ start,
+                                   const int* __restrict__ pop, const int* __restrict__ keep,
+                                   const int* __restrict__ kidx, int runs, long long* __restrict__ ckey,
+                                   int* __restrict__ cfirst, int* __restrict__ cpop)
+{
+  int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= runs || !keep[r]) return;
+  int c     = kidx[r];
+  ckey[c]   = ukey[r];
+  cfirst[c] = start[r];
+  cpop[c]   = pop[r];
+}
+
+/** z[c] = f * E8 point of y[first member] / f: the center of kept cell c (build_cells.cuh:86-103). */
+template <int B>
+__global__ void cell_center_kernel(const float* __restrict__ y, const int* __restrict__ sidx,
+                                   const int* __restrict__ cfirst, int M, float f, float* __restrict__ z)
+{
+  int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= M) return;
+  const float* r = y + static_cast<int64_t>(sidx[cfirst[c]]) * 8 * B;
+#pragma unroll
+  for (int j = 0; j < B; j++) {
+    float x[8], p[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+      x[k] = r[8 * j + k] / f;
+    e8_point(x, p);
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+      z[static_cast<int64_t>(c) * 8 * B + 8 * j + k] = p[k] * f;
+  }
+}
+
+/**
+ * Sort key of sorted row i: (kept cell << 32) | distance bits to the cell center (rows of cells
+ * without a list sort last).  A stable sort on it orders every cell's members nearest first, ties by
+ * row id.
+ */
+__global__ void member_key_kernel(const float* __restrict__ y, int w, const int* __restrict__ sidx,
+                                  const int* __restrict__ rid, const int* __restrict__ keep,
+                                  const int* __restrict__ kidx, const float* __restrict__ z, int64_t n,
+                                  unsigned long long* __restrict__ key)
+{
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  int r = rid[i] - 1;
+  if (!keep[r]) {
+    key[i] = ~0ULL;
+    return;
+  }
+  int c             = kidx[r];
+  const float* v    = y + static_cast<int64_t>(sidx[i]) * w;
+  const float* zc   = z + static_cast<int64_t>(c) * w;
+  float dd          = 0.f;
+  for (int s = 0; s < w; s++) {
+    float e = v[s] - zc[s];
+    dd      = fmaf(e, e, dd);
+  }
+  key[i] = (static_cast<unsigned long long>(c) << 32) | __float_as_uint(dd);
+}
+
+/** List of cell c: its first l members by distance, the nearest repeated when it has fewer. */
+__global__ void list_fill_kernel(const int* __restrict__ sidx2, const int* __restrict__ cstart,
+                                 const int* __restrict__ cpop, int M, int l, int* __restrict__ lists)
+{
+  int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= static_cast<int64_t>(M) * l) return;
+  int c = static_cast<int>(t / l), j = static_cast<int>(t % l);
+  lists[t] = sidx2[cstart[c] + (j < cpop[c] ? j : 0)];
+}
+
+__global__ void bucket_kernel(const long long* __restrict__ ckey, int M, long long mask,
+                              unsigned* __restrict__ bucket, int* __restrict__ seq)
+{
+  int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= M) return;
+  bucket[c] = static_cast<unsigned>(ckey[c] & mask);
+  seq[c]    = c;
+}
+
+/** Cells in (bucket, id) order: keys and list rows gathered by the bucket sort's permutation. */
+__global__ void level_gather_kernel(const long long* __restrict__ ckey, const int* __restrict__ lists,
+                                    const int* __restrict__ perm, int M, int l, long long* __restrict__ okey,
+                                    int* __restrict__ olists)
+{
+  int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= static_cast<int64_t>(M) * l) return;
+  int c = static_cast<int>(t / l), j = static_cast<int>(t % l);
+  int p = perm[c];
+  olists[t] = lists[static_cast<int64_t>(p) * l + j];
+  if (j == 0) okey[c] = ckey[p];
+}
+
+/** offs[b] = the number of cells in buckets below b, for b in [0, T] (CSR over the buckets). */
+__global__ void offsets_kernel(const unsigned* __restrict__ sbucket, int M, int64_t T, int* __restrict__ offs)
+{
+  int64_t b = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (b > T) return;
+  int lo = 0, hi = M;
+  while (lo < hi) {
+    int mid = (lo + hi) >> 1;
+    if (static_cast<int64_t>(sbucket[mid]) < b)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  offs[b] = lo;
+}
+
+/** v [n, S] = (x - mean) @ basis; amax[s] = max |v[:, s]| (float bits of non-negatives order as uints). */
+__global__ __launch_bounds__(256) void sketch_project_kernel(const __half* __restrict__ x, int64_t n, int d,
+                                                             const float* __restrict__ mean,
+                                                             const float* __restrict__ basis, int S,
+                                                             float* __restrict__ v, unsigned* __restrict__ amax)
+{
+  int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= n * S) return;
+  int64_t i = t / S;
+  int s     = static_cast<int>(t % S);
+  float acc = 0.f;
+  for (int k = 0; k < d; k++)
+    acc = fmaf(__half2float(x[i * d + k]) - mean[k], basis[static_cast<int64_t>(k) * S + s], acc);
+  v[t] = acc;
+  atomicMax(amax + s, __float_as_uint(fabsf(acc)));
+}
+
+/** codes = clamp(rint(v / scale), -127, 127) (build_setup.cuh:183-190). */
+__global__ void quantize_kernel(const float* __restrict__ v, const float* __restrict__ scale, int64_t n, int S,
+                                signed char* __restrict__ out)
+{
+  int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= n * S) return;
+  float q = rintf(v[t] / scale[t % S]);
+  out[t]  = static_cast<signed char>(fminf(127.f, fmaxf(-127.f, q)));
+}
+
+__global__ void half_to_float_kernel(const __half* __restrict__ x, int64_t total, float* __restrict__ out)
+{
+  int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t < total) out[t] = __half2float(x[t]);
+}
+
+template <typename T>
+void ensure(dbuf& b, int64_t count)
+{
+  size_t want = static_cast<size_t>(std::max<int64_t>(count, 1)) * sizeof(T);
+  if (b.size < want) b = dbuf(want + want / 8);
+}
+
+/** Runs a rocPRIM device call after sizing its temporary storage (grown as needed, never short). */
+template <typename F>
+void with_tmp(dbuf& tmp, F&& call)
+{
+  size_t need = 0;
+  OCTEX_HIP(call(static_cast<void*>(nullptr), need));
+  if (tmp.size < need) tmp = dbuf(need + need / 8);
+  size_t have = tmp.size;
+  OCTEX_HIP(call(tmp.ptr, have));
+}
+
+}  // namespace
+
+// ================================================================== host side
+
+void pca_scatter(const __half* x, int64_t n, int d, int64_t step, int64_t ns, const float* mean, double* G,
+                 hipStream_t s)
+{
+  dbuf A(static_cast<size_t>(ns) * d * sizeof(double));
+  pca_sample_kernel<<<grid_for(ns * d, 256), 256, 0, s>>>(x, ns, step, d, mean, A.as<double>());
+  dim3 grid((d + 15) / 16, (d + 15) / 16);
+  scatter_kernel<<<grid, 256, 0, s>>>(A.as<double>(), ns, d, G);
+  OCTEX_HIP(hipGetLastError());
+  OCTEX_HIP(hipStreamSynchronize(s));
+}
+
+void project_rows(const __half* x, int64_t n, int d, const float* mean, const float* U, const float* shift, int w,
+                  float* y, hipStream_t s)
+{
+  OCTEX_EXPECTS(w <= kMaxW, "octex: blocks must be at most 8");
+  const size_t smem = static_cast<size_t>(d * w + d) * sizeof(float);
+  OCTEX_EXPECTS(smem <= 160 * 1024, "octex: dimension x 8 blocks too large for the projection kernel");
+  OCTEX_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&project_rows_kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
+  project_rows_kernel<<<grid_for(n, 256), 256, smem, s>>>(x, n, d, mean, U, shift, w, y);
+  OCTEX_HIP(hipGetLastError());
+}
+
+void half_to_float(const __half* x, int64_t total, float* out, hipStream_t s)
+{
+  if (total == 0) return;
+  half_to_float_kernel<<<grid_for(total, 256), 256, 0, s>>>(x, total, out);
+  OCTEX_HIP(hipGetLastError());
+}
+
+void make_sketch(const __half* x, int64_t n, int d, const float* mean, const float* basis, int S,
+                 std::vector<float>& scale, signed char* codes, hipStream_t s)
+{
+  const int64_t chunk = std::min<int64_t>(n, int64_t{1} << 22);
+  dbuf v(static_cast<size_t>(chunk) * S * sizeof(float)), amax(S * sizeof(unsigned)), dscale(S * sizeof(float));
+  OCTEX_HIP(hipMemsetAsync(amax.ptr, 0, amax.size, s));
+  for (int64_t r0 = 0; r0 < n; r0 += chunk) {
+    int64_t m = std::min(chunk, n - r0);
+    sketch_project_kernel<<<grid_for(m * S, 256), 256, 0, s>>>(x + r0 * d, m, d, mean, basis, S, v.as<float>(),
+                                                              amax.as<unsigned>());
+  }
+  std::vector<unsigned> ha(S);
+  OCTEX_HIP(hipMemcpyAsync(ha.data(), amax.ptr, S * sizeof(unsigned), hipMemcpyDeviceToHost, s));
+  OCTEX_HIP(hipStreamSynchronize(s));
+  scale.resize(S);
+  for (int k = 0; k < S; k++) {
+    float am;
+    std::memcpy(&am, &ha[k], sizeof(float));
+    scale[k] = am > 0.f ? am / 127.f : 1.f;
+  }
+  OCTEX_HIP(hipMemcpyAsync(dscale.ptr, scale.data(), S * sizeof(float), hipMemcpyHostToDevice, s));
+  for (int64_t r0 = 0; r0 < n; r0 += chunk) {
+    int64_t m = std::min(chunk, n - r0);
+    sketch_project_kernel<<<grid_for(m * S, 256), 256, 0, s>>>(x + r0 * d, m, d, mean, basis, S, v.as<float>(),
+                                                              amax.as<unsigned>());
+    quantize_kernel<<<grid_for(m * S, 256), 256, 0, s>>>(v.as<float>(), dscale.as<float>(), m, S, codes + r0 * S);
+  }
+  OCTEX_HIP(hipGetLastError());
+  OCTEX_HIP(hipStreamSynchronize(s));
+}
+
+void cell_builder::reserve(int64_t n_, int w_, hipStream_t s_)
+{
+  n = n_;
+  w = w_;
+  s = s_;
+  ensure<long long>(keys, n);
+  ensure<long long>(skeys, n);
+  ensure<int>(idx, n);
+  ensure<int>(sidx, n);
+  ensure<int>(sidx2, n);
+  ensure<int>(rid, n);
+  ensure<int>(flag, n);
+  ensure<unsigned long long>(mkey, n);
+  ensure<unsigned long long>(mkey2, n);
+}
+
+auto cell_builder::level(const float* y, int B, float f, int min_cell, int l, int log_buckets, int* offs_out,
+                         dbuf& keys_out, dbuf& lists_out) -> int64_t
+{
+  const int64_t T = int64_t{1} << log_buckets;
+  auto g          = grid_for(n, 256);
+  switch (B) {
+#define OCTEX_HASH(b) \
+  case b: cell_hash_kernel<b><<<g, 256, 0, s>>>(y, n, f, keys.as<long long>(), idx.as<int>()); break;
+    OCTEX_HASH(1) OCTEX_HASH(2) OCTEX_HASH(3) OCTEX_HASH(4) OCTEX_HASH(5) OCTEX_HASH(6) OCTEX_HASH(8)
+#undef OCTEX_HASH
+    default: fail("octex: blocks must be 1-6 or 8");
+  }
+  with_tmp(tmp, [&](void* p, size_t& b) {
+    return rocprim::radix_sort_pairs(p, b, keys.as<long long>(), skeys.as<long long>(), idx.as<int>(), sidx.as<int>(),
+                                     n, 0, 64, s);
+  });
+  run_flag_kernel<<<g, 256, 0, s>>>(skeys.as<long long>(), n, flag.as<int>());
+  with_tmp(tmp, [&](void* p, size_t& b) {
+    return rocprim::inclusive_scan(p, b, flag.as<int>(), rid.as<int>(), n, rocprim::plus<int>(), s);
+  });
+  int runs = 0;
+  OCTEX_HIP(hipMemcpyAsync(&runs, rid.as<int>() + n - 1, sizeof(int), hipMemcpyDeviceToHost, s));
+  OCTEX_HIP(hipStreamSynchronize(s));
+  ensure<int>(start, runs + 1);
+  ensure<long long>(ukey, runs);
+  ensure<int>(pop, runs);
+  ensure<int>(keep, runs);
+  ensure<int>(kidx, runs);
+  run_start_kernel<<<g, 256, 0, s>>>(skeys.as<long long>(), rid.as<int>(), n, start.as<int>(), ukey.as<long long>());
+  run_keep_kernel<<<grid_for(runs, 256), 256, 0, s>>>(start.as<int>(), runs, n, min_cell, pop.as<int>(),
+                                                      keep.as<int>());
+  with_tmp(tmp, [&](void* p, size_t& b) {
+    return rocprim::exclusive_scan(p, b, keep.as<int>(), kidx.as<int>(), 0, runs, rocprim::plus<int>(), s);
+  });
+  int last[2] = {0, 0};
+  OCTEX_HIP(hipMemcpyAsync(&last[0], kidx.as<int>() + runs - 1, sizeof(int), hipMemcpyDeviceToHost, s));
+  OCTEX_HIP(hipMemcpyAsync(&last[1], keep.as<int>() + runs - 1, sizeof(int), hipMemcpyDeviceToHost, s));
+  OCTEX_HIP(hipStreamSynchronize(s));
+  const int M = last[0] + last[1];
+  ensure<long long>(ckey, M);
+  ensure<int>(cfirst, M);
+  ensure<int>(cpop, M);
+  ensure<int>(cstart, M);
+  ensure<float>(z, static_cast<int64_t>(M) * w);
+  run_compact_kernel<<<grid_for(runs, 256), 256, 0, s>>>(ukey.as<long long>(), start.as<int>(), pop.as<int>(),
+                                                          keep.as<int>(), kidx.as<int>(), runs, ckey.as<long long>(),
+                                                          cfirst.as<int>(), cpop.as<int>());
+  if (M > 0) {
+    auto gm = grid_for(M, 256);
+    switch (B) {
+#define OCTEX_CENTER(b)                                                                                        \
+  case b:                                                                                                      \
+    cell_center_kernel<b><<<gm, 256, 0, s>>>(y, sidx.as<int>(), cfirst.as<int>(), M, f, z.as<float>());        \
+    break;
+      OCTEX_CENTER(1) OCTEX_CENTER(2) OCTEX_CENTER(3) OCTEX_CENTER(4) OCTEX_CENTER(5) OCTEX_CENTER(6) OCTEX_CENTER(8)
+#undef OCTEX_CENTER
+    }
+  }
+  member_key_kernel<<<g, 256, 0, s>>>(y, w, sidx.as<int>(), rid.as<int>(), keep.as<int>(), kidx.as<int>(),
+                                      z.as<float>(), n, mkey.as<unsigned long long>());
+  with_tmp(tmp, [&](void* p, size_t& b) {
+    return rocprim::radix_sort_pairs(p, b, mkey.as<unsigned long long>(), mkey2.as<unsigned long long>(),
+                                     sidx.as<int>(), sidx2.as<int>(), n, 0, 64, s);
+  });
+  if (M > 0)
+    with_tmp(tmp, [&](void* p, size_t& b) {
+      return rocprim::exclusive_scan(p, b, cpop.as<int>(), cstart.as<int>(), 0, M, rocprim::plus<int>(), s);
+    });
+  ensure<int>(lists_tmp, static_cast<int64_t>(M) * l);
+  ensure<unsigned>(bucket, M);
+  ensure<unsigned>(sbucket, M);
+  ensure<int>(seq, M);
+  ensure<int>(perm, M);
+  keys_out  = dbuf(static_cast<size_t>(std::max(M, 1)) * sizeof(long long));
+  lists_out = dbuf(static_cast<size_t>(std::max<int64_t>(int64_t{M} * l, 1)) * sizeof(int));
+  if (M > 0) {
+    list_fill_kernel<<<grid_for(int64_t{M} * l, 256), 256, 0, s>>>(sidx2.as<int>(), cstart.as<int>(), cpop.as<int>(),
+                                                                    M, l, lists_tmp.as<int>());
+    bucket_kernel<<<grid_for(M, 256), 256, 0, s>>>(ckey.as<long long>(), M, T - 1, bucket.as<unsigned>(),
+                                                   seq.as<int>());
+    with_tmp(tmp, [&](void* p, size_t& b) {
+      return rocprim::radix_sort_pairs(p, b, bucket.as<unsigned>(), sbucket.as<unsigned>(), seq.as<int>(),
+                                       perm.as<int>(), M, 0, log_buckets, s);
+    });
+    level_gather_kernel<<<grid_for(int64_t{M} * l, 256), 256, 0, s>>>(ckey.as<long long>(), lists_tmp.as<int>(),
+                                                                       perm.as<int>(), M, l,
+                                                                       keys_out.as<long long>(), lists_out.as<int>());
+  }
+  offsets_kernel<<<grid_for(T + 1, 256), 256, 0, s>>>(sbucket.as<unsigned>(), M, T, offs_out);
+  OCTEX_HIP(hipGetLastError());
+  OCTEX_HIP(hipStreamSynchronize(s));
+  return M;
+}
+
+}  // namespace cuvs::neighbors::octex::detail

@@ -1,0 +1,43 @@
+// Device side of the octex index builder (build_kernels.hip).
+#pragma once
+
+#include "common.hpp"
+
+#include <hip/hip_fp16.h>
+
+#include <cstdint>
+#include <vector>
+
+namespace cuvs::neighbors::octex::detail {
+
+/** G [d, d] (device, fp64) = A^T A of the ns sampled rows x[i * step] - mean. */
+void pca_scatter(const __half* x, int64_t n, int d, int64_t step, int64_t ns, const float* mean, double* G,
+                 hipStream_t s);
+/** y [n, w] = (x - mean) @ U [d, w] + shift (fp32). */
+void project_rows(const __half* x, int64_t n, int d, const float* mean, const float* U, const float* shift, int w,
+                  float* y, hipStream_t s);
+void half_to_float(const __half* x, int64_t total, float* out, hipStream_t s);
+/** The int8 sketch: scale = amax / 127 per coordinate, codes = round(((x - mean) @ basis) / scale). */
+void make_sketch(const __half* x, int64_t n, int d, const float* mean, const float* basis, int S,
+                 std::vector<float>& scale, signed char* codes, hipStream_t s);
+
+/** Scratch of the cells of one level of one copy (reused across levels and copies). */
+struct cell_builder {
+  int64_t n     = 0;
+  int w         = 0;
+  hipStream_t s = nullptr;
+  dbuf keys, skeys, idx, sidx, sidx2, rid, flag, mkey, mkey2, tmp;
+  dbuf start, ukey, pop, keep, kidx, ckey, cfirst, cpop, cstart, z, lists_tmp, bucket, sbucket, seq, perm;
+
+  void reserve(int64_t n, int w, hipStream_t s);
+  /**
+   * The cells of the projected rows y [n, w] at spacing f: cells of at least min_cell rows, each with
+   * the list of its l members nearest to its center (the nearest repeated when fewer), in (bucket,
+   * id) order.  offs_out [T + 1] (device) receives the CSR over the buckets, keys_out / lists_out
+   * the ids and list rows.  Returns the number of cells.
+   */
+  auto level(const float* y, int B, float f, int min_cell, int l, int log_buckets, int* offs_out, dbuf& keys_out,
+             dbuf& lists_out) -> int64_t;
+};
+
+}  // namespace cuvs::neighbors::octex::detail

@@ -2,6 +2,7 @@
 // core C API it needs (resources, stream, last error text; c/src/core/exceptions.hpp:17-33), on
 // DLPack tensors in HIP device memory (kDLROCM) or host memory (kDLCPU, kDLROCMHost).
 
+#include "build.hpp"
 #include "common.hpp"
 #include "index_impl.hpp"
 #include "search.hpp"
@@ -423,5 +424,162 @@ extern "C" cuvsError_t octexIndexPlanInfo(cuvsOctexIndex_t index, int32_t* info)
     auto const& pl = *ix.plans.begin()->second;
     int32_t v[] = {pl.m, pl.k, pl.KO, pl.lr, pl.W, pl.W2, pl.R1, pl.R2, pl.FR, pl.graph != nullptr ? 1 : 0};
     std::memcpy(info, v, sizeof(v));
+  });
+}
+
+extern "C" cuvsError_t octexBuildInMemory(cuvsResources_t res, cuvsOctexIndexParams_t params, DLManagedTensor* dataset,
+                                          const char* path, cuvsOctexIndex_t index, double* seconds)
+{
+  return translate_exceptions([=] {
+    (void)as_res(res);
+    OCTEX_EXPECTS(params != nullptr && dataset != nullptr && index != nullptr, "octex: NULL argument");
+    OCTEX_EXPECTS(index->addr == 0, "octex: the index handle already holds an index");
+    const auto p   = to_cpp(*params);
+    auto const& t  = dataset->dl_tensor;
+    const bool dev = t.device.device_type == kDLROCM;
+    const int64_t n = t.shape[0], d = t.shape[1];
+    std::vector<__half> host(static_cast<size_t>(n * d));
+    if (t.dtype.code == kDLFloat && t.dtype.bits == 16) {
+      auto* x = dl_matrix<__half>(dataset, dev);
+      OCTEX_HIP(hipMemcpy(host.data(), x, host.size() * sizeof(__half), hipMemcpyDefault));
+    } else if (t.dtype.code == kDLFloat && t.dtype.bits == 32) {
+      auto* x = dl_matrix<float>(dataset, dev);
+      std::vector<float> f;
+      const float* src = x;
+      if (dev) {
+        f.resize(host.size());
+        OCTEX_HIP(hipMemcpy(f.data(), x, f.size() * sizeof(float), hipMemcpyDefault));
+        src = f.data();
+      }
+      for (size_t i = 0; i < host.size(); i++)
+        host[i] = __float2half(src[i]);
+    } else {
+      octex::detail::fail("octex: the dataset must be float32 or float16");
+    }
+    octex::detail::build_record rec;
+    auto impl = octex::detail::build_in_memory(p, host.data(), n, d, rec);
+    if (path != nullptr) octex::detail::write_index(*impl, rec, p, std::string(path));
+    if (seconds != nullptr) *seconds = rec.phases.empty() ? 0.0 : rec.phases.back().second;
+    index->addr = reinterpret_cast<uintptr_t>(new octex::index(impl));
+  });
+}
+
+extern "C" cuvsError_t octexIndexProfileBatch(cuvsOctexIndex_t index, cuvsOctexSearchParams_t params,
+                                              DLManagedTensor* queries, int64_t k, int32_t reps, char* names,
+                                              double* ms, int32_t* nstages, int64_t* counters)
+{
+  return translate_exceptions([=] {
+    OCTEX_EXPECTS(params != nullptr && queries != nullptr && names != nullptr && ms != nullptr, "octex: NULL argument");
+    auto& idx      = *as_index(*index);
+    auto& ix       = idx.impl();
+    auto const p   = to_cpp(*params);
+    const bool dev = queries->dl_tensor.device.device_type == kDLROCM;
+    auto* q        = dl_matrix<float>(queries, dev);
+    const int64_t nq = queries->dl_tensor.shape[0];
+    OCTEX_EXPECTS(nq <= std::max(p.batch, 1), "octex: the profiled queries must fit one batch");
+    OCTEX_EXPECTS(p.waves <= 16, "octex: at most 16 waves are profiled");
+    std::vector<int64_t> nb(nq * k);
+    std::vector<float> nd(nq * k);
+    raft::resources r;
+    std::vector<float> hq;
+    const float* qh = q;
+    if (dev) {
+      hq.resize(static_cast<size_t>(nq * ix.dim));
+      OCTEX_HIP(hipMemcpy(hq.data(), q, hq.size() * sizeof(float), hipMemcpyDeviceToHost));
+      qh = hq.data();
+    }
+    // a normal search first: the plan, and the queries in its buffer
+    octex::detail::search_impl(r, p, idx, qh, nq, ix.dim, nb.data(), nd.data(), k, true, false);
+    std::shared_ptr<octex::detail::plan> pl;
+    {
+      std::lock_guard<std::mutex> lock(ix.mu);
+      pl = ix.plans.begin()->second;
+    }
+    std::lock_guard<std::mutex> lock(pl->mu);
+    OCTEX_HIP(hipSetDevice(ix.device));
+    std::vector<std::string> nm;
+    std::vector<double> t;
+    octex::detail::profile_counters cnt;
+    octex::detail::profile_batch(ix, *pl, std::max(reps, 1), nm, t, cnt);
+    OCTEX_EXPECTS(nm.size() <= 64, "octex: too many stages");
+    for (size_t i = 0; i < nm.size(); i++) {
+      std::memset(names + 32 * i, 0, 32);
+      std::strncpy(names + 32 * i, nm[i].c_str(), 31);
+      ms[i] = t[i];
+    }
+    *nstages = static_cast<int32_t>(nm.size());
+    if (counters != nullptr) {
+      int64_t v[4 + 48] = {cnt.seg_hits, cnt.entries1, cnt.distinct1, cnt.reranked1};
+      for (int w = 0; w < 16; w++) {
+        v[4 + w]      = cnt.starts2[w];
+        v[4 + 16 + w] = cnt.distinct2[w];
+        v[4 + 32 + w] = cnt.reranked2[w];
+      }
+      std::memcpy(counters, v, sizeof(v));
+    }
+  });
+}
+
+extern "C" cuvsError_t octexIndexCopyArray(cuvsOctexIndex_t index, const char* name, int32_t copy, void* dst,
+                                           int64_t bytes, int64_t* size)
+{
+  return translate_exceptions([=] {
+    auto& ix = as_index(*index)->impl();
+    std::string n(name != nullptr ? name : "");
+    const void* src = nullptr;
+    size_t sz       = 0;
+    std::vector<int64_t> rows;
+    auto pick = [&](octex::detail::dbuf const& b) {
+      src = b.ptr;
+      sz  = b.size;
+    };
+    if (n == "lists") {
+      OCTEX_EXPECTS(copy >= 0 && copy < ix.copies, "octex: no copy %d", copy);
+      if (!ix.copy_lists.empty()) {
+        src = ix.copy_lists[copy].ptr;
+        sz  = static_cast<size_t>(ix.list_rows[copy]) * ix.list_len * sizeof(int32_t);
+      } else {
+        src = ix.lists.as<int32_t>() + copy * ix.stride;
+        sz  = static_cast<size_t>(ix.stride) * sizeof(int32_t);
+      }
+    } else if (n == "keys") pick(ix.keys);
+    else if (n == "offsets") pick(ix.offsets);
+    else if (n == "base") pick(ix.base);
+    else if (n == "ucatT") pick(ix.ucatT);
+    else if (n == "shift") pick(ix.shift);
+    else if (n == "inv_f") pick(ix.inv_f);
+    else if (n == "mean") pick(ix.mean);
+    else if (n == "basis") pick(ix.basis);
+    else if (n == "scale") pick(ix.scale);
+    else if (n == "sketch") {
+      src = ix.code();
+      sz  = static_cast<size_t>(ix.n) * ix.sketch_width;
+    } else if (n == "vectors") {
+      src = ix.vecs();
+      sz  = static_cast<size_t>(ix.n) * ix.dim * sizeof(__half);
+    } else if (n == "table") {
+      src = ix.rows();
+      sz  = static_cast<size_t>(ix.n) * ix.table_len * sizeof(int32_t);
+    } else if (n == "meta") {  // n, dim, copies, blocks, levels, list_len, log_buckets, sketch_width, table_len, mmax, T1
+      static thread_local int64_t v[11];
+      int64_t m[11] = {ix.n, ix.dim, ix.copies, ix.blocks, ix.levels(), ix.list_len, ix.log_buckets, ix.sketch_width,
+                       ix.table_len, ix.mmax, ix.T1};
+      std::memcpy(v, m, sizeof(m));
+      if (size != nullptr) *size = sizeof(m);
+      if (dst != nullptr) std::memcpy(dst, m, std::min<size_t>(sizeof(m), static_cast<size_t>(bytes)));
+      return;
+    } else if (n == "spacings") {
+      if (size != nullptr) *size = static_cast<int64_t>(ix.spacings.size() * sizeof(float));
+      if (dst != nullptr)
+        std::memcpy(dst, ix.spacings.data(), std::min<size_t>(ix.spacings.size() * sizeof(float), bytes));
+      return;
+    } else {
+      octex::detail::fail("octex: unknown index array %s", n.c_str());
+    }
+    if (size != nullptr) *size = static_cast<int64_t>(sz);
+    if (dst != nullptr && bytes > 0 && src != nullptr) {
+      OCTEX_HIP(hipSetDevice(ix.device));
+      OCTEX_HIP(hipMemcpy(dst, src, std::min<size_t>(sz, static_cast<size_t>(bytes)), hipMemcpyDefault));
+    }
   });
 }

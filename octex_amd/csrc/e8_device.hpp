@@ -1,0 +1,114 @@
+// E8 closest-point decoding and the 64-bit cell id on the device (the reference: detail/e8.cuh:13-85),
+// shared by the search kernels and the index builder.  D8 rounding with the parity fix, the nearer
+// of D8 and D8 + 1/2 (ties: D8) with distances t = x - a, acc = fma(t, t, acc), and the hash of
+// 2 p over the primes with the 64-bit mixer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace cuvs::neighbors::octex::detail {
+
+namespace {
+
+__constant__ long long kPrimes[8] = {1000003LL,
+                                     998244353LL,
+                                     1000000007LL,
+                                     2147483647LL,
+                                     1099511627791LL,
+                                     4398042316799LL,
+                                     70368744177643LL,
+                                     1125899906842597LL};  // e8.cuh:13-20
+constexpr unsigned long long kMix = 0x9E3779B97F4A7C15ULL;  // e8.cuh:21
+
+// ------------------------------------------------------------------ E8 (e8.cuh:24-85)
+
+/** Nearest point of D8: round every coordinate, then fix the parity at the worst-rounded one. */
+__device__ __forceinline__ void d8(const float (&x)[8], float (&f)[8])
+{
+  float s  = 0.f;
+  int im   = 0;
+  float em = -1.f, ei = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    f[i]     = rintf(x[i]);
+    s        = s + f[i];
+    float e  = x[i] - f[i];
+    float ae = fabsf(e);
+    if (ae > em) {
+      em = ae;
+      im = i;
+      ei = e;
+    }
+  }
+  if (fmodf(s, 2.f) != 0.f) {
+    const float step = ei >= 0.f ? 1.f : -1.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      if (i == im) f[i] = f[i] + step;
+  }
+}
+
+/** Nearest point of E8 = D8 u (D8 + 1/2): the nearer of the two cosets' points (ties: D8). */
+__device__ __forceinline__ void e8_point(const float (&x)[8], float (&p)[8])
+{
+  float a[8], c[8], xs[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++)
+    xs[i] = x[i] - 0.5f;
+  d8(x, a);
+  d8(xs, c);
+  float da = 0.f, dc = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    c[i]     = c[i] + 0.5f;
+    float ta = x[i] - a[i];
+    float tc = x[i] - c[i];
+    da       = fmaf(ta, ta, da);
+    dc       = fmaf(tc, tc, dc);
+  }
+  const bool useA = da <= dc;
+#pragma unroll
+  for (int i = 0; i < 8; i++)
+    p[i] = useA ? a[i] : c[i];
+}
+
+/** Block hash: sum of 2 p_i times the i-th prime (64-bit wraparound). */
+__device__ __forceinline__ unsigned long long block_hash(const float (&p)[8])
+{
+  unsigned long long hb = 0;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    long long p2 = static_cast<long long>(2.f * p[i]);
+    hb += static_cast<unsigned long long>(p2) * static_cast<unsigned long long>(kPrimes[i]);
+  }
+  return hb;
+}
+
+__device__ __forceinline__ long long finish_hash(unsigned long long h)
+{
+  long long hs = static_cast<long long>(h);
+  hs           = static_cast<long long>(static_cast<unsigned long long>(hs ^ (hs >> 31)) * kMix);
+  return hs ^ (hs >> 29);
+}
+
+/** 64-bit cell id of the E8^B point nearest to y * inv_f. */
+template <int B>
+__device__ __forceinline__ long long e8b_hash64(const float (&y)[8 * B], float inv_f)
+{
+  unsigned long long h = 0;
+#pragma unroll
+  for (int j = 0; j < B; j++) {
+    float x[8], p[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      x[i] = y[8 * j + i] * inv_f;
+    e8_point(x, p);
+    unsigned long long hb = block_hash(p);
+    h                     = (j == 0) ? hb : h * kMix + hb;
+  }
+  return finish_hash(h);
+}
+
+}  // namespace
+
+}  // namespace cuvs::neighbors::octex::detail

@@ -2,7 +2,8 @@
 // detail/index_impl.hpp:115-177, for a single device).
 //
 // HBM layout (one allocation per array):
-//   lists    i32 [C, stride]        cell lists of all levels of every copy (stride = rows * l)
+//   lists    i32 [C, stride]        cell lists of all levels of every copy (stride = rows * l), or one
+//                                   allocation per copy; list_ptr i64 [C] holds each copy's address
 //   keys     i64 [C, L, mmax]       cell ids per (copy, level) in (bucket, id) order
 //   offsets  i32 [C, L, 2^logT + 1] CSR of the buckets into keys
 //   base     i32 [C, L]             first cell row of every level
@@ -42,7 +43,11 @@ struct index_impl {
   int device         = 0;
   hipStream_t stream = nullptr;
 
-  dbuf lists, keys, offsets, base, ucatT, shift, inv_f, mean, basis, scale;
+  dbuf lists;                     // the loader's lists [C, stride] (one allocation)
+  std::vector<dbuf> copy_lists;   // or the builder's, one allocation per copy
+  dbuf list_ptr;                  // i64 [C]: device address of every copy's lists
+  std::vector<int64_t> list_rows; // cell rows of every copy (builder)
+  dbuf keys, offsets, base, ucatT, shift, inv_f, mean, basis, scale;
   dbuf sketch, vectors, table;
   hbuf host_sketch, host_vectors, host_table;
   int64_t stride = 0, mmax = 0, T1 = 0;

@@ -9,6 +9,7 @@
 // operation is contracted.
 
 #include "common.hpp"
+#include "e8_device.hpp"
 #include "kernels.hpp"
 
 #include <hip/hip_fp16.h>
@@ -22,105 +23,6 @@ namespace {
 
 constexpr unsigned kIdHash = 2654435761u;
 constexpr uint64_t kEmpty  = ~0ULL;
-
-__constant__ long long kPrimes[8] = {1000003LL,
-                                     998244353LL,
-                                     1000000007LL,
-                                     2147483647LL,
-                                     1099511627791LL,
-                                     4398042316799LL,
-                                     70368744177643LL,
-                                     1125899906842597LL};  // e8.cuh:13-20
-constexpr unsigned long long kMix = 0x9E3779B97F4A7C15ULL;  // e8.cuh:21
-
-// ------------------------------------------------------------------ E8 (e8.cuh:24-85)
-
-/** Nearest point of D8: round every coordinate, then fix the parity at the worst-rounded one. */
-__device__ __forceinline__ void d8(const float (&x)[8], float (&f)[8])
-{
-  float s  = 0.f;
-  int im   = 0;
-  float em = -1.f, ei = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; i++) {
-    f[i]     = rintf(x[i]);
-    s        = s + f[i];
-    float e  = x[i] - f[i];
-    float ae = fabsf(e);
-    if (ae > em) {
-      em = ae;
-      im = i;
-      ei = e;
-    }
-  }
-  if (fmodf(s, 2.f) != 0.f) {
-    const float step = ei >= 0.f ? 1.f : -1.f;
-#pragma unroll
-    for (int i = 0; i < 8; i++)
-      if (i == im) f[i] = f[i] + step;
-  }
-}
-
-/** Nearest point of E8 = D8 u (D8 + 1/2): the nearer of the two cosets' points (ties: D8). */
-__device__ __forceinline__ void e8_point(const float (&x)[8], float (&p)[8])
-{
-  float a[8], c[8], xs[8];
-#pragma unroll
-  for (int i = 0; i < 8; i++)
-    xs[i] = x[i] - 0.5f;
-  d8(x, a);
-  d8(xs, c);
-  float da = 0.f, dc = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; i++) {
-    c[i]     = c[i] + 0.5f;
-    float ta = x[i] - a[i];
-    float tc = x[i] - c[i];
-    da       = fmaf(ta, ta, da);
-    dc       = fmaf(tc, tc, dc);
-  }
-  const bool useA = da <= dc;
-#pragma unroll
-  for (int i = 0; i < 8; i++)
-    p[i] = useA ? a[i] : c[i];
-}
-
-/** Block hash: sum of 2 p_i times the i-th prime (64-bit wraparound). */
-__device__ __forceinline__ unsigned long long block_hash(const float (&p)[8])
-{
-  unsigned long long hb = 0;
-#pragma unroll
-  for (int i = 0; i < 8; i++) {
-    long long p2 = static_cast<long long>(2.f * p[i]);
-    hb += static_cast<unsigned long long>(p2) * static_cast<unsigned long long>(kPrimes[i]);
-  }
-  return hb;
-}
-
-__device__ __forceinline__ long long finish_hash(unsigned long long h)
-{
-  long long hs = static_cast<long long>(h);
-  hs           = static_cast<long long>(static_cast<unsigned long long>(hs ^ (hs >> 31)) * kMix);
-  return hs ^ (hs >> 29);
-}
-
-/** 64-bit cell id of the E8^B point nearest to y * inv_f. */
-template <int B>
-__device__ __forceinline__ long long e8b_hash64(const float (&y)[8 * B], float inv_f)
-{
-  unsigned long long h = 0;
-#pragma unroll
-  for (int j = 0; j < B; j++) {
-    float x[8], p[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++)
-      x[i] = y[8 * j + i] * inv_f;
-    e8_point(x, p);
-    unsigned long long hb = block_hash(p);
-    h                     = (j == 0) ? hb : h * kMix + hb;
-  }
-  return finish_hash(h);
-}
 
 // ------------------------------------------------------------------ query preparation
 
@@ -326,18 +228,19 @@ __device__ __forceinline__ int hash_log_dev(int total, int log_cap)
  */
 template <bool kRows>
 __global__ __launch_bounds__(kGatherThreads) void gather_kernel(
-  const int2* __restrict__ seg, int nseg, const int* __restrict__ lists, int64_t stride,
+  const int2* __restrict__ seg, int nseg, const long long* __restrict__ list_ptr,
   const int* __restrict__ table, int table_len, int64_t N, const signed char* __restrict__ code,
   const float* __restrict__ scale, const float* __restrict__ qs, int S, int W, int logW,
   int* __restrict__ cand, float* __restrict__ dist, int* __restrict__ nout)
 {
   const int q = blockIdx.x;
-  extern __shared__ int sm[];
-  float* qv = reinterpret_cast<float*>(sm);
-  float* sc = qv + S;
-  int* pre  = reinterpret_cast<int*>(sc + S);  // [nseg + 1] exclusive prefix
-  int* st   = pre + nseg + 1;                  // [nseg] segment starts
-  int* ht   = st + nseg;                       // hash set
+  extern __shared__ long long smq[];
+  const int** lp = reinterpret_cast<const int**>(smq);  // [nseg] list of every copy (lists only)
+  float* qv      = reinterpret_cast<float*>(smq + nseg);
+  float* sc      = qv + S;
+  int* pre       = reinterpret_cast<int*>(sc + S);  // [nseg + 1] exclusive prefix
+  int* st        = pre + nseg + 1;                  // [nseg] segment starts
+  int* ht        = st + nseg;                       // hash set
   __shared__ int cnt;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, nw = blockDim.x >> 6;
   for (int i = tid; i < S; i += blockDim.x) {
@@ -359,6 +262,7 @@ __global__ __launch_bounds__(kGatherThreads) void gather_kernel(
       if (c < nseg) {
         pre[c] = carry + v - sl.y;
         st[c]  = sl.x;
+        if constexpr (!kRows) lp[c] = reinterpret_cast<const int*>(list_ptr[c]);
       }
       carry += __shfl(v, 63);
     }
@@ -387,7 +291,7 @@ __global__ __launch_bounds__(kGatherThreads) void gather_kernel(
       if constexpr (kRows) {
         v = table[static_cast<int64_t>(st[lo]) * table_len + (i - pre[lo])];
       } else {
-        v = lists[static_cast<int64_t>(lo) * stride + st[lo] + (i - pre[lo])];
+        v = lp[lo][st[lo] + (i - pre[lo])];
       }
       if (v >= 0 && v < N) {  // -1: padding of a table row (search_kernels.cuh:213)
         unsigned s = (static_cast<unsigned>(v) * kIdHash) & (HT - 1);
@@ -934,10 +838,11 @@ void launch_probe(const __half* Y, int m, int C, int L, int B, const float* inv_
 
 auto gather_smem(int W, int S, int nseg) -> size_t
 {
-  return static_cast<size_t>(W + 2 * S + 2 * nseg + 1) * sizeof(int);
+  return static_cast<size_t>(nseg) * sizeof(long long) +
+         static_cast<size_t>(W + 2 * S + 2 * nseg + 1) * sizeof(int);
 }
 
-void launch_gather(bool rows, const int2* seg, int nseg, int m, const int* lists, int64_t stride,
+void launch_gather(bool rows, const int2* seg, int nseg, int m, const long long* list_ptr,
                    const int* table, int table_len, int64_t n, const signed char* code, const float* scale,
                    const float* qs, int S, int W, int logW, int* cand, float* dist, int* nout,
                    hipStream_t s)
@@ -951,12 +856,12 @@ void launch_gather(bool rows, const int2* seg, int nseg, int m, const int* lists
   if (rows) {
     OCTEX_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gather_kernel<true>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
-    gather_kernel<true><<<m, kGatherThreads, smem, s>>>(seg, nseg, lists, stride, table, table_len, n, code,
+    gather_kernel<true><<<m, kGatherThreads, smem, s>>>(seg, nseg, list_ptr, table, table_len, n, code,
                                                         scale, qs, S, W, logW, cand, dist, nout);
   } else {
     OCTEX_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gather_kernel<false>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
-    gather_kernel<false><<<m, kGatherThreads, smem, s>>>(seg, nseg, lists, stride, table, table_len, n, code,
+    gather_kernel<false><<<m, kGatherThreads, smem, s>>>(seg, nseg, list_ptr, table, table_len, n, code,
                                                          scale, qs, S, W, logW, cand, dist, nout);
   }
   OCTEX_HIP(hipGetLastError());

@@ -49,7 +49,8 @@ void launch_probe(const __half* Y, int m, int C, int L, int B, const float* inv_
 /** LDS bytes of a gather over `nseg` segments per query with hash sets up to W slots. */
 auto gather_smem(int W, int S, int nseg) -> size_t;
 /** Ids at or above `n` (a corrupt list or table entry) are skipped like the -1 padding. */
-void launch_gather(bool rows, const int2* seg, int nseg, int m, const int* lists, int64_t stride,
+/** Lists: segment c of a query reads copy c's lists at list_ptr[c] (a device pointer per copy). */
+void launch_gather(bool rows, const int2* seg, int nseg, int m, const long long* list_ptr,
                    const int* table, int table_len, int64_t n, const signed char* code, const float* scale,
                    const float* qs, int S, int W, int logW, int* cand, float* dist, int* nout,
                    hipStream_t s);

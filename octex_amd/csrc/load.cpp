@@ -197,6 +197,12 @@ auto load(raft::resources const& res, std::string const& path, load_params const
       upload_to(ix.lists.as<int32_t>() + c * ix.stride, tmp.data(), ix.stride * sizeof(int32_t), ix.stream);
     }
   }
+  {
+    std::vector<long long> hp(Cg);
+    for (int c = 0; c < Cg; c++)
+      hp[c] = reinterpret_cast<long long>(ix.lists.as<int32_t>() + c * ix.stride);
+    ix.list_ptr = upload(ix, hp.data(), hp.size() * sizeof(long long));
+  }
   ix.mmax    = keys.dim(2);
   ix.keys    = put(reinterpret_cast<const char*>(keys.as<int64_t>()), L * ix.mmax * sizeof(int64_t));
   ix.offsets = put(reinterpret_cast<const char*>(offsets.as<int32_t>()), L * ix.T1 * sizeof(int32_t));

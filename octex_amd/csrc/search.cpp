@@ -12,6 +12,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <functional>
 #include <cstring>
 #include <string>
 
@@ -58,7 +59,7 @@ void first_round(index_impl const& ix, plan const& pl, hipStream_t s)
   launch_probe(pl.Y.as<__half>(), m, C, ix.levels(), ix.blocks, ix.inv_f.as<float>(), ix.offsets.as<int>(),
                ix.T1, ix.keys.as<long long>(), ix.mmax, ix.base.as<int>(), ix.list_len, pl.lr,
                ix.log_buckets, pl.seg.as<int2>(), s);
-  launch_gather(false, pl.seg.as<int2>(), C, m, ix.lists.as<int>(), ix.stride, nullptr, 0, ix.n, ix.code(),
+  launch_gather(false, pl.seg.as<int2>(), C, m, ix.list_ptr.as<long long>(), nullptr, 0, ix.n, ix.code(),
                 ix.scale.as<float>(), pl.qs.as<float>(), S, pl.W, pl.logW, pl.cand.as<int>(),
                 pl.dist.as<float>(), pl.nin.as<int>(), s);
   if (pl.sp.sketch_rank)
@@ -78,7 +79,7 @@ void wave_round(index_impl const& ix, plan const& pl, hipStream_t s)
   for (int wv = 0; wv < nw; wv++) {
     launch_pick_starts(pl.si.as<long long>(), m, pl.KO, pl.done.as<long long>(), st * nw, wv * st, st,
                        ix.table_len, pl.seg2.as<int2>(), s);
-    launch_gather(true, pl.seg2.as<int2>(), st, m, nullptr, 0, ix.rows(), ix.table_len, ix.n, ix.code(),
+    launch_gather(true, pl.seg2.as<int2>(), st, m, nullptr, ix.rows(), ix.table_len, ix.n, ix.code(),
                   ix.scale.as<float>(), pl.qs.as<float>(), S, pl.W2, pl.logW2, pl.cand2.as<int>(),
                   pl.dist2.as<float>(), pl.n2.as<int>(), s);
     if (pl.sp.sketch_rank)
@@ -253,6 +254,132 @@ void search_impl(raft::resources const& res, search_params const& sp, index cons
   OCTEX_HIP(hipStreamWaitEvent(call, pl->ev_out, 0));
   if (host_out) OCTEX_HIP(hipStreamSynchronize(call));
   OCTEX_HIP(hipSetDevice(cur));
+}
+
+/**
+ * One batch of the plan launched kernel by kernel with HIP events around every launch on the index's
+ * stream, `reps` times (the queries already in the plan's query buffer).  Returns the average
+ * milliseconds per launch by stage name, in launch order, and the work counters of the batch.
+ */
+void profile_batch(index_impl& ix, plan& pl, int reps, std::vector<std::string>& names, std::vector<double>& ms,
+                   profile_counters& cnt)
+{
+  hipStream_t s = ix.stream;
+  const int D = static_cast<int>(ix.dim), S = ix.sketch_width, C = ix.copies, m = pl.m;
+  std::vector<std::pair<std::string, std::function<void()>>> steps;
+  auto add = [&](std::string n, std::function<void()> f) { steps.emplace_back(std::move(n), std::move(f)); };
+  add("center", [&] {
+    launch_center(pl.qbuf.as<float>(), ix.mean.as<float>(), m, D, pl.qc.as<float>(), pl.qh.as<__half>(), s);
+  });
+  add("project", [&] {
+    launch_project(pl.qh.as<__half>(), ix.ucatT.as<__half>(), ix.shift.as<__half>(), m, D, C * 8 * ix.blocks,
+                   pl.Y.as<__half>(), s);
+  });
+  add("sketch_query", [&] { launch_sketch_query(pl.qc.as<float>(), ix.basis.as<float>(), m, D, S, pl.qs.as<float>(), s); });
+  add("probe", [&] {
+    launch_probe(pl.Y.as<__half>(), m, C, ix.levels(), ix.blocks, ix.inv_f.as<float>(), ix.offsets.as<int>(), ix.T1,
+                 ix.keys.as<long long>(), ix.mmax, ix.base.as<int>(), ix.list_len, pl.lr, ix.log_buckets,
+                 pl.seg.as<int2>(), s);
+  });
+  add("gather_lists", [&] {
+    launch_gather(false, pl.seg.as<int2>(), C, m, ix.list_ptr.as<long long>(), nullptr, 0, ix.n, ix.code(),
+                  ix.scale.as<float>(), pl.qs.as<float>(), S, pl.W, pl.logW, pl.cand.as<int>(), pl.dist.as<float>(),
+                  pl.nin.as<int>(), s);
+  });
+  if (pl.sp.sketch_rank)
+    add("sketch_keep", [&] {
+      launch_sketch_keep(pl.cand.as<int>(), pl.dist.as<float>(), pl.nin.as<int>(), m, pl.W, pl.KO,
+                         pl.si.as<long long>(), pl.sd.as<float>(), true, s);
+    });
+  else
+    add("rerank_keep", [&] {
+      launch_rerank_keep(pl.cand.as<int>(), pl.dist.as<float>(), pl.nin.as<int>(), m, pl.W, ix.vecs(), D,
+                         pl.qbuf.as<float>(), pl.R1, pl.KO, pl.si.as<long long>(), pl.sd.as<float>(), true, s);
+    });
+  const int st = pl.sp.starts, nw = pl.sp.waves;
+  for (int wv = 0; wv < nw; wv++) {
+    add("pick_starts", [&, wv] {
+      launch_pick_starts(pl.si.as<long long>(), m, pl.KO, pl.done.as<long long>(), st * nw, wv * st, st, ix.table_len,
+                         pl.seg2.as<int2>(), s);
+    });
+    add("gather_rows", [&] {
+      launch_gather(true, pl.seg2.as<int2>(), st, m, nullptr, ix.rows(), ix.table_len, ix.n, ix.code(),
+                    ix.scale.as<float>(), pl.qs.as<float>(), S, pl.W2, pl.logW2, pl.cand2.as<int>(),
+                    pl.dist2.as<float>(), pl.n2.as<int>(), s);
+    });
+    if (pl.sp.sketch_rank)
+      add("sketch_keep_wave", [&] {
+        launch_sketch_keep(pl.cand2.as<int>(), pl.dist2.as<float>(), pl.n2.as<int>(), m, pl.W2, pl.KO,
+                           pl.si.as<long long>(), pl.sd.as<float>(), false, s);
+      });
+    else
+      add("rerank_keep_wave", [&] {
+        launch_rerank_keep(pl.cand2.as<int>(), pl.dist2.as<float>(), pl.n2.as<int>(), m, pl.W2, ix.vecs(), D,
+                           pl.qbuf.as<float>(), pl.R2, pl.KO, pl.si.as<long long>(), pl.sd.as<float>(), false, s);
+      });
+  }
+  if (pl.sp.sketch_rank && pl.FR > 0)
+    add("final_rerank", [&] {
+      launch_final_rerank(pl.si.as<long long>(), m, pl.KO, pl.FR, ix.vecs(), D, pl.qbuf.as<float>(), pl.k,
+                          pl.bi.as<long long>(), pl.bd.as<float>(), s);
+    });
+  else
+    add("take_k", [&] {
+      launch_take_k(pl.si.as<long long>(), pl.sd.as<float>(), m, pl.KO, pl.k, pl.bi.as<long long>(),
+                    pl.bd.as<float>(), s);
+    });
+  std::vector<hipEvent_t> ev(steps.size() + 1);
+  for (auto& e : ev)
+    OCTEX_HIP(hipEventCreate(&e));
+  names.clear();
+  ms.assign(steps.size(), 0.0);
+  for (auto& st2 : steps)
+    names.push_back(st2.first);
+  cnt = profile_counters{};
+  std::vector<int> nin(m), n2(m);
+  std::vector<int2> segh(static_cast<size_t>(m) * std::max(C, st));
+  for (int r = 0; r < reps; r++) {
+    const bool last = r + 1 == reps;
+    int wv = -1;
+    for (size_t i = 0; i < steps.size(); i++) {
+      OCTEX_HIP(hipEventRecord(ev[i], s));
+      steps[i].second();
+      OCTEX_HIP(hipEventRecord(ev[i + 1], s));
+      OCTEX_HIP(hipEventSynchronize(ev[i + 1]));
+      float t = 0;
+      OCTEX_HIP(hipEventElapsedTime(&t, ev[i], ev[i + 1]));
+      ms[i] += t / reps;
+      if (!last) continue;
+      // work counters of the last repetition, read between launches (outside the timed pairs)
+      const std::string& nm = steps[i].first;
+      if (nm == "probe") {
+        OCTEX_HIP(hipMemcpy(segh.data(), pl.seg.ptr, sizeof(int2) * m * C, hipMemcpyDeviceToHost));
+        for (int64_t j = 0; j < int64_t{m} * C; j++) {
+          cnt.seg_hits += segh[j].y > 0;
+          cnt.entries1 += segh[j].y;
+        }
+      } else if (nm == "gather_lists") {
+        OCTEX_HIP(hipMemcpy(nin.data(), pl.nin.ptr, sizeof(int) * m, hipMemcpyDeviceToHost));
+        for (int v : nin) {
+          cnt.distinct1 += v;
+          cnt.reranked1 += std::min(v, pl.sp.sketch_rank ? pl.KO : pl.R1);
+        }
+      } else if (nm == "pick_starts") {
+        wv++;
+        OCTEX_HIP(hipMemcpy(segh.data(), pl.seg2.ptr, sizeof(int2) * m * st, hipMemcpyDeviceToHost));
+        for (int64_t j = 0; j < int64_t{m} * st; j++)
+          cnt.starts2[wv] += segh[j].y > 0;
+      } else if (nm == "gather_rows") {
+        OCTEX_HIP(hipMemcpy(n2.data(), pl.n2.ptr, sizeof(int) * m, hipMemcpyDeviceToHost));
+        for (int v : n2) {
+          cnt.distinct2[wv] += v;
+          cnt.reranked2[wv] += std::min(v, pl.sp.sketch_rank ? pl.KO : pl.R2);
+        }
+      }
+    }
+  }
+  for (auto& e : ev)
+    (void)hipEventDestroy(e);
 }
 
 }  // namespace detail

@@ -8,6 +8,7 @@
 #include <memory>
 #include <mutex>
 #include <string>
+#include <vector>
 
 namespace cuvs::neighbors::octex::detail {
 
@@ -34,6 +35,13 @@ auto plan_key(search_params const& sp, int m, int k) -> std::string;
 auto get_plan(index_impl& ix, search_params const& sp, int m, int k) -> std::shared_ptr<plan>;
 /** One batch of the plan on stream s (graph replay, or direct launches without a graph). */
 void run_batch(index_impl const& ix, plan const& pl, hipStream_t s);
+/** Work counters of one profiled batch (summed over its m queries; per wave for the waves). */
+struct profile_counters {
+  int64_t seg_hits = 0, entries1 = 0, distinct1 = 0, reranked1 = 0;
+  int64_t starts2[16] = {}, distinct2[16] = {}, reranked2[16] = {};
+};
+void profile_batch(index_impl& ix, plan& pl, int reps, std::vector<std::string>& names, std::vector<double>& ms,
+                   profile_counters& cnt);
 /**
  * The batch loop (search.cu:816-961).  resident: the queries of the previous call stay in place in
  * the plan's query buffer (one batch only) and nothing is copied in or out (the timing protocol).

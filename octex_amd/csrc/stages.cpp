@@ -8,6 +8,7 @@
 #include <octex_amd/octex_amd.h>
 
 #include <exception>
+#include <vector>
 
 namespace {
 
@@ -104,9 +105,18 @@ extern "C" cuvsError_t octexStageGather(int32_t rows, const int32_t* seg, int32_
     else
       need(lists, "lists");
     OCTEX_EXPECTS(W >= (1 << kMinLogHash) && (W & (W - 1)) == 0, "octex: W must be a power of two >= 2048");
-    launch_gather(rows != 0, reinterpret_cast<const int2*>(seg), nseg, m, lists, stride, table, table_len, n,
-                  reinterpret_cast<const signed char*>(code), scale, qs, S, W, log2_ceil(W), cand, dist,
+    dbuf ptrs;
+    if (!rows) {  // the pointer of every copy's lists: lists + c * stride
+      std::vector<long long> hp(nseg);
+      for (int c = 0; c < nseg; c++)
+        hp[c] = reinterpret_cast<long long>(lists + static_cast<int64_t>(c) * stride);
+      ptrs = dbuf(hp.size() * sizeof(long long));
+      OCTEX_HIP(hipMemcpy(ptrs.ptr, hp.data(), ptrs.size, hipMemcpyHostToDevice));
+    }
+    launch_gather(rows != 0, reinterpret_cast<const int2*>(seg), nseg, m, ptrs.as<long long>(), table, table_len,
+                  n, reinterpret_cast<const signed char*>(code), scale, qs, S, W, log2_ceil(W), cand, dist,
                   nout, s);
+    OCTEX_HIP(hipStreamSynchronize(s));
   });
 }
 

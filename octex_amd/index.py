@@ -243,6 +243,33 @@ class Index:
                   ct.c_int64(out.nbytes), None)
         return out
 
+    def array(self, name, dtype, copy=0):
+        """A host copy (numpy) of an array of the index (introspection; see octexIndexCopyArray)."""
+        size = ct.c_int64(0)
+        _lib.call("octexIndexCopyArray", self._handle, name.encode(), ct.c_int32(copy), None, ct.c_int64(0),
+                  ct.byref(size))
+        out = np.empty(size.value // np.dtype(dtype).itemsize, dtype)
+        _lib.call("octexIndexCopyArray", self._handle, name.encode(), ct.c_int32(copy), ct.c_void_p(out.ctypes.data),
+                  ct.c_int64(out.nbytes), None)
+        return out
+
+    def profile_batch(self, queries, k=10, reps=3, **params):
+        """Per-kernel milliseconds of one batch (HIP events around every launch) and its work counters."""
+        p = search_params(**params)
+        dq = _lib.Dl(queries)
+        names = ct.create_string_buffer(64 * 32)
+        ms = (ct.c_double * 64)()
+        ns = ct.c_int32(0)
+        cnt = (ct.c_int64 * 52)()
+        _lib.call("octexIndexProfileBatch", self._handle, ct.byref(p), dq.ptr, ct.c_int64(k), ct.c_int32(reps), names,
+                  ms, ct.byref(ns), cnt)
+        raw = names.raw
+        stages = [(raw[32 * i : 32 * i + 32].split(b"\0")[0].decode(), ms[i]) for i in range(ns.value)]
+        c = list(cnt)
+        counters = dict(seg_hits=c[0], entries1=c[1], distinct1=c[2], reranked1=c[3], starts2=c[4:20],
+                        distinct2=c[20:36], reranked2=c[36:52])
+        return stages, counters
+
     def plan_info(self):
         arr = (ct.c_int32 * 10)()
         _lib.call("octexIndexPlanInfo", self._handle, arr)
@@ -307,3 +334,28 @@ def build(dataset, path=None, *, metric="sqeuclidean", placement="shard", vector
                table_on_host=table_on_host, shard_vectors=shard_vectors, sketch=sketch)
     idx._tmpdir = tmp
     return idx
+
+
+def build_in_memory(dataset, path=None, **index_params_):
+    """Build an index of `dataset` [n, dim] in the GPU's memory and return it ready to search (no round trip
+    through files); with `path` the index directory is written as well.  Returns (index, build seconds)."""
+    params = index_params(**index_params_)
+    if _is_torch(dataset):
+        x = dataset.detach().contiguous()
+    else:
+        x = np.asarray(dataset)
+        if x.dtype not in (np.float32, np.float16):
+            x = x.astype(np.float32)
+        x = np.ascontiguousarray(x)
+    res = _lib.Resources()
+    dx = _lib.Dl(x)
+    handle = ct.POINTER(_lib.IndexHandle)()
+    _lib.call("cuvsOctexIndexCreate", ct.byref(handle))
+    secs = ct.c_double(0)
+    try:
+        _lib.call("octexBuildInMemory", res.h, ct.byref(params), dx.ptr,
+                  os.fsencode(path) if path is not None else None, handle, ct.byref(secs))
+    except Exception:
+        _lib.lib().cuvsOctexIndexDestroy(handle)
+        raise
+    return Index(handle, path if path is not None else "", load_args={}), secs.value

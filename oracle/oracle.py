@@ -189,6 +189,9 @@ class Index:
     """The arrays of an index directory as the loader places them (one device, replicate)."""
 
     def __init__(self, path, list_limit=0, copies_limit=0):
+        if not isinstance(path, (str, bytes, os.PathLike)):
+            self._from_live(path)
+            return
         with open(os.path.join(path, "meta.json")) as f:
             meta = json.load(f)
         if int(meta.get("format", 1)) != 1:
@@ -235,9 +238,42 @@ class Index:
         self.vectors = _c(load("vectors"), np.float16).view(np.uint16)
         self.table = _c(load("table"), np.int32) if self.table_len > 0 else None
         assert self.keys.shape[1] == L and proj.shape[2] == w, "octex: bad shapes"
+        self._struct(L)
+
+    def _from_live(self, live):
+        """The arrays of a loaded or built octex_amd index, copied to the host (the same index the GPU searches)."""
+        meta = live.array("meta", np.int64)
+        n, dim, C, blocks, L, list_len, log_buckets, S, table_len, mmax, T1 = (int(v) for v in meta)
+        self.n, self.dim, self.copies, self.blocks, self.list_len = n, dim, C, blocks, list_len
+        self.log_buckets, self.sketch_width, self.table_len = log_buckets, S, table_len
+        self.spacings = [float(v) for v in live.array("spacings", np.float32)]
+        w = 8 * blocks
+        per = [live.array("lists", np.int32, copy=c) for c in range(C)]
+        stride = max(len(p) for p in per)
+        self.lists = np.zeros((C, stride), np.int32)
+        for c, p in enumerate(per):
+            self.lists[c, : len(p)] = p
+        del per
+        self.keys = live.array("keys", np.int64).reshape(C, L, mmax)
+        self.offsets = live.array("offsets", np.int32).reshape(C, L, T1)
+        self.base = live.array("base", np.int32).reshape(C, L)
+        ucatT = live.array("ucatT", np.uint16).reshape(C * w, dim)
+        self.ucat = np.ascontiguousarray(ucatT.T)
+        self.shift = live.array("shift", np.uint16)
+        self.inv_f = live.array("inv_f", np.float32)
+        self.mean = live.array("mean", np.float32)
+        self.basis = live.array("basis", np.float32).reshape(dim, S)
+        self.scale = live.array("scale", np.float32)
+        self.sketch = live.array("sketch", np.int8).reshape(n, S)
+        self.vectors = live.array("vectors", np.uint16).reshape(n, dim)
+        self.table = live.array("table", np.int32).reshape(n, table_len) if table_len > 0 else None
+        self.meta = {}
+        self._struct(L)
+
+    def _struct(self, L):
         s = OrcIndex()
         s.n, s.dim = self.n, self.dim
-        s.copies, s.blocks, s.levels, s.list_len = C, self.blocks, L, ll
+        s.copies, s.blocks, s.levels, s.list_len = self.copies, self.blocks, L, self.list_len
         s.log_buckets, s.sketch_width, s.table_len = self.log_buckets, self.sketch_width, self.table_len
         s.inv_f = self.inv_f.ctypes.data
         s.lists, s.stride = self.lists.ctypes.data, self.lists.shape[1]
