@@ -28,22 +28,24 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor figure
 
 CONFIGS = {
-    # configs[1] of BASELINE.json
+    # configs[1] of BASELINE.json; the index as the reference's paper SIFT1M build (copies 200, lists of 32, no
+    # reverse edges) with the reference's default sketch width for d = 128 (128), cells of >= 2 rows for lists
     "sift1m": dict(n=1_000_000, d=128, nq=10_000, clusters=1000, kind="sift", batch=10_000,
-                   index=dict(copies=200, list_len=32, sketch_width=64, table_len=64, min_cell=2, reverse_edges=False,
-                              seed=0)),
+                   index=dict(copies=200, list_len=32, table_len=64, min_cell=2, reverse_edges=False, seed=0)),
     # a small stand-in for quick checks
     "small": dict(n=100_000, d=128, nq=10_000, clusters=100, kind="sift", batch=10_000,
-                  index=dict(copies=64, list_len=32, sketch_width=64, table_len=64, min_cell=2, reverse_edges=False,
-                             seed=0, log_buckets=18)),
+                  index=dict(copies=64, list_len=32, table_len=64, min_cell=2, reverse_edges=False, seed=0,
+                             log_buckets=18)),
 }
 
-SWEEP = [  # ordered from cheaper to dearer
-    dict(read=16, starts=64, waves=1, rerank=64, wave_rerank=64),
-    dict(read=24, starts=64, waves=1, rerank=64, wave_rerank=64),
+SWEEP = [  # ordered from cheaper to dearer; the fastest one at recall >= 0.99 is timed
+    dict(read=4, starts=16, waves=1, rerank=16, wave_rerank=16),
+    dict(read=4, starts=32, waves=1, rerank=16, wave_rerank=16),
+    dict(read=8, starts=16, waves=1, rerank=16, wave_rerank=16),
+    dict(read=8, starts=32, waves=1, rerank=32, wave_rerank=32),
+    dict(read=16, starts=32, waves=1, rerank=32, wave_rerank=32),
     dict(read=32, starts=64, waves=2, rerank=64, wave_rerank=64),
     dict(read=32, starts=128, waves=2, rerank=128, wave_rerank=128),
-    dict(read=32, starts=128, waves=3, rerank=128, wave_rerank=128),
 ]
 
 
@@ -177,7 +179,8 @@ def main():
     # roofline of the dominant kernel: HIP events around every launch of one batch on the index's stream
     stages, cnt = index.profile_batch(Qd, k=k, reps=5, **params)
     info = index.plan_info()
-    C, S, D, w = index.copies, 64 if "sketch_width" not in cfg["index"] else cfg["index"]["sketch_width"], X.shape[1], 32
+    meta = index.array("meta", np.int64)
+    C, D, w, S = index.copies, X.shape[1], 8 * int(meta[3]), int(meta[7])
     totals, per_launch, waves_seen = {}, [], {}
     for name, ms in stages:
         wv = waves_seen.get(name, 0)
