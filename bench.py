@@ -132,6 +132,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU time of the CPU-baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--params", default=None, help="JSON search parameters (skips the sweep)")
+    ap.add_argument("--save-index", default=None, help="also write the built index directory here")
+    ap.add_argument("--load-index", default=None, help="load this index directory instead of building one")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build searches on one GPU; runs on several GPUs are not part of it", file=sys.stderr)
@@ -149,8 +151,14 @@ def main():
     t0 = time.time()
     gt = ground_truth(X, Q, k, torch)
     log(f"ground truth in {time.time() - t0:.1f} s")
-    index, build_s = octex_amd.build_in_memory(X, **cfg["index"])
-    log(f"index built in {build_s:.1f} s: {index}, {index.device_bytes[0] / 2**30:.1f} GiB")
+    if args.load_index:
+        t0 = time.time()
+        index = octex_amd.load(args.load_index)
+        build_s = None
+        log(f"index loaded in {time.time() - t0:.1f} s: {index}")
+    else:
+        index, build_s = octex_amd.build_in_memory(X, path=args.save_index, **cfg["index"])
+        log(f"index built in {build_s:.1f} s: {index}, {index.device_bytes[0] / 2**30:.1f} GiB")
     Qd = torch.from_numpy(Q).cuda()
 
     # the fastest sweep point at recall >= 0.99
@@ -238,7 +246,7 @@ def main():
             "search": params,
             "recall@10": round(rec, 5),
             "recall_target_met": rec >= 0.99,
-            "build_seconds": round(build_s, 1),
+            "build_seconds": round(build_s, 1) if build_s is not None else None,
             "index_gib": round(index.device_bytes[0] / 2**30, 2),
             "sweep": points,
             "stages": per_launch,
