@@ -31,12 +31,32 @@ CONFIGS = {
     # configs[1] of BASELINE.json; the index as the reference's paper SIFT1M build (copies 200, lists of 32, no
     # reverse edges) with the reference's default sketch width for d = 128 (128), cells of >= 2 rows for lists
     "sift1m": dict(n=1_000_000, d=128, nq=10_000, clusters=1000, kind="sift", batch=10_000,
+                   desc="seeded Gaussian mixture as BASELINE.json configs[1]",
                    index=dict(copies=200, list_len=32, table_len=64, min_cell=2, reverse_edges=False, seed=0)),
+    # configs[3] of BASELINE.json: 100M L2-normalized rows, d = 96, of a 10,000-component mixture (centroids N(0, 1),
+    # sigma 0.4) stored fp16; the index as the reference's paper Deep100M build (lists of 64, cells of >= 10 rows,
+    # table 64) with the reference's default sketch width for d = 96 (96: this mixture's variance is spread over
+    # all 96 PCA axes, so a 64-wide sketch ranks poorly), and as many copies as fit one MI355X's 288 GB next to
+    # the vectors, sketch, table and search buffers (1.3 GB of lists per copy on this data)
+    "deep100m": dict(n=100_000_000, d=96, nq=10_000, clusters=10_000, kind="deep", batch=10_000,
+                     desc="seeded normalized Gaussian mixture as BASELINE.json configs[3], fp16 rows",
+                     index=dict(copies=150, list_len=64, min_cell=10, table_len=64, seed=0)),
     # a small stand-in for quick checks
-    "small": dict(n=100_000, d=128, nq=10_000, clusters=100, kind="sift", batch=10_000,
+    "small": dict(n=100_000, d=128, nq=10_000, clusters=100, kind="sift", batch=10_000, desc="small SIFT-like mixture",
                   index=dict(copies=64, list_len=32, table_len=64, min_cell=2, reverse_edges=False, seed=0,
                              log_buckets=18)),
 }
+
+SWEEP_DEEP = [
+    dict(read=16, starts=64, waves=2, rerank=128, wave_rerank=128),
+    dict(read=16, starts=128, waves=2, rerank=128, wave_rerank=128),
+    dict(read=16, starts=128, waves=2, rerank=128, wave_rerank=256),
+    dict(read=32, starts=128, waves=2, rerank=128, wave_rerank=256),
+    dict(read=32, starts=128, waves=3, rerank=128, wave_rerank=256),
+    dict(read=32, starts=192, waves=2, rerank=128, wave_rerank=256),
+    dict(read=48, starts=192, waves=3, rerank=128, wave_rerank=256),
+    dict(read=64, starts=256, waves=3, rerank=256, wave_rerank=256),
+]
 
 SWEEP = [  # ordered from cheaper to dearer; the fastest one at recall >= 0.99 is timed
     dict(read=4, starts=16, waves=1, rerank=16, wave_rerank=16),
@@ -70,23 +90,59 @@ def make_data(cfg):
     return X, Q.astype(np.float32)
 
 
+class TopK:
+    """Running exact k nearest neighbors of the queries Qd (fp32 on the GPU) over row blocks of the base."""
+
+    def __init__(self, Qd, k, torch):
+        self.torch, self.Q, self.k = torch, Qd, k
+        self.d = torch.full((len(Qd), k), float("inf"), device=Qd.device)
+        self.i = torch.zeros((len(Qd), k), dtype=torch.int64, device=Qd.device)
+
+    def add(self, Xb, r0):
+        torch = self.torch
+        dd = (Xb * Xb).sum(1)[None, :] - 2 * (self.Q @ Xb.T)
+        v, i = torch.topk(dd, self.k, dim=1, largest=False)
+        cd = torch.cat([self.d, v], 1)
+        ci = torch.cat([self.i, i + r0], 1)
+        o = torch.argsort(cd, dim=1)[:, : self.k]
+        self.d, self.i = torch.gather(cd, 1, o), torch.gather(ci, 1, o)
+
+
+def make_deep(cfg, k, torch):
+    """Deep-like rows on the GPU: centroids N(0, 1)^d, rows = centroid + 0.4 N(0, 1), L2-normalized, stored fp16
+    (torch's CUDA generator, seed 0 for the base and 1 for the queries).  The exact neighbors are computed block
+    by block as the rows are made, over the fp16 values; the base goes to host memory."""
+    d, C, n, nq = cfg["d"], cfg["clusters"], cfg["n"], cfg["nq"]
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0)
+    centers = torch.randn((C, d), generator=g, device="cuda")
+    gq = torch.Generator(device="cuda")
+    gq.manual_seed(1)
+    Q = centers[torch.randint(0, C, (nq,), generator=gq, device="cuda")]
+    Q = Q + 0.4 * torch.randn((nq, d), generator=gq, device="cuda")
+    Q = (Q / Q.norm(dim=1, keepdim=True)).contiguous()
+    X = np.empty((n, d), np.float16)
+    top = TopK(Q, k, torch)
+    step = 1 << 18
+    for r0 in range(0, n, step):
+        m = min(step, n - r0)
+        x = centers[torch.randint(0, C, (m,), generator=g, device="cuda")]
+        x = x + 0.4 * torch.randn((m, d), generator=g, device="cuda")
+        xh = (x / x.norm(dim=1, keepdim=True)).half()
+        top.add(xh.float(), r0)
+        X[r0 : r0 + m] = xh.cpu().numpy()
+        if r0 % (1 << 24) == 0:
+            log(f"data: {r0 + m:,} of {n:,} rows")
+    return X, Q.cpu().numpy(), top.i.cpu().numpy()
+
+
 def ground_truth(X, Q, k, torch):
     """Exact k nearest neighbors on the GPU (fp32; integer-valued data makes every distance exact)."""
-    Xd = torch.from_numpy(X).cuda()
-    Qd = torch.from_numpy(Q).cuda()
-    xn = (Xd * Xd).sum(1)
-    best_d = torch.full((len(Q), k), float("inf"), device="cuda")
-    best_i = torch.zeros((len(Q), k), dtype=torch.int64, device="cuda")
+    top = TopK(torch.from_numpy(Q).cuda(), k, torch)
     step = 1 << 17
     for r0 in range(0, len(X), step):
-        dd = xn[None, r0 : r0 + step] - 2 * (Qd @ Xd[r0 : r0 + step].T)
-        v, i = torch.topk(dd, k, dim=1, largest=False)
-        cd = torch.cat([best_d, v], 1)
-        ci = torch.cat([best_i, i + r0], 1)
-        o = torch.argsort(cd, dim=1)[:, :k]
-        best_d, best_i = torch.gather(cd, 1, o), torch.gather(ci, 1, o)
-    del Xd
-    return best_i.cpu().numpy()
+        top.add(torch.from_numpy(X[r0 : r0 + step]).cuda(), r0)
+    return top.i.cpu().numpy()
 
 
 def recall(I, gt, k=10):
@@ -134,6 +190,7 @@ def main():
     ap.add_argument("--params", default=None, help="JSON search parameters (skips the sweep)")
     ap.add_argument("--save-index", default=None, help="also write the built index directory here")
     ap.add_argument("--load-index", default=None, help="load this index directory instead of building one")
+    ap.add_argument("--n", type=int, default=None, help="override the number of base vectors (a scaled-down run)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build searches on one GPU; runs on several GPUs are not part of it", file=sys.stderr)
@@ -143,14 +200,23 @@ def main():
 
     import octex_amd
 
+    torch.backends.cuda.matmul.allow_tf32 = False  # exact fp32 ground truth
+
     cfg = CONFIGS[args.config]
     k = 10
+    if args.n:
+        cfg = dict(cfg, n=args.n)
     t0 = time.time()
-    X, Q = make_data(cfg)
-    log(f"data {X.shape} queries {Q.shape} in {time.time() - t0:.1f} s")
-    t0 = time.time()
-    gt = ground_truth(X, Q, k, torch)
-    log(f"ground truth in {time.time() - t0:.1f} s")
+    if cfg["kind"] == "deep":
+        X, Q, gt = make_deep(cfg, k, torch)
+        torch.cuda.empty_cache()  # the index needs the memory the ground-truth blocks were cached in
+        log(f"data {X.shape} queries {Q.shape} and ground truth in {time.time() - t0:.1f} s")
+    else:
+        X, Q = make_data(cfg)
+        log(f"data {X.shape} queries {Q.shape} in {time.time() - t0:.1f} s")
+        t0 = time.time()
+        gt = ground_truth(X, Q, k, torch)
+        log(f"ground truth in {time.time() - t0:.1f} s")
     if args.load_index:
         t0 = time.time()
         index = octex_amd.load(args.load_index)
@@ -162,7 +228,7 @@ def main():
     Qd = torch.from_numpy(Q).cuda()
 
     # the fastest sweep point at recall >= 0.99
-    sweep = [json.loads(args.params)] if args.params else SWEEP
+    sweep = [json.loads(args.params)] if args.params else (SWEEP_DEEP if cfg["kind"] == "deep" else SWEEP)
     chosen, points = None, []
     for p in sweep:
         p = dict(p, batch=cfg["batch"])
@@ -193,7 +259,7 @@ def main():
     for name, ms in stages:
         wv = waves_seen.get(name, 0)
         waves_seen[name] = wv + 1
-        b = stage_bytes(name, wv, cnt, len(Q), C, S, D, info["KO"], 64, params["starts"], w)
+        b = stage_bytes(name, wv, cnt, len(Q), C, S, D, info["KO"], int(meta[8]), params["starts"], w)
         per_launch.append(dict(stage=name, wave=wv, ms=round(ms, 4), bytes=b,
                                gbs=round(b / (ms * 1e-3) / 1e9, 1) if b else None))
         totals[name] = totals.get(name, 0.0) + ms
@@ -238,10 +304,10 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16 rerank, int8 sketch, fp32 accumulate",
-        "data": "synthetic (seeded Gaussian mixture, BASELINE.json configs[1])",
+        "data": f"synthetic ({cfg['desc']})",
         "config": {
-            "workload": f"{args.config}: {X.shape[0]} x {X.shape[1]} SIFT-like mixture, {len(Q)} queries, k=10, "
-                        f"batch {cfg['batch']}",
+            "workload": f"{args.config}: {X.shape[0]} x {X.shape[1]} {cfg['kind']}-like mixture, {len(Q)} queries, "
+                        f"k=10, batch {cfg['batch']}",
             "index": cfg["index"],
             "search": params,
             "recall@10": round(rec, 5),

@@ -331,6 +331,9 @@ void searched_table(index_impl& ix, index const& idx, int k, bool reverse_edges,
             o[t] = -1;
         }
       });
+      if ((r0 / chunk + 1) % 16 == 0)
+        build_log("table pass %zu: %lld of %lld rows, %.1f s\n", v + 1, static_cast<long long>(r0 + m),
+                  static_cast<long long>(n), seconds_since(t0));
     }
     if (plan[v].waves > 0) drop_table(ix);
     if (reverse_edges) {
@@ -346,9 +349,10 @@ void searched_table(index_impl& ix, index const& idx, int k, bool reverse_edges,
   }
 }
 
-auto build_in_memory(index_params const& params, const __half* x, int64_t n, int64_t d, build_record& rec)
+auto build_in_memory(index_params const& params, dataset_view const& x, build_record& rec)
   -> std::shared_ptr<index_impl>
 {
+  const int64_t n = x.n, d = x.d;
   const auto t_all = std::chrono::steady_clock::now();
   const int C = params.copies, b = params.blocks, w = 8 * b, l = params.list_len;
   const int L     = static_cast<int>(params.spacings.size());
@@ -390,15 +394,33 @@ auto build_in_memory(index_params const& params, const __half* x, int64_t n, int
   // the fp16 vectors: the index's own, read by every step of the build
   ix.vectors = dbuf(static_cast<size_t>(n) * d * sizeof(__half));
   ix.bytes += static_cast<int64_t>(ix.vectors.size);
-  OCTEX_HIP(hipMemcpy(ix.vectors.ptr, x, ix.vectors.size, hipMemcpyHostToDevice));
+  if (!x.f32) {
+    OCTEX_HIP(hipMemcpy(ix.vectors.ptr, x.data, ix.vectors.size, x.device ? hipMemcpyDeviceToDevice
+                                                                           : hipMemcpyHostToDevice));
+  } else if (x.device) {
+    float_to_half(static_cast<const float*>(x.data), n * d, ix.vectors.as<__half>(), s);
+  } else {  // fp32 rows from the host in pieces, rounded on the GPU
+    const int64_t piece = std::min<int64_t>(n * d, int64_t{1} << 26);
+    dbuf tmp(static_cast<size_t>(piece) * sizeof(float));
+    for (int64_t o = 0; o < n * d; o += piece) {
+      const int64_t m = std::min(piece, n * d - o);
+      OCTEX_HIP(hipMemcpyAsync(tmp.ptr, static_cast<const float*>(x.data) + o, m * sizeof(float),
+                               hipMemcpyHostToDevice, s));
+      float_to_half(tmp.as<float>(), m, ix.vectors.as<__half>() + o, s);
+    }
+  }
+  OCTEX_HIP(hipStreamSynchronize(s));
   const __half* xd = ix.vectors.as<__half>();
 
-  // PCA of a sample (build_setup.cuh:40-103)
+  // PCA of a sample (build_setup.cuh:40-103): every step-th row
   const int64_t step = std::max<int64_t>(1, n / 200000), ns = (n + step - 1) / step;
+  std::vector<__half> sample(static_cast<size_t>(ns) * d);
+  OCTEX_HIP(hipMemcpy2D(sample.data(), d * sizeof(__half), xd, step * d * sizeof(__half), d * sizeof(__half), ns,
+                        hipMemcpyDeviceToHost));
   std::vector<double> mu(d, 0.0);
   for (int64_t i = 0; i < ns; i++)
     for (int64_t j = 0; j < d; j++)
-      mu[j] += static_cast<double>(__half2float(x[i * step * d + j]));
+      mu[j] += static_cast<double>(__half2float(sample[i * d + j]));
   rec.mean.resize(d);
   for (int64_t j = 0; j < d; j++)
     rec.mean[j] = static_cast<float>(mu[j] / static_cast<double>(ns));
@@ -462,6 +484,15 @@ auto build_in_memory(index_params const& params, const __half* x, int64_t n, int
       }
       OCTEX_HIP(hipStreamSynchronize(s));
       ix.bytes += static_cast<int64_t>(ix.copy_lists[c].size);
+      if (c == 0 || (c + 1) % 25 == 0 || c + 1 == C) {
+        size_t fr = 0, tot = 0;
+        OCTEX_HIP(hipMemGetInfo(&fr, &tot));
+        std::string cells;
+        for (int j = 0; j < L; j++)
+          cells += " " + std::to_string(rec.cells[static_cast<size_t>(c) * L + j]);
+        build_log("copy %d: cells%s, %.3f GB of lists, %.1f GB free\n", c + 1, cells.c_str(),
+                  static_cast<double>(ix.copy_lists[c].size) / 1e9, static_cast<double>(fr) / 1e9);
+      }
     }
   }
   // keys [C, L, mmax], zero padded; the per-copy list pointers
@@ -469,6 +500,8 @@ auto build_in_memory(index_params const& params, const __half* x, int64_t n, int
   for (auto v : rec.cells)
     mmax = std::max(mmax, v);
   ix.mmax = mmax;
+  build_log("keys: [%d, %d, %lld], %.2f GB\n", C, L, static_cast<long long>(mmax),
+            static_cast<double>(C) * L * mmax * 8 / 1e9);
   ix.keys = dbuf(static_cast<size_t>(C) * L * mmax * sizeof(int64_t));
   ix.bytes += static_cast<int64_t>(ix.keys.size);
   OCTEX_HIP(hipMemsetAsync(ix.keys.ptr, 0, ix.keys.size, s));
@@ -682,10 +715,10 @@ void write_index(index_impl const& ix, build_record const& rec, index_params con
 
 namespace {
 
-void build_half(index_params const& params, const __half* x, int64_t n, int64_t d, std::string const& path)
+void build_to(index_params const& params, detail::dataset_view const& x, std::string const& path)
 {
   detail::build_record rec;
-  auto impl = detail::build_in_memory(params, x, n, d, rec);
+  auto impl = detail::build_in_memory(params, x, rec);
   detail::write_index(*impl, rec, params, path);
 }
 
@@ -694,20 +727,13 @@ void build_half(index_params const& params, const __half* x, int64_t n, int64_t 
 void build(raft::resources const&, index_params const& params,
            raft::host_matrix_view<const float, int64_t, raft::row_major> dataset, std::string const& path)
 {
-  const int64_t n = dataset.extent(0), d = dataset.extent(1);
-  std::vector<__half> xh(static_cast<size_t>(n) * d);
-  const float* src = dataset.data_handle();
-  detail::parallel_for(n * d, [&](int64_t i0, int64_t i1) {
-    for (int64_t i = i0; i < i1; i++)
-      xh[i] = __float2half(src[i]);
-  });
-  build_half(params, xh.data(), n, d, path);
+  build_to(params, {dataset.data_handle(), dataset.extent(0), dataset.extent(1), true, false}, path);
 }
 
 void build(raft::resources const&, index_params const& params,
            raft::host_matrix_view<const half, int64_t, raft::row_major> dataset, std::string const& path)
 {
-  build_half(params, dataset.data_handle(), dataset.extent(0), dataset.extent(1), path);
+  build_to(params, {dataset.data_handle(), dataset.extent(0), dataset.extent(1), false, false}, path);
 }
 
 }  // namespace cuvs::neighbors::octex

@@ -21,8 +21,19 @@ struct build_record {
   std::vector<std::pair<std::string, double>> phases;
 };
 
-/** Build the index of the fp16 rows x [n, d] (host) in the HBM of params.devices[0] (or the current GPU). */
-auto build_in_memory(index_params const& params, const __half* x, int64_t n, int64_t d, build_record& rec)
+/** The dataset of a build: row-major [n, d], fp16 or fp32, in host or device memory. */
+struct dataset_view {
+  const void* data = nullptr;
+  int64_t n = 0, d = 0;
+  bool f32    = false;
+  bool device = false;
+};
+
+/**
+ * Build the index of x in the HBM of params.devices[0] (or the current GPU).  The rows are stored as
+ * fp16 (round to nearest) whatever their type; a device dataset is read in place.
+ */
+auto build_in_memory(index_params const& params, dataset_view const& x, build_record& rec)
   -> std::shared_ptr<index_impl>;
 /** Write the format-1 directory of a built index (meta.json last). */
 void write_index(index_impl const& ix, build_record const& rec, index_params const& params, std::string const& path);

@@ -275,6 +275,12 @@ __global__ void half_to_float_kernel(const __half* __restrict__ x, int64_t total
   if (t < total) out[t] = __half2float(x[t]);
 }
 
+__global__ void float_to_half_kernel(const float* __restrict__ x, int64_t total, __half* __restrict__ out)
+{
+  int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t < total) out[t] = __float2half_rn(x[t]);
+}
+
 template <typename T>
 void ensure(dbuf& b, int64_t count)
 {
@@ -323,8 +329,23 @@ void project_rows(const __half* x, int64_t n, int d, const float* mean, const fl
 void half_to_float(const __half* x, int64_t total, float* out, hipStream_t s)
 {
   if (total == 0) return;
-  half_to_float_kernel<<<grid_for(total, 256), 256, 0, s>>>(x, total, out);
-  OCTEX_HIP(hipGetLastError());
+  constexpr int64_t kPiece = int64_t{1} << 30;  // a launch covers fewer than 2^32 work-items
+  for (int64_t o = 0; o < total; o += kPiece) {
+    const int64_t m = std::min(kPiece, total - o);
+    half_to_float_kernel<<<grid_for(m, 256), 256, 0, s>>>(x + o, m, out + o);
+    OCTEX_HIP(hipGetLastError());
+  }
+}
+
+void float_to_half(const float* x, int64_t total, __half* out, hipStream_t s)
+{
+  if (total == 0) return;
+  constexpr int64_t kPiece = int64_t{1} << 30;
+  for (int64_t o = 0; o < total; o += kPiece) {
+    const int64_t m = std::min(kPiece, total - o);
+    float_to_half_kernel<<<grid_for(m, 256), 256, 0, s>>>(x + o, m, out + o);
+    OCTEX_HIP(hipGetLastError());
+  }
 }
 
 void make_sketch(const __half* x, int64_t n, int d, const float* mean, const float* basis, int S,

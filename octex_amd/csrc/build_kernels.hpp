@@ -17,6 +17,8 @@ void pca_scatter(const __half* x, int64_t n, int d, int64_t step, int64_t ns, co
 void project_rows(const __half* x, int64_t n, int d, const float* mean, const float* U, const float* shift, int w,
                   float* y, hipStream_t s);
 void half_to_float(const __half* x, int64_t total, float* out, hipStream_t s);
+/** out = fp16(x), round to nearest even (device arrays). */
+void float_to_half(const float* x, int64_t total, __half* out, hipStream_t s);
 /** The int8 sketch: scale = amax / 127 per coordinate, codes = round(((x - mean) @ basis) / scale). */
 void make_sketch(const __half* x, int64_t n, int d, const float* mean, const float* basis, int S,
                  std::vector<float>& scale, signed char* codes, hipStream_t s);

@@ -157,6 +157,25 @@ auto dl_matrix(DLManagedTensor* m, bool device) -> T*
   return reinterpret_cast<T*>(static_cast<char*>(t.data) + t.byte_offset);
 }
 
+/** The dataset of a build, where it lies: float32 or float16, host or device. */
+auto dataset_of(DLManagedTensor* m) -> octex::detail::dataset_view
+{
+  OCTEX_EXPECTS(m != nullptr, "octex: a DLPack tensor is NULL");
+  auto const& t  = m->dl_tensor;
+  const bool dev = t.device.device_type == kDLROCM;  // pinned host memory is read as host memory
+  octex::detail::dataset_view v;
+  if (t.dtype.code == kDLFloat && t.dtype.bits == 32) {
+    v.data = dl_matrix<float>(m, dev);
+    v.f32  = true;
+  } else if (t.dtype.code == kDLFloat && t.dtype.bits == 16) {
+    v.data = dl_matrix<__half>(m, dev);
+  } else {
+    octex::detail::fail("octex: the dataset must be float32 or float16");
+  }
+  v.n = t.shape[0], v.d = t.shape[1], v.device = dev;
+  return v;
+}
+
 }  // namespace
 
 // ==================================================================== cuVS core
@@ -310,29 +329,11 @@ extern "C" cuvsError_t cuvsOctexBuild(cuvsResources_t res, cuvsOctexIndexParams_
   return translate_exceptions([=] {
     OCTEX_EXPECTS(path != nullptr, "octex: the index directory is NULL");
     OCTEX_EXPECTS(params != nullptr && dataset != nullptr, "octex: NULL parameters or dataset");
-    auto* r           = as_res(res);
-    const auto p      = to_cpp(*params);
-    auto const& t     = dataset->dl_tensor;
-    const bool dev    = t.device.device_type == kDLROCM;
-    const std::string dir(path);
-    auto run = [&](auto tag) {
-      using T    = decltype(tag);
-      T* data    = dl_matrix<T>(dataset, dev);
-      int64_t n  = t.shape[0], d = t.shape[1];
-      std::vector<T> host;
-      if (dev) {  // the build reads the dataset from the host
-        host.resize(static_cast<size_t>(n * d));
-        OCTEX_HIP(hipMemcpy(host.data(), data, sizeof(T) * host.size(), hipMemcpyDefault));
-        data = host.data();
-      }
-      octex::build(*r, p, raft::host_matrix_view<const T, int64_t, raft::row_major>(data, n, d), dir);
-    };
-    if (t.dtype.code == kDLFloat && t.dtype.bits == 32)
-      run(float{});
-    else if (t.dtype.code == kDLFloat && t.dtype.bits == 16)
-      run(__half{});
-    else
-      octex::detail::fail("octex: the dataset must be float32 or float16");
+    (void)as_res(res);
+    const auto p = to_cpp(*params);
+    octex::detail::build_record rec;
+    auto impl = octex::detail::build_in_memory(p, dataset_of(dataset), rec);
+    octex::detail::write_index(*impl, rec, p, std::string(path));
   });
 }
 
@@ -434,30 +435,9 @@ extern "C" cuvsError_t octexBuildInMemory(cuvsResources_t res, cuvsOctexIndexPar
     (void)as_res(res);
     OCTEX_EXPECTS(params != nullptr && dataset != nullptr && index != nullptr, "octex: NULL argument");
     OCTEX_EXPECTS(index->addr == 0, "octex: the index handle already holds an index");
-    const auto p   = to_cpp(*params);
-    auto const& t  = dataset->dl_tensor;
-    const bool dev = t.device.device_type == kDLROCM;
-    const int64_t n = t.shape[0], d = t.shape[1];
-    std::vector<__half> host(static_cast<size_t>(n * d));
-    if (t.dtype.code == kDLFloat && t.dtype.bits == 16) {
-      auto* x = dl_matrix<__half>(dataset, dev);
-      OCTEX_HIP(hipMemcpy(host.data(), x, host.size() * sizeof(__half), hipMemcpyDefault));
-    } else if (t.dtype.code == kDLFloat && t.dtype.bits == 32) {
-      auto* x = dl_matrix<float>(dataset, dev);
-      std::vector<float> f;
-      const float* src = x;
-      if (dev) {
-        f.resize(host.size());
-        OCTEX_HIP(hipMemcpy(f.data(), x, f.size() * sizeof(float), hipMemcpyDefault));
-        src = f.data();
-      }
-      for (size_t i = 0; i < host.size(); i++)
-        host[i] = __float2half(src[i]);
-    } else {
-      octex::detail::fail("octex: the dataset must be float32 or float16");
-    }
+    const auto p = to_cpp(*params);
     octex::detail::build_record rec;
-    auto impl = octex::detail::build_in_memory(p, host.data(), n, d, rec);
+    auto impl = octex::detail::build_in_memory(p, dataset_of(dataset), rec);
     if (path != nullptr) octex::detail::write_index(*impl, rec, p, std::string(path));
     if (seconds != nullptr) *seconds = rec.phases.empty() ? 0.0 : rec.phases.back().second;
     index->addr = reinterpret_cast<uintptr_t>(new octex::index(impl));

@@ -136,10 +136,13 @@ def test_build_inputs(octex, data, tmp_path):
     """float16 and device (torch) datasets build the same index as float32 host data."""
     X = data[0][:3000]
     a, _ = octex.build_in_memory(X, copies=8, seed=2, log_buckets=12, table_len=16)
-    b, _ = octex.build_in_memory(torch.from_numpy(X).cuda(), copies=8, seed=2, log_buckets=12, table_len=16)
+    xf = torch.from_numpy(X).cuda()
+    b, _ = octex.build_in_memory(xf, copies=8, seed=2, log_buckets=12, table_len=16)
     c, _ = octex.build_in_memory(X.astype(np.float16), copies=8, seed=2, log_buckets=12, table_len=16)
+    xh = xf.half()
+    e, _ = octex.build_in_memory(xh, copies=8, seed=2, log_buckets=12, table_len=16)
     Q = data[1]
-    r = [ix.search(Q, k=10, read=16, starts=32) for ix in (a, b, c)]
+    r = [ix.search(Q, k=10, read=16, starts=32) for ix in (a, b, c, e)]
     for D, I in r[1:]:
         assert np.array_equal(I, r[0][1]) and np.array_equal(D, r[0][0])
 
