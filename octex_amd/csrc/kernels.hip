@@ -16,6 +16,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 namespace cuvs::neighbors::octex::detail {
 
@@ -217,22 +218,86 @@ __device__ __forceinline__ int hash_log_dev(int total, int log_cap)
 }
 
 /**
+ * Sketch scores of the candidates crow[0, n) of one query (search_kernels.cuh:227-251).  The reference
+ * lets an Lr-lane group (Lr = the next power of two >= S / 16, at most 32) score one candidate: lane
+ * `sub` reduces 16-element chunk `sub` as u = fma(code, scale, -qs), d = fma(u, u, d), then the group
+ * adds by an xor butterfly.  Here GS = max(1, Lr / 4) lanes score a candidate, each holding the
+ * chunks sub = g, g + GS, ..., so a wavefront has 64 / GS rows in flight instead of 64 / Lr: the
+ * butterfly levels of width >= GS become in-lane adds of the same operands in the same order, the
+ * rest stay shuffles, and every score is bit-identical to the Lr-lane reduction.
+ */
+template <int LR>
+__device__ __forceinline__ void sketch_scores(const int* crow, int n, const signed char* __restrict__ code,
+                                              int S, const float* qv, const float* sc, float* drow)
+{
+  constexpr int GS  = LR > 4 ? LR / 4 : 1;  // lanes per candidate
+  constexpr int NS  = LR / GS;              // chunks per lane
+  constexpr int RPW = 64 / GS;              // candidates per wavefront
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int g = lane % GS, nch = S / 16;
+  for (int j0 = wid * RPW; j0 < n; j0 += nw * RPW) {
+    asm volatile("" ::: "memory");  // scale and qs are re-read from LDS, not held in registers
+    const int j = j0 + lane / GS;
+    float part[NS];
+#pragma unroll
+    for (int t = 0; t < NS; t++)
+      part[t] = 0.f;
+    if (j < n) {
+      const signed char* x = code + static_cast<int64_t>(crow[j]) * S;
+      int4 w[NS];
+#pragma unroll
+      for (int t = 0; t < NS; t++) {  // every load of the row first
+        const int sub = g + t * GS;
+        if (sub < nch) w[t] = *reinterpret_cast<const int4*>(x + sub * 16);
+      }
+#pragma unroll
+      for (int t = 0; t < NS; t++) {
+        const int sub = g + t * GS;
+        if (sub < nch) {
+          const signed char* bb = reinterpret_cast<const signed char*>(&w[t]);
+          const float* scs      = sc + sub * 16;
+          const float* qvs      = qv + sub * 16;
+          float d               = 0.f;
+#pragma unroll
+          for (int e = 0; e < 16; e++) {
+            float u = fmaf(static_cast<float>(bb[e]), scs[e], -qvs[e]);
+            d       = fmaf(u, u, d);
+          }
+          part[t] = d;
+        }
+      }
+    }
+#pragma unroll
+    for (int o = LR / 2; o >= GS; o >>= 1)  // butterfly levels inside the lane: sub i += sub i + o
+#pragma unroll
+      for (int t = 0; t < o / GS; t++)
+        part[t] = part[t] + part[t + o / GS];
+    float d = part[0];
+#pragma unroll
+    for (int o = GS / 2; o; o >>= 1)
+      d += __shfl_xor(d, o);
+    if (j < n && g == 0) drow[j] = d;
+  }
+}
+
+/**
  * Distinct ids of all segments of a query with their sketch scores.  The entries of all segments are
- * split evenly over the workgroup (exclusive prefix of the segment lengths, binary search per entry);
- * an LDS open-addressing set drops duplicates; new ids are appended to the query's candidate row by
- * one atomic per wavefront.  Then Lr lanes per candidate read its sketch row (16 bytes each) and
- * reduce the score by an xor butterfly.
+ * split evenly over the workgroup (exclusive prefix of the segment lengths, binary search per entry),
+ * kUnroll entries per thread with their loads issued together; an LDS open-addressing set drops
+ * duplicates; new ids are appended to the query's candidate row by one atomic per wavefront.  Then the
+ * candidates are scored (sketch_scores; LR = the reference's lanes per candidate for this S).
  *
  * kRows = false: segment c = (first entry, length) in the lists of copy c (row stride `stride`).
  * kRows = true:  segment = (row, length) of the neighbor table [N, table_len]; -1 entries skipped.
  */
-template <bool kRows>
+template <bool kRows, int LR>
 __global__ __launch_bounds__(kGatherThreads) void gather_kernel(
   const int2* __restrict__ seg, int nseg, const long long* __restrict__ list_ptr,
   const int* __restrict__ table, int table_len, int64_t N, const signed char* __restrict__ code,
   const float* __restrict__ scale, const float* __restrict__ qs, int S, int W, int logW,
   int* __restrict__ cand, float* __restrict__ dist, int* __restrict__ nout)
 {
+  constexpr int kUnroll = 4;
   const int q = blockIdx.x;
   extern __shared__ long long smq[];
   const int** lp = reinterpret_cast<const int**>(smq);  // [nseg] list of every copy (lists only)
@@ -242,7 +307,7 @@ __global__ __launch_bounds__(kGatherThreads) void gather_kernel(
   int* st        = pre + nseg + 1;                  // [nseg] segment starts
   int* ht        = st + nseg;                       // hash set
   __shared__ int cnt;
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, nw = blockDim.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   for (int i = tid; i < S; i += blockDim.x) {
     qv[i] = qs[static_cast<int64_t>(q) * S + i];
     sc[i] = scale[i];
@@ -275,75 +340,60 @@ __global__ __launch_bounds__(kGatherThreads) void gather_kernel(
     ht[i] = -1;
   __syncthreads();
   int* crow = cand + static_cast<int64_t>(q) * W;
-  for (int i0 = 0; i0 < total; i0 += blockDim.x) {
-    const int i = i0 + tid;
-    bool fresh  = false;
-    int v       = -1;
-    if (i < total) {
-      int lo = 0, hi = nseg - 1;
-      while (lo < hi) {
-        int mid = (lo + hi + 1) >> 1;
-        if (pre[mid] <= i)
-          lo = mid;
-        else
-          hi = mid - 1;
+  const int step = blockDim.x;
+  for (int i0 = 0; i0 < total; i0 += step * kUnroll) {
+    int v[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++) {  // the loads of kUnroll entries, issued together
+      const int i = i0 + u * step + tid;
+      v[u]        = -1;
+      if (i < total) {
+        int lo = 0, hi = nseg - 1;
+        while (lo < hi) {
+          int mid = (lo + hi + 1) >> 1;
+          if (pre[mid] <= i)
+            lo = mid;
+          else
+            hi = mid - 1;
+        }
+        if constexpr (kRows) {
+          v[u] = table[static_cast<int64_t>(st[lo]) * table_len + (i - pre[lo])];
+        } else {
+          v[u] = lp[lo][st[lo] + (i - pre[lo])];
+        }
       }
-      if constexpr (kRows) {
-        v = table[static_cast<int64_t>(st[lo]) * table_len + (i - pre[lo])];
-      } else {
-        v = lp[lo][st[lo] + (i - pre[lo])];
-      }
-      if (v >= 0 && v < N) {  // -1: padding of a table row (search_kernels.cuh:213)
-        unsigned s = (static_cast<unsigned>(v) * kIdHash) & (HT - 1);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++) {
+      bool fresh = false;
+      if (v[u] >= 0 && v[u] < N) {  // -1: padding of a table row (search_kernels.cuh:213)
+        unsigned h = (static_cast<unsigned>(v[u]) * kIdHash) & (HT - 1);
         for (int p = 0; p < HT; p++) {
-          int prev = atomicCAS(&ht[s], -1, v);
+          int prev = atomicCAS(&ht[h], -1, v[u]);
           if (prev == -1) {
             fresh = true;
             break;
           }
-          if (prev == v) break;
-          s = (s + 1) & (HT - 1);
+          if (prev == v[u]) break;
+          h = (h + 1) & (HT - 1);
         }
       }
-    }
-    const unsigned long long mask = __ballot(fresh);
-    if (mask != 0) {
-      const int leader = __ffsll(static_cast<long long>(mask)) - 1;
-      int at           = 0;
-      if (lane == leader) at = atomicAdd(&cnt, __popcll(mask));
-      at = __shfl(at, leader);
-      if (fresh) {
-        int slot = at + __popcll(mask & ((1ULL << lane) - 1ULL));
-        if (slot < W) crow[slot] = v;
+      const unsigned long long mask = __ballot(fresh);
+      if (mask != 0) {
+        const int leader = __ffsll(static_cast<long long>(mask)) - 1;
+        int at           = 0;
+        if (lane == leader) at = atomicAdd(&cnt, __popcll(mask));
+        at = __shfl(at, leader);
+        if (fresh) {
+          int slot = at + __popcll(mask & ((1ULL << lane) - 1ULL));
+          if (slot < W) crow[slot] = v[u];
+        }
       }
     }
   }
   __syncthreads();
   const int n = min(cnt, W);
-  int Lr      = 1;  // lanes per candidate: the next power of two >= S / 16, at most 32
-  while (Lr < S / 16 && Lr < 32)
-    Lr <<= 1;
-  const int G = 64 / Lr, sub = lane & (Lr - 1);
-  float* drow = dist + static_cast<int64_t>(q) * W;
-  for (int j0 = wid * G; j0 < n; j0 += nw * G) {
-    const int j = j0 + lane / Lr;
-    float d     = 0.f;
-    if (j < n) {
-      const signed char* x = code + static_cast<int64_t>(crow[j]) * S;
-      for (int k = sub * 16; k < S; k += Lr * 16) {
-        int4 w                = *reinterpret_cast<const int4*>(x + k);
-        const signed char* bb = reinterpret_cast<const signed char*>(&w);
-#pragma unroll
-        for (int t = 0; t < 16; t++) {
-          float u = fmaf(static_cast<float>(bb[t]), sc[k + t], -qv[k + t]);
-          d       = fmaf(u, u, d);
-        }
-      }
-    }
-    for (int o = Lr >> 1; o; o >>= 1)
-      d += __shfl_xor(d, o);
-    if (j < n && sub == 0) drow[j] = d;
-  }
+  sketch_scores<LR>(crow, n, code, S, qv, sc, dist + static_cast<int64_t>(q) * W);
   if (tid == 0) nout[q] = n;
 }
 
@@ -485,14 +535,79 @@ __device__ void select_smallest(const unsigned* __restrict__ kd, const int* __re
 }
 
 /**
- * Squared distances of the fp16 rows sid[0, ns) to the fp32 query sq (search_kernels.cuh:325-342):
- * one wavefront per row, lane l takes the half2 pairs l, l + 64, ..., then a 64-lane xor butterfly.
+ * Squared distance of one fp16 row of P = D / 2 <= 64 half2 pairs to the fp32 query sq, computed by one
+ * lane in the order of the 64-lane reduction of exact_distances: pair k's partial
+ * fma(b, b, fma(a, a, 0)) stands for lane k (zero for k >= P), then the butterfly levels 32, 16, ..., 1
+ * as adds of the same operands.  The row is read as P / 4 16-byte loads, all issued first.
  */
+template <int P>
+__device__ __forceinline__ float row_distance(const __half* __restrict__ row, const float* sq)
+{
+  static_assert(P % 4 == 0 && P <= 64, "pairs per row");
+  const uint4* x = reinterpret_cast<const uint4*>(row);
+  uint4 w[P / 4];
+#pragma unroll
+  for (int c = 0; c < P / 4; c++)
+    w[c] = x[c];
+  const __half2* h = reinterpret_cast<const __half2*>(w);
+  float v[32];
+#pragma unroll
+  for (int i = 0; i < 32; i++) {
+    float lo = 0.f, hi = 0.f;
+    if (i < P) {
+      float2 f = __half22float2(h[i]);
+      float a = f.x - sq[2 * i], b = f.y - sq[2 * i + 1];
+      lo      = fmaf(b, b, fmaf(a, a, 0.f));
+    }
+    if (i + 32 < P) {
+      float2 f = __half22float2(h[i + 32]);
+      float a = f.x - sq[2 * (i + 32)], b = f.y - sq[2 * (i + 32) + 1];
+      hi      = fmaf(b, b, fmaf(a, a, 0.f));
+    }
+    v[i] = lo + hi;
+  }
+#pragma unroll
+  for (int o = 16; o; o >>= 1)
+#pragma unroll
+    for (int i = 0; i < o; i++)
+      v[i] = v[i] + v[i + o];
+  return v[0];
+}
+
+template <int P>
+__device__ void exact_rows(const int* sid, int ns, const __half* __restrict__ vectors, const float* sq, float* sd)
+{
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  for (int j = wid * 64 + lane; j - lane < ns; j += nw * 64)
+    if (j < ns) sd[j] = row_distance<P>(vectors + static_cast<int64_t>(sid[j]) * (2 * P), sq);
+}
+
+/**
+ * Squared distances of the fp16 rows sid[0, ns) to the fp32 query sq (search_kernels.cuh:325-342):
+ * the value of a 64-lane reduction in which lane l takes the half2 pairs l, l + 64, ... (fma(a, a, acc),
+ * fma(b, b, acc)) and an xor butterfly adds the lanes.  kLanePerRow (D <= 128, a multiple of 8; chosen
+ * for deep reranks) scores a row per lane (row_distance, 64 rows in flight per wavefront), otherwise a
+ * wavefront scores a row (fewer registers, better for a few rows or wide ones).
+ */
+template <bool kLanePerRow>
 __device__ void exact_distances(const int* sid, int ns, const __half* __restrict__ vectors, int D,
                                 const float* sq, float* sd)
 {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  const int P    = D / 2;
+  if constexpr (kLanePerRow) {
+    switch (D / 8) {
+#define OCTEX_ROWS(r) \
+  case r: exact_rows<4 * r>(sid, ns, vectors, sq, sd); break;
+      OCTEX_ROWS(1) OCTEX_ROWS(2) OCTEX_ROWS(3) OCTEX_ROWS(4) OCTEX_ROWS(5) OCTEX_ROWS(6) OCTEX_ROWS(7)
+      OCTEX_ROWS(8) OCTEX_ROWS(9) OCTEX_ROWS(10) OCTEX_ROWS(11) OCTEX_ROWS(12) OCTEX_ROWS(13) OCTEX_ROWS(14)
+      OCTEX_ROWS(15) OCTEX_ROWS(16)
+#undef OCTEX_ROWS
+      default: break;
+    }
+    __syncthreads();
+    return;
+  }
+  const int P = D / 2;
   for (int j = wid; j < ns; j += nw) {
     const __half2* x = reinterpret_cast<const __half2*>(vectors + static_cast<int64_t>(sid[j]) * D);
     float acc        = 0.f;
@@ -584,6 +699,7 @@ __device__ void store_keys(const uint64_t* key, int P, int KO, long long* pb, fl
  * Exact rerank of the R sketch-nearest candidates of a query, merged into its kept list of the best
  * KO (search_kernels.cuh:421-467).  fresh: the kept list starts empty.
  */
+template <bool kLanePerRow>
 __global__ __launch_bounds__(kKeepThreads) void rerank_keep_kernel(
   const int* __restrict__ cand, const float* __restrict__ dist, const int* __restrict__ nin, int W,
   const __half* __restrict__ vectors, int D, const float* __restrict__ Q, int R, int KO,
@@ -602,7 +718,7 @@ __global__ __launch_bounds__(kKeepThreads) void rerank_keep_kernel(
   select_smallest(reinterpret_cast<const unsigned*>(dist + static_cast<int64_t>(q) * W),
                   cand + static_cast<int64_t>(q) * W, n, R, sid, nullptr, hist, st);
   const int ns = st.nsel;
-  exact_distances(sid, ns, vectors, D, sq, sd);
+  exact_distances<kLanePerRow>(sid, ns, vectors, D, sq, sd);
   long long* pb = bi + static_cast<int64_t>(q) * KO;
   float* pd     = bd + static_cast<int64_t>(q) * KO;
   int P         = 2;
@@ -709,6 +825,7 @@ __global__ __launch_bounds__(256) void pick_starts_kernel(const long long* __res
 }
 
 /** Exact rerank of the first R kept entries (sketch-rank mode) into the best k (:634-669). */
+template <bool kLanePerRow>
 __global__ __launch_bounds__(kKeepThreads) void final_rerank_kernel(
   const long long* __restrict__ si, int KO, int R, const __half* __restrict__ vectors, int D,
   const float* __restrict__ Q, int k, long long* __restrict__ bi, float* __restrict__ bd)
@@ -736,7 +853,7 @@ __global__ __launch_bounds__(kKeepThreads) void final_rerank_kernel(
   }
   __syncthreads();
   const int ns = nsel;
-  exact_distances(sid, ns, vectors, D, sq, sd);
+  exact_distances<kLanePerRow>(sid, ns, vectors, D, sq, sd);
   int P = 2;
   while (P < R)
     P <<= 1;
@@ -853,18 +970,38 @@ void launch_gather(bool rows, const int2* seg, int nseg, int m, const long long*
   OCTEX_EXPECTS(S % 16 == 0 && S >= 16 && S <= 512, "octex: sketch width: a multiple of 16, <= 512");
   const size_t smem = gather_smem(W, S, nseg);
   OCTEX_EXPECTS(smem <= 160 * 1024, "octex: gather needs %zu bytes of LDS (max 160 KiB)", smem);
-  if (rows) {
-    OCTEX_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gather_kernel<true>),
+  int Lr = 1;  // the reference's lanes per candidate: the next power of two >= S / 16, at most 32
+  while (Lr < S / 16 && Lr < 32)
+    Lr <<= 1;
+  auto go = [&](auto rows_tag, auto lr_tag) {
+    constexpr bool R = decltype(rows_tag)::value;
+    constexpr int LR = decltype(lr_tag)::value;
+    OCTEX_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gather_kernel<R, LR>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
-    gather_kernel<true><<<m, kGatherThreads, smem, s>>>(seg, nseg, list_ptr, table, table_len, n, code,
-                                                        scale, qs, S, W, logW, cand, dist, nout);
-  } else {
-    OCTEX_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gather_kernel<false>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
-    gather_kernel<false><<<m, kGatherThreads, smem, s>>>(seg, nseg, list_ptr, table, table_len, n, code,
-                                                         scale, qs, S, W, logW, cand, dist, nout);
-  }
+    gather_kernel<R, LR><<<m, kGatherThreads, smem, s>>>(seg, nseg, list_ptr, table, table_len, n, code, scale,
+                                                          qs, S, W, logW, cand, dist, nout);
+  };
+  auto by_lr = [&](auto rows_tag) {
+    switch (Lr) {
+      case 1: go(rows_tag, std::integral_constant<int, 1>{}); break;
+      case 2: go(rows_tag, std::integral_constant<int, 2>{}); break;
+      case 4: go(rows_tag, std::integral_constant<int, 4>{}); break;
+      case 8: go(rows_tag, std::integral_constant<int, 8>{}); break;
+      case 16: go(rows_tag, std::integral_constant<int, 16>{}); break;
+      default: go(rows_tag, std::integral_constant<int, 32>{}); break;
+    }
+  };
+  if (rows)
+    by_lr(std::true_type{});
+  else
+    by_lr(std::false_type{});
   OCTEX_HIP(hipGetLastError());
+}
+
+/** Exact distances a row per lane for reranks of at least 32 rows of D <= 128 (a multiple of 8). */
+static auto lane_per_row(int R, int D) -> bool
+{
+  return R >= 32 && D % 8 == 0 && D <= 128;
 }
 
 void launch_rerank_keep(const int* cand, const float* dist, const int* nin, int m, int W,
@@ -875,8 +1012,12 @@ void launch_rerank_keep(const int* cand, const float* dist, const int* nin, int 
   OCTEX_EXPECTS(R >= 1 && R <= kMaxRerank && KO + R <= kMaxKeepSort && KO >= 1,
                 "octex: rerank in [1, 512] and max(starts, k) + rerank <= 1024");
   OCTEX_EXPECTS(D % 2 == 0, "octex: the dimension must be even");
-  rerank_keep_kernel<<<m, kKeepThreads, D * sizeof(float), s>>>(cand, dist, nin, W, vectors, D, Q, R,
-                                                                KO, si, sd, fresh);
+  if (lane_per_row(R, D))
+    rerank_keep_kernel<true><<<m, kKeepThreads, D * sizeof(float), s>>>(cand, dist, nin, W, vectors, D, Q, R, KO,
+                                                                      si, sd, fresh);
+  else
+    rerank_keep_kernel<false><<<m, kKeepThreads, D * sizeof(float), s>>>(cand, dist, nin, W, vectors, D, Q, R, KO,
+                                                                       si, sd, fresh);
   OCTEX_HIP(hipGetLastError());
 }
 
@@ -905,7 +1046,10 @@ void launch_final_rerank(const long long* si, int m, int KO, int R, const __half
   if (m == 0) return;
   OCTEX_EXPECTS(R >= k && R <= kMaxRerank && R <= KO,
                 "octex: final_rerank 0 (sketch order) or k <= final_rerank <= 512");
-  final_rerank_kernel<<<m, kKeepThreads, D * sizeof(float), s>>>(si, KO, R, vectors, D, Q, k, bi, bd);
+  if (lane_per_row(R, D))
+    final_rerank_kernel<true><<<m, kKeepThreads, D * sizeof(float), s>>>(si, KO, R, vectors, D, Q, k, bi, bd);
+  else
+    final_rerank_kernel<false><<<m, kKeepThreads, D * sizeof(float), s>>>(si, KO, R, vectors, D, Q, k, bi, bd);
   OCTEX_HIP(hipGetLastError());
 }
 

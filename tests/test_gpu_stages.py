@@ -241,10 +241,11 @@ def random_candidates(g, m, W, n_max, N, ties=True):
     return cand, dist, nin
 
 
+@pytest.mark.parametrize("R", [16, 48])  # a row per wavefront / a row per lane
 @pytest.mark.parametrize("fresh", [True, False])
-def test_rerank_keep_matches_oracle(L, ix, dix, small_index, fresh):
+def test_rerank_keep_matches_oracle(L, ix, dix, small_index, fresh, R):
     g = np.random.default_rng(4 + fresh)
-    m, W, KO, R = 40, 2048, 64, 48
+    m, W, KO = 40, 2048, 64
     cand, dist, nin = random_candidates(g, m, W, 1500, ix.n)
     Q = small_index["Q"][:m]
     si = np.full((m, KO), -1, np.int64)
@@ -303,9 +304,10 @@ def test_pick_starts_matches_oracle(L):
         si = np.stack([np.concatenate([g.permutation(r[:200]), r[200:]]) for r in si])  # a new kept order
 
 
-def test_final_rerank_and_take_k(L, ix, dix, small_index):
+@pytest.mark.parametrize("R", [20, 64])
+def test_final_rerank_and_take_k(L, ix, dix, small_index, R):
     g = np.random.default_rng(9)
-    m, KO, R, k = 25, 128, 64, 10
+    m, KO, k = 25, 128, 10
     si = np.stack([g.choice(ix.n, KO, replace=False) for _ in range(m)]).astype(np.int64)
     si[:, 40:50] = -1
     Q = small_index["Q"][:m]
