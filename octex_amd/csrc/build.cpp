@@ -26,6 +26,7 @@
 #include <cstdlib>
 #include <filesystem>
 #include <fstream>
+#include <memory>
 #include <numeric>
 #include <random>
 #include <sstream>
@@ -194,51 +195,113 @@ struct reverse_rule {
 
 void merge_reverse(std::vector<int32_t> const& fwd, int64_t n, reverse_rule const& rr, std::vector<int32_t>& table)
 {
-  const int kin = rr.kin;
-  std::vector<int32_t> cnt(n + 1, 0);
-  parallel_for(n, [&](int64_t v0, int64_t v1) {
+  // Every reverse entry (u <- v at forward rank r) goes to the block of 2^16 u's that holds u, by
+  // sequential appends per thread (threads own ascending v ranges, so a block's entries arrive in v
+  // order); each block is then bucketed by u, and each u's entries stably by r: (r, v) order.
+  const int kin = rr.kin, ks = rr.ks;
+  OCTEX_EXPECTS(ks <= 256, "octex: the reverse-edge merge takes forward rows of at most 256 entries");
+  constexpr int kLogBlock = 16;
+  const int64_t B = (n >> kLogBlock) + 1;
+  const int T     = static_cast<int>(std::clamp<int64_t>(n / 4096, 1, 16));
+  auto v_range   = [&](int t) { return std::make_pair(n * t / T, n * (t + 1) / T); };
+  auto run       = [&](auto&& body) {
+    std::vector<std::thread> th;
+    for (int t = 0; t < T; t++)
+      th.emplace_back(body, t);
+    for (auto& x : th)
+      x.join();
+  };
+  std::vector<int64_t> pos(static_cast<size_t>(T) * B, 0);  // [t][block]
+  run([&](int t) {
+    auto [v0, v1] = v_range(t);
+    std::vector<int64_t> c(B, 0);
     for (int64_t v = v0; v < v1; v++)
-      for (int r = 0; r < rr.ks; r++) {
-        int32_t u = fwd[v * kin + r];
-        if (u >= 0 && u != v) __atomic_fetch_add(&cnt[u + 1], 1, __ATOMIC_RELAXED);
+      for (int r = 0; r < ks; r++) {
+        const int32_t u = fwd[v * kin + r];
+        if (u >= 0 && u != v) c[u >> kLogBlock]++;
       }
+    std::copy(c.begin(), c.end(), pos.begin() + static_cast<int64_t>(t) * B);
   });
-  std::vector<int64_t> off(n + 1, 0);
-  for (int64_t u = 0; u < n; u++)
-    off[u + 1] = off[u] + cnt[u + 1];
-  std::vector<uint64_t> ent(off[n]);
-  std::vector<int64_t> cur(off.begin(), off.end() - 1);
-  parallel_for(n, [&](int64_t v0, int64_t v1) {
+  std::vector<int64_t> boff(B + 1, 0);  // block-major, thread-minor
+  int64_t acc = 0;
+  for (int64_t b = 0; b < B; b++) {
+    boff[b] = acc;
+    for (int t = 0; t < T; t++) {
+      int64_t& p = pos[static_cast<size_t>(t) * B + b];
+      const int64_t c = p;
+      p = acc;
+      acc += c;
+    }
+  }
+  boff[B] = acc;
+  std::unique_ptr<uint64_t[]> ent(new uint64_t[std::max<int64_t>(acc, 1)]);  // (u % 2^16) << 40 | r << 32 | v
+  run([&](int t) {
+    auto [v0, v1] = v_range(t);
+    int64_t* p = pos.data() + static_cast<int64_t>(t) * B;
     for (int64_t v = v0; v < v1; v++)
-      for (int r = 0; r < rr.ks; r++) {
-        int32_t u = fwd[v * kin + r];
-        if (u >= 0 && u != v) {
-          int64_t at = __atomic_fetch_add(&cur[u], 1, __ATOMIC_RELAXED);
-          ent[at]    = (static_cast<uint64_t>(r) << 32) | static_cast<uint32_t>(v);
-        }
+      for (int r = 0; r < ks; r++) {
+        const int32_t u = fwd[v * kin + r];
+        if (u >= 0 && u != v)
+          ent[p[u >> kLogBlock]++] = (static_cast<uint64_t>(u & ((1 << kLogBlock) - 1)) << 40) |
+                                     (static_cast<uint64_t>(r) << 32) | static_cast<uint32_t>(v);
       }
   });
   table.assign(static_cast<size_t>(n) * rr.kout, -1);
-  parallel_for(n, [&](int64_t u0, int64_t u1) {
-    std::vector<int32_t> pri;
-    for (int64_t u = u0; u < u1; u++) {
-      std::sort(ent.begin() + off[u], ent.begin() + off[u + 1]);
-      pri.clear();
-      for (int t = 0; t < rr.kf; t++)
-        pri.push_back(fwd[u * kin + t]);
-      for (int t = 0; t < rr.kr && off[u] + t < off[u + 1]; t++)
-        pri.push_back(static_cast<int32_t>(ent[off[u] + t] & 0xffffffffULL));
-      for (int t = rr.kf; t < kin; t++)
-        pri.push_back(fwd[u * kin + t]);
-      int o = 0;
-      int32_t* row = table.data() + u * rr.kout;
-      for (size_t i = 0; i < pri.size() && o < rr.kout; i++) {
-        int32_t v = pri[i];
-        if (v < 0 || v == u) continue;
-        bool dup = false;
-        for (int j = 0; j < o; j++)
-          dup |= row[j] == v;
-        if (!dup) row[o++] = v;
+  std::atomic<int64_t> next{0};
+  run([&](int) {
+    std::vector<int32_t> cu, tmp;
+    std::vector<uint64_t> srt;
+    std::vector<int32_t> rc(ks + 1);
+    const int log_hs = std::max(8, log2_ceil(4 * int64_t{rr.kout}));  // at most a quarter full
+    const unsigned hmask = (1u << log_hs) - 1;
+    std::vector<uint32_t> stamp(hmask + 1, 0);
+    std::vector<int32_t> slot(hmask + 1);
+    uint32_t epoch = 0;
+    for (int64_t b; (b = next.fetch_add(1)) < B;) {
+      const int64_t u0 = b << kLogBlock, nu = std::min<int64_t>(int64_t{1} << kLogBlock, n - u0);
+      const int64_t e0 = boff[b], ne = boff[b + 1] - e0;
+      cu.assign(nu + 1, 0);
+      srt.resize(ne);
+      for (int64_t i = 0; i < ne; i++)
+        cu[(ent[e0 + i] >> 40) + 1]++;
+      for (int64_t u = 0; u < nu; u++)
+        cu[u + 1] += cu[u];
+      std::vector<int32_t> at(cu.begin(), cu.end() - 1);
+      for (int64_t i = 0; i < ne; i++) {
+        const uint64_t e = ent[e0 + i];
+        srt[at[e >> 40]++] = e;
+      }
+      for (int64_t ul = 0; ul < nu; ul++) {
+        const int64_t u    = u0 + ul;
+        const uint64_t* eu = srt.data() + cu[ul];
+        const int m        = cu[ul + 1] - cu[ul];
+        std::fill(rc.begin(), rc.end(), 0);
+        for (int i = 0; i < m; i++)
+          rc[((eu[i] >> 32) & 0xff) + 1]++;
+        for (int r = 0; r < ks; r++)
+          rc[r + 1] += rc[r];
+        if (static_cast<int>(tmp.size()) < m) tmp.resize(m);
+        for (int i = 0; i < m; i++)
+          tmp[rc[(eu[i] >> 32) & 0xff]++] = static_cast<int32_t>(eu[i] & 0xffffffffULL);
+        // kf forward, up to kr reverse, the other forward entries: the first kout distinct
+        int o         = 0;
+        int32_t* row  = table.data() + u * rr.kout;
+        epoch++;
+        auto add = [&](int32_t v) {
+          if (v < 0 || v == u || o >= rr.kout) return;
+          unsigned h = (static_cast<uint32_t>(v) * 2654435761u) >> (32 - log_hs);
+          for (; stamp[h] == epoch; h = (h + 1) & hmask)
+            if (slot[h] == v) return;
+          stamp[h] = epoch;
+          slot[h]  = v;
+          row[o++] = v;
+        };
+        for (int t = 0; t < rr.kf; t++)
+          add(fwd[u * kin + t]);
+        for (int t = 0; t < std::min(m, rr.kr); t++)
+          add(tmp[t]);
+        for (int t = rr.kf; t < kin && o < rr.kout; t++)
+          add(fwd[u * kin + t]);
       }
     }
   });

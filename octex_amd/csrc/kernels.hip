@@ -168,11 +168,12 @@ __global__ __launch_bounds__(256) void probe_kernel(const __half* __restrict__ Y
                                                     int64_t Mmax, const int* __restrict__ base,
                                                     int l, int lr, int logT, int2* __restrict__ seg)
 {
-  int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (t >= static_cast<int64_t>(m) * C) return;
-  const int c = static_cast<int>(t % C);
+  const int c     = static_cast<int>(t / m);  // a wavefront: 64 queries of one copy, so its offsets and
+  const int64_t u = (t % m) * C + c;          // keys lookups stay inside that copy's tables (few pages)
   float y[8 * B];
-  const uint4* yp = reinterpret_cast<const uint4*>(Y + t * 8 * B);
+  const uint4* yp = reinterpret_cast<const uint4*>(Y + u * 8 * B);
 #pragma unroll
   for (int i = 0; i < B; i++) {
     uint4 u        = yp[i];
@@ -203,7 +204,7 @@ __global__ __launch_bounds__(256) void probe_kernel(const __half* __restrict__ Y
       break;
     }
   }
-  seg[t] = sg;
+  seg[u] = sg;
 }
 
 // ------------------------------------------------------------------ gather (search_kernels.cuh:138-253)
@@ -218,65 +219,61 @@ __device__ __forceinline__ int hash_log_dev(int total, int log_cap)
 }
 
 /**
- * Sketch scores of the candidates crow[0, n) of one query (search_kernels.cuh:227-251).  The reference
- * lets an Lr-lane group (Lr = the next power of two >= S / 16, at most 32) score one candidate: lane
- * `sub` reduces 16-element chunk `sub` as u = fma(code, scale, -qs), d = fma(u, u, d), then the group
- * adds by an xor butterfly.  Here GS = max(1, Lr / 4) lanes score a candidate, each holding the
- * chunks sub = g, g + GS, ..., so a wavefront has 64 / GS rows in flight instead of 64 / Lr: the
- * butterfly levels of width >= GS become in-lane adds of the same operands in the same order, the
- * rest stay shuffles, and every score is bit-identical to the Lr-lane reduction.
+ * Sketch scores of the candidates crow[0, n) of one query (search_kernels.cuh:227-251): an LR-lane
+ * group (LR = the next power of two >= S / 16, at most 32) scores a candidate, lane `sub` reducing the
+ * 16-element chunks sub, sub + LR, ... as u = fma(code, scale, -qs), d = fma(u, u, d), then an xor
+ * butterfly over the group.  A candidate's row is read by one load instruction of its group (one
+ * address translation per row: rows lie anywhere in a sketch of many GB), and every group has kRows
+ * candidates' loads in flight before it computes.
  */
 template <int LR>
 __device__ __forceinline__ void sketch_scores(const int* crow, int n, const signed char* __restrict__ code,
                                               int S, const float* qv, const float* sc, float* drow)
 {
-  constexpr int GS  = LR > 4 ? LR / 4 : 1;  // lanes per candidate
-  constexpr int NS  = LR / GS;              // chunks per lane
-  constexpr int RPW = 64 / GS;              // candidates per wavefront
+  constexpr int kRows = 4;        // candidates per group in flight
+  constexpr int GPW   = 64 / LR;  // groups per wavefront
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  const int g = lane % GS, nch = S / 16;
-  for (int j0 = wid * RPW; j0 < n; j0 += nw * RPW) {
-    asm volatile("" ::: "memory");  // scale and qs are re-read from LDS, not held in registers
-    const int j = j0 + lane / GS;
-    float part[NS];
+  const int sub = lane & (LR - 1), grp = lane / LR;
+  const int k = sub * 16;         // this lane's chunk (S <= 512 = 32 chunks: one chunk per lane)
+  const bool has = k < S;
+  float s16[16], q16[16];         // the chunk's scale and query sketch, held in registers
 #pragma unroll
-    for (int t = 0; t < NS; t++)
-      part[t] = 0.f;
-    if (j < n) {
-      const signed char* x = code + static_cast<int64_t>(crow[j]) * S;
-      int4 w[NS];
+  for (int e = 0; e < 16; e++) {
+    s16[e] = has ? sc[k + e] : 0.f;
+    q16[e] = has ? qv[k + e] : 0.f;
+  }
+  const int per_wave = GPW * kRows;
+  // Loads are unconditional (past-the-end candidates read the last one, chunkless lanes chunk 0) so
+  // that every row of the group is requested before the first one is used.
+  for (int j0 = wid * per_wave; j0 < n; j0 += nw * per_wave) {
+    int id[kRows];
 #pragma unroll
-      for (int t = 0; t < NS; t++) {  // every load of the row first
-        const int sub = g + t * GS;
-        if (sub < nch) w[t] = *reinterpret_cast<const int4*>(x + sub * 16);
+    for (int r = 0; r < kRows; r++)  // candidate j0 + r * GPW + grp
+      id[r] = crow[min(j0 + r * GPW + grp, n - 1)];
+    int4 w[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; r++)
+      w[r] = *reinterpret_cast<const int4*>(code + static_cast<int64_t>(id[r]) * S + (has ? k : 0));
+    float d[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; r++) {
+      const signed char* bb = reinterpret_cast<const signed char*>(&w[r]);
+      float acc             = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        float u = fmaf(static_cast<float>(bb[e]), s16[e], -q16[e]);
+        acc     = fmaf(u, u, acc);
       }
-#pragma unroll
-      for (int t = 0; t < NS; t++) {
-        const int sub = g + t * GS;
-        if (sub < nch) {
-          const signed char* bb = reinterpret_cast<const signed char*>(&w[t]);
-          const float* scs      = sc + sub * 16;
-          const float* qvs      = qv + sub * 16;
-          float d               = 0.f;
-#pragma unroll
-          for (int e = 0; e < 16; e++) {
-            float u = fmaf(static_cast<float>(bb[e]), scs[e], -qvs[e]);
-            d       = fmaf(u, u, d);
-          }
-          part[t] = d;
-        }
-      }
+      d[r] = has ? acc : 0.f;
     }
 #pragma unroll
-    for (int o = LR / 2; o >= GS; o >>= 1)  // butterfly levels inside the lane: sub i += sub i + o
+    for (int r = 0; r < kRows; r++) {
 #pragma unroll
-      for (int t = 0; t < o / GS; t++)
-        part[t] = part[t] + part[t + o / GS];
-    float d = part[0];
-#pragma unroll
-    for (int o = GS / 2; o; o >>= 1)
-      d += __shfl_xor(d, o);
-    if (j < n && g == 0) drow[j] = d;
+      for (int o = LR >> 1; o; o >>= 1)
+        d[r] += __shfl_xor(d[r], o);
+      const int j = j0 + r * GPW + grp;
+      if (j < n && sub == 0) drow[j] = d[r];
+    }
   }
 }
 
@@ -344,25 +341,25 @@ __global__ __launch_bounds__(kGatherThreads) void gather_kernel(
   for (int i0 = 0; i0 < total; i0 += step * kUnroll) {
     int v[kUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; u++) {  // the loads of kUnroll entries, issued together
-      const int i = i0 + u * step + tid;
-      v[u]        = -1;
-      if (i < total) {
-        int lo = 0, hi = nseg - 1;
-        while (lo < hi) {
-          int mid = (lo + hi + 1) >> 1;
-          if (pre[mid] <= i)
-            lo = mid;
-          else
-            hi = mid - 1;
-        }
-        if constexpr (kRows) {
-          v[u] = table[static_cast<int64_t>(st[lo]) * table_len + (i - pre[lo])];
-        } else {
-          v[u] = lp[lo][st[lo] + (i - pre[lo])];
-        }
+    for (int u = 0; u < kUnroll; u++) {  // kUnroll entries' loads issued together (past the end: the last)
+      const int i = min(i0 + u * step + tid, total - 1);
+      int lo = 0, hi = nseg - 1;
+      while (lo < hi) {
+        int mid = (lo + hi + 1) >> 1;
+        if (pre[mid] <= i)
+          lo = mid;
+        else
+          hi = mid - 1;
+      }
+      if constexpr (kRows) {
+        v[u] = table[static_cast<int64_t>(st[lo]) * table_len + (i - pre[lo])];
+      } else {
+        v[u] = lp[lo][st[lo] + (i - pre[lo])];
       }
     }
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++)
+      if (i0 + u * step + tid >= total) v[u] = -1;
 #pragma unroll
     for (int u = 0; u < kUnroll; u++) {
       bool fresh = false;
@@ -535,93 +532,47 @@ __device__ void select_smallest(const unsigned* __restrict__ kd, const int* __re
 }
 
 /**
- * Squared distance of one fp16 row of P = D / 2 <= 64 half2 pairs to the fp32 query sq, computed by one
- * lane in the order of the 64-lane reduction of exact_distances: pair k's partial
- * fma(b, b, fma(a, a, 0)) stands for lane k (zero for k >= P), then the butterfly levels 32, 16, ..., 1
- * as adds of the same operands.  The row is read as P / 4 16-byte loads, all issued first.
+ * Squared distances of the fp16 rows sid[0, ns) to the fp32 query sq (search_kernels.cuh:325-342): a
+ * wavefront scores a row, lane l taking the half2 pairs l, l + 64, ... (acc = fma(a, a, acc),
+ * fma(b, b, acc)), then a 64-lane xor butterfly.  A row is read by one load instruction (one address
+ * translation for a row anywhere in many GB of vectors) and every wavefront has kRows rows in flight.
  */
-template <int P>
-__device__ __forceinline__ float row_distance(const __half* __restrict__ row, const float* sq)
-{
-  static_assert(P % 4 == 0 && P <= 64, "pairs per row");
-  const uint4* x = reinterpret_cast<const uint4*>(row);
-  uint4 w[P / 4];
-#pragma unroll
-  for (int c = 0; c < P / 4; c++)
-    w[c] = x[c];
-  const __half2* h = reinterpret_cast<const __half2*>(w);
-  float v[32];
-#pragma unroll
-  for (int i = 0; i < 32; i++) {
-    float lo = 0.f, hi = 0.f;
-    if (i < P) {
-      float2 f = __half22float2(h[i]);
-      float a = f.x - sq[2 * i], b = f.y - sq[2 * i + 1];
-      lo      = fmaf(b, b, fmaf(a, a, 0.f));
-    }
-    if (i + 32 < P) {
-      float2 f = __half22float2(h[i + 32]);
-      float a = f.x - sq[2 * (i + 32)], b = f.y - sq[2 * (i + 32) + 1];
-      hi      = fmaf(b, b, fmaf(a, a, 0.f));
-    }
-    v[i] = lo + hi;
-  }
-#pragma unroll
-  for (int o = 16; o; o >>= 1)
-#pragma unroll
-    for (int i = 0; i < o; i++)
-      v[i] = v[i] + v[i + o];
-  return v[0];
-}
-
-template <int P>
-__device__ void exact_rows(const int* sid, int ns, const __half* __restrict__ vectors, const float* sq, float* sd)
-{
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  for (int j = wid * 64 + lane; j - lane < ns; j += nw * 64)
-    if (j < ns) sd[j] = row_distance<P>(vectors + static_cast<int64_t>(sid[j]) * (2 * P), sq);
-}
-
-/**
- * Squared distances of the fp16 rows sid[0, ns) to the fp32 query sq (search_kernels.cuh:325-342):
- * the value of a 64-lane reduction in which lane l takes the half2 pairs l, l + 64, ... (fma(a, a, acc),
- * fma(b, b, acc)) and an xor butterfly adds the lanes.  kLanePerRow (D <= 128, a multiple of 8; chosen
- * for deep reranks) scores a row per lane (row_distance, 64 rows in flight per wavefront), otherwise a
- * wavefront scores a row (fewer registers, better for a few rows or wide ones).
- */
-template <bool kLanePerRow>
 __device__ void exact_distances(const int* sid, int ns, const __half* __restrict__ vectors, int D,
                                 const float* sq, float* sd)
 {
+  constexpr int kRows = 8;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  if constexpr (kLanePerRow) {
-    switch (D / 8) {
-#define OCTEX_ROWS(r) \
-  case r: exact_rows<4 * r>(sid, ns, vectors, sq, sd); break;
-      OCTEX_ROWS(1) OCTEX_ROWS(2) OCTEX_ROWS(3) OCTEX_ROWS(4) OCTEX_ROWS(5) OCTEX_ROWS(6) OCTEX_ROWS(7)
-      OCTEX_ROWS(8) OCTEX_ROWS(9) OCTEX_ROWS(10) OCTEX_ROWS(11) OCTEX_ROWS(12) OCTEX_ROWS(13) OCTEX_ROWS(14)
-      OCTEX_ROWS(15) OCTEX_ROWS(16)
-#undef OCTEX_ROWS
-      default: break;
-    }
-    __syncthreads();
-    return;
-  }
   const int P = D / 2;
-  for (int j = wid; j < ns; j += nw) {
-    const __half2* x = reinterpret_cast<const __half2*>(vectors + static_cast<int64_t>(sid[j]) * D);
-    float acc        = 0.f;
+  for (int j0 = wid * kRows; j0 < ns; j0 += nw * kRows) {
+    const __half2* x[kRows];
+    float acc[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; r++) {  // past-the-end rows read the last row (results dropped)
+      acc[r] = 0.f;
+      x[r]   = reinterpret_cast<const __half2*>(vectors + static_cast<int64_t>(sid[min(j0 + r, ns - 1)]) * D);
+    }
     for (int k = lane; k < P; k += 64) {
-      float2 v = __half22float2(x[k]);
-      float a  = v.x - sq[2 * k];
-      float b  = v.y - sq[2 * k + 1];
-      acc      = fmaf(a, a, acc);
-      acc      = fmaf(b, b, acc);
+      __half2 h[kRows];
+#pragma unroll
+      for (int r = 0; r < kRows; r++)  // every row's pair first
+        h[r] = x[r][k];
+      const float q0 = sq[2 * k], q1 = sq[2 * k + 1];
+#pragma unroll
+      for (int r = 0; r < kRows; r++) {
+        float2 v = __half22float2(h[r]);
+        float a  = v.x - q0;
+        float b  = v.y - q1;
+        acc[r]   = fmaf(a, a, acc[r]);
+        acc[r]   = fmaf(b, b, acc[r]);
+      }
     }
 #pragma unroll
-    for (int o = 32; o; o >>= 1)
-      acc += __shfl_xor(acc, o);
-    if (lane == 0) sd[j] = acc;
+    for (int r = 0; r < kRows; r++) {
+#pragma unroll
+      for (int o = 32; o; o >>= 1)
+        acc[r] += __shfl_xor(acc[r], o);
+      if (lane == 0 && j0 + r < ns) sd[j0 + r] = acc[r];
+    }
   }
   __syncthreads();
 }
@@ -699,7 +650,6 @@ __device__ void store_keys(const uint64_t* key, int P, int KO, long long* pb, fl
  * Exact rerank of the R sketch-nearest candidates of a query, merged into its kept list of the best
  * KO (search_kernels.cuh:421-467).  fresh: the kept list starts empty.
  */
-template <bool kLanePerRow>
 __global__ __launch_bounds__(kKeepThreads) void rerank_keep_kernel(
   const int* __restrict__ cand, const float* __restrict__ dist, const int* __restrict__ nin, int W,
   const __half* __restrict__ vectors, int D, const float* __restrict__ Q, int R, int KO,
@@ -718,7 +668,7 @@ __global__ __launch_bounds__(kKeepThreads) void rerank_keep_kernel(
   select_smallest(reinterpret_cast<const unsigned*>(dist + static_cast<int64_t>(q) * W),
                   cand + static_cast<int64_t>(q) * W, n, R, sid, nullptr, hist, st);
   const int ns = st.nsel;
-  exact_distances<kLanePerRow>(sid, ns, vectors, D, sq, sd);
+  exact_distances(sid, ns, vectors, D, sq, sd);
   long long* pb = bi + static_cast<int64_t>(q) * KO;
   float* pd     = bd + static_cast<int64_t>(q) * KO;
   int P         = 2;
@@ -825,7 +775,6 @@ __global__ __launch_bounds__(256) void pick_starts_kernel(const long long* __res
 }
 
 /** Exact rerank of the first R kept entries (sketch-rank mode) into the best k (:634-669). */
-template <bool kLanePerRow>
 __global__ __launch_bounds__(kKeepThreads) void final_rerank_kernel(
   const long long* __restrict__ si, int KO, int R, const __half* __restrict__ vectors, int D,
   const float* __restrict__ Q, int k, long long* __restrict__ bi, float* __restrict__ bd)
@@ -853,7 +802,7 @@ __global__ __launch_bounds__(kKeepThreads) void final_rerank_kernel(
   }
   __syncthreads();
   const int ns = nsel;
-  exact_distances<kLanePerRow>(sid, ns, vectors, D, sq, sd);
+  exact_distances(sid, ns, vectors, D, sq, sd);
   int P = 2;
   while (P < R)
     P <<= 1;
@@ -998,12 +947,6 @@ void launch_gather(bool rows, const int2* seg, int nseg, int m, const long long*
   OCTEX_HIP(hipGetLastError());
 }
 
-/** Exact distances a row per lane for reranks of at least 32 rows of D <= 128 (a multiple of 8). */
-static auto lane_per_row(int R, int D) -> bool
-{
-  return R >= 32 && D % 8 == 0 && D <= 128;
-}
-
 void launch_rerank_keep(const int* cand, const float* dist, const int* nin, int m, int W,
                         const __half* vectors, int D, const float* Q, int R, int KO, long long* si,
                         float* sd, bool fresh, hipStream_t s)
@@ -1012,12 +955,8 @@ void launch_rerank_keep(const int* cand, const float* dist, const int* nin, int 
   OCTEX_EXPECTS(R >= 1 && R <= kMaxRerank && KO + R <= kMaxKeepSort && KO >= 1,
                 "octex: rerank in [1, 512] and max(starts, k) + rerank <= 1024");
   OCTEX_EXPECTS(D % 2 == 0, "octex: the dimension must be even");
-  if (lane_per_row(R, D))
-    rerank_keep_kernel<true><<<m, kKeepThreads, D * sizeof(float), s>>>(cand, dist, nin, W, vectors, D, Q, R, KO,
-                                                                      si, sd, fresh);
-  else
-    rerank_keep_kernel<false><<<m, kKeepThreads, D * sizeof(float), s>>>(cand, dist, nin, W, vectors, D, Q, R, KO,
-                                                                       si, sd, fresh);
+  rerank_keep_kernel<<<m, kKeepThreads, D * sizeof(float), s>>>(cand, dist, nin, W, vectors, D, Q, R, KO, si, sd,
+                                                                fresh);
   OCTEX_HIP(hipGetLastError());
 }
 
@@ -1046,10 +985,7 @@ void launch_final_rerank(const long long* si, int m, int KO, int R, const __half
   if (m == 0) return;
   OCTEX_EXPECTS(R >= k && R <= kMaxRerank && R <= KO,
                 "octex: final_rerank 0 (sketch order) or k <= final_rerank <= 512");
-  if (lane_per_row(R, D))
-    final_rerank_kernel<true><<<m, kKeepThreads, D * sizeof(float), s>>>(si, KO, R, vectors, D, Q, k, bi, bd);
-  else
-    final_rerank_kernel<false><<<m, kKeepThreads, D * sizeof(float), s>>>(si, KO, R, vectors, D, Q, k, bi, bd);
+  final_rerank_kernel<<<m, kKeepThreads, D * sizeof(float), s>>>(si, KO, R, vectors, D, Q, k, bi, bd);
   OCTEX_HIP(hipGetLastError());
 }
 

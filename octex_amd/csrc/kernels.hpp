@@ -18,7 +18,7 @@ constexpr int kMaxKeepSort    = 1024;   // kept + reranked keys sorted together
 constexpr int kMaxSketchKO    = 1024;   // kept entries of the sketch merge
 constexpr int kPickHash       = 8192;   // hash set of the expanded start points
 constexpr int kMaxExpanded    = 6144;   // start points expanded by earlier waves
-constexpr int kGatherThreads  = 512;
+constexpr int kGatherThreads  = 256;
 constexpr int kKeepThreads    = 256;
 
 /** log2 of the hash set of a query reading `total` entries: ceil(log2(1.5 total)) in [11, log_cap]. */
