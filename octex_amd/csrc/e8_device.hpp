@@ -91,9 +91,9 @@ __device__ __forceinline__ long long finish_hash(unsigned long long h)
   return hs ^ (hs >> 29);
 }
 
-/** 64-bit cell id of the E8^B point nearest to y * inv_f. */
-template <int B>
-__device__ __forceinline__ long long e8b_hash64(const float (&y)[8 * B], float inv_f)
+/** 64-bit cell id of the E8^B point nearest to y * inv_f; coord(i) gives y[i] as a float. */
+template <int B, typename Coord>
+__device__ __forceinline__ long long e8b_hash64_of(Coord const& coord, float inv_f)
 {
   unsigned long long h = 0;
 #pragma unroll
@@ -101,12 +101,19 @@ __device__ __forceinline__ long long e8b_hash64(const float (&y)[8 * B], float i
     float x[8], p[8];
 #pragma unroll
     for (int i = 0; i < 8; i++)
-      x[i] = y[8 * j + i] * inv_f;
+      x[i] = coord(8 * j + i) * inv_f;
     e8_point(x, p);
     unsigned long long hb = block_hash(p);
     h                     = (j == 0) ? hb : h * kMix + hb;
   }
   return finish_hash(h);
+}
+
+/** 64-bit cell id of the E8^B point nearest to y * inv_f. */
+template <int B>
+__device__ __forceinline__ long long e8b_hash64(const float (&y)[8 * B], float inv_f)
+{
+  return e8b_hash64_of<B>([&](int i) { return y[i]; }, inv_f);
 }
 
 }  // namespace

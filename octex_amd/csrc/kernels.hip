@@ -68,10 +68,11 @@ __device__ __forceinline__ half4_t load_h4(const __half* __restrict__ a, int r, 
 
 /**
  * Y [m, N] = qh [m, K] @ ucatT [N, K]^T + shift (search.cu:305-320 as one MFMA kernel): every wave
- * computes a 16-query x 64-output tile with v_mfma_f32_16x16x16_f16 (A = 16 outputs x 16 k of
- * ucatT, B = 16 k x 16 queries of qh), fp32 accumulation, the fp16 shift added in fp32 and one
- * rounding to fp16.  Lane l holds D[4 (l / 16) + r][l % 16]: 4 consecutive outputs of one query,
- * stored as one 8-byte write.
+ * computes a 64-query x 64-output tile as 4 x 4 v_mfma_f32_16x16x16_f16 tiles (A = 16 outputs x 16 k
+ * of ucatT, B = 16 k x 16 queries of qh), so each fragment it loads feeds four MFMAs; fp32
+ * accumulation over k in steps of 16, the fp16 shift added in fp32 and one rounding to fp16.  Lane l
+ * holds D[4 (l / 16) + r][l % 16]: 4 consecutive outputs of one query, stored as one 8-byte write.
+ * A workgroup is 4 waves along the outputs (64 queries x 256 outputs).
  */
 __global__ __launch_bounds__(256) void project_kernel(const __half* __restrict__ qh,
                                                       const __half* __restrict__ ucatT,
@@ -79,38 +80,50 @@ __global__ __launch_bounds__(256) void project_kernel(const __half* __restrict__
                                                       int N, __half* __restrict__ Y)
 {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int q0   = (blockIdx.x * 4 + wid) * 16;
-  const int n0   = blockIdx.y * 64;
+  const int q0   = blockIdx.x * 64;
+  const int n0   = (blockIdx.y * 4 + wid) * 64;
+  if (n0 >= N) return;  // no barriers below: a wave past the outputs just ends
   const bool vec = (K & 3) == 0;
   const int kq   = (lane >> 4) * 4;
-  const int ql   = q0 + (lane & 15);
-  float4_t acc[4];
+  float4_t acc[4][4];
 #pragma unroll
-  for (int t = 0; t < 4; t++)
-    acc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+      acc[i][t] = float4_t{0.f, 0.f, 0.f, 0.f};
   for (int k0 = 0; k0 < K; k0 += 16) {
-    half4_t b = load_h4(qh, ql, m, K, k0 + kq, vec);
+    half4_t a[4], b[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      b[i] = load_h4(qh, q0 + i * 16 + (lane & 15), m, K, k0 + kq, vec);
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+      a[t] = load_h4(ucatT, n0 + t * 16 + (lane & 15), N, K, k0 + kq, vec);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int t = 0; t < 4; t++)
+        acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x16f16(a[t], b[i], acc[i][t], 0, 0, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int ql = q0 + i * 16 + (lane & 15);
+    if (ql >= m) continue;
+    __half* yrow = Y + static_cast<int64_t>(ql) * N;
 #pragma unroll
     for (int t = 0; t < 4; t++) {
-      half4_t a = load_h4(ucatT, n0 + t * 16 + (lane & 15), N, K, k0 + kq, vec);
-      acc[t]    = __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, acc[t], 0, 0, 0);
-    }
-  }
-  if (ql >= m) return;
-  __half* yrow = Y + static_cast<int64_t>(ql) * N;
-#pragma unroll
-  for (int t = 0; t < 4; t++) {
-    const int nb = n0 + t * 16 + kq;
-    __half o[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++)
-      o[r] = __float2half(acc[t][r] + (nb + r < N ? __half2float(shift[nb + r]) : 0.f));
-    if (nb + 3 < N && (N & 3) == 0) {
-      *reinterpret_cast<uint2*>(yrow + nb) = *reinterpret_cast<uint2*>(o);
-    } else {
+      const int nb = n0 + t * 16 + kq;
+      __half o[4];
 #pragma unroll
       for (int r = 0; r < 4; r++)
-        if (nb + r < N) yrow[nb + r] = o[r];
+        o[r] = __float2half(acc[i][t][r] + (nb + r < N ? __half2float(shift[nb + r]) : 0.f));
+      if (nb + 3 < N && (N & 3) == 0) {
+        *reinterpret_cast<uint2*>(yrow + nb) = *reinterpret_cast<uint2*>(o);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          if (nb + r < N) yrow[nb + r] = o[r];
+      }
     }
   }
 }
@@ -131,7 +144,7 @@ __global__ void sketch_query_kernel(const float* __restrict__ qc, const float* _
 }
 
 template <int B>
-__global__ void e8_kernel(const float* __restrict__ y, int64_t n, float inv_f, float* __restrict__ p,
+__global__ __launch_bounds__(256) void e8_kernel(const float* __restrict__ y, int64_t n, float inv_f, float* __restrict__ p,
                           long long* __restrict__ h)
 {
   int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -172,23 +185,17 @@ __global__ __launch_bounds__(256) void probe_kernel(const __half* __restrict__ Y
   if (t >= static_cast<int64_t>(m) * C) return;
   const int c     = static_cast<int>(t / m);  // a wavefront: 64 queries of one copy, so its offsets and
   const int64_t u = (t % m) * C + c;          // keys lookups stay inside that copy's tables (few pages)
-  float y[8 * B];
+  uint4 yv[B];  // the fp16 row, widened per use (fewer registers than 8B floats)
   const uint4* yp = reinterpret_cast<const uint4*>(Y + u * 8 * B);
 #pragma unroll
-  for (int i = 0; i < B; i++) {
-    uint4 u        = yp[i];
-    const __half2* h = reinterpret_cast<const __half2*>(&u);
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      float2 v            = __half22float2(h[j]);
-      y[8 * i + 2 * j]     = v.x;
-      y[8 * i + 2 * j + 1] = v.y;
-    }
-  }
+  for (int i = 0; i < B; i++)
+    yv[i] = yp[i];
+  const __half* yh = reinterpret_cast<const __half*>(yv);
+  auto coord       = [&](int i) { return __half2float(yh[i]); };
   int2 sg              = make_int2(0, 0);
   const long long mask = (1LL << logT) - 1;
   for (int j = 0; j < L; j++) {
-    long long h          = e8b_hash64<B>(y, inv_f[j]);
+    long long h          = e8b_hash64_of<B>(coord, inv_f[j]);
     int bk               = static_cast<int>(h & mask);
     const int* o         = off + (static_cast<int64_t>(c) * L + j) * T1 + bk;
     const long long* kk  = keys + (static_cast<int64_t>(c) * L + j) * Mmax;
@@ -847,7 +854,7 @@ void launch_project(const __half* qh, const __half* ucatT, const __half* shift, 
 {
   if (m == 0 || N == 0) return;
   OCTEX_EXPECTS(K >= 1, "octex: projection needs a positive dimension");
-  dim3 grid(static_cast<unsigned>((m + 63) / 64), static_cast<unsigned>((N + 63) / 64));
+  dim3 grid(static_cast<unsigned>((m + 63) / 64), static_cast<unsigned>((N + 255) / 256));
   project_kernel<<<grid, 256, 0, s>>>(qh, ucatT, shift, m, K, N, Y);
   OCTEX_HIP(hipGetLastError());
 }
