@@ -55,6 +55,22 @@ cuvsError_t octexIndexProfileBatch(cuvsOctexIndex_t index, cuvsOctexSearchParams
 cuvsError_t octexIndexCopyArray(cuvsOctexIndex_t index, const char* name, int32_t copy, void* dst, int64_t bytes,
                                 int64_t* size);
 
+/**
+ * Copy bytes [offset, offset + bytes) of an array named as in octexIndexCopyArray (not "meta" or
+ * "spacings") to dst; a range outside the array is an error.  Used to read a few list rows of a
+ * large index without copying whole arrays.
+ */
+cuvsError_t octexIndexCopyArrayRange(cuvsOctexIndex_t index, const char* name, int32_t copy, int64_t offset,
+                                     void* dst, int64_t bytes);
+
+/**
+ * Copy `count` ranges of `bytes` bytes (a multiple of 4) at byte offsets[r] (host, multiples of 4) of an
+ * array named as in octexIndexCopyArray to dst [count, bytes] (host or device), gathered on the GPU in
+ * one launch; a range outside the array is an error.
+ */
+cuvsError_t octexIndexCopyArrayRanges(cuvsOctexIndex_t index, const char* name, int32_t copy,
+                                      const int64_t* offsets, int64_t count, int64_t bytes, void* dst);
+
 /** The cached plan's shape: {m, k, KO, lr, W, W2, rerank, wave_rerank, final_rerank, graph?}. */
 cuvsError_t octexIndexPlanInfo(cuvsOctexIndex_t index, int32_t* info);
 

@@ -117,6 +117,7 @@ EXPORTS = (
     "cuvsOctexIndexGetCopies", "cuvsOctexIndexGetNumDevices", "cuvsOctexIndexGetDevices",
     "cuvsOctexIndexGetDeviceBytes", "cuvsOctexBuild", "cuvsOctexLoad", "cuvsOctexSearch",
     "octexIndexCopyPlanBuffer", "octexIndexPlanInfo", "octexBuildInMemory", "octexIndexProfileBatch", "octexIndexCopyArray",
+    "octexIndexCopyArrayRange", "octexIndexCopyArrayRanges",
     "octexStageCenter", "octexStageProject", "octexStageSketchQuery", "octexStageE8", "octexStageProbe",
     "octexStageGather", "octexStageRerankKeep", "octexStageSketchKeep", "octexStagePickStarts",
     "octexStageFinalRerank", "octexStageTakeK",

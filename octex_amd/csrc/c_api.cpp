@@ -4,6 +4,7 @@
 
 #include "build.hpp"
 #include "common.hpp"
+#include "kernels.hpp"
 #include "index_impl.hpp"
 #include "search.hpp"
 
@@ -500,66 +501,103 @@ extern "C" cuvsError_t octexIndexProfileBatch(cuvsOctexIndex_t index, cuvsOctexS
   });
 }
 
+namespace {
+
+/** The device (or pinned host) bytes of an index array by name: lists of one copy, or a whole array. */
+auto index_array(octex::detail::index_impl& ix, std::string const& n, int32_t copy) -> std::pair<const void*, size_t>
+{
+  auto of = [](octex::detail::dbuf const& b) { return std::pair<const void*, size_t>(b.ptr, b.size); };
+  if (n == "lists") {
+    OCTEX_EXPECTS(copy >= 0 && copy < ix.copies, "octex: no copy %d", copy);
+    if (!ix.copy_lists.empty())
+      return {ix.copy_lists[copy].ptr, static_cast<size_t>(ix.list_rows[copy]) * ix.list_len * sizeof(int32_t)};
+    return {ix.lists.as<int32_t>() + copy * ix.stride, static_cast<size_t>(ix.stride) * sizeof(int32_t)};
+  }
+  if (n == "keys") return of(ix.keys);
+  if (n == "offsets") return of(ix.offsets);
+  if (n == "base") return of(ix.base);
+  if (n == "ucatT") return of(ix.ucatT);
+  if (n == "shift") return of(ix.shift);
+  if (n == "inv_f") return of(ix.inv_f);
+  if (n == "mean") return of(ix.mean);
+  if (n == "basis") return of(ix.basis);
+  if (n == "scale") return of(ix.scale);
+  if (n == "sketch") return {ix.code(), static_cast<size_t>(ix.n) * ix.sketch_width};
+  if (n == "vectors") return {ix.vecs(), static_cast<size_t>(ix.n) * ix.dim * sizeof(__half)};
+  if (n == "table") return {ix.rows(), static_cast<size_t>(ix.n) * ix.table_len * sizeof(int32_t)};
+  octex::detail::fail("octex: unknown index array %s", n.c_str());
+}
+
+}  // namespace
+
 extern "C" cuvsError_t octexIndexCopyArray(cuvsOctexIndex_t index, const char* name, int32_t copy, void* dst,
                                            int64_t bytes, int64_t* size)
 {
   return translate_exceptions([=] {
     auto& ix = as_index(*index)->impl();
     std::string n(name != nullptr ? name : "");
-    const void* src = nullptr;
-    size_t sz       = 0;
-    std::vector<int64_t> rows;
-    auto pick = [&](octex::detail::dbuf const& b) {
-      src = b.ptr;
-      sz  = b.size;
-    };
-    if (n == "lists") {
-      OCTEX_EXPECTS(copy >= 0 && copy < ix.copies, "octex: no copy %d", copy);
-      if (!ix.copy_lists.empty()) {
-        src = ix.copy_lists[copy].ptr;
-        sz  = static_cast<size_t>(ix.list_rows[copy]) * ix.list_len * sizeof(int32_t);
-      } else {
-        src = ix.lists.as<int32_t>() + copy * ix.stride;
-        sz  = static_cast<size_t>(ix.stride) * sizeof(int32_t);
-      }
-    } else if (n == "keys") pick(ix.keys);
-    else if (n == "offsets") pick(ix.offsets);
-    else if (n == "base") pick(ix.base);
-    else if (n == "ucatT") pick(ix.ucatT);
-    else if (n == "shift") pick(ix.shift);
-    else if (n == "inv_f") pick(ix.inv_f);
-    else if (n == "mean") pick(ix.mean);
-    else if (n == "basis") pick(ix.basis);
-    else if (n == "scale") pick(ix.scale);
-    else if (n == "sketch") {
-      src = ix.code();
-      sz  = static_cast<size_t>(ix.n) * ix.sketch_width;
-    } else if (n == "vectors") {
-      src = ix.vecs();
-      sz  = static_cast<size_t>(ix.n) * ix.dim * sizeof(__half);
-    } else if (n == "table") {
-      src = ix.rows();
-      sz  = static_cast<size_t>(ix.n) * ix.table_len * sizeof(int32_t);
-    } else if (n == "meta") {  // n, dim, copies, blocks, levels, list_len, log_buckets, sketch_width, table_len, mmax, T1
-      static thread_local int64_t v[11];
+    if (n == "meta") {  // n, dim, copies, blocks, levels, list_len, log_buckets, sketch_width, table_len, mmax, T1
       int64_t m[11] = {ix.n, ix.dim, ix.copies, ix.blocks, ix.levels(), ix.list_len, ix.log_buckets, ix.sketch_width,
                        ix.table_len, ix.mmax, ix.T1};
-      std::memcpy(v, m, sizeof(m));
       if (size != nullptr) *size = sizeof(m);
       if (dst != nullptr) std::memcpy(dst, m, std::min<size_t>(sizeof(m), static_cast<size_t>(bytes)));
       return;
-    } else if (n == "spacings") {
+    }
+    if (n == "spacings") {
       if (size != nullptr) *size = static_cast<int64_t>(ix.spacings.size() * sizeof(float));
       if (dst != nullptr)
         std::memcpy(dst, ix.spacings.data(), std::min<size_t>(ix.spacings.size() * sizeof(float), bytes));
       return;
-    } else {
-      octex::detail::fail("octex: unknown index array %s", n.c_str());
     }
+    auto [src, sz] = index_array(ix, n, copy);
     if (size != nullptr) *size = static_cast<int64_t>(sz);
     if (dst != nullptr && bytes > 0 && src != nullptr) {
       OCTEX_HIP(hipSetDevice(ix.device));
       OCTEX_HIP(hipMemcpy(dst, src, std::min<size_t>(sz, static_cast<size_t>(bytes)), hipMemcpyDefault));
     }
+  });
+}
+
+extern "C" cuvsError_t octexIndexCopyArrayRanges(cuvsOctexIndex_t index, const char* name, int32_t copy,
+                                                 const int64_t* offsets, int64_t count, int64_t bytes, void* dst)
+{
+  return translate_exceptions([=] {
+    OCTEX_EXPECTS(count >= 0 && bytes >= 0 && (count == 0 || (offsets != nullptr && dst != nullptr)),
+                  "octex: NULL offsets or destination");
+    if (count == 0 || bytes == 0) return;
+    auto& ix       = as_index(*index)->impl();
+    auto [src, sz] = index_array(ix, std::string(name != nullptr ? name : ""), copy);
+    OCTEX_EXPECTS(bytes % 4 == 0, "octex: ranges are whole 32-bit words");
+    std::vector<int64_t> words(static_cast<size_t>(count));
+    for (int64_t r = 0; r < count; r++) {
+      OCTEX_EXPECTS(offsets[r] >= 0 && offsets[r] % 4 == 0 && static_cast<size_t>(offsets[r] + bytes) <= sz,
+                    "octex: range %lld (bytes [%lld, %lld)) is outside the array (%zu bytes) or unaligned",
+                    static_cast<long long>(r), static_cast<long long>(offsets[r]),
+                    static_cast<long long>(offsets[r] + bytes), sz);
+      words[r] = offsets[r] / 4;
+    }
+    OCTEX_HIP(hipSetDevice(ix.device));
+    octex::detail::dbuf doff(words.size() * sizeof(int64_t)), dout(static_cast<size_t>(count * bytes));
+    OCTEX_HIP(hipMemcpy(doff.ptr, words.data(), doff.size, hipMemcpyHostToDevice));
+    octex::detail::launch_copy_ranges(static_cast<const uint32_t*>(src), doff.as<int64_t>(), count,
+                                      static_cast<int>(bytes / 4), dout.as<uint32_t>(), ix.stream);
+    OCTEX_HIP(hipStreamSynchronize(ix.stream));
+    OCTEX_HIP(hipMemcpy(dst, dout.ptr, dout.size, hipMemcpyDefault));
+  });
+}
+
+extern "C" cuvsError_t octexIndexCopyArrayRange(cuvsOctexIndex_t index, const char* name, int32_t copy,
+                                                int64_t offset, void* dst, int64_t bytes)
+{
+  return translate_exceptions([=] {
+    OCTEX_EXPECTS(dst != nullptr || bytes == 0, "octex: NULL destination");
+    auto& ix       = as_index(*index)->impl();
+    auto [src, sz] = index_array(ix, std::string(name != nullptr ? name : ""), copy);
+    OCTEX_EXPECTS(offset >= 0 && bytes >= 0 && static_cast<size_t>(offset + bytes) <= sz,
+                  "octex: bytes [%lld, %lld) are outside the array (%zu bytes)", static_cast<long long>(offset),
+                  static_cast<long long>(offset + bytes), sz);
+    if (bytes == 0) return;
+    OCTEX_HIP(hipSetDevice(ix.device));
+    OCTEX_HIP(hipMemcpy(dst, static_cast<const char*>(src) + offset, static_cast<size_t>(bytes), hipMemcpyDefault));
   });
 }

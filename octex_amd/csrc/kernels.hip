@@ -128,19 +128,36 @@ __global__ __launch_bounds__(256) void project_kernel(const __half* __restrict__
   }
 }
 
-/** qs [m, S] = qc [m, D] @ basis [D, S]: one thread per output, sequential fma over d. */
-__global__ void sketch_query_kernel(const float* __restrict__ qc, const float* __restrict__ basis,
-                                    int m, int D, int S, float* __restrict__ qs)
+/**
+ * qs [m, S] = qc [m, D] @ basis [D, S] with one sequential fma chain over d per output (fp32; the
+ * reference uses a TF32 GEMM here).  A workgroup takes 16 queries (their rows staged in LDS) by 64
+ * sketch coordinates; a thread keeps 4 queries' chains for one coordinate, so every basis load feeds
+ * four fmas.
+ */
+__global__ __launch_bounds__(256) void sketch_query_kernel(const float* __restrict__ qc,
+                                                           const float* __restrict__ basis, int m, int D,
+                                                           int S, float* __restrict__ qs)
 {
-  int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (t >= static_cast<int64_t>(m) * S) return;
-  int64_t q = t / S;
-  int s     = static_cast<int>(t % S);
-  const float* r = qc + q * D;
-  float acc      = 0.f;
-  for (int d = 0; d < D; d++)
-    acc = fmaf(r[d], basis[static_cast<int64_t>(d) * S + s], acc);
-  qs[t] = acc;
+  extern __shared__ float rows[];  // [16, D]
+  const int q0 = blockIdx.y * 16, s = blockIdx.x * 64 + (threadIdx.x & 63), ty = threadIdx.x >> 6;
+  for (int i = threadIdx.x; i < 16 * D; i += blockDim.x) {
+    const int q = q0 + i / D;
+    rows[i]     = q < m ? qc[static_cast<int64_t>(q) * D + i % D] : 0.f;
+  }
+  __syncthreads();
+  if (s >= S) return;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int d = 0; d < D; d++) {
+    const float b = basis[static_cast<int64_t>(d) * S + s];
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+      acc[r] = fmaf(rows[(4 * ty + r) * D + d], b, acc[r]);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int q = q0 + 4 * ty + r;
+    if (q < m) qs[static_cast<int64_t>(q) * S + s] = acc[r];
+  }
 }
 
 template <int B>
@@ -172,6 +189,8 @@ __global__ __launch_bounds__(256) void e8_kernel(const float* __restrict__ y, in
 /**
  * One lane per (query, copy): for levels fine to coarse, the cell id of y * inv_f[j], its bucket,
  * and a scan of the bucket's keys; the first hit gives seg = ((base + p) * l, lr), none (0, 0).
+ * The id of level j + 1 is computed while level j's bucket is being read (the hit level is often
+ * not the finest, and the loads are dependent HBM round trips).
  */
 template <int B>
 __global__ __launch_bounds__(256) void probe_kernel(const __half* __restrict__ Y, int m, int C,
@@ -194,12 +213,14 @@ __global__ __launch_bounds__(256) void probe_kernel(const __half* __restrict__ Y
   auto coord       = [&](int i) { return __half2float(yh[i]); };
   int2 sg              = make_int2(0, 0);
   const long long mask = (1LL << logT) - 1;
+  long long h          = e8b_hash64_of<B>(coord, inv_f[0]);
   for (int j = 0; j < L; j++) {
-    long long h          = e8b_hash64_of<B>(coord, inv_f[j]);
-    int bk               = static_cast<int>(h & mask);
-    const int* o         = off + (static_cast<int64_t>(c) * L + j) * T1 + bk;
-    const long long* kk  = keys + (static_cast<int64_t>(c) * L + j) * Mmax;
+    const int bk        = static_cast<int>(h & mask);
+    const int* o        = off + (static_cast<int64_t>(c) * L + j) * T1 + bk;
+    const long long* kk = keys + (static_cast<int64_t>(c) * L + j) * Mmax;
     const int p0 = o[0], p1 = o[1];
+    // the next level's cell id is computed while this level's bucket loads are in flight
+    const long long hn = j + 1 < L ? e8b_hash64_of<B>(coord, inv_f[j + 1]) : 0;
     int hit = -1;
     for (int p = p0; p < p1; p++)
       if (kk[p] == h) {
@@ -210,6 +231,7 @@ __global__ __launch_bounds__(256) void probe_kernel(const __half* __restrict__ Y
       sg = make_int2((base[c * L + j] + hit) * l, lr);
       break;
     }
+    h = hn;
   }
   seg[u] = sg;
 }
@@ -828,6 +850,15 @@ __global__ void take_k_kernel(const long long* __restrict__ si, const float* __r
   bd[t]     = sd[q * KO + j];
 }
 
+/** out[r] = the `words` 32-bit words of src at word offset off[r] (one workgroup per range). */
+__global__ void copy_ranges_kernel(const uint32_t* __restrict__ src, const int64_t* __restrict__ off, int64_t n,
+                                   int words, uint32_t* __restrict__ out)
+{
+  for (int64_t r = blockIdx.x; r < n; r += gridDim.x)
+    for (int i = threadIdx.x; i < words; i += blockDim.x)
+      out[r * words + i] = src[off[r] + i];
+}
+
 }  // namespace
 
 // ================================================================== launchers
@@ -862,9 +893,11 @@ void launch_project(const __half* qh, const __half* ucatT, const __half* shift, 
 void launch_sketch_query(const float* qc, const float* basis, int m, int D, int S, float* qs,
                          hipStream_t s)
 {
-  const int64_t total = static_cast<int64_t>(m) * S;
-  if (total == 0) return;
-  sketch_query_kernel<<<grid_for(total, 256), 256, 0, s>>>(qc, basis, m, D, S, qs);
+  if (static_cast<int64_t>(m) * S == 0) return;
+  OCTEX_EXPECTS(D >= 1 && 16 * static_cast<int64_t>(D) * sizeof(float) <= 64 * 1024,
+                "octex: the sketch query stages 16 query rows of at most 4096 values in LDS");
+  dim3 grid(static_cast<unsigned>((S + 63) / 64), static_cast<unsigned>((m + 15) / 16));
+  sketch_query_kernel<<<grid, 256, 16 * D * sizeof(float), s>>>(qc, basis, m, D, S, qs);
   OCTEX_HIP(hipGetLastError());
 }
 
@@ -1002,6 +1035,14 @@ void launch_take_k(const long long* si, const float* sd, int m, int KO, int k, l
   const int64_t total = static_cast<int64_t>(m) * k;
   if (total == 0) return;
   take_k_kernel<<<grid_for(total, 256), 256, 0, s>>>(si, sd, KO, k, m, bi, bd);
+  OCTEX_HIP(hipGetLastError());
+}
+
+void launch_copy_ranges(const uint32_t* src, const int64_t* off, int64_t n, int words, uint32_t* out,
+                        hipStream_t s)
+{
+  if (n == 0 || words == 0) return;
+  copy_ranges_kernel<<<static_cast<unsigned>(std::min<int64_t>(n, 65536)), 64, 0, s>>>(src, off, n, words, out);
   OCTEX_HIP(hipGetLastError());
 }
 

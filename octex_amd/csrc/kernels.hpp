@@ -63,6 +63,9 @@ void launch_pick_starts(const long long* si, int m, int KO, long long* done, int
                         int rowlen, int2* seg2, hipStream_t s);
 void launch_final_rerank(const long long* si, int m, int KO, int R, const __half* vectors, int D,
                          const float* Q, int k, long long* bi, float* bd, hipStream_t s);
+/** out [n, words] = the 32-bit words src[off[r], off[r] + words) of every range r (offsets on the device). */
+void launch_copy_ranges(const uint32_t* src, const int64_t* off, int64_t n, int words, uint32_t* out,
+                        hipStream_t s);
 void launch_take_k(const long long* si, const float* sd, int m, int KO, int k, long long* bi,
                    float* bd, hipStream_t s);
 

@@ -253,6 +253,31 @@ class Index:
                   ct.c_int64(out.nbytes), None)
         return out
 
+    def array_size(self, name, copy=0):
+        """Bytes of an index array (see octexIndexCopyArray)."""
+        size = ct.c_int64(0)
+        _lib.call("octexIndexCopyArray", self._handle, name.encode(), ct.c_int32(copy), None, ct.c_int64(0),
+                  ct.byref(size))
+        return size.value
+
+    def array_range(self, name, dtype, start, count, copy=0):
+        """Elements [start, start + count) of an index array (see octexIndexCopyArrayRange)."""
+        out = np.empty(count, dtype)
+        isz = np.dtype(dtype).itemsize
+        _lib.call("octexIndexCopyArrayRange", self._handle, name.encode(), ct.c_int32(copy), ct.c_int64(start * isz),
+                  ct.c_void_p(out.ctypes.data), ct.c_int64(out.nbytes))
+        return out
+
+    def array_ranges(self, name, dtype, starts, count, copy=0):
+        """Rows [starts[r], starts[r] + count) of an index array, gathered on the GPU: [len(starts), count]."""
+        isz = np.dtype(dtype).itemsize
+        offs = np.ascontiguousarray(np.asarray(starts, np.int64) * isz)
+        out = np.empty((len(offs), count), dtype)
+        _lib.call("octexIndexCopyArrayRanges", self._handle, name.encode(), ct.c_int32(copy),
+                  ct.c_void_p(offs.ctypes.data), ct.c_int64(len(offs)), ct.c_int64(count * isz),
+                  ct.c_void_p(out.ctypes.data))
+        return out
+
     def profile_batch(self, queries, k=10, reps=3, **params):
         """Per-kernel milliseconds of one batch (HIP events around every launch) and its work counters."""
         p = search_params(**params)

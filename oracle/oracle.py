@@ -188,9 +188,12 @@ def exact_dist(x_h, q):
 class Index:
     """The arrays of an index directory as the loader places them (one device, replicate)."""
 
-    def __init__(self, path, list_limit=0, copies_limit=0):
+    def __init__(self, path, list_limit=0, copies_limit=0, queries=None, read=32):
+        """path: an index directory, or a live octex_amd.Index whose arrays are copied to the host.  For a
+        live index, `queries` (with the search's `read`) limits the lists copied to the rows these
+        queries' probes reach; the other rows read as zeros (an index too large for host memory)."""
         if not isinstance(path, (str, bytes, os.PathLike)):
-            self._from_live(path)
+            self._from_live(path, queries, read)
             return
         with open(os.path.join(path, "meta.json")) as f:
             meta = json.load(f)
@@ -240,7 +243,7 @@ class Index:
         assert self.keys.shape[1] == L and proj.shape[2] == w, "octex: bad shapes"
         self._struct(L)
 
-    def _from_live(self, live):
+    def _from_live(self, live, queries=None, read=32):
         """The arrays of a loaded or built octex_amd index, copied to the host (the same index the GPU searches)."""
         meta = live.array("meta", np.int64)
         n, dim, C, blocks, L, list_len, log_buckets, S, table_len, mmax, T1 = (int(v) for v in meta)
@@ -248,12 +251,16 @@ class Index:
         self.log_buckets, self.sketch_width, self.table_len = log_buckets, S, table_len
         self.spacings = [float(v) for v in live.array("spacings", np.float32)]
         w = 8 * blocks
-        per = [live.array("lists", np.int32, copy=c) for c in range(C)]
-        stride = max(len(p) for p in per)
-        self.lists = np.zeros((C, stride), np.int32)
-        for c, p in enumerate(per):
-            self.lists[c, : len(p)] = p
-        del per
+        if queries is None:
+            per = [live.array("lists", np.int32, copy=c) for c in range(C)]
+            stride = max(len(p) for p in per)
+            self.lists = np.zeros((C, stride), np.int32)
+            for c, p in enumerate(per):
+                self.lists[c, : len(p)] = p
+            del per
+        else:  # zero-filled and lazily committed: only the rows copied below take host memory
+            stride = max(live.array_size("lists", copy=c) for c in range(C)) // 4
+            self.lists = np.zeros((C, stride), np.int32)
         self.keys = live.array("keys", np.int64).reshape(C, L, mmax)
         self.offsets = live.array("offsets", np.int32).reshape(C, L, T1)
         self.base = live.array("base", np.int32).reshape(C, L)
@@ -269,6 +276,19 @@ class Index:
         self.table = live.array("table", np.int32).reshape(n, table_len) if table_len > 0 else None
         self.meta = {}
         self._struct(L)
+        if queries is not None:  # the list rows of these queries' probes (the segments the search reads)
+            _, qh = center(queries, self.mean)
+            Y, _ = project(qh, self.ucat, self.shift)
+            seg = probe(self, Y, read)
+            for c in range(C):
+                sc = seg[:, c, :]
+                sc = sc[sc[:, 1] > 0]
+                if len(sc) == 0:
+                    continue
+                ln = int(sc[:, 1].max())  # every segment reads min(read, list_len) entries
+                starts = np.unique(sc[:, 0]).astype(np.int64)
+                rows = live.array_ranges("lists", np.int32, starts, ln, copy=c)
+                self.lists[c, starts[:, None] + np.arange(ln)[None, :]] = rows
 
     def _struct(self, L):
         s = OrcIndex()

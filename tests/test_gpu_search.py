@@ -183,3 +183,29 @@ def test_errors(octex, small_index):
         octex.load(small_index["path"] + "_missing")
     assert index.size == 4000 and index.dim == 64 and index.copies == 16 and len(index.devices) == 1
     assert index.device_bytes[0] > 0
+
+
+def test_oracle_index_with_probed_rows_only(octex, small_index):
+    """The host copy that keeps only the list rows a sample's probes reach (the CPU baseline of an index
+    too large for host memory) searches that sample exactly like the full copy; array ranges read the
+    same bytes as whole arrays and reject ranges outside them."""
+    from octex_amd._lib import OctexError
+
+    index = octex.load(small_index["path"])
+    Q = small_index["Q"][:50]
+    full = O.Index(index)
+    part = O.Index(index, queries=Q, read=PARAMS["read"])
+    assert (part.lists != 0).sum() < (full.lists != 0).sum()
+    D1, I1 = O.search(full, Q, k=10, **PARAMS)
+    D2, I2 = O.search(part, Q, k=10, **PARAMS)
+    assert np.array_equal(I1, I2) and np.array_equal(D1, D2)
+    lists3 = index.array("lists", np.int32, copy=3)
+    assert np.array_equal(index.array_range("lists", np.int32, 100, 37, copy=3), lists3[100:137])
+    assert index.array_size("lists", copy=3) == lists3.nbytes
+    starts = np.array([0, 64, 7, len(lists3) - 16])
+    got = index.array_ranges("lists", np.int32, starts, 16, copy=3)
+    assert np.array_equal(got, np.stack([lists3[s : s + 16] for s in starts]))
+    with pytest.raises(OctexError, match="outside the array"):
+        index.array_ranges("lists", np.int32, [len(lists3) - 8], 16, copy=3)
+    with pytest.raises(OctexError, match="outside the array"):
+        index.array_range("lists", np.int32, len(lists3) - 2, 3, copy=3)
