@@ -47,55 +47,90 @@ auto alloc(int64_t count, int fill = -2) -> dbuf
   return b;
 }
 
-/** First round: m queries over all copies, the best KO kept in si / sd (search.cu:294-407). */
-void first_round(index_impl const& ix, plan const& pl, hipStream_t s)
-{
-  const int D = static_cast<int>(ix.dim), S = ix.sketch_width, C = ix.copies;
-  const int m = pl.m;
-  launch_center(pl.qbuf.as<float>(), ix.mean.as<float>(), m, D, pl.qc.as<float>(), pl.qh.as<__half>(), s);
-  launch_project(pl.qh.as<__half>(), ix.ucatT.as<__half>(), ix.shift.as<__half>(), m, D, C * 8 * ix.blocks,
-                 pl.Y.as<__half>(), s);
-  launch_sketch_query(pl.qc.as<float>(), ix.basis.as<float>(), m, D, S, pl.qs.as<float>(), s);
-  launch_probe(pl.Y.as<__half>(), m, C, ix.levels(), ix.blocks, ix.inv_f.as<float>(), ix.offsets.as<int>(),
-               ix.T1, ix.keys.as<long long>(), ix.mmax, ix.base.as<int>(), ix.list_len, pl.lr,
-               ix.log_buckets, pl.seg.as<int2>(), s);
-  launch_gather(false, pl.seg.as<int2>(), C, m, ix.list_ptr.as<long long>(), nullptr, 0, ix.n, ix.code(),
-                ix.scale.as<float>(), pl.qs.as<float>(), S, pl.W, pl.logW, pl.cand.as<int>(),
-                pl.dist.as<float>(), pl.nin.as<int>(), s);
-  if (pl.sp.sketch_rank)
-    launch_sketch_keep(pl.cand.as<int>(), pl.dist.as<float>(), pl.nin.as<int>(), m, pl.W, pl.KO,
-                       pl.si.as<long long>(), pl.sd.as<float>(), true, s);
-  else
-    launch_rerank_keep(pl.cand.as<int>(), pl.dist.as<float>(), pl.nin.as<int>(), m, pl.W, ix.vecs(), D,
-                       pl.qbuf.as<float>(), pl.R1, pl.KO, pl.si.as<long long>(), pl.sd.as<float>(), true,
-                       s);
-}
+/** One stage of a batch: its name (as profiled) and its launch on the index's stream. */
+struct stage {
+  std::string name;
+  std::function<void()> launch;
+};
 
-/** Waves over the neighbor table and the best k into bi / bd (search.cu:411-518). */
-void wave_round(index_impl const& ix, plan const& pl, hipStream_t s)
+/**
+ * The launches of one batch in order (search.cu:294-518): the first round over all copies with the
+ * best KO kept in si / sd, then the waves over the neighbor table, then the best k into bi / bd.
+ */
+auto batch_stages(index_impl const& ix, plan const& pl, hipStream_t s) -> std::vector<stage>
 {
-  const int D = static_cast<int>(ix.dim), S = ix.sketch_width, m = pl.m;
+  const int D = static_cast<int>(ix.dim), S = ix.sketch_width, C = ix.copies, m = pl.m;
+  std::vector<stage> out;
+  auto add = [&](const char* n, std::function<void()> f) { out.push_back({n, std::move(f)}); };
+  add("center", [&ix, &pl, s, m, D] {
+    launch_center(pl.qbuf.as<float>(), ix.mean.as<float>(), m, D, pl.qc.as<float>(), pl.qh.as<__half>(), s);
+  });
+  add("project", [&ix, &pl, s, m, D, C] {
+    launch_project(pl.qh.as<__half>(), ix.ucatT.as<__half>(), ix.shift.as<__half>(), m, D, C * 8 * ix.blocks,
+                   pl.Y.as<__half>(), s);
+  });
+  add("sketch_query", [&ix, &pl, s, m, D, S] {
+    launch_sketch_query(pl.qc.as<float>(), ix.basis.as<float>(), m, D, S, pl.qs.as<float>(), s);
+  });
+  add("probe", [&ix, &pl, s, m, C] {
+    launch_probe(pl.Y.as<__half>(), m, C, ix.levels(), ix.blocks, ix.inv_f.as<float>(), ix.offsets.as<int>(), ix.T1,
+                 ix.keys.as<long long>(), ix.mmax, ix.base.as<int>(), ix.list_len, pl.lr, ix.log_buckets,
+                 pl.seg.as<int2>(), s);
+  });
+  add("gather_lists", [&ix, &pl, s, m, S, C] {
+    launch_gather(false, pl.seg.as<int2>(), C, m, ix.list_ptr.as<long long>(), nullptr, 0, ix.n, ix.code(),
+                  ix.scale.as<float>(), pl.qs.as<float>(), S, pl.W, pl.logW, pl.cand.as<int>(), pl.dist.as<float>(),
+                  pl.nin.as<int>(), s);
+  });
+  if (pl.sp.sketch_rank)
+    add("sketch_keep", [&pl, s, m] {
+      launch_sketch_keep(pl.cand.as<int>(), pl.dist.as<float>(), pl.nin.as<int>(), m, pl.W, pl.KO,
+                         pl.si.as<long long>(), pl.sd.as<float>(), true, s);
+    });
+  else
+    add("rerank_keep", [&ix, &pl, s, m, D] {
+      launch_rerank_keep(pl.cand.as<int>(), pl.dist.as<float>(), pl.nin.as<int>(), m, pl.W, ix.vecs(), D,
+                         pl.qbuf.as<float>(), pl.R1, pl.KO, pl.si.as<long long>(), pl.sd.as<float>(), true, s);
+    });
   const int st = pl.sp.starts, nw = pl.sp.waves;
   for (int wv = 0; wv < nw; wv++) {
-    launch_pick_starts(pl.si.as<long long>(), m, pl.KO, pl.done.as<long long>(), st * nw, wv * st, st,
-                       ix.table_len, pl.seg2.as<int2>(), s);
-    launch_gather(true, pl.seg2.as<int2>(), st, m, nullptr, ix.rows(), ix.table_len, ix.n, ix.code(),
-                  ix.scale.as<float>(), pl.qs.as<float>(), S, pl.W2, pl.logW2, pl.cand2.as<int>(),
-                  pl.dist2.as<float>(), pl.n2.as<int>(), s);
+    add("pick_starts", [&ix, &pl, s, m, st, nw, wv] {
+      launch_pick_starts(pl.si.as<long long>(), m, pl.KO, pl.done.as<long long>(), st * nw, wv * st, st,
+                         ix.table_len, pl.seg2.as<int2>(), s);
+    });
+    add("gather_rows", [&ix, &pl, s, m, S, st] {
+      launch_gather(true, pl.seg2.as<int2>(), st, m, nullptr, ix.rows(), ix.table_len, ix.n, ix.code(),
+                    ix.scale.as<float>(), pl.qs.as<float>(), S, pl.W2, pl.logW2, pl.cand2.as<int>(),
+                    pl.dist2.as<float>(), pl.n2.as<int>(), s);
+    });
     if (pl.sp.sketch_rank)
-      launch_sketch_keep(pl.cand2.as<int>(), pl.dist2.as<float>(), pl.n2.as<int>(), m, pl.W2, pl.KO,
-                         pl.si.as<long long>(), pl.sd.as<float>(), false, s);
+      add("sketch_keep_wave", [&pl, s, m] {
+        launch_sketch_keep(pl.cand2.as<int>(), pl.dist2.as<float>(), pl.n2.as<int>(), m, pl.W2, pl.KO,
+                           pl.si.as<long long>(), pl.sd.as<float>(), false, s);
+      });
     else
-      launch_rerank_keep(pl.cand2.as<int>(), pl.dist2.as<float>(), pl.n2.as<int>(), m, pl.W2, ix.vecs(),
-                         D, pl.qbuf.as<float>(), pl.R2, pl.KO, pl.si.as<long long>(),
-                         pl.sd.as<float>(), false, s);
+      add("rerank_keep_wave", [&ix, &pl, s, m, D] {
+        launch_rerank_keep(pl.cand2.as<int>(), pl.dist2.as<float>(), pl.n2.as<int>(), m, pl.W2, ix.vecs(), D,
+                           pl.qbuf.as<float>(), pl.R2, pl.KO, pl.si.as<long long>(), pl.sd.as<float>(), false, s);
+      });
   }
   if (pl.sp.sketch_rank && pl.FR > 0)
-    launch_final_rerank(pl.si.as<long long>(), m, pl.KO, pl.FR, ix.vecs(), D, pl.qbuf.as<float>(), pl.k,
-                        pl.bi.as<long long>(), pl.bd.as<float>(), s);
+    add("final_rerank", [&ix, &pl, s, m, D] {
+      launch_final_rerank(pl.si.as<long long>(), m, pl.KO, pl.FR, ix.vecs(), D, pl.qbuf.as<float>(), pl.k,
+                          pl.bi.as<long long>(), pl.bd.as<float>(), s);
+    });
   else
-    launch_take_k(pl.si.as<long long>(), pl.sd.as<float>(), m, pl.KO, pl.k, pl.bi.as<long long>(),
-                  pl.bd.as<float>(), s);
+    add("take_k", [&pl, s, m] {
+      launch_take_k(pl.si.as<long long>(), pl.sd.as<float>(), m, pl.KO, pl.k, pl.bi.as<long long>(), pl.bd.as<float>(),
+                    s);
+    });
+  return out;
+}
+
+void launch_batch(index_impl const& ix, plan const& pl, hipStream_t s)
+{
+  for (auto& st : batch_stages(ix, pl, s))
+    st.launch();
 }
 
 auto make_plan(index_impl& ix, search_params const& sp, int m, int k) -> std::shared_ptr<plan>
@@ -163,15 +198,13 @@ auto make_plan(index_impl& ix, search_params const& sp, int m, int k) -> std::sh
   // one eager run (code objects loaded, LDS limits set), then the capture of the whole batch
   hipStream_t s = ix.stream;
   OCTEX_HIP(hipDeviceSynchronize());
-  first_round(ix, *pl, s);
-  wave_round(ix, *pl, s);
+  launch_batch(ix, *pl, s);
   OCTEX_HIP(hipStreamSynchronize(s));
   if (sp.use_graph) {
     hipGraph_t graph = nullptr;
     OCTEX_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
     try {
-      first_round(ix, *pl, s);
-      wave_round(ix, *pl, s);
+      launch_batch(ix, *pl, s);
     } catch (...) {
       hipGraph_t g2 = nullptr;
       (void)hipStreamEndCapture(s, &g2);
@@ -214,8 +247,7 @@ void run_batch(index_impl const& ix, plan const& pl, hipStream_t s)
   if (pl.graph != nullptr) {
     OCTEX_HIP(hipGraphLaunch(pl.graph, s));
   } else {
-    first_round(ix, pl, s);
-    wave_round(ix, pl, s);
+    launch_batch(ix, pl, s);
   }
 }
 
@@ -265,76 +297,15 @@ void profile_batch(index_impl& ix, plan& pl, int reps, std::vector<std::string>&
                    profile_counters& cnt)
 {
   hipStream_t s = ix.stream;
-  const int D = static_cast<int>(ix.dim), S = ix.sketch_width, C = ix.copies, m = pl.m;
-  std::vector<std::pair<std::string, std::function<void()>>> steps;
-  auto add = [&](std::string n, std::function<void()> f) { steps.emplace_back(std::move(n), std::move(f)); };
-  add("center", [&] {
-    launch_center(pl.qbuf.as<float>(), ix.mean.as<float>(), m, D, pl.qc.as<float>(), pl.qh.as<__half>(), s);
-  });
-  add("project", [&] {
-    launch_project(pl.qh.as<__half>(), ix.ucatT.as<__half>(), ix.shift.as<__half>(), m, D, C * 8 * ix.blocks,
-                   pl.Y.as<__half>(), s);
-  });
-  add("sketch_query", [&] { launch_sketch_query(pl.qc.as<float>(), ix.basis.as<float>(), m, D, S, pl.qs.as<float>(), s); });
-  add("probe", [&] {
-    launch_probe(pl.Y.as<__half>(), m, C, ix.levels(), ix.blocks, ix.inv_f.as<float>(), ix.offsets.as<int>(), ix.T1,
-                 ix.keys.as<long long>(), ix.mmax, ix.base.as<int>(), ix.list_len, pl.lr, ix.log_buckets,
-                 pl.seg.as<int2>(), s);
-  });
-  add("gather_lists", [&] {
-    launch_gather(false, pl.seg.as<int2>(), C, m, ix.list_ptr.as<long long>(), nullptr, 0, ix.n, ix.code(),
-                  ix.scale.as<float>(), pl.qs.as<float>(), S, pl.W, pl.logW, pl.cand.as<int>(), pl.dist.as<float>(),
-                  pl.nin.as<int>(), s);
-  });
-  if (pl.sp.sketch_rank)
-    add("sketch_keep", [&] {
-      launch_sketch_keep(pl.cand.as<int>(), pl.dist.as<float>(), pl.nin.as<int>(), m, pl.W, pl.KO,
-                         pl.si.as<long long>(), pl.sd.as<float>(), true, s);
-    });
-  else
-    add("rerank_keep", [&] {
-      launch_rerank_keep(pl.cand.as<int>(), pl.dist.as<float>(), pl.nin.as<int>(), m, pl.W, ix.vecs(), D,
-                         pl.qbuf.as<float>(), pl.R1, pl.KO, pl.si.as<long long>(), pl.sd.as<float>(), true, s);
-    });
-  const int st = pl.sp.starts, nw = pl.sp.waves;
-  for (int wv = 0; wv < nw; wv++) {
-    add("pick_starts", [&, wv] {
-      launch_pick_starts(pl.si.as<long long>(), m, pl.KO, pl.done.as<long long>(), st * nw, wv * st, st, ix.table_len,
-                         pl.seg2.as<int2>(), s);
-    });
-    add("gather_rows", [&] {
-      launch_gather(true, pl.seg2.as<int2>(), st, m, nullptr, ix.rows(), ix.table_len, ix.n, ix.code(),
-                    ix.scale.as<float>(), pl.qs.as<float>(), S, pl.W2, pl.logW2, pl.cand2.as<int>(),
-                    pl.dist2.as<float>(), pl.n2.as<int>(), s);
-    });
-    if (pl.sp.sketch_rank)
-      add("sketch_keep_wave", [&] {
-        launch_sketch_keep(pl.cand2.as<int>(), pl.dist2.as<float>(), pl.n2.as<int>(), m, pl.W2, pl.KO,
-                           pl.si.as<long long>(), pl.sd.as<float>(), false, s);
-      });
-    else
-      add("rerank_keep_wave", [&] {
-        launch_rerank_keep(pl.cand2.as<int>(), pl.dist2.as<float>(), pl.n2.as<int>(), m, pl.W2, ix.vecs(), D,
-                           pl.qbuf.as<float>(), pl.R2, pl.KO, pl.si.as<long long>(), pl.sd.as<float>(), false, s);
-      });
-  }
-  if (pl.sp.sketch_rank && pl.FR > 0)
-    add("final_rerank", [&] {
-      launch_final_rerank(pl.si.as<long long>(), m, pl.KO, pl.FR, ix.vecs(), D, pl.qbuf.as<float>(), pl.k,
-                          pl.bi.as<long long>(), pl.bd.as<float>(), s);
-    });
-  else
-    add("take_k", [&] {
-      launch_take_k(pl.si.as<long long>(), pl.sd.as<float>(), m, pl.KO, pl.k, pl.bi.as<long long>(),
-                    pl.bd.as<float>(), s);
-    });
+  const int C = ix.copies, m = pl.m, st = pl.sp.starts;
+  auto steps    = batch_stages(ix, pl, s);
   std::vector<hipEvent_t> ev(steps.size() + 1);
   for (auto& e : ev)
     OCTEX_HIP(hipEventCreate(&e));
   names.clear();
   ms.assign(steps.size(), 0.0);
   for (auto& st2 : steps)
-    names.push_back(st2.first);
+    names.push_back(st2.name);
   cnt = profile_counters{};
   std::vector<int> nin(m), n2(m);
   std::vector<int2> segh(static_cast<size_t>(m) * std::max(C, st));
@@ -343,7 +314,7 @@ void profile_batch(index_impl& ix, plan& pl, int reps, std::vector<std::string>&
     int wv = -1;
     for (size_t i = 0; i < steps.size(); i++) {
       OCTEX_HIP(hipEventRecord(ev[i], s));
-      steps[i].second();
+      steps[i].launch();
       OCTEX_HIP(hipEventRecord(ev[i + 1], s));
       OCTEX_HIP(hipEventSynchronize(ev[i + 1]));
       float t = 0;
@@ -351,7 +322,7 @@ void profile_batch(index_impl& ix, plan& pl, int reps, std::vector<std::string>&
       ms[i] += t / reps;
       if (!last) continue;
       // work counters of the last repetition, read between launches (outside the timed pairs)
-      const std::string& nm = steps[i].first;
+      const std::string& nm = steps[i].name;
       if (nm == "probe") {
         OCTEX_HIP(hipMemcpy(segh.data(), pl.seg.ptr, sizeof(int2) * m * C, hipMemcpyDeviceToHost));
         for (int64_t j = 0; j < int64_t{m} * C; j++) {
