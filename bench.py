@@ -2,10 +2,11 @@
 """Benchmark of octex's batched search on one MI355X: queries/sec at recall@10 >= 0.99 (k = 10), with the achieved
 HBM bandwidth of the dominant kernel against the roofline and the CPU oracle's rate on the same index.
 
-Workload: 1M float32 vectors, d = 128, from a 1,000-component Gaussian mixture
-(centroids uniform in [0, 128], sigma 12), clipped to [0, 255] and rounded; 10,000 queries from the same mixture;
-k = 10, batch 10,000.  Seeded synthetic data (no datasets are downloaded).  The index is built on the GPU by this
-library's builder at the start of the run.
+Workload (default --config deep100m, BASELINE.json configs[3], the north star's target): 100M L2-normalized rows,
+d = 96, of a 10,000-component Gaussian mixture (centroids N(0, 1), sigma 0.4) stored fp16 in HBM; 10,000 queries
+from the same mixture; k = 10, batch 10,000.  --config sift1m is configs[1] (1M x 128 SIFT-like mixture).  Seeded
+synthetic data (no datasets are downloaded).  The index is built on the GPU by this library's builder at the start
+of the run (about 6 minutes at 100M).
 
 Protocol (the reference's octex_bench.cu:223-242): queries resident in HBM, one capture run, warm-up, then `steps`
 timed searches of the whole batch bracketed by device synchronizations.  A short sweep over search parameters picks
@@ -160,6 +161,11 @@ class ProfilerRegion:
                 break
             except OSError:
                 continue
+        log(f"profiler region markers: {'roctx' if self.lib is not None else 'none (roctx library not found)'}")
+        if self.lib is not None:  # roctxProfilerResume / Pause(roctx_thread_id_t tid), tid 0 = every thread
+            for fn in (self.lib.roctxProfilerResume, self.lib.roctxProfilerPause):
+                fn.argtypes = [ctypes.c_uint64]
+                fn.restype = ctypes.c_int
 
     def __enter__(self):
         if self.lib is not None:
@@ -209,7 +215,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="sift1m", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="deep100m", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU time of the CPU-baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--params", default=None, help="JSON search parameters (skips the sweep)")

@@ -323,7 +323,7 @@ void set_table(index_impl& ix, std::vector<int32_t> const& rows, int k)
     ix.table = dbuf(bytes);
     ix.bytes += static_cast<int64_t>(bytes);
   }
-  OCTEX_HIP(hipMemcpy(ix.table.ptr, rows.data(), bytes, hipMemcpyHostToDevice));
+  upload(ix.table.ptr, rows.data(), bytes, ix.stream);
   ix.table_len = k;
 }
 
@@ -458,18 +458,18 @@ auto build_in_memory(index_params const& params, dataset_view const& x, build_re
   ix.vectors = dbuf(static_cast<size_t>(n) * d * sizeof(__half));
   ix.bytes += static_cast<int64_t>(ix.vectors.size);
   if (!x.f32) {
-    OCTEX_HIP(hipMemcpy(ix.vectors.ptr, x.data, ix.vectors.size, x.device ? hipMemcpyDeviceToDevice
-                                                                           : hipMemcpyHostToDevice));
+    OCTEX_HIP(hipMemcpyAsync(ix.vectors.ptr, x.data, ix.vectors.size,
+                             x.device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, s));
   } else if (x.device) {
     float_to_half(static_cast<const float*>(x.data), n * d, ix.vectors.as<__half>(), s);
   } else {  // fp32 rows from the host in pieces, rounded on the GPU
     const int64_t piece = std::min<int64_t>(n * d, int64_t{1} << 26);
     dbuf tmp(static_cast<size_t>(piece) * sizeof(float));
-    for (int64_t o = 0; o < n * d; o += piece) {
+    for (int64_t o = 0; o < n * d; o += piece) {  // tmp is rewritten only after the previous piece's kernel
       const int64_t m = std::min(piece, n * d - o);
-      OCTEX_HIP(hipMemcpyAsync(tmp.ptr, static_cast<const float*>(x.data) + o, m * sizeof(float),
-                               hipMemcpyHostToDevice, s));
+      upload(tmp.ptr, static_cast<const float*>(x.data) + o, m * sizeof(float), s);
       float_to_half(tmp.as<float>(), m, ix.vectors.as<__half>() + o, s);
+      OCTEX_HIP(hipStreamSynchronize(s));
     }
   }
   OCTEX_HIP(hipStreamSynchronize(s));
@@ -478,8 +478,7 @@ auto build_in_memory(index_params const& params, dataset_view const& x, build_re
   // PCA of a sample (build_setup.cuh:40-103): every step-th row
   const int64_t step = std::max<int64_t>(1, n / 200000), ns = (n + step - 1) / step;
   std::vector<__half> sample(static_cast<size_t>(ns) * d);
-  OCTEX_HIP(hipMemcpy2D(sample.data(), d * sizeof(__half), xd, step * d * sizeof(__half), d * sizeof(__half), ns,
-                        hipMemcpyDeviceToHost));
+  sample_rows(xd, ns, step, static_cast<int>(d), sample.data(), s);
   std::vector<double> mu(d, 0.0);
   for (int64_t i = 0; i < ns; i++)
     for (int64_t j = 0; j < d; j++)
@@ -488,7 +487,7 @@ auto build_in_memory(index_params const& params, dataset_view const& x, build_re
   for (int64_t j = 0; j < d; j++)
     rec.mean[j] = static_cast<float>(mu[j] / static_cast<double>(ns));
   ix.mean = dbuf(d * sizeof(float));
-  OCTEX_HIP(hipMemcpy(ix.mean.ptr, rec.mean.data(), d * sizeof(float), hipMemcpyHostToDevice));
+  upload(ix.mean.ptr, rec.mean.data(), d * sizeof(float), s);
   std::vector<double> G(static_cast<size_t>(d) * d);
   {
     dbuf dG(G.size() * sizeof(double));
@@ -502,6 +501,15 @@ auto build_in_memory(index_params const& params, dataset_view const& x, build_re
     pvec[i] = static_cast<float>(V[i]);
   const int p = std::min<int>(params.pca_dims, static_cast<int>(d));
   make_projections(pvec, vals, ns, d, p, w, C, params.seed, rec.proj, rec.shift);
+  {
+    double msum = 0, vsum = 0;
+    for (auto v : rec.mean)
+      msum += v;
+    for (auto v : vals)
+      vsum += v;
+    build_log("pca: %lld sampled rows, mean sum %.6g, eigenvalue sum %.6g, top %.6g\n", static_cast<long long>(ns),
+              msum, vsum, vals.empty() ? 0.0 : vals[0]);
+  }
   phase("setup");
 
   // cells of every copy
@@ -519,8 +527,8 @@ auto build_in_memory(index_params const& params, dataset_view const& x, build_re
     dbuf y(static_cast<size_t>(n) * w * sizeof(float)), U(static_cast<size_t>(d) * w * sizeof(float)),
       sh(w * sizeof(float));
     for (int c = 0; c < C; c++) {
-      OCTEX_HIP(hipMemcpy(U.ptr, rec.proj.data() + static_cast<size_t>(c) * d * w, U.size, hipMemcpyHostToDevice));
-      OCTEX_HIP(hipMemcpy(sh.ptr, rec.shift.data() + static_cast<size_t>(c) * w, sh.size, hipMemcpyHostToDevice));
+      upload(U.ptr, rec.proj.data() + static_cast<size_t>(c) * d * w, U.size, s);
+      upload(sh.ptr, rec.shift.data() + static_cast<size_t>(c) * w, sh.size, s);
       project_rows(xd, n, static_cast<int>(d), ix.mean.as<float>(), U.as<float>(), sh.as<float>(), w, y.as<float>(), s);
       std::vector<dbuf> level_lists(L);
       level_keys[c].resize(L);
@@ -582,9 +590,9 @@ auto build_in_memory(index_params const& params, dataset_view const& x, build_re
     for (int c = 0; c < C; c++)
       hp[c] = reinterpret_cast<long long>(ix.copy_lists[c].ptr);
     ix.list_ptr = dbuf(hp.size() * sizeof(long long));
-    OCTEX_HIP(hipMemcpy(ix.list_ptr.ptr, hp.data(), ix.list_ptr.size, hipMemcpyHostToDevice));
+    upload(ix.list_ptr.ptr, hp.data(), ix.list_ptr.size, s);
     ix.base = dbuf(rec.base.size() * sizeof(int32_t));
-    OCTEX_HIP(hipMemcpy(ix.base.ptr, rec.base.data(), ix.base.size, hipMemcpyHostToDevice));
+    upload(ix.base.ptr, rec.base.data(), ix.base.size, s);
   }
   // the search-side arrays of the loader (load.cu:385-402): fp16 ucatT and shift, inv_f of the JSON text
   {
@@ -601,9 +609,9 @@ auto build_in_memory(index_params const& params, dataset_view const& x, build_re
     ix.ucatT = dbuf(uc.size() * sizeof(__half));
     ix.shift = dbuf(shh.size() * sizeof(__half));
     ix.inv_f = dbuf(inv.size() * sizeof(float));
-    OCTEX_HIP(hipMemcpy(ix.ucatT.ptr, uc.data(), ix.ucatT.size, hipMemcpyHostToDevice));
-    OCTEX_HIP(hipMemcpy(ix.shift.ptr, shh.data(), ix.shift.size, hipMemcpyHostToDevice));
-    OCTEX_HIP(hipMemcpy(ix.inv_f.ptr, inv.data(), ix.inv_f.size, hipMemcpyHostToDevice));
+    upload(ix.ucatT.ptr, uc.data(), ix.ucatT.size, s);
+    upload(ix.shift.ptr, shh.data(), ix.shift.size, s);
+    upload(ix.inv_f.ptr, inv.data(), ix.inv_f.size, s);
   }
   phase("copies");
 
@@ -615,11 +623,11 @@ auto build_in_memory(index_params const& params, dataset_view const& x, build_re
   ix.basis  = dbuf(rec.basis.size() * sizeof(float));
   ix.sketch = dbuf(static_cast<size_t>(n) * S);
   ix.bytes += static_cast<int64_t>(ix.sketch.size);
-  OCTEX_HIP(hipMemcpy(ix.basis.ptr, rec.basis.data(), ix.basis.size, hipMemcpyHostToDevice));
+  upload(ix.basis.ptr, rec.basis.data(), ix.basis.size, s);
   make_sketch(xd, n, static_cast<int>(d), ix.mean.as<float>(), ix.basis.as<float>(), S, rec.scale,
               ix.sketch.as<signed char>(), s);
   ix.scale = dbuf(S * sizeof(float));
-  OCTEX_HIP(hipMemcpy(ix.scale.ptr, rec.scale.data(), ix.scale.size, hipMemcpyHostToDevice));
+  upload(ix.scale.ptr, rec.scale.data(), ix.scale.size, s);
   phase("sketch");
 
   // neighbor table, searched by this library's search

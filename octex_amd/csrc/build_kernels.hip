@@ -31,6 +31,14 @@ __global__ void pca_sample_kernel(const __half* __restrict__ x, int64_t ns, int6
   A[t]      = static_cast<double>(__half2float(x[i * step * d + k]) - mean[k]);
 }
 
+__global__ void sample_rows_kernel(const __half* __restrict__ x, int64_t ns, int64_t step, int d,
+                                   __half* __restrict__ out)
+{
+  int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= ns * d) return;
+  out[t] = x[(t / d) * step * d + t % d];
+}
+
 /** G = A^T A (fp64) by 16 x 16 output tiles, samples staged through LDS in chunks of 64 rows. */
 __global__ __launch_bounds__(256) void scatter_kernel(const double* __restrict__ A, int64_t ns, int d,
                                                       double* __restrict__ G)
@@ -311,6 +319,16 @@ void pca_scatter(const __half* x, int64_t n, int d, int64_t step, int64_t ns, co
   dim3 grid((d + 15) / 16, (d + 15) / 16);
   scatter_kernel<<<grid, 256, 0, s>>>(A.as<double>(), ns, d, G);
   OCTEX_HIP(hipGetLastError());
+  OCTEX_HIP(hipStreamSynchronize(s));
+}
+
+void sample_rows(const __half* x, int64_t ns, int64_t step, int d, __half* host_out, hipStream_t s)
+{
+  if (ns * d == 0) return;
+  dbuf tmp(static_cast<size_t>(ns) * d * sizeof(__half));
+  sample_rows_kernel<<<grid_for(ns * d, 256), 256, 0, s>>>(x, ns, step, d, tmp.as<__half>());
+  OCTEX_HIP(hipGetLastError());
+  OCTEX_HIP(hipMemcpyAsync(host_out, tmp.ptr, tmp.size, hipMemcpyDeviceToHost, s));
   OCTEX_HIP(hipStreamSynchronize(s));
 }
 

@@ -13,6 +13,8 @@ namespace cuvs::neighbors::octex::detail {
 /** G [d, d] (device, fp64) = A^T A of the ns sampled rows x[i * step] - mean. */
 void pca_scatter(const __half* x, int64_t n, int d, int64_t step, int64_t ns, const float* mean, double* G,
                  hipStream_t s);
+/** host_out [ns, d] = the rows x[i * step] (device to host through a compact device copy). */
+void sample_rows(const __half* x, int64_t ns, int64_t step, int d, __half* host_out, hipStream_t s);
 /** y [n, w] = (x - mean) @ U [d, w] + shift (fp32). */
 void project_rows(const __half* x, int64_t n, int d, const float* mean, const float* U, const float* shift, int w,
                   float* y, hipStream_t s);

@@ -553,6 +553,7 @@ extern "C" cuvsError_t octexIndexCopyArray(cuvsOctexIndex_t index, const char* n
     if (size != nullptr) *size = static_cast<int64_t>(sz);
     if (dst != nullptr && bytes > 0 && src != nullptr) {
       OCTEX_HIP(hipSetDevice(ix.device));
+      OCTEX_HIP(hipStreamSynchronize(ix.stream));  // the index's own stream may still write it
       OCTEX_HIP(hipMemcpy(dst, src, std::min<size_t>(sz, static_cast<size_t>(bytes)), hipMemcpyDefault));
     }
   });
@@ -578,7 +579,7 @@ extern "C" cuvsError_t octexIndexCopyArrayRanges(cuvsOctexIndex_t index, const c
     }
     OCTEX_HIP(hipSetDevice(ix.device));
     octex::detail::dbuf doff(words.size() * sizeof(int64_t)), dout(static_cast<size_t>(count * bytes));
-    OCTEX_HIP(hipMemcpy(doff.ptr, words.data(), doff.size, hipMemcpyHostToDevice));
+    octex::detail::upload(doff.ptr, words.data(), doff.size, ix.stream);
     octex::detail::launch_copy_ranges(static_cast<const uint32_t*>(src), doff.as<int64_t>(), count,
                                       static_cast<int>(bytes / 4), dout.as<uint32_t>(), ix.stream);
     OCTEX_HIP(hipStreamSynchronize(ix.stream));
@@ -598,6 +599,7 @@ extern "C" cuvsError_t octexIndexCopyArrayRange(cuvsOctexIndex_t index, const ch
                   static_cast<long long>(offset + bytes), sz);
     if (bytes == 0) return;
     OCTEX_HIP(hipSetDevice(ix.device));
+    OCTEX_HIP(hipStreamSynchronize(ix.stream));
     OCTEX_HIP(hipMemcpy(dst, static_cast<const char*>(src) + offset, static_cast<size_t>(bytes), hipMemcpyDefault));
   });
 }

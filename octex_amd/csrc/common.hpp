@@ -99,6 +99,18 @@ struct hbuf {
   }
 };
 
+/**
+ * A host-to-device copy that is on the device when this returns and ordered before later work on s.  A
+ * plain hipMemcpy from pageable memory may return before its DMA lands, and a non-blocking stream does
+ * not wait for the null stream, so a kernel on s could read the old bytes.
+ */
+inline void upload(void* dst, const void* src, size_t bytes, hipStream_t s)
+{
+  if (bytes == 0) return;
+  OCTEX_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s));
+  OCTEX_HIP(hipStreamSynchronize(s));
+}
+
 inline auto grid_for(int64_t total, int threads) -> unsigned
 {
   return static_cast<unsigned>((total + threads - 1) / threads);

@@ -38,7 +38,7 @@ void upload_to(void* dst, const void* src, size_t bytes, hipStream_t s)
   constexpr size_t kChunk = size_t{64} << 20;
   if (bytes == 0) return;
   if (bytes <= kChunk) {
-    OCTEX_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    detail::upload(dst, src, bytes, s);
     return;
   }
   hbuf stage[2] = {hbuf(kChunk), hbuf(kChunk)};

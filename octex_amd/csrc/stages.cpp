@@ -111,7 +111,7 @@ extern "C" cuvsError_t octexStageGather(int32_t rows, const int32_t* seg, int32_
       for (int c = 0; c < nseg; c++)
         hp[c] = reinterpret_cast<long long>(lists + static_cast<int64_t>(c) * stride);
       ptrs = dbuf(hp.size() * sizeof(long long));
-      OCTEX_HIP(hipMemcpy(ptrs.ptr, hp.data(), ptrs.size, hipMemcpyHostToDevice));
+      upload(ptrs.ptr, hp.data(), ptrs.size, s);
     }
     launch_gather(rows != 0, reinterpret_cast<const int2*>(seg), nseg, m, ptrs.as<long long>(), table, table_len,
                   n, reinterpret_cast<const signed char*>(code), scale, qs, S, W, log2_ceil(W), cand, dist,
