@@ -49,8 +49,9 @@ cuvsError_t octexIndexProfileBatch(cuvsOctexIndex_t index, cuvsOctexSearchParams
 /**
  * Copy an array of a loaded or built index to dst (host or device), at most `bytes`; *size receives
  * its size: "lists" (of copy `copy`), "keys", "offsets", "base", "ucatT", "shift", "inv_f", "mean",
- * "basis", "scale", "sketch", "vectors", "table", "spacings" (float32), and "meta" (11 int64: n, dim,
- * copies, blocks, levels, list_len, log_buckets, sketch_width, table_len, mmax, T1).
+ * "basis", "scale", "sketch" ([n, sketch_pitch]: rows padded in memory), "vectors", "table",
+ * "spacings" (float32), and "meta" (12 int64: n, dim, copies, blocks, levels, list_len, log_buckets,
+ * sketch_width, table_len, mmax, T1, sketch_pitch).
  */
 cuvsError_t octexIndexCopyArray(cuvsOctexIndex_t index, const char* name, int32_t copy, void* dst, int64_t bytes,
                                 int64_t* size);

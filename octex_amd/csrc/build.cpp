@@ -621,10 +621,11 @@ auto build_in_memory(index_params const& params, dataset_view const& x, build_re
     for (int sI = 0; sI < S; sI++)
       rec.basis[r * S + sI] = pvec[r * d + sI];
   ix.basis  = dbuf(rec.basis.size() * sizeof(float));
-  ix.sketch = dbuf(static_cast<size_t>(n) * S);
+  ix.sketch_pitch = sketch_pitch_for(S);
+  ix.sketch       = dbuf(static_cast<size_t>(n) * ix.sketch_pitch);
   ix.bytes += static_cast<int64_t>(ix.sketch.size);
   upload(ix.basis.ptr, rec.basis.data(), ix.basis.size, s);
-  make_sketch(xd, n, static_cast<int>(d), ix.mean.as<float>(), ix.basis.as<float>(), S, rec.scale,
+  make_sketch(xd, n, static_cast<int>(d), ix.mean.as<float>(), ix.basis.as<float>(), S, ix.sketch_pitch, rec.scale,
               ix.sketch.as<signed char>(), s);
   ix.scale = dbuf(S * sizeof(float));
   upload(ix.scale.ptr, rec.scale.data(), ix.scale.size, s);
@@ -680,6 +681,23 @@ class npy_stream {
       size_t m = std::min(bytes, z.size());
       put(z.data(), m);
       bytes -= m;
+    }
+  }
+  /** rows of `row_bytes` stored `pitch` bytes apart on the device, written back to back */
+  void put_device_rows(const void* p, int64_t rows, size_t row_bytes, size_t pitch)
+  {
+    if (pitch == row_bytes) {
+      put_device(p, static_cast<size_t>(rows) * row_bytes);
+      return;
+    }
+    const int64_t chunk = std::max<int64_t>(1, (int64_t{64} << 20) / static_cast<int64_t>(pitch));
+    std::vector<char> h(static_cast<size_t>(std::min(chunk, rows)) * pitch);
+    for (int64_t r0 = 0; r0 < rows; r0 += chunk) {
+      const int64_t m = std::min(chunk, rows - r0);
+      OCTEX_HIP(hipMemcpy(h.data(), static_cast<const char*>(p) + r0 * pitch, static_cast<size_t>(m) * pitch,
+                          hipMemcpyDeviceToHost));
+      for (int64_t r = 0; r < m; r++)
+        put(h.data() + r * pitch, row_bytes);
     }
   }
   void put_device(const void* p, size_t bytes)
@@ -748,7 +766,7 @@ void write_index(index_impl const& ix, build_record const& rec, index_params con
   write_npy(file("sketch_scale.npy"), rec.scale.data(), {int64_t{S}});
   {
     npy_stream sk(file("sketch.npy"), "|i1", {n, int64_t{S}});
-    sk.put_device(ix.sketch.ptr, static_cast<size_t>(n) * S);
+    sk.put_device_rows(ix.sketch.ptr, n, S, ix.sketch_pitch);
     sk.close();
   }
   {

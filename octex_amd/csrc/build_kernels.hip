@@ -269,11 +269,17 @@ __global__ __launch_bounds__(256) void sketch_project_kernel(const __half* __res
 
 /** codes = clamp(rint(v / scale), -127, 127) (build_setup.cuh:183-190). */
 __global__ void quantize_kernel(const float* __restrict__ v, const float* __restrict__ scale, int64_t n, int S,
-                                signed char* __restrict__ out)
+                                int pitch, signed char* __restrict__ out)
 {
   int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (t >= n * S) return;
-  float q = rintf(v[t] / scale[t % S]);
+  if (t >= n * pitch) return;
+  const int64_t i = t / pitch;
+  const int s     = static_cast<int>(t % pitch);
+  if (s >= S) {  // the row's padding
+    out[t] = 0;
+    return;
+  }
+  float q = rintf(v[i * S + s] / scale[s]);
   out[t]  = static_cast<signed char>(fminf(127.f, fmaxf(-127.f, q)));
 }
 
@@ -366,7 +372,7 @@ void float_to_half(const float* x, int64_t total, __half* out, hipStream_t s)
   }
 }
 
-void make_sketch(const __half* x, int64_t n, int d, const float* mean, const float* basis, int S,
+void make_sketch(const __half* x, int64_t n, int d, const float* mean, const float* basis, int S, int pitch,
                  std::vector<float>& scale, signed char* codes, hipStream_t s)
 {
   const int64_t chunk = std::min<int64_t>(n, int64_t{1} << 22);
@@ -391,7 +397,8 @@ void make_sketch(const __half* x, int64_t n, int d, const float* mean, const flo
     int64_t m = std::min(chunk, n - r0);
     sketch_project_kernel<<<grid_for(m * S, 256), 256, 0, s>>>(x + r0 * d, m, d, mean, basis, S, v.as<float>(),
                                                               amax.as<unsigned>());
-    quantize_kernel<<<grid_for(m * S, 256), 256, 0, s>>>(v.as<float>(), dscale.as<float>(), m, S, codes + r0 * S);
+    quantize_kernel<<<grid_for(m * pitch, 256), 256, 0, s>>>(v.as<float>(), dscale.as<float>(), m, S, pitch,
+                                                             codes + r0 * pitch);
   }
   OCTEX_HIP(hipGetLastError());
   OCTEX_HIP(hipStreamSynchronize(s));

@@ -21,8 +21,8 @@ void project_rows(const __half* x, int64_t n, int d, const float* mean, const fl
 void half_to_float(const __half* x, int64_t total, float* out, hipStream_t s);
 /** out = fp16(x), round to nearest even (device arrays). */
 void float_to_half(const float* x, int64_t total, __half* out, hipStream_t s);
-/** The int8 sketch: scale = amax / 127 per coordinate, codes = round(((x - mean) @ basis) / scale). */
-void make_sketch(const __half* x, int64_t n, int d, const float* mean, const float* basis, int S,
+/** The int8 sketch: scale = amax / 127 per coordinate, codes [n, pitch] = round(((x - mean) @ basis) / scale). */
+void make_sketch(const __half* x, int64_t n, int d, const float* mean, const float* basis, int S, int pitch,
                  std::vector<float>& scale, signed char* codes, hipStream_t s);
 
 /** Scratch of the cells of one level of one copy (reused across levels and copies). */

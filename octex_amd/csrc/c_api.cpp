@@ -522,7 +522,7 @@ auto index_array(octex::detail::index_impl& ix, std::string const& n, int32_t co
   if (n == "mean") return of(ix.mean);
   if (n == "basis") return of(ix.basis);
   if (n == "scale") return of(ix.scale);
-  if (n == "sketch") return {ix.code(), static_cast<size_t>(ix.n) * ix.sketch_width};
+  if (n == "sketch") return {ix.code(), static_cast<size_t>(ix.n) * ix.sketch_pitch};
   if (n == "vectors") return {ix.vecs(), static_cast<size_t>(ix.n) * ix.dim * sizeof(__half)};
   if (n == "table") return {ix.rows(), static_cast<size_t>(ix.n) * ix.table_len * sizeof(int32_t)};
   octex::detail::fail("octex: unknown index array %s", n.c_str());
@@ -536,9 +536,10 @@ extern "C" cuvsError_t octexIndexCopyArray(cuvsOctexIndex_t index, const char* n
   return translate_exceptions([=] {
     auto& ix = as_index(*index)->impl();
     std::string n(name != nullptr ? name : "");
-    if (n == "meta") {  // n, dim, copies, blocks, levels, list_len, log_buckets, sketch_width, table_len, mmax, T1
-      int64_t m[11] = {ix.n, ix.dim, ix.copies, ix.blocks, ix.levels(), ix.list_len, ix.log_buckets, ix.sketch_width,
-                       ix.table_len, ix.mmax, ix.T1};
+    if (n == "meta") {  // n, dim, copies, blocks, levels, list_len, log_buckets, sketch_width, table_len, mmax, T1,
+                        // sketch_pitch
+      int64_t m[12] = {ix.n,           ix.dim,       ix.copies,    ix.blocks, ix.levels(), ix.list_len,
+                       ix.log_buckets, ix.sketch_width, ix.table_len, ix.mmax, ix.T1,     ix.sketch_pitch};
       if (size != nullptr) *size = sizeof(m);
       if (dst != nullptr) std::memcpy(dst, m, std::min<size_t>(sizeof(m), static_cast<size_t>(bytes)));
       return;

@@ -31,10 +31,25 @@ namespace cuvs::neighbors::octex::detail {
 
 struct plan;  // buffers and graph of one (batch, k, search parameters); search.cpp
 
+/**
+ * Bytes between two sketch rows of S codes in memory: the next power of two for S <= 128, else a multiple
+ * of 128, so that no row straddles a 128-byte cache line (a 96-byte row at a 96-byte stride touches 1.5
+ * lines on average; padded to 128 it touches one).  The directory keeps rows of S bytes.
+ */
+inline auto sketch_pitch_for(int S) -> int
+{
+  if (S > 128) return (S + 127) / 128 * 128;
+  int p = 16;
+  while (p < S)
+    p <<= 1;
+  return p;
+}
+
 struct index_impl {
   // meta.json
   int64_t n = 0, dim = 0;
   int copies = 0, blocks = 4, list_len = 0, log_buckets = 20, sketch_width = 0, table_len = 0;
+  int sketch_pitch = 0;  // bytes between sketch rows in memory (sketch_pitch_for(sketch_width))
   std::vector<float> spacings;
   std::string path;
 

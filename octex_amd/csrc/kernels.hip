@@ -257,7 +257,7 @@ __device__ __forceinline__ int hash_log_dev(int total, int log_cap)
  */
 template <int LR>
 __device__ __forceinline__ void sketch_scores(const int* crow, int n, const signed char* __restrict__ code,
-                                              int S, const float* qv, const float* sc, float* drow)
+                                              int S, int pitch, const float* qv, const float* sc, float* drow)
 {
   constexpr int kRows = 4;        // candidates per group in flight
   constexpr int GPW   = 64 / LR;  // groups per wavefront
@@ -282,7 +282,7 @@ __device__ __forceinline__ void sketch_scores(const int* crow, int n, const sign
     int4 w[kRows];
 #pragma unroll
     for (int r = 0; r < kRows; r++)
-      w[r] = *reinterpret_cast<const int4*>(code + static_cast<int64_t>(id[r]) * S + (has ? k : 0));
+      w[r] = *reinterpret_cast<const int4*>(code + static_cast<int64_t>(id[r]) * pitch + (has ? k : 0));
     float d[kRows];
 #pragma unroll
     for (int r = 0; r < kRows; r++) {
@@ -320,7 +320,7 @@ template <bool kRows, int LR>
 __global__ __launch_bounds__(kGatherThreads) void gather_kernel(
   const int2* __restrict__ seg, int nseg, const long long* __restrict__ list_ptr,
   const int* __restrict__ table, int table_len, int64_t N, const signed char* __restrict__ code,
-  const float* __restrict__ scale, const float* __restrict__ qs, int S, int W, int logW,
+  const float* __restrict__ scale, const float* __restrict__ qs, int S, int pitch, int W, int logW,
   int* __restrict__ cand, float* __restrict__ dist, int* __restrict__ nout)
 {
   constexpr int kUnroll = 4;
@@ -419,7 +419,7 @@ __global__ __launch_bounds__(kGatherThreads) void gather_kernel(
   }
   __syncthreads();
   const int n = min(cnt, W);
-  sketch_scores<LR>(crow, n, code, S, qv, sc, dist + static_cast<int64_t>(q) * W);
+  sketch_scores<LR>(crow, n, code, S, pitch, qv, sc, dist + static_cast<int64_t>(q) * W);
   if (tid == 0) nout[q] = n;
 }
 
@@ -949,10 +949,11 @@ auto gather_smem(int W, int S, int nseg) -> size_t
 }
 
 void launch_gather(bool rows, const int2* seg, int nseg, int m, const long long* list_ptr,
-                   const int* table, int table_len, int64_t n, const signed char* code, const float* scale,
-                   const float* qs, int S, int W, int logW, int* cand, float* dist, int* nout,
-                   hipStream_t s)
+                   const int* table, int table_len, int64_t n, const signed char* code, int pitch,
+                   const float* scale, const float* qs, int S, int W, int logW, int* cand, float* dist,
+                   int* nout, hipStream_t s)
 {
+  OCTEX_EXPECTS(pitch >= S && pitch % 16 == 0, "octex: sketch rows are at least S bytes apart, 16-byte aligned");
   if (m == 0) return;
   OCTEX_EXPECTS(nseg >= 1, "octex: a gather needs at least one segment per query");
   OCTEX_EXPECTS(W == (1 << logW) && W <= kMaxHash, "octex: hash set size");
@@ -968,7 +969,7 @@ void launch_gather(bool rows, const int2* seg, int nseg, int m, const long long*
     OCTEX_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gather_kernel<R, LR>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
     gather_kernel<R, LR><<<m, kGatherThreads, smem, s>>>(seg, nseg, list_ptr, table, table_len, n, code, scale,
-                                                          qs, S, W, logW, cand, dist, nout);
+                                                          qs, S, pitch, W, logW, cand, dist, nout);
   };
   auto by_lr = [&](auto rows_tag) {
     switch (Lr) {

@@ -50,10 +50,11 @@ void launch_probe(const __half* Y, int m, int C, int L, int B, const float* inv_
 auto gather_smem(int W, int S, int nseg) -> size_t;
 /** Ids at or above `n` (a corrupt list or table entry) are skipped like the -1 padding. */
 /** Lists: segment c of a query reads copy c's lists at list_ptr[c] (a device pointer per copy). */
+/** code [n, pitch]: the S sketch codes of row v start at code + v * pitch. */
 void launch_gather(bool rows, const int2* seg, int nseg, int m, const long long* list_ptr,
-                   const int* table, int table_len, int64_t n, const signed char* code, const float* scale,
-                   const float* qs, int S, int W, int logW, int* cand, float* dist, int* nout,
-                   hipStream_t s);
+                   const int* table, int table_len, int64_t n, const signed char* code, int pitch,
+                   const float* scale, const float* qs, int S, int W, int logW, int* cand, float* dist,
+                   int* nout, hipStream_t s);
 void launch_rerank_keep(const int* cand, const float* dist, const int* nin, int m, int W,
                         const __half* vectors, int D, const float* Q, int R, int KO, long long* si,
                         float* sd, bool fresh, hipStream_t s);

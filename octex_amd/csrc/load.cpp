@@ -231,12 +231,36 @@ auto load(raft::resources const& res, std::string const& path, load_params const
   ix.mean  = upload(ix, mean.as<float>(), D * sizeof(float));
   ix.basis = upload(ix, basis.as<float>(), D * S * sizeof(float));
   ix.scale = upload(ix, scale.as<float>(), S * sizeof(float));
-  const size_t code_bytes = static_cast<size_t>(N * S);
-  if (params.sketch == sketch_placement::host) {
-    sketch.as<int8_t>();
-    ix.host_sketch = to_pinned(sketch, code_bytes);
-  } else {
-    ix.sketch = upload(ix, sketch.as<int8_t>(), code_bytes);
+  ix.sketch_pitch = detail::sketch_pitch_for(S);
+  if (ix.sketch_pitch == S) {
+    const size_t code_bytes = static_cast<size_t>(N * S);
+    if (params.sketch == sketch_placement::host) {
+      sketch.as<int8_t>();
+      ix.host_sketch = to_pinned(sketch, code_bytes);
+    } else {
+      ix.sketch = upload(ix, sketch.as<int8_t>(), code_bytes);
+    }
+  } else {  // rows of S codes spread to the padded pitch, a chunk of rows at a time
+    const int64_t P = ix.sketch_pitch;
+    const char* src = reinterpret_cast<const char*>(sketch.as<int8_t>());
+    const bool host = params.sketch == sketch_placement::host;
+    if (host)
+      ix.host_sketch = hbuf(static_cast<size_t>(N * P));
+    else {
+      ix.sketch = dbuf(static_cast<size_t>(N * P));
+      ix.bytes += static_cast<int64_t>(ix.sketch.size);
+    }
+    const int64_t chunk = std::max<int64_t>(1, (int64_t{64} << 20) / P);
+    std::vector<char> tmp(host ? 0 : static_cast<size_t>(std::min(chunk, N) * P), 0);
+    for (int64_t r0 = 0; r0 < N; r0 += chunk) {
+      const int64_t m = std::min(chunk, N - r0);
+      char* dst       = host ? static_cast<char*>(ix.host_sketch.ptr) + r0 * P : tmp.data();
+      for (int64_t r = 0; r < m; r++) {
+        std::memcpy(dst + r * P, src + (r0 + r) * S, S);
+        std::memset(dst + r * P + S, 0, P - S);
+      }
+      if (!host) upload_to(ix.sketch.as<char>() + r0 * P, tmp.data(), static_cast<size_t>(m * P), ix.stream);
+    }
   }
   const size_t vec_bytes = static_cast<size_t>(N * D) * sizeof(__half);
   if (params.vectors_on_host) {

@@ -114,7 +114,7 @@ extern "C" cuvsError_t octexStageGather(int32_t rows, const int32_t* seg, int32_
       upload(ptrs.ptr, hp.data(), ptrs.size, s);
     }
     launch_gather(rows != 0, reinterpret_cast<const int2*>(seg), nseg, m, ptrs.as<long long>(), table, table_len,
-                  n, reinterpret_cast<const signed char*>(code), scale, qs, S, W, log2_ceil(W), cand, dist,
+                  n, reinterpret_cast<const signed char*>(code), S, scale, qs, S, W, log2_ceil(W), cand, dist,
                   nout, s);
     OCTEX_HIP(hipStreamSynchronize(s));
   });

@@ -246,7 +246,7 @@ class Index:
     def _from_live(self, live, queries=None, read=32):
         """The arrays of a loaded or built octex_amd index, copied to the host (the same index the GPU searches)."""
         meta = live.array("meta", np.int64)
-        n, dim, C, blocks, L, list_len, log_buckets, S, table_len, mmax, T1 = (int(v) for v in meta)
+        n, dim, C, blocks, L, list_len, log_buckets, S, table_len, mmax, T1, pitch = (int(v) for v in meta)
         self.n, self.dim, self.copies, self.blocks, self.list_len = n, dim, C, blocks, list_len
         self.log_buckets, self.sketch_width, self.table_len = log_buckets, S, table_len
         self.spacings = [float(v) for v in live.array("spacings", np.float32)]
@@ -271,7 +271,7 @@ class Index:
         self.mean = live.array("mean", np.float32)
         self.basis = live.array("basis", np.float32).reshape(dim, S)
         self.scale = live.array("scale", np.float32)
-        self.sketch = live.array("sketch", np.int8).reshape(n, S)
+        self.sketch = np.ascontiguousarray(live.array("sketch", np.int8).reshape(n, pitch)[:, :S])
         self.vectors = live.array("vectors", np.uint16).reshape(n, dim)
         self.table = live.array("table", np.int32).reshape(n, table_len) if table_len > 0 else None
         self.meta = {}
