@@ -426,7 +426,7 @@ __global__ __launch_bounds__(kGatherThreads) void gather_kernel(
 // ------------------------------------------------------------------ selection and merges
 
 struct select_state {
-  unsigned prefix, kk, eq, idprefix, kk2;
+  unsigned prefix, kk, eq, idprefix, kk2, kmin, kmax;
   int nsel, need_id;
 };
 
@@ -471,22 +471,28 @@ __device__ __forceinline__ bool pick_digit(const unsigned* hist, unsigned& kk, u
  * :259-322 with a deterministic tie rule): a radix select over the distance bits finds the threshold
  * T; when only some of the keys equal to T are taken, a second radix select over their ids takes the
  * smallest ids.  Selected ids (and keys when skey is set) go to sid / skey in any order; nsel in st.
- * All threads of the workgroup call it.
+ * Each thread keeps its first kCache keys in registers for every pass (the rest are read again), and
+ * the digits on which the smallest and the largest key agree are taken without a histogram pass (every
+ * key has them; the candidates of one query share most exponent bits, which would otherwise send all
+ * of them to one bin).  All threads of the workgroup call it.
  */
 __device__ void select_smallest(const unsigned* __restrict__ kd, const int* __restrict__ cid, int n,
                                 int R, int* sid, float* skey, unsigned* hist, select_state& st)
 {
-  const int tid = threadIdx.x, wid = tid >> 6;
+  constexpr int kCache = 4;
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, nthr = blockDim.x;
   if (tid == 0) {
     st.prefix  = 0;
     st.kk      = min(R, n);
     st.nsel    = 0;
     st.need_id = 0;
-    st.eq      = 0;
+    st.eq      = static_cast<unsigned>(n);
+    st.kmin    = ~0u;
+    st.kmax    = 0u;
   }
   __syncthreads();
   if (n <= R) {
-    for (int i = tid; i < n; i += blockDim.x) {
+    for (int i = tid; i < n; i += nthr) {
       sid[i] = cid[i];
       if (skey) skey[i] = __uint_as_float(kd[i]);
     }
@@ -494,16 +500,59 @@ __device__ void select_smallest(const unsigned* __restrict__ kd, const int* __re
     __syncthreads();
     return;
   }
+  // valid keys are finite non-negative floats (below 0x7f800000); kNone marks an empty register slot
+  constexpr unsigned kNone = ~0u;
+  unsigned kr[kCache];
+  unsigned lo = ~0u, hi = 0u;
+#pragma unroll
+  for (int j = 0; j < kCache; j++) {
+    const int i = tid + j * nthr;
+    kr[j]       = i < n ? kd[i] : kNone;
+  }
+#pragma unroll
+  for (int j = 0; j < kCache; j++)
+    if (kr[j] != kNone) {
+      lo = min(lo, kr[j]);
+      hi = max(hi, kr[j]);
+    }
+  for (int i = tid + kCache * nthr; i < n; i += nthr) {
+    const unsigned k = kd[i];
+    lo               = min(lo, k);
+    hi               = max(hi, k);
+  }
+#pragma unroll
+  for (int o = 32; o; o >>= 1) {
+    lo = min(lo, static_cast<unsigned>(__shfl_xor(static_cast<int>(lo), o)));
+    hi = max(hi, static_cast<unsigned>(__shfl_xor(static_cast<int>(hi), o)));
+  }
+  if (lane == 0) {
+    atomicMin(&st.kmin, lo);
+    atomicMax(&st.kmax, hi);
+  }
+  __syncthreads();
+  const unsigned kmin = st.kmin, kmax = st.kmax;
+  // every key, from the registers (kNone skipped) and then from memory
+  auto for_keys = [&](auto&& f) {
+#pragma unroll
+    for (int j = 0; j < kCache; j++)
+      if (kr[j] != kNone) f(kr[j], tid + j * nthr);
+    for (int i = tid + kCache * nthr; i < n; i += nthr)
+      f(kd[i], i);
+  };
   unsigned mask = 0;
   for (int shift = 24; shift >= 0; shift -= 8) {
-    for (int i = tid; i < 256; i += blockDim.x)
+    if ((kmin >> shift) == (kmax >> shift)) {  // a digit every key has: taken without a pass
+      if (tid == 0) st.prefix |= ((kmin >> shift) & 255u) << shift;
+      mask |= 255u << shift;
+      continue;
+    }
+    for (int i = tid; i < 256; i += nthr)
       hist[i] = 0;
     __syncthreads();
     const unsigned pf = st.prefix;
-    for (int i = tid; i < n; i += blockDim.x) {
-      unsigned k = kd[i];
+    for_keys([&](unsigned k, int) {
       if ((k & mask) == pf) atomicAdd(&hist[(k >> shift) & 255u], 1u);
-    }
+    });
     __syncthreads();
     if (wid == 0) {
       unsigned kk = st.kk, digit = 0, pop = 0;
@@ -516,6 +565,7 @@ __device__ void select_smallest(const unsigned* __restrict__ kd, const int* __re
     mask |= 255u << shift;
     __syncthreads();
   }
+  __syncthreads();
   const unsigned T = st.prefix;
   if (st.kk < st.eq) {  // ties at T: the smallest ids among the keys equal to T
     if (tid == 0) {
@@ -526,14 +576,16 @@ __device__ void select_smallest(const unsigned* __restrict__ kd, const int* __re
     __syncthreads();
     unsigned imask = 0;
     for (int shift = 24; shift >= 0; shift -= 8) {
-      for (int i = tid; i < 256; i += blockDim.x)
+      for (int i = tid; i < 256; i += nthr)
         hist[i] = 0;
       __syncthreads();
       const unsigned pf = st.idprefix;
-      for (int i = tid; i < n; i += blockDim.x) {
-        unsigned id = static_cast<unsigned>(cid[i]);
-        if (kd[i] == T && (id & imask) == pf) atomicAdd(&hist[(id >> shift) & 255u], 1u);
-      }
+      for_keys([&](unsigned k, int i) {
+        if (k == T) {
+          const unsigned id = static_cast<unsigned>(cid[i]);
+          if ((id & imask) == pf) atomicAdd(&hist[(id >> shift) & 255u], 1u);
+        }
+      });
       __syncthreads();
       if (wid == 0) {
         unsigned kk = st.kk2, digit = 0, pop = 0;
@@ -548,15 +600,13 @@ __device__ void select_smallest(const unsigned* __restrict__ kd, const int* __re
   }
   const bool by_id   = st.need_id != 0;
   const unsigned Tid = st.idprefix;
-  for (int i = tid; i < n; i += blockDim.x) {
-    unsigned k = kd[i];
-    bool take  = k < T || (k == T && (!by_id || static_cast<unsigned>(cid[i]) <= Tid));
-    if (take) {
+  for_keys([&](unsigned k, int i) {
+    if (k < T || (k == T && (!by_id || static_cast<unsigned>(cid[i]) <= Tid))) {
       int s  = atomicAdd(&st.nsel, 1);
       sid[s] = cid[i];
       if (skey) skey[s] = __uint_as_float(k);
     }
-  }
+  });
   __syncthreads();
 }
 
