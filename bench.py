@@ -193,7 +193,7 @@ def time_search(index, Qd, k, params, steps, warmup, torch):
     return (time.perf_counter() - t0) / steps
 
 
-def stage_bytes(name, wave, cnt, m, C, S, D, KO, table_len, starts, w):
+def stage_bytes(name, wave, cnt, m, C, S, D, KO, table_len, starts, w, L):
     """Algorithmic bytes of one launch: every distinct row read once at its natural size (no cache-line inflation)."""
     if name == "gather_lists":
         return m * C * 8 + cnt["entries1"] * 4 + cnt["distinct1"] * (S + 8) + m * (S * 4 + 4)
@@ -203,8 +203,9 @@ def stage_bytes(name, wave, cnt, m, C, S, D, KO, table_len, starts, w):
         return cnt["distinct1"] * 8 + cnt["reranked1"] * 2 * D + m * (12 * KO + 4 * D + 4)
     if name == "rerank_keep_wave":
         return cnt["distinct2"][wave] * 8 + cnt["reranked2"][wave] * 2 * D + m * (24 * KO + 4 * D + 4)
-    if name == "probe":  # Y rows, one offsets pair and one key per (query, copy), the segment out
-        return m * C * (2 * w + 8 + 8 + 8)
+    if name == "probe":  # Y rows and segments out; an offsets pair and a key per level tried (finest first)
+        tried = sum((j + 1) * h for j, h in enumerate(cnt["hit_level"])) + L * (m * C - cnt["seg_hits"])
+        return m * C * (2 * w + 8) + tried * (8 + 8)
     if name == "project":
         return m * D * 2 + C * w * D * 2 + m * C * w * 2
     return None
@@ -227,6 +228,8 @@ def main():
         print("bench.py: this build searches on one GPU; runs on several GPUs are not part of it", file=sys.stderr)
         sys.exit(2)
 
+    # the builder reports its phases on stderr (a 100M build runs for minutes)
+    os.environ.setdefault("OCTEX_VERBOSE", "1")
     import torch
 
     import octex_amd
@@ -290,7 +293,7 @@ def main():
     for name, ms in stages:
         wv = waves_seen.get(name, 0)
         waves_seen[name] = wv + 1
-        b = stage_bytes(name, wv, cnt, len(Q), C, S, D, info["KO"], int(meta[8]), params["starts"], w)
+        b = stage_bytes(name, wv, cnt, len(Q), C, S, D, info["KO"], int(meta[8]), params["starts"], w, int(meta[4]))
         per_launch.append(dict(stage=name, wave=wv, ms=round(ms, 4), bytes=b,
                                gbs=round(b / (ms * 1e-3) / 1e9, 1) if b else None))
         totals[name] = totals.get(name, 0.0) + ms
@@ -299,6 +302,7 @@ def main():
     avg_ms = sum(x["ms"] for x in dl) / len(dl)
     avg_bytes = sum(x["bytes"] for x in dl) / len(dl)
     achieved = avg_bytes / (avg_ms * 1e-3) / 1e9
+    log(f"probe hits by level {cnt['hit_level'][:int(meta[4])]}, misses {len(Q) * C - cnt['seg_hits']}")
     log("stages: " + ", ".join(f"{x['stage']}[{x['wave']}] {x['ms']:.3f} ms {x['gbs']} GB/s" for x in per_launch))
 
     # CPU baseline: the oracle (C++ restatement of the search) on the same index, a bounded query sample

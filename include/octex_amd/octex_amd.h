@@ -38,9 +38,10 @@ cuvsError_t octexBuildInMemory(cuvsResources_t res, cuvsOctexIndexParams_t param
  * Profile one batch of queries [m <= batch, dim] (float32, host or device): a normal search, then the
  * same batch launched kernel by kernel `reps` times with HIP events around every launch on the index's
  * stream.  names (64 x 32 chars) and ms receive the stages in launch order with their average
- * milliseconds, *nstages their count; counters (52 int64, optional): probe hits, list entries read,
+ * milliseconds, *nstages their count; counters (60 int64, optional): probe hits, list entries read,
  * distinct first-round candidates, first-round reranked, then per wave (16 each) valid start points,
- * distinct candidates and reranked entries, all summed over the batch's m rows.
+ * distinct candidates and reranked entries, then probe hits by level (8, the finest first), all
+ * summed over the batch's m rows.
  */
 cuvsError_t octexIndexProfileBatch(cuvsOctexIndex_t index, cuvsOctexSearchParams_t params, DLManagedTensor* queries,
                                    int64_t k, int32_t reps, char* names, double* ms, int32_t* nstages,

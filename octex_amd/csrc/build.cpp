@@ -394,12 +394,13 @@ void searched_table(index_impl& ix, index const& idx, int k, bool reverse_edges,
             o[t] = -1;
         }
       });
-      if ((r0 / chunk + 1) % 16 == 0)
+      if ((r0 / chunk + 1) % 8 == 0)
         build_log("table pass %zu: %lld of %lld rows, %.1f s\n", v + 1, static_cast<long long>(r0 + m),
                   static_cast<long long>(n), seconds_since(t0));
     }
     if (plan[v].waves > 0) drop_table(ix);
     if (reverse_edges) {
+      build_log("table pass %zu: searched in %.1f s, merging reverse edges\n", v + 1, seconds_since(t0));
       merge_reverse(fwd, n, rr, table);
     } else {
       table.assign(static_cast<size_t>(n) * k, -1);

@@ -187,10 +187,13 @@ __global__ __launch_bounds__(256) void e8_kernel(const float* __restrict__ y, in
 // ------------------------------------------------------------------ probe (search_kernels.cuh:84-127)
 
 /**
- * One lane per (query, copy): for levels fine to coarse, the cell id of y * inv_f[j], its bucket,
- * and a scan of the bucket's keys; the first hit gives seg = ((base + p) * l, lr), none (0, 0).
- * The id of level j + 1 is computed while level j's bucket is being read (the hit level is often
- * not the finest, and the loads are dependent HBM round trips).
+ * One lane per (query, copy, level): the levels of a (query, copy) are L neighbouring lanes of one
+ * wavefront (64 / L groups per wavefront, the groups of a wavefront all of one copy), so every
+ * level's cell id, bucket and key lookup run at once instead of one level after another, and a lane
+ * holds one E8^B decode.  A lane computes the cell id of y * inv_f[j], reads its bucket's bounds and
+ * compares the bucket's keys four at a time; a ballot then gives each group its finest level with a
+ * hit, whose lane writes seg = ((base + p) * l, lr); a group without a hit writes (0, 0) from its
+ * level-0 lane.  Every lane reaches the ballot.
  */
 template <int B>
 __global__ __launch_bounds__(256) void probe_kernel(const __half* __restrict__ Y, int m, int C,
@@ -200,40 +203,59 @@ __global__ __launch_bounds__(256) void probe_kernel(const __half* __restrict__ Y
                                                     int64_t Mmax, const int* __restrict__ base,
                                                     int l, int lr, int logT, int2* __restrict__ seg)
 {
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (t >= static_cast<int64_t>(m) * C) return;
-  const int c     = static_cast<int>(t / m);  // a wavefront: 64 queries of one copy, so its offsets and
-  const int64_t u = (t % m) * C + c;          // keys lookups stay inside that copy's tables (few pages)
-  uint4 yv[B];  // the fp16 row, widened per use (fewer registers than 8B floats)
-  const uint4* yp = reinterpret_cast<const uint4*>(Y + u * 8 * B);
+  const int lane = threadIdx.x & 63;
+  const int G    = 64 / L;  // groups per wavefront
+  const int gi = lane / L, j = lane - gi * L;
+  const int64_t wave  = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
+  const int64_t total = static_cast<int64_t>(m) * C;
+  const int64_t g     = wave * G + gi;  // (copy, query) = (g / m, g % m): a wavefront's groups share a copy
+  const bool active   = gi < G && g < total;
+  int c = 0;
+  int64_t u = 0;
+  int hit   = -1;
+  if (active) {
+    c = static_cast<int>(g / m);
+    u = (g % m) * C + c;
+    // E8 blocks one after another (a block's 8 fp16 coordinates are one 16-byte load; the row's
+    // other blocks then come from the same cache line), so that one decode is live at a time
+    const uint4* yp   = reinterpret_cast<const uint4*>(Y + u * 8 * B);
+    const float inv   = inv_f[j];
+    unsigned long long hh = 0;
+#pragma unroll 1
+    for (int jb = 0; jb < B; jb++) {
+      const uint4 w    = yp[jb];
+      const __half* hv = reinterpret_cast<const __half*>(&w);
+      float x[8], pt[8];
 #pragma unroll
-  for (int i = 0; i < B; i++)
-    yv[i] = yp[i];
-  const __half* yh = reinterpret_cast<const __half*>(yv);
-  auto coord       = [&](int i) { return __half2float(yh[i]); };
-  int2 sg              = make_int2(0, 0);
-  const long long mask = (1LL << logT) - 1;
-  long long h          = e8b_hash64_of<B>(coord, inv_f[0]);
-  for (int j = 0; j < L; j++) {
-    const int bk        = static_cast<int>(h & mask);
+      for (int i = 0; i < 8; i++)
+        x[i] = __half2float(hv[i]) * inv;
+      e8_point(x, pt);
+      const unsigned long long hb = block_hash(pt);
+      hh                          = jb == 0 ? hb : hh * kMix + hb;
+    }
+    const long long h   = finish_hash(hh);
+    const int bk        = static_cast<int>(h & ((1LL << logT) - 1));
     const int* o        = off + (static_cast<int64_t>(c) * L + j) * T1 + bk;
     const long long* kk = keys + (static_cast<int64_t>(c) * L + j) * Mmax;
     const int p0 = o[0], p1 = o[1];
-    // the next level's cell id is computed while this level's bucket loads are in flight
-    const long long hn = j + 1 < L ? e8b_hash64_of<B>(coord, inv_f[j + 1]) : 0;
-    int hit = -1;
-    for (int p = p0; p < p1; p++)
-      if (kk[p] == h) {
-        hit = p;
-        break;
-      }
-    if (hit >= 0) {
-      sg = make_int2((base[c * L + j] + hit) * l, lr);
-      break;
+    for (int p = p0; p < p1 && hit < 0; p += 4) {  // keys of the bucket, four loads in flight
+      long long k4[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        k4[i] = kk[min(p + i, p1 - 1)];
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        if (hit < 0 && p + i < p1 && k4[i] == h) hit = p + i;
     }
-    h = hn;
   }
-  seg[u] = sg;
+  const unsigned long long hits = __ballot(hit >= 0);
+  if (!active) return;
+  const unsigned gm = static_cast<unsigned>(hits >> (gi * L)) & (L >= 32 ? ~0u : (1u << L) - 1u);
+  const int fin     = gm != 0 ? __ffs(static_cast<int>(gm)) - 1 : -1;  // the finest level with a hit
+  if (fin >= 0 && j == fin)
+    seg[u] = make_int2((base[c * L + j] + hit) * l, lr);
+  else if (fin < 0 && j == 0)
+    seg[u] = make_int2(0, 0);
 }
 
 // ------------------------------------------------------------------ gather (search_kernels.cuh:138-253)
@@ -975,7 +997,10 @@ void launch_probe(const __half* Y, int m, int C, int L, int B, const float* inv_
   const int64_t tot = static_cast<int64_t>(m) * C;
   if (tot == 0) return;
   OCTEX_EXPECTS(T1 == (int64_t{1} << logT) + 1, "octex: offsets rows must hold 2^log_buckets + 1 entries");
-  auto g = grid_for(tot, 256);
+  OCTEX_EXPECTS(L >= 1 && L <= 32, "octex: the probe takes 1 to 32 spacings");
+  const int G         = 64 / L;  // (query, copy) groups per wavefront
+  const int64_t waves = (tot + G - 1) / G;
+  auto g              = grid_for(waves * 64, 256);
 #define OCTEX_PROBE(b) \
   probe_kernel<b><<<g, 256, 0, s>>>(Y, m, C, L, inv_f, off, T1, keys, Mmax, base, l, lr, logT, seg)
   switch (B) {

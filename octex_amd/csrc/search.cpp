@@ -325,9 +325,18 @@ void profile_batch(index_impl& ix, plan& pl, int reps, std::vector<std::string>&
       const std::string& nm = steps[i].name;
       if (nm == "probe") {
         OCTEX_HIP(hipMemcpy(segh.data(), pl.seg.ptr, sizeof(int2) * m * C, hipMemcpyDeviceToHost));
+        const int L = ix.levels();
+        std::vector<int> base(static_cast<size_t>(C) * L);
+        OCTEX_HIP(hipMemcpy(base.data(), ix.base.ptr, sizeof(int) * base.size(), hipMemcpyDeviceToHost));
         for (int64_t j = 0; j < int64_t{m} * C; j++) {
           cnt.seg_hits += segh[j].y > 0;
           cnt.entries1 += segh[j].y;
+          if (segh[j].y > 0) {  // the level whose rows hold the segment's cell
+            const int* bc = base.data() + (j % C) * L;
+            const int row = segh[j].x / ix.list_len;
+            const int lv  = static_cast<int>(std::upper_bound(bc, bc + L, row) - bc) - 1;
+            cnt.hit_level[std::clamp(lv, 0, 7)]++;
+          }
         }
       } else if (nm == "gather_lists") {
         OCTEX_HIP(hipMemcpy(nin.data(), pl.nin.ptr, sizeof(int) * m, hipMemcpyDeviceToHost));

@@ -39,6 +39,7 @@ void run_batch(index_impl const& ix, plan const& pl, hipStream_t s);
 struct profile_counters {
   int64_t seg_hits = 0, entries1 = 0, distinct1 = 0, reranked1 = 0;
   int64_t starts2[16] = {}, distinct2[16] = {}, reranked2[16] = {};
+  int64_t hit_level[8] = {};  // probe hits by level (0 the finest); misses are m C - seg_hits
 };
 void profile_batch(index_impl& ix, plan& pl, int reps, std::vector<std::string>& names, std::vector<double>& ms,
                    profile_counters& cnt);

@@ -285,14 +285,14 @@ class Index:
         names = ct.create_string_buffer(64 * 32)
         ms = (ct.c_double * 64)()
         ns = ct.c_int32(0)
-        cnt = (ct.c_int64 * 52)()
+        cnt = (ct.c_int64 * 60)()
         _lib.call("octexIndexProfileBatch", self._handle, ct.byref(p), dq.ptr, ct.c_int64(k), ct.c_int32(reps), names,
                   ms, ct.byref(ns), cnt)
         raw = names.raw
         stages = [(raw[32 * i : 32 * i + 32].split(b"\0")[0].decode(), ms[i]) for i in range(ns.value)]
         c = list(cnt)
         counters = dict(seg_hits=c[0], entries1=c[1], distinct1=c[2], reranked1=c[3], starts2=c[4:20],
-                        distinct2=c[20:36], reranked2=c[36:52])
+                        distinct2=c[20:36], reranked2=c[36:52], hit_level=c[52:60])
         return stages, counters
 
     def plan_info(self):

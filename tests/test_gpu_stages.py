@@ -182,6 +182,28 @@ def test_probe_matches_oracle(L, ix, dix, small_index):
     assert (ref[:200, :, 1] > 0).mean() > 0.9 and (ref[200:, :, 1] == 0).mean() > 0.5
 
 
+@pytest.mark.parametrize("blocks,spacings,log_buckets,min_cell", [
+    (2, [1.5, 2.0, 2.5, 3.2, 4.0, 5.0, 6.5], 4, 3),  # 7 levels, 16 buckets: many keys per bucket
+    (3, [2.5], 6, 1),                                # one level
+    (1, [1.0, 1.4, 2.0, 2.8, 4.0, 5.6, 8.0, 11.0, 16.0, 22.0, 32.0], 8, 4),  # 11 levels: 5 groups per wavefront
+])
+def test_probe_level_and_bucket_shapes(L, tmp_path, blocks, spacings, log_buckets, min_cell):
+    X, _ = clustered(n=1500, m=10, d=32, clusters=8, seed=11)
+    path = str(tmp_path / "probe")
+    O.build(X, path, copies=6, blocks=blocks, pca_dims=32, spacings=spacings, list_len=8, table_len=0,
+            log_buckets=log_buckets, min_cell=min_cell, member_lists=True, seed=4)
+    pix = O.Index(path)
+    pdix = dict(inv_f=dev(pix.inv_f), offsets=dev(pix.offsets), keys=dev(pix.keys), base=dev(pix.base))
+    Y = queries_Y(pix, X[:300], extra_random=100)
+    seg = run_probe(L, pix, pdix, Y, pix.list_len)
+    ref = O.probe(pix, Y, read=pix.list_len)
+    assert np.array_equal(host(seg), ref)
+    rows = ref[:, :, 0] // pix.list_len
+    levels = (rows[..., None] >= pix.base.reshape(1, pix.copies, -1)).sum(-1) - 1
+    hit = ref[:, :, 1] > 0
+    assert hit.mean() > 0.3 and (len(spacings) == 1 or len(np.unique(levels[hit])) > 1)  # hits at several levels
+
+
 def gather_gpu(L, ix, dix, seg, qs, rows, W=4096):
     m, nseg = seg.shape[0], seg.shape[1]
     cand = torch.full((m, W), -5, dtype=torch.int32, device="cuda")
