@@ -219,6 +219,9 @@ def main():
     ap.add_argument("--config", default="deep100m", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU time of the CPU-baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also copy 1 GiB device to device inside the profiled region (the known-size kernel that "
+                         "scales rocprof's FETCH_SIZE / WRITE_SIZE counters to bytes)")
     ap.add_argument("--params", default=None, help="JSON search parameters (skips the sweep)")
     ap.add_argument("--save-index", default=None, help="also write the built index directory here")
     ap.add_argument("--load-index", default=None, help="load this index directory instead of building one")
@@ -282,6 +285,14 @@ def main():
     with ProfilerRegion():
         sec = time_search(index, Qd, k, params, steps=args.steps, warmup=args.warmup, torch=torch)
         stages, cnt = index.profile_batch(Qd, k=k, reps=5, **params)
+        if args.copy_calibration:  # 1 GiB read + 1 GiB written by one elementwise copy kernel
+            src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+            dst = torch.empty_like(src)
+            torch.cuda.synchronize()
+            dst.copy_(src)
+            torch.cuda.synchronize()
+            log("calibration copy: 1073741824 bytes read, 1073741824 bytes written")
+            del src, dst
     qps = len(Q) / sec
     D_, I_ = index.search(Qd, k=k, **params)
     rec = recall(I_.cpu().numpy(), gt)

@@ -40,12 +40,13 @@ __device__ __forceinline__ void d8(const float (&x)[8], float (&f)[8])
       ei = e;
     }
   }
-  if (fmodf(s, 2.f) != 0.f) {
-    const float step = ei >= 0.f ? 1.f : -1.f;
+  // fmodf(s, 2) != 0, with the integer parity for |s| < 2^24 (every such s here is an integer, and fmodf's
+  // general reduction loop is costly); larger, infinite or NaN sums take fmodf itself
+  const bool odd   = fabsf(s) < 16777216.f ? (static_cast<int>(s) & 1) != 0 : fmodf(s, 2.f) != 0.f;
+  const float step = ei >= 0.f ? 1.f : -1.f;
 #pragma unroll
-    for (int i = 0; i < 8; i++)
-      if (i == im) f[i] = f[i] + step;
-  }
+  for (int i = 0; i < 8; i++)  // selects, not branches: the fixed coordinate differs between lanes
+    f[i] = (odd && i == im) ? f[i] + step : f[i];
 }
 
 /** Nearest point of E8 = D8 u (D8 + 1/2): the nearer of the two cosets' points (ties: D8). */
@@ -72,14 +73,30 @@ __device__ __forceinline__ void e8_point(const float (&x)[8], float (&p)[8])
     p[i] = useA ? a[i] : c[i];
 }
 
-/** Block hash: sum of 2 p_i times the i-th prime (64-bit wraparound). */
+/**
+ * Block hash: sum of 2 p_i times the i-th prime (64-bit wraparound).  2 p_i is converted to int64 as a
+ * 32-bit conversion sign-extended when every |2 p_i| < 2^31 (the same integer, and the float-to-int64
+ * conversion has no single instruction); otherwise by the int64 conversion itself.
+ */
 __device__ __forceinline__ unsigned long long block_hash(const float (&p)[8])
 {
-  unsigned long long hb = 0;
+  float amax = 0.f;
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
-    long long p2 = static_cast<long long>(2.f * p[i]);
-    hb += static_cast<unsigned long long>(p2) * static_cast<unsigned long long>(kPrimes[i]);
+  for (int i = 0; i < 8; i++)
+    amax = fmaxf(amax, fabsf(2.f * p[i]));
+  unsigned long long hb = 0;
+  if (amax < 2147483648.f) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const long long p2 = static_cast<long long>(static_cast<int>(2.f * p[i]));
+      hb += static_cast<unsigned long long>(p2) * static_cast<unsigned long long>(kPrimes[i]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const long long p2 = static_cast<long long>(2.f * p[i]);
+      hb += static_cast<unsigned long long>(p2) * static_cast<unsigned long long>(kPrimes[i]);
+    }
   }
   return hb;
 }

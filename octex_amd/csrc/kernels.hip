@@ -4,8 +4,8 @@
 //
 // Arithmetic pins shared with the CPU oracle: E8 distances t = x - a, acc = fma(t, t, acc); the
 // sketch score u = fma(code, scale, -qs), d = fma(u, u, d) over Lr-lane chunks then an xor butterfly;
-// the exact distance over 64 lanes (pairs l, l + 64, ...), acc = fma(a, a, acc), fma(b, b, acc), then
-// an xor butterfly; selections by (distance bits, id).  Built with -ffp-contract=off so that no other
+// the exact distance over LX-lane groups (8-element chunks sub, sub + LX, ...), acc = fma(t, t, acc),
+// then an xor butterfly; selections by (distance bits, id).  Built with -ffp-contract=off so that no other
 // operation is contracted.
 
 #include "common.hpp"
@@ -270,16 +270,19 @@ __device__ __forceinline__ int hash_log_dev(int total, int log_cap)
 }
 
 /**
- * Sketch scores of the candidates crow[0, n) of one query (search_kernels.cuh:227-251): an LR-lane
+ * Sketch scores of the candidates ht[cl[0, n)] (LDS: the hash-set slots of the query's distinct ids in
+ * the order they were added) of one query (search_kernels.cuh:227-251): an LR-lane
  * group (LR = the next power of two >= S / 16, at most 32) scores a candidate, lane `sub` reducing the
  * 16-element chunks sub, sub + LR, ... as u = fma(code, scale, -qs), d = fma(u, u, d), then an xor
- * butterfly over the group.  A candidate's row is read by one load instruction of its group (one
- * address translation per row: rows lie anywhere in a sketch of many GB), and every group has kRows
- * candidates' loads in flight before it computes.
+ * butterfly over the group; the group's lane 0 writes the id and its score to crow / drow.  A
+ * candidate's row is read by one load instruction of its group (one address translation per row: rows
+ * lie anywhere in a sketch of many GB), and every group has kRows candidates' loads in flight before it
+ * computes.
  */
 template <int LR>
-__device__ __forceinline__ void sketch_scores(const int* crow, int n, const signed char* __restrict__ code,
-                                              int S, int pitch, const float* qv, const float* sc, float* drow)
+__device__ __forceinline__ void sketch_scores(const unsigned short* cl, const int* ht, int n,
+                                              const signed char* __restrict__ code, int S, int pitch,
+                                              const float2* sq, int* crow, float* drow)
 {
   constexpr int kRows = 4;        // candidates per group in flight
   constexpr int GPW   = 64 / LR;  // groups per wavefront
@@ -290,8 +293,9 @@ __device__ __forceinline__ void sketch_scores(const int* crow, int n, const sign
   float s16[16], q16[16];         // the chunk's scale and query sketch, held in registers
 #pragma unroll
   for (int e = 0; e < 16; e++) {
-    s16[e] = has ? sc[k + e] : 0.f;
-    q16[e] = has ? qv[k + e] : 0.f;
+    const float2 v = has ? sq[k + e] : make_float2(0.f, 0.f);
+    s16[e]         = v.x;
+    q16[e]         = v.y;
   }
   const int per_wave = GPW * kRows;
   // Loads are unconditional (past-the-end candidates read the last one, chunkless lanes chunk 0) so
@@ -300,7 +304,7 @@ __device__ __forceinline__ void sketch_scores(const int* crow, int n, const sign
     int id[kRows];
 #pragma unroll
     for (int r = 0; r < kRows; r++)  // candidate j0 + r * GPW + grp
-      id[r] = crow[min(j0 + r * GPW + grp, n - 1)];
+      id[r] = ht[cl[min(j0 + r * GPW + grp, n - 1)]];
     int4 w[kRows];
 #pragma unroll
     for (int r = 0; r < kRows; r++)
@@ -315,98 +319,123 @@ __device__ __forceinline__ void sketch_scores(const int* crow, int n, const sign
         float u = fmaf(static_cast<float>(bb[e]), s16[e], -q16[e]);
         acc     = fmaf(u, u, acc);
       }
-      d[r] = has ? acc : 0.f;
+      d[r] = acc;
     }
 #pragma unroll
     for (int r = 0; r < kRows; r++) {
+      if (!has) d[r] = 0.f;
 #pragma unroll
       for (int o = LR >> 1; o; o >>= 1)
         d[r] += __shfl_xor(d[r], o);
       const int j = j0 + r * GPW + grp;
-      if (j < n && sub == 0) drow[j] = d[r];
+      if (j < n && sub == 0) {
+        crow[j] = id[r];
+        drow[j] = d[r];
+      }
     }
   }
 }
 
 /**
- * Distinct ids of all segments of a query with their sketch scores.  The entries of all segments are
- * split evenly over the workgroup (exclusive prefix of the segment lengths, binary search per entry),
- * kUnroll entries per thread with their loads issued together; an LDS open-addressing set drops
- * duplicates; new ids are appended to the query's candidate row by one atomic per wavefront.  Then the
- * candidates are scored (sketch_scores; LR = the reference's lanes per candidate for this S).
+ * Distinct ids of all segments of a query with their sketch scores.  Wavefront 0 compacts the
+ * non-empty segments (entry pointer and exclusive prefix of the lengths) into LDS; the entries are then
+ * split evenly over the workgroup, kUnroll per thread with their loads issued together (entry i of a
+ * query whose non-empty segments all have one length len lies in segment i / len, otherwise a binary
+ * search over the prefix finds it); an LDS open-addressing set drops duplicates and the slots of new ids
+ * are appended to an LDS candidate list (16-bit slot numbers) by one atomic per wavefront.  Then the candidates are scored
+ * (sketch_scores; LR = the reference's lanes per candidate for this S) and written with their scores.
  *
- * kRows = false: segment c = (first entry, length) in the lists of copy c (row stride `stride`).
+ * kRows = false: segment c = (first entry, length) in the lists of copy c (at list_ptr[c]).
  * kRows = true:  segment = (row, length) of the neighbor table [N, table_len]; -1 entries skipped.
+ * The candidate list holds cap = min(W, nseg * max_len) ids (max_len: the longest segment).
  */
 template <bool kRows, int LR>
 __global__ __launch_bounds__(kGatherThreads) void gather_kernel(
   const int2* __restrict__ seg, int nseg, const long long* __restrict__ list_ptr,
   const int* __restrict__ table, int table_len, int64_t N, const signed char* __restrict__ code,
-  const float* __restrict__ scale, const float* __restrict__ qs, int S, int pitch, int W, int logW,
+  const float* __restrict__ scale, const float* __restrict__ qs, int S, int pitch, int W, int logW, int cap,
   int* __restrict__ cand, float* __restrict__ dist, int* __restrict__ nout)
 {
   constexpr int kUnroll = 4;
   const int q = blockIdx.x;
   extern __shared__ long long smq[];
-  const int** lp = reinterpret_cast<const int**>(smq);  // [nseg] list of every copy (lists only)
-  float* qv      = reinterpret_cast<float*>(smq + nseg);
-  float* sc      = qv + S;
-  int* pre       = reinterpret_cast<int*>(sc + S);  // [nseg + 1] exclusive prefix
-  int* st        = pre + nseg + 1;                  // [nseg] segment starts
-  int* ht        = st + nseg;                       // hash set
-  __shared__ int cnt;
+  const int** sp = reinterpret_cast<const int**>(smq);  // [nseg] first entry of every non-empty segment
+  float2* sq     = reinterpret_cast<float2*>(smq + nseg);  // [S] (scale, query sketch) per coordinate
+  int* pre       = reinterpret_cast<int*>(sq + S);  // [nseg + 1] exclusive prefix of the compacted lengths
+  int* ht        = pre + nseg + 1;                  // [W] hash set
+  auto* cl       = reinterpret_cast<unsigned short*>(ht + W);  // [cap] slots of the candidates
+  __shared__ int cnt, nsp, ulen;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   for (int i = tid; i < S; i += blockDim.x) {
-    qv[i] = qs[static_cast<int64_t>(q) * S + i];
-    sc[i] = scale[i];
+    sq[i] = make_float2(scale[i], qs[static_cast<int64_t>(q) * S + i]);
   }
   if (tid == 0) cnt = 0;
   if (wid == 0) {
-    int carry = 0;
+    int carry = 0, at = 0, lmin = 0x7fffffff, lmax = 0;
     for (int c0 = 0; c0 < nseg; c0 += 64) {
       const int c = c0 + lane;
       int2 sl     = c < nseg ? seg[static_cast<int64_t>(q) * nseg + c] : make_int2(0, 0);
-      int v       = sl.y;
+      if (sl.y < 0) sl.y = 0;
+      const bool keep               = sl.y > 0;
+      const unsigned long long mask = __ballot(keep);
+      const int o                   = at + __popcll(mask & ((1ULL << lane) - 1ULL));
+      int v                         = sl.y;
 #pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        int u = __shfl_up(v, o);
-        if (lane >= o) v += u;
+      for (int d = 1; d < 64; d <<= 1) {
+        int u = __shfl_up(v, d);
+        if (lane >= d) v += u;
       }
-      if (c < nseg) {
-        pre[c] = carry + v - sl.y;
-        st[c]  = sl.x;
-        if constexpr (!kRows) lp[c] = reinterpret_cast<const int*>(list_ptr[c]);
+      if (keep) {
+        pre[o] = carry + v - sl.y;
+        if constexpr (kRows)
+          sp[o] = table + static_cast<int64_t>(sl.x) * table_len;
+        else
+          sp[o] = reinterpret_cast<const int*>(list_ptr[c]) + sl.x;
+        lmin = min(lmin, sl.y);
+        lmax = max(lmax, sl.y);
       }
       carry += __shfl(v, 63);
+      at += __popcll(mask);
     }
-    if (lane == 0) pre[nseg] = carry;
+#pragma unroll
+    for (int d = 32; d; d >>= 1) {
+      lmin = min(lmin, __shfl_xor(lmin, d));
+      lmax = max(lmax, __shfl_xor(lmax, d));
+    }
+    if (lane == 0) {
+      pre[at] = carry;
+      nsp     = at;
+      ulen    = at > 0 && lmin == lmax ? lmax : 0;  // one length for every non-empty segment
+    }
   }
   __syncthreads();
-  const int total = pre[nseg];
+  const int ns = nsp, len = ulen;
+  const int total = pre[ns];
   const int HT    = 1 << hash_log_dev(total, logW);
   for (int i = tid; i < HT; i += blockDim.x)
     ht[i] = -1;
   __syncthreads();
-  int* crow = cand + static_cast<int64_t>(q) * W;
   const int step = blockDim.x;
   for (int i0 = 0; i0 < total; i0 += step * kUnroll) {
     int v[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; u++) {  // kUnroll entries' loads issued together (past the end: the last)
       const int i = min(i0 + u * step + tid, total - 1);
-      int lo = 0, hi = nseg - 1;
-      while (lo < hi) {
-        int mid = (lo + hi + 1) >> 1;
-        if (pre[mid] <= i)
-          lo = mid;
-        else
-          hi = mid - 1;
-      }
-      if constexpr (kRows) {
-        v[u] = table[static_cast<int64_t>(st[lo]) * table_len + (i - pre[lo])];
+      int sg;
+      if (len > 0) {
+        sg = i / len;
       } else {
-        v[u] = lp[lo][st[lo] + (i - pre[lo])];
+        int lo = 0, hi = ns - 1;
+        while (lo < hi) {
+          int mid = (lo + hi + 1) >> 1;
+          if (pre[mid] <= i)
+            lo = mid;
+          else
+            hi = mid - 1;
+        }
+        sg = lo;
       }
+      v[u] = sp[sg][i - pre[sg]];
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; u++)
@@ -414,8 +443,9 @@ __global__ __launch_bounds__(kGatherThreads) void gather_kernel(
 #pragma unroll
     for (int u = 0; u < kUnroll; u++) {
       bool fresh = false;
+      unsigned h = 0;
       if (v[u] >= 0 && v[u] < N) {  // -1: padding of a table row (search_kernels.cuh:213)
-        unsigned h = (static_cast<unsigned>(v[u]) * kIdHash) & (HT - 1);
+        h = (static_cast<unsigned>(v[u]) * kIdHash) & (HT - 1);
         for (int p = 0; p < HT; p++) {
           int prev = atomicCAS(&ht[h], -1, v[u]);
           if (prev == -1) {
@@ -434,14 +464,15 @@ __global__ __launch_bounds__(kGatherThreads) void gather_kernel(
         at = __shfl(at, leader);
         if (fresh) {
           int slot = at + __popcll(mask & ((1ULL << lane) - 1ULL));
-          if (slot < W) crow[slot] = v[u];
+          if (slot < cap) cl[slot] = static_cast<unsigned short>(h);
         }
       }
     }
   }
   __syncthreads();
-  const int n = min(cnt, W);
-  sketch_scores<LR>(crow, n, code, S, pitch, qv, sc, dist + static_cast<int64_t>(q) * W);
+  const int n = min(cnt, cap);
+  sketch_scores<LR>(cl, ht, n, code, S, pitch, sq, cand + static_cast<int64_t>(q) * W,
+                    dist + static_cast<int64_t>(q) * W);
   if (tid == 0) nout[q] = n;
 }
 
@@ -633,46 +664,67 @@ __device__ void select_smallest(const unsigned* __restrict__ kd, const int* __re
 }
 
 /**
- * Squared distances of the fp16 rows sid[0, ns) to the fp32 query sq (search_kernels.cuh:325-342): a
- * wavefront scores a row, lane l taking the half2 pairs l, l + 64, ... (acc = fma(a, a, acc),
- * fma(b, b, acc)), then a 64-lane xor butterfly.  A row is read by one load instruction (one address
- * translation for a row anywhere in many GB of vectors) and every wavefront has kRows rows in flight.
+ * Squared distances of the fp16 rows sid[0, ns) to the fp32 query sq (search_kernels.cuh:325-342 with
+ * another lane split): an LX-lane group scores a row (LX = the next power of two >= D / 8, at most
+ * 32), lane sub reducing the 8-element chunks sub, sub + LX, ... in order as t = x - q,
+ * acc = fma(t, t, acc), then an xor butterfly over the group.  A chunk is one 16-byte load when rows are
+ * 16-byte aligned (D a multiple of 8), and every group has kRows rows in flight.
  */
-__device__ void exact_distances(const int* sid, int ns, const __half* __restrict__ vectors, int D,
-                                const float* sq, float* sd)
+template <int LX>
+__device__ void exact_distances_t(const int* sid, int ns, const __half* __restrict__ vectors, int D,
+                                  const float* sq, float* sd)
 {
-  constexpr int kRows = 8;
+  constexpr int kRows = 4, GPW = 64 / LX;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  const int P = D / 2;
-  for (int j0 = wid * kRows; j0 < ns; j0 += nw * kRows) {
-    const __half2* x[kRows];
+  const int sub = lane & (LX - 1), grp = lane / LX;
+  const int nch = (D + 7) / 8;
+  const bool vec = (D & 7) == 0;
+  for (int j0 = wid * GPW * kRows; j0 < ns; j0 += nw * GPW * kRows) {
+    const __half* x[kRows];
     float acc[kRows];
 #pragma unroll
     for (int r = 0; r < kRows; r++) {  // past-the-end rows read the last row (results dropped)
       acc[r] = 0.f;
-      x[r]   = reinterpret_cast<const __half2*>(vectors + static_cast<int64_t>(sid[min(j0 + r, ns - 1)]) * D);
+      x[r]   = vectors + static_cast<int64_t>(sid[min(j0 + r * GPW + grp, ns - 1)]) * D;
     }
-    for (int k = lane; k < P; k += 64) {
-      __half2 h[kRows];
+    for (int c = sub; c < nch; c += LX) {
+      const int k0 = 8 * c;
+      uint4 w[kRows];
 #pragma unroll
-      for (int r = 0; r < kRows; r++)  // every row's pair first
-        h[r] = x[r][k];
-      const float q0 = sq[2 * k], q1 = sq[2 * k + 1];
+      for (int r = 0; r < kRows; r++) {  // every row's chunk first
+        if (vec) {
+          w[r] = *reinterpret_cast<const uint4*>(x[r] + k0);
+        } else {
+          __half h[8];
+#pragma unroll
+          for (int e = 0; e < 8; e++)
+            h[e] = k0 + e < D ? x[r][k0 + e] : __float2half(0.f);
+          w[r] = *reinterpret_cast<const uint4*>(h);
+        }
+      }
+      float qk[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++)
+        qk[e] = k0 + e < D ? sq[k0 + e] : 0.f;
 #pragma unroll
       for (int r = 0; r < kRows; r++) {
-        float2 v = __half22float2(h[r]);
-        float a  = v.x - q0;
-        float b  = v.y - q1;
-        acc[r]   = fmaf(a, a, acc[r]);
-        acc[r]   = fmaf(b, b, acc[r]);
+        const __half* h = reinterpret_cast<const __half*>(&w[r]);
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          if (k0 + e < D) {
+            const float t = __half2float(h[e]) - qk[e];
+            acc[r]        = fmaf(t, t, acc[r]);
+          }
+        }
       }
     }
 #pragma unroll
     for (int r = 0; r < kRows; r++) {
 #pragma unroll
-      for (int o = 32; o; o >>= 1)
+      for (int o = LX >> 1; o; o >>= 1)
         acc[r] += __shfl_xor(acc[r], o);
-      if (lane == 0 && j0 + r < ns) sd[j0 + r] = acc[r];
+      const int j = j0 + r * GPW + grp;
+      if (sub == 0 && j < ns) sd[j] = acc[r];
     }
   }
   __syncthreads();
@@ -751,6 +803,7 @@ __device__ void store_keys(const uint64_t* key, int P, int KO, long long* pb, fl
  * Exact rerank of the R sketch-nearest candidates of a query, merged into its kept list of the best
  * KO (search_kernels.cuh:421-467).  fresh: the kept list starts empty.
  */
+template <int LX>
 __global__ __launch_bounds__(kKeepThreads) void rerank_keep_kernel(
   const int* __restrict__ cand, const float* __restrict__ dist, const int* __restrict__ nin, int W,
   const __half* __restrict__ vectors, int D, const float* __restrict__ Q, int R, int KO,
@@ -769,7 +822,7 @@ __global__ __launch_bounds__(kKeepThreads) void rerank_keep_kernel(
   select_smallest(reinterpret_cast<const unsigned*>(dist + static_cast<int64_t>(q) * W),
                   cand + static_cast<int64_t>(q) * W, n, R, sid, nullptr, hist, st);
   const int ns = st.nsel;
-  exact_distances(sid, ns, vectors, D, sq, sd);
+  exact_distances_t<LX>(sid, ns, vectors, D, sq, sd);
   long long* pb = bi + static_cast<int64_t>(q) * KO;
   float* pd     = bd + static_cast<int64_t>(q) * KO;
   int P         = 2;
@@ -876,6 +929,7 @@ __global__ __launch_bounds__(256) void pick_starts_kernel(const long long* __res
 }
 
 /** Exact rerank of the first R kept entries (sketch-rank mode) into the best k (:634-669). */
+template <int LX>
 __global__ __launch_bounds__(kKeepThreads) void final_rerank_kernel(
   const long long* __restrict__ si, int KO, int R, const __half* __restrict__ vectors, int D,
   const float* __restrict__ Q, int k, long long* __restrict__ bi, float* __restrict__ bd)
@@ -903,7 +957,7 @@ __global__ __launch_bounds__(kKeepThreads) void final_rerank_kernel(
   }
   __syncthreads();
   const int ns = nsel;
-  exact_distances(sid, ns, vectors, D, sq, sd);
+  exact_distances_t<LX>(sid, ns, vectors, D, sq, sd);
   int P = 2;
   while (P < R)
     P <<= 1;
@@ -934,6 +988,28 @@ __global__ void copy_ranges_kernel(const uint32_t* __restrict__ src, const int64
 }  // namespace
 
 // ================================================================== launchers
+
+namespace {
+
+/** f(std::integral_constant<int, LX>) with LX = the exact-distance lanes per row for dimension D. */
+template <typename F>
+void with_lx(int D, F&& f)
+{
+  const int nch = (D + 7) / 8;
+  int lx        = 1;
+  while (lx < nch && lx < 32)
+    lx <<= 1;
+  switch (lx) {
+    case 1: f(std::integral_constant<int, 1>{}); break;
+    case 2: f(std::integral_constant<int, 2>{}); break;
+    case 4: f(std::integral_constant<int, 4>{}); break;
+    case 8: f(std::integral_constant<int, 8>{}); break;
+    case 16: f(std::integral_constant<int, 16>{}); break;
+    default: f(std::integral_constant<int, 32>{}); break;
+  }
+}
+
+}  // namespace
 
 void launch_center(const float* q, const float* mu, int64_t m, int D, float* qc, __half* qh,
                    hipStream_t s)
@@ -1017,13 +1093,18 @@ void launch_probe(const __half* Y, int m, int C, int L, int B, const float* inv_
   OCTEX_HIP(hipGetLastError());
 }
 
-auto gather_smem(int W, int S, int nseg) -> size_t
+auto gather_cap(int W, int nseg, int max_len) -> int
 {
-  return static_cast<size_t>(nseg) * sizeof(long long) +
-         static_cast<size_t>(W + 2 * S + 2 * nseg + 1) * sizeof(int);
+  return static_cast<int>(std::min<int64_t>(W, static_cast<int64_t>(nseg) * std::max(max_len, 1)));
 }
 
-void launch_gather(bool rows, const int2* seg, int nseg, int m, const long long* list_ptr,
+auto gather_smem(int W, int S, int nseg, int max_len) -> size_t
+{
+  return static_cast<size_t>(nseg) * sizeof(long long) + static_cast<size_t>(W + 2 * S + nseg + 1) * sizeof(int) +
+         static_cast<size_t>(gather_cap(W, nseg, max_len)) * sizeof(unsigned short);
+}
+
+void launch_gather(bool rows, const int2* seg, int nseg, int max_len, int m, const long long* list_ptr,
                    const int* table, int table_len, int64_t n, const signed char* code, int pitch,
                    const float* scale, const float* qs, int S, int W, int logW, int* cand, float* dist,
                    int* nout, hipStream_t s)
@@ -1031,10 +1112,12 @@ void launch_gather(bool rows, const int2* seg, int nseg, int m, const long long*
   OCTEX_EXPECTS(pitch >= S && pitch % 16 == 0, "octex: sketch rows are at least S bytes apart, 16-byte aligned");
   if (m == 0) return;
   OCTEX_EXPECTS(nseg >= 1, "octex: a gather needs at least one segment per query");
+  OCTEX_EXPECTS(max_len >= 0, "octex: segment lengths are non-negative");
   OCTEX_EXPECTS(W == (1 << logW) && W <= kMaxHash, "octex: hash set size");
   OCTEX_EXPECTS(S % 16 == 0 && S >= 16 && S <= 512, "octex: sketch width: a multiple of 16, <= 512");
-  const size_t smem = gather_smem(W, S, nseg);
+  const size_t smem = gather_smem(W, S, nseg, max_len);
   OCTEX_EXPECTS(smem <= 160 * 1024, "octex: gather needs %zu bytes of LDS (max 160 KiB)", smem);
+  const int cap = gather_cap(W, nseg, max_len);
   int Lr = 1;  // the reference's lanes per candidate: the next power of two >= S / 16, at most 32
   while (Lr < S / 16 && Lr < 32)
     Lr <<= 1;
@@ -1044,7 +1127,7 @@ void launch_gather(bool rows, const int2* seg, int nseg, int m, const long long*
     OCTEX_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gather_kernel<R, LR>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
     gather_kernel<R, LR><<<m, kGatherThreads, smem, s>>>(seg, nseg, list_ptr, table, table_len, n, code, scale,
-                                                          qs, S, pitch, W, logW, cand, dist, nout);
+                                                          qs, S, pitch, W, logW, cap, cand, dist, nout);
   };
   auto by_lr = [&](auto rows_tag) {
     switch (Lr) {
@@ -1071,8 +1154,10 @@ void launch_rerank_keep(const int* cand, const float* dist, const int* nin, int 
   OCTEX_EXPECTS(R >= 1 && R <= kMaxRerank && KO + R <= kMaxKeepSort && KO >= 1,
                 "octex: rerank in [1, 512] and max(starts, k) + rerank <= 1024");
   OCTEX_EXPECTS(D % 2 == 0, "octex: the dimension must be even");
-  rerank_keep_kernel<<<m, kKeepThreads, D * sizeof(float), s>>>(cand, dist, nin, W, vectors, D, Q, R, KO, si, sd,
-                                                                fresh);
+  with_lx(D, [&](auto lx) {
+    rerank_keep_kernel<decltype(lx)::value>
+      <<<m, kKeepThreads, D * sizeof(float), s>>>(cand, dist, nin, W, vectors, D, Q, R, KO, si, sd, fresh);
+  });
   OCTEX_HIP(hipGetLastError());
 }
 
@@ -1101,7 +1186,10 @@ void launch_final_rerank(const long long* si, int m, int KO, int R, const __half
   if (m == 0) return;
   OCTEX_EXPECTS(R >= k && R <= kMaxRerank && R <= KO,
                 "octex: final_rerank 0 (sketch order) or k <= final_rerank <= 512");
-  final_rerank_kernel<<<m, kKeepThreads, D * sizeof(float), s>>>(si, KO, R, vectors, D, Q, k, bi, bd);
+  with_lx(D, [&](auto lx) {
+    final_rerank_kernel<decltype(lx)::value><<<m, kKeepThreads, D * sizeof(float), s>>>(si, KO, R, vectors, D, Q, k,
+                                                                                        bi, bd);
+  });
   OCTEX_HIP(hipGetLastError());
 }
 

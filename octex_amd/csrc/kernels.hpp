@@ -18,7 +18,7 @@ constexpr int kMaxKeepSort    = 1024;   // kept + reranked keys sorted together
 constexpr int kMaxSketchKO    = 1024;   // kept entries of the sketch merge
 constexpr int kPickHash       = 8192;   // hash set of the expanded start points
 constexpr int kMaxExpanded    = 6144;   // start points expanded by earlier waves
-constexpr int kGatherThreads  = 256;
+constexpr int kGatherThreads  = 512;
 constexpr int kKeepThreads    = 256;
 
 /** log2 of the hash set of a query reading `total` entries: ceil(log2(1.5 total)) in [11, log_cap]. */
@@ -47,11 +47,12 @@ void launch_probe(const __half* Y, int m, int C, int L, int B, const float* inv_
                   int64_t T1, const long long* keys, int64_t Mmax, const int* base, int l, int lr,
                   int logT, int2* seg, hipStream_t s);
 /** LDS bytes of a gather over `nseg` segments per query with hash sets up to W slots. */
-auto gather_smem(int W, int S, int nseg) -> size_t;
+auto gather_smem(int W, int S, int nseg, int max_len) -> size_t;
 /** Ids at or above `n` (a corrupt list or table entry) are skipped like the -1 padding. */
 /** Lists: segment c of a query reads copy c's lists at list_ptr[c] (a device pointer per copy). */
 /** code [n, pitch]: the S sketch codes of row v start at code + v * pitch. */
-void launch_gather(bool rows, const int2* seg, int nseg, int m, const long long* list_ptr,
+/** max_len: no segment is longer (a query keeps at most min(W, nseg * max_len) candidates). */
+void launch_gather(bool rows, const int2* seg, int nseg, int max_len, int m, const long long* list_ptr,
                    const int* table, int table_len, int64_t n, const signed char* code, int pitch,
                    const float* scale, const float* qs, int S, int W, int logW, int* cand, float* dist,
                    int* nout, hipStream_t s);

@@ -78,7 +78,7 @@ auto batch_stages(index_impl const& ix, plan const& pl, hipStream_t s) -> std::v
                  pl.seg.as<int2>(), s);
   });
   add("gather_lists", [&ix, &pl, s, m, S, C] {
-    launch_gather(false, pl.seg.as<int2>(), C, m, ix.list_ptr.as<long long>(), nullptr, 0, ix.n, ix.code(),
+    launch_gather(false, pl.seg.as<int2>(), C, pl.lr, m, ix.list_ptr.as<long long>(), nullptr, 0, ix.n, ix.code(),
                   ix.sketch_pitch, ix.scale.as<float>(), pl.qs.as<float>(), S, pl.W, pl.logW, pl.cand.as<int>(), pl.dist.as<float>(),
                   pl.nin.as<int>(), s);
   });
@@ -99,7 +99,7 @@ auto batch_stages(index_impl const& ix, plan const& pl, hipStream_t s) -> std::v
                          ix.table_len, pl.seg2.as<int2>(), s);
     });
     add("gather_rows", [&ix, &pl, s, m, S, st] {
-      launch_gather(true, pl.seg2.as<int2>(), st, m, nullptr, ix.rows(), ix.table_len, ix.n, ix.code(),
+      launch_gather(true, pl.seg2.as<int2>(), st, ix.table_len, m, nullptr, ix.rows(), ix.table_len, ix.n, ix.code(),
                     ix.sketch_pitch, ix.scale.as<float>(), pl.qs.as<float>(), S, pl.W2, pl.logW2, pl.cand2.as<int>(),
                     pl.dist2.as<float>(), pl.n2.as<int>(), s);
     });

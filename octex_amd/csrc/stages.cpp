@@ -113,7 +113,14 @@ extern "C" cuvsError_t octexStageGather(int32_t rows, const int32_t* seg, int32_
       ptrs = dbuf(hp.size() * sizeof(long long));
       upload(ptrs.ptr, hp.data(), ptrs.size, s);
     }
-    launch_gather(rows != 0, reinterpret_cast<const int2*>(seg), nseg, m, ptrs.as<long long>(), table, table_len,
+    int max_len = 0;  // the longest segment (sizes the candidate list)
+    {
+      std::vector<int2> hs(static_cast<size_t>(m) * nseg);
+      if (!hs.empty()) OCTEX_HIP(hipMemcpy(hs.data(), seg, hs.size() * sizeof(int2), hipMemcpyDefault));
+      for (auto const& v : hs)
+        max_len = std::max(max_len, v.y);
+    }
+    launch_gather(rows != 0, reinterpret_cast<const int2*>(seg), nseg, max_len, m, ptrs.as<long long>(), table, table_len,
                   n, reinterpret_cast<const signed char*>(code), S, scale, qs, S, W, log2_ceil(W), cand, dist,
                   nout, s);
     OCTEX_HIP(hipStreamSynchronize(s));

@@ -184,25 +184,32 @@ float sketch_dist(const int8_t* x, const float* sc, const float* qv, int S)
   return part[0];
 }
 
-/** search_kernels.cuh:325-342 over 64 lanes. */
+/**
+ * search_kernels.cuh:325-342 with the lane split of the HIP kernel: LX lanes per row (the next power
+ * of two >= D / 8, at most 32), lane sub summing the 8-element chunks sub, sub + LX, ... in order with
+ * t = x - q, acc = fma(t, t, acc), then the xor butterfly over the LX lanes.
+ */
 float exact_dist(const uint16_t* x, const float* q, int D)
 {
-  float part[64];
-  for (int l = 0; l < 64; l++) {
+  const int nch = (D + 7) / 8;
+  int LX        = 1;
+  while (LX < nch && LX < 32)
+    LX <<= 1;
+  float part[32];
+  for (int sub = 0; sub < LX; sub++) {
     float acc = 0.f;
-    for (int k = l; k < D / 2; k += 64) {
-      float a = h2f(x[2 * k]) - q[2 * k];
-      float b = h2f(x[2 * k + 1]) - q[2 * k + 1];
-      acc     = std::fma(a, a, acc);
-      acc     = std::fma(b, b, acc);
-    }
-    part[l] = acc;
+    for (int c = sub; c < nch; c += LX)
+      for (int e = 0; e < 8 && 8 * c + e < D; e++) {
+        const float t = h2f(x[8 * c + e]) - q[8 * c + e];
+        acc           = std::fma(t, t, acc);
+      }
+    part[sub] = acc;
   }
-  for (int o = 32; o; o >>= 1) {
-    float nx[64];
-    for (int i = 0; i < 64; i++)
+  for (int o = LX >> 1; o; o >>= 1) {
+    float nx[32];
+    for (int i = 0; i < LX; i++)
       nx[i] = part[i] + part[i ^ o];
-    std::memcpy(part, nx, sizeof(part));
+    std::memcpy(part, nx, sizeof(float) * LX);
   }
   return part[0];
 }

@@ -10,9 +10,10 @@
  *   - E8 distances da/dc:   t = x - a; acc = fma(t, t, acc)                 (e8.cuh:56-57)
  *   - sketch score:         u = fma(code, scale, -qs); d = fma(u, u, d), Lr-lane chunks of 16 then
  *                           an xor butterfly over o = Lr/2 .. 1            (search_kernels.cuh:227-251)
- *   - exact distance:       64 lanes, lane l takes half2 pairs l, l+64, ...; a = x0 - q0, b = x1 - q1;
- *                           acc = fma(a, a, acc); acc = fma(b, b, acc); xor butterfly over 32 .. 1
- *                           (search_kernels.cuh:325-342 with the wave64 lane count)
+ *   - exact distance:       LX lanes per row (the next power of two >= D / 8, at most 32), lane sub
+ *                           takes the 8-element chunks sub, sub + LX, ... in order; t = x - q;
+ *                           acc = fma(t, t, acc); xor butterfly over LX/2 .. 1
+ *                           (search_kernels.cuh:325-342 with 16-byte chunks per lane)
  *   - selections:           the R smallest by (distance bits, id); the reference takes threshold ties in
  *                           atomicAdd order (search_kernels.cuh:307), here the smallest ids win.
  * Parity unpinned at bit level against the reference itself: the fp16 projection (cuBLASLt order), the

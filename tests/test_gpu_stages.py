@@ -263,18 +263,20 @@ def random_candidates(g, m, W, n_max, N, ties=True):
     return cand, dist, nin
 
 
-@pytest.mark.parametrize("R", [16, 48])  # a row per wavefront / a row per lane
+# (KO, R): the kept list and the reranked rows sort together in P = pow2 >= KO + R keys: P = 32 sorts in LDS,
+# P = 128 holds one key in half the threads, P = 512 two keys per thread, P = 1024 four
+@pytest.mark.parametrize("KO,R", [(64, 16), (64, 48), (10, 20), (256, 256), (512, 512)])
 @pytest.mark.parametrize("fresh", [True, False])
-def test_rerank_keep_matches_oracle(L, ix, dix, small_index, fresh, R):
+def test_rerank_keep_matches_oracle(L, ix, dix, small_index, fresh, KO, R):
     g = np.random.default_rng(4 + fresh)
-    m, W, KO = 40, 2048, 64
+    m, W = 40, 2048
     cand, dist, nin = random_candidates(g, m, W, 1500, ix.n)
     Q = small_index["Q"][:m]
     si = np.full((m, KO), -1, np.int64)
     sd = np.full((m, KO), np.inf, np.float32)
     if not fresh:
         for q in range(m):
-            ids = g.choice(ix.n, 50, replace=False)
+            ids = g.choice(ix.n, min(50, KO), replace=False)
             ex = np.array([O.exact_dist(ix.vectors[i], Q[q]) for i in ids], np.float32)
             si[q], sd[q] = O.merge_keep(si[q], sd[q], ids.astype(np.int32), ex, True)
     dsi, dsd = dev(si), dev(sd)
