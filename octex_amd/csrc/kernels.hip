@@ -216,15 +216,19 @@ __global__ __launch_bounds__(256) void probe_kernel(const __half* __restrict__ Y
   if (active) {
     c = static_cast<int>(g / m);
     u = (g % m) * C + c;
-    // E8 blocks one after another (a block's 8 fp16 coordinates are one 16-byte load; the row's
-    // other blocks then come from the same cache line), so that one decode is live at a time
+    // the row's B 16-byte loads issued together; then the E8 blocks one after another, a scheduling
+    // barrier between blocks keeping one decode live at a time (interleaved decodes need 2-3x the
+    // registers, and the wavefronts per SIMD are what hide the bucket lookups' latency)
     const uint4* yp   = reinterpret_cast<const uint4*>(Y + u * 8 * B);
     const float inv   = inv_f[j];
+    uint4 yv[B];
+#pragma unroll
+    for (int jb = 0; jb < B; jb++)
+      yv[jb] = yp[jb];
     unsigned long long hh = 0;
-#pragma unroll 1
+#pragma unroll
     for (int jb = 0; jb < B; jb++) {
-      const uint4 w    = yp[jb];
-      const __half* hv = reinterpret_cast<const __half*>(&w);
+      const __half* hv = reinterpret_cast<const __half*>(&yv[jb]);
       float x[8], pt[8];
 #pragma unroll
       for (int i = 0; i < 8; i++)
@@ -232,6 +236,7 @@ __global__ __launch_bounds__(256) void probe_kernel(const __half* __restrict__ Y
       e8_point(x, pt);
       const unsigned long long hb = block_hash(pt);
       hh                          = jb == 0 ? hb : hh * kMix + hb;
+      __builtin_amdgcn_sched_barrier(0);
     }
     const long long h   = finish_hash(hh);
     const int bk        = static_cast<int>(h & ((1LL << logT) - 1));
@@ -529,7 +534,7 @@ __device__ __forceinline__ bool pick_digit(const unsigned* hist, unsigned& kk, u
  * key has them; the candidates of one query share most exponent bits, which would otherwise send all
  * of them to one bin).  All threads of the workgroup call it.
  */
-__device__ void select_smallest(const unsigned* __restrict__ kd, const int* __restrict__ cid, int n,
+__device__ __noinline__ void select_smallest(const unsigned* __restrict__ kd, const int* __restrict__ cid, int n,
                                 int R, int* sid, float* skey, unsigned* hist, select_state& st)
 {
   constexpr int kCache = 4;
@@ -661,6 +666,187 @@ __device__ void select_smallest(const unsigned* __restrict__ kd, const int* __re
     }
   });
   __syncthreads();
+}
+
+/**
+ * Slot of this lane's item in a list appended to by several wavefronts: one atomic per wavefront on
+ * *count, the lanes with pred set numbered in lane order (-1 for the others).  Every lane of the
+ * wavefront calls it.
+ */
+__device__ __forceinline__ int wave_append(bool pred, int* count)
+{
+  const int lane                = threadIdx.x & 63;
+  const unsigned long long mask = __ballot(pred);
+  if (mask == 0) return -1;
+  const int leader = __ffsll(static_cast<long long>(mask)) - 1;
+  int base         = 0;
+  if (lane == leader) base = atomicAdd(count, __popcll(mask));
+  base = __shfl(base, leader);
+  return pred ? base + __popcll(mask & ((1ULL << lane) - 1ULL)) : -1;
+}
+
+constexpr int kBins     = 2048;  // histogram of the two-pass selection
+constexpr int kTieCap   = 256;   // keys of the threshold bin ranked directly
+constexpr int kSelCache = 8;     // keys per thread held in registers
+
+struct bin_select_state {
+  unsigned kmin, kmax;
+  int bstar, below, ntb, nsel;
+  int wtot[16];
+};
+
+struct bin_select_lds {
+  unsigned hist[kBins];
+  unsigned tkey[kTieCap];
+  int tid[kTieCap];
+  bin_select_state bs;
+  select_state st;  // the radix selection's, for the fallback
+};
+
+/**
+ * The R smallest of n (distance, id) pairs of a query by (distance bits, id) (search_kernels.cuh
+ * :259-322 with a deterministic tie rule) in two passes over the keys, which stay in registers
+ * (kSelCache per thread; the rest are read again): a kBins-bin histogram of (key - kmin) >> shift,
+ * shift fitting the keys' range into the bins, gives the bin b* where the count reaches R; keys of
+ * lower bins are taken, and the keys of bin b* are ranked by (key, id) among themselves, the
+ * R - (count below b*) smallest taken.  When b* holds more than kTieCap keys the radix selection
+ * (select_smallest) selects instead, with the same result.  Selected ids (and keys when skey is set)
+ * go to sid / skey in any order; their count is returned in every thread.  All threads of the
+ * workgroup call it.
+ */
+__device__ int select_by_bins(const unsigned* __restrict__ kd, const int* __restrict__ cid, int n, int R, int* sid,
+                              float* skey, bin_select_lds& sh)
+{
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, nthr = blockDim.x;
+  auto& bs = sh.bs;
+  if (n <= R) {
+    for (int i = tid; i < n; i += nthr) {
+      sid[i] = cid[i];
+      if (skey) skey[i] = __uint_as_float(kd[i]);
+    }
+    __syncthreads();
+    return n;
+  }
+  if (tid == 0) {
+    bs.kmin = ~0u;
+    bs.kmax = 0u;
+    bs.ntb  = 0;
+    bs.nsel = 0;
+  }
+  constexpr unsigned kNone = ~0u;  // an empty register slot (valid keys are finite non-negative floats)
+  unsigned kr[kSelCache];
+  unsigned lo = ~0u, hi = 0u;
+#pragma unroll
+  for (int j = 0; j < kSelCache; j++) {
+    const int i = tid + j * nthr;
+    kr[j]       = i < n ? kd[i] : kNone;
+    if (kr[j] != kNone) {
+      lo = min(lo, kr[j]);
+      hi = max(hi, kr[j]);
+    }
+  }
+  for (int i = tid + kSelCache * nthr; i < n; i += nthr) {
+    const unsigned k = kd[i];
+    lo               = min(lo, k);
+    hi               = max(hi, k);
+  }
+#pragma unroll
+  for (int o = 32; o; o >>= 1) {
+    lo = min(lo, static_cast<unsigned>(__shfl_xor(static_cast<int>(lo), o)));
+    hi = max(hi, static_cast<unsigned>(__shfl_xor(static_cast<int>(hi), o)));
+  }
+  for (int i = tid; i < kBins; i += nthr)
+    sh.hist[i] = 0;
+  __syncthreads();
+  if (lane == 0) {
+    atomicMin(&bs.kmin, lo);
+    atomicMax(&bs.kmax, hi);
+  }
+  __syncthreads();
+  const unsigned kmin = bs.kmin, range = bs.kmax - bs.kmin;
+  const int shift = range < static_cast<unsigned>(kBins) ? 0 : (32 - __clz(static_cast<int>(range))) - 11;
+  // every key with its index, registers first (uniform trip counts: the appends below use ballots)
+  auto for_keys = [&](auto&& f) {
+#pragma unroll
+    for (int j = 0; j < kSelCache; j++)
+      f(kr[j], tid + j * nthr, kr[j] != kNone);
+    for (int i0 = kSelCache * nthr; i0 < n; i0 += nthr) {
+      const int i = i0 + tid;
+      f(i < n ? kd[i] : kNone, i, i < n);
+    }
+  };
+  for_keys([&](unsigned k, int, bool ok) {
+    if (ok) atomicAdd(&sh.hist[(k - kmin) >> shift], 1u);
+  });
+  __syncthreads();
+  // the bin where the running count reaches R: thread t scans bins [t per, (t + 1) per)
+  const int per = kBins / nthr;
+  unsigned s    = 0;
+  for (int b = 0; b < per; b++)
+    s += sh.hist[tid * per + b];
+  unsigned incl = s;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const unsigned u = __shfl_up(incl, o);
+    if (lane >= o) incl += u;
+  }
+  if (lane == 63) bs.wtot[wid] = static_cast<int>(incl);
+  __syncthreads();
+  unsigned excl = incl - s;
+  for (int w = 0; w < wid; w++)
+    excl += static_cast<unsigned>(bs.wtot[w]);
+  if (excl < static_cast<unsigned>(R) && static_cast<unsigned>(R) <= excl + s) {
+    unsigned cum = excl;
+    for (int b = 0; b < per; b++) {
+      const unsigned h = sh.hist[tid * per + b];
+      if (cum + h >= static_cast<unsigned>(R)) {
+        bs.bstar = tid * per + b;
+        bs.below = static_cast<int>(cum);
+        break;
+      }
+      cum += h;
+    }
+  }
+  __syncthreads();
+  const unsigned bstar = static_cast<unsigned>(bs.bstar);
+  const int need       = R - bs.below;
+  for_keys([&](unsigned k, int i, bool ok) {
+    const unsigned b = (k - kmin) >> shift;
+    const int at     = wave_append(ok && b < bstar, &bs.nsel);
+    if (at >= 0) {
+      sid[at] = cid[i];
+      if (skey) skey[at] = __uint_as_float(k);
+    }
+    const int t = wave_append(ok && b == bstar, &bs.ntb);
+    if (t >= 0 && t < kTieCap) {
+      sh.tkey[t] = k;
+      sh.tid[t]  = cid[i];
+    }
+  });
+  __syncthreads();
+  const int ntb = bs.ntb;
+  if (ntb > kTieCap) {  // too many keys in one bin: the radix passes
+    __syncthreads();
+    select_smallest(kd, cid, n, R, sid, skey, sh.hist, sh.st);
+    return sh.st.nsel;
+  }
+  for (int i = tid; i < ntb; i += nthr) {  // rank of each tie-bin key by (key, id) among them
+    const unsigned ki = sh.tkey[i], ii = static_cast<unsigned>(sh.tid[i]);
+    int rank          = 0;
+    for (int j = 0; j < ntb; j++) {
+      const unsigned kj = sh.tkey[j], ij = static_cast<unsigned>(sh.tid[j]);
+      rank += (kj < ki || (kj == ki && ij < ii)) ? 1 : 0;
+    }
+    if (rank < need) {
+      const int at = atomicAdd(&bs.nsel, 1);
+      sid[at]      = static_cast<int>(ii);
+      if (skey) skey[at] = __uint_as_float(ki);
+    }
+  }
+  __syncthreads();
+  const int ns = bs.nsel;
+  __syncthreads();
+  return ns;
 }
 
 /**
@@ -811,17 +997,15 @@ __global__ __launch_bounds__(kKeepThreads) void rerank_keep_kernel(
 {
   const int q = blockIdx.x;
   extern __shared__ float sq[];
-  __shared__ unsigned hist[256];
-  __shared__ select_state st;
+  __shared__ bin_select_lds sel;
   __shared__ int sid[kMaxRerank];
   __shared__ float sd[kMaxRerank];
   __shared__ uint64_t key[kMaxKeepSort];
   const int n = min(nin[q], W);
   for (int i = threadIdx.x; i < D; i += blockDim.x)
     sq[i] = Q[static_cast<int64_t>(q) * D + i];
-  select_smallest(reinterpret_cast<const unsigned*>(dist + static_cast<int64_t>(q) * W),
-                  cand + static_cast<int64_t>(q) * W, n, R, sid, nullptr, hist, st);
-  const int ns = st.nsel;
+  const int ns = select_by_bins(reinterpret_cast<const unsigned*>(dist + static_cast<int64_t>(q) * W),
+                                cand + static_cast<int64_t>(q) * W, n, R, sid, nullptr, sel);
   exact_distances_t<LX>(sid, ns, vectors, D, sq, sd);
   long long* pb = bi + static_cast<int64_t>(q) * KO;
   float* pd     = bd + static_cast<int64_t>(q) * KO;
@@ -841,15 +1025,13 @@ __global__ __launch_bounds__(512) void sketch_keep_kernel(const int* __restrict_
                                                           float* __restrict__ sd, bool fresh)
 {
   const int q = blockIdx.x;
-  __shared__ unsigned hist[256];
-  __shared__ select_state st;
+  __shared__ bin_select_lds sel;
   __shared__ int sid[kMaxSketchKO];
   __shared__ float sdv[kMaxSketchKO];
   __shared__ uint64_t key[2 * kMaxSketchKO];
   const int n = min(nin[q], W);
-  select_smallest(reinterpret_cast<const unsigned*>(dist + static_cast<int64_t>(q) * W),
-                  cand + static_cast<int64_t>(q) * W, n, KO, sid, sdv, hist, st);
-  const int ns  = st.nsel;
+  const int ns = select_by_bins(reinterpret_cast<const unsigned*>(dist + static_cast<int64_t>(q) * W),
+                                cand + static_cast<int64_t>(q) * W, n, KO, sid, sdv, sel);
   long long* pb = si + static_cast<int64_t>(q) * KO;
   float* pd     = sd + static_cast<int64_t>(q) * KO;
   int P         = 2;

@@ -250,7 +250,9 @@ def test_gather_rows_matches_oracle(L, ix, dix):
 # ---------------------------------------------------------------- keep, pick, final
 
 
-def random_candidates(g, m, W, n_max, N, ties=True):
+def random_candidates(g, m, W, n_max, N, ties=True, kind=None):
+    """Candidate rows of m queries: integer distances in [0, 40) (ties), uniform ones, or all equal."""
+    kind = kind or ("ties" if ties else "uniform")
     cand = np.full((m, W), -9, np.int32)
     dist = np.zeros((m, W), np.float32)
     nin = g.integers(1, n_max, m).astype(np.int32)
@@ -259,7 +261,12 @@ def random_candidates(g, m, W, n_max, N, ties=True):
     for q in range(m):
         n = nin[q]
         cand[q, :n] = g.choice(N, n, replace=False)
-        dist[q, :n] = g.integers(0, 40, n) if ties else g.uniform(0, 100, n)
+        if kind == "ties":
+            dist[q, :n] = g.integers(0, 40, n)
+        elif kind == "uniform":
+            dist[q, :n] = g.uniform(0, 100, n)
+        else:
+            dist[q, :n] = 7.25
     return cand, dist, nin
 
 
@@ -285,6 +292,26 @@ def test_rerank_keep_matches_oracle(L, ix, dix, small_index, fresh, KO, R):
            i32(R), i32(KO), P(dsi), P(dsd), i32(fresh), None)
     for q in range(m):
         ri, rd = O.rerank_keep(ix, cand[q, : nin[q]], dist[q, : nin[q]], Q[q], R, si[q], sd[q], fresh)
+        assert np.array_equal(host(dsi)[q], ri), f"query {q}"
+        assert np.array_equal(host(dsd)[q], rd), f"query {q}"
+
+
+# the selection's paths: a threshold bin of a few keys (uniform), of many equal keys ranked by id (ties), and
+# of more keys than the ranked buffer holds (equal: every key in one bin, selected by radix passes)
+@pytest.mark.parametrize("kind", ["uniform", "ties", "equal"])
+def test_rerank_keep_selection_paths(L, ix, dix, small_index, kind):
+    g = np.random.default_rng(9)
+    m, W, KO, R = 24, 4096, 64, 128
+    cand, dist, nin = random_candidates(g, m, W, 3000, ix.n, kind=kind)
+    Q = small_index["Q"][:m]
+    si = np.full((m, KO), -1, np.int64)
+    sd = np.full((m, KO), np.inf, np.float32)
+    dsi, dsd = dev(si), dev(sd)
+    dc, dd, dn, dQ = dev(cand), dev(dist), dev(nin), dev(Q)
+    L.call("octexStageRerankKeep", P(dc), P(dd), P(dn), i32(m), i32(W), P(dix["vectors"]), i32(ix.dim), P(dQ),
+           i32(R), i32(KO), P(dsi), P(dsd), i32(1), None)
+    for q in range(m):
+        ri, rd = O.rerank_keep(ix, cand[q, : nin[q]], dist[q, : nin[q]], Q[q], R, si[q], sd[q], True)
         assert np.array_equal(host(dsi)[q], ri), f"query {q}"
         assert np.array_equal(host(dsd)[q], rd), f"query {q}"
 
