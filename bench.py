@@ -53,6 +53,10 @@ SWEEP_DEEP = [
     dict(read=16, starts=32, waves=1, rerank=64, wave_rerank=64),
     dict(read=16, starts=32, waves=2, rerank=64, wave_rerank=64),
     dict(read=16, starts=64, waves=1, rerank=128, wave_rerank=128),
+    dict(read=16, starts=48, waves=2, rerank=96, wave_rerank=96),
+    dict(read=12, starts=64, waves=2, rerank=128, wave_rerank=128),
+    dict(read=16, starts=64, waves=2, rerank=96, wave_rerank=96),
+    dict(read=16, starts=64, waves=2, rerank=64, wave_rerank=128),
     dict(read=16, starts=64, waves=2, rerank=128, wave_rerank=128),
     dict(read=32, starts=64, waves=2, rerank=128, wave_rerank=128),
     dict(read=16, starts=128, waves=2, rerank=128, wave_rerank=128),

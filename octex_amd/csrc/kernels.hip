@@ -187,13 +187,37 @@ __global__ __launch_bounds__(256) void e8_kernel(const float* __restrict__ y, in
 // ------------------------------------------------------------------ probe (search_kernels.cuh:84-127)
 
 /**
- * One lane per (query, copy, level): the levels of a (query, copy) are L neighbouring lanes of one
- * wavefront (64 / L groups per wavefront, the groups of a wavefront all of one copy), so every
- * level's cell id, bucket and key lookup run at once instead of one level after another, and a lane
- * holds one E8^B decode.  A lane computes the cell id of y * inv_f[j], reads its bucket's bounds and
- * compares the bucket's keys four at a time; a ballot then gives each group its finest level with a
- * hit, whose lane writes seg = ((base + p) * l, lr); a group without a hit writes (0, 0) from its
- * level-0 lane.  Every lane reaches the ballot.
+ * Cell id of the E8^B point nearest to y * inv for the fp16 row yv (B 16-byte pieces): the blocks are
+ * decoded one after another, a scheduling barrier between blocks keeping one decode live at a time
+ * (interleaved decodes need 2-3x the registers, and the wavefronts per SIMD hide the bucket lookups).
+ */
+template <int B>
+__device__ __forceinline__ long long probe_cell_id(const uint4 (&yv)[B], float inv)
+{
+  unsigned long long hh = 0;
+#pragma unroll
+  for (int jb = 0; jb < B; jb++) {
+    const __half* hv = reinterpret_cast<const __half*>(&yv[jb]);
+    float x[8], pt[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      x[i] = __half2float(hv[i]) * inv;
+    e8_point(x, pt);
+    const unsigned long long hb = block_hash(pt);
+    hh                          = jb == 0 ? hb : hh * kMix + hb;
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  return finish_hash(hh);
+}
+
+/**
+ * Levels fine to coarse for every (query, copy) item, stopping at the first level whose bucket holds
+ * the cell id (search_kernels.cuh:84-127).  A wavefront owns `chunk` consecutive items (item t: copy
+ * t / m, query t % m, so a wavefront's lookups stay in one copy's tables); each lane holds one item and
+ * its next level, and runs one level per step: the cell id of y * inv_f[level], the bucket's bounds,
+ * its keys four loads at a time.  A lane whose item is decided (a hit: seg = ((base + p) * l, lr); no
+ * level left: (0, 0)) takes the wavefront's next item, so lanes stay busy until the chunk runs out
+ * instead of every item paying for all L levels.  The loop ends for the whole wavefront together.
  */
 template <int B>
 __global__ __launch_bounds__(256) void probe_kernel(const __half* __restrict__ Y, int m, int C,
@@ -201,66 +225,68 @@ __global__ __launch_bounds__(256) void probe_kernel(const __half* __restrict__ Y
                                                     const int* __restrict__ off, int64_t T1,
                                                     const long long* __restrict__ keys,
                                                     int64_t Mmax, const int* __restrict__ base,
-                                                    int l, int lr, int logT, int2* __restrict__ seg)
+                                                    int l, int lr, int logT, int64_t chunk,
+                                                    int2* __restrict__ seg)
 {
-  const int lane = threadIdx.x & 63;
-  const int G    = 64 / L;  // groups per wavefront
-  const int gi = lane / L, j = lane - gi * L;
-  const int64_t wave  = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
-  const int64_t total = static_cast<int64_t>(m) * C;
-  const int64_t g     = wave * G + gi;  // (copy, query) = (g / m, g % m): a wavefront's groups share a copy
-  const bool active   = gi < G && g < total;
-  int c = 0;
+  const int lane         = threadIdx.x & 63;
+  const int64_t total    = static_cast<int64_t>(m) * C;
+  const int64_t wave     = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
+  const int64_t first    = wave * chunk;
+  const int64_t last     = min(first + chunk, total);
+  const unsigned long long below = (1ULL << lane) - 1ULL;
+  int64_t next = first;  // the wavefront's next unassigned item (uniform)
+  int64_t item = first + lane < last ? first + lane : -1;
+  next += 64;
+  int lvl = 0, c = 0;
   int64_t u = 0;
-  int hit   = -1;
-  if (active) {
-    c = static_cast<int>(g / m);
-    u = (g % m) * C + c;
-    // the row's B 16-byte loads issued together; then the E8 blocks one after another, a scheduling
-    // barrier between blocks keeping one decode live at a time (interleaved decodes need 2-3x the
-    // registers, and the wavefronts per SIMD are what hide the bucket lookups' latency)
+  uint4 yv[B];
+  auto start = [&]() {  // a new item: its copy, its output slot, its fp16 row
+    c                 = static_cast<int>(item / m);
+    u                 = (item % m) * C + c;
     const uint4* yp   = reinterpret_cast<const uint4*>(Y + u * 8 * B);
-    const float inv   = inv_f[j];
-    uint4 yv[B];
 #pragma unroll
     for (int jb = 0; jb < B; jb++)
       yv[jb] = yp[jb];
-    unsigned long long hh = 0;
+    lvl = 0;
+  };
+  if (item >= 0) start();
+  while (__ballot(item >= 0) != 0) {
+    bool done = false;
+    if (item >= 0) {
+      const long long h   = probe_cell_id<B>(yv, inv_f[lvl]);
+      const int bk        = static_cast<int>(h & ((1LL << logT) - 1));
+      const int* o        = off + (static_cast<int64_t>(c) * L + lvl) * T1 + bk;
+      const long long* kk = keys + (static_cast<int64_t>(c) * L + lvl) * Mmax;
+      const int p0 = o[0], p1 = o[1];
+      int hit      = -1;
+      for (int p = p0; p < p1 && hit < 0; p += 4) {  // keys of the bucket, four loads in flight
+        long long k4[4];
 #pragma unroll
-    for (int jb = 0; jb < B; jb++) {
-      const __half* hv = reinterpret_cast<const __half*>(&yv[jb]);
-      float x[8], pt[8];
+        for (int i = 0; i < 4; i++)
+          k4[i] = kk[min(p + i, p1 - 1)];
 #pragma unroll
-      for (int i = 0; i < 8; i++)
-        x[i] = __half2float(hv[i]) * inv;
-      e8_point(x, pt);
-      const unsigned long long hb = block_hash(pt);
-      hh                          = jb == 0 ? hb : hh * kMix + hb;
-      __builtin_amdgcn_sched_barrier(0);
+        for (int i = 0; i < 4; i++)
+          if (hit < 0 && p + i < p1 && k4[i] == h) hit = p + i;
+      }
+      if (hit >= 0) {
+        seg[u] = make_int2((base[c * L + lvl] + hit) * l, lr);
+        done   = true;
+      } else if (lvl + 1 == L) {
+        seg[u] = make_int2(0, 0);
+        done   = true;
+      } else {
+        lvl++;
+      }
     }
-    const long long h   = finish_hash(hh);
-    const int bk        = static_cast<int>(h & ((1LL << logT) - 1));
-    const int* o        = off + (static_cast<int64_t>(c) * L + j) * T1 + bk;
-    const long long* kk = keys + (static_cast<int64_t>(c) * L + j) * Mmax;
-    const int p0 = o[0], p1 = o[1];
-    for (int p = p0; p < p1 && hit < 0; p += 4) {  // keys of the bucket, four loads in flight
-      long long k4[4];
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-        k4[i] = kk[min(p + i, p1 - 1)];
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-        if (hit < 0 && p + i < p1 && k4[i] == h) hit = p + i;
+    // decided lanes (and idle ones) take the next items in lane order
+    const unsigned long long fr = __ballot(done || item < 0);
+    if (done || item < 0) {
+      const int64_t t = next + __popcll(fr & below);
+      item            = t < last ? t : -1;
+      if (item >= 0) start();
     }
+    next += __popcll(fr);
   }
-  const unsigned long long hits = __ballot(hit >= 0);
-  if (!active) return;
-  const unsigned gm = static_cast<unsigned>(hits >> (gi * L)) & (L >= 32 ? ~0u : (1u << L) - 1u);
-  const int fin     = gm != 0 ? __ffs(static_cast<int>(gm)) - 1 : -1;  // the finest level with a hit
-  if (fin >= 0 && j == fin)
-    seg[u] = make_int2((base[c * L + j] + hit) * l, lr);
-  else if (fin < 0 && j == 0)
-    seg[u] = make_int2(0, 0);
 }
 
 // ------------------------------------------------------------------ gather (search_kernels.cuh:138-253)
@@ -1255,12 +1281,20 @@ void launch_probe(const __half* Y, int m, int C, int L, int B, const float* inv_
   const int64_t tot = static_cast<int64_t>(m) * C;
   if (tot == 0) return;
   OCTEX_EXPECTS(T1 == (int64_t{1} << logT) + 1, "octex: offsets rows must hold 2^log_buckets + 1 entries");
-  OCTEX_EXPECTS(L >= 1 && L <= 32, "octex: the probe takes 1 to 32 spacings");
-  const int G         = 64 / L;  // (query, copy) groups per wavefront
-  const int64_t waves = (tot + G - 1) / G;
+  OCTEX_EXPECTS(L >= 1, "octex: at least one spacing");
+  // items per wavefront: about 16 wavefronts per CU over the whole grid, at least one item per lane
+  static const int cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    return n;
+  }();
+  const int64_t chunk = std::max<int64_t>(64, (tot + int64_t{16} * cus - 1) / (int64_t{16} * cus));
+  const int64_t waves = (tot + chunk - 1) / chunk;
   auto g              = grid_for(waves * 64, 256);
 #define OCTEX_PROBE(b) \
-  probe_kernel<b><<<g, 256, 0, s>>>(Y, m, C, L, inv_f, off, T1, keys, Mmax, base, l, lr, logT, seg)
+  probe_kernel<b><<<g, 256, 0, s>>>(Y, m, C, L, inv_f, off, T1, keys, Mmax, base, l, lr, logT, chunk, seg)
   switch (B) {
     case 1: OCTEX_PROBE(1); break;
     case 2: OCTEX_PROBE(2); break;
