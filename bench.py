@@ -215,6 +215,22 @@ def stage_bytes(name, wave, cnt, m, C, S, D, KO, table_len, starts, w, L):
     return None
 
 
+def measured_traffic(config, params, stage, n):
+    """HBM bytes per launch of a stage from the committed rocprof counter summary of this workload
+    (profiles/traffic_<config>.json: FETCH_SIZE and WRITE_SIZE per dispatch, scaled by what the same counters
+    read for a 1 GiB device copy), when it was measured with these search parameters; else None."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{config}.json")
+    if not os.path.isfile(path):
+        return None
+    with open(path) as f:
+        t = json.load(f)
+    keys = ("read", "starts", "waves", "rerank", "wave_rerank")
+    if t.get("n") != n or any(t.get("params", {}).get(k) != params.get(k) for k in keys):
+        return None
+    k = t.get("kernels", {}).get(stage)
+    return None if k is None else int(k["hbm_bytes_per_launch"])
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -317,6 +333,7 @@ def main():
     avg_ms = sum(x["ms"] for x in dl) / len(dl)
     avg_bytes = sum(x["bytes"] for x in dl) / len(dl)
     achieved = avg_bytes / (avg_ms * 1e-3) / 1e9
+    traffic = measured_traffic(args.config, params, dominant, X.shape[0])
     log(f"probe hits by level {cnt['hit_level'][:int(meta[4])]}, misses {len(Q) * C - cnt['seg_hits']}")
     log("stages: " + ", ".join(f"{x['stage']}[{x['wave']}] {x['ms']:.3f} ms {x['gbs']} GB/s" for x in per_launch))
 
@@ -379,7 +396,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
             "avg_launch_ms": round(avg_ms, 4),
             "algorithmic_bytes_per_launch": int(avg_bytes),
         },
