@@ -301,19 +301,17 @@ __device__ __forceinline__ int hash_log_dev(int total, int log_cap)
 }
 
 /**
- * Sketch scores of the candidates ht[cl[0, n)] (LDS: the hash-set slots of the query's distinct ids in
- * the order they were added) of one query (search_kernels.cuh:227-251): an LR-lane
- * group (LR = the next power of two >= S / 16, at most 32) scores a candidate, lane `sub` reducing the
- * 16-element chunks sub, sub + LR, ... as u = fma(code, scale, -qs), d = fma(u, u, d), then an xor
- * butterfly over the group; the group's lane 0 writes the id and its score to crow / drow.  A
+ * Sketch scores of a query's candidates 0..n-1 (search_kernels.cuh:227-251): an LR-lane group (LR = the
+ * next power of two >= S / 16, at most 32) scores a candidate, lane `sub` reducing the 16-element chunks
+ * sub, sub + LR, ... as u = fma(code, scale, -qs), d = fma(u, u, d), then an xor butterfly over the
+ * group; the group's lane 0 hands (j, id, score) to put.  id_of(j) gives candidate j's id.  A
  * candidate's row is read by one load instruction of its group (one address translation per row: rows
  * lie anywhere in a sketch of many GB), and every group has kRows candidates' loads in flight before it
  * computes.
  */
-template <int LR>
-__device__ __forceinline__ void sketch_scores(const unsigned short* cl, const int* ht, int n,
-                                              const signed char* __restrict__ code, int S, int pitch,
-                                              const float2* sq, int* crow, float* drow)
+template <int LR, typename IdOf, typename Put>
+__device__ __forceinline__ void sketch_scores(int n, IdOf const& id_of, const signed char* __restrict__ code, int S,
+                                              int pitch, const float2* sq, Put const& put)
 {
   constexpr int kRows = 4;        // candidates per group in flight
   constexpr int GPW   = 64 / LR;  // groups per wavefront
@@ -335,7 +333,7 @@ __device__ __forceinline__ void sketch_scores(const unsigned short* cl, const in
     int id[kRows];
 #pragma unroll
     for (int r = 0; r < kRows; r++)  // candidate j0 + r * GPW + grp
-      id[r] = ht[cl[min(j0 + r * GPW + grp, n - 1)]];
+      id[r] = id_of(min(j0 + r * GPW + grp, n - 1));
     int4 w[kRows];
 #pragma unroll
     for (int r = 0; r < kRows; r++)
@@ -359,48 +357,37 @@ __device__ __forceinline__ void sketch_scores(const unsigned short* cl, const in
       for (int o = LR >> 1; o; o >>= 1)
         d[r] += __shfl_xor(d[r], o);
       const int j = j0 + r * GPW + grp;
-      if (j < n && sub == 0) {
-        crow[j] = id[r];
-        drow[j] = d[r];
-      }
+      if (j < n && sub == 0) put(j, id[r], d[r]);
     }
   }
 }
 
+/** Per-query state of collect_candidates (LDS). */
+struct collect_state {
+  int cnt, nsp, ulen;
+};
+
 /**
- * Distinct ids of all segments of a query with their sketch scores.  Wavefront 0 compacts the
- * non-empty segments (entry pointer and exclusive prefix of the lengths) into LDS; the entries are then
- * split evenly over the workgroup, kUnroll per thread with their loads issued together (entry i of a
- * query whose non-empty segments all have one length len lies in segment i / len, otherwise a binary
- * search over the prefix finds it); an LDS open-addressing set drops duplicates and the slots of new ids
- * are appended to an LDS candidate list (16-bit slot numbers) by one atomic per wavefront.  Then the candidates are scored
- * (sketch_scores; LR = the reference's lanes per candidate for this S) and written with their scores.
+ * The distinct ids of a query's segments (search_kernels.cuh:138-222).  Wavefront 0 compacts the
+ * non-empty segments (entry pointer sp and exclusive prefix pre of the lengths) into LDS; the entries
+ * are then split evenly over the workgroup, kUnroll per thread with their loads issued together (entry
+ * i of a query whose non-empty segments all have one length len lies in segment i / len, otherwise a
+ * binary search over the prefix finds it); an LDS open-addressing set ht (of up to W slots) drops
+ * duplicates, and each new id gets the next number by one atomic per wavefront: add(slot, id, h) with
+ * h its hash-set slot, for slot < cap.  Returns min(distinct count, cap) in every thread.
  *
  * kRows = false: segment c = (first entry, length) in the lists of copy c (at list_ptr[c]).
  * kRows = true:  segment = (row, length) of the neighbor table [N, table_len]; -1 entries skipped.
- * The candidate list holds cap = min(W, nseg * max_len) ids (max_len: the longest segment).
  */
-template <bool kRows, int LR>
-__global__ __launch_bounds__(kGatherThreads) void gather_kernel(
-  const int2* __restrict__ seg, int nseg, const long long* __restrict__ list_ptr,
-  const int* __restrict__ table, int table_len, int64_t N, const signed char* __restrict__ code,
-  const float* __restrict__ scale, const float* __restrict__ qs, int S, int pitch, int W, int logW, int cap,
-  int* __restrict__ cand, float* __restrict__ dist, int* __restrict__ nout)
+template <bool kRows, typename Add>
+__device__ int collect_candidates(const int2* __restrict__ seg, int nseg, const long long* __restrict__ list_ptr,
+                                  const int* __restrict__ table, int table_len, int64_t N, int logW, int cap,
+                                  const int** sp, int* pre, int* ht, collect_state& cs, Add const& add)
 {
   constexpr int kUnroll = 4;
   const int q = blockIdx.x;
-  extern __shared__ long long smq[];
-  const int** sp = reinterpret_cast<const int**>(smq);  // [nseg] first entry of every non-empty segment
-  float2* sq     = reinterpret_cast<float2*>(smq + nseg);  // [S] (scale, query sketch) per coordinate
-  int* pre       = reinterpret_cast<int*>(sq + S);  // [nseg + 1] exclusive prefix of the compacted lengths
-  int* ht        = pre + nseg + 1;                  // [W] hash set
-  auto* cl       = reinterpret_cast<unsigned short*>(ht + W);  // [cap] slots of the candidates
-  __shared__ int cnt, nsp, ulen;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  for (int i = tid; i < S; i += blockDim.x) {
-    sq[i] = make_float2(scale[i], qs[static_cast<int64_t>(q) * S + i]);
-  }
-  if (tid == 0) cnt = 0;
+  if (tid == 0) cs.cnt = 0;
   if (wid == 0) {
     int carry = 0, at = 0, lmin = 0x7fffffff, lmax = 0;
     for (int c0 = 0; c0 < nseg; c0 += 64) {
@@ -435,12 +422,12 @@ __global__ __launch_bounds__(kGatherThreads) void gather_kernel(
     }
     if (lane == 0) {
       pre[at] = carry;
-      nsp     = at;
-      ulen    = at > 0 && lmin == lmax ? lmax : 0;  // one length for every non-empty segment
+      cs.nsp  = at;
+      cs.ulen = at > 0 && lmin == lmax ? lmax : 0;  // one length for every non-empty segment
     }
   }
   __syncthreads();
-  const int ns = nsp, len = ulen;
+  const int ns = cs.nsp, len = cs.ulen;
   const int total = pre[ns];
   const int HT    = 1 << hash_log_dev(total, logW);
   for (int i = tid; i < HT; i += blockDim.x)
@@ -491,208 +478,55 @@ __global__ __launch_bounds__(kGatherThreads) void gather_kernel(
       if (mask != 0) {
         const int leader = __ffsll(static_cast<long long>(mask)) - 1;
         int at           = 0;
-        if (lane == leader) at = atomicAdd(&cnt, __popcll(mask));
+        if (lane == leader) at = atomicAdd(&cs.cnt, __popcll(mask));
         at = __shfl(at, leader);
         if (fresh) {
-          int slot = at + __popcll(mask & ((1ULL << lane) - 1ULL));
-          if (slot < cap) cl[slot] = static_cast<unsigned short>(h);
+          const int slot = at + __popcll(mask & ((1ULL << lane) - 1ULL));
+          if (slot < cap) add(slot, v[u], h);
         }
       }
     }
   }
   __syncthreads();
-  const int n = min(cnt, cap);
-  sketch_scores<LR>(cl, ht, n, code, S, pitch, sq, cand + static_cast<int64_t>(q) * W,
-                    dist + static_cast<int64_t>(q) * W);
-  if (tid == 0) nout[q] = n;
+  return min(cs.cnt, cap);
+}
+
+/**
+ * Distinct ids of all segments of a query with their sketch scores (collect_candidates, then
+ * sketch_scores with LR = the reference's lanes per candidate for this S), written to the query's rows of
+ * cand / dist and their count to nout.  The candidates are kept as 16-bit hash-set slot numbers in LDS.
+ */
+template <bool kRows, int LR>
+__global__ __launch_bounds__(kGatherThreads) void gather_kernel(
+  const int2* __restrict__ seg, int nseg, const long long* __restrict__ list_ptr,
+  const int* __restrict__ table, int table_len, int64_t N, const signed char* __restrict__ code,
+  const float* __restrict__ scale, const float* __restrict__ qs, int S, int pitch, int W, int logW, int cap,
+  int* __restrict__ cand, float* __restrict__ dist, int* __restrict__ nout)
+{
+  const int q = blockIdx.x;
+  extern __shared__ long long smq[];
+  const int** sp = reinterpret_cast<const int**>(smq);  // [nseg] first entry of every non-empty segment
+  float2* sq     = reinterpret_cast<float2*>(smq + nseg);  // [S] (scale, query sketch) per coordinate
+  int* pre       = reinterpret_cast<int*>(sq + S);  // [nseg + 1] exclusive prefix of the compacted lengths
+  int* ht        = pre + nseg + 1;                  // [W] hash set
+  auto* cl       = reinterpret_cast<unsigned short*>(ht + W);  // [cap] slots of the candidates
+  __shared__ collect_state cs;
+  for (int i = threadIdx.x; i < S; i += blockDim.x)
+    sq[i] = make_float2(scale[i], qs[static_cast<int64_t>(q) * S + i]);
+  const int n = collect_candidates<kRows>(seg, nseg, list_ptr, table, table_len, N, logW, cap, sp, pre, ht, cs,
+                                          [&](int slot, int, unsigned h) { cl[slot] = static_cast<unsigned short>(h); });
+  int* crow   = cand + static_cast<int64_t>(q) * W;
+  float* drow = dist + static_cast<int64_t>(q) * W;
+  sketch_scores<LR>(
+    n, [&](int j) { return ht[cl[j]]; }, code, S, pitch, sq,
+    [&](int j, int id, float d) {
+      crow[j] = id;
+      drow[j] = d;
+    });
+  if (threadIdx.x == 0) nout[q] = n;
 }
 
 // ------------------------------------------------------------------ selection and merges
-
-struct select_state {
-  unsigned prefix, kk, eq, idprefix, kk2, kmin, kmax;
-  int nsel, need_id;
-};
-
-/**
- * Wave 0 finds the digit d of a 256-bin histogram where the running count reaches kk (1 <= kk <=
- * the histogram's total); returns true in the one lane that holds d, with kk reduced to the count
- * still to take inside bin d and binpop the population of bin d.
- */
-__device__ __forceinline__ bool pick_digit(const unsigned* hist, unsigned& kk, unsigned& digit,
-                                           unsigned& binpop)
-{
-  const int lane = threadIdx.x & 63;
-  unsigned h[4], s = 0;
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    h[j] = hist[4 * lane + j];
-    s += h[j];
-  }
-  unsigned incl = s;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    unsigned u = __shfl_up(incl, o);
-    if (lane >= o) incl += u;
-  }
-  const unsigned excl = incl - s;
-  const unsigned want = kk;
-  if (!(excl < want && want <= incl)) return false;
-  unsigned cum = excl;
-  int j        = 0;
-  for (; j < 3; j++) {
-    if (cum + h[j] >= want) break;
-    cum += h[j];
-  }
-  kk     = want - cum;
-  digit  = 4 * lane + j;
-  binpop = h[j];
-  return true;
-}
-
-/**
- * The R smallest of n (distance, id) pairs of a query by (distance bits, id) (search_kernels.cuh
- * :259-322 with a deterministic tie rule): a radix select over the distance bits finds the threshold
- * T; when only some of the keys equal to T are taken, a second radix select over their ids takes the
- * smallest ids.  Selected ids (and keys when skey is set) go to sid / skey in any order; nsel in st.
- * Each thread keeps its first kCache keys in registers for every pass (the rest are read again), and
- * the digits on which the smallest and the largest key agree are taken without a histogram pass (every
- * key has them; the candidates of one query share most exponent bits, which would otherwise send all
- * of them to one bin).  All threads of the workgroup call it.
- */
-__device__ __noinline__ void select_smallest(const unsigned* __restrict__ kd, const int* __restrict__ cid, int n,
-                                int R, int* sid, float* skey, unsigned* hist, select_state& st)
-{
-  constexpr int kCache = 4;
-  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, nthr = blockDim.x;
-  if (tid == 0) {
-    st.prefix  = 0;
-    st.kk      = min(R, n);
-    st.nsel    = 0;
-    st.need_id = 0;
-    st.eq      = static_cast<unsigned>(n);
-    st.kmin    = ~0u;
-    st.kmax    = 0u;
-  }
-  __syncthreads();
-  if (n <= R) {
-    for (int i = tid; i < n; i += nthr) {
-      sid[i] = cid[i];
-      if (skey) skey[i] = __uint_as_float(kd[i]);
-    }
-    if (tid == 0) st.nsel = n;
-    __syncthreads();
-    return;
-  }
-  // valid keys are finite non-negative floats (below 0x7f800000); kNone marks an empty register slot
-  constexpr unsigned kNone = ~0u;
-  unsigned kr[kCache];
-  unsigned lo = ~0u, hi = 0u;
-#pragma unroll
-  for (int j = 0; j < kCache; j++) {
-    const int i = tid + j * nthr;
-    kr[j]       = i < n ? kd[i] : kNone;
-  }
-#pragma unroll
-  for (int j = 0; j < kCache; j++)
-    if (kr[j] != kNone) {
-      lo = min(lo, kr[j]);
-      hi = max(hi, kr[j]);
-    }
-  for (int i = tid + kCache * nthr; i < n; i += nthr) {
-    const unsigned k = kd[i];
-    lo               = min(lo, k);
-    hi               = max(hi, k);
-  }
-#pragma unroll
-  for (int o = 32; o; o >>= 1) {
-    lo = min(lo, static_cast<unsigned>(__shfl_xor(static_cast<int>(lo), o)));
-    hi = max(hi, static_cast<unsigned>(__shfl_xor(static_cast<int>(hi), o)));
-  }
-  if (lane == 0) {
-    atomicMin(&st.kmin, lo);
-    atomicMax(&st.kmax, hi);
-  }
-  __syncthreads();
-  const unsigned kmin = st.kmin, kmax = st.kmax;
-  // every key, from the registers (kNone skipped) and then from memory
-  auto for_keys = [&](auto&& f) {
-#pragma unroll
-    for (int j = 0; j < kCache; j++)
-      if (kr[j] != kNone) f(kr[j], tid + j * nthr);
-    for (int i = tid + kCache * nthr; i < n; i += nthr)
-      f(kd[i], i);
-  };
-  unsigned mask = 0;
-  for (int shift = 24; shift >= 0; shift -= 8) {
-    if ((kmin >> shift) == (kmax >> shift)) {  // a digit every key has: taken without a pass
-      if (tid == 0) st.prefix |= ((kmin >> shift) & 255u) << shift;
-      mask |= 255u << shift;
-      continue;
-    }
-    for (int i = tid; i < 256; i += nthr)
-      hist[i] = 0;
-    __syncthreads();
-    const unsigned pf = st.prefix;
-    for_keys([&](unsigned k, int) {
-      if ((k & mask) == pf) atomicAdd(&hist[(k >> shift) & 255u], 1u);
-    });
-    __syncthreads();
-    if (wid == 0) {
-      unsigned kk = st.kk, digit = 0, pop = 0;
-      if (pick_digit(hist, kk, digit, pop)) {
-        st.kk     = kk;
-        st.prefix = pf | (digit << shift);
-        st.eq     = pop;
-      }
-    }
-    mask |= 255u << shift;
-    __syncthreads();
-  }
-  __syncthreads();
-  const unsigned T = st.prefix;
-  if (st.kk < st.eq) {  // ties at T: the smallest ids among the keys equal to T
-    if (tid == 0) {
-      st.idprefix = 0;
-      st.kk2      = st.kk;
-      st.need_id  = 1;
-    }
-    __syncthreads();
-    unsigned imask = 0;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-      for (int i = tid; i < 256; i += nthr)
-        hist[i] = 0;
-      __syncthreads();
-      const unsigned pf = st.idprefix;
-      for_keys([&](unsigned k, int i) {
-        if (k == T) {
-          const unsigned id = static_cast<unsigned>(cid[i]);
-          if ((id & imask) == pf) atomicAdd(&hist[(id >> shift) & 255u], 1u);
-        }
-      });
-      __syncthreads();
-      if (wid == 0) {
-        unsigned kk = st.kk2, digit = 0, pop = 0;
-        if (pick_digit(hist, kk, digit, pop)) {
-          st.kk2      = kk;
-          st.idprefix = pf | (digit << shift);
-        }
-      }
-      imask |= 255u << shift;
-      __syncthreads();
-    }
-  }
-  const bool by_id   = st.need_id != 0;
-  const unsigned Tid = st.idprefix;
-  for_keys([&](unsigned k, int i) {
-    if (k < T || (k == T && (!by_id || static_cast<unsigned>(cid[i]) <= Tid))) {
-      int s  = atomicAdd(&st.nsel, 1);
-      sid[s] = cid[i];
-      if (skey) skey[s] = __uint_as_float(k);
-    }
-  });
-  __syncthreads();
-}
 
 /**
  * Slot of this lane's item in a list appended to by several wavefronts: one atomic per wavefront on
@@ -726,19 +560,18 @@ struct bin_select_lds {
   unsigned tkey[kTieCap];
   int tid[kTieCap];
   bin_select_state bs;
-  select_state st;  // the radix selection's, for the fallback
 };
 
 /**
  * The R smallest of n (distance, id) pairs of a query by (distance bits, id) (search_kernels.cuh
- * :259-322 with a deterministic tie rule) in two passes over the keys, which stay in registers
- * (kSelCache per thread; the rest are read again): a kBins-bin histogram of (key - kmin) >> shift,
+ * :259-322 with a deterministic tie rule) in two passes over the keys, kSelCache per thread held in
+ * registers (the rest are read again): a kBins-bin histogram of (key - kmin) >> shift,
  * shift fitting the keys' range into the bins, gives the bin b* where the count reaches R; keys of
  * lower bins are taken, and the keys of bin b* are ranked by (key, id) among themselves, the
- * R - (count below b*) smallest taken.  When b* holds more than kTieCap keys the radix selection
- * (select_smallest) selects instead, with the same result.  Selected ids (and keys when skey is set)
- * go to sid / skey in any order; their count is returned in every thread.  All threads of the
- * workgroup call it.
+ * R - (count below b*) smallest taken.  The keys of b* are ranked from a buffer of kTieCap entries; when
+ * b* holds more (many equal or nearly equal distances), each of them is ranked by a scan over all the
+ * keys instead, with the same result.  Selected ids (and keys when skey is set) go to sid / skey in any
+ * order; their count is returned in every thread.  All threads of the workgroup call it.
  */
 __device__ int select_by_bins(const unsigned* __restrict__ kd, const int* __restrict__ cid, int n, int R, int* sid,
                               float* skey, bin_select_lds& sh)
@@ -760,10 +593,11 @@ __device__ int select_by_bins(const unsigned* __restrict__ kd, const int* __rest
     bs.nsel = 0;
   }
   constexpr unsigned kNone = ~0u;  // an empty register slot (valid keys are finite non-negative floats)
-  unsigned kr[kSelCache];
+  constexpr int kCache = kSelCache;
+  unsigned kr[kCache];
   unsigned lo = ~0u, hi = 0u;
 #pragma unroll
-  for (int j = 0; j < kSelCache; j++) {
+  for (int j = 0; j < kCache; j++) {
     const int i = tid + j * nthr;
     kr[j]       = i < n ? kd[i] : kNone;
     if (kr[j] != kNone) {
@@ -771,7 +605,7 @@ __device__ int select_by_bins(const unsigned* __restrict__ kd, const int* __rest
       hi = max(hi, kr[j]);
     }
   }
-  for (int i = tid + kSelCache * nthr; i < n; i += nthr) {
+  for (int i = tid + kCache * nthr; i < n; i += nthr) {
     const unsigned k = kd[i];
     lo               = min(lo, k);
     hi               = max(hi, k);
@@ -794,9 +628,9 @@ __device__ int select_by_bins(const unsigned* __restrict__ kd, const int* __rest
   // every key with its index, registers first (uniform trip counts: the appends below use ballots)
   auto for_keys = [&](auto&& f) {
 #pragma unroll
-    for (int j = 0; j < kSelCache; j++)
+    for (int j = 0; j < kCache; j++)
       f(kr[j], tid + j * nthr, kr[j] != kNone);
-    for (int i0 = kSelCache * nthr; i0 < n; i0 += nthr) {
+    for (int i0 = kCache * nthr; i0 < n; i0 += nthr) {
       const int i = i0 + tid;
       f(i < n ? kd[i] : kNone, i, i < n);
     }
@@ -851,10 +685,26 @@ __device__ int select_by_bins(const unsigned* __restrict__ kd, const int* __rest
   });
   __syncthreads();
   const int ntb = bs.ntb;
-  if (ntb > kTieCap) {  // too many keys in one bin: the radix passes
+  if (ntb > kTieCap) {  // more keys in bin b* than the buffer holds: rank each against every key of b*
+    for (int i = tid; i < n; i += nthr) {
+      const unsigned ki = kd[i];
+      if (((ki - kmin) >> shift) != bstar) continue;
+      const unsigned ii = static_cast<unsigned>(cid[i]);
+      int rank          = 0;
+      for (int j = 0; j < n; j++) {
+        const unsigned kj = kd[j];
+        if (((kj - kmin) >> shift) == bstar && (kj < ki || (kj == ki && static_cast<unsigned>(cid[j]) < ii))) rank++;
+      }
+      if (rank < need) {
+        const int at = atomicAdd(&bs.nsel, 1);
+        sid[at]      = static_cast<int>(ii);
+        if (skey) skey[at] = __uint_as_float(ki);
+      }
+    }
     __syncthreads();
-    select_smallest(kd, cid, n, R, sid, skey, sh.hist, sh.st);
-    return sh.st.nsel;
+    const int ns = bs.nsel;
+    __syncthreads();
+    return ns;
   }
   for (int i = tid; i < ntb; i += nthr) {  // rank of each tie-bin key by (key, id) among them
     const unsigned ki = sh.tkey[i], ii = static_cast<unsigned>(sh.tid[i]);
@@ -883,8 +733,8 @@ __device__ int select_by_bins(const unsigned* __restrict__ kd, const int* __rest
  * 16-byte aligned (D a multiple of 8), and every group has kRows rows in flight.
  */
 template <int LX>
-__device__ void exact_distances_t(const int* sid, int ns, const __half* __restrict__ vectors, int D,
-                                  const float* sq, float* sd)
+__device__ void exact_distances(const int* sid, int ns, const __half* __restrict__ vectors, int D, const float* sq,
+                                float* sd)
 {
   constexpr int kRows = 4, GPW = 64 / LX;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
@@ -1032,7 +882,7 @@ __global__ __launch_bounds__(kKeepThreads) void rerank_keep_kernel(
     sq[i] = Q[static_cast<int64_t>(q) * D + i];
   const int ns = select_by_bins(reinterpret_cast<const unsigned*>(dist + static_cast<int64_t>(q) * W),
                                 cand + static_cast<int64_t>(q) * W, n, R, sid, nullptr, sel);
-  exact_distances_t<LX>(sid, ns, vectors, D, sq, sd);
+  exact_distances<LX>(sid, ns, vectors, D, sq, sd);
   long long* pb = bi + static_cast<int64_t>(q) * KO;
   float* pd     = bd + static_cast<int64_t>(q) * KO;
   int P         = 2;
@@ -1165,7 +1015,7 @@ __global__ __launch_bounds__(kKeepThreads) void final_rerank_kernel(
   }
   __syncthreads();
   const int ns = nsel;
-  exact_distances_t<LX>(sid, ns, vectors, D, sq, sd);
+  exact_distances<LX>(sid, ns, vectors, D, sq, sd);
   int P = 2;
   while (P < R)
     P <<= 1;
@@ -1218,6 +1068,7 @@ void with_lx(int D, F&& f)
 }
 
 }  // namespace
+
 
 void launch_center(const float* q, const float* mu, int64_t m, int D, float* qc, __half* qh,
                    hipStream_t s)
@@ -1403,8 +1254,8 @@ void launch_final_rerank(const long long* si, int m, int KO, int R, const __half
   OCTEX_EXPECTS(R >= k && R <= kMaxRerank && R <= KO,
                 "octex: final_rerank 0 (sketch order) or k <= final_rerank <= 512");
   with_lx(D, [&](auto lx) {
-    final_rerank_kernel<decltype(lx)::value><<<m, kKeepThreads, D * sizeof(float), s>>>(si, KO, R, vectors, D, Q, k,
-                                                                                        bi, bd);
+    final_rerank_kernel<decltype(lx)::value>
+      <<<m, kKeepThreads, D * sizeof(float), s>>>(si, KO, R, vectors, D, Q, k, bi, bd);
   });
   OCTEX_HIP(hipGetLastError());
 }

@@ -79,8 +79,8 @@ auto batch_stages(index_impl const& ix, plan const& pl, hipStream_t s) -> std::v
   });
   add("gather_lists", [&ix, &pl, s, m, S, C] {
     launch_gather(false, pl.seg.as<int2>(), C, pl.lr, m, ix.list_ptr.as<long long>(), nullptr, 0, ix.n, ix.code(),
-                  ix.sketch_pitch, ix.scale.as<float>(), pl.qs.as<float>(), S, pl.W, pl.logW, pl.cand.as<int>(), pl.dist.as<float>(),
-                  pl.nin.as<int>(), s);
+                  ix.sketch_pitch, ix.scale.as<float>(), pl.qs.as<float>(), S, pl.W, pl.logW, pl.cand.as<int>(),
+                  pl.dist.as<float>(), pl.nin.as<int>(), s);
   });
   if (pl.sp.sketch_rank)
     add("sketch_keep", [&pl, s, m] {
