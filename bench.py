@@ -215,20 +215,26 @@ def stage_bytes(name, wave, cnt, m, C, S, D, KO, table_len, starts, w, L):
     return None
 
 
-def measured_traffic(config, params, stage, n):
+def measured_traffic(config, params, stage, n, algorithmic):
     """HBM bytes per launch of a stage from the committed rocprof counter summary of this workload
     (profiles/traffic_<config>.json: FETCH_SIZE and WRITE_SIZE per dispatch, scaled by what the same counters
-    read for a 1 GiB device copy), when it was measured with these search parameters; else None."""
+    read for a 1 GiB device copy).  Measured with the same search parameters: that figure; with others: the
+    measured bytes per algorithmic byte of the stage times this run's algorithmic bytes (labelled so)."""
     path = os.path.join(ROOT, "profiles", f"traffic_{config}.json")
     if not os.path.isfile(path):
-        return None
+        return None, None
     with open(path) as f:
         t = json.load(f)
-    keys = ("read", "starts", "waves", "rerank", "wave_rerank")
-    if t.get("n") != n or any(t.get("params", {}).get(k) != params.get(k) for k in keys):
-        return None
     k = t.get("kernels", {}).get(stage)
-    return None if k is None else int(k["hbm_bytes_per_launch"])
+    if t.get("n") != n or k is None:
+        return None, None
+    keys = ("read", "starts", "waves", "rerank", "wave_rerank")
+    if all(t.get("params", {}).get(x) == params.get(x) for x in keys):
+        return int(k["hbm_bytes_per_launch"]), "rocprof FETCH_SIZE + WRITE_SIZE, same parameters"
+    if k.get("algorithmic_bytes_per_launch"):
+        ratio = k["hbm_bytes_per_launch"] / k["algorithmic_bytes_per_launch"]
+        return int(ratio * algorithmic), f"rocprof bytes per algorithmic byte ({ratio:.3f}) measured at {t['params']}"
+    return None, None
 
 
 def main():
@@ -333,7 +339,7 @@ def main():
     avg_ms = sum(x["ms"] for x in dl) / len(dl)
     avg_bytes = sum(x["bytes"] for x in dl) / len(dl)
     achieved = avg_bytes / (avg_ms * 1e-3) / 1e9
-    traffic = measured_traffic(args.config, params, dominant, X.shape[0])
+    traffic, traffic_source = measured_traffic(args.config, params, dominant, X.shape[0], avg_bytes)
     log(f"probe hits by level {cnt['hit_level'][:int(meta[4])]}, misses {len(Q) * C - cnt['seg_hits']}")
     log("stages: " + ", ".join(f"{x['stage']}[{x['wave']}] {x['ms']:.3f} ms {x['gbs']} GB/s" for x in per_launch))
 
@@ -397,6 +403,7 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            "traffic_source": traffic_source,
             "avg_launch_ms": round(avg_ms, 4),
             "algorithmic_bytes_per_launch": int(avg_bytes),
         },
