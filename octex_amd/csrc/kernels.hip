@@ -329,15 +329,22 @@ __device__ __forceinline__ void sketch_scores(int n, IdOf const& id_of, const si
   const int per_wave = GPW * kRows;
   // Loads are unconditional (past-the-end candidates read the last one, chunkless lanes chunk 0) so
   // that every row of the group is requested before the first one is used.
-  for (int j0 = wid * per_wave; j0 < n; j0 += nw * per_wave) {
-    int id[kRows];
+  const int stride = nw * per_wave;
+  int id[kRows];
+  if (wid * per_wave < n) {
 #pragma unroll
     for (int r = 0; r < kRows; r++)  // candidate j0 + r * GPW + grp
-      id[r] = id_of(min(j0 + r * GPW + grp, n - 1));
+      id[r] = id_of(min(wid * per_wave + r * GPW + grp, n - 1));
+  }
+  for (int j0 = wid * per_wave; j0 < n; j0 += stride) {
     int4 w[kRows];
 #pragma unroll
     for (int r = 0; r < kRows; r++)
       w[r] = *reinterpret_cast<const int4*>(code + static_cast<int64_t>(id[r]) * pitch + (has ? k : 0));
+    int idn[kRows];  // the next rows' ids, read while these rows are in flight
+#pragma unroll
+    for (int r = 0; r < kRows; r++)
+      idn[r] = j0 + stride < n ? id_of(min(j0 + stride + r * GPW + grp, n - 1)) : 0;
     float d[kRows];
 #pragma unroll
     for (int r = 0; r < kRows; r++) {
@@ -359,6 +366,9 @@ __device__ __forceinline__ void sketch_scores(int n, IdOf const& id_of, const si
       const int j = j0 + r * GPW + grp;
       if (j < n && sub == 0) put(j, id[r], d[r]);
     }
+#pragma unroll
+    for (int r = 0; r < kRows; r++)
+      id[r] = idn[r];
   }
 }
 
