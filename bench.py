@@ -42,6 +42,12 @@ CONFIGS = {
     "deep100m": dict(n=100_000_000, d=96, nq=10_000, clusters=10_000, kind="deep", batch=10_000,
                      desc="seeded normalized Gaussian mixture as BASELINE.json configs[3], fp16 rows",
                      index=dict(copies=150, list_len=64, min_cell=10, table_len=64, seed=0)),
+    # configs[2] of BASELINE.json: 1M x 960 non-negative half-normal features (scale 0.05) plus per-cluster offsets
+    # U[0, 0.1] of a 1,000-component mixture, 1,000 queries, batch 1,000; the index as the reference's paper GIST
+    # build (lists of 64, sketch 128, table 64, no reverse edges) with 150 copies
+    "gist1m": dict(n=1_000_000, d=960, nq=1_000, clusters=1000, kind="gist", batch=1_000,
+                   desc="seeded half-normal mixture as BASELINE.json configs[2]",
+                   index=dict(copies=150, list_len=64, table_len=64, sketch_width=128, reverse_edges=False, seed=0)),
     # a small stand-in for quick checks
     "small": dict(n=100_000, d=128, nq=10_000, clusters=100, kind="sift", batch=10_000, desc="small SIFT-like mixture",
                   index=dict(copies=64, list_len=32, table_len=64, min_cell=2, reverse_edges=False, seed=0,
@@ -61,6 +67,15 @@ SWEEP_DEEP = [
     dict(read=32, starts=64, waves=2, rerank=128, wave_rerank=128),
     dict(read=16, starts=128, waves=2, rerank=128, wave_rerank=128),
     dict(read=32, starts=128, waves=2, rerank=128, wave_rerank=256),
+]
+
+SWEEP_GIST = [
+    dict(read=8, starts=32, waves=1, rerank=64, wave_rerank=64),
+    dict(read=16, starts=32, waves=1, rerank=64, wave_rerank=64),
+    dict(read=16, starts=64, waves=1, rerank=64, wave_rerank=64),
+    dict(read=16, starts=64, waves=2, rerank=64, wave_rerank=64),
+    dict(read=32, starts=64, waves=2, rerank=128, wave_rerank=128),
+    dict(read=32, starts=128, waves=2, rerank=128, wave_rerank=128),
 ]
 
 SWEEP = [  # ordered from cheaper to dearer; the fastest one at recall >= 0.99 is timed
@@ -139,6 +154,26 @@ def make_deep(cfg, k, torch):
         if r0 % (1 << 24) == 0:
             log(f"data: {r0 + m:,} of {n:,} rows")
     return X, Q.cpu().numpy(), top.i.cpu().numpy()
+
+
+def make_gist(cfg, torch):
+    """GIST-like rows on the GPU: |N(0, 0.05^2)| features plus a per-cluster offset U[0, 0.1] of one of `clusters`
+    components (torch's CUDA generator, seed 0 for the base and 1 for the queries), fp32 on the host."""
+    d, C, n, nq = cfg["d"], cfg["clusters"], cfg["n"], cfg["nq"]
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0)
+    offs = 0.1 * torch.rand((C, d), generator=g, device="cuda")
+    X = np.empty((n, d), np.float32)
+    step = 1 << 17
+    for r0 in range(0, n, step):
+        m = min(step, n - r0)
+        x = offs[torch.randint(0, C, (m,), generator=g, device="cuda")]
+        X[r0 : r0 + m] = (x + (0.05 * torch.randn((m, d), generator=g, device="cuda")).abs()).cpu().numpy()
+    gq = torch.Generator(device="cuda")
+    gq.manual_seed(1)
+    q = offs[torch.randint(0, C, (nq,), generator=gq, device="cuda")]
+    Q = (q + (0.05 * torch.randn((nq, d), generator=gq, device="cuda")).abs()).cpu().numpy()
+    return X, Q
 
 
 def ground_truth(X, Q, k, torch):
@@ -275,7 +310,7 @@ def main():
         torch.cuda.empty_cache()  # the index needs the memory the ground-truth blocks were cached in
         log(f"data {X.shape} queries {Q.shape} and ground truth in {time.time() - t0:.1f} s")
     else:
-        X, Q = make_data(cfg)
+        X, Q = make_gist(cfg, torch) if cfg["kind"] == "gist" else make_data(cfg)
         log(f"data {X.shape} queries {Q.shape} in {time.time() - t0:.1f} s")
         t0 = time.time()
         gt = ground_truth(X, Q, k, torch)
@@ -291,7 +326,8 @@ def main():
     Qd = torch.from_numpy(Q).cuda()
 
     # the fastest sweep point at recall >= 0.99
-    sweep = [json.loads(args.params)] if args.params else (SWEEP_DEEP if cfg["kind"] == "deep" else SWEEP)
+    sweeps = {"deep": SWEEP_DEEP, "gist": SWEEP_GIST}
+    sweep = [json.loads(args.params)] if args.params else sweeps.get(cfg["kind"], SWEEP)
     chosen, points = None, []
     for p in sweep:
         p = dict(p, batch=cfg["batch"])
