@@ -44,10 +44,12 @@ CONFIGS = {
                      index=dict(copies=150, list_len=64, min_cell=10, table_len=64, seed=0)),
     # configs[2] of BASELINE.json: 1M x 960 non-negative half-normal features (scale 0.05) plus per-cluster offsets
     # U[0, 0.1] of a 1,000-component mixture, 1,000 queries, batch 1,000; the index as the reference's paper GIST
-    # build (lists of 64, sketch 128, table 64, no reverse edges) with 150 copies
+    # build (lists of 64, sketch 128, table 64, no reverse edges) with 150 copies, member lists of cells of >= 16
+    # rows (the reference's GIST build uses exact lists, which this builder does not make)
     "gist1m": dict(n=1_000_000, d=960, nq=1_000, clusters=1000, kind="gist", batch=1_000,
                    desc="seeded half-normal mixture as BASELINE.json configs[2]",
-                   index=dict(copies=150, list_len=64, table_len=64, sketch_width=128, reverse_edges=False, seed=0)),
+                   index=dict(copies=150, list_len=64, min_cell=16, table_len=64, sketch_width=128, reverse_edges=False,
+                              seed=0)),
     # a small stand-in for quick checks
     "small": dict(n=100_000, d=128, nq=10_000, clusters=100, kind="sift", batch=10_000, desc="small SIFT-like mixture",
                   index=dict(copies=64, list_len=32, table_len=64, min_cell=2, reverse_edges=False, seed=0,
@@ -70,12 +72,12 @@ SWEEP_DEEP = [
 ]
 
 SWEEP_GIST = [
-    dict(read=8, starts=32, waves=1, rerank=64, wave_rerank=64),
     dict(read=16, starts=32, waves=1, rerank=64, wave_rerank=64),
-    dict(read=16, starts=64, waves=1, rerank=64, wave_rerank=64),
     dict(read=16, starts=64, waves=2, rerank=64, wave_rerank=64),
     dict(read=32, starts=64, waves=2, rerank=128, wave_rerank=128),
     dict(read=32, starts=128, waves=2, rerank=128, wave_rerank=128),
+    dict(read=64, starts=128, waves=3, rerank=256, wave_rerank=256),
+    dict(read=64, starts=128, waves=4, rerank=512, wave_rerank=512),
 ]
 
 SWEEP = [  # ordered from cheaper to dearer; the fastest one at recall >= 0.99 is timed
