@@ -44,8 +44,9 @@ CONFIGS = {
                      index=dict(copies=150, list_len=64, min_cell=10, table_len=64, seed=0)),
     # configs[2] of BASELINE.json: 1M x 960 non-negative half-normal features (scale 0.05) plus per-cluster offsets
     # U[0, 0.1] of a 1,000-component mixture, 1,000 queries, batch 1,000; the index as the reference's paper GIST
-    # build (lists of 64, sketch 128, table 64, no reverse edges) with 150 copies, member lists of cells of >= 16
-    # rows (the reference's GIST build uses exact lists, which this builder does not make)
+    # build (lists of 64, sketch 128, exact table of 64, no reverse edges) with 150 copies and member lists of cells
+    # of >= 16 rows (the paper's exact lists, --index-params '{"exact_lists": true}', cost 80 s more to build here
+    # and give the same recall on this data)
     "gist1m": dict(n=1_000_000, d=960, nq=1_000, clusters=1000, kind="gist", batch=1_000,
                    desc="seeded half-normal mixture as BASELINE.json configs[2]",
                    index=dict(copies=150, list_len=64, min_cell=16, table_len=64, sketch_width=128, reverse_edges=False,
@@ -73,10 +74,13 @@ SWEEP_DEEP = [
 
 SWEEP_GIST = [
     dict(read=16, starts=32, waves=1, rerank=64, wave_rerank=64),
-    dict(read=16, starts=64, waves=2, rerank=64, wave_rerank=64),
     dict(read=32, starts=64, waves=2, rerank=128, wave_rerank=128),
-    dict(read=32, starts=128, waves=2, rerank=128, wave_rerank=128),
     dict(read=64, starts=128, waves=3, rerank=256, wave_rerank=256),
+    dict(read=32, starts=64, waves=3, rerank=512, wave_rerank=512),
+    dict(read=64, starts=64, waves=4, rerank=512, wave_rerank=512),
+    dict(read=64, starts=128, waves=3, rerank=512, wave_rerank=512),
+    dict(read=64, starts=128, waves=4, rerank=256, wave_rerank=512),
+    dict(read=32, starts=128, waves=4, rerank=512, wave_rerank=512),
     dict(read=64, starts=128, waves=4, rerank=512, wave_rerank=512),
 ]
 
@@ -289,6 +293,8 @@ def main():
     ap.add_argument("--save-index", default=None, help="also write the built index directory here")
     ap.add_argument("--load-index", default=None, help="load this index directory instead of building one")
     ap.add_argument("--n", type=int, default=None, help="override the number of base vectors (a scaled-down run)")
+    ap.add_argument("--index-params", default=None,
+                    help="JSON index parameters merged over the workload's (e.g. exact_lists)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build searches on one GPU; runs on several GPUs are not part of it", file=sys.stderr)
@@ -306,6 +312,8 @@ def main():
     k = 10
     if args.n:
         cfg = dict(cfg, n=args.n)
+    if args.index_params:
+        cfg = dict(cfg, index=dict(cfg["index"], **json.loads(args.index_params)))
     t0 = time.time()
     if cfg["kind"] == "deep":
         X, Q, gt = make_deep(cfg, k, torch)

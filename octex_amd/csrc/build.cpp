@@ -24,6 +24,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <filesystem>
 #include <fstream>
 #include <memory>
@@ -193,7 +194,8 @@ struct reverse_rule {
   int kin, kf, ks, kr, kout;
 };
 
-void merge_reverse(std::vector<int32_t> const& fwd, int64_t n, reverse_rule const& rr, std::vector<int32_t>& table)
+void merge_reverse(std::vector<int32_t> const& fwd, int64_t n, reverse_rule const& rr, std::vector<int32_t>& table,
+                   const float* fdist = nullptr)
 {
   // Every reverse entry (u <- v at forward rank r) goes to the block of 2^16 u's that holds u, by
   // sequential appends per thread (threads own ascending v ranges, so a block's entries arrive in v
@@ -249,8 +251,9 @@ void merge_reverse(std::vector<int32_t> const& fwd, int64_t n, reverse_rule cons
   table.assign(static_cast<size_t>(n) * rr.kout, -1);
   std::atomic<int64_t> next{0};
   run([&](int) {
-    std::vector<int32_t> cu, tmp;
+    std::vector<int32_t> cu, tmp, tmpr;
     std::vector<uint64_t> srt;
+    std::vector<std::pair<uint32_t, int32_t>> kd;  // (distance bits, id) of the kept entries
     std::vector<int32_t> rc(ks + 1);
     const int log_hs = std::max(8, log2_ceil(4 * int64_t{rr.kout}));  // at most a quarter full
     const unsigned hmask = (1u << log_hs) - 1;
@@ -280,14 +283,21 @@ void merge_reverse(std::vector<int32_t> const& fwd, int64_t n, reverse_rule cons
           rc[((eu[i] >> 32) & 0xff) + 1]++;
         for (int r = 0; r < ks; r++)
           rc[r + 1] += rc[r];
-        if (static_cast<int>(tmp.size()) < m) tmp.resize(m);
-        for (int i = 0; i < m; i++)
-          tmp[rc[(eu[i] >> 32) & 0xff]++] = static_cast<int32_t>(eu[i] & 0xffffffffULL);
+        if (static_cast<int>(tmp.size()) < m) {
+          tmp.resize(m);
+          tmpr.resize(m);
+        }
+        for (int i = 0; i < m; i++) {
+          const int at2 = rc[(eu[i] >> 32) & 0xff]++;
+          tmp[at2]      = static_cast<int32_t>(eu[i] & 0xffffffffULL);
+          tmpr[at2]     = static_cast<int32_t>((eu[i] >> 32) & 0xff);
+        }
         // kf forward, up to kr reverse, the other forward entries: the first kout distinct
         int o         = 0;
         int32_t* row  = table.data() + u * rr.kout;
         epoch++;
-        auto add = [&](int32_t v) {
+        kd.clear();
+        auto add = [&](int32_t v, float dv) {
           if (v < 0 || v == u || o >= rr.kout) return;
           unsigned h = (static_cast<uint32_t>(v) * 2654435761u) >> (32 - log_hs);
           for (; stamp[h] == epoch; h = (h + 1) & hmask)
@@ -295,13 +305,25 @@ void merge_reverse(std::vector<int32_t> const& fwd, int64_t n, reverse_rule cons
           stamp[h] = epoch;
           slot[h]  = v;
           row[o++] = v;
+          if (fdist != nullptr) {
+            uint32_t bits;
+            const float c = dv > 0.f ? dv : 0.f;
+            std::memcpy(&bits, &c, sizeof(bits));
+            kd.emplace_back(bits, v);
+          }
         };
+        auto fd = [&](int64_t r, int t) { return fdist != nullptr ? fdist[r * kin + t] : 0.f; };
         for (int t = 0; t < rr.kf; t++)
-          add(fwd[u * kin + t]);
-        for (int t = 0; t < std::min(m, rr.kr); t++)
-          add(tmp[t]);
+          add(fwd[u * kin + t], fd(u, t));
+        for (int t = 0; t < std::min(m, rr.kr); t++)  // a reverse entry's distance: v's forward one to u
+          add(tmp[t], fd(tmp[t], tmpr[t]));
         for (int t = rr.kf; t < kin && o < rr.kout; t++)
-          add(fwd[u * kin + t]);
+          add(fwd[u * kin + t], fd(u, t));
+        if (fdist != nullptr) {  // the kept entries nearest first, ties by id (build_table.cuh:240-251)
+          std::sort(kd.begin(), kd.end());
+          for (size_t t = 0; t < kd.size(); t++)
+            row[t] = kd[t].second;
+        }
       }
     }
   });
@@ -336,6 +358,65 @@ void drop_table(index_impl& ix)
   ix.bytes -= static_cast<int64_t>(ix.table.size);
   ix.table     = dbuf();
   ix.table_len = 0;
+}
+
+/**
+ * The exact neighbor table (build_table.cuh:57-142, 529-554): the k + 1 nearest rows of every row by
+ * brute force on the GPU (knn_rows over the fp16 vectors), the row itself dropped and distances
+ * clamped at zero (drop_self_kernel, :60-74), then reverse edges merged by the half rule (kf = ks =
+ * kr = k / 2) with the kept entries ordered nearest first (merge_rows_kernel, :166-252).
+ */
+void exact_table(index_impl& ix, int k, bool reverse_edges, std::vector<int32_t>& table)
+{
+  const int64_t n = ix.n, d = ix.dim;
+  OCTEX_EXPECTS(k >= 1 && k < n, "octex: table_len must be in [1, n)");
+  OCTEX_EXPECTS(k + 1 <= 128, "octex: the exact neighbor table takes table_len <= 127");
+  const int K = k + 1;
+  hipStream_t s = ix.stream;
+  const __half* xd = ix.vectors.as<__half>();
+  dbuf norms(static_cast<size_t>(n) * sizeof(float));
+  row_norms(xd, n, static_cast<int>(d), norms.as<float>(), s);
+  const int64_t chunk = std::min<int64_t>(n, int64_t{1} << 18);
+  dbuf od(static_cast<size_t>(chunk) * K * sizeof(float)), oi(static_cast<size_t>(chunk) * K * sizeof(int32_t));
+  std::vector<float> hd(static_cast<size_t>(chunk) * K);
+  std::vector<int32_t> hi(static_cast<size_t>(chunk) * K);
+  std::vector<int32_t> fid(static_cast<size_t>(n) * k);
+  std::vector<float> fdist(static_cast<size_t>(n) * k);
+  const auto t0 = std::chrono::steady_clock::now();
+  for (int64_t r0 = 0; r0 < n; r0 += chunk) {
+    const int64_t m = std::min(chunk, n - r0);
+    knn_rows(xd + r0 * d, norms.as<float>() + r0, m, xd, norms.as<float>(), n, static_cast<int>(d), K, od.as<float>(),
+             oi.as<int32_t>(), s);
+    OCTEX_HIP(hipMemcpyAsync(hd.data(), od.ptr, static_cast<size_t>(m) * K * sizeof(float), hipMemcpyDeviceToHost, s));
+    OCTEX_HIP(hipMemcpyAsync(hi.data(), oi.ptr, static_cast<size_t>(m) * K * sizeof(int32_t), hipMemcpyDeviceToHost,
+                             s));
+    OCTEX_HIP(hipStreamSynchronize(s));
+    parallel_for(m, [&](int64_t i0, int64_t i1) {
+      for (int64_t i = i0; i < i1; i++) {
+        int t = 0;
+        for (int j = 0; j < K && t < k; j++) {
+          const int32_t v = hi[i * K + j];
+          if (v == r0 + i) continue;
+          const float dv                 = hd[i * K + j];
+          fid[(r0 + i) * k + t]          = v;
+          fdist[(r0 + i) * k + t]        = v < 0 ? INFINITY : (dv > 0.f ? dv : 0.f);
+          t++;
+        }
+        for (; t < k; t++) {
+          fid[(r0 + i) * k + t]   = -1;
+          fdist[(r0 + i) * k + t] = INFINITY;
+        }
+      }
+    });
+    build_log("exact table: %lld of %lld rows, %.1f s\n", static_cast<long long>(r0 + m), static_cast<long long>(n),
+              seconds_since(t0));
+  }
+  if (reverse_edges) {
+    const int h = std::max(1, k / 2);
+    merge_reverse(fid, n, reverse_rule{k, h, h, h, k}, table, fdist.data());
+  } else {
+    table = std::move(fid);
+  }
 }
 
 /**
@@ -434,8 +515,8 @@ auto build_in_memory(index_params const& params, dataset_view const& x, build_re
   OCTEX_EXPECTS(params.log_buckets >= 1 && params.log_buckets <= 30, "octex: log_buckets in [1, 30]");
   OCTEX_EXPECTS(d % 2 == 0, "octex: the dimension must be even");
   OCTEX_EXPECTS(S % 16 == 0 && S <= 512, "octex: sketch width: a multiple of 16, <= 512");
-  OCTEX_EXPECTS(!params.exact_lists,
-                "octex: exact_lists is not supported by this builder (lists come from the cell members)");
+  const bool exact_lists = params.exact_lists && !params.member_lists;  // member lists first (build_cells.cuh:505)
+  OCTEX_EXPECTS(!exact_lists || l <= 128, "octex: exact lists take list_len <= 128");
   int cur = 0;
   OCTEX_HIP(hipGetDevice(&cur));
   auto impl = std::make_shared<index_impl>();
@@ -537,7 +618,7 @@ auto build_in_memory(index_params const& params, dataset_view const& x, build_re
       for (int j = 0; j < L; j++) {
         const int mc = (params.min_cell > 1 && j < L - 1) ? params.min_cell : 1;
         int* offs    = ix.offsets.as<int32_t>() + (static_cast<int64_t>(c) * L + j) * (T + 1);
-        int64_t M    = cb.level(y.as<float>(), b, params.spacings[j], mc, l, params.log_buckets, offs,
+        int64_t M    = cb.level(y.as<float>(), b, params.spacings[j], mc, l, params.log_buckets, exact_lists, offs,
                                 level_keys[c][j], level_lists[j]);
         rec.base[static_cast<size_t>(c) * L + j]  = static_cast<int32_t>(row);
         rec.cells[static_cast<size_t>(c) * L + j] = M;
@@ -556,7 +637,7 @@ auto build_in_memory(index_params const& params, dataset_view const& x, build_re
       }
       OCTEX_HIP(hipStreamSynchronize(s));
       ix.bytes += static_cast<int64_t>(ix.copy_lists[c].size);
-      if (c == 0 || (c + 1) % 25 == 0 || c + 1 == C) {
+      if (c == 0 || (c + 1) % 25 == 0 || c + 1 == C || exact_lists) {
         size_t fr = 0, tot = 0;
         OCTEX_HIP(hipMemGetInfo(&fr, &tot));
         std::string cells;
@@ -632,11 +713,15 @@ auto build_in_memory(index_params const& params, dataset_view const& x, build_re
   upload(ix.scale.ptr, rec.scale.data(), ix.scale.size, s);
   phase("sketch");
 
-  // neighbor table, searched by this library's search
+  // neighbor table: exact up to exact_table_max rows (build.cu:354-360), else searched by this library's search
   if (k > 0) {
-    index idx(impl);
     std::vector<int32_t> table;
-    searched_table(ix, idx, k, params.reverse_edges, params.table_passes, params.table_sketch_order, table);
+    if (n <= params.exact_table_max) {
+      exact_table(ix, k, params.reverse_edges, table);
+    } else {
+      index idx(impl);
+      searched_table(ix, idx, k, params.reverse_edges, params.table_passes, params.table_sketch_order, table);
+    }
     set_table(ix, table, k);
     phase("table");
   }

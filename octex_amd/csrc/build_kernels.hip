@@ -295,6 +295,243 @@ __global__ void float_to_half_kernel(const float* __restrict__ x, int64_t total,
   if (t < total) out[t] = __float2half_rn(x[t]);
 }
 
+// ------------------------------------------------------------------ exact k nearest neighbors
+
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kKnnQ    = 64;   // query rows per workgroup
+constexpr int kKnnRows = 128;  // database rows per step: 4 waves x 32
+constexpr int kKnnCap  = 256;  // LDS keys per query row: the K kept (K <= 128) and one step's appends
+
+__device__ __forceinline__ float knn_f(__half v) { return __half2float(v); }
+__device__ __forceinline__ float knn_f(float v) { return v; }
+
+/** out[i] = sum of x[i, :]^2 in fp32, sequentially over the coordinates. */
+template <typename T>
+__global__ void row_norms_kernel(const T* __restrict__ x, int64_t n, int d, float* __restrict__ out)
+{
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const T* r = x + i * d;
+  float acc  = 0.f;
+  for (int k = 0; k < d; k++) {
+    float v = knn_f(r[k]);
+    acc     = fmaf(v, v, acc);
+  }
+  out[i] = acc;
+}
+
+/** Four fp16 of row r, columns k..k+3, of a row-major [rows, d] matrix; zeros outside it. */
+__device__ __forceinline__ half4_t knn_h4(const __half* __restrict__ a, int64_t r, int64_t rows, int d, int k,
+                                          bool vec)
+{
+  half4_t v = {0, 0, 0, 0};
+  if (r >= rows) return v;
+  const __half* p = a + r * d + k;
+  if (vec && k + 3 < d) {
+    uint2 u = *reinterpret_cast<const uint2*>(p);
+    v       = *reinterpret_cast<half4_t*>(&u);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      if (k + j < d) v[j] = static_cast<_Float16>(__half2float(p[j]));
+  }
+  return v;
+}
+
+/** Float bits mapped to an unsigned order (negative values first) and back. */
+__device__ __forceinline__ unsigned knn_ord(float x)
+{
+  unsigned u = __float_as_uint(x);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float knn_unord(unsigned o)
+{
+  return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
+}
+
+/**
+ * MFMA fragments of the distance tiles: fp16 rows by v_mfma_f32_16x16x16_f16 (lane l supplies
+ * elements 4 (l / 16) .. + 3 of a 16-wide k step for row l % 16), fp32 rows by
+ * v_mfma_f32_16x16x4_f32 (lane l supplies element l / 16 of a 4-wide k step).  Both leave D[4 (l / 16)
+ * + r][l % 16] in lane l.
+ */
+template <typename T>
+struct knn_op;
+template <>
+struct knn_op<__half> {
+  using frag                 = half4_t;
+  static constexpr int kStep = 16;
+  __device__ static frag load(const __half* a, int64_t r, int64_t rows, int d, int k0, int lane, bool vec)
+  {
+    return knn_h4(a, r, rows, d, k0 + (lane >> 4) * 4, vec);
+  }
+  __device__ static float4_t mma(frag a, frag b, float4_t c)
+  {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct knn_op<float> {
+  using frag                 = float;
+  static constexpr int kStep = 4;
+  __device__ static frag load(const float* a, int64_t r, int64_t rows, int d, int k0, int lane, bool)
+  {
+    const int k = k0 + (lane >> 4);
+    return (r < rows && k < d) ? a[r * d + k] : 0.f;
+  }
+  __device__ static float4_t mma(frag a, frag b, float4_t c)
+  {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+};
+
+/**
+ * Every query row's LDS keys (ordered distance << 32 | row) sorted ascending by a bitonic network over
+ * all kKnnQ x kKnnCap slots (unused slots padded with ~0), the first K kept, the threshold set to the
+ * K-th distance.  Called by the whole workgroup.
+ */
+__device__ void knn_compact(unsigned long long* key, int* cnt, float* tau, int K)
+{
+  __syncthreads();
+  for (int t = threadIdx.x; t < kKnnQ * kKnnCap; t += blockDim.x)
+    if ((t % kKnnCap) >= cnt[t / kKnnCap]) key[t] = ~0ULL;
+  for (int size = 2; size <= kKnnCap; size <<= 1)
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      __syncthreads();
+      for (int t = threadIdx.x; t < kKnnQ * kKnnCap / 2; t += blockDim.x) {
+        const int q = t / (kKnnCap / 2), h = t % (kKnnCap / 2);
+        const int lo = ((h & ~(stride - 1)) << 1) | (h & (stride - 1)), hi = lo | stride;
+        const bool up = (lo & size) == 0;
+        unsigned long long* s = key + q * kKnnCap;
+        const unsigned long long x = s[lo], y = s[hi];
+        if ((x > y) == up) {
+          s[lo] = y;
+          s[hi] = x;
+        }
+      }
+    }
+  __syncthreads();
+  if (threadIdx.x < kKnnQ) {
+    const int q = threadIdx.x, c = min(cnt[q], K);
+    cnt[q]      = c;
+    tau[q]      = c >= K ? knn_unord(static_cast<unsigned>(key[q * kKnnCap + K - 1] >> 32)) : INFINITY;
+  }
+  __syncthreads();
+}
+
+/**
+ * The K nearest database rows X [n, d] of each query row Q [m, d] by squared L2 distance
+ * |q|^2 + |x|^2 - 2 q.x (fp32; the dot products by MFMA, knn_op: fp16 products are exact in fp32 and
+ * accumulated in fp32), ties by row.  A workgroup owns 64 query rows and scans every database row,
+ * 128 per step: wave w computes rows [32 w, 32 w + 32) of the step against the 64 queries as 4 x 2
+ * MFMA tiles (lane l holds rows 4 (l / 16) + r of a 16-row tile for query l % 16).  A distance at or
+ * below its query's threshold is appended to the query's LDS keys; when a query holds more than
+ * kKnnCap - kKnnRows keys after a step, knn_compact keeps the K smallest and lowers the thresholds, so
+ * a step's appends always fit.  out_d / out_i [m, K], sorted; -1 / +inf past the n rows.
+ */
+template <typename T>
+__global__ __launch_bounds__(256) void knn_kernel(const T* __restrict__ Q, const float* __restrict__ qn, int64_t m,
+                                                  const T* __restrict__ X, const float* __restrict__ xn, int64_t n,
+                                                  int d, int K, float* __restrict__ out_d, int* __restrict__ out_i)
+{
+  using op = knn_op<T>;
+  __shared__ unsigned long long key[kKnnQ * kKnnCap];
+  __shared__ int cnt[kKnnQ];
+  __shared__ float tau[kKnnQ];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int64_t q0 = static_cast<int64_t>(blockIdx.x) * kKnnQ;
+  const bool vec   = (d & 3) == 0;
+  const int kq     = (lane >> 4) * 4;
+  if (tid < kKnnQ) {
+    cnt[tid] = 0;
+    tau[tid] = INFINITY;
+  }
+  float qq[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int64_t q = q0 + i * 16 + (lane & 15);
+    qq[i]           = q < m ? qn[q] : 0.f;
+  }
+  __syncthreads();
+  for (int64_t r0 = 0; r0 < n; r0 += kKnnRows) {
+    const int64_t rw = r0 + wid * 32;
+    float4_t acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int t = 0; t < 2; t++)
+        acc[i][t] = float4_t{0.f, 0.f, 0.f, 0.f};
+    typename op::frag a[2], b[4];
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+      a[t] = op::load(X, rw + t * 16 + (lane & 15), n, d, 0, lane, vec);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      b[i] = op::load(Q, q0 + i * 16 + (lane & 15), m, d, 0, lane, vec);
+    for (int k0 = 0; k0 < d; k0 += op::kStep) {
+      typename op::frag na[2], nb[4];  // the next k step's fragments, loaded while this one multiplies
+      const int kn = k0 + op::kStep;
+#pragma unroll
+      for (int t = 0; t < 2; t++)
+        na[t] = op::load(X, rw + t * 16 + (lane & 15), n, d, kn, lane, vec);
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        nb[i] = op::load(Q, q0 + i * 16 + (lane & 15), m, d, kn, lane, vec);
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+          acc[i][t] = op::mma(a[t], b[i], acc[i][t]);
+#pragma unroll
+      for (int t = 0; t < 2; t++)
+        a[t] = na[t];
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        b[i] = nb[i];
+    }
+    float xr[2][4];
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int64_t row = rw + t * 16 + kq + r;
+        xr[t][r]          = row < n ? xn[row] : 0.f;
+      }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int ql   = i * 16 + (lane & 15);
+      const float th = tau[ql];
+#pragma unroll
+      for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int64_t row = rw + t * 16 + kq + r;
+          const float dd    = fmaf(-2.f, acc[i][t][r], qq[i] + xr[t][r]);
+          if (row < n && dd <= th) {
+            const int p           = atomicAdd(&cnt[ql], 1);
+            key[ql * kKnnCap + p] = (static_cast<unsigned long long>(knn_ord(dd)) << 32) |
+                                    static_cast<unsigned>(row);
+          }
+        }
+    }
+    __syncthreads();  // every append of the step is in
+    const int full = tid < kKnnQ && cnt[tid] > kKnnCap - kKnnRows;
+    if (__syncthreads_or(full)) knn_compact(key, cnt, tau, K);
+  }
+  knn_compact(key, cnt, tau, K);
+  for (int t = tid; t < kKnnQ * K; t += blockDim.x) {
+    const int ql = t / K, j = t % K;
+    const int64_t q = q0 + ql;
+    if (q >= m) continue;
+    const bool ok                = j < cnt[ql];
+    const unsigned long long e   = key[ql * kKnnCap + j];
+    out_i[q * K + j]             = ok ? static_cast<int>(e & 0xffffffffULL) : -1;
+    out_d[q * K + j]             = ok ? knn_unord(static_cast<unsigned>(e >> 32)) : INFINITY;
+  }
+}
+
 template <typename T>
 void ensure(dbuf& b, int64_t count)
 {
@@ -349,6 +586,34 @@ void project_rows(const __half* x, int64_t n, int d, const float* mean, const fl
   project_rows_kernel<<<grid_for(n, 256), 256, smem, s>>>(x, n, d, mean, U, shift, w, y);
   OCTEX_HIP(hipGetLastError());
 }
+
+template <typename T>
+void row_norms(const T* x, int64_t n, int d, float* out, hipStream_t s)
+{
+  if (n == 0) return;
+  row_norms_kernel<T><<<grid_for(n, 256), 256, 0, s>>>(x, n, d, out);
+  OCTEX_HIP(hipGetLastError());
+}
+template void row_norms<__half>(const __half*, int64_t, int, float*, hipStream_t);
+template void row_norms<float>(const float*, int64_t, int, float*, hipStream_t);
+
+template <typename T>
+void knn_rows(const T* Q, const float* qn, int64_t m, const T* X, const float* xn, int64_t n, int d, int K,
+              float* out_d, int* out_i, hipStream_t s)
+{
+  OCTEX_EXPECTS(K >= 1 && K <= kKnnCap - kKnnRows, "octex: exact neighbors: at most %d per row",
+                kKnnCap - kKnnRows);
+  OCTEX_EXPECTS(n < (int64_t{1} << 31) && d >= 1, "octex: exact neighbors: at most 2^31 - 1 rows");
+  if (m == 0) return;
+  const int64_t blocks = (m + kKnnQ - 1) / kKnnQ;
+  OCTEX_EXPECTS(blocks < (int64_t{1} << 31), "octex: exact neighbors: too many query rows");
+  knn_kernel<T><<<static_cast<unsigned>(blocks), 256, 0, s>>>(Q, qn, m, X, xn, n, d, K, out_d, out_i);
+  OCTEX_HIP(hipGetLastError());
+}
+template void knn_rows<__half>(const __half*, const float*, int64_t, const __half*, const float*, int64_t, int, int,
+                               float*, int*, hipStream_t);
+template void knn_rows<float>(const float*, const float*, int64_t, const float*, const float*, int64_t, int, int,
+                              float*, int*, hipStream_t);
 
 void half_to_float(const __half* x, int64_t total, float* out, hipStream_t s)
 {
@@ -420,8 +685,8 @@ void cell_builder::reserve(int64_t n_, int w_, hipStream_t s_)
   ensure<unsigned long long>(mkey2, n);
 }
 
-auto cell_builder::level(const float* y, int B, float f, int min_cell, int l, int log_buckets, int* offs_out,
-                         dbuf& keys_out, dbuf& lists_out) -> int64_t
+auto cell_builder::level(const float* y, int B, float f, int min_cell, int l, int log_buckets, bool exact,
+                         int* offs_out, dbuf& keys_out, dbuf& lists_out) -> int64_t
 {
   const int64_t T = int64_t{1} << log_buckets;
   auto g          = grid_for(n, 256);
@@ -478,16 +743,18 @@ auto cell_builder::level(const float* y, int B, float f, int min_cell, int l, in
 #undef OCTEX_CENTER
     }
   }
-  member_key_kernel<<<g, 256, 0, s>>>(y, w, sidx.as<int>(), rid.as<int>(), keep.as<int>(), kidx.as<int>(),
-                                      z.as<float>(), n, mkey.as<unsigned long long>());
-  with_tmp(tmp, [&](void* p, size_t& b) {
-    return rocprim::radix_sort_pairs(p, b, mkey.as<unsigned long long>(), mkey2.as<unsigned long long>(),
-                                     sidx.as<int>(), sidx2.as<int>(), n, 0, 64, s);
-  });
-  if (M > 0)
+  if (!exact) {
+    member_key_kernel<<<g, 256, 0, s>>>(y, w, sidx.as<int>(), rid.as<int>(), keep.as<int>(), kidx.as<int>(),
+                                        z.as<float>(), n, mkey.as<unsigned long long>());
     with_tmp(tmp, [&](void* p, size_t& b) {
-      return rocprim::exclusive_scan(p, b, cpop.as<int>(), cstart.as<int>(), 0, M, rocprim::plus<int>(), s);
+      return rocprim::radix_sort_pairs(p, b, mkey.as<unsigned long long>(), mkey2.as<unsigned long long>(),
+                                       sidx.as<int>(), sidx2.as<int>(), n, 0, 64, s);
     });
+    if (M > 0)
+      with_tmp(tmp, [&](void* p, size_t& b) {
+        return rocprim::exclusive_scan(p, b, cpop.as<int>(), cstart.as<int>(), 0, M, rocprim::plus<int>(), s);
+      });
+  }
   ensure<int>(lists_tmp, static_cast<int64_t>(M) * l);
   ensure<unsigned>(bucket, M);
   ensure<unsigned>(sbucket, M);
@@ -496,8 +763,18 @@ auto cell_builder::level(const float* y, int B, float f, int min_cell, int l, in
   keys_out  = dbuf(static_cast<size_t>(std::max(M, 1)) * sizeof(long long));
   lists_out = dbuf(static_cast<size_t>(std::max<int64_t>(int64_t{M} * l, 1)) * sizeof(int));
   if (M > 0) {
-    list_fill_kernel<<<grid_for(int64_t{M} * l, 256), 256, 0, s>>>(sidx2.as<int>(), cstart.as<int>(), cpop.as<int>(),
-                                                                    M, l, lists_tmp.as<int>());
+    if (exact) {  // the l projected rows nearest to each center, by brute force (build_cells.cuh:506-510, 567-599)
+      ensure<float>(ynorm, n);
+      ensure<float>(znorm, M);
+      ensure<float>(kdist, static_cast<int64_t>(M) * l);
+      row_norms<float>(y, n, w, ynorm.as<float>(), s);
+      row_norms<float>(z.as<float>(), M, w, znorm.as<float>(), s);
+      knn_rows<float>(z.as<float>(), znorm.as<float>(), M, y, ynorm.as<float>(), n, w, l, kdist.as<float>(),
+                      lists_tmp.as<int>(), s);
+    } else {
+      list_fill_kernel<<<grid_for(int64_t{M} * l, 256), 256, 0, s>>>(sidx2.as<int>(), cstart.as<int>(),
+                                                                      cpop.as<int>(), M, l, lists_tmp.as<int>());
+    }
     bucket_kernel<<<grid_for(M, 256), 256, 0, s>>>(ckey.as<long long>(), M, T - 1, bucket.as<unsigned>(),
                                                    seq.as<int>());
     with_tmp(tmp, [&](void* p, size_t& b) {

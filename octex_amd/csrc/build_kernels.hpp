@@ -19,6 +19,17 @@ void sample_rows(const __half* x, int64_t ns, int64_t step, int d, __half* host_
 void project_rows(const __half* x, int64_t n, int d, const float* mean, const float* U, const float* shift, int w,
                   float* y, hipStream_t s);
 void half_to_float(const __half* x, int64_t total, float* out, hipStream_t s);
+/** out [n] = squared norms of the rows x [n, d] (fp16 or fp32), in fp32. */
+template <typename T>
+void row_norms(const T* x, int64_t n, int d, float* out, hipStream_t s);
+/**
+ * The K (<= 128) nearest rows of X [n, d] to each row of Q [m, d] (fp16 or fp32) by squared L2 distance
+ * (fp32 from the squared norms qn / xn and MFMA dot products), ties by row: out_d / out_i [m, K]
+ * ascending, -1 / +inf padded when n < K (device arrays).
+ */
+template <typename T>
+void knn_rows(const T* Q, const float* qn, int64_t m, const T* X, const float* xn, int64_t n, int d, int K,
+              float* out_d, int* out_i, hipStream_t s);
 /** out = fp16(x), round to nearest even (device arrays). */
 void float_to_half(const float* x, int64_t total, __half* out, hipStream_t s);
 /** The int8 sketch: scale = amax / 127 per coordinate, codes [n, pitch] = round(((x - mean) @ basis) / scale). */
@@ -32,16 +43,17 @@ struct cell_builder {
   hipStream_t s = nullptr;
   dbuf keys, skeys, idx, sidx, sidx2, rid, flag, mkey, mkey2, tmp;
   dbuf start, ukey, pop, keep, kidx, ckey, cfirst, cpop, cstart, z, lists_tmp, bucket, sbucket, seq, perm;
+  dbuf ynorm, znorm, kdist;
 
   void reserve(int64_t n, int w, hipStream_t s);
   /**
    * The cells of the projected rows y [n, w] at spacing f: cells of at least min_cell rows, each with
-   * the list of its l members nearest to its center (the nearest repeated when fewer), in (bucket,
-   * id) order.  offs_out [T + 1] (device) receives the CSR over the buckets, keys_out / lists_out
+   * the list of its l members nearest to its center (the nearest repeated when fewer), or with
+   * `exact` the l rows nearest to its center among all n (ties by row), in (bucket, id) order.  offs_out [T + 1] (device) receives the CSR over the buckets, keys_out / lists_out
    * the ids and list rows.  Returns the number of cells.
    */
-  auto level(const float* y, int B, float f, int min_cell, int l, int log_buckets, int* offs_out, dbuf& keys_out,
-             dbuf& lists_out) -> int64_t;
+  auto level(const float* y, int B, float f, int min_cell, int l, int log_buckets, bool exact, int* offs_out,
+             dbuf& keys_out, dbuf& lists_out) -> int64_t;
 };
 
 }  // namespace cuvs::neighbors::octex::detail

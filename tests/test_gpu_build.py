@@ -155,5 +155,100 @@ def test_build_errors(octex, data, tmp_path):
         octex.build(X[:10], tmp_path / "a", copies=2)
     with pytest.raises(OctexError, match="pca_dims must be at least 8 \\* blocks"):
         octex.build(X, tmp_path / "b", copies=2, pca_dims=16, list_len=8, table_len=8)
-    with pytest.raises(OctexError, match="exact_lists is not supported"):
-        octex.build(X, tmp_path / "c", copies=2, exact_lists=True, list_len=8, table_len=8)
+    X = data[0][:300]
+    with pytest.raises(OctexError, match="exact lists take list_len <= 128"):
+        octex.build(X, tmp_path / "c", copies=2, exact_lists=True, list_len=129, table_len=8)
+    with pytest.raises(OctexError, match="table_len <= 127"):
+        octex.build(X, tmp_path / "d", copies=2, list_len=8, table_len=128)
+
+
+def _table(path):
+    return np.load(os.path.join(path, "table.npy"))
+
+
+@pytest.mark.parametrize("n,d,reverse", [(3000, 32, True), (3000, 32, False), (2500, 30, True), (100, 32, True)])
+def test_exact_table_matches_oracle(octex, tmp_path, n, d, reverse):
+    """The exact neighbor table (build_table.cuh:57-142, 529-554) of integer-valued rows, whose squared
+    distances are exact in fp32 and fp64 alike, equals the oracle's row for row: brute force with ties
+    by id, the row itself dropped, reverse edges merged by the half rule and ordered nearest first.
+    d = 30 takes the kernel's unaligned loads, n = 100 a single partial step."""
+    g = np.random.default_rng(n + d)
+    X = g.integers(0, 8, size=(n, d)).astype(np.float32)
+    b = 4 if d >= 32 else 3
+    kw = dict(copies=2, blocks=b, pca_dims=d, list_len=8, table_len=16, log_buckets=10, member_lists=True,
+              reverse_edges=reverse, seed=1)
+    octex.build(X, tmp_path / "gpu", **kw)
+    O.build(X, str(tmp_path / "cpu"), **kw)
+    tg, tc = _table(tmp_path / "gpu"), _table(tmp_path / "cpu")
+    assert tg.shape == (n, 16)
+    assert np.array_equal(tg, tc)
+
+
+def test_exact_table_real_valued(octex, data, tmp_path):
+    """On real-valued rows the forward table holds the exact k nearest (fp64) up to near ties of the
+    fp32 expanded distance |x|^2 + |y|^2 - 2 x.y, nearest first; no self, no duplicates."""
+    X = data[0][:4000]
+    k = 24
+    octex.build(X, tmp_path / "gpu", copies=2, list_len=8, table_len=k, log_buckets=10, reverse_edges=False, seed=1)
+    tg = _table(tmp_path / "gpu")
+    Xh = X.astype(np.float16).astype(np.float64)
+    d2 = (Xh**2).sum(1)[:, None] - 2 * Xh @ Xh.T + (Xh**2).sum(1)[None, :]
+    np.fill_diagonal(d2, np.inf)
+    kth = np.sort(d2, axis=1)[:, k - 1]
+    got = np.take_along_axis(d2, tg.astype(np.int64), 1)
+    assert (tg >= 0).all() and (tg != np.arange(len(X))[:, None]).all()
+    assert all(len(set(r)) == k for r in tg)
+    assert (got <= kth[:, None] * (1 + 1e-5) + 1e-3).all()
+    assert (np.diff(got, axis=1) >= -1e-3 * got[:, 1:]).all()
+
+
+def test_searched_table_when_over_exact_max(octex, data):
+    """Above exact_table_max the table comes from the library's own search (build_table.cuh:557-843): rows
+    without self or duplicates, and an index that still reaches the reference's recall bar."""
+    X, Q, _ = data
+    X = X[:6000]
+    idx, _ = octex.build_in_memory(X, copies=32, seed=4, log_buckets=14, table_len=32, min_cell=4, exact_table_max=0)
+    tab = idx.array("table", np.int32).reshape(len(X), 32)
+    assert (tab < len(X)).all() and (tab != np.arange(len(X))[:, None]).all()
+    gt, _ = exact_knn(X.astype(np.float16).astype(np.float32), Q)
+    D, I = idx.search(Q, k=10)
+    assert recall(I, gt) >= 0.95
+
+
+def test_exact_lists(octex, tmp_path):
+    """exact_lists (build_cells.cuh:506-510, 567-599): the list of every cell holds the l projected rows
+    nearest to the cell's center (f times the E8 point of a member's projection / f), among all rows,
+    up to near ties of fp32 distances; member_lists takes precedence."""
+    X, _ = clustered(n=2000, m=10, d=32, clusters=10, seed=9)
+    path = str(tmp_path / "ex")
+    l = 16
+    octex.build(X, path, copies=2, list_len=l, table_len=8, log_buckets=10, exact_lists=True, seed=5)
+    ix = O.Index(path)
+    Xh = X.astype(np.float16).astype(np.float64)
+    cells = np.load(os.path.join(path, "cells.npy"))
+    checked = 0
+    for c in range(2):
+        proj = np.load(os.path.join(path, "proj.npy"))[c].astype(np.float64)
+        shift = np.load(os.path.join(path, "shift.npy"))[c].astype(np.float64)
+        y = (Xh - ix.mean.astype(np.float64)) @ proj + shift
+        for j, f in enumerate(ix.spacings):
+            M = cells[c, j]
+            keys = ix.keys[c, j, :M]
+            p, h = O.e8_batch((y / f).astype(np.float32), ix.blocks, 1.0)
+            first = {}
+            for r, hv in enumerate(h):
+                first.setdefault(int(hv), r)
+            r0 = ix.base[c, j]
+            rows = ix.lists[c, r0 * l : (r0 + M) * l].reshape(M, l)
+            for ci in range(0, M, max(1, M // 40)):
+                if int(keys[ci]) not in first:
+                    continue  # the member's fp64 projection rounds to another cell
+                z = p[first[int(keys[ci])]].astype(np.float64) * f
+                dz = ((y - z) ** 2).sum(1)
+                lth = np.sort(dz)[l - 1]
+                # the GPU's fp32 |z|^2 + |y|^2 - 2 z.y errs by a few ulp of the norms
+                tol = 1e-5 * ((z**2).sum() + (y**2).sum(1).max()) + 1e-4 * lth
+                assert len(set(rows[ci])) == l
+                assert (dz[rows[ci]] <= lth + tol).all()
+                checked += 1
+    assert checked > 50
