@@ -450,6 +450,9 @@ def main():
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "traffic_source": traffic_source,
+            # the measured HBM bytes as a rate over the same launches, against the same peak
+            "traffic_gbs": round(traffic / (avg_ms * 1e-3) / 1e9, 1) if traffic else None,
+            "traffic_frac": round(traffic / (avg_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) if traffic else None,
             "avg_launch_ms": round(avg_ms, 4),
             "algorithmic_bytes_per_launch": int(avg_bytes),
         },

@@ -71,60 +71,88 @@ __device__ __forceinline__ half4_t load_h4(const __half* __restrict__ a, int r, 
  * computes a 64-query x 64-output tile as 4 x 4 v_mfma_f32_16x16x16_f16 tiles (A = 16 outputs x 16 k
  * of ucatT, B = 16 k x 16 queries of qh), so each fragment it loads feeds four MFMAs; fp32
  * accumulation over k in steps of 16, the fp16 shift added in fp32 and one rounding to fp16.  Lane l
- * holds D[4 (l / 16) + r][l % 16]: 4 consecutive outputs of one query, stored as one 8-byte write.
- * A workgroup is 4 waves along the outputs (64 queries x 256 outputs).
+ * holds D[4 (l / 16) + r][l % 16]: 4 consecutive outputs of one query, written to an LDS tile and
+ * stored by rows, 16 bytes per lane.  A workgroup is 4 waves along the outputs (64 queries x 256
+ * outputs).  The fragments of 4 k steps are loaded before their MFMAs and the shift before the
+ * products, so a wave's loads overlap.
  */
 __global__ __launch_bounds__(256) void project_kernel(const __half* __restrict__ qh,
                                                       const __half* __restrict__ ucatT,
                                                       const __half* __restrict__ shift, int m, int K,
                                                       int N, __half* __restrict__ Y)
 {
+  __shared__ __align__(16) __half tile[4][64][72];  // a wave's 64 x 64 outputs, rows padded to 144 bytes
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int q0   = blockIdx.x * 64;
   const int n0   = (blockIdx.y * 4 + wid) * 64;
-  if (n0 >= N) return;  // no barriers below: a wave past the outputs just ends
+  const bool active = n0 < N;  // a wave past the outputs computes nothing but meets the barrier
   const bool vec = (K & 3) == 0;
   const int kq   = (lane >> 4) * 4;
+  // the shift of this lane's 16 outputs, read once and in flight during the products
+  float sh[4][4];
+#pragma unroll
+  for (int t = 0; t < 4; t++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int nb = n0 + t * 16 + kq + r;
+      sh[t][r]     = nb < N ? __half2float(shift[nb]) : 0.f;
+    }
   float4_t acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; i++)
 #pragma unroll
     for (int t = 0; t < 4; t++)
       acc[i][t] = float4_t{0.f, 0.f, 0.f, 0.f};
-  for (int k0 = 0; k0 < K; k0 += 16) {
-    half4_t a[4], b[4];
+  // k in chunks of 4 steps of 16: a chunk's 32 fragment loads are issued back to back, so a wave waits
+  // for memory once per chunk rather than once per step
+  constexpr int kChunk = 4;
+  for (int c0 = 0; active && c0 < K; c0 += 16 * kChunk) {
+    half4_t a[kChunk][4], b[kChunk][4];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-      b[i] = load_h4(qh, q0 + i * 16 + (lane & 15), m, K, k0 + kq, vec);
+    for (int j = 0; j < kChunk; j++) {
+      if (c0 + 16 * j >= K) break;  // uniform: the steps past K of a partial last chunk
+      const int k = c0 + 16 * j + kq;
 #pragma unroll
-    for (int t = 0; t < 4; t++)
-      a[t] = load_h4(ucatT, n0 + t * 16 + (lane & 15), N, K, k0 + kq, vec);
-#pragma unroll
-    for (int i = 0; i < 4; i++)
+      for (int i = 0; i < 4; i++)
+        b[j][i] = load_h4(qh, q0 + i * 16 + (lane & 15), m, K, k, vec);
 #pragma unroll
       for (int t = 0; t < 4; t++)
-        acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x16f16(a[t], b[i], acc[i][t], 0, 0, 0);
+        a[j][t] = load_h4(ucatT, n0 + t * 16 + (lane & 15), N, K, k, vec);
+    }
+#pragma unroll
+    for (int j = 0; j < kChunk; j++) {
+      if (c0 + 16 * j >= K) break;
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+          acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x16f16(a[j][t], b[j][i], acc[i][t], 0, 0, 0);
+    }
   }
+  // the tile through LDS: lane l holds 4 consecutive outputs of query l % 16 per MFMA tile, so direct
+  // stores would write every 128-byte line of Y in four 32-byte pieces; read back by rows, a lane
+  // stores 16 bytes and 8 lanes a whole line
+  if (active) {
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int ql = q0 + i * 16 + (lane & 15);
-    if (ql >= m) continue;
-    __half* yrow = Y + static_cast<int64_t>(ql) * N;
+    for (int i = 0; i < 4; i++)
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-      const int nb = n0 + t * 16 + kq;
-      __half o[4];
-#pragma unroll
-      for (int r = 0; r < 4; r++)
-        o[r] = __float2half(acc[i][t][r] + (nb + r < N ? __half2float(shift[nb + r]) : 0.f));
-      if (nb + 3 < N && (N & 3) == 0) {
-        *reinterpret_cast<uint2*>(yrow + nb) = *reinterpret_cast<uint2*>(o);
-      } else {
+      for (int t = 0; t < 4; t++) {
+        __half o[4];
 #pragma unroll
         for (int r = 0; r < 4; r++)
-          if (nb + r < N) yrow[nb + r] = o[r];
+          o[r] = __float2half(acc[i][t][r] + sh[t][r]);
+        *reinterpret_cast<uint2*>(&tile[wid][i * 16 + (lane & 15)][t * 16 + kq]) = *reinterpret_cast<uint2*>(o);
       }
-    }
+  }
+  __syncthreads();
+  if (!active) return;
+#pragma unroll
+  for (int pass = 0; pass < 8; pass++) {
+    const int row = pass * 8 + (lane >> 3), col = (lane & 7) * 8;
+    const int q = q0 + row, nb = n0 + col;
+    if (q < m && nb < N)  // N is a multiple of 8: a lane's 8 outputs are all in or all out
+      *reinterpret_cast<uint4*>(Y + static_cast<int64_t>(q) * N + nb) =
+        *reinterpret_cast<const uint4*>(&tile[wid][row][col]);
   }
 }
 
@@ -1102,6 +1130,7 @@ void launch_project(const __half* qh, const __half* ucatT, const __half* shift, 
 {
   if (m == 0 || N == 0) return;
   OCTEX_EXPECTS(K >= 1, "octex: projection needs a positive dimension");
+  OCTEX_EXPECTS(N % 8 == 0, "octex: projection outputs must be a multiple of 8 (copies x 8 blocks)");
   dim3 grid(static_cast<unsigned>((m + 63) / 64), static_cast<unsigned>((N + 255) / 256));
   project_kernel<<<grid, 256, 0, s>>>(qh, ucatT, shift, m, K, N, Y);
   OCTEX_HIP(hipGetLastError());

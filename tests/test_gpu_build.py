@@ -252,3 +252,14 @@ def test_exact_lists(octex, tmp_path):
                 assert (dz[rows[ci]] <= lth + tol).all()
                 checked += 1
     assert checked > 50
+
+
+def test_exact_table_reference_rule(octex, tmp_path):
+    """The GPU builder's exact table with reverse edges meets the reference's own test of it
+    (test_build.cu:266-377, mode 0)."""
+    from test_oracle import check_exact_table, table_mode_data
+
+    x, k = table_mode_data(), 12
+    octex.build(x, tmp_path / "t", copies=2, blocks=2, pca_dims=16, list_len=8, log_buckets=10, sketch_width=16,
+                table_len=k, reverse_edges=True, seed=0)
+    check_exact_table(_table(tmp_path / "t"), x, k)

@@ -382,6 +382,8 @@ def test_stage_errors(L):
     with pytest.raises(OctexError, match="blocks must be 1-6 or 8"):
         x = torch.zeros((4, 56), device="cuda")
         L.call("octexStageE8", P(x), i64(4), i32(7), ct.c_float(1.0), P(x), P(x), None)
+    with pytest.raises(OctexError, match="multiple of 8"):
+        L.call("octexStageProject", P(x), P(x), P(x), i32(4), i32(8), i32(36), P(x), None)
     with pytest.raises(OctexError, match="rerank in \\[1, 512\\]"):
         L.call("octexStageRerankKeep", P(x), P(x), P(x), i32(1), i32(2048), P(x), i32(64), P(x), i32(600), i32(10),
                P(x), P(x), i32(1), None)

@@ -322,3 +322,60 @@ def test_index_directory_format(small_index):
             b = k & (T - 1)
             assert (np.diff(b) >= 0).all()  # (bucket, hash) order
             assert np.array_equal(np.searchsorted(b, np.arange(T + 1)), offs[c, j])
+
+
+def table_mode_data(n=1500, d=32, seed=5):
+    """The rows of the reference's table test (test_build.cu:268-277): N(0, 1) plus i % 23 on the first 3
+    coordinates."""
+    g = np.random.default_rng(seed)
+    x = g.standard_normal((n, d)).astype(np.float32)
+    x[:, :3] += (np.arange(n) % 23).astype(np.float32)[:, None]
+    return x
+
+
+def check_exact_table(table, x, k):
+    """The reference's check of an exact table with reverse edges (test_build.cu:278-377): the exact top k of
+    every row (fp64 over the fp16 rows, self excluded); the expected row by the prototype rule (first k/2
+    forward, up to k/2 reverse entries of rank < k/2 by (rank, id), then the rest forward, duplicates dropped,
+    cut to k); every table row complete, without self or duplicates, sorted by distance, and its entries in
+    the expected row (at most 1 in 1000 outside, for near ties)."""
+    n = len(x)
+    xh = x.astype(np.float16).astype(np.float64)
+    d2 = (xh**2).sum(1)[:, None] - 2 * xh @ xh.T + (xh**2).sum(1)[None, :]
+    np.fill_diagonal(d2, np.inf)
+    exact = np.argsort(d2, axis=1, kind="stable")[:, :k]
+    h = k // 2
+    rv = [[] for _ in range(n)]
+    for v in range(n):
+        for r in range(h):
+            rv[exact[v, r]].append((r, v))
+    outside = 0
+    for u in range(n):
+        cand = list(exact[u, :h]) + [v for _, v in sorted(rv[u])[:h]] + list(exact[u, h:])
+        expect = []
+        for v in cand:
+            if len(expect) < k and v not in expect:
+                expect.append(v)
+        row = table[u]
+        assert (row >= 0).all() and (row != u).all() and len(set(row.tolist())) == k
+        dv = d2[u, row]
+        assert (np.diff(dv) >= -1e-3 * (1 + dv[:-1])).all()
+        outside += int(np.sum(~np.isin(row, expect)))
+    assert outside <= n * k // 1000
+
+
+def test_exact_table_rule(tmp_path):
+    """The oracle's exact neighbor table with reverse edges meets the reference's own test of it."""
+    x, k = table_mode_data(), 12
+    O.build(x, str(tmp_path / "t"), copies=2, blocks=2, pca_dims=16, list_len=8, log_buckets=10, sketch_width=16,
+            table_len=k, reverse_edges=True, member_lists=True, seed=0)
+    check_exact_table(np.load(tmp_path / "t" / "table.npy"), x, k)
+
+
+def test_exact_table_rule_catches_a_wrong_merge(tmp_path):
+    """The check fails on the forward-only table (reverse edges dropped): it is not vacuous."""
+    x, k = table_mode_data(), 12
+    O.build(x, str(tmp_path / "f"), copies=2, blocks=2, pca_dims=16, list_len=8, log_buckets=10, sketch_width=16,
+            table_len=k, reverse_edges=False, member_lists=True, seed=0)
+    with pytest.raises(AssertionError):
+        check_exact_table(np.load(tmp_path / "f" / "table.npy"), x, k)
