@@ -42,6 +42,15 @@ CONFIGS = {
     "deep100m": dict(n=100_000_000, d=96, nq=10_000, clusters=10_000, kind="deep", batch=10_000,
                      desc="seeded normalized Gaussian mixture as BASELINE.json configs[3], fp16 rows",
                      index=dict(copies=150, list_len=64, min_cell=10, table_len=64, seed=0)),
+    # configs[4] of BASELINE.json (1B rows, fp16 vectors in pinned host memory, sketch-rank search) at a tenth of its
+    # size: a 1B index does not build within one GPU session here.  The rows of deep100m; the index as configs[4]
+    # (lists of 16, searched table of 32, sketch 96 in HBM) with the vectors moved to pinned host memory after the
+    # build; sketch-rank search with a final exact rerank of 32 over the host link (frontier_deep1B.jsonl:41 of
+    # the reference: read 16, starts 512, waves 5)
+    "deep100m-host": dict(n=100_000_000, d=96, nq=10_000, clusters=10_000, kind="deep", batch=10_000,
+                          desc="seeded normalized Gaussian mixture as BASELINE.json configs[3]/[4], fp16 rows, "
+                               "vectors in pinned host memory",
+                          index=dict(copies=150, list_len=16, min_cell=10, table_len=32, seed=0), host=("vectors",)),
     # configs[2] of BASELINE.json: 1M x 960 non-negative half-normal features (scale 0.05) plus per-cluster offsets
     # U[0, 0.1] of a 1,000-component mixture, 1,000 queries, batch 1,000; the index as the reference's paper GIST
     # build (lists of 64, sketch 128, exact table of 64, no reverse edges) with 150 copies and member lists of cells
@@ -51,6 +60,13 @@ CONFIGS = {
                    desc="seeded half-normal mixture as BASELINE.json configs[2]",
                    index=dict(copies=150, list_len=64, min_cell=16, table_len=64, sketch_width=128, reverse_edges=False,
                               seed=0)),
+    # configs[0] of BASELINE.json, the reference's CPU-runnable case: 100k rows, d = 128, of a 100-component
+    # Gaussian mixture (centroids N(0, 1), sigma 0.3), 1,000 queries, the reference's default index (200 copies,
+    # lists of 64, exact table of 64 with reverse edges) but for log_buckets 16; the search sweep ends at the
+    # default read 32 / starts 128 / waves 2
+    "cpu100k": dict(n=100_000, d=128, nq=1_000, clusters=100, kind="gauss", batch=1_000,
+                    desc="seeded Gaussian mixture as BASELINE.json configs[0]",
+                    index=dict(log_buckets=16, seed=0)),
     # a small stand-in for quick checks
     "small": dict(n=100_000, d=128, nq=10_000, clusters=100, kind="sift", batch=10_000, desc="small SIFT-like mixture",
                   index=dict(copies=64, list_len=32, table_len=64, min_cell=2, reverse_edges=False, seed=0,
@@ -82,6 +98,13 @@ SWEEP_GIST = [
     dict(read=64, starts=128, waves=4, rerank=256, wave_rerank=512),
     dict(read=32, starts=128, waves=4, rerank=512, wave_rerank=512),
     dict(read=64, starts=128, waves=4, rerank=512, wave_rerank=512),
+]
+
+SWEEP_HOST = [  # sketch-rank mode: the exact distances only in the final rerank, over the host link
+    dict(read=16, starts=128, waves=3, rerank=128, wave_rerank=128, sketch_rank=True, final_rerank=32),
+    dict(read=16, starts=256, waves=4, rerank=128, wave_rerank=128, sketch_rank=True, final_rerank=32),
+    dict(read=16, starts=512, waves=5, rerank=128, wave_rerank=128, sketch_rank=True, final_rerank=32),
+    dict(read=32, starts=512, waves=5, rerank=128, wave_rerank=128, sketch_rank=True, final_rerank=64),
 ]
 
 SWEEP = [  # ordered from cheaper to dearer; the fastest one at recall >= 0.99 is timed
@@ -162,6 +185,27 @@ def make_deep(cfg, k, torch):
     return X, Q.cpu().numpy(), top.i.cpu().numpy()
 
 
+def make_gauss(cfg):
+    """Gaussian mixture: centroids N(0, 1)^d, rows = centroid + 0.3 N(0, 1) (data seed 0, queries 1)."""
+    d, C = cfg["d"], cfg["clusters"]
+    g = np.random.default_rng(0)
+    centers = g.standard_normal((C, d), dtype=np.float32)
+    X = (centers[g.integers(0, C, cfg["n"])] + 0.3 * g.standard_normal((cfg["n"], d), dtype=np.float32))
+    gq = np.random.default_rng(1)
+    Q = centers[gq.integers(0, C, cfg["nq"])] + 0.3 * gq.standard_normal((cfg["nq"], d), dtype=np.float32)
+    return X.astype(np.float32), Q.astype(np.float32)
+
+
+def distance_error(X, Q, D, I, rows=1000):
+    """Largest relative error of the returned distances against fp64 distances over the fp16 rows (first rows
+    queries)."""
+    Qs, Ds, Is = Q[:rows].astype(np.float64), np.asarray(D[:rows], np.float64), np.asarray(I[:rows])
+    V = np.asarray(X[np.clip(Is, 0, None).ravel()], dtype=np.float16).astype(np.float64).reshape(*Is.shape, -1)
+    exact = ((V - Qs[:, None, :]) ** 2).sum(-1)
+    ok = Is >= 0
+    return float(np.max(np.abs(Ds[ok] - exact[ok]) / np.maximum(exact[ok], 1e-12)))
+
+
 def make_gist(cfg, torch):
     """GIST-like rows on the GPU: |N(0, 0.05^2)| features plus a per-cluster offset U[0, 0.1] of one of `clusters`
     components (torch's CUDA generator, seed 0 for the base and 1 for the queries), fp32 on the host."""
@@ -238,8 +282,14 @@ def time_search(index, Qd, k, params, steps, warmup, torch):
     return (time.perf_counter() - t0) / steps
 
 
-def stage_bytes(name, wave, cnt, m, C, S, D, KO, table_len, starts, w, L):
+def stage_bytes(name, wave, cnt, m, C, S, D, KO, table_len, starts, w, L, FR=0, k=10):
     """Algorithmic bytes of one launch: every distinct row read once at its natural size (no cache-line inflation)."""
+    if name == "sketch_keep":
+        return cnt["distinct1"] * 8 + m * 24 * KO
+    if name == "sketch_keep_wave":
+        return cnt["distinct2"][wave] * 8 + m * 24 * KO
+    if name == "final_rerank":  # FR rows per query (from host memory when the vectors are there)
+        return m * (FR * 2 * D + 12 * KO + 4 * D + 12 * k)
     if name == "gather_lists":
         return m * C * 8 + cnt["entries1"] * 4 + cnt["distinct1"] * (S + 8) + m * (S * 4 + 4)
     if name == "gather_rows":
@@ -320,7 +370,8 @@ def main():
         torch.cuda.empty_cache()  # the index needs the memory the ground-truth blocks were cached in
         log(f"data {X.shape} queries {Q.shape} and ground truth in {time.time() - t0:.1f} s")
     else:
-        X, Q = make_gist(cfg, torch) if cfg["kind"] == "gist" else make_data(cfg)
+        X, Q = {"gist": lambda: make_gist(cfg, torch), "gauss": lambda: make_gauss(cfg)}.get(
+            cfg["kind"], lambda: make_data(cfg))()
         log(f"data {X.shape} queries {Q.shape} in {time.time() - t0:.1f} s")
         t0 = time.time()
         gt = ground_truth(X, Q, k, torch)
@@ -333,11 +384,15 @@ def main():
     else:
         index, build_s = octex_amd.build_in_memory(X, path=args.save_index, **cfg["index"])
         log(f"index built in {build_s:.1f} s: {index}, {index.device_bytes[0] / 2**30:.1f} GiB")
+    if cfg.get("host"):  # the load placements of the workload: arrays moved to pinned host memory
+        index.place_on_host(**{a: True for a in cfg["host"]})
+        log(f"{', '.join(cfg['host'])} moved to pinned host memory: {index.device_bytes[0] / 2**30:.1f} GiB in HBM")
     Qd = torch.from_numpy(Q).cuda()
 
     # the fastest sweep point at recall >= 0.99
     sweeps = {"deep": SWEEP_DEEP, "gist": SWEEP_GIST}
-    sweep = [json.loads(args.params)] if args.params else sweeps.get(cfg["kind"], SWEEP)
+    sweep = [json.loads(args.params)] if args.params else (SWEEP_HOST if cfg.get("host") else sweeps.get(cfg["kind"],
+                                                                                                        SWEEP))
     chosen, points = None, []
     for p in sweep:
         p = dict(p, batch=cfg["batch"])
@@ -368,6 +423,7 @@ def main():
     qps = len(Q) / sec
     D_, I_ = index.search(Qd, k=k, **params)
     rec = recall(I_.cpu().numpy(), gt)
+    derr = distance_error(X, Q, D_.cpu().numpy(), I_.cpu().numpy())
     log(f"timed: {sec * 1e3:.3f} ms per batch of {len(Q)}, {qps:,.0f} QPS, recall {rec:.4f}")
     info = index.plan_info()
     meta = index.array("meta", np.int64)
@@ -376,7 +432,8 @@ def main():
     for name, ms in stages:
         wv = waves_seen.get(name, 0)
         waves_seen[name] = wv + 1
-        b = stage_bytes(name, wv, cnt, len(Q), C, S, D, info["KO"], int(meta[8]), params["starts"], w, int(meta[4]))
+        b = stage_bytes(name, wv, cnt, len(Q), C, S, D, info["KO"], int(meta[8]), params["starts"], w, int(meta[4]),
+                        FR=info["final_rerank"], k=k)
         per_launch.append(dict(stage=name, wave=wv, ms=round(ms, 4), bytes=b,
                                gbs=round(b / (ms * 1e-3) / 1e9, 1) if b else None))
         totals[name] = totals.get(name, 0.0) + ms
@@ -433,8 +490,10 @@ def main():
             "workload": f"{args.config}: {X.shape[0]} x {X.shape[1]} {cfg['kind']}-like mixture, {len(Q)} queries, "
                         f"k=10, batch {cfg['batch']}",
             "index": cfg["index"],
+            "host_arrays": list(cfg.get("host", ())),
             "search": params,
             "recall@10": round(rec, 5),
+            "distance_max_rel_err": derr,
             "recall_target_met": rec >= 0.99,
             "build_seconds": round(build_s, 1) if build_s is not None else None,
             "index_gib": round(index.device_bytes[0] / 2**30, 2),

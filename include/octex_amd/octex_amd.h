@@ -76,6 +76,15 @@ cuvsError_t octexIndexCopyArrayRanges(cuvsOctexIndex_t index, const char* name, 
 /** The cached plan's shape: {m, k, KO, lr, W, W2, rerank, wave_rerank, final_rerank, graph?}. */
 cuvsError_t octexIndexPlanInfo(cuvsOctexIndex_t index, int32_t* info);
 
+/**
+ * Move the fp16 vectors, the neighbor table and / or the sketch of an index (nonzero flags) from HBM to
+ * pinned host memory, where the kernels read them over the host link: the placements vectors_on_host,
+ * table_on_host and sketch = host of load_params (load.cu:159-185, 444-476) for an index built in
+ * memory.  Cached search plans are dropped.  No counterpart in the reference, whose builder always
+ * writes a directory that load() then places.
+ */
+cuvsError_t octexIndexPlaceOnHost(cuvsOctexIndex_t index, int32_t vectors, int32_t table, int32_t sketch);
+
 /* ---- stage entry points (fp16 arrays as raw 16-bit words) ---- */
 
 /** qc = q - mu, qh = fp16(qc) (search_kernels.cuh:57-69). */

@@ -503,6 +503,30 @@ extern "C" cuvsError_t octexIndexProfileBatch(cuvsOctexIndex_t index, cuvsOctexS
   });
 }
 
+extern "C" cuvsError_t octexIndexPlaceOnHost(cuvsOctexIndex_t index, int32_t vectors, int32_t table, int32_t sketch)
+{
+  return translate_exceptions([=] {
+    auto& ix = as_index(*index)->impl();
+    OCTEX_HIP(hipSetDevice(ix.device));
+    OCTEX_HIP(hipStreamSynchronize(ix.stream));
+    {
+      std::lock_guard<std::mutex> lock(ix.mu);
+      ix.plans.clear();  // cached plans and their graphs hold the arrays' device addresses
+    }
+    auto move = [&](octex::detail::dbuf& d, octex::detail::hbuf& h) {
+      if (d.ptr == nullptr) return;  // on the host already, or absent
+      octex::detail::hbuf to(d.size);
+      OCTEX_HIP(hipMemcpy(to.ptr, d.ptr, d.size, hipMemcpyDeviceToHost));
+      ix.bytes -= static_cast<int64_t>(d.size);
+      d = octex::detail::dbuf();
+      h = std::move(to);
+    };
+    if (vectors != 0) move(ix.vectors, ix.host_vectors);
+    if (table != 0) move(ix.table, ix.host_table);
+    if (sketch != 0) move(ix.sketch, ix.host_sketch);
+  });
+}
+
 namespace {
 
 /** The device (or pinned host) bytes of an index array by name: lists of one copy, or a whole array. */

@@ -295,6 +295,13 @@ class Index:
                         distinct2=c[20:36], reranked2=c[36:52], hit_level=c[52:60])
         return stages, counters
 
+    def place_on_host(self, vectors=True, table=False, sketch=False):
+        """Move the vectors / neighbor table / sketch to pinned host memory (the load placements
+        vectors_on_host, table_on_host and sketch="host" for an index built in memory)."""
+        _lib.call("octexIndexPlaceOnHost", self._handle, ct.c_int32(int(bool(vectors))),
+                  ct.c_int32(int(bool(table))), ct.c_int32(int(bool(sketch))))
+        return self
+
     def plan_info(self):
         arr = (ct.c_int32 * 10)()
         _lib.call("octexIndexPlanInfo", self._handle, arr)

@@ -263,3 +263,24 @@ def test_exact_table_reference_rule(octex, tmp_path):
     octex.build(x, tmp_path / "t", copies=2, blocks=2, pca_dims=16, list_len=8, log_buckets=10, sketch_width=16,
                 table_len=k, reverse_edges=True, seed=0)
     check_exact_table(_table(tmp_path / "t"), x, k)
+
+
+def test_place_on_host_keeps_results(octex, data):
+    """Vectors, table and sketch moved to pinned host memory after an in-memory build (the load placements
+    vectors_on_host, table_on_host, sketch = host) give the same results, in both search modes, with the
+    device bytes reduced by their size."""
+    X, Q, _ = data
+    X = X[:5000]
+    idx, _ = octex.build_in_memory(X, copies=16, seed=6, log_buckets=12, table_len=32)
+    p = dict(read=16, starts=64, waves=2)
+    ps = dict(p, sketch_rank=True, final_rerank=32)
+    before = [idx.search(Q, k=10, **p), idx.search(Q, k=10, **ps)]
+    dev0 = idx.device_bytes[0]
+    idx.place_on_host(vectors=True, table=True, sketch=True)
+    moved = len(X) * (64 * 2 + 32 * 4) + idx.array_size("sketch")
+    assert idx.device_bytes[0] == dev0 - moved
+    after = [idx.search(Q, k=10, **p), idx.search(Q, k=10, **ps)]
+    for (D0, I0), (D1, I1) in zip(before, after):
+        assert np.array_equal(I0, I1) and np.array_equal(D0, D1)
+    idx.place_on_host(vectors=True)  # a second call moves nothing
+    assert idx.device_bytes[0] == dev0 - moved
