@@ -80,8 +80,9 @@ cuvsError_t octexIndexPlanInfo(cuvsOctexIndex_t index, int32_t* info);
  * Move the fp16 vectors, the neighbor table and / or the sketch of an index (nonzero flags) from HBM to
  * pinned host memory, where the kernels read them over the host link: the placements vectors_on_host,
  * table_on_host and sketch = host of load_params (load.cu:159-185, 444-476) for an index built in
- * memory.  Cached search plans are dropped.  No counterpart in the reference, whose builder always
- * writes a directory that load() then places.
+ * memory.  Cached search plans are dropped.  Searches of the index from other threads wait for it, and the
+ * device copies are freed only after the work already on the index's stream.  No counterpart in the reference,
+ * whose builder always writes a directory that load() then places.
  */
 cuvsError_t octexIndexPlaceOnHost(cuvsOctexIndex_t index, int32_t vectors, int32_t table, int32_t sketch);
 

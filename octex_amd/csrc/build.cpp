@@ -334,6 +334,7 @@ void merge_reverse(std::vector<int32_t> const& fwd, int64_t n, reverse_rule cons
 /** The neighbor rows [n, k] of an in-memory index, replacing its table (the reference's set_table). */
 void set_table(index_impl& ix, std::vector<int32_t> const& rows, int k)
 {
+  std::lock_guard<std::mutex> run(ix.stream_mu);
   {
     std::lock_guard<std::mutex> lock(ix.mu);
     ix.plans.clear();
@@ -351,6 +352,7 @@ void set_table(index_impl& ix, std::vector<int32_t> const& rows, int k)
 
 void drop_table(index_impl& ix)
 {
+  std::lock_guard<std::mutex> run(ix.stream_mu);
   {
     std::lock_guard<std::mutex> lock(ix.mu);
     ix.plans.clear();

@@ -381,6 +381,7 @@ extern "C" cuvsError_t octexIndexCopyPlanBuffer(cuvsOctexIndex_t index, const ch
 {
   return translate_exceptions([=] {
     auto& ix = as_index(*index)->impl();
+    std::lock_guard<std::mutex> run(ix.stream_mu);
     std::shared_ptr<octex::detail::plan> pl;
     {
       std::lock_guard<std::mutex> lock(ix.mu);
@@ -471,12 +472,13 @@ extern "C" cuvsError_t octexIndexProfileBatch(cuvsOctexIndex_t index, cuvsOctexS
     }
     // a normal search first: the plan, and the queries in its buffer
     octex::detail::search_impl(r, p, idx, qh, nq, ix.dim, nb.data(), nd.data(), k, true, false);
+    std::lock_guard<std::mutex> run(ix.stream_mu);
     std::shared_ptr<octex::detail::plan> pl;
     {
       std::lock_guard<std::mutex> lock(ix.mu);
+      OCTEX_EXPECTS(!ix.plans.empty(), "octex: the profiled plan was evicted by another search");
       pl = ix.plans.begin()->second;
     }
-    std::lock_guard<std::mutex> lock(pl->mu);
     OCTEX_HIP(hipSetDevice(ix.device));
     std::vector<std::string> nm;
     std::vector<double> t;
@@ -507,6 +509,7 @@ extern "C" cuvsError_t octexIndexPlaceOnHost(cuvsOctexIndex_t index, int32_t vec
 {
   return translate_exceptions([=] {
     auto& ix = as_index(*index)->impl();
+    std::lock_guard<std::mutex> run(ix.stream_mu);
     OCTEX_HIP(hipSetDevice(ix.device));
     OCTEX_HIP(hipStreamSynchronize(ix.stream));
     {

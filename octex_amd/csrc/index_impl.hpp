@@ -84,8 +84,12 @@ struct index_impl {
     return host_table.ptr != nullptr ? static_cast<const int*>(host_table.dptr) : table.as<const int>();
   }
 
-  std::mutex mu;
+  std::mutex mu;  // the plan cache
   std::map<std::string, std::shared_ptr<plan>> plans;
+  // Held by whoever works on `stream`: plan creation (its graph capture), a search's batches, the release of
+  // an evicted plan (whose destructor waits for the stream), introspection and placement changes.  Work of
+  // another thread reaching the stream during a capture would be captured into, or invalidate, that graph.
+  std::mutex stream_mu;
 
   index_impl() = default;
   index_impl(index_impl const&) = delete;

@@ -532,9 +532,11 @@ __device__ int collect_candidates(const int2* __restrict__ seg, int nseg, const 
 /**
  * Distinct ids of all segments of a query with their sketch scores (collect_candidates, then
  * sketch_scores with LR = the reference's lanes per candidate for this S), written to the query's rows of
- * cand / dist and their count to nout.  The candidates are kept as 16-bit hash-set slot numbers in LDS.
+ * cand / dist and their count to nout.  The candidates are kept as hash-set slot numbers: 16-bit in LDS
+ * (kLdsSlots), or, when they do not fit in LDS beside a large hash set, in the query's own row of cand,
+ * where candidate j's slot is read and then overwritten by its id by the one lane group that scores it.
  */
-template <bool kRows, int LR>
+template <bool kRows, int LR, bool kLdsSlots>
 __global__ __launch_bounds__(kGatherThreads) void gather_kernel(
   const int2* __restrict__ seg, int nseg, const long long* __restrict__ list_ptr,
   const int* __restrict__ table, int table_len, int64_t N, const signed char* __restrict__ code,
@@ -547,16 +549,28 @@ __global__ __launch_bounds__(kGatherThreads) void gather_kernel(
   float2* sq     = reinterpret_cast<float2*>(smq + nseg);  // [S] (scale, query sketch) per coordinate
   int* pre       = reinterpret_cast<int*>(sq + S);  // [nseg + 1] exclusive prefix of the compacted lengths
   int* ht        = pre + nseg + 1;                  // [W] hash set
-  auto* cl       = reinterpret_cast<unsigned short*>(ht + W);  // [cap] slots of the candidates
+  auto* cl       = reinterpret_cast<unsigned short*>(ht + W);  // [cap] slots of the candidates (kLdsSlots)
   __shared__ collect_state cs;
+  int* crow   = cand + static_cast<int64_t>(q) * W;
+  float* drow = dist + static_cast<int64_t>(q) * W;
   for (int i = threadIdx.x; i < S; i += blockDim.x)
     sq[i] = make_float2(scale[i], qs[static_cast<int64_t>(q) * S + i]);
   const int n = collect_candidates<kRows>(seg, nseg, list_ptr, table, table_len, N, logW, cap, sp, pre, ht, cs,
-                                          [&](int slot, int, unsigned h) { cl[slot] = static_cast<unsigned short>(h); });
-  int* crow   = cand + static_cast<int64_t>(q) * W;
-  float* drow = dist + static_cast<int64_t>(q) * W;
+                                          [&](int slot, int, unsigned h) {
+                                            if constexpr (kLdsSlots)
+                                              cl[slot] = static_cast<unsigned short>(h);
+                                            else
+                                              crow[slot] = static_cast<int>(h);
+                                          });
   sketch_scores<LR>(
-    n, [&](int j) { return ht[cl[j]]; }, code, S, pitch, sq,
+    n,
+    [&](int j) {
+      if constexpr (kLdsSlots)
+        return ht[cl[j]];
+      else
+        return ht[crow[j]];
+    },
+    code, S, pitch, sq,
     [&](int j, int id, float d) {
       crow[j] = id;
       drow[j] = d;
@@ -1204,10 +1218,10 @@ auto gather_cap(int W, int nseg, int max_len) -> int
   return static_cast<int>(std::min<int64_t>(W, static_cast<int64_t>(nseg) * std::max(max_len, 1)));
 }
 
-auto gather_smem(int W, int S, int nseg, int max_len) -> size_t
+auto gather_smem(int W, int S, int nseg, int max_len, bool lds_slots) -> size_t
 {
   return static_cast<size_t>(nseg) * sizeof(long long) + static_cast<size_t>(W + 2 * S + nseg + 1) * sizeof(int) +
-         static_cast<size_t>(gather_cap(W, nseg, max_len)) * sizeof(unsigned short);
+         (lds_slots ? static_cast<size_t>(gather_cap(W, nseg, max_len)) * sizeof(unsigned short) : 0);
 }
 
 void launch_gather(bool rows, const int2* seg, int nseg, int max_len, int m, const long long* list_ptr,
@@ -1221,8 +1235,10 @@ void launch_gather(bool rows, const int2* seg, int nseg, int max_len, int m, con
   OCTEX_EXPECTS(max_len >= 0, "octex: segment lengths are non-negative");
   OCTEX_EXPECTS(W == (1 << logW) && W <= kMaxHash, "octex: hash set size");
   OCTEX_EXPECTS(S % 16 == 0 && S >= 16 && S <= 512, "octex: sketch width: a multiple of 16, <= 512");
-  const size_t smem = gather_smem(W, S, nseg, max_len);
-  OCTEX_EXPECTS(smem <= 160 * 1024, "octex: gather needs %zu bytes of LDS (max 160 KiB)", smem);
+  constexpr size_t kLds = 160 * 1024;
+  const bool lds_slots  = gather_smem(W, S, nseg, max_len, true) <= kLds;  // else the slots go to cand
+  const size_t smem     = gather_smem(W, S, nseg, max_len, lds_slots);
+  OCTEX_EXPECTS(smem <= kLds, "octex: gather needs %zu bytes of LDS (max 160 KiB)", smem);
   const int cap = gather_cap(W, nseg, max_len);
   int Lr = 1;  // the reference's lanes per candidate: the next power of two >= S / 16, at most 32
   while (Lr < S / 16 && Lr < 32)
@@ -1230,10 +1246,16 @@ void launch_gather(bool rows, const int2* seg, int nseg, int max_len, int m, con
   auto go = [&](auto rows_tag, auto lr_tag) {
     constexpr bool R = decltype(rows_tag)::value;
     constexpr int LR = decltype(lr_tag)::value;
-    OCTEX_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&gather_kernel<R, LR>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
-    gather_kernel<R, LR><<<m, kGatherThreads, smem, s>>>(seg, nseg, list_ptr, table, table_len, n, code, scale,
-                                                          qs, S, pitch, W, logW, cap, cand, dist, nout);
+    auto launch      = [&](auto kernel) {
+      OCTEX_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    static_cast<int>(smem)));
+      kernel<<<m, kGatherThreads, smem, s>>>(seg, nseg, list_ptr, table, table_len, n, code, scale, qs, S, pitch, W,
+                                             logW, cap, cand, dist, nout);
+    };
+    if (lds_slots)
+      launch(&gather_kernel<R, LR, true>);
+    else
+      launch(&gather_kernel<R, LR, false>);
   };
   auto by_lr = [&](auto rows_tag) {
     switch (Lr) {

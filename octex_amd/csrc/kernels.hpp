@@ -46,8 +46,9 @@ void launch_e8(const float* y, int64_t n, int b, float inv_f, float* p, long lon
 void launch_probe(const __half* Y, int m, int C, int L, int B, const float* inv_f, const int* off,
                   int64_t T1, const long long* keys, int64_t Mmax, const int* base, int l, int lr,
                   int logT, int2* seg, hipStream_t s);
-/** LDS bytes of a gather over `nseg` segments per query with hash sets up to W slots. */
-auto gather_smem(int W, int S, int nseg, int max_len) -> size_t;
+/** LDS bytes of a gather over `nseg` segments per query with hash sets up to W slots; lds_slots: with the
+ * candidates' 16-bit slot list in LDS too (else it is kept in the query's row of cand). */
+auto gather_smem(int W, int S, int nseg, int max_len, bool lds_slots) -> size_t;
 /** Ids at or above `n` (a corrupt list or table entry) are skipped like the -1 padding. */
 /** Lists: segment c of a query reads copy c's lists at list_ptr[c] (a device pointer per copy). */
 /** code [n, pitch]: the S sketch codes of row v start at code + v * pitch. */

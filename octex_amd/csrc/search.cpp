@@ -32,6 +32,9 @@ index_impl::~index_impl()
 
 plan::~plan()
 {
+  // an evicted plan can be released by a search whose batch is still running on the index's stream: its
+  // graph and buffers go only after that work
+  if (stream != nullptr) (void)hipStreamSynchronize(stream);
   if (graph != nullptr) (void)hipGraphExecDestroy(graph);
   if (ev_in != nullptr) (void)hipEventDestroy(ev_in);
   if (ev_out != nullptr) (void)hipEventDestroy(ev_out);
@@ -136,6 +139,7 @@ void launch_batch(index_impl const& ix, plan const& pl, hipStream_t s)
 auto make_plan(index_impl& ix, search_params const& sp, int m, int k) -> std::shared_ptr<plan>
 {
   auto pl   = std::make_shared<plan>();
+  pl->stream = ix.stream;
   pl->sp    = sp;
   pl->m     = m;
   pl->k     = k;
@@ -263,8 +267,8 @@ void search_impl(raft::resources const& res, search_params const& sp, index cons
   OCTEX_HIP(hipGetDevice(&cur));
   OCTEX_HIP(hipSetDevice(ix.device));
   const int m = static_cast<int>(std::min<int64_t>(std::max(sp.batch, 1), nq));
-  auto pl     = get_plan(ix, sp, m, static_cast<int>(k));
-  std::lock_guard<std::mutex> lock(pl->mu);
+  std::unique_lock<std::mutex> run(ix.stream_mu);
+  auto pl = get_plan(ix, sp, m, static_cast<int>(k));  // released before `run` on every path
   const int64_t D  = ix.dim;
   hipStream_t s    = ix.stream;
   hipStream_t call = raft::resource::get_cuda_stream(res);
@@ -284,6 +288,8 @@ void search_impl(raft::resources const& res, search_params const& sp, index cons
   }
   OCTEX_HIP(hipEventRecord(pl->ev_out, s));
   OCTEX_HIP(hipStreamWaitEvent(call, pl->ev_out, 0));
+  pl.reset();  // an evicted plan goes here, with the stream lock held
+  run.unlock();
   if (host_out) OCTEX_HIP(hipStreamSynchronize(call));
   OCTEX_HIP(hipSetDevice(cur));
 }

@@ -24,8 +24,8 @@ struct plan {
   dbuf qbuf, qc, qh, Y, qs, seg, cand, dist, nin, si, sd, done, seg2, cand2, dist2, n2, bi, bd;
   hipGraphExec_t graph = nullptr;
   hipEvent_t ev_in = nullptr, ev_out = nullptr;
+  hipStream_t stream = nullptr;  // the index's stream, where every batch of the plan runs
   int64_t buffer_bytes = 0;
-  std::mutex mu;
   plan() = default;
   plan(plan const&) = delete;
   ~plan();

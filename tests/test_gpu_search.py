@@ -71,6 +71,21 @@ def test_search_matches_oracle(octex, small_index):
     assert np.allclose(qs, O.sketch_query(qc, oix.basis), rtol=1e-5, atol=1e-4)
 
 
+@pytest.mark.parametrize("sketch_rank", [False, True])
+def test_large_wave_gather_matches_oracle(octex, small_index, sketch_rank):
+    """starts 512 over table rows of 32 (configs[4]'s setting): the wave gather's hash set of 2^15 slots leaves
+    no LDS for the candidates' slot list, which then lives in the query's row of cand; results as the oracle's."""
+    index = octex.load(small_index["path"])
+    oix = O.Index(small_index["path"])
+    Q = small_index["Q"]
+    assert oix.table_len == 32
+    p = dict(read=16, starts=512, waves=2, rerank=128, wave_rerank=128, sketch_rank=sketch_rank, final_rerank=32)
+    D, I = index.search(Q, k=10, **p)
+    assert index.plan_info()["W2"] == 1 << 15
+    Do, Io, tr, _, _ = oracle_given_gpu_projections(index, oix, Q, 10, **p)
+    assert_same_results(D, I, Do, Io)
+
+
 def test_search_recall_and_distances(octex, small_index):
     index = octex.load(small_index["path"])
     Q = small_index["Q"]
@@ -102,6 +117,35 @@ def test_graph_equals_direct_launches(octex, small_index):
     for _ in range(3):  # replays of one graph, with eager work in between
         D3, I3 = index.search(Q, k=10, **PARAMS)
         assert np.array_equal(I1, I3) and np.array_equal(D1, D3)
+
+
+def test_concurrent_searches(octex, small_index):
+    """Threads searching one index with different parameter sets (each call evicts the other's cached plan,
+    search.cu:804-813, while that plan's batch may still run) get the results of serial searches."""
+    import threading
+
+    index = octex.load(small_index["path"])
+    Q = small_index["Q"]
+    sets = [dict(k=10, **PARAMS), dict(k=5, read=8, starts=32, waves=1), dict(k=10, batch=37, **PARAMS)]
+    want = [index.search(Q, **p) for p in sets]
+    errors = []
+
+    def worker(t):
+        try:
+            for r in range(6):
+                j = (t + r) % len(sets)
+                D, I = index.search(Q, **sets[j])
+                if not (np.array_equal(I, want[j][1]) and np.array_equal(D, want[j][0])):
+                    errors.append((t, r, j))
+        except Exception as e:  # noqa: BLE001 - reported below
+            errors.append((t, repr(e)))
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(3)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    assert not errors, errors
 
 
 def test_device_tensors(octex, small_index):
