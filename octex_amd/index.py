@@ -14,6 +14,7 @@ import ctypes as ct
 import json
 import os
 import shutil
+import sys
 import tempfile
 
 import numpy as np
@@ -124,6 +125,38 @@ def _is_torch(a):
     return type(a).__module__.startswith("torch")
 
 
+def _is_foreign(a):
+    """An array of another framework (CuPy, JAX, ...) that exports DLPack or __cuda_array_interface__."""
+    return (not isinstance(a, np.ndarray) and not _is_torch(a)
+            and (hasattr(a, "__dlpack__") or hasattr(a, "__cuda_array_interface__")))
+
+
+def _as_torch(a):
+    """A torch view of a foreign array (no copy): through DLPack, or __cuda_array_interface__."""
+    import torch
+
+    return torch.from_dlpack(a) if hasattr(a, "__dlpack__") else torch.as_tensor(a, device="cuda")
+
+
+def _in_framework_of(a, t):
+    """The torch result t as an array of a's framework, through its module's from_dlpack when it has one
+    (octex/_arrays.py answers in the framework of the input); torch otherwise."""
+    mod = sys.modules.get(type(a).__module__.partition(".")[0])
+    conv = getattr(mod, "from_dlpack", None)
+    return conv(t) if conv is not None else t
+
+
+def _copy_into(dst, src):
+    """Write the result src (numpy or torch) into the caller's array dst (numpy, torch, or foreign)."""
+    if isinstance(dst, np.ndarray):
+        dst[...] = src.cpu().numpy() if _is_torch(src) else src
+        return
+    import torch
+
+    d = dst if _is_torch(dst) else _as_torch(dst)
+    d.copy_(src if _is_torch(src) else torch.from_numpy(np.ascontiguousarray(src)))
+
+
 class Index:
     """An octex index placed on a GPU. Create it with build() or load()."""
 
@@ -191,16 +224,27 @@ class Index:
 
     def search(self, queries, k=10, *, read=32, starts=128, waves=2, rerank=128, wave_rerank=128, batch=10000,
                sketch_rank=False, final_rerank=32, neighbors=None, distances=None, **ablation):
-        """Approximate k nearest neighbors of a batch of queries [m, dim] (float32).
+        """Approximate k nearest neighbors of a batch of queries [m, dim] (float32): numpy, torch (host or GPU), or
+        any array with DLPack or __cuda_array_interface__.
 
         Returns (distances, neighbors): float32 squared Euclidean distances and int64 ids [m, k], nearest first,
-        in the framework (and on the GPU) of the queries.
+        in the framework (and on the GPU) of the queries; given `neighbors` / `distances` arrays are written.
         """
         k = int(k)
         if k <= 0:
             raise ValueError("octex: k must be positive")
         params = search_params(read=read, starts=starts, waves=waves, rerank=rerank, wave_rerank=wave_rerank,
                                batch=batch, sketch_rank=sketch_rank, final_rerank=final_rerank, **ablation)
+        if _is_foreign(queries):  # searched as a torch view, answered in the queries' framework
+            D, I = self.search(_as_torch(queries), k, read=read, starts=starts, waves=waves, rerank=rerank,
+                               wave_rerank=wave_rerank, batch=batch, sketch_rank=sketch_rank,
+                               final_rerank=final_rerank, **ablation)
+            if neighbors is not None:
+                _copy_into(neighbors, I)
+            if distances is not None:
+                _copy_into(distances, D)
+            return (distances if distances is not None else _in_framework_of(queries, D),
+                    neighbors if neighbors is not None else _in_framework_of(queries, I))
         if _is_torch(queries):
             import torch
 
@@ -227,10 +271,10 @@ class Index:
         if _is_torch(queries) and q.is_cuda:
             self._res.sync()
         if neighbors is not None:
-            neighbors[...] = I
+            _copy_into(neighbors, I)
             I = neighbors
         if distances is not None:
-            distances[...] = D
+            _copy_into(distances, D)
             D = distances
         return D, I
 

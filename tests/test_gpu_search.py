@@ -148,6 +148,47 @@ def test_concurrent_searches(octex, small_index):
     assert not errors, errors
 
 
+class _Foreign:
+    """An array of a framework octex_amd does not know, exporting DLPack only (as CuPy's arrays do)."""
+
+    __module__ = "fakearrays"
+
+    def __init__(self, t):
+        self.t = t
+
+    def __dlpack__(self, **kw):
+        return self.t.__dlpack__(**kw)
+
+    def __dlpack_device__(self):
+        return self.t.__dlpack_device__()
+
+
+def test_foreign_arrays(octex, small_index, monkeypatch):
+    """Queries of another framework are searched without a copy and answered in that framework (through its
+    module's from_dlpack, octex/_arrays.py); given output arrays of it are written (int32 ids too)."""
+    import sys
+    import types
+
+    mod = types.ModuleType("fakearrays")
+    mod.from_dlpack = lambda x: _Foreign(torch.from_dlpack(x))
+    monkeypatch.setitem(sys.modules, "fakearrays", mod)
+    index = octex.load(small_index["path"])
+    Q = small_index["Q"]
+    D1, I1 = index.search(Q, k=10, **PARAMS)
+    q = _Foreign(torch.from_numpy(Q).cuda())
+    D2, I2 = index.search(q, k=10, **PARAMS)
+    assert isinstance(D2, _Foreign) and isinstance(I2, _Foreign) and I2.t.is_cuda
+    assert np.array_equal(I1, I2.t.cpu().numpy()) and np.array_equal(D1, D2.t.cpu().numpy())
+    nb = _Foreign(torch.empty((len(Q), 10), dtype=torch.int32, device="cuda"))
+    ds = _Foreign(torch.empty((len(Q), 10), dtype=torch.float32, device="cuda"))
+    D3, I3 = index.search(q, k=10, neighbors=nb, distances=ds, **PARAMS)
+    assert I3 is nb and D3 is ds
+    assert np.array_equal(nb.t.cpu().numpy(), I1) and np.array_equal(ds.t.cpu().numpy(), D1)
+    host_ids = np.empty((len(Q), 10), np.uint32)  # numpy outputs of device queries
+    index.search(torch.from_numpy(Q).cuda(), k=10, neighbors=host_ids, **PARAMS)
+    assert np.array_equal(host_ids, I1)
+
+
 def test_device_tensors(octex, small_index):
     index = octex.load(small_index["path"])
     Q = small_index["Q"]
