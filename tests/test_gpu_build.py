@@ -219,39 +219,12 @@ def test_exact_lists(octex, tmp_path):
     """exact_lists (build_cells.cuh:506-510, 567-599): the list of every cell holds the l projected rows
     nearest to the cell's center (f times the E8 point of a member's projection / f), among all rows,
     up to near ties of fp32 distances; member_lists takes precedence."""
+    from test_oracle import check_exact_lists
+
     X, _ = clustered(n=2000, m=10, d=32, clusters=10, seed=9)
     path = str(tmp_path / "ex")
-    l = 16
-    octex.build(X, path, copies=2, list_len=l, table_len=8, log_buckets=10, exact_lists=True, seed=5)
-    ix = O.Index(path)
-    Xh = X.astype(np.float16).astype(np.float64)
-    cells = np.load(os.path.join(path, "cells.npy"))
-    checked = 0
-    for c in range(2):
-        proj = np.load(os.path.join(path, "proj.npy"))[c].astype(np.float64)
-        shift = np.load(os.path.join(path, "shift.npy"))[c].astype(np.float64)
-        y = (Xh - ix.mean.astype(np.float64)) @ proj + shift
-        for j, f in enumerate(ix.spacings):
-            M = cells[c, j]
-            keys = ix.keys[c, j, :M]
-            p, h = O.e8_batch((y / f).astype(np.float32), ix.blocks, 1.0)
-            first = {}
-            for r, hv in enumerate(h):
-                first.setdefault(int(hv), r)
-            r0 = ix.base[c, j]
-            rows = ix.lists[c, r0 * l : (r0 + M) * l].reshape(M, l)
-            for ci in range(0, M, max(1, M // 40)):
-                if int(keys[ci]) not in first:
-                    continue  # the member's fp64 projection rounds to another cell
-                z = p[first[int(keys[ci])]].astype(np.float64) * f
-                dz = ((y - z) ** 2).sum(1)
-                lth = np.sort(dz)[l - 1]
-                # the GPU's fp32 |z|^2 + |y|^2 - 2 z.y errs by a few ulp of the norms
-                tol = 1e-5 * ((z**2).sum() + (y**2).sum(1).max()) + 1e-4 * lth
-                assert len(set(rows[ci])) == l
-                assert (dz[rows[ci]] <= lth + tol).all()
-                checked += 1
-    assert checked > 50
+    octex.build(X, path, copies=2, list_len=16, table_len=8, log_buckets=10, exact_lists=True, seed=5)
+    assert check_exact_lists(path, X) > 50
 
 
 def test_exact_table_reference_rule(octex, tmp_path):

@@ -379,3 +379,54 @@ def test_exact_table_rule_catches_a_wrong_merge(tmp_path):
             table_len=k, reverse_edges=False, member_lists=True, seed=0)
     with pytest.raises(AssertionError):
         check_exact_table(np.load(tmp_path / "f" / "table.npy"), x, k)
+
+
+def check_exact_lists(path, X, stride=40):
+    """Every sampled cell's list holds the l rows nearest to the cell's center among all rows: the projections
+    y = (x16 - mean) @ proj + shift recomputed in fp64 from the directory, the center f times the E8 point of a
+    member's y / f; up to near ties of fp32 distances (a few ulp of the squared norms).  Returns the number of
+    cells checked."""
+    ix = O.Index(path)
+    l = ix.list_len
+    Xh = X.astype(np.float16).astype(np.float64)
+    cells = np.load(os.path.join(path, "cells.npy"))
+    checked = 0
+    for c in range(ix.copies):
+        proj = np.load(os.path.join(path, "proj.npy"))[c].astype(np.float64)
+        shift = np.load(os.path.join(path, "shift.npy"))[c].astype(np.float64)
+        y = (Xh - ix.mean.astype(np.float64)) @ proj + shift
+        for j, f in enumerate(ix.spacings):
+            M = cells[c, j]
+            keys = ix.keys[c, j, :M]
+            p, h = O.e8_batch((y / f).astype(np.float32), ix.blocks, 1.0)
+            first = {}
+            for r, hv in enumerate(h):
+                first.setdefault(int(hv), r)
+            r0 = ix.base[c, j]
+            rows = ix.lists[c, r0 * l : (r0 + M) * l].reshape(M, l)
+            for ci in range(0, M, max(1, M // stride)):
+                if int(keys[ci]) not in first:
+                    continue  # the member's fp64 projection rounds to another cell
+                z = p[first[int(keys[ci])]].astype(np.float64) * f
+                dz = ((y - z) ** 2).sum(1)
+                lth = np.sort(dz)[l - 1]
+                tol = 1e-5 * ((z**2).sum() + (y**2).sum(1).max()) + 1e-4 * lth
+                assert len(set(rows[ci].tolist())) == l
+                assert (dz[rows[ci]] <= lth + tol).all()
+                checked += 1
+    return checked
+
+
+def test_oracle_exact_lists(tmp_path):
+    """The oracle's exact lists (build_cells.cuh:506-510, 567-599) hold each cell center's l nearest rows."""
+    X, _ = clustered(n=1500, m=10, d=32, clusters=10, seed=9)
+    O.build(X, str(tmp_path / "e"), copies=2, list_len=16, table_len=8, log_buckets=10, exact_lists=True, seed=5)
+    assert check_exact_lists(str(tmp_path / "e"), X) > 50
+
+
+def test_exact_list_check_catches_member_lists(tmp_path):
+    """The same check fails on member lists (the l nearest members of the cell only): it is not vacuous."""
+    X, _ = clustered(n=1500, m=10, d=32, clusters=10, seed=9)
+    O.build(X, str(tmp_path / "m"), copies=2, list_len=16, table_len=8, log_buckets=10, member_lists=True, seed=5)
+    with pytest.raises(AssertionError):
+        check_exact_lists(str(tmp_path / "m"), X)
