@@ -13,6 +13,7 @@
 #include <rocprim/device/device_scan.hpp>
 
 #include <cstdint>
+#include <type_traits>
 
 namespace cuvs::neighbors::octex::detail {
 
@@ -303,6 +304,7 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 constexpr int kKnnQ    = 64;   // query rows per workgroup
 constexpr int kKnnRows = 128;  // database rows per step: 4 waves x 32
 constexpr int kKnnCap  = 256;  // LDS keys per query row: the K kept (K <= 128) and one step's appends
+constexpr int kKnnChunk = 8;   // k steps whose fragments are loaded together
 
 __device__ __forceinline__ float knn_f(__half v) { return __half2float(v); }
 __device__ __forceinline__ float knn_f(float v) { return v; }
@@ -322,22 +324,30 @@ __global__ void row_norms_kernel(const T* __restrict__ x, int64_t n, int d, floa
   out[i] = acc;
 }
 
-/** Four fp16 of row r, columns k..k+3, of a row-major [rows, d] matrix; zeros outside it. */
-__device__ __forceinline__ half4_t knn_h4(const __half* __restrict__ a, int64_t r, int64_t rows, int d, int k,
-                                          bool vec)
+/**
+ * Four fp16 at columns k..k+3 of `row` (a row pointer, or row 0 of the matrix when the row is past its end:
+ * `ok` false), zeros when !ok.  FULL: every column k read lies inside the row (d a multiple of 16), so the load
+ * is one unconditional 8-byte load and a select; otherwise each element is checked against d.  The loads are
+ * never under a per-lane branch: that made the compiler wait for every earlier load before the next one.
+ */
+template <bool FULL>
+__device__ __forceinline__ half4_t knn_h4(const __half* __restrict__ row, bool ok, int d, int k)
 {
-  half4_t v = {0, 0, 0, 0};
-  if (r >= rows) return v;
-  const __half* p = a + r * d + k;
-  if (vec && k + 3 < d) {
-    uint2 u = *reinterpret_cast<const uint2*>(p);
-    v       = *reinterpret_cast<half4_t*>(&u);
+  if constexpr (FULL) {
+    uint2 u         = *reinterpret_cast<const uint2*>(row + k);
+    const half4_t v = *reinterpret_cast<half4_t*>(&u);
+    const half4_t z = {0, 0, 0, 0};
+    return ok ? v : z;
   } else {
+    half4_t v;
 #pragma unroll
-    for (int j = 0; j < 4; j++)
-      if (k + j < d) v[j] = static_cast<_Float16>(__half2float(p[j]));
+    for (int j = 0; j < 4; j++) {
+      const bool in  = ok && k + j < d;
+      const __half h = row[in ? k + j : 0];
+      v[j]           = in ? static_cast<_Float16>(__half2float(h)) : static_cast<_Float16>(0.f);
+    }
+    return v;
   }
-  return v;
 }
 
 /** Float bits mapped to an unsigned order (negative values first) and back. */
@@ -363,9 +373,11 @@ template <>
 struct knn_op<__half> {
   using frag                 = half4_t;
   static constexpr int kStep = 16;
-  __device__ static frag load(const __half* a, int64_t r, int64_t rows, int d, int k0, int lane, bool vec)
+  static constexpr int kFull = 16;  // d a multiple of this: every lane's columns lie inside the row
+  template <bool FULL>
+  __device__ static frag load(const __half* row, bool ok, int d, int k0, int lane)
   {
-    return knn_h4(a, r, rows, d, k0 + (lane >> 4) * 4, vec);
+    return knn_h4<FULL>(row, ok, d, k0 + (lane >> 4) * 4);
   }
   __device__ static float4_t mma(frag a, frag b, float4_t c)
   {
@@ -376,10 +388,14 @@ template <>
 struct knn_op<float> {
   using frag                 = float;
   static constexpr int kStep = 4;
-  __device__ static frag load(const float* a, int64_t r, int64_t rows, int d, int k0, int lane, bool)
+  static constexpr int kFull = 4;
+  template <bool FULL>
+  __device__ static frag load(const float* row, bool ok, int d, int k0, int lane)
   {
-    const int k = k0 + (lane >> 4);
-    return (r < rows && k < d) ? a[r * d + k] : 0.f;
+    const int k   = k0 + (lane >> 4);
+    const bool in = FULL ? ok : (ok && k < d);
+    const float v = row[in ? k : 0];  // unconditional load, then a select
+    return in ? v : 0.f;
   }
   __device__ static float4_t mma(frag a, frag b, float4_t c)
   {
@@ -426,12 +442,13 @@ __device__ void knn_compact(unsigned long long* key, int* cnt, float* tau, int K
  * |q|^2 + |x|^2 - 2 q.x (fp32; the dot products by MFMA, knn_op: fp16 products are exact in fp32 and
  * accumulated in fp32), ties by row.  A workgroup owns 64 query rows and scans every database row,
  * 128 per step: wave w computes rows [32 w, 32 w + 32) of the step against the 64 queries as 4 x 2
- * MFMA tiles (lane l holds rows 4 (l / 16) + r of a 16-row tile for query l % 16).  A distance at or
+ * MFMA tiles (lane l holds rows 4 (l / 16) + r of a 16-row tile for query l % 16), the fragments of 8 k steps
+ * loaded together before their MFMAs.  A distance at or
  * below its query's threshold is appended to the query's LDS keys; when a query holds more than
  * kKnnCap - kKnnRows keys after a step, knn_compact keeps the K smallest and lowers the thresholds, so
  * a step's appends always fit.  out_d / out_i [m, K], sorted; -1 / +inf past the n rows.
  */
-template <typename T>
+template <typename T, bool FULL>
 __global__ __launch_bounds__(256) void knn_kernel(const T* __restrict__ Q, const float* __restrict__ qn, int64_t m,
                                                   const T* __restrict__ X, const float* __restrict__ xn, int64_t n,
                                                   int d, int K, float* __restrict__ out_d, int* __restrict__ out_i)
@@ -442,7 +459,6 @@ __global__ __launch_bounds__(256) void knn_kernel(const T* __restrict__ Q, const
   __shared__ float tau[kKnnQ];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int64_t q0 = static_cast<int64_t>(blockIdx.x) * kKnnQ;
-  const bool vec   = (d & 3) == 0;
   const int kq     = (lane >> 4) * 4;
   if (tid < kKnnQ) {
     cnt[tid] = 0;
@@ -463,33 +479,47 @@ __global__ __launch_bounds__(256) void knn_kernel(const T* __restrict__ Q, const
 #pragma unroll
       for (int t = 0; t < 2; t++)
         acc[i][t] = float4_t{0.f, 0.f, 0.f, 0.f};
-    typename op::frag a[2], b[4];
+    // this step's rows and the workgroup's queries: row pointers (row 0 past the end) and validity, the same
+    // for every k step
+    const T* xrow[2];
+    const T* qrow[4];
+    bool xok[2], qok[4];
 #pragma unroll
-    for (int t = 0; t < 2; t++)
-      a[t] = op::load(X, rw + t * 16 + (lane & 15), n, d, 0, lane, vec);
+    for (int t = 0; t < 2; t++) {
+      const int64_t r = rw + t * 16 + (lane & 15);
+      xok[t]          = r < n;
+      xrow[t]         = X + (xok[t] ? r : 0) * d;
+    }
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-      b[i] = op::load(Q, q0 + i * 16 + (lane & 15), m, d, 0, lane, vec);
-    for (int k0 = 0; k0 < d; k0 += op::kStep) {
-      typename op::frag na[2], nb[4];  // the next k step's fragments, loaded while this one multiplies
-      const int kn = k0 + op::kStep;
+    for (int i = 0; i < 4; i++) {
+      const int64_t r = q0 + i * 16 + (lane & 15);
+      qok[i]          = r < m;
+      qrow[i]         = Q + (qok[i] ? r : 0) * d;
+    }
+    // k in chunks of kKnnChunk steps: the chunk's fragment loads (unconditional, see knn_h4) are all in flight
+    // before its MFMAs, so a step of rows waits for memory once per chunk (once for d <= 128 fp16, <= 32 fp32)
+    for (int c0 = 0; c0 < d; c0 += op::kStep * kKnnChunk) {
+      typename op::frag a[kKnnChunk][2], b[kKnnChunk][4];
 #pragma unroll
-      for (int t = 0; t < 2; t++)
-        na[t] = op::load(X, rw + t * 16 + (lane & 15), n, d, kn, lane, vec);
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-        nb[i] = op::load(Q, q0 + i * 16 + (lane & 15), m, d, kn, lane, vec);
-#pragma unroll
-      for (int i = 0; i < 4; i++)
+      for (int j = 0; j < kKnnChunk; j++) {
+        if (c0 + op::kStep * j >= d) break;  // uniform
+        const int k = c0 + op::kStep * j;
 #pragma unroll
         for (int t = 0; t < 2; t++)
-          acc[i][t] = op::mma(a[t], b[i], acc[i][t]);
+          a[j][t] = op::template load<FULL>(xrow[t], xok[t], d, k, lane);
 #pragma unroll
-      for (int t = 0; t < 2; t++)
-        a[t] = na[t];
+        for (int i = 0; i < 4; i++)
+          b[j][i] = op::template load<FULL>(qrow[i], qok[i], d, k, lane);
+      }
 #pragma unroll
-      for (int i = 0; i < 4; i++)
-        b[i] = nb[i];
+      for (int j = 0; j < kKnnChunk; j++) {
+        if (c0 + op::kStep * j >= d) break;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+          for (int t = 0; t < 2; t++)
+            acc[i][t] = op::mma(a[j][t], b[j][i], acc[i][t]);
+      }
     }
     float xr[2][4];
 #pragma unroll
@@ -497,7 +527,8 @@ __global__ __launch_bounds__(256) void knn_kernel(const T* __restrict__ Q, const
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int64_t row = rw + t * 16 + kq + r;
-        xr[t][r]          = row < n ? xn[row] : 0.f;
+        const float v     = xn[row < n ? row : 0];  // unconditional load, then a select
+        xr[t][r]          = row < n ? v : 0.f;
       }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -607,7 +638,10 @@ void knn_rows(const T* Q, const float* qn, int64_t m, const T* X, const float* x
   if (m == 0) return;
   const int64_t blocks = (m + kKnnQ - 1) / kKnnQ;
   OCTEX_EXPECTS(blocks < (int64_t{1} << 31), "octex: exact neighbors: too many query rows");
-  knn_kernel<T><<<static_cast<unsigned>(blocks), 256, 0, s>>>(Q, qn, m, X, xn, n, d, K, out_d, out_i);
+  if (d % knn_op<T>::kFull == 0)
+    knn_kernel<T, true><<<static_cast<unsigned>(blocks), 256, 0, s>>>(Q, qn, m, X, xn, n, d, K, out_d, out_i);
+  else
+    knn_kernel<T, false><<<static_cast<unsigned>(blocks), 256, 0, s>>>(Q, qn, m, X, xn, n, d, K, out_d, out_i);
   OCTEX_HIP(hipGetLastError());
 }
 template void knn_rows<__half>(const __half*, const float*, int64_t, const __half*, const float*, int64_t, int, int,

@@ -48,22 +48,30 @@ __global__ void pad_rows_kernel(float* __restrict__ q, int from, int m, int D)
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
-/** Four consecutive fp16 of row r (k..k+3) of a row-major [rows, K] matrix, zeros outside it. */
-__device__ __forceinline__ half4_t load_h4(const __half* __restrict__ a, int r, int rows, int K, int k,
-                                           bool vec)
+/**
+ * Four consecutive fp16 at columns k..k+3 of `row` (a row pointer, or row 0 of the matrix when the row is past
+ * its end: `ok` false), zeros when !ok.  FULL: every column read lies inside the row (K a multiple of 16), so
+ * it is one unconditional 8-byte load and a select; otherwise each element is checked against K.  No load is
+ * under a per-lane branch: that made the compiler wait for every earlier load before the next one.
+ */
+template <bool FULL>
+__device__ __forceinline__ half4_t load_h4(const __half* __restrict__ row, bool ok, int K, int k)
 {
-  half4_t v = {0, 0, 0, 0};
-  if (r >= rows) return v;
-  const __half* p = a + static_cast<int64_t>(r) * K + k;
-  if (vec && k + 3 < K) {
-    uint2 u = *reinterpret_cast<const uint2*>(p);
-    v       = *reinterpret_cast<half4_t*>(&u);
+  if constexpr (FULL) {
+    uint2 u         = *reinterpret_cast<const uint2*>(row + k);
+    const half4_t v = *reinterpret_cast<half4_t*>(&u);
+    const half4_t z = {0, 0, 0, 0};
+    return ok ? v : z;
   } else {
+    half4_t v;
 #pragma unroll
-    for (int j = 0; j < 4; j++)
-      if (k + j < K) v[j] = static_cast<_Float16>(__half2float(p[j]));
+    for (int j = 0; j < 4; j++) {
+      const bool in  = ok && k + j < K;
+      const __half h = row[in ? k + j : 0];
+      v[j]           = in ? static_cast<_Float16>(__half2float(h)) : static_cast<_Float16>(0.f);
+    }
+    return v;
   }
-  return v;
 }
 
 /**
@@ -76,6 +84,7 @@ __device__ __forceinline__ half4_t load_h4(const __half* __restrict__ a, int r, 
  * outputs).  The fragments of 4 k steps are loaded before their MFMAs and the shift before the
  * products, so a wave's loads overlap.
  */
+template <bool FULL>
 __global__ __launch_bounds__(256) void project_kernel(const __half* __restrict__ qh,
                                                       const __half* __restrict__ ucatT,
                                                       const __half* __restrict__ shift, int m, int K,
@@ -86,17 +95,33 @@ __global__ __launch_bounds__(256) void project_kernel(const __half* __restrict__
   const int q0   = blockIdx.x * 64;
   const int n0   = (blockIdx.y * 4 + wid) * 64;
   const bool active = n0 < N;  // a wave past the outputs computes nothing but meets the barrier
-  const bool vec = (K & 3) == 0;
-  const int kq   = (lane >> 4) * 4;
+  const int kq      = (lane >> 4) * 4;
   // the shift of this lane's 16 outputs, read once and in flight during the products
   float sh[4][4];
 #pragma unroll
   for (int t = 0; t < 4; t++)
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-      const int nb = n0 + t * 16 + kq + r;
-      sh[t][r]     = nb < N ? __half2float(shift[nb]) : 0.f;
+      const int nb  = n0 + t * 16 + kq + r;
+      const float v = __half2float(shift[nb < N ? nb : 0]);  // unconditional load, then a select
+      sh[t][r]      = nb < N ? v : 0.f;
     }
+  // this lane's rows of qh and ucatT: pointers (row 0 past the end) and validity, the same for every k step
+  const __half* qrow[4];
+  const __half* urow[4];
+  bool qok[4], uok[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int r = q0 + i * 16 + (lane & 15);
+    qok[i]      = r < m;
+    qrow[i]     = qh + static_cast<int64_t>(qok[i] ? r : 0) * K;
+  }
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    const int r = n0 + t * 16 + (lane & 15);
+    uok[t]      = r < N;
+    urow[t]     = ucatT + static_cast<int64_t>(uok[t] ? r : 0) * K;
+  }
   float4_t acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; i++)
@@ -114,10 +139,10 @@ __global__ __launch_bounds__(256) void project_kernel(const __half* __restrict__
       const int k = c0 + 16 * j + kq;
 #pragma unroll
       for (int i = 0; i < 4; i++)
-        b[j][i] = load_h4(qh, q0 + i * 16 + (lane & 15), m, K, k, vec);
+        b[j][i] = load_h4<FULL>(qrow[i], qok[i], K, k);
 #pragma unroll
       for (int t = 0; t < 4; t++)
-        a[j][t] = load_h4(ucatT, n0 + t * 16 + (lane & 15), N, K, k, vec);
+        a[j][t] = load_h4<FULL>(urow[t], uok[t], K, k);
     }
 #pragma unroll
     for (int j = 0; j < kChunk; j++) {
@@ -784,15 +809,14 @@ __device__ int select_by_bins(const unsigned* __restrict__ kd, const int* __rest
  * acc = fma(t, t, acc), then an xor butterfly over the group.  A chunk is one 16-byte load when rows are
  * 16-byte aligned (D a multiple of 8), and every group has kRows rows in flight.
  */
-template <int LX>
-__device__ void exact_distances(const int* sid, int ns, const __half* __restrict__ vectors, int D, const float* sq,
-                                float* sd)
+template <int LX, bool VEC>
+__device__ __forceinline__ void exact_distances_rows(const int* sid, int ns, const __half* __restrict__ vectors, int D,
+                                     const float* sq, float* sd)
 {
-  constexpr int kRows = 4, GPW = 64 / LX;
+  constexpr int kRows = VEC ? 4 : 1, GPW = 64 / LX;  // rows in flight per group (one for the rare unaligned D)
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
   const int sub = lane & (LX - 1), grp = lane / LX;
   const int nch = (D + 7) / 8;
-  const bool vec = (D & 7) == 0;
   for (int j0 = wid * GPW * kRows; j0 < ns; j0 += nw * GPW * kRows) {
     const __half* x[kRows];
     float acc[kRows];
@@ -805,27 +829,29 @@ __device__ void exact_distances(const int* sid, int ns, const __half* __restrict
       const int k0 = 8 * c;
       uint4 w[kRows];
 #pragma unroll
-      for (int r = 0; r < kRows; r++) {  // every row's chunk first
-        if (vec) {
+      for (int r = 0; r < kRows; r++) {  // every row's chunk first, all kRows loads in flight together
+        if constexpr (VEC) {
           w[r] = *reinterpret_cast<const uint4*>(x[r] + k0);
         } else {
           __half h[8];
 #pragma unroll
-          for (int e = 0; e < 8; e++)
-            h[e] = k0 + e < D ? x[r][k0 + e] : __float2half(0.f);
+          for (int e = 0; e < 8; e++) {  // unconditional loads of clamped columns, then a select
+            const __half v = x[r][k0 + e < D ? k0 + e : 0];
+            h[e]           = k0 + e < D ? v : __float2half(0.f);
+          }
           w[r] = *reinterpret_cast<const uint4*>(h);
         }
       }
       float qk[8];
 #pragma unroll
       for (int e = 0; e < 8; e++)
-        qk[e] = k0 + e < D ? sq[k0 + e] : 0.f;
+        qk[e] = (VEC || k0 + e < D) ? sq[k0 + e] : 0.f;
 #pragma unroll
       for (int r = 0; r < kRows; r++) {
         const __half* h = reinterpret_cast<const __half*>(&w[r]);
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-          if (k0 + e < D) {
+          if (VEC || k0 + e < D) {
             const float t = __half2float(h[e]) - qk[e];
             acc[r]        = fmaf(t, t, acc[r]);
           }
@@ -842,6 +868,18 @@ __device__ void exact_distances(const int* sid, int ns, const __half* __restrict
     }
   }
   __syncthreads();
+}
+
+/** exact_distances_rows with the row layout chosen once per call: a runtime test of D inside the row loop made
+ * the compiler wait for each row's load before issuing the next. */
+template <int LX>
+__device__ __forceinline__ void exact_distances(const int* sid, int ns, const __half* __restrict__ vectors, int D,
+                                                const float* sq, float* sd)
+{
+  if ((D & 7) == 0)
+    exact_distances_rows<LX, true>(sid, ns, vectors, D, sq, sd);
+  else
+    exact_distances_rows<LX, false>(sid, ns, vectors, D, sq, sd);
 }
 
 /** Ascending bitonic sort of P (a power of two) 64-bit keys in LDS. */
@@ -1146,7 +1184,10 @@ void launch_project(const __half* qh, const __half* ucatT, const __half* shift, 
   OCTEX_EXPECTS(K >= 1, "octex: projection needs a positive dimension");
   OCTEX_EXPECTS(N % 8 == 0, "octex: projection outputs must be a multiple of 8 (copies x 8 blocks)");
   dim3 grid(static_cast<unsigned>((m + 63) / 64), static_cast<unsigned>((N + 255) / 256));
-  project_kernel<<<grid, 256, 0, s>>>(qh, ucatT, shift, m, K, N, Y);
+  if (K % 16 == 0)
+    project_kernel<true><<<grid, 256, 0, s>>>(qh, ucatT, shift, m, K, N, Y);
+  else
+    project_kernel<false><<<grid, 256, 0, s>>>(qh, ucatT, shift, m, K, N, Y);
   OCTEX_HIP(hipGetLastError());
 }
 
