@@ -650,8 +650,8 @@ struct bin_select_lds {
  * keys instead, with the same result.  Selected ids (and keys when skey is set) go to sid / skey in any
  * order; their count is returned in every thread.  All threads of the workgroup call it.
  */
-__device__ int select_by_bins(const unsigned* __restrict__ kd, const int* __restrict__ cid, int n, int R, int* sid,
-                              float* skey, bin_select_lds& sh)
+__device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, const int* __restrict__ cid, int n,
+                                              int R, int* sid, float* skey, bin_select_lds& sh)
 {
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, nthr = blockDim.x;
   auto& bs = sh.bs;
@@ -747,19 +747,37 @@ __device__ int select_by_bins(const unsigned* __restrict__ kd, const int* __rest
   __syncthreads();
   const unsigned bstar = static_cast<unsigned>(bs.bstar);
   const int need       = R - bs.below;
-  for_keys([&](unsigned k, int i, bool ok) {
+  // the candidate ids of the cached keys, loaded together before they are placed (unconditional loads of
+  // clamped indices: an id read under the per-lane "selected" branch waited for the previous one)
+  int ci[kCache];
+#pragma unroll
+  for (int j = 0; j < kCache; j++) {
+    const int i = tid + j * nthr;
+    ci[j]       = cid[i < n ? i : 0];
+  }
+  auto place = [&](unsigned k, int id, bool ok) {
     const unsigned b = (k - kmin) >> shift;
     const int at     = wave_append(ok && b < bstar, &bs.nsel);
     if (at >= 0) {
-      sid[at] = cid[i];
+      sid[at] = id;
       if (skey) skey[at] = __uint_as_float(k);
     }
     const int t = wave_append(ok && b == bstar, &bs.ntb);
     if (t >= 0 && t < kTieCap) {
       sh.tkey[t] = k;
-      sh.tid[t]  = cid[i];
+      sh.tid[t]  = id;
     }
-  });
+  };
+#pragma unroll
+  for (int j = 0; j < kCache; j++)
+    place(kr[j], ci[j], kr[j] != kNone);
+  for (int i0 = kCache * nthr; i0 < n; i0 += nthr) {  // keys past the cache: key and id read together
+    const int i  = i0 + tid;
+    const int ii = i < n ? i : 0;
+    const unsigned kv = kd[ii];
+    const int id      = cid[ii];
+    place(i < n ? kv : kNone, id, i < n);
+  }
   __syncthreads();
   const int ntb = bs.ntb;
   if (ntb > kTieCap) {  // more keys in bin b* than the buffer holds: rank each against every key of b*
