@@ -1,0 +1,59 @@
+"""bench.py's helpers on the CPU: the workloads of BASELINE.json, the algorithmic byte counts of every stage
+(both search modes), the committed rocprof traffic lookup, the distance check, and the one-GPU refusal."""
+
+import os
+import subprocess
+import sys
+
+import numpy as np
+from conftest import ROOT
+
+sys.path.insert(0, ROOT)
+import bench  # noqa: E402
+
+COUNTERS = dict(seg_hits=1_400_000, entries1=10_000 * 1800, distinct1=10_000 * 1700, reranked1=10_000 * 128,
+                starts2=[10_000 * 64] * 16, distinct2=[10_000 * 3000] * 16, reranked2=[10_000 * 128] * 16,
+                hit_level=[600_000, 500_000, 200_000, 80_000, 20_000, 0, 0, 0])
+
+
+def test_workloads():
+    assert {"deep100m", "sift1m", "gist1m", "cpu100k", "deep100m-host"} <= set(bench.CONFIGS)
+    assert bench.CONFIGS["deep100m"]["n"] == 100_000_000 and bench.CONFIGS["deep100m"]["d"] == 96
+    assert bench.CONFIGS["deep100m-host"]["host"] == ("vectors",)
+
+
+def test_stage_bytes_cover_every_stage():
+    args = dict(m=10_000, C=150, S=96, D=96, KO=64, table_len=64, starts=64, w=32, L=5, FR=32)
+    for name in ("gather_lists", "gather_rows", "rerank_keep", "rerank_keep_wave", "probe", "project", "sketch_keep",
+                 "sketch_keep_wave", "final_rerank"):
+        b = bench.stage_bytes(name, 0, COUNTERS, **args)
+        assert isinstance(b, int) and b > 0, name
+    assert bench.stage_bytes("center", 0, COUNTERS, **args) is None
+    # gather_rows: starts + table rows + every distinct sketch row at S + 8 bytes + the query's sketch
+    want = 10_000 * 64 * 8 + 10_000 * 64 * 64 * 4 + 10_000 * 3000 * (96 + 8) + 10_000 * (96 * 4 + 4)
+    assert bench.stage_bytes("gather_rows", 0, COUNTERS, **args) == want
+
+
+def test_measured_traffic_from_the_committed_profile():
+    p = dict(read=12, starts=64, waves=2, rerank=128, wave_rerank=128)
+    t, src = bench.measured_traffic("deep100m", p, "gather_rows", 100_000_000, 2.5e9)
+    assert t == 3_233_023_976 and "same parameters" in src
+    t2, src2 = bench.measured_traffic("deep100m", dict(p, read=16), "gather_rows", 100_000_000, 2.5e9)
+    assert t2 is not None and "per algorithmic byte" in src2
+    assert bench.measured_traffic("sift1m", p, "gather_rows", 1_000_000, 1e9) == (None, None)
+
+
+def test_distance_error():
+    g = np.random.default_rng(0)
+    X = g.standard_normal((500, 16)).astype(np.float32)
+    Q = g.standard_normal((20, 16)).astype(np.float32)
+    I = g.integers(0, 500, (20, 10))
+    Xh = X.astype(np.float16).astype(np.float64)
+    D = ((Xh[I] - Q.astype(np.float64)[:, None, :]) ** 2).sum(-1).astype(np.float32)
+    assert bench.distance_error(X, Q, D, I) < 1e-6
+    assert bench.distance_error(X, Q, D * 1.01, I) > 5e-3
+
+
+def test_one_gpu_only():
+    out = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True, text=True)
+    assert out.returncode != 0 and "one GPU" in (out.stdout + out.stderr)
