@@ -86,6 +86,16 @@ cuvsError_t octexIndexPlanInfo(cuvsOctexIndex_t index, int32_t* info);
  */
 cuvsError_t octexIndexPlaceOnHost(cuvsOctexIndex_t index, int32_t vectors, int32_t table, int32_t sketch);
 
+/**
+ * Open and check an index directory on the host, as cuvsOctexLoad does before it touches a device:
+ * meta.json parsed ("files" remapping honoured, unknown keys ignored), every array's dtype and full shape
+ * compared with meta.json, the copies the load parameters select, and every level's cell table inside its
+ * keys and lists.  info (10 int64, optional): n, dim, copies selected, copies in the directory, blocks,
+ * levels, list_len, log_buckets, sketch_width, table_len.  Makes no HIP call, so it runs without a GPU.
+ * No counterpart in the reference, whose load reads and places in one pass (load.cu:206-494).
+ */
+cuvsError_t octexIndexCheckDirectory(const char* path, cuvsOctexLoadParams_t params, int64_t* info);
+
 /* ---- stage entry points (fp16 arrays as raw 16-bit words) ---- */
 
 /** qc = q - mu, qh = fp16(qc) (search_kernels.cuh:57-69). */

@@ -117,7 +117,7 @@ EXPORTS = (
     "cuvsOctexIndexGetCopies", "cuvsOctexIndexGetNumDevices", "cuvsOctexIndexGetDevices",
     "cuvsOctexIndexGetDeviceBytes", "cuvsOctexBuild", "cuvsOctexLoad", "cuvsOctexSearch",
     "octexIndexCopyPlanBuffer", "octexIndexPlanInfo", "octexBuildInMemory", "octexIndexProfileBatch", "octexIndexCopyArray",
-    "octexIndexCopyArrayRange", "octexIndexCopyArrayRanges",
+    "octexIndexCopyArrayRange", "octexIndexCopyArrayRanges", "octexIndexCheckDirectory",
     "octexStageCenter", "octexStageProject", "octexStageSketchQuery", "octexStageE8", "octexStageProbe",
     "octexStageGather", "octexStageRerankKeep", "octexStageSketchKeep", "octexStagePickStarts",
     "octexStageFinalRerank", "octexStageTakeK",

@@ -734,84 +734,35 @@ auto build_in_memory(index_params const& params, dataset_view const& x, build_re
 
 namespace {
 
-/** Streams an .npy file: header first, then the data in pieces. */
-class npy_stream {
- public:
-  npy_stream(std::string const& path, const char* descr, std::vector<int64_t> const& shape) : path_(path)
-  {
-    std::string sh = "(";
-    for (size_t i = 0; i < shape.size(); i++) {
-      sh += std::to_string(shape[i]);
-      if (shape.size() == 1 || i + 1 < shape.size()) sh += ",";
-      if (i + 1 < shape.size()) sh += " ";
-    }
-    sh += ")";
-    std::string hdr = std::string("{'descr': '") + descr + "', 'fortran_order': False, 'shape': " + sh + ", }";
-    const size_t total = 10 + hdr.size() + 1;
-    hdr.append((64 - total % 64) % 64, ' ');
-    hdr += '\n';
-    f_ = std::fopen(path.c_str(), "wb");
-    OCTEX_EXPECTS(f_ != nullptr, "octex: cannot write %s", path.c_str());
-    const char magic[8] = {'\x93', 'N', 'U', 'M', 'P', 'Y', '\x01', '\x00'};
-    const uint16_t hl   = static_cast<uint16_t>(hdr.size());
-    put(magic, 8);
-    put(&hl, 2);
-    put(hdr.data(), hdr.size());
+/** Device bytes appended to an .npy file through a host buffer of at most 64 MB. */
+void put_device(npy_writer& w, const void* p, size_t bytes)
+{
+  constexpr size_t kChunk = size_t{64} << 20;
+  std::vector<char> h(std::min(bytes, kChunk));
+  for (size_t o = 0; o < bytes; o += kChunk) {
+    const size_t m = std::min(kChunk, bytes - o);
+    OCTEX_HIP(hipMemcpy(h.data(), static_cast<const char*>(p) + o, m, hipMemcpyDeviceToHost));
+    w.put(h.data(), m);
   }
-  void put(const void* p, size_t bytes)
-  {
-    OCTEX_EXPECTS(bytes == 0 || std::fwrite(p, 1, bytes, f_) == bytes, "octex: short write %s", path_.c_str());
-  }
-  void zeros(size_t bytes)
-  {
-    static const std::vector<char> z(1 << 20, 0);
-    while (bytes > 0) {
-      size_t m = std::min(bytes, z.size());
-      put(z.data(), m);
-      bytes -= m;
-    }
-  }
-  /** rows of `row_bytes` stored `pitch` bytes apart on the device, written back to back */
-  void put_device_rows(const void* p, int64_t rows, size_t row_bytes, size_t pitch)
-  {
-    if (pitch == row_bytes) {
-      put_device(p, static_cast<size_t>(rows) * row_bytes);
-      return;
-    }
-    const int64_t chunk = std::max<int64_t>(1, (int64_t{64} << 20) / static_cast<int64_t>(pitch));
-    std::vector<char> h(static_cast<size_t>(std::min(chunk, rows)) * pitch);
-    for (int64_t r0 = 0; r0 < rows; r0 += chunk) {
-      const int64_t m = std::min(chunk, rows - r0);
-      OCTEX_HIP(hipMemcpy(h.data(), static_cast<const char*>(p) + r0 * pitch, static_cast<size_t>(m) * pitch,
-                          hipMemcpyDeviceToHost));
-      for (int64_t r = 0; r < m; r++)
-        put(h.data() + r * pitch, row_bytes);
-    }
-  }
-  void put_device(const void* p, size_t bytes)
-  {
-    constexpr size_t kChunk = size_t{64} << 20;
-    std::vector<char> h(std::min(bytes, kChunk));
-    for (size_t o = 0; o < bytes; o += kChunk) {
-      size_t m = std::min(kChunk, bytes - o);
-      OCTEX_HIP(hipMemcpy(h.data(), static_cast<const char*>(p) + o, m, hipMemcpyDeviceToHost));
-      put(h.data(), m);
-    }
-  }
-  ~npy_stream()
-  {
-    if (f_ != nullptr) std::fclose(f_);
-  }
-  void close()
-  {
-    OCTEX_EXPECTS(std::fclose(f_) == 0, "octex: short write %s", path_.c_str());
-    f_ = nullptr;
-  }
+}
 
- private:
-  std::string path_;
-  FILE* f_ = nullptr;
-};
+/** Rows of `row_bytes` stored `pitch` bytes apart on the device, appended back to back. */
+void put_device_rows(npy_writer& w, const void* p, int64_t rows, size_t row_bytes, size_t pitch)
+{
+  if (pitch == row_bytes) {
+    put_device(w, p, static_cast<size_t>(rows) * row_bytes);
+    return;
+  }
+  const int64_t chunk = std::max<int64_t>(1, (int64_t{64} << 20) / static_cast<int64_t>(pitch));
+  std::vector<char> h(static_cast<size_t>(std::min(chunk, rows)) * pitch);
+  for (int64_t r0 = 0; r0 < rows; r0 += chunk) {
+    const int64_t m = std::min(chunk, rows - r0);
+    OCTEX_HIP(hipMemcpy(h.data(), static_cast<const char*>(p) + r0 * pitch, static_cast<size_t>(m) * pitch,
+                        hipMemcpyDeviceToHost));
+    for (int64_t r = 0; r < m; r++)
+      w.put(h.data() + r * pitch, row_bytes);
+  }
+}
 
 }  // namespace
 
@@ -829,23 +780,23 @@ void write_index(index_impl const& ix, build_record const& rec, index_params con
   write_npy(file("base.npy"), rec.base.data(), {C, L});
   write_npy(file("cells.npy"), rec.cells.data(), {C, L});
   {
-    npy_stream k(file("keys.npy"), "<i8", {C, L, ix.mmax});
-    k.put_device(ix.keys.ptr, ix.keys.size);
+    npy_writer k(file("keys.npy"), "<i8", {C, L, ix.mmax});
+    put_device(k, ix.keys.ptr, ix.keys.size);
     k.close();
   }
   {
-    npy_stream o(file("offsets.npy"), "<i4", {C, L, T1});
-    o.put_device(ix.offsets.ptr, ix.offsets.size);
+    npy_writer o(file("offsets.npy"), "<i4", {C, L, T1});
+    put_device(o, ix.offsets.ptr, ix.offsets.size);
     o.close();
   }
   {
     int64_t lmax = 0;
     for (auto r : ix.list_rows)
       lmax = std::max(lmax, r * l);
-    npy_stream ls(file("lists.npy"), "<i4", {C, lmax});
+    npy_writer ls(file("lists.npy"), "<i4", {C, lmax});
     for (int c = 0; c < C; c++) {
       const size_t bytes = static_cast<size_t>(ix.list_rows[c] * l) * sizeof(int32_t);
-      ls.put_device(ix.copy_lists[c].ptr, bytes);
+      put_device(ls, ix.copy_lists[c].ptr, bytes);
       ls.zeros(static_cast<size_t>(lmax) * sizeof(int32_t) - bytes);
     }
     ls.close();
@@ -853,18 +804,18 @@ void write_index(index_impl const& ix, build_record const& rec, index_params con
   write_npy(file("sketch_basis.npy"), rec.basis.data(), {d, int64_t{S}});
   write_npy(file("sketch_scale.npy"), rec.scale.data(), {int64_t{S}});
   {
-    npy_stream sk(file("sketch.npy"), "|i1", {n, int64_t{S}});
-    sk.put_device_rows(ix.sketch.ptr, n, S, ix.sketch_pitch);
+    npy_writer sk(file("sketch.npy"), "|i1", {n, int64_t{S}});
+    put_device_rows(sk, ix.sketch.ptr, n, S, ix.sketch_pitch);
     sk.close();
   }
   {
-    npy_stream v(file("vectors.npy"), "<f2", {n, d});
-    v.put_device(ix.vectors.ptr, static_cast<size_t>(n) * d * sizeof(__half));
+    npy_writer v(file("vectors.npy"), "<f2", {n, d});
+    put_device(v, ix.vectors.ptr, static_cast<size_t>(n) * d * sizeof(__half));
     v.close();
   }
   if (ix.table_len > 0) {
-    npy_stream t(file("table.npy"), "<i4", {n, int64_t{ix.table_len}});
-    t.put_device(ix.table.ptr, static_cast<size_t>(n) * ix.table_len * sizeof(int32_t));
+    npy_writer t(file("table.npy"), "<i4", {n, int64_t{ix.table_len}});
+    put_device(t, ix.table.ptr, static_cast<size_t>(n) * ix.table_len * sizeof(int32_t));
     t.close();
   }
   // meta.json last: a directory without it is incomplete (build.cu:67-98, 423-424)

@@ -4,6 +4,7 @@
 
 #include "build.hpp"
 #include "common.hpp"
+#include "directory.hpp"
 #include "kernels.hpp"
 #include "index_impl.hpp"
 #include "search.hpp"
@@ -375,6 +376,21 @@ extern "C" cuvsError_t cuvsOctexSearch(cuvsResources_t res, cuvsOctexSearchParam
 }
 
 // ==================================================================== introspection (octex_amd.h)
+
+extern "C" cuvsError_t octexIndexCheckDirectory(const char* path, cuvsOctexLoadParams_t params, int64_t* info)
+{
+  return translate_exceptions([=] {
+    OCTEX_EXPECTS(path != nullptr, "octex: the index directory is NULL");
+    const auto p = params != nullptr ? to_cpp(*params) : octex::load_params{};
+    auto dir     = octex::detail::open_directory(std::string(path), p);
+    if (info != nullptr) {
+      const int64_t v[10] = {dir.n,      dir.dim,         static_cast<int64_t>(dir.copy_list.size()),
+                             dir.all_copies, dir.blocks, static_cast<int64_t>(dir.spacings.size()),
+                             dir.list_len, dir.log_buckets, dir.sketch_width, dir.table_len};
+      std::memcpy(info, v, sizeof(v));
+    }
+  });
+}
 
 extern "C" cuvsError_t octexIndexCopyPlanBuffer(cuvsOctexIndex_t index, const char* name, void* dst,
                                                 int64_t bytes, int64_t* size)

@@ -3,6 +3,7 @@
 // [C * 8b, D] and the shifts fp16, inv_f = float(1 / spacing) from the JSON value (load.cu:385-402).
 
 #include "common.hpp"
+#include "directory.hpp"
 #include "index_impl.hpp"
 #include "meta.hpp"
 #include "npy.hpp"
@@ -10,6 +11,7 @@
 #include <hip/hip_fp16.h>
 
 #include <algorithm>
+#include <cmath>
 #include <fstream>
 #include <sstream>
 #include <thread>
@@ -79,87 +81,150 @@ auto to_pinned(npy_file const& f, size_t bytes) -> hbuf
 
 }  // namespace
 
+namespace detail {
+
+auto open_directory(std::string const& path, load_params const& params) -> directory
+{
+  directory dir;
+  dir.path               = path;
+  const std::string text = read_text(path + "/meta.json");
+  auto meta              = json_parser(text).parse();
+  OCTEX_EXPECTS(static_cast<int>(meta.number("format", 1)) == 1, "octex: unknown index format");
+  auto count = [&](const char* key, double dflt) {
+    const double v = meta.number(key, dflt);
+    OCTEX_EXPECTS(v >= 0 && v == std::floor(v) && v < 9.2e18, "octex: meta.json: %s must be a non-negative integer",
+                  key);
+    return static_cast<int64_t>(v);
+  };
+  dir.n            = count("n", 0);
+  dir.dim          = count("dim", 0);
+  dir.all_copies   = static_cast<int>(count("copies", 0));
+  dir.blocks       = static_cast<int>(count("blocks", 4));
+  dir.list_len     = static_cast<int>(count("list_len", 0));
+  dir.log_buckets  = static_cast<int>(count("log_buckets", 20));
+  dir.sketch_width = static_cast<int>(count("sketch_width", 0));
+  dir.table_len    = static_cast<int>(count("table_len", 0));
+  if (auto sp = meta.get("spacings"); sp != nullptr && sp->kind == json_value::array_v)
+    for (auto const& v : sp->a) {
+      OCTEX_EXPECTS(v.kind == json_value::number_v && v.d > 0, "octex: meta.json: spacings must be positive numbers");
+      dir.spacings.push_back(v.d);
+    }
+  if (auto fm = meta.get("files"); fm != nullptr && fm->kind == json_value::object_v)
+    for (auto const& [name, where] : fm->o) {
+      OCTEX_EXPECTS(where.kind == json_value::string_v && !where.s.empty(),
+                    "octex: meta.json: files.%s must be a path", name.c_str());
+      dir.files[name] = where.s;
+    }
+  OCTEX_EXPECTS(dir.dim % 2 == 0, "octex: the dimension must be even");
+  OCTEX_EXPECTS(dir.sketch_width % 16 == 0 && dir.sketch_width <= 512 && dir.sketch_width > 0,
+                "octex: sketch width: a multiple of 16, <= 512");
+  OCTEX_EXPECTS(dir.blocks >= 1 && dir.blocks <= 8 && dir.blocks != 7, "octex: blocks must be 1-6 or 8");
+  OCTEX_EXPECTS(!dir.spacings.empty(), "octex: at least one spacing");
+  OCTEX_EXPECTS(dir.list_len >= 1 && dir.log_buckets >= 1 && dir.log_buckets <= 30 && dir.n >= 1 && dir.n < (int64_t{1} << 31),
+                "octex: meta.json: list_len, log_buckets or n out of range");
+
+  // copies: the saved parts (equal consecutive ranges) cut to copies_per_part, or the first copies_limit
+  // copies of a single part (load.cu:252-263); one GPU holds them all
+  const int nparts = std::max(1, params.parts);
+  for (int q = 0; q < nparts; q++) {
+    const int lo = static_cast<int>(int64_t{dir.all_copies} * q / nparts);
+    int hi       = static_cast<int>(int64_t{dir.all_copies} * (q + 1) / nparts);
+    if (params.copies_per_part > 0) hi = std::min(hi, lo + params.copies_per_part);
+    if (nparts == 1 && params.copies_limit > 0) hi = std::min(hi, lo + params.copies_limit);
+    for (int c = lo; c < hi; c++)
+      dir.copy_list.push_back(c);
+  }
+  OCTEX_EXPECTS(!dir.copy_list.empty(), "octex: a device holds no copies (fewer copies or parts than devices)");
+
+  auto file = [&](std::string const& name) {
+    auto it = dir.files.find(name);
+    if (it == dir.files.end()) return path + "/" + name + ".npy";
+    return it->second[0] == '/' ? it->second : path + "/" + it->second;
+  };
+  const int64_t C = dir.all_copies, L = static_cast<int64_t>(dir.spacings.size()), w = 8 * dir.blocks;
+  const int64_t D = dir.dim, N = dir.n, S = dir.sketch_width, T1 = (int64_t{1} << dir.log_buckets) + 1;
+  // every array with its dtype and full shape against meta.json, before anything is read from it
+  auto open = [&](std::string const& name, const char* descr, std::vector<int64_t> const& shape) {
+    npy_file f(file(name));
+    OCTEX_EXPECTS(f.hdr.descr == descr, "octex: %s has dtype %s, expected %s", f.path().c_str(), f.hdr.descr.c_str(),
+                  descr);
+    bool same = f.shape().size() == shape.size();
+    for (size_t i = 0; same && i < shape.size(); i++)
+      same = shape[i] < 0 ? f.shape()[i] >= 0 : f.shape()[i] == shape[i];
+    std::string want, got;
+    for (auto v : shape)
+      want += (want.empty() ? "" : ", ") + (v < 0 ? std::string("*") : std::to_string(v));
+    for (auto v : f.shape())
+      got += (got.empty() ? "" : ", ") + std::to_string(v);
+    OCTEX_EXPECTS(same, "octex: %s has shape (%s), meta.json needs (%s)", f.path().c_str(), got.c_str(), want.c_str());
+    return f;
+  };
+  dir.lists   = open("lists", "<i4", {C, -1});
+  dir.keys    = open("keys", "<i8", {C, L, -1});
+  dir.offsets = open("offsets", "<i4", {C, L, T1});
+  dir.base    = open("base", "<i4", {C, L});
+  dir.proj    = open("proj", "<f4", {C, D, w});
+  dir.shift   = open("shift", "<f4", {C, w});
+  dir.mean    = open("mean", "<f4", {D});
+  dir.basis   = open("sketch_basis", "<f4", {D, S});
+  dir.scale   = open("sketch_scale", "<f4", {S});
+  dir.sketch  = open("sketch", "|i1", {N, S});
+  dir.vectors = open("vectors", "<f2", {N, D});
+  if (dir.table_len > 0) dir.table = open("table", "<i4", {N, dir.table_len});
+  OCTEX_EXPECTS(dir.lists.dim(1) % dir.list_len == 0, "octex: lists rows hold %lld entries, not a multiple of list_len %d",
+                static_cast<long long>(dir.lists.dim(1)), dir.list_len);
+  // the cell tables stay inside their arrays: every bucket run inside keys, every level's rows inside lists
+  const int64_t mmax = dir.keys.dim(2), rows = dir.lists.dim(1) / dir.list_len;
+  const int32_t* off = dir.offsets.as<int32_t>();
+  const int32_t* bs  = dir.base.as<int32_t>();
+  for (int c : dir.copy_list)
+    for (int64_t j = 0; j < L; j++) {
+      const int32_t* o  = off + (c * L + j) * T1;
+      const int64_t end = o[T1 - 1];
+      OCTEX_EXPECTS(o[0] == 0 && end <= mmax && bs[c * L + j] >= 0 && bs[c * L + j] + end <= rows,
+                    "octex: copy %d level %lld: its cells run past keys (%lld) or lists (%lld rows)", c,
+                    static_cast<long long>(j), static_cast<long long>(mmax), static_cast<long long>(rows));
+    }
+  return dir;
+}
+
+}  // namespace detail
+
 auto load(raft::resources const& res, std::string const& path, load_params const& params) -> index
 {
   (void)res;
+  detail::directory dir = detail::open_directory(path, params);  // every check, no device call
   int cur = 0;
   OCTEX_HIP(hipGetDevice(&cur));
   auto impl = std::make_shared<index_impl>();
   auto& ix  = *impl;
   ix.path   = path;
   ix.params = params;
-  const std::string text = read_text(path + "/meta.json");
-  auto meta              = detail::json_parser(text).parse();
-  OCTEX_EXPECTS(static_cast<int>(meta.number("format", 1)) == 1, "octex: unknown index format");
-  ix.n             = static_cast<int64_t>(meta.number("n", 0));
-  ix.dim           = static_cast<int64_t>(meta.number("dim", 0));
-  const int all_c  = static_cast<int>(meta.number("copies", 0));
-  ix.blocks        = static_cast<int>(meta.number("blocks", 4));
-  ix.list_len      = static_cast<int>(meta.number("list_len", 0));
-  ix.log_buckets   = static_cast<int>(meta.number("log_buckets", 20));
-  ix.sketch_width  = static_cast<int>(meta.number("sketch_width", 0));
-  ix.table_len     = static_cast<int>(meta.number("table_len", 0));
-  std::vector<double> spacings;
-  if (auto sp = meta.get("spacings"); sp != nullptr && sp->kind == detail::json_value::array_v)
-    for (auto const& v : sp->a)
-      spacings.push_back(v.d);
-  for (double f : spacings)
+  ix.n            = dir.n;
+  ix.dim          = dir.dim;
+  ix.blocks       = dir.blocks;
+  ix.list_len     = dir.list_len;
+  ix.log_buckets  = dir.log_buckets;
+  ix.sketch_width = dir.sketch_width;
+  ix.table_len    = dir.table_len;
+  for (double f : dir.spacings)
     ix.spacings.push_back(static_cast<float>(f));
-  std::map<std::string, std::string> files;
-  if (auto fm = meta.get("files"); fm != nullptr && fm->kind == detail::json_value::object_v)
-    for (auto const& kv : fm->o)
-      files[kv.first] = kv.second.s;
-  auto file = [&](std::string const& name) {
-    auto it = files.find(name);
-    if (it == files.end()) return path + "/" + name + ".npy";
-    return it->second[0] == '/' ? it->second : path + "/" + it->second;
-  };
-  OCTEX_EXPECTS(ix.dim % 2 == 0, "octex: the dimension must be even");
-  OCTEX_EXPECTS(ix.sketch_width % 16 == 0 && ix.sketch_width <= 512 && ix.sketch_width > 0,
-                "octex: sketch width: a multiple of 16, <= 512");
-  OCTEX_EXPECTS(ix.blocks >= 1 && ix.blocks <= 8 && ix.blocks != 7, "octex: blocks must be 1-6 or 8");
-  const int ll = params.list_limit > 0 ? std::min(params.list_limit, ix.list_len) : ix.list_len;
-
-  // one GPU holds the whole index: the first listed device, or the current one
+  const int all_c = dir.all_copies;
+  const int ll    = params.list_limit > 0 ? std::min(params.list_limit, ix.list_len) : ix.list_len;
   ix.device  = params.devices.empty() ? cur : params.devices.front();
   ix.devices = {ix.device};
-  // copies: the saved parts (equal consecutive ranges) cut to copies_per_part, or the first
-  // copies_limit copies of a single part (load.cu:252-263)
-  const int nparts = std::max(1, params.parts);
-  std::vector<int> cl;
-  for (int q = 0; q < nparts; q++) {
-    int lo = static_cast<int>(int64_t{all_c} * q / nparts);
-    int hi = static_cast<int>(int64_t{all_c} * (q + 1) / nparts);
-    if (params.copies_per_part > 0) hi = std::min(hi, lo + params.copies_per_part);
-    if (nparts == 1 && params.copies_limit > 0) hi = std::min(hi, lo + params.copies_limit);
-    for (int c = lo; c < hi; c++)
-      cl.push_back(c);
-  }
-  OCTEX_EXPECTS(!cl.empty(), "octex: a device holds no copies (fewer copies or parts than devices)");
+  std::vector<int> const& cl = dir.copy_list;
   ix.copies = static_cast<int>(cl.size());
-
-  npy_file lists(file("lists")), keys(file("keys")), offsets(file("offsets")), base(file("base"));
-  npy_file proj(file("proj")), shift(file("shift")), mean(file("mean"));
-  npy_file basis(file("sketch_basis")), scale(file("sketch_scale"));
-  npy_file sketch(file("sketch")), vectors(file("vectors"));
-  std::unique_ptr<npy_file> table;
-  if (ix.table_len > 0) table = std::make_unique<npy_file>(file("table"));
-
+  npy_file const &lists = dir.lists, &keys = dir.keys, &offsets = dir.offsets, &base = dir.base;
+  npy_file const &proj = dir.proj, &shift = dir.shift, &mean = dir.mean, &basis = dir.basis, &scale = dir.scale;
+  npy_file const &sketch = dir.sketch, &vectors = dir.vectors;
+  npy_file const* table = ix.table_len > 0 ? &dir.table : nullptr;
+  std::vector<double> const& spacings = dir.spacings;
   const int L     = ix.levels();
   const int width = 8 * ix.blocks;
   const int64_t D = ix.dim, N = ix.n, S = ix.sketch_width;
-  OCTEX_EXPECTS(L >= 1, "octex: at least one spacing");
-  OCTEX_EXPECTS(lists.dim(0) == all_c && keys.dim(1) == L && proj.dim(2) == width &&
-                  offsets.dim(1) == L && base.dim(1) == L && proj.dim(1) == D,
-                "octex: bad shapes");
-  OCTEX_EXPECTS(vectors.shape().size() >= 2 && vectors.dim(0) == N && vectors.dim(1) == D,
-                "octex: vectors shape");
-  OCTEX_EXPECTS(sketch.dim(0) == N && sketch.dim(1) == S, "octex: sketch shape");
-  OCTEX_EXPECTS(!table || (table->dim(0) == N && table->dim(1) == ix.table_len), "octex: table shape");
   ix.T1 = offsets.dim(2);
-  OCTEX_EXPECTS(ix.T1 == (int64_t{1} << ix.log_buckets) + 1,
-                "octex: offsets hold %lld buckets, log_buckets %d", static_cast<long long>(ix.T1 - 1),
-                ix.log_buckets);
+  (void)all_c;
 
   OCTEX_HIP(hipSetDevice(ix.device));
   OCTEX_HIP(hipStreamCreateWithFlags(&ix.stream, hipStreamNonBlocking));

@@ -1,126 +1,136 @@
-"""Faiss-style GPU index answered by octex on MI355X: the interface of faiss.Index (octex/faiss.py:10-166 of the
-reference), without importing faiss.
+"""Faiss-style adapter: GPU index classes with the faiss.Index calls (d, ntotal, is_trained, metric_type, train,
+add, search, reset) answered by an octex index, so that
 
-    from octex_amd import faiss
-    index = faiss.IndexOctex(d, copies=64)      # or faiss.GpuIndexCagra(faiss.StandardGpuResources(), d)
-    index.add(xb)                               # the index is built by the first search after an add
-    D, I = index.search(xq, 10)                 # float32 squared distances, int64 ids, nearest first
-    faiss.write_index(index, "index_dir"); index = faiss.read_index("index_dir")
+    from octex_amd import faiss                  # instead of: import faiss
+    index = faiss.IndexOctex(d)                  # or faiss.GpuIndexCagra(faiss.StandardGpuResources(), d)
+    index.add(xb)
+    D, I = index.search(xq, k)
 
-Vectors are added in batches (numpy or torch, host or GPU); ids are positions in the order of the adds.  Results
-come back in the framework of the queries.  Only METRIC_L2 is supported.
+runs unchanged.  The reference ships the same adapter (octex/faiss.py); class names, constructor forms and
+error texts follow it.  Added vectors are kept on the host in the order of the adds (ids are their positions)
+and the octex index is built when a search first needs it, or by build().  Only METRIC_L2 is served.
+faiss itself is never imported.
 """
 
 import os
 
 import numpy as np
 
-from . import index as _index
+from . import _arrays
+from . import index as _octex
 
-METRIC_INNER_PRODUCT, METRIC_L2 = 0, 1  # faiss.METRIC_INNER_PRODUCT, faiss.METRIC_L2
-LOAD_ARGS = ("placement", "vectors_on_host", "shard_vectors", "table_on_host", "sketch")
+METRIC_INNER_PRODUCT, METRIC_L2 = 0, 1  # faiss.METRIC_INNER_PRODUCT / faiss.METRIC_L2
+PLACEMENT_FIELDS = ("placement", "vectors_on_host", "shard_vectors", "table_on_host", "sketch")
 
 
-def _check_metric(metric):
+def _l2_only(metric):
     if metric != METRIC_L2:
         raise ValueError("octex.faiss: only METRIC_L2 is supported (octex searches by squared Euclidean distance)")
 
 
-def _host_rows(x):
-    """A host numpy matrix (float32, or float16 kept as is) of a numpy, torch or DLPack array."""
-    if type(x).__module__.startswith("torch"):
-        x = x.detach().cpu().numpy()
-    elif not isinstance(x, np.ndarray) and hasattr(x, "__dlpack__"):
-        try:
-            x = np.from_dlpack(x)
-        except (RuntimeError, BufferError, TypeError):  # device memory: through torch
-            import torch
-
-            x = torch.from_dlpack(x).cpu().numpy()
-    x = np.asarray(x)
-    if x.dtype not in (np.float32, np.float16):
-        x = x.astype(np.float32)
-    if x.ndim != 2:
-        raise ValueError("octex.faiss: vectors must be a matrix [n, d]")
-    return np.ascontiguousarray(x)
-
-
 class SearchParametersOctex:
-    """Per-call search parameters (fields of cuvs::neighbors::octex::search_params); other names are ignored."""
+    """Per-call search parameters: octex's search_params fields (`params`); other names (CAGRA's) are dropped."""
 
     def __init__(self, **kwargs):
-        self.params = {k: v for k, v in kwargs.items() if k in _index.SEARCH_PARAMS}
+        self.params = {k: kwargs[k] for k in kwargs if k in _octex.SEARCH_PARAMS}
 
 
 SearchParametersCagra = SearchParametersOctex
 
 
-class IndexOctex:
-    """An octex index with the faiss.Index interface: d, ntotal, is_trained, metric_type, train, add, search, reset.
+class _Rows:
+    """The vectors added so far, on the host, in order; fp16 blocks stay fp16 while every block is fp16."""
 
-    Keyword arguments: octex index parameters (copies, list_len, table_len, seed, devices, ...), load arguments
-    (placement, vectors_on_host, ...) and default search parameters (read, starts, waves, ...).
+    def __init__(self, d):
+        self.d = d
+        self.blocks = []
+        self.count = 0
+
+    def add(self, x):
+        x = _arrays.host_rows(x, (np.float32, np.float16), "vectors")
+        if x.shape[1] != self.d:
+            raise ValueError(f"octex.faiss: vectors have dimension {x.shape[1]}, the index {self.d}")
+        self.blocks.append(x)
+        self.count += x.shape[0]
+
+    def matrix(self):
+        if len(self.blocks) == 1:
+            return self.blocks[0]
+        dtype = np.float16 if all(b.dtype == np.float16 for b in self.blocks) else np.float32
+        return np.concatenate([b.astype(dtype, copy=False) for b in self.blocks])
+
+
+class IndexOctex:
+    """An octex index with the faiss.Index interface.
+
+    Keyword arguments are octex's index parameters (copies, list_len, table_len, seed, devices, ...: kept in
+    `index_params`), the load placement (placement, vectors_on_host, ...: `load_args`) and default search
+    parameters (read, starts, waves, ...: `search_params`).
     """
 
     def __init__(self, d, metric=METRIC_L2, **kwargs):
-        _check_metric(metric)
+        _l2_only(metric)
         self.d, self.metric_type, self.is_trained = int(d), metric, True
-        self.index_params = {k: v for k, v in kwargs.items() if k in _index.INDEX_PARAMS}
-        self.load_args = {k: v for k, v in kwargs.items() if k in LOAD_ARGS}
-        self.search_params = {k: v for k, v in kwargs.items() if k in _index.SEARCH_PARAMS}
-        unknown = set(kwargs) - set(self.index_params) - set(self.load_args) - set(self.search_params)
-        if unknown:
-            raise TypeError(f"octex.faiss: unknown parameters {sorted(unknown)}")
+        self.index_params, self.load_args, self.search_params = {}, {}, {}
+        for name, value in kwargs.items():
+            if name in _octex.INDEX_PARAMS:
+                self.index_params[name] = value
+            elif name in PLACEMENT_FIELDS:
+                self.load_args[name] = value
+            elif name in _octex.SEARCH_PARAMS:
+                self.search_params[name] = value
+            else:
+                raise TypeError(f"octex.faiss: unknown parameters {sorted(set(kwargs) - set(self._accepted()))}")
         self.reset()
+
+    @staticmethod
+    def _accepted():
+        return set(_octex.INDEX_PARAMS) | set(PLACEMENT_FIELDS) | set(_octex.SEARCH_PARAMS)
+
+    def reset(self):
+        self._rows = _Rows(self.d)  # None after read_index: the rows are in the index directory
+        self._index = None          # the octex index of the rows, once built
+        self._stale = False         # rows added since the build
 
     @property
     def ntotal(self):
-        return (0 if self._built is None else self._built.size) + sum(len(x) for x in self._pending)
-
-    def reset(self):
-        self._parts = []  # host batches of the built index, in order
-        self._pending = []  # batches added since
-        self._built = None
+        if self._rows is None:
+            return self._index.size
+        return self._rows.count
 
     def train(self, x):
-        pass
+        """Nothing to train (as for Faiss's flat indexes)."""
 
     def add(self, x):
-        x = _host_rows(x)
-        if x.shape[1] != self.d:
-            raise ValueError(f"octex.faiss: vectors have dimension {x.shape[1]}, the index {self.d}")
-        self._pending.append(x)
+        if self._rows is None:  # read from a directory: its stored vectors come first
+            self._rows = _Rows(self.d)
+            self._rows.add(np.asarray(_octex.stored_vectors(self._index.path)))
+        self._rows.add(x)
+        self._stale = True
 
     def build(self):
-        """Build the index of every vector added so far (otherwise the next search does)."""
-        if self._built is not None and not self._pending:
+        """Build the octex index of every vector added so far (a search does it when needed)."""
+        if self._index is not None and not self._stale:
             return self
-        if self._built is not None and not self._parts:  # read from a directory: start from its vectors
-            self._parts = [np.asarray(_index.stored_vectors(self._built.path))]
-        parts = self._parts + self._pending
-        if not parts:
+        if self._rows is None or self._rows.count == 0:
             raise RuntimeError("octex.faiss: the index is empty")
-        data = parts[0] if len(parts) == 1 else np.concatenate([p.astype(np.float32, copy=False) for p in parts])
-        self._built = _index.build(data, **self.load_args, **self.index_params)
-        self._parts, self._pending = parts, []
+        self._index = _octex.build(self._rows.matrix(), **self.load_args, **self.index_params)
+        self._stale = False
         return self
 
     def search(self, x, k, *, params=None, D=None, I=None):
-        if self._built is None or self._pending:
-            self.build()
-        sp = dict(self.search_params)
-        if params is not None:
-            sp.update(getattr(params, "params", {}))
-        return self._built.search(x, k, distances=D, neighbors=I, **sp)
+        self.build()
+        p = dict(self.search_params, **(getattr(params, "params", None) or {}))
+        return self._index.search(x, k, distances=D, neighbors=I, **p)
 
     @property
     def octex(self):
-        """The octex_amd.Index underneath (built on access)."""
-        return self.build()._built
+        """The octex_amd.Index of the added vectors (built on access)."""
+        return self.build()._index
 
 
 class StandardGpuResources:
-    """Accepted for faiss.StandardGpuResources compatibility; octex keeps its own streams."""
+    """faiss.StandardGpuResources stand-in: octex manages its own HIP resources."""
 
     def noTempMemory(self):
         pass
@@ -130,7 +140,7 @@ class StandardGpuResources:
 
 
 class GpuIndexCagraConfig:
-    """Accepted for faiss.GpuIndexCagraConfig compatibility: `device` picks the GPU, the rest is ignored."""
+    """faiss.GpuIndexCagraConfig stand-in: `device` chooses the GPU; the graph fields are not used."""
 
     def __init__(self):
         self.device = None
@@ -139,13 +149,14 @@ class GpuIndexCagraConfig:
 
 
 class GpuIndexCagra(IndexOctex):
-    """faiss.GpuIndexCagra(res, d, metric, config): train(x) builds the index of x, as in Faiss."""
+    """faiss.GpuIndexCagra(res, d, metric, config), or GpuIndexCagra(d): train(x) builds the index of x."""
 
     def __init__(self, res=None, d=None, metric=METRIC_L2, config=None, **kwargs):
-        if d is None and isinstance(res, int):  # GpuIndexCagra(d)
-            res, d = None, res
-        if config is not None and getattr(config, "device", None) is not None:
-            kwargs.setdefault("devices", [int(config.device)])
+        if d is None and isinstance(res, int):
+            d = res
+        device = getattr(config, "device", None)
+        if device is not None and "devices" not in kwargs:
+            kwargs["devices"] = [int(device)]
         super().__init__(d, metric, **kwargs)
         self.is_trained = False
 
@@ -153,7 +164,6 @@ class GpuIndexCagra(IndexOctex):
         self.reset()
         self.add(x)
         self.build()
-        self.is_trained = True
 
     def add(self, x):
         super().add(x)
@@ -166,8 +176,9 @@ def write_index(index, path):
 
 
 def read_index(path, **kwargs):
-    """An IndexOctex over an index directory; keyword arguments: load placement and default search parameters."""
-    loaded = _index.load(os.fspath(path), **{k: v for k, v in kwargs.items() if k not in _index.SEARCH_PARAMS})
-    out = IndexOctex(loaded.dim, **{k: v for k, v in kwargs.items() if k in _index.SEARCH_PARAMS})
-    out._built = loaded
-    return out
+    """An IndexOctex over an index directory; keyword arguments are load arguments and search defaults."""
+    search = {k: v for k, v in kwargs.items() if k in _octex.SEARCH_PARAMS}
+    loaded = _octex.load(os.fspath(path), **{k: v for k, v in kwargs.items() if k not in search})
+    index = IndexOctex(loaded.dim, **search)
+    index._rows, index._index = None, loaded
+    return index

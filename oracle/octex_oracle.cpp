@@ -78,6 +78,22 @@ inline uint32_t fbits(float f)
   std::memcpy(&u, &f, 4);
   return u;
 }
+
+/**
+ * fp64 -> fp16 with a single rounding to nearest even.  The value is first taken to fp32 by rounding to
+ * odd (truncate toward zero, then set the last significand bit when inexact); fp32 keeps 13 more bits than
+ * fp16, so the second rounding sees every tie and every sticky bit the direct rounding would.
+ */
+uint16_t d2h(double d)
+{
+  float f = static_cast<float>(d);
+  if (std::isfinite(f) && static_cast<double>(f) != d) {
+    if (std::fabs(static_cast<double>(f)) > std::fabs(d)) f = std::nextafter(f, 0.0f);
+    uint32_t u = fbits(f) | 1u;
+    std::memcpy(&f, &u, 4);
+  }
+  return f2h(f);
+}
 inline float bitsf(uint32_t u)
 {
   float f;
@@ -388,9 +404,7 @@ void project_rows(const uint16_t* qh, int64_t r0, int64_t r1, int D, const uint1
         acc[j] += a * u[j];
     }
     for (int j = 0; j < wdt; j++) {
-      // fp16 rounding of the fp64 value: through float is exact enough (the double->float rounding
-      // can only matter within 2^-29 relative of an fp16 tie, reported by the ulp test)
-      Y[q * wdt + j] = f2h(static_cast<float>(acc[j]));
+      Y[q * wdt + j] = d2h(acc[j]);  // one rounding of the fp64 value
       if (Yd) Yd[q * wdt + j] = acc[j];
     }
   }

@@ -185,13 +185,32 @@ def exact_dist(x_h, q):
 # ---------------------------------------------------------------- index
 
 
+def copy_selection(all_copies, parts=0, copies_per_part=0, copies_limit=0):
+    """The copies a load places (load.cu:252-263): `parts` equal consecutive ranges, each cut to copies_per_part,
+    or the first copies_limit copies of a single part."""
+    nparts = max(1, parts)
+    sel = []
+    for q in range(nparts):
+        lo, hi = all_copies * q // nparts, all_copies * (q + 1) // nparts
+        if copies_per_part > 0:
+            hi = min(hi, lo + copies_per_part)
+        if nparts == 1 and copies_limit > 0:
+            hi = min(hi, lo + copies_limit)
+        sel.extend(range(lo, hi))
+    if not sel:
+        raise ValueError("octex: a device holds no copies (fewer copies or parts than devices)")
+    return np.array(sel, np.int64)
+
+
 class Index:
     """The arrays of an index directory as the loader places them (one device, replicate)."""
 
-    def __init__(self, path, list_limit=0, copies_limit=0, queries=None, read=32):
+    def __init__(self, path, list_limit=0, copies_limit=0, queries=None, read=32, parts=0, copies_per_part=0):
         """path: an index directory, or a live octex_amd.Index whose arrays are copied to the host.  For a
         live index, `queries` (with the search's `read`) limits the lists copied to the rows these
-        queries' probes reach; the other rows read as zeros (an index too large for host memory)."""
+        queries' probes reach; the other rows read as zeros (an index too large for host memory).
+        parts / copies_per_part / copies_limit select copies as the reference's loader does
+        (load.cu:252-263)."""
         if not isinstance(path, (str, bytes, os.PathLike)):
             self._from_live(path, queries, read)
             return
@@ -217,22 +236,23 @@ class Index:
         self.table_len = int(meta.get("table_len", 0))
         self.spacings = [float(v) for v in meta["spacings"]]
         L = len(self.spacings)
-        C = min(all_copies, copies_limit) if copies_limit > 0 else all_copies
+        sel = copy_selection(all_copies, parts, copies_per_part, copies_limit)
+        C = len(sel)
         self.copies = C
         w = 8 * self.blocks
         ll = min(list_limit, list_len) if list_limit > 0 else list_len
-        lists = np.asarray(load("lists")[:C])
+        lists = np.asarray(load("lists")[sel])
         if ll != list_len:  # load.cu:361-379
             rows = lists.shape[1] // list_len
             lists = np.ascontiguousarray(lists[:, : rows * list_len].reshape(C, rows, list_len)[:, :, :ll].reshape(C, -1))
         self.list_len = ll
         self.lists = _c(lists, np.int32)
-        self.keys = _c(load("keys")[:C], np.int64)
-        self.offsets = _c(load("offsets")[:C], np.int32)
-        self.base = _c(load("base")[:C], np.int32)
-        proj = np.asarray(load("proj")[:C], np.float32)  # [C, D, w]
+        self.keys = _c(load("keys")[sel], np.int64)
+        self.offsets = _c(load("offsets")[sel], np.int32)
+        self.base = _c(load("base")[sel], np.int32)
+        proj = np.asarray(load("proj")[sel], np.float32)  # [C, D, w]
         self.ucat = f2h(np.ascontiguousarray(proj.transpose(1, 0, 2)).reshape(self.dim, C * w))  # load.cu:385-393
-        self.shift = f2h(np.asarray(load("shift")[:C], np.float32).reshape(-1))
+        self.shift = f2h(np.asarray(load("shift")[sel], np.float32).reshape(-1))
         self.inv_f = np.array([np.float32(1.0 / f) for f in self.spacings], np.float32)  # load.cu:397-399: the JSON double
         self.mean = _c(load("mean"), np.float32)
         self.basis = _c(load("sketch_basis"), np.float32)
@@ -242,6 +262,38 @@ class Index:
         self.table = _c(load("table"), np.int32) if self.table_len > 0 else None
         assert self.keys.shape[1] == L and proj.shape[2] == w, "octex: bad shapes"
         self._struct(L)
+
+    @classmethod
+    def from_arrays(cls, *, inv_f, offsets, keys, base, list_len, blocks, lists=None, n=0, dim=8):
+        """An index of the probe's arrays only (keys [C, L, mmax], offsets [C, L, 2^logT + 1], base [C, L],
+        inv_f [L]), for hand-built cell tables such as the reference's probe test (test_search.cu:86-170);
+        the other arrays are empty placeholders."""
+        self = cls.__new__(cls)
+        self.keys = _c(keys, np.int64)
+        self.offsets = _c(offsets, np.int32)
+        self.base = _c(base, np.int32)
+        self.inv_f = _c(inv_f, np.float32)
+        C, L = self.keys.shape[:2]
+        T1 = self.offsets.shape[2]
+        assert self.offsets.shape[:2] == (C, L) and self.base.shape == (C, L) and self.inv_f.shape == (L,)
+        assert T1 >= 2 and (T1 - 1) & (T1 - 2) == 0, "offsets rows hold 2^logT + 1 entries"
+        self.n, self.dim, self.copies, self.blocks, self.list_len = n, dim, C, blocks, list_len
+        self.log_buckets = (T1 - 1).bit_length() - 1
+        self.sketch_width, self.table_len = 0, 0
+        self.spacings = [float(1.0 / v) for v in self.inv_f]
+        self.lists = _c(lists if lists is not None else np.zeros((C, 1)), np.int32)
+        w = 8 * blocks
+        self.ucat = np.zeros((dim, C * w), np.uint16)
+        self.shift = np.zeros(C * w, np.uint16)
+        self.mean = np.zeros(dim, np.float32)
+        self.basis = np.zeros((dim, 1), np.float32)
+        self.scale = np.zeros(1, np.float32)
+        self.sketch = np.zeros((1, 1), np.int8)
+        self.vectors = np.zeros((1, dim), np.uint16)
+        self.table = None
+        self.meta = {}
+        self._struct(L)
+        return self
 
     def _from_live(self, live, queries=None, read=32):
         """The arrays of a loaded or built octex_amd index, copied to the host (the same index the GPU searches)."""

@@ -198,6 +198,26 @@ def test_device_tensors(octex, small_index):
     assert np.array_equal(I1, I2.cpu().numpy()) and np.array_equal(D1, D2.cpu().numpy())
 
 
+def test_search_on_a_side_stream(octex, small_index):
+    """Device queries written on a torch side stream (after long work on it) are searched on that stream: the
+    search waits for them, and its results are ready on that stream, as a serial host search's."""
+    index = octex.load(small_index["path"])
+    Q = small_index["Q"]
+    D1, I1 = index.search(Q, k=10, **PARAMS)
+    side = torch.cuda.Stream()  # default priority
+    with torch.cuda.stream(side):
+        q = torch.zeros(Q.shape, dtype=torch.float32, device="cuda")
+        src = torch.from_numpy(Q).cuda()
+        a = torch.randn((4096, 4096), device="cuda")
+        for _ in range(12):  # keeps the side stream busy before the queries are written
+            a = torch.mm(a, a) * 1e-3
+        q.copy_(src + a[:1, :1] * 0)
+        D2, I2 = index.search(q, k=10, **PARAMS)
+        D2, I2 = D2.cpu().numpy(), I2.cpu().numpy()
+    assert np.array_equal(I1, I2) and np.array_equal(D1, D2)
+    torch.cuda.synchronize()
+
+
 def test_sketch_rank_matches_oracle(octex, small_index):
     index = octex.load(small_index["path"])
     oix = O.Index(small_index["path"])

@@ -8,7 +8,7 @@ import ctypes as ct
 import numpy as np
 import pytest
 from conftest import clustered
-from test_oracle import check_e8, e8_inputs
+from test_oracle import check_e8, check_probe, e8_inputs, probe_construction
 
 from oracle import oracle as O
 
@@ -171,6 +171,23 @@ def run_probe(L, ix, dix, Y, lr):
            P(dix["inv_f"]), P(dix["offsets"]), i64(ix.offsets.shape[2]), P(dix["keys"]), i64(ix.keys.shape[2]),
            P(dix["base"]), i32(ix.list_len), i32(lr), i32(ix.log_buckets), P(seg), None)
     return seg
+
+
+@pytest.mark.parametrize("case", [
+    dict(),  # the reference's probe test shape (test_search.cu:86-170)
+    dict(m=60, C=5, spacing=(0.5, 1.0, 2.0, 4.0, 8.0), logT=3, l=16, lr=9, seed=3, absent=(5, 6, 17)),
+    dict(m=300, C=7, spacing=(1.0, 2.0, 4.0), b=2, logT=5, l=8, lr=8, seed=4, absent=tuple(range(0, 300, 13))),
+])
+def test_probe_construction_matches_reference(L, case):
+    """The probe over hand-built cell tables: exactly (row * l, lr) at the finest level holding each query's
+    cell, (0, 0) when none does; the oracle gives the same segments."""
+    arrays, Y, want = probe_construction(**case)
+    pix = O.Index.from_arrays(**arrays)
+    pdix = dict(inv_f=dev(pix.inv_f), offsets=dev(pix.offsets), keys=dev(pix.keys), base=dev(pix.base))
+    lr = int(want[:, :, 1].max())
+    seg = host(run_probe(L, pix, pdix, Y, lr))
+    check_probe(seg, want)
+    check_probe(O.probe(pix, Y, read=lr), want)
 
 
 def test_probe_matches_oracle(L, ix, dix, small_index):

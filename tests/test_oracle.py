@@ -248,16 +248,190 @@ def test_gather_is_the_union(small_index):
     assert set(cand2.tolist()) == rows
 
 
-def test_probe_construction(small_index):
-    """A query equal to a database row's own projection finds a cell in every copy (test_search.cu:86-170 shape):
-    seg = (row * l, lr) with the row's id in the segment at the coarsest level at the latest."""
-    ix = O.Index(small_index["path"])
-    X = small_index["X"][:20]
-    qc, qh = O.center(X, ix.mean)
-    Y, _ = O.project(qh, ix.ucat, ix.shift)
-    seg = O.probe(ix, Y, read=ix.list_len)
-    assert (seg[:, :, 1] == ix.list_len).mean() > 0.9
-    assert ((seg[:, :, 0] % ix.list_len) == 0).all()
+def probe_construction(m=7, C=3, spacing=(1.0, 4.0), b=4, logT=4, l=5, lr=3, seed=7, absent=()):
+    """The reference's probe test (test_search.cu:86-170): projections y [m, C, 8b] ~ N(0, 2) rounded to fp16;
+    per copy and level a cell table holding the cell of every second query at the finest level (query q even)
+    and of all queries at every coarser level, keys in (bucket, hash) order with their CSR offsets and the
+    levels' first rows.  Queries listed in `absent` get no cell at any level.  Returns the probe's arrays, the
+    fp16 projections and the segments it must produce: (row * l, lr) at the finest level holding the query's
+    cell, (0, 0) when no level does (the absent queries' projections lie far from every other query's, so no
+    shared coarse cell lists them)."""
+    g = np.random.default_rng(seed)
+    L, w, T = len(spacing), 8 * b, 1 << logT
+    y = g.normal(0.0, 2.0, (m, C, w))
+    y[list(absent)] = y[list(absent)] * 40 + 300  # far from every other query's cell at every level
+    y = O.h2f(O.f2h(y.reshape(m * C, w).astype(np.float32)))
+    inv = np.array([np.float32(1.0) / np.float32(f) for f in spacing], np.float32)  # 1.f / spacing[j]
+    h = np.stack([O.e8_batch(y, b, float(inv[j]))[1] for j in range(L)], 1).reshape(m, C, L)
+    keys = np.zeros((C, L, m), np.int64)
+    off = np.zeros((C, L, T + 1), np.int32)
+    base = np.zeros((C, L), np.int32)
+    row = {}
+    rows = 0
+    for c in range(C):
+        for j in range(L):
+            base[c, j] = rows
+            cells = sorted({(int(h[q, c, j]) & (T - 1), int(h[q, c, j])) for q in range(m)
+                            if q not in absent and (j > 0 or q % 2 == 0)})
+            for p, (_, hh) in enumerate(cells):
+                keys[c, j, p] = hh
+                row[c, j, hh] = rows + p
+            cnt = np.bincount([bk for bk, _ in cells], minlength=T)
+            off[c, j, 1:] = np.cumsum(cnt)
+            rows += len(cells)
+    want = np.zeros((m, C, 2), np.int32)
+    for q in range(m):
+        for c in range(C):
+            if q in absent:
+                continue
+            j = 0 if q % 2 == 0 else 1
+            want[q, c] = (row[c, j, int(h[q, c, j])] * l, lr)
+    arrays = dict(inv_f=inv, offsets=off, keys=keys, base=base, list_len=l, blocks=b)
+    return arrays, O.f2h(y).reshape(m, C * w), want
+
+
+def check_probe(seg, want):
+    assert np.array_equal(seg, want), f"{(seg != want).any(-1).sum()} of {want.shape[0] * want.shape[1]} segments differ"
+
+
+def test_probe_construction_reference():
+    """The reference test's exact shape: m 7, C 3, L 2 (spacings 1 and 4), b 4, 16 buckets, l 5, lr 3."""
+    arrays, Y, want = probe_construction()
+    seg = O.probe(O.Index.from_arrays(**arrays), Y, read=3)
+    check_probe(seg, want)
+
+
+def test_probe_construction_levels_and_misses():
+    """More queries and copies, five levels, eight buckets (several keys per bucket), queries with no cell."""
+    arrays, Y, want = probe_construction(m=60, C=5, spacing=(0.5, 1.0, 2.0, 4.0, 8.0), logT=3, l=16, lr=9,
+                                         seed=3, absent=(5, 6, 17))
+    assert (want[[5, 6, 17], :, 1] == 0).all() and (want[:, :, 1] > 0).sum() == 57 * 5
+    check_probe(O.probe(O.Index.from_arrays(**arrays), Y, read=9), want)
+
+
+def test_probe_construction_catches_plausible_mistakes():
+    """Planted mistakes on the CPU: a probe walking the levels coarse to fine (the oracle over the same tables
+    with the level order reversed), a first row off by one, and segments of the wrong length all fail."""
+    arrays, Y, want = probe_construction(m=40, C=4, spacing=(1.0, 2.0, 4.0), seed=11)
+    rev = dict(arrays, inv_f=arrays["inv_f"][::-1], offsets=arrays["offsets"][:, ::-1], keys=arrays["keys"][:, ::-1],
+               base=arrays["base"][:, ::-1])
+    with pytest.raises(AssertionError):
+        check_probe(O.probe(O.Index.from_arrays(**rev), Y, read=3), want)
+    with pytest.raises(AssertionError):
+        check_probe(O.probe(O.Index.from_arrays(**dict(arrays, base=arrays["base"] + 1)), Y, read=3), want)
+    with pytest.raises(AssertionError):
+        check_probe(O.probe(O.Index.from_arrays(**arrays), Y, read=4), want)
+
+
+# ---------------------------------------------------------------- query preparation against fp64 numpy
+
+
+def check_center(q, mu, qc, qh):
+    """qc = q - mu in fp32 (one IEEE rounding), qh = fp16(qc) rounded to nearest even (search_kernels.cuh:57-69)."""
+    assert np.array_equal(qc, q - mu[None, :])
+    assert np.array_equal(qh, qc.astype(np.float16).view(np.uint16))
+
+
+def test_center_matches_numpy():
+    g = np.random.default_rng(21)
+    q = (g.standard_normal((50, 96)) * 3).astype(np.float32)
+    mu = g.standard_normal(96).astype(np.float32)
+    q[0, :8] = mu[:8] + np.float32(2.0**-20)  # cancellation: tiny centred values, fp16 subnormals
+    check_center(q, mu, *O.center(q, mu))
+    qc, qh = O.center(q, mu)
+    with pytest.raises(AssertionError):  # not centred before the fp16 rounding
+        check_center(q, mu, qc, q.astype(np.float16).view(np.uint16))
+    with pytest.raises(AssertionError):  # rounded toward zero instead of to nearest
+        check_center(q, mu, qc, (qc.view(np.uint32) >> 13 << 13).view(np.float32).astype(np.float16).view(np.uint16))
+
+
+def project_fp64(qh, ucat, shift):
+    """qh @ ucat + shift of fp16 operands in fp64: every product is exact, the sum of at most a few thousand
+    terms is within 1e-13 relative of the exact one."""
+    return O.h2f(qh).astype(np.float64) @ O.h2f(ucat).astype(np.float64) + O.h2f(shift).astype(np.float64)[None, :]
+
+
+def check_project(qh, ucat, shift, Y, Yd):
+    """Yd equals the fp64 product plus shift (search.cu:305-320: Y = qh ucat + shift, fp16 operands), and Y is
+    Yd rounded once to fp16 (numpy's float64 -> float16 rounds directly)."""
+    ref = project_fp64(qh, ucat, shift)
+    mag = np.abs(O.h2f(qh).astype(np.float64)) @ np.abs(O.h2f(ucat).astype(np.float64)) + np.abs(O.h2f(shift))
+    assert (np.abs(Yd - ref) <= 1e-13 * mag + 1e-300).all()
+    assert np.array_equal(Y, Yd.astype(np.float16).view(np.uint16))
+
+
+@pytest.mark.parametrize("m,D,wdt", [(40, 96, 256), (16, 128, 64), (9, 960, 32), (20, 32, 32)])
+def test_project_matches_numpy(m, D, wdt):
+    g = np.random.default_rng(m * D)
+    qh = O.f2h(g.standard_normal((m, D)).astype(np.float32))
+    ucat = O.f2h((g.standard_normal((D, wdt)) / np.sqrt(D)).astype(np.float32))
+    shift = O.f2h(g.uniform(0, 2, wdt).astype(np.float32))
+    Y, Yd = O.project(qh, ucat, shift)
+    check_project(qh, ucat, shift, Y, Yd)
+
+
+def test_project_rounds_once_at_fp16_ties():
+    """Sums on and just beside an fp16 tie (1 + 2^-11 is halfway between 1 and 1 + 2^-10): 1 + 2^-11 + 2^-30
+    must round up, which a detour through fp32 (where 2^-30 vanishes, leaving the tie) would round to 1."""
+    qh = O.f2h(np.array([[1.0, 2.0**-11, 2.0**-15, 0.0], [1.0, 2.0**-11, 0.0, 0.0], [1.0, 2.0**-11, -(2.0**-15), 0.0]],
+                        np.float32))
+    ucat = O.f2h(np.array([[1.0, 0.0], [1.0, 0.0], [2.0**-15, 0.0], [0.0, 1.0]], np.float32))
+    shift = O.f2h(np.zeros(2, np.float32))
+    Y, Yd = O.project(qh, ucat, shift)
+    assert Yd[0, 0] == 1 + 2.0**-11 + 2.0**-30
+    check_project(qh, ucat, shift, Y, Yd)
+    assert list(Y[:, 0]) == list(O.f2h(np.array([1 + 2.0**-10, 1.0, 1.0], np.float32)))
+
+
+def test_project_catches_plausible_mistakes():
+    g = np.random.default_rng(5)
+    D = wdt = 64
+    qh = O.f2h(g.standard_normal((12, D)).astype(np.float32))
+    ucat = O.f2h((g.standard_normal((D, wdt)) / 8).astype(np.float32))
+    shift = O.f2h(g.uniform(0, 2, wdt).astype(np.float32))
+    Y, Yd = O.project(qh, ucat, shift)
+    with pytest.raises(AssertionError):  # transposed projection
+        Yt, Ydt = O.project(qh, np.ascontiguousarray(ucat.T), shift)
+        check_project(qh, ucat, shift, Yt, Ydt)
+    with pytest.raises(AssertionError):  # shift dropped
+        Y0, Yd0 = O.project(qh, ucat, np.zeros_like(shift))
+        check_project(qh, ucat, shift, Y0, Yd0)
+    with pytest.raises(AssertionError):  # fp32 accumulation rounded twice
+        Yf = (O.h2f(qh) @ O.h2f(ucat) + O.h2f(shift)).astype(np.float16).view(np.uint16)
+        check_project(qh, ucat, shift, Yf, (O.h2f(qh) @ O.h2f(ucat) + O.h2f(shift)).astype(np.float64))
+
+
+def check_sketch_query(qc, basis, qs):
+    """qs = qc @ basis as the fp32 rounding of the fp64 sum: within half an fp32 ulp plus the fp64 sum's own error
+    (search.cu:323-341 computes it in TF32, which no MI355X arithmetic reproduces; full fp32 is the pin)."""
+    ref = qc.astype(np.float64) @ basis.astype(np.float64)
+    mag = np.abs(qc.astype(np.float64)) @ np.abs(basis.astype(np.float64))
+    half_ulp = np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64) / 2
+    assert (np.abs(qs.astype(np.float64) - ref) <= half_ulp + 1e-13 * mag).all()
+
+
+@pytest.mark.parametrize("m,D,S", [(30, 96, 64), (8, 960, 128), (5, 128, 512)])
+def test_sketch_query_matches_numpy(m, D, S):
+    g = np.random.default_rng(D + S)
+    qc = g.standard_normal((m, D)).astype(np.float32)
+    basis = (g.standard_normal((D, S)) / np.sqrt(D)).astype(np.float32)
+    check_sketch_query(qc, basis, O.sketch_query(qc, basis))
+
+
+def test_sketch_query_catches_plausible_mistakes():
+    g = np.random.default_rng(6)
+    D = S = 64
+    qc = g.standard_normal((20, D)).astype(np.float32)
+    basis = g.standard_normal((D, S)).astype(np.float32)
+    with pytest.raises(AssertionError):  # transposed basis
+        check_sketch_query(qc, basis, O.sketch_query(qc, np.ascontiguousarray(basis.T)))
+    with pytest.raises(AssertionError):  # the last coordinate dropped
+        check_sketch_query(qc, basis, O.sketch_query(qc[:, :-1], basis[:-1]))
+    with pytest.raises(AssertionError):  # a sequential fp32 sum (error grows with D)
+        acc = np.zeros((20, S), np.float32)
+        for d in range(D):
+            acc = (acc + qc[:, d : d + 1] * basis[d][None, :]).astype(np.float32)
+        check_sketch_query(qc, basis, acc)
 
 
 def test_search_recall(small_index):
