@@ -137,6 +137,18 @@ def _torch_operand(t, origin, want, name, stream):
     return Operand(t, origin, stream)
 
 
+def shape_of(a):
+    """The shape of an array of any supported framework (a DLPack-only array through a torch view)."""
+    if hasattr(a, "shape"):
+        return tuple(int(v) for v in a.shape)
+    cai = getattr(a, "__cuda_array_interface__", None)
+    if cai is not None:
+        return tuple(int(v) for v in cai["shape"])
+    import torch
+
+    return tuple(int(v) for v in torch.from_dlpack(a).shape)
+
+
 def write_into(dst, src):
     """Copy the result src (numpy or torch) into the caller's array dst (numpy, torch or foreign), converting
     the element type as numpy's / torch's assignment does."""

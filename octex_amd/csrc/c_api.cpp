@@ -404,32 +404,12 @@ extern "C" cuvsError_t octexIndexCopyPlanBuffer(cuvsOctexIndex_t index, const ch
       OCTEX_EXPECTS(!ix.plans.empty(), "octex: no search ran on this index yet");
       pl = ix.plans.begin()->second;
     }
-    std::string n(name != nullptr ? name : "");
-    octex::detail::dbuf const* b = nullptr;
-    if (n == "queries") b = &pl->qbuf;
-    else if (n == "qc") b = &pl->qc;
-    else if (n == "qh") b = &pl->qh;
-    else if (n == "Y") b = &pl->Y;
-    else if (n == "qs") b = &pl->qs;
-    else if (n == "seg") b = &pl->seg;
-    else if (n == "cand") b = &pl->cand;
-    else if (n == "dist") b = &pl->dist;
-    else if (n == "nin") b = &pl->nin;
-    else if (n == "si") b = &pl->si;
-    else if (n == "sd") b = &pl->sd;
-    else if (n == "done") b = &pl->done;
-    else if (n == "seg2") b = &pl->seg2;
-    else if (n == "cand2") b = &pl->cand2;
-    else if (n == "dist2") b = &pl->dist2;
-    else if (n == "n2") b = &pl->n2;
-    else if (n == "bi") b = &pl->bi;
-    else if (n == "bd") b = &pl->bd;
-    else octex::detail::fail("octex: unknown plan buffer %s", n.c_str());
-    if (size != nullptr) *size = static_cast<int64_t>(b->size);
-    if (dst != nullptr && bytes > 0) {
+    auto [src, sz] = octex::detail::named_buffer(ix, pl->shape, pl->buf, std::string(name != nullptr ? name : ""));
+    if (size != nullptr) *size = static_cast<int64_t>(sz);
+    if (dst != nullptr && bytes > 0 && src != nullptr) {
       OCTEX_HIP(hipSetDevice(ix.device));
       OCTEX_HIP(hipStreamSynchronize(ix.stream));
-      OCTEX_HIP(hipMemcpy(dst, b->ptr, std::min<size_t>(b->size, static_cast<size_t>(bytes)), hipMemcpyDefault));
+      OCTEX_HIP(hipMemcpy(dst, src, std::min<size_t>(sz, static_cast<size_t>(bytes)), hipMemcpyDefault));
     }
   });
 }
@@ -441,7 +421,8 @@ extern "C" cuvsError_t octexIndexPlanInfo(cuvsOctexIndex_t index, int32_t* info)
     std::lock_guard<std::mutex> lock(ix.mu);
     OCTEX_EXPECTS(!ix.plans.empty(), "octex: no search ran on this index yet");
     auto const& pl = *ix.plans.begin()->second;
-    int32_t v[] = {pl.m, pl.k, pl.KO, pl.lr, pl.W, pl.W2, pl.R1, pl.R2, pl.FR, pl.graph != nullptr ? 1 : 0};
+    auto const& sh = pl.shape;
+    int32_t v[] = {sh.m, sh.k, sh.KO, sh.lr, sh.W, sh.W2, sh.R1, sh.R2, sh.FR, pl.graph != nullptr ? 1 : 0};
     std::memcpy(info, v, sizeof(v));
   });
 }
@@ -490,10 +471,12 @@ extern "C" cuvsError_t octexIndexProfileBatch(cuvsOctexIndex_t index, cuvsOctexS
     octex::detail::search_impl(r, p, idx, qh, nq, ix.dim, nb.data(), nd.data(), k, true, false);
     std::lock_guard<std::mutex> run(ix.stream_mu);
     std::shared_ptr<octex::detail::plan> pl;
-    {
+    {  // the plan of this call's parameters: another thread's search may have replaced it since
       std::lock_guard<std::mutex> lock(ix.mu);
-      OCTEX_EXPECTS(!ix.plans.empty(), "octex: the profiled plan was evicted by another search");
-      pl = ix.plans.begin()->second;
+      const int m = static_cast<int>(std::min<int64_t>(std::max(p.batch, 1), nq));
+      auto it     = ix.plans.find(octex::detail::plan_key(p, m, static_cast<int>(k)));
+      OCTEX_EXPECTS(it != ix.plans.end(), "octex: the profiled plan was evicted by another search");
+      pl = it->second;
     }
     OCTEX_HIP(hipSetDevice(ix.device));
     std::vector<std::string> nm;

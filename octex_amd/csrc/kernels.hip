@@ -555,13 +555,85 @@ __device__ int collect_candidates(const int2* __restrict__ seg, int nseg, const 
 }
 
 /**
+ * Slot of this lane's item in a list appended to by several wavefronts: one atomic per wavefront on
+ * *count, the lanes with pred set numbered in lane order (-1 for the others).  Every lane of the
+ * wavefront calls it.
+ */
+__device__ __forceinline__ int wave_append(bool pred, int* count)
+{
+  const int lane                = threadIdx.x & 63;
+  const unsigned long long mask = __ballot(pred);
+  if (mask == 0) return -1;
+  const int leader = __ffsll(static_cast<long long>(mask)) - 1;
+  int base         = 0;
+  if (lane == leader) base = atomicAdd(count, __popcll(mask));
+  base = __shfl(base, leader);
+  return pred ? base + __popcll(mask & ((1ULL << lane) - 1ULL)) : -1;
+}
+
+/**
+ * collect_candidates without the load balance (the reference's ablation, gather_warp_kernel of
+ * search_kernels.cuh:687-760): wavefront w reads the segments w, w + wavefronts, ... whole, one entry per
+ * lane, so a query's longest segments set its time.  The same hash set, the same distinct ids and the same
+ * add(slot, id, h) calls (slot numbers in another order).
+ */
+template <bool kRows, typename Add>
+__device__ int collect_segments_whole(const int2* __restrict__ seg, int nseg, const long long* __restrict__ list_ptr,
+                                      const int* __restrict__ table, int table_len, int64_t N, int logW, int cap,
+                                      int* ht, collect_state& cs, Add const& add)
+{
+  const int q = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, nw = blockDim.x >> 6;
+  if (tid == 0) {
+    cs.cnt  = 0;
+    cs.ulen = 0;
+  }
+  __syncthreads();
+  int part = 0;
+  for (int c = tid; c < nseg; c += blockDim.x)
+    part += max(seg[static_cast<int64_t>(q) * nseg + c].y, 0);
+  if (part > 0) atomicAdd(&cs.ulen, part);
+  __syncthreads();
+  const int HT = 1 << hash_log_dev(cs.ulen, logW);
+  for (int i = tid; i < HT; i += blockDim.x)
+    ht[i] = -1;
+  __syncthreads();
+  for (int c = wid; c < nseg; c += nw) {
+    const int2 sl = seg[static_cast<int64_t>(q) * nseg + c];
+    const int* src = kRows ? table + static_cast<int64_t>(sl.x) * table_len
+                           : reinterpret_cast<const int*>(list_ptr[c]) + sl.x;
+    for (int e0 = 0; e0 < sl.y; e0 += 64) {  // uniform over the wavefront
+      const int e = e0 + lane;
+      const int v = e < sl.y ? src[e] : -1;
+      bool fresh  = false;
+      unsigned h  = 0;
+      if (v >= 0 && v < N) {
+        h = (static_cast<unsigned>(v) * kIdHash) & (HT - 1);
+        for (int p = 0; p < HT; p++) {
+          const int prev = atomicCAS(&ht[h], -1, v);
+          if (prev == -1) {
+            fresh = true;
+            break;
+          }
+          if (prev == v) break;
+          h = (h + 1) & (HT - 1);
+        }
+      }
+      const int slot = wave_append(fresh, &cs.cnt);
+      if (fresh && slot < cap) add(slot, v, h);
+    }
+  }
+  __syncthreads();
+  return min(cs.cnt, cap);
+}
+
+/**
  * Distinct ids of all segments of a query with their sketch scores (collect_candidates, then
  * sketch_scores with LR = the reference's lanes per candidate for this S), written to the query's rows of
  * cand / dist and their count to nout.  The candidates are kept as hash-set slot numbers: 16-bit in LDS
  * (kLdsSlots), or, when they do not fit in LDS beside a large hash set, in the query's own row of cand,
  * where candidate j's slot is read and then overwritten by its id by the one lane group that scores it.
  */
-template <bool kRows, int LR, bool kLdsSlots>
+template <bool kRows, int LR, bool kLdsSlots, bool kBalanced>
 __global__ __launch_bounds__(kGatherThreads) void gather_kernel(
   const int2* __restrict__ seg, int nseg, const long long* __restrict__ list_ptr,
   const int* __restrict__ table, int table_len, int64_t N, const signed char* __restrict__ code,
@@ -580,13 +652,17 @@ __global__ __launch_bounds__(kGatherThreads) void gather_kernel(
   float* drow = dist + static_cast<int64_t>(q) * W;
   for (int i = threadIdx.x; i < S; i += blockDim.x)
     sq[i] = make_float2(scale[i], qs[static_cast<int64_t>(q) * S + i]);
-  const int n = collect_candidates<kRows>(seg, nseg, list_ptr, table, table_len, N, logW, cap, sp, pre, ht, cs,
-                                          [&](int slot, int, unsigned h) {
-                                            if constexpr (kLdsSlots)
-                                              cl[slot] = static_cast<unsigned short>(h);
-                                            else
-                                              crow[slot] = static_cast<int>(h);
-                                          });
+  auto keep_slot = [&](int slot, int, unsigned h) {
+    if constexpr (kLdsSlots)
+      cl[slot] = static_cast<unsigned short>(h);
+    else
+      crow[slot] = static_cast<int>(h);
+  };
+  int n = 0;
+  if constexpr (kBalanced)
+    n = collect_candidates<kRows>(seg, nseg, list_ptr, table, table_len, N, logW, cap, sp, pre, ht, cs, keep_slot);
+  else
+    n = collect_segments_whole<kRows>(seg, nseg, list_ptr, table, table_len, N, logW, cap, ht, cs, keep_slot);
   sketch_scores<LR>(
     n,
     [&](int j) {
@@ -605,22 +681,6 @@ __global__ __launch_bounds__(kGatherThreads) void gather_kernel(
 
 // ------------------------------------------------------------------ selection and merges
 
-/**
- * Slot of this lane's item in a list appended to by several wavefronts: one atomic per wavefront on
- * *count, the lanes with pred set numbered in lane order (-1 for the others).  Every lane of the
- * wavefront calls it.
- */
-__device__ __forceinline__ int wave_append(bool pred, int* count)
-{
-  const int lane                = threadIdx.x & 63;
-  const unsigned long long mask = __ballot(pred);
-  if (mask == 0) return -1;
-  const int leader = __ffsll(static_cast<long long>(mask)) - 1;
-  int base         = 0;
-  if (lane == leader) base = atomicAdd(count, __popcll(mask));
-  base = __shfl(base, leader);
-  return pred ? base + __popcll(mask & ((1ULL << lane) - 1ULL)) : -1;
-}
 
 constexpr int kBins     = 2048;  // histogram of the two-pass selection
 constexpr int kTieCap   = 256;   // keys of the threshold bin ranked directly
@@ -900,73 +960,167 @@ __device__ __forceinline__ void exact_distances(const int* sid, int ns, const __
     exact_distances_rows<LX, false>(sid, ns, vectors, D, sq, sd);
 }
 
-/** Ascending bitonic sort of P (a power of two) 64-bit keys in LDS. */
-__device__ void bitonic_sort(uint64_t* key, int P)
-{
-  for (int size = 2; size <= P; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = threadIdx.x; i < P; i += blockDim.x) {
-        int j = i ^ stride;
-        if (j > i) {
-          bool up    = (i & size) == 0;
-          uint64_t a = key[i], b = key[j];
-          if ((a > b) == up) {
-            key[i] = b;
-            key[j] = a;
-          }
-        }
-      }
-      __syncthreads();
-    }
-  }
-}
+// ------------------------------------------------------------------ kept-list merges (search_kernels.cuh:345-508)
 
+/** A (distance, id) pair as one 64-bit key ordered by (distance bits, id): distances are non-negative. */
 __device__ __forceinline__ uint64_t dist_key(float d, long long id)
 {
   return (static_cast<uint64_t>(__float_as_uint(d)) << 32) | static_cast<unsigned>(id);
 }
 
-/** The kept list (unless fresh) and ns new (distance, id) pairs as P keys (search_kernels.cuh:372-392). */
-__device__ void load_keys(uint64_t* key, int P, const long long* pb, const float* pd, int KO,
-                          bool fresh, const int* sid, const float* sdv, int ns)
+/**
+ * One compare-exchange step (size, stride) of a bitonic sorting network over keys held in registers: thread t
+ * holds elements base + C t + j, j < C, of a sequence of C blockDim keys (base a multiple of it).  Each element
+ * keeps the smaller or the larger of itself and its partner (index ^ stride), as its position in the
+ * ascending / descending run of length `size` says.  Partners in the same thread are compared in registers,
+ * partners in the same wavefront are exchanged by lane shuffles, partners in other wavefronts through LDS (xch,
+ * C blockDim keys) between two barriers.
+ */
+template <int C>
+__device__ __forceinline__ void bitonic_step(uint64_t (&k)[C], uint64_t* xch, int64_t base, int64_t size, int stride)
 {
-  for (int i = threadIdx.x; i < P; i += blockDim.x) {
-    uint64_t k = kEmpty;
-    if (i < KO) {
-      if (!fresh && pb[i] >= 0) k = dist_key(pd[i], pb[i]);
-    } else if (i - KO < ns) {
-      k = dist_key(sdv[i - KO], sid[i - KO]);
+  const int t = threadIdx.x;
+  auto keep_min = [&](int j) {
+    const int64_t i = base + C * t + j;
+    return ((i & stride) == 0) == ((i & size) == 0);
+  };
+  if (stride < C) {
+#pragma unroll
+    for (int j = 0; j < C; j++) {
+      const int jp = j ^ stride;
+      if (jp > j) {
+        const uint64_t a = k[j], b = k[jp];
+        const bool lo   = keep_min(j);
+        k[j]            = lo ? min(a, b) : max(a, b);
+        k[jp]           = lo ? max(a, b) : min(a, b);
+      }
     }
-    key[i] = k;
+  } else if (stride < 64 * C) {
+#pragma unroll
+    for (int j = 0; j < C; j++) {
+      const uint64_t p = __shfl_xor(k[j], stride / C);
+      k[j]             = keep_min(j) ? min(k[j], p) : max(k[j], p);
+    }
+  } else {
+    __syncthreads();  // the previous exchange has been read
+#pragma unroll
+    for (int j = 0; j < C; j++)
+      xch[C * t + j] = k[j];
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < C; j++) {
+      const uint64_t p = xch[(C * t + j) ^ stride];
+      k[j]             = keep_min(j) ? min(k[j], p) : max(k[j], p);
+    }
   }
-  __syncthreads();
 }
 
-/**
- * The first KO distinct sorted keys to (pb, pd), padded with (-1, +inf) (search_kernels.cuh:396-415):
- * wavefront 0 walks the keys 64 at a time and places every distinct key by a ballot prefix count.
- */
-__device__ void store_keys(const uint64_t* key, int P, int KO, long long* pb, float* pd)
+/** Ascending sort of the C blockDim keys held in registers (thread t: keys C t .. C t + C - 1 of the result). */
+template <int C>
+__device__ __forceinline__ void block_sort(uint64_t (&k)[C], uint64_t* xch)
 {
-  if ((threadIdx.x >> 6) != 0) return;
-  const int lane = threadIdx.x & 63;
-  int at         = 0;
-  for (int i0 = 0; i0 < P && at < KO; i0 += 64) {
-    const int i      = i0 + lane;
-    const uint64_t k = i < P ? key[i] : kEmpty;
-    const bool keep  = k != kEmpty && (i == 0 || key[i - 1] != k);
-    const unsigned long long mask = __ballot(keep);
-    const int o = at + __popcll(mask & ((1ULL << lane) - 1ULL));
-    if (keep && o < KO) {
-      pb[o] = static_cast<long long>(static_cast<unsigned>(k & 0xffffffffULL));
-      pd[o] = __uint_as_float(static_cast<unsigned>(k >> 32));
+  const int total = C * static_cast<int>(blockDim.x);
+  for (int size = 2; size <= total; size <<= 1)
+    for (int stride = size >> 1; stride > 0; stride >>= 1)
+      bitonic_step<C>(k, xch, 0, size, stride);
+}
+
+/** Exclusive prefix sum of one int per thread over the workgroup (<= 16 wavefronts); *total gets the sum. */
+__device__ __forceinline__ int block_exclusive_sum(int v, int* wsum, int* total)
+{
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+  int incl = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int u = __shfl_up(incl, d);
+    if (lane >= d) incl += u;
+  }
+  if (lane == 63) wsum[wid] = incl;
+  __syncthreads();
+  int before = 0, all = 0;
+  for (int w = 0; w < nw; w++) {
+    before += w < wid ? wsum[w] : 0;
+    all += wsum[w];
+  }
+  *total = all;
+  __syncthreads();  // wsum may be reused by the caller
+  return before + incl - v;
+}
+
+/** LDS of a kept-list merge of up to KEYS keys (C blockDim for the largest C a kernel uses). */
+template <int KEYS>
+struct merge_lds {
+  uint64_t xch[KEYS];
+  int wsum[16];
+  uint64_t last[16];
+};
+
+/**
+ * The kept list merged with new keys (search_kernels.cuh:379-415): the keys of the kept list (pb, pd: KO entries,
+ * ignored when `fresh`, -1 entries empty) and the ns new (sdv[i], sid[i]) pairs, sorted together in registers,
+ * and the first KO distinct keys written back to (pb, pd), padded with (-1, +inf).  Thread t loads elements
+ * C t .. C t + C - 1 of the concatenation (kept first), so equal keys end next to each other after the sort; a
+ * key is kept when it differs from its predecessor, and its place is the number of kept keys before it (a
+ * workgroup prefix sum).  ns <= C blockDim - KO.  Every thread of the workgroup calls it.
+ */
+template <int C, int KEYS>
+__device__ void merge_keep(long long* pb, float* pd, int KO, bool fresh, const int* sid, const float* sdv, int ns,
+                           long long* ob, float* od, int KOout, merge_lds<KEYS>& sh)
+{
+  const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
+  uint64_t k[C];
+#pragma unroll
+  for (int j = 0; j < C; j++) {
+    const int i = C * t + j;
+    uint64_t v  = kEmpty;
+    if (i < KO) {
+      const long long id = (!fresh && pb != nullptr) ? pb[i] : -1;
+      if (id >= 0) v = dist_key(pd[i], id);
+    } else if (i - KO < ns) {
+      v = dist_key(sdv[i - KO], sid[i - KO]);
     }
-    at += __popcll(mask);
+    k[j] = v;
   }
-  for (int o = min(at, KO) + lane; o < KO; o += 64) {
-    pb[o] = -1;
-    pd[o] = INFINITY;
+  __syncthreads();  // the kept list is read before it is overwritten below
+  block_sort<C>(k, sh.xch);
+  // the predecessor of this thread's first key: the previous lane's last, or the previous wavefront's
+  uint64_t prev = __shfl_up(k[C - 1], 1);
+  if (lane == 63) sh.last[wid] = k[C - 1];
+  __syncthreads();
+  if (lane == 0) prev = wid > 0 ? sh.last[wid - 1] : kEmpty - 1;
+  bool keep[C];
+  int mine = 0;
+#pragma unroll
+  for (int j = 0; j < C; j++) {
+    keep[j] = k[j] != kEmpty && k[j] != (j == 0 ? prev : k[j - 1]);
+    mine += keep[j] ? 1 : 0;
   }
+  int total = 0;
+  int at    = block_exclusive_sum(mine, sh.wsum, &total);
+#pragma unroll
+  for (int j = 0; j < C; j++) {
+    if (keep[j] && at < KOout) {
+      ob[at] = static_cast<long long>(static_cast<unsigned>(k[j] & 0xffffffffULL));
+      od[at] = __uint_as_float(static_cast<unsigned>(k[j] >> 32));
+    }
+    at += keep[j] ? 1 : 0;
+  }
+  for (int o = min(total, KOout) + t; o < KOout; o += blockDim.x) {
+    ob[o] = -1;
+    od[o] = INFINITY;
+  }
+}
+
+/** f(std::integral_constant<int, C>) with C the keys per thread that hold `keys` keys over `threads` threads. */
+template <typename F>
+__device__ __forceinline__ void with_keys_per_thread(int keys, int threads, F&& f)
+{
+  if (keys <= threads)
+    f(std::integral_constant<int, 1>{});
+  else if (keys <= 2 * threads)
+    f(std::integral_constant<int, 2>{});
+  else
+    f(std::integral_constant<int, 4>{});
 }
 
 /**
@@ -981,24 +1135,24 @@ __global__ __launch_bounds__(kKeepThreads) void rerank_keep_kernel(
 {
   const int q = blockIdx.x;
   extern __shared__ float sq[];
-  __shared__ bin_select_lds sel;
+  __shared__ union {
+    bin_select_lds sel;
+    merge_lds<kMaxKeepSort> merge;
+  } u;
   __shared__ int sid[kMaxRerank];
   __shared__ float sd[kMaxRerank];
-  __shared__ uint64_t key[kMaxKeepSort];
   const int n = min(nin[q], W);
   for (int i = threadIdx.x; i < D; i += blockDim.x)
     sq[i] = Q[static_cast<int64_t>(q) * D + i];
   const int ns = select_by_bins(reinterpret_cast<const unsigned*>(dist + static_cast<int64_t>(q) * W),
-                                cand + static_cast<int64_t>(q) * W, n, R, sid, nullptr, sel);
+                                cand + static_cast<int64_t>(q) * W, n, R, sid, nullptr, u.sel);
   exact_distances<LX>(sid, ns, vectors, D, sq, sd);
   long long* pb = bi + static_cast<int64_t>(q) * KO;
   float* pd     = bd + static_cast<int64_t>(q) * KO;
-  int P         = 2;
-  while (P < KO + R)
-    P <<= 1;
-  load_keys(key, P, pb, pd, KO, fresh, sid, sd, ns);
-  bitonic_sort(key, P);
-  store_keys(key, P, KO, pb, pd);
+  with_keys_per_thread(KO + ns, blockDim.x, [&](auto c) {
+    constexpr int C = decltype(c)::value;
+    merge_keep<C>(pb, pd, KO, fresh, sid, sd, ns, pb, pd, KO, u.merge);
+  });
 }
 
 /** The KO sketch-nearest candidates merged into the kept list by sketch distance (:471-508). */
@@ -1009,27 +1163,66 @@ __global__ __launch_bounds__(512) void sketch_keep_kernel(const int* __restrict_
                                                           float* __restrict__ sd, bool fresh)
 {
   const int q = blockIdx.x;
-  __shared__ bin_select_lds sel;
+  __shared__ union {
+    bin_select_lds sel;
+    merge_lds<2 * kMaxSketchKO> merge;
+  } u;
   __shared__ int sid[kMaxSketchKO];
   __shared__ float sdv[kMaxSketchKO];
-  __shared__ uint64_t key[2 * kMaxSketchKO];
-  const int n = min(nin[q], W);
+  const int n  = min(nin[q], W);
   const int ns = select_by_bins(reinterpret_cast<const unsigned*>(dist + static_cast<int64_t>(q) * W),
-                                cand + static_cast<int64_t>(q) * W, n, KO, sid, sdv, sel);
+                                cand + static_cast<int64_t>(q) * W, n, KO, sid, sdv, u.sel);
   long long* pb = si + static_cast<int64_t>(q) * KO;
   float* pd     = sd + static_cast<int64_t>(q) * KO;
-  int P         = 2;
-  while (P < KO + ns)
-    P <<= 1;
-  load_keys(key, P, pb, pd, KO, fresh, sid, sdv, ns);
-  bitonic_sort(key, P);
-  store_keys(key, P, KO, pb, pd);
+  with_keys_per_thread(KO + ns, blockDim.x, [&](auto c) {
+    constexpr int C = decltype(c)::value;
+    merge_keep<C>(pb, pd, KO, fresh, sid, sdv, ns, pb, pd, KO, u.merge);
+  });
 }
+
+/**
+ * A set of up to kPickHash ids in LDS, in buckets of four slots: an id lives in its home bucket (a multiplicative
+ * hash) or, when that is full, in the next buckets.  A lookup reads a whole bucket with one 16-byte load.
+ */
+struct id_buckets {
+  static constexpr int kSlots = 4, kBuckets = kPickHash / kSlots;
+  int4 b[kBuckets];
+
+  __device__ static unsigned home(long long v)
+  {
+    return ((static_cast<unsigned>(v) * kIdHash) >> 7) & (kBuckets - 1);
+  }
+  __device__ void clear()
+  {
+    for (int i = threadIdx.x; i < kBuckets; i += blockDim.x)
+      b[i] = make_int4(-1, -1, -1, -1);
+  }
+  __device__ void insert(int v)
+  {
+    for (unsigned h = home(v), p = 0; p < kBuckets; p++, h = (h + 1) & (kBuckets - 1)) {
+      int* slot = reinterpret_cast<int*>(&b[h]);
+      for (int j = 0; j < kSlots; j++) {
+        const int prev = atomicCAS(&slot[j], -1, v);
+        if (prev == -1 || prev == v) return;
+      }
+    }
+  }
+  __device__ bool contains(int v) const
+  {
+    for (unsigned h = home(v), p = 0; p < kBuckets; p++, h = (h + 1) & (kBuckets - 1)) {
+      const int4 w = b[h];
+      if (w.x == v || w.y == v || w.z == v || w.w == v) return true;
+      if (w.w == -1) return false;  // a bucket with a free slot ends the run
+    }
+    return false;
+  }
+};
 
 /**
  * Start points of a wave (search_kernels.cuh:571-631): the first S kept entries (best first) that no
  * earlier wave expanded (done[:, :off]), written to done[:, off:off + S] and to the gather segments
- * seg2 = (row, rowlen); (-1 / (0, 0)) when fewer remain.
+ * seg2 = (row, rowlen); (-1 / (0, 0)) when fewer remain.  The expanded ids go into an LDS bucket set, every
+ * thread marks its kept entries fresh or not, and wavefront 0 takes the fresh ones in order by ballots.
  */
 __global__ __launch_bounds__(256) void pick_starts_kernel(const long long* __restrict__ si, int KO,
                                                           long long* __restrict__ done, int E,
@@ -1037,40 +1230,22 @@ __global__ __launch_bounds__(256) void pick_starts_kernel(const long long* __res
                                                           int2* __restrict__ seg2)
 {
   const int q = blockIdx.x;
-  __shared__ int ht[kPickHash];
+  __shared__ id_buckets seen;
   __shared__ unsigned char fresh[kMaxSketchKO];
   const long long* ps = si + static_cast<int64_t>(q) * KO;
   long long* pd       = done + static_cast<int64_t>(q) * E;
-  for (int i = threadIdx.x; i < kPickHash; i += blockDim.x)
-    ht[i] = -1;
-  __syncthreads();
-  for (int i = threadIdx.x; i < off; i += blockDim.x) {
-    long long v = pd[i];
-    if (v < 0) continue;
-    unsigned h = (static_cast<unsigned>(v) * kIdHash) & (kPickHash - 1);
-    for (int p = 0; p < kPickHash; p++) {
-      int prev = atomicCAS(&ht[h], -1, static_cast<int>(v));
-      if (prev == -1 || prev == static_cast<int>(v)) break;
-      h = (h + 1) & (kPickHash - 1);
+  if (off > 0) {
+    seen.clear();
+    __syncthreads();
+    for (int i = threadIdx.x; i < off; i += blockDim.x) {
+      const long long v = pd[i];
+      if (v >= 0) seen.insert(static_cast<int>(v));
     }
+    __syncthreads();
   }
-  __syncthreads();
   for (int i = threadIdx.x; i < KO; i += blockDim.x) {
-    long long v = ps[i];
-    bool f      = v >= 0;
-    if (f) {
-      unsigned h = (static_cast<unsigned>(v) * kIdHash) & (kPickHash - 1);
-      for (int p = 0; p < kPickHash; p++) {
-        int t = ht[h];
-        if (t == -1) break;
-        if (t == static_cast<int>(v)) {
-          f = false;
-          break;
-        }
-        h = (h + 1) & (kPickHash - 1);
-      }
-    }
-    fresh[i] = f;
+    const long long v = ps[i];
+    fresh[i]          = v >= 0 && (off == 0 || !seen.contains(static_cast<int>(v)));
   }
   __syncthreads();
   if ((threadIdx.x >> 6) != 0) return;
@@ -1094,7 +1269,11 @@ __global__ __launch_bounds__(256) void pick_starts_kernel(const long long* __res
   }
 }
 
-/** Exact rerank of the first R kept entries (sketch-rank mode) into the best k (:634-669). */
+/**
+ * Exact rerank of the first R kept entries (sketch-rank mode) into the best k (:634-669): the valid entries
+ * (id >= 0) are numbered by a workgroup prefix count, their exact distances computed, and the (distance, id)
+ * keys merged into an empty list of k.
+ */
 template <int LX>
 __global__ __launch_bounds__(kKeepThreads) void final_rerank_kernel(
   const long long* __restrict__ si, int KO, int R, const __half* __restrict__ vectors, int D,
@@ -1102,34 +1281,239 @@ __global__ __launch_bounds__(kKeepThreads) void final_rerank_kernel(
 {
   const int q = blockIdx.x;
   extern __shared__ float sq[];
+  __shared__ merge_lds<kMaxRerank> m2;
   __shared__ int sid[kMaxRerank];
   __shared__ float sd[kMaxRerank];
-  __shared__ uint64_t key[kMaxRerank];
-  __shared__ int nsel;
+  __shared__ int nvalid;
   const long long* ps = si + static_cast<int64_t>(q) * KO;
   for (int i = threadIdx.x; i < D; i += blockDim.x)
     sq[i] = Q[static_cast<int64_t>(q) * D + i];
-  if (threadIdx.x < 64) {  // the valid entries among the first R, in order (ballot compaction)
-    const int lane = threadIdx.x;
-    int at         = 0;
-    for (int i0 = 0; i0 < R; i0 += 64) {
-      const int i    = i0 + lane;
-      const bool ok  = i < R && ps[i] >= 0;
-      const unsigned long long mask = __ballot(ok);
-      if (ok) sid[at + __popcll(mask & ((1ULL << lane) - 1ULL))] = static_cast<int>(ps[i]);
-      at += __popcll(mask);
-    }
-    if (lane == 0) nsel = at;
+  // R <= 512 = 2 entries per thread, in order
+  long long v[2];
+  int mine = 0;
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int i = 2 * threadIdx.x + j;
+    v[j]        = i < R ? ps[i] : -1;
+    mine += v[j] >= 0 ? 1 : 0;
+  }
+  int total = 0;
+  int at    = block_exclusive_sum(mine, m2.wsum, &total);
+#pragma unroll
+  for (int j = 0; j < 2; j++)
+    if (v[j] >= 0) sid[at++] = static_cast<int>(v[j]);
+  if (threadIdx.x == 0) nvalid = total;
+  __syncthreads();
+  const int ns = nvalid;
+  exact_distances<LX>(sid, ns, vectors, D, sq, sd);
+  with_keys_per_thread(ns, blockDim.x, [&](auto c) {
+    constexpr int C = decltype(c)::value < 2 ? decltype(c)::value : 2;
+    merge_keep<C>(nullptr, nullptr, 0, true, sid, sd, ns, bi + static_cast<int64_t>(q) * k,
+                  bd + static_cast<int64_t>(q) * k, k, m2);
+  });
+}
+
+// ------------------------------------------------------------------ unfused merge (fused_merge = false)
+//
+// The reference's ablation of the fused kernels (search.cu:213-291, search_kernels.cuh:798-954): candidate keys
+// sorted in global memory, a pool of the kept list and the R best candidates, the pools sorted, and the first KO
+// distinct keys kept; start points by a sorted list of the expanded ids.  Same results as the fused kernels.
+
+/** ukey[q, j] = (dist, id) key of candidate j < n of query q, the empty key past n (W per query). */
+__global__ void cand_keys_kernel(const int* __restrict__ cand, const float* __restrict__ dist,
+                                 const int* __restrict__ nin, int W, uint64_t* __restrict__ ukey)
+{
+  const int q     = blockIdx.x;
+  const int n     = min(nin[q], W);
+  const int64_t o = static_cast<int64_t>(q) * W;
+  for (int j = threadIdx.x; j < W; j += blockDim.x)
+    ukey[o + j] = j < n ? dist_key(dist[o + j], cand[o + j]) : kEmpty;
+}
+
+/**
+ * Every row of keys [rows, width] sorted ascending in place (width a power of two, one workgroup per row).
+ * Tiles of C blockDim keys are sorted in registers; for rows wider than a tile the bitonic steps whose
+ * partners lie in other tiles run over global memory, each followed by a barrier.
+ */
+template <int C>
+__global__ __launch_bounds__(256) void sort_rows_kernel(uint64_t* __restrict__ keys, int width)
+{
+  __shared__ uint64_t xch[C * 256];
+  uint64_t* row  = keys + static_cast<int64_t>(blockIdx.x) * width;
+  const int tile = C * static_cast<int>(blockDim.x);
+  const int t    = threadIdx.x;
+  // every step of the sizes up to a tile stays inside the tile: one pass over the tiles
+  for (int base = 0; base < width; base += tile) {
+    uint64_t k[C];
+#pragma unroll
+    for (int j = 0; j < C; j++)
+      k[j] = row[base + C * t + j];
+    for (int size = 2; size <= tile; size <<= 1)
+      for (int st = size >> 1; st > 0; st >>= 1)
+        bitonic_step<C>(k, xch, base, size, st);
+#pragma unroll
+    for (int j = 0; j < C; j++)
+      row[base + C * t + j] = k[j];
   }
   __syncthreads();
-  const int ns = nsel;
-  exact_distances<LX>(sid, ns, vectors, D, sq, sd);
-  int P = 2;
-  while (P < R)
-    P <<= 1;
-  load_keys(key, P, nullptr, nullptr, 0, true, sid, sd, ns);
-  bitonic_sort(key, P);
-  store_keys(key, P, k, bi + static_cast<int64_t>(q) * k, bd + static_cast<int64_t>(q) * k);
+  for (int size = 2 * tile; size <= width; size <<= 1) {
+    int stride = size >> 1;
+    for (; stride >= tile; stride >>= 1) {  // partners in other tiles: through global memory
+      for (int i = t; i < width; i += blockDim.x) {
+        const int p = i ^ stride;
+        if (p > i) {
+          const uint64_t a = row[i], b = row[p];
+          if ((a > b) == ((i & size) == 0)) {
+            row[i] = b;
+            row[p] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+    for (int base = 0; base < width; base += tile) {  // the rest of this size inside each tile
+      uint64_t k[C];
+#pragma unroll
+      for (int j = 0; j < C; j++)
+        k[j] = row[base + C * t + j];
+      for (int st = stride; st > 0; st >>= 1)
+        bitonic_step<C>(k, xch, base, size, st);
+#pragma unroll
+      for (int j = 0; j < C; j++)
+        row[base + C * t + j] = k[j];
+    }
+    __syncthreads();
+  }
+}
+
+/**
+ * The pool of each query [pool keys]: its kept list (none when fresh), then its first min(R, n) sorted
+ * candidates, with exact distances (vectors non-null) or their sketch distances, the empty key after.
+ */
+template <int LX>
+__global__ __launch_bounds__(kKeepThreads) void pool_keys_kernel(
+  const uint64_t* __restrict__ sorted, const int* __restrict__ nin, int W, const __half* __restrict__ vectors, int D,
+  const float* __restrict__ Q, int R, const long long* __restrict__ si, const float* __restrict__ sd, int KO,
+  bool fresh, int pool, uint64_t* __restrict__ out)
+{
+  const int q = blockIdx.x;
+  extern __shared__ float sq[];
+  __shared__ int sid[kMaxSketchKO];
+  __shared__ float sdist[kMaxSketchKO];
+  const uint64_t* sk   = sorted + static_cast<int64_t>(q) * W;
+  const int ns         = min(R, min(nin[q], W));
+  const long long* pb  = si + static_cast<int64_t>(q) * KO;
+  const float* pdv     = sd + static_cast<int64_t>(q) * KO;
+  uint64_t* po         = out + static_cast<int64_t>(q) * pool;
+  for (int i = threadIdx.x; i < pool; i += blockDim.x) {
+    uint64_t v = kEmpty;
+    if (i < KO) {
+      if (!fresh && pb[i] >= 0) v = dist_key(pdv[i], pb[i]);
+    } else if (i - KO < ns && vectors == nullptr) {
+      v = sk[i - KO];
+    }
+    po[i] = v;
+  }
+  if (vectors == nullptr) return;
+  for (int i = threadIdx.x; i < D; i += blockDim.x)
+    sq[i] = Q[static_cast<int64_t>(q) * D + i];
+  for (int i = threadIdx.x; i < ns; i += blockDim.x)
+    sid[i] = static_cast<int>(sk[i] & 0xffffffffULL);
+  __syncthreads();
+  exact_distances<LX>(sid, ns, vectors, D, sq, sdist);
+  for (int i = threadIdx.x; i < ns; i += blockDim.x)
+    po[KO + i] = dist_key(sdist[i], sid[i]);
+}
+
+/** The first KO distinct keys of every sorted pool into the kept list, padded with (-1, +inf): one wavefront
+ * per query, the distinct keys placed by ballot counts. */
+__global__ __launch_bounds__(64) void keep_distinct_kernel(const uint64_t* __restrict__ pooled, int pool, int KO,
+                                                          long long* __restrict__ si, float* __restrict__ sd)
+{
+  const int q = blockIdx.x, lane = threadIdx.x;
+  const uint64_t* key = pooled + static_cast<int64_t>(q) * pool;
+  long long* pb       = si + static_cast<int64_t>(q) * KO;
+  float* pd           = sd + static_cast<int64_t>(q) * KO;
+  int at              = 0;
+  for (int i0 = 0; i0 < pool && at < KO; i0 += 64) {
+    const int i      = i0 + lane;
+    const uint64_t v = i < pool ? key[i] : kEmpty;
+    const bool keep  = v != kEmpty && (i == 0 || key[i - 1] != v);
+    const unsigned long long mask = __ballot(keep);
+    const int o = at + __popcll(mask & ((1ULL << lane) - 1ULL));
+    if (keep && o < KO) {
+      pb[o] = static_cast<long long>(static_cast<unsigned>(v & 0xffffffffULL));
+      pd[o] = __uint_as_float(static_cast<unsigned>(v >> 32));
+    }
+    at += __popcll(mask);
+  }
+  for (int o = min(at, KO) + lane; o < KO; o += 64) {
+    pb[o] = -1;
+    pd[o] = INFINITY;
+  }
+}
+
+/** dsort[q, i] = done[q, i] + 1 for i < off (ids >= -1 as unsigned keys), the empty key up to Ep. */
+__global__ void done_keys_kernel(const long long* __restrict__ done, int E, int off, int Ep,
+                                 uint64_t* __restrict__ dsort)
+{
+  const int q = blockIdx.x;
+  for (int i = threadIdx.x; i < Ep; i += blockDim.x)
+    dsort[static_cast<int64_t>(q) * Ep + i] =
+      i < off ? static_cast<uint64_t>(done[static_cast<int64_t>(q) * E + i] + 1) : kEmpty;
+}
+
+/** fresh[q, i]: kept entry i of query q is an id no earlier wave expanded (a binary search of the sorted ids). */
+__global__ void mark_fresh_kernel(const long long* __restrict__ si, int KO, const uint64_t* __restrict__ dsort,
+                                  int Ep, int off, int64_t total, unsigned char* __restrict__ fresh)
+{
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= total) return;
+  const long long v = si[t];
+  bool f            = v >= 0;
+  if (f && off > 0) {
+    const uint64_t want = static_cast<uint64_t>(v + 1);
+    const uint64_t* d   = dsort + (t / KO) * Ep;
+    int lo = 0, hi = off;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (d[mid] < want)
+        lo = mid + 1;
+      else
+        hi = mid;
+    }
+    f = !(lo < off && d[lo] == want);
+  }
+  fresh[t] = f;
+}
+
+/** The first S fresh kept entries of every query as its start points (one wavefront per query, by ballots), as
+ * pick_starts_kernel writes them. */
+__global__ __launch_bounds__(64) void take_starts_kernel(const long long* __restrict__ si,
+                                                        const unsigned char* __restrict__ fresh, int KO,
+                                                        long long* __restrict__ done, int E, int off, int S,
+                                                        int rowlen, int2* __restrict__ seg2)
+{
+  const int q = blockIdx.x, lane = threadIdx.x;
+  const long long* ps     = si + static_cast<int64_t>(q) * KO;
+  const unsigned char* fr = fresh + static_cast<int64_t>(q) * KO;
+  long long* pd           = done + static_cast<int64_t>(q) * E;
+  int at                  = 0;
+  for (int i0 = 0; i0 < KO && at < S; i0 += 64) {
+    const int i     = i0 + lane;
+    const bool take = i < KO && fr[i];
+    const unsigned long long mask = __ballot(take);
+    const int o = at + __popcll(mask & ((1ULL << lane) - 1ULL));
+    if (take && o < S) {
+      pd[off + o]                            = ps[i];
+      seg2[static_cast<int64_t>(q) * S + o] = make_int2(static_cast<int>(ps[i]), rowlen);
+    }
+    at += __popcll(mask);
+  }
+  for (int o = min(at, S) + lane; o < S; o += 64) {
+    pd[off + o]                            = -1;
+    seg2[static_cast<int64_t>(q) * S + o] = make_int2(0, 0);
+  }
 }
 
 __global__ void take_k_kernel(const long long* __restrict__ si, const float* __restrict__ sd, int KO,
@@ -1283,10 +1667,12 @@ auto gather_smem(int W, int S, int nseg, int max_len, bool lds_slots) -> size_t
          (lds_slots ? static_cast<size_t>(gather_cap(W, nseg, max_len)) * sizeof(unsigned short) : 0);
 }
 
-void launch_gather(bool rows, const int2* seg, int nseg, int max_len, int m, const long long* list_ptr,
-                   const int* table, int table_len, int64_t n, const signed char* code, int pitch,
-                   const float* scale, const float* qs, int S, int W, int logW, int* cand, float* dist,
-                   int* nout, hipStream_t s)
+namespace {
+
+template <bool kBalanced>
+void gather_impl(bool rows, const int2* seg, int nseg, int max_len, int m, const long long* list_ptr,
+                 const int* table, int table_len, int64_t n, const signed char* code, int pitch, const float* scale,
+                 const float* qs, int S, int W, int logW, int* cand, float* dist, int* nout, hipStream_t s)
 {
   OCTEX_EXPECTS(pitch >= S && pitch % 16 == 0, "octex: sketch rows are at least S bytes apart, 16-byte aligned");
   if (m == 0) return;
@@ -1312,9 +1698,9 @@ void launch_gather(bool rows, const int2* seg, int nseg, int max_len, int m, con
                                              logW, cap, cand, dist, nout);
     };
     if (lds_slots)
-      launch(&gather_kernel<R, LR, true>);
+      launch(&gather_kernel<R, LR, true, kBalanced>);
     else
-      launch(&gather_kernel<R, LR, false>);
+      launch(&gather_kernel<R, LR, false, kBalanced>);
   };
   auto by_lr = [&](auto rows_tag) {
     switch (Lr) {
@@ -1330,6 +1716,82 @@ void launch_gather(bool rows, const int2* seg, int nseg, int max_len, int m, con
     by_lr(std::true_type{});
   else
     by_lr(std::false_type{});
+  OCTEX_HIP(hipGetLastError());
+}
+
+/** sort_rows_kernel over rows of `width` keys (a power of two): up to 256 threads, up to 16 keys each. */
+void sort_rows(uint64_t* keys, int rows, int width, hipStream_t s)
+{
+  if (rows == 0 || width <= 1) return;
+  OCTEX_EXPECTS((width & (width - 1)) == 0, "octex: sorted rows hold a power of two keys");
+  const int threads = std::min(256, width);
+  const int c       = std::min(16, width / threads);
+  switch (c) {
+    case 1: sort_rows_kernel<1><<<rows, threads, 0, s>>>(keys, width); break;
+    case 2: sort_rows_kernel<2><<<rows, threads, 0, s>>>(keys, width); break;
+    case 4: sort_rows_kernel<4><<<rows, threads, 0, s>>>(keys, width); break;
+    case 8: sort_rows_kernel<8><<<rows, threads, 0, s>>>(keys, width); break;
+    default: sort_rows_kernel<16><<<rows, threads, 0, s>>>(keys, width); break;
+  }
+  OCTEX_HIP(hipGetLastError());
+}
+
+}  // namespace
+
+void launch_gather(bool rows, const int2* seg, int nseg, int max_len, int m, const long long* list_ptr,
+                   const int* table, int table_len, int64_t n, const signed char* code, int pitch,
+                   const float* scale, const float* qs, int S, int W, int logW, int* cand, float* dist,
+                   int* nout, hipStream_t s)
+{
+  gather_impl<true>(rows, seg, nseg, max_len, m, list_ptr, table, table_len, n, code, pitch, scale, qs, S, W, logW,
+                    cand, dist, nout, s);
+}
+
+void launch_gather_segments(bool rows, const int2* seg, int nseg, int max_len, int m, const long long* list_ptr,
+                            const int* table, int table_len, int64_t n, const signed char* code, int pitch,
+                            const float* scale, const float* qs, int S, int W, int logW, int* cand, float* dist,
+                            int* nout, hipStream_t s)
+{
+  gather_impl<false>(rows, seg, nseg, max_len, m, list_ptr, table, table_len, n, code, pitch, scale, qs, S, W, logW,
+                     cand, dist, nout, s);
+}
+
+void launch_unfused_keep(const int* cand, const float* dist, const int* nin, int m, int W, const __half* vectors,
+                         int D, const float* Q, int R, int KO, int pool, bool fresh, uint64_t* ukey, uint64_t* upool,
+                         long long* si, float* sd, hipStream_t s)
+{
+  if (m == 0) return;
+  OCTEX_EXPECTS(R >= 1 && R <= kMaxSketchKO && KO >= 1 && KO + R <= pool && (pool & (pool - 1)) == 0,
+                "octex: unfused merge pools: kept + reranked keys in a power of two");
+  OCTEX_EXPECTS(vectors == nullptr || R <= kMaxRerank, "octex: rerank in [1, 512] and max(starts, k) + rerank <= 1024");
+  cand_keys_kernel<<<m, 256, 0, s>>>(cand, dist, nin, W, ukey);
+  OCTEX_HIP(hipGetLastError());
+  sort_rows(ukey, m, W, s);
+  with_lx(D, [&](auto lx) {
+    pool_keys_kernel<decltype(lx)::value><<<m, kKeepThreads, vectors != nullptr ? D * sizeof(float) : 0, s>>>(
+      ukey, nin, W, vectors, D, Q, R, si, sd, KO, fresh, pool, upool);
+  });
+  OCTEX_HIP(hipGetLastError());
+  sort_rows(upool, m, pool, s);
+  keep_distinct_kernel<<<m, 64, 0, s>>>(upool, pool, KO, si, sd);
+  OCTEX_HIP(hipGetLastError());
+}
+
+void launch_unfused_pick(const long long* si, int m, int KO, long long* done, int E, int off, int S, int rowlen,
+                         uint64_t* dsort, int Ep, unsigned char* fresh, int2* seg2, hipStream_t s)
+{
+  if (m == 0) return;
+  OCTEX_EXPECTS(KO <= kMaxSketchKO && off <= kMaxExpanded && off + S <= E && off <= Ep,
+                "octex: starts * (waves - 1) <= 6144");
+  if (off > 0) {
+    done_keys_kernel<<<m, 256, 0, s>>>(done, E, off, Ep, dsort);
+    OCTEX_HIP(hipGetLastError());
+    sort_rows(dsort, m, Ep, s);
+  }
+  const int64_t total = int64_t{m} * KO;
+  mark_fresh_kernel<<<grid_for(total, 256), 256, 0, s>>>(si, KO, dsort, Ep, off, total, fresh);
+  OCTEX_HIP(hipGetLastError());
+  take_starts_kernel<<<m, 64, 0, s>>>(si, fresh, KO, done, E, off, S, rowlen, seg2);
   OCTEX_HIP(hipGetLastError());
 }
 

@@ -57,6 +57,25 @@ void launch_gather(bool rows, const int2* seg, int nseg, int max_len, int m, con
                    const int* table, int table_len, int64_t n, const signed char* code, int pitch,
                    const float* scale, const float* qs, int S, int W, int logW, int* cand, float* dist,
                    int* nout, hipStream_t s);
+/** launch_gather without the load balance (balanced_gather = false): a wavefront reads each segment whole
+ * (search_kernels.cuh:687-792).  Same arguments and results. */
+void launch_gather_segments(bool rows, const int2* seg, int nseg, int max_len, int m, const long long* list_ptr,
+                            const int* table, int table_len, int64_t n, const signed char* code, int pitch,
+                            const float* scale, const float* qs, int S, int W, int logW, int* cand, float* dist,
+                            int* nout, hipStream_t s);
+/**
+ * The kept list merged with a round's candidates without the fused kernels (fused_merge = false,
+ * search.cu:213-253): every candidate's key into ukey [m, W] and each row sorted, the pool of the kept list
+ * (none when fresh) and the R first sorted candidates with exact distances (vectors non-null; their sketch
+ * distances when null) into upool [m, pool] and sorted, the first KO distinct keys into si / sd.
+ */
+void launch_unfused_keep(const int* cand, const float* dist, const int* nin, int m, int W, const __half* vectors,
+                         int D, const float* Q, int R, int KO, int pool, bool fresh, uint64_t* ukey, uint64_t* upool,
+                         long long* si, float* sd, hipStream_t s);
+/** Start points without the fused selection (search.cu:261-291): the ids earlier waves expanded sorted into
+ * dsort [m, Ep], kept entries marked fresh by binary search, the first S fresh taken. */
+void launch_unfused_pick(const long long* si, int m, int KO, long long* done, int E, int off, int S, int rowlen,
+                         uint64_t* dsort, int Ep, unsigned char* fresh, int2* seg2, hipStream_t s);
 void launch_rerank_keep(const int* cand, const float* dist, const int* nin, int m, int W,
                         const __half* vectors, int D, const float* Q, int R, int KO, long long* si,
                         float* sd, bool fresh, hipStream_t s);

@@ -12,9 +12,10 @@
 
 #include <algorithm>
 #include <cmath>
-#include <functional>
 #include <cstring>
+#include <functional>
 #include <string>
+#include <type_traits>
 
 namespace cuvs::neighbors::octex {
 
@@ -40,17 +41,117 @@ plan::~plan()
   if (ev_out != nullptr) (void)hipEventDestroy(ev_out);
 }
 
-namespace {
-
-template <typename T>
-auto alloc(int64_t count, int fill = -2) -> dbuf
+auto make_shape(index_impl const& ix, search_params const& sp, int m, int k) -> plan_shape
 {
-  dbuf b(static_cast<size_t>(std::max<int64_t>(count, 1)) * sizeof(T));
-  if (fill != -2) OCTEX_HIP(hipMemset(b.ptr, fill, b.size));
-  return b;
+  plan_shape sh;
+  sh.sp = sp;
+  sh.m  = m;
+  sh.k  = k;
+  sh.KO = std::max(sp.starts, k);
+  sh.lr = std::min(sp.read, ix.list_len);
+  sh.R1 = sp.rerank;
+  sh.R2 = sp.wave_rerank;
+  sh.FR = std::min(sp.final_rerank, sh.KO);
+  const int S = sp.starts, C = ix.copies;
+  // parameter limits (search.cu:638-656, 681-692): the same checks and texts
+  OCTEX_EXPECTS(m >= 1 && k >= 1, "octex: a batch of at least one query and k >= 1");
+  OCTEX_EXPECTS(sp.read >= 1 && sp.starts >= 1 && sp.waves >= 0, "octex: read, starts >= 1 and waves >= 0");
+  OCTEX_EXPECTS(sp.waves == 0 || ix.table_len > 0, "octex: waves need the neighbor table");
+  OCTEX_EXPECTS(sh.KO <= (sp.sketch_rank ? kMaxSketchKO : kMaxRerank),
+                "octex: max(starts, k) must be <= 512 (1024 with sketch_rank)");
+  OCTEX_EXPECTS(sp.sketch_rank || (sp.rerank >= 1 && sp.rerank <= kMaxRerank && sh.KO + sp.rerank <= kMaxKeepSort),
+                "octex: rerank in [1, 512] and max(starts, k) + rerank <= 1024");
+  OCTEX_EXPECTS(sp.sketch_rank || sp.waves == 0 ||
+                  (sp.wave_rerank >= 1 && sp.wave_rerank <= kMaxRerank && sh.KO + sp.wave_rerank <= kMaxKeepSort),
+                "octex: wave_rerank in [1, 512] and max(starts, k) + wave_rerank <= 1024");
+  OCTEX_EXPECTS(!sp.sketch_rank || sh.FR == 0 || (k <= sh.FR && sh.FR <= kMaxRerank),
+                "octex: final_rerank 0 (sketch order) or k <= final_rerank <= 512");
+  OCTEX_EXPECTS(sp.waves <= 1 || S * (sp.waves - 1) <= kMaxExpanded, "octex: starts * (waves - 1) <= 6144");
+  const int log_max = log2_ceil(kMaxHash);
+  OCTEX_EXPECTS(int64_t{C} * sh.lr <= kMaxHash, "octex: copies x read too large for the shared-memory hash set");
+  sh.logW = std::clamp(log2_ceil(static_cast<int64_t>(std::ceil(C * sh.lr * 1.5f))), kMinLogHash, log_max);
+  sh.W    = 1 << sh.logW;
+  if (sp.waves > 0) {
+    OCTEX_EXPECTS(int64_t{S} * ix.table_len <= kMaxHash,
+                  "octex: starts x table_len too large for the shared-memory hash set");
+    sh.logW2 = std::clamp(log2_ceil(static_cast<int64_t>(std::ceil(S * ix.table_len * 1.5f))), kMinLogHash, log_max);
+    sh.W2    = 1 << sh.logW2;
+  }
+  if (!sp.fused_merge) {  // the pools of the unfused merge: the kept list and the R best candidates
+    auto pool = [&](int R) { return 1 << log2_ceil(sh.KO + (sp.sketch_rank ? sh.KO : R)); };
+    sh.pool1 = pool(sh.R1);
+    sh.pool2 = sp.waves > 0 ? pool(sh.R2) : 0;
+    sh.Ep    = sp.waves > 1 ? 1 << log2_ceil(int64_t{S} * (sp.waves - 1)) : 0;
+  }
+  return sh;
 }
 
-/** One stage of a batch: its name (as profiled) and its launch on the index's stream. */
+auto carve_buffers(index_impl const& ix, plan_shape const& sh, void* base, batch_buffers* out) -> size_t
+{
+  const int64_t m = sh.m, D = ix.dim, C = ix.copies, S = ix.sketch_width, st = sh.sp.starts;
+  const int64_t wdt = int64_t{8} * ix.blocks * C;
+  size_t at = 0;
+  auto take = [&](auto*& p, int64_t count) {
+    using T = std::remove_pointer_t<std::remove_reference_t<decltype(p)>>;
+    at = (at + 255) / 256 * 256;
+    p  = base != nullptr && count > 0 ? reinterpret_cast<T*>(static_cast<char*>(base) + at) : nullptr;
+    at += static_cast<size_t>(std::max<int64_t>(count, 0)) * sizeof(T);
+  };
+  batch_buffers b;
+  take(b.qbuf, m * D);
+  take(b.qc, m * D);
+  take(b.qh, m * D);
+  take(b.Y, m * wdt);
+  take(b.qs, m * S);
+  take(b.seg, m * C);
+  take(b.cand, m * sh.W);
+  take(b.dist, m * sh.W);
+  take(b.nin, m);
+  take(b.si, m * sh.KO);
+  take(b.sd, m * sh.KO);
+  if (sh.sp.waves > 0) {
+    take(b.done, m * st * sh.sp.waves);
+    take(b.seg2, m * st);
+    take(b.cand2, m * sh.W2);
+    take(b.dist2, m * sh.W2);
+    take(b.n2, m);
+  }
+  take(b.bi, m * sh.k);
+  take(b.bd, m * sh.k);
+  if (!sh.sp.fused_merge) {
+    take(b.ukey, m * std::max(sh.W, sh.W2));
+    take(b.upool, m * std::max(sh.pool1, sh.pool2));
+    take(b.dsort, m * sh.Ep);
+    take(b.fresh, m * sh.KO);
+  }
+  if (out != nullptr) *out = b;
+  return (at + 255) / 256 * 256;
+}
+
+auto named_buffer(index_impl const& ix, plan_shape const& sh, batch_buffers const& b, std::string const& n)
+  -> std::pair<const void*, size_t>
+{
+  const size_t m = static_cast<size_t>(sh.m), D = static_cast<size_t>(ix.dim), C = static_cast<size_t>(ix.copies);
+  const size_t S = static_cast<size_t>(ix.sketch_width), st = static_cast<size_t>(sh.sp.starts);
+  const size_t wv = static_cast<size_t>(sh.sp.waves), W = static_cast<size_t>(sh.W), W2 = static_cast<size_t>(sh.W2);
+  const size_t KO = static_cast<size_t>(sh.KO), k = static_cast<size_t>(sh.k);
+  const size_t wdt = size_t{8} * static_cast<size_t>(ix.blocks) * C;
+  const std::pair<const char*, std::pair<const void*, size_t>> all[] = {
+    {"queries", {b.qbuf, m * D * 4}}, {"qc", {b.qc, m * D * 4}},     {"qh", {b.qh, m * D * 2}},
+    {"Y", {b.Y, m * wdt * 2}},        {"qs", {b.qs, m * S * 4}},     {"seg", {b.seg, m * C * 8}},
+    {"cand", {b.cand, m * W * 4}},    {"dist", {b.dist, m * W * 4}}, {"nin", {b.nin, m * 4}},
+    {"si", {b.si, m * KO * 8}},       {"sd", {b.sd, m * KO * 4}},    {"done", {b.done, m * st * wv * 8}},
+    {"seg2", {b.seg2, m * st * 8}},   {"cand2", {b.cand2, m * W2 * 4}}, {"dist2", {b.dist2, m * W2 * 4}},
+    {"n2", {b.n2, wv > 0 ? m * 4 : 0}}, {"bi", {b.bi, m * k * 8}},  {"bd", {b.bd, m * k * 4}},
+  };
+  for (auto const& [name, where] : all)
+    if (n == name) return where.first != nullptr ? where : std::pair<const void*, size_t>(nullptr, 0);
+  fail("octex: unknown plan buffer %s", n.c_str());
+}
+
+namespace {
+
+/** One stage of a batch: its name (as profiled) and its launch. */
 struct stage {
   std::string name;
   std::function<void()> launch;
@@ -58,157 +159,100 @@ struct stage {
 
 /**
  * The launches of one batch in order (search.cu:294-518): the first round over all copies with the
- * best KO kept in si / sd, then the waves over the neighbor table, then the best k into bi / bd.
+ * best KO kept in si / sd, then the waves over the neighbor table, then the best k into bi / bd.  The
+ * reference's ablation switches pick other kernels with the same results: balanced_gather = false reads
+ * every segment whole by one wavefront (gather_warp_kernel, search_kernels.cuh:687-792), fused_merge =
+ * false keeps and picks start points through sorts in global memory (search.cu:213-291).
  */
-auto batch_stages(index_impl const& ix, plan const& pl, hipStream_t s) -> std::vector<stage>
+auto batch_stages(index_impl const& ix, plan_shape const& sh, batch_buffers const& b, hipStream_t s)
+  -> std::vector<stage>
 {
-  const int D = static_cast<int>(ix.dim), S = ix.sketch_width, C = ix.copies, m = pl.m;
+  const int D = static_cast<int>(ix.dim), S = ix.sketch_width, C = ix.copies, m = sh.m;
+  const bool balanced = sh.sp.balanced_gather, fused = sh.sp.fused_merge, sketch_rank = sh.sp.sketch_rank;
   std::vector<stage> out;
   auto add = [&](const char* n, std::function<void()> f) { out.push_back({n, std::move(f)}); };
-  add("center", [&ix, &pl, s, m, D] {
-    launch_center(pl.qbuf.as<float>(), ix.mean.as<float>(), m, D, pl.qc.as<float>(), pl.qh.as<__half>(), s);
+  add("center", [&ix, b, s, m, D] { launch_center(b.qbuf, ix.mean.as<float>(), m, D, b.qc, b.qh, s); });
+  add("project", [&ix, b, s, m, D, C] {
+    launch_project(b.qh, ix.ucatT.as<__half>(), ix.shift.as<__half>(), m, D, C * 8 * ix.blocks, b.Y, s);
   });
-  add("project", [&ix, &pl, s, m, D, C] {
-    launch_project(pl.qh.as<__half>(), ix.ucatT.as<__half>(), ix.shift.as<__half>(), m, D, C * 8 * ix.blocks,
-                   pl.Y.as<__half>(), s);
+  add("sketch_query", [&ix, b, s, m, D, S] { launch_sketch_query(b.qc, ix.basis.as<float>(), m, D, S, b.qs, s); });
+  add("probe", [&ix, b, sh, s, m, C] {
+    launch_probe(b.Y, m, C, ix.levels(), ix.blocks, ix.inv_f.as<float>(), ix.offsets.as<int>(), ix.T1,
+                 ix.keys.as<long long>(), ix.mmax, ix.base.as<int>(), ix.list_len, sh.lr, ix.log_buckets, b.seg, s);
   });
-  add("sketch_query", [&ix, &pl, s, m, D, S] {
-    launch_sketch_query(pl.qc.as<float>(), ix.basis.as<float>(), m, D, S, pl.qs.as<float>(), s);
-  });
-  add("probe", [&ix, &pl, s, m, C] {
-    launch_probe(pl.Y.as<__half>(), m, C, ix.levels(), ix.blocks, ix.inv_f.as<float>(), ix.offsets.as<int>(), ix.T1,
-                 ix.keys.as<long long>(), ix.mmax, ix.base.as<int>(), ix.list_len, pl.lr, ix.log_buckets,
-                 pl.seg.as<int2>(), s);
-  });
-  add("gather_lists", [&ix, &pl, s, m, S, C] {
-    launch_gather(false, pl.seg.as<int2>(), C, pl.lr, m, ix.list_ptr.as<long long>(), nullptr, 0, ix.n, ix.code(),
-                  ix.sketch_pitch, ix.scale.as<float>(), pl.qs.as<float>(), S, pl.W, pl.logW, pl.cand.as<int>(),
-                  pl.dist.as<float>(), pl.nin.as<int>(), s);
-  });
-  if (pl.sp.sketch_rank)
-    add("sketch_keep", [&pl, s, m] {
-      launch_sketch_keep(pl.cand.as<int>(), pl.dist.as<float>(), pl.nin.as<int>(), m, pl.W, pl.KO,
-                         pl.si.as<long long>(), pl.sd.as<float>(), true, s);
+  // stage names as profiled: the ablation paths are marked, so a profile shows which kernels ran
+  const std::string whole = balanced ? "" : "_whole", unfused = fused ? "" : "_unfused";
+  auto gather = [&](std::string const& name, bool rows, const int2* seg, int nseg, int max_len, int W, int logW,
+                    int* cand, float* dist, int* n) {
+    add((name + whole).c_str(), [&ix, b, s, m, S, rows, seg, nseg, max_len, W, logW, cand, dist, n, balanced] {
+      (balanced ? launch_gather : launch_gather_segments)(
+        rows, seg, nseg, max_len, m, rows ? nullptr : ix.list_ptr.as<long long>(), rows ? ix.rows() : nullptr,
+        ix.table_len, ix.n, ix.code(), ix.sketch_pitch, ix.scale.as<float>(), b.qs, S, W, logW, cand, dist, n, s);
     });
-  else
-    add("rerank_keep", [&ix, &pl, s, m, D] {
-      launch_rerank_keep(pl.cand.as<int>(), pl.dist.as<float>(), pl.nin.as<int>(), m, pl.W, ix.vecs(), D,
-                         pl.qbuf.as<float>(), pl.R1, pl.KO, pl.si.as<long long>(), pl.sd.as<float>(), true, s);
-    });
-  const int st = pl.sp.starts, nw = pl.sp.waves;
-  for (int wv = 0; wv < nw; wv++) {
-    add("pick_starts", [&ix, &pl, s, m, st, nw, wv] {
-      launch_pick_starts(pl.si.as<long long>(), m, pl.KO, pl.done.as<long long>(), st * nw, wv * st, st,
-                         ix.table_len, pl.seg2.as<int2>(), s);
-    });
-    add("gather_rows", [&ix, &pl, s, m, S, st] {
-      launch_gather(true, pl.seg2.as<int2>(), st, ix.table_len, m, nullptr, ix.rows(), ix.table_len, ix.n, ix.code(),
-                    ix.sketch_pitch, ix.scale.as<float>(), pl.qs.as<float>(), S, pl.W2, pl.logW2, pl.cand2.as<int>(),
-                    pl.dist2.as<float>(), pl.n2.as<int>(), s);
-    });
-    if (pl.sp.sketch_rank)
-      add("sketch_keep_wave", [&pl, s, m] {
-        launch_sketch_keep(pl.cand2.as<int>(), pl.dist2.as<float>(), pl.n2.as<int>(), m, pl.W2, pl.KO,
-                           pl.si.as<long long>(), pl.sd.as<float>(), false, s);
+  };
+  // the kept list merged with a round's candidates: fused (one kernel) or through global-memory sorts
+  auto keep = [&](std::string const& base_name, const int* cand, const float* dist, const int* n, int W, int R,
+                  int pool, bool fresh) {
+    const std::string nm = base_name + unfused;
+    const char* name     = nm.c_str();
+    if (fused && sketch_rank)
+      add(name, [b, sh, s, m, cand, dist, n, W, fresh] {
+        launch_sketch_keep(cand, dist, n, m, W, sh.KO, b.si, b.sd, fresh, s);
+      });
+    else if (fused)
+      add(name, [&ix, b, sh, s, m, D, cand, dist, n, W, R, fresh] {
+        launch_rerank_keep(cand, dist, n, m, W, ix.vecs(), D, b.qbuf, R, sh.KO, b.si, b.sd, fresh, s);
       });
     else
-      add("rerank_keep_wave", [&ix, &pl, s, m, D] {
-        launch_rerank_keep(pl.cand2.as<int>(), pl.dist2.as<float>(), pl.n2.as<int>(), m, pl.W2, ix.vecs(), D,
-                           pl.qbuf.as<float>(), pl.R2, pl.KO, pl.si.as<long long>(), pl.sd.as<float>(), false, s);
+      add(name, [&ix, b, sh, s, m, D, cand, dist, n, W, R, pool, fresh, sketch_rank] {
+        launch_unfused_keep(cand, dist, n, m, W, sketch_rank ? nullptr : ix.vecs(), D, b.qbuf,
+                            sketch_rank ? sh.KO : R, sh.KO, pool, fresh, b.ukey, b.upool, b.si, b.sd, s);
       });
+  };
+  gather("gather_lists", false, b.seg, C, sh.lr, sh.W, sh.logW, b.cand, b.dist, b.nin);
+  keep(sketch_rank ? "sketch_keep" : "rerank_keep", b.cand, b.dist, b.nin, sh.W, sh.R1, sh.pool1, true);
+  const int st = sh.sp.starts, nw = sh.sp.waves;
+  for (int wv = 0; wv < nw; wv++) {
+    add(("pick_starts" + unfused).c_str(), [&ix, b, sh, s, m, st, nw, wv, fused] {
+      if (fused)
+        launch_pick_starts(b.si, m, sh.KO, b.done, st * nw, wv * st, st, ix.table_len, b.seg2, s);
+      else
+        launch_unfused_pick(b.si, m, sh.KO, b.done, st * nw, wv * st, st, ix.table_len, b.dsort, sh.Ep, b.fresh,
+                            b.seg2, s);
+    });
+    gather("gather_rows", true, b.seg2, st, ix.table_len, sh.W2, sh.logW2, b.cand2, b.dist2, b.n2);
+    keep(sketch_rank ? "sketch_keep_wave" : "rerank_keep_wave", b.cand2, b.dist2, b.n2, sh.W2, sh.R2, sh.pool2,
+         false);
   }
-  if (pl.sp.sketch_rank && pl.FR > 0)
-    add("final_rerank", [&ix, &pl, s, m, D] {
-      launch_final_rerank(pl.si.as<long long>(), m, pl.KO, pl.FR, ix.vecs(), D, pl.qbuf.as<float>(), pl.k,
-                          pl.bi.as<long long>(), pl.bd.as<float>(), s);
+  if (sketch_rank && sh.FR > 0)
+    add("final_rerank", [&ix, b, sh, s, m, D] {
+      launch_final_rerank(b.si, m, sh.KO, sh.FR, ix.vecs(), D, b.qbuf, sh.k, b.bi, b.bd, s);
     });
   else
-    add("take_k", [&pl, s, m] {
-      launch_take_k(pl.si.as<long long>(), pl.sd.as<float>(), m, pl.KO, pl.k, pl.bi.as<long long>(), pl.bd.as<float>(),
-                    s);
-    });
+    add("take_k", [b, sh, s, m] { launch_take_k(b.si, b.sd, m, sh.KO, sh.k, b.bi, b.bd, s); });
   return out;
-}
-
-void launch_batch(index_impl const& ix, plan const& pl, hipStream_t s)
-{
-  for (auto& st : batch_stages(ix, pl, s))
-    st.launch();
 }
 
 auto make_plan(index_impl& ix, search_params const& sp, int m, int k) -> std::shared_ptr<plan>
 {
-  auto pl   = std::make_shared<plan>();
+  auto pl    = std::make_shared<plan>();
   pl->stream = ix.stream;
-  pl->sp    = sp;
-  pl->m     = m;
-  pl->k     = k;
-  pl->KO    = std::max(sp.starts, k);
-  pl->lr    = std::min(sp.read, ix.list_len);
-  pl->R1    = sp.rerank;
-  pl->R2    = sp.wave_rerank;
-  pl->FR    = std::min(sp.final_rerank, pl->KO);
-  const int D = static_cast<int>(ix.dim), S = sp.starts, sw = ix.sketch_width, C = ix.copies;
-  // parameter limits (search.cu:638-656, 681-692): the same checks and texts
-  OCTEX_EXPECTS(sp.read >= 1 && sp.starts >= 1 && sp.waves >= 0, "octex: read, starts >= 1 and waves >= 0");
-  OCTEX_EXPECTS(sp.waves == 0 || ix.table_len > 0, "octex: waves need the neighbor table");
-  OCTEX_EXPECTS(pl->KO <= (sp.sketch_rank ? kMaxSketchKO : kMaxRerank),
-                "octex: max(starts, k) must be <= 512 (1024 with sketch_rank)");
-  OCTEX_EXPECTS(sp.sketch_rank || (sp.rerank >= 1 && sp.rerank <= kMaxRerank && pl->KO + sp.rerank <= kMaxKeepSort),
-                "octex: rerank in [1, 512] and max(starts, k) + rerank <= 1024");
-  OCTEX_EXPECTS(sp.sketch_rank || sp.waves == 0 ||
-                  (sp.wave_rerank >= 1 && sp.wave_rerank <= kMaxRerank && pl->KO + sp.wave_rerank <= kMaxKeepSort),
-                "octex: wave_rerank in [1, 512] and max(starts, k) + wave_rerank <= 1024");
-  OCTEX_EXPECTS(!sp.sketch_rank || pl->FR == 0 || (k <= pl->FR && pl->FR <= kMaxRerank),
-                "octex: final_rerank 0 (sketch order) or k <= final_rerank <= 512");
-  OCTEX_EXPECTS(sp.waves <= 1 || S * (sp.waves - 1) <= kMaxExpanded, "octex: starts * (waves - 1) <= 6144");
-  const int log_max = log2_ceil(kMaxHash);
-  OCTEX_EXPECTS(int64_t{C} * pl->lr <= kMaxHash, "octex: copies x read too large for the shared-memory hash set");
-  pl->logW = std::clamp(log2_ceil(static_cast<int64_t>(std::ceil(C * pl->lr * 1.5f))), kMinLogHash, log_max);
-  pl->W    = 1 << pl->logW;
-  if (sp.waves > 0) {
-    OCTEX_EXPECTS(int64_t{S} * ix.table_len <= kMaxHash,
-                  "octex: starts x table_len too large for the shared-memory hash set");
-    pl->logW2 = std::clamp(log2_ceil(static_cast<int64_t>(std::ceil(S * ix.table_len * 1.5f))), kMinLogHash, log_max);
-    pl->W2    = 1 << pl->logW2;
-  }
-  const int wdt = 8 * ix.blocks * C;
-  pl->qbuf      = alloc<float>(int64_t{m} * D, 0);
-  pl->qc        = alloc<float>(int64_t{m} * D);
-  pl->qh        = alloc<__half>(int64_t{m} * D);
-  pl->Y         = alloc<__half>(int64_t{m} * wdt);
-  pl->qs        = alloc<float>(int64_t{m} * sw);
-  pl->seg       = alloc<int2>(int64_t{m} * C);
-  pl->cand      = alloc<int>(int64_t{m} * pl->W);
-  pl->dist      = alloc<float>(int64_t{m} * pl->W);
-  pl->nin       = alloc<int>(m);
-  pl->si        = alloc<long long>(int64_t{m} * pl->KO, 0xff);
-  pl->sd        = alloc<float>(int64_t{m} * pl->KO);
-  if (sp.waves > 0) {
-    pl->done  = alloc<long long>(int64_t{m} * S * sp.waves);
-    pl->seg2  = alloc<int2>(int64_t{m} * S);
-    pl->cand2 = alloc<int>(int64_t{m} * pl->W2);
-    pl->dist2 = alloc<float>(int64_t{m} * pl->W2);
-    pl->n2    = alloc<int>(m);
-  }
-  pl->bi = alloc<long long>(int64_t{m} * k);
-  pl->bd = alloc<float>(int64_t{m} * k);
-  for (dbuf const* b : {&pl->qbuf, &pl->qc, &pl->qh, &pl->Y, &pl->qs, &pl->seg, &pl->cand, &pl->dist,
-                        &pl->nin, &pl->si, &pl->sd, &pl->done, &pl->seg2, &pl->cand2, &pl->dist2,
-                        &pl->n2, &pl->bi, &pl->bd})
-    pl->buffer_bytes += static_cast<int64_t>(b->size);
+  pl->shape  = make_shape(ix, sp, m, k);
+  pl->block  = dbuf(carve_buffers(ix, pl->shape, nullptr, nullptr));
+  carve_buffers(ix, pl->shape, pl->block.ptr, &pl->buf);
   OCTEX_HIP(hipEventCreateWithFlags(&pl->ev_in, hipEventDisableTiming));
   OCTEX_HIP(hipEventCreateWithFlags(&pl->ev_out, hipEventDisableTiming));
-  // one eager run (code objects loaded, LDS limits set), then the capture of the whole batch
+  // one eager run on zeroed buffers (code objects loaded, LDS limits set), then the capture of the whole batch
   hipStream_t s = ix.stream;
   OCTEX_HIP(hipDeviceSynchronize());
-  launch_batch(ix, *pl, s);
+  OCTEX_HIP(hipMemsetAsync(pl->block.ptr, 0, pl->block.size, s));
+  launch_batch(ix, pl->shape, pl->buf, s);
   OCTEX_HIP(hipStreamSynchronize(s));
   if (sp.use_graph) {
     hipGraph_t graph = nullptr;
     OCTEX_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
     try {
-      launch_batch(ix, *pl, s);
+      launch_batch(ix, pl->shape, pl->buf, s);
     } catch (...) {
       hipGraph_t g2 = nullptr;
       (void)hipStreamEndCapture(s, &g2);
@@ -223,6 +267,12 @@ auto make_plan(index_impl& ix, search_params const& sp, int m, int k) -> std::sh
 }
 
 }  // namespace
+
+void launch_batch(index_impl const& ix, plan_shape const& sh, batch_buffers const& b, hipStream_t s)
+{
+  for (auto& st : batch_stages(ix, sh, b, s))
+    st.launch();
+}
 
 auto plan_key(search_params const& sp, int m, int k) -> std::string
 {
@@ -251,7 +301,7 @@ void run_batch(index_impl const& ix, plan const& pl, hipStream_t s)
   if (pl.graph != nullptr) {
     OCTEX_HIP(hipGraphLaunch(pl.graph, s));
   } else {
-    launch_batch(ix, pl, s);
+    launch_batch(ix, pl.shape, pl.buf, s);
   }
 }
 
@@ -269,6 +319,7 @@ void search_impl(raft::resources const& res, search_params const& sp, index cons
   const int m = static_cast<int>(std::min<int64_t>(std::max(sp.batch, 1), nq));
   std::unique_lock<std::mutex> run(ix.stream_mu);
   auto pl = get_plan(ix, sp, m, static_cast<int>(k));  // released before `run` on every path
+  auto const& b    = pl->buf;
   const int64_t D  = ix.dim;
   hipStream_t s    = ix.stream;
   hipStream_t call = raft::resource::get_cuda_stream(res);
@@ -277,13 +328,13 @@ void search_impl(raft::resources const& res, search_params const& sp, index cons
   for (int64_t b0 = 0; b0 < nq; b0 += m) {
     const int n = static_cast<int>(std::min<int64_t>(m, nq - b0));
     if (!resident) {
-      OCTEX_HIP(hipMemcpyAsync(pl->qbuf.ptr, queries + b0 * D, sizeof(float) * n * D, hipMemcpyDefault, s));
-      if (n < m) launch_pad_rows(pl->qbuf.as<float>(), n, m, static_cast<int>(D), s);
+      OCTEX_HIP(hipMemcpyAsync(b.qbuf, queries + b0 * D, sizeof(float) * n * D, hipMemcpyDefault, s));
+      if (n < m) launch_pad_rows(b.qbuf, n, m, static_cast<int>(D), s);
     }
     run_batch(ix, *pl, s);
     if (!resident) {
-      OCTEX_HIP(hipMemcpyAsync(neighbors + b0 * k, pl->bi.ptr, sizeof(int64_t) * n * k, hipMemcpyDefault, s));
-      OCTEX_HIP(hipMemcpyAsync(distances + b0 * k, pl->bd.ptr, sizeof(float) * n * k, hipMemcpyDefault, s));
+      OCTEX_HIP(hipMemcpyAsync(neighbors + b0 * k, b.bi, sizeof(int64_t) * n * k, hipMemcpyDefault, s));
+      OCTEX_HIP(hipMemcpyAsync(distances + b0 * k, b.bd, sizeof(float) * n * k, hipMemcpyDefault, s));
     }
   }
   OCTEX_HIP(hipEventRecord(pl->ev_out, s));
@@ -303,8 +354,10 @@ void profile_batch(index_impl& ix, plan& pl, int reps, std::vector<std::string>&
                    profile_counters& cnt)
 {
   hipStream_t s = ix.stream;
-  const int C = ix.copies, m = pl.m, st = pl.sp.starts;
-  auto steps    = batch_stages(ix, pl, s);
+  auto const& sh = pl.shape;
+  auto const& b  = pl.buf;
+  const int C = ix.copies, m = sh.m, st = sh.sp.starts;
+  auto steps    = batch_stages(ix, sh, b, s);
   std::vector<hipEvent_t> ev(steps.size() + 1);
   for (auto& e : ev)
     OCTEX_HIP(hipEventCreate(&e));
@@ -330,7 +383,7 @@ void profile_batch(index_impl& ix, plan& pl, int reps, std::vector<std::string>&
       // work counters of the last repetition, read between launches (outside the timed pairs)
       const std::string& nm = steps[i].name;
       if (nm == "probe") {
-        OCTEX_HIP(hipMemcpy(segh.data(), pl.seg.ptr, sizeof(int2) * m * C, hipMemcpyDeviceToHost));
+        OCTEX_HIP(hipMemcpy(segh.data(), b.seg, sizeof(int2) * m * C, hipMemcpyDeviceToHost));
         const int L = ix.levels();
         std::vector<int> base(static_cast<size_t>(C) * L);
         OCTEX_HIP(hipMemcpy(base.data(), ix.base.ptr, sizeof(int) * base.size(), hipMemcpyDeviceToHost));
@@ -345,21 +398,21 @@ void profile_batch(index_impl& ix, plan& pl, int reps, std::vector<std::string>&
           }
         }
       } else if (nm == "gather_lists") {
-        OCTEX_HIP(hipMemcpy(nin.data(), pl.nin.ptr, sizeof(int) * m, hipMemcpyDeviceToHost));
+        OCTEX_HIP(hipMemcpy(nin.data(), b.nin, sizeof(int) * m, hipMemcpyDeviceToHost));
         for (int v : nin) {
           cnt.distinct1 += v;
-          cnt.reranked1 += std::min(v, pl.sp.sketch_rank ? pl.KO : pl.R1);
+          cnt.reranked1 += std::min(v, sh.sp.sketch_rank ? sh.KO : sh.R1);
         }
       } else if (nm == "pick_starts") {
         wv++;
-        OCTEX_HIP(hipMemcpy(segh.data(), pl.seg2.ptr, sizeof(int2) * m * st, hipMemcpyDeviceToHost));
+        OCTEX_HIP(hipMemcpy(segh.data(), b.seg2, sizeof(int2) * m * st, hipMemcpyDeviceToHost));
         for (int64_t j = 0; j < int64_t{m} * st; j++)
           cnt.starts2[wv] += segh[j].y > 0;
       } else if (nm == "gather_rows") {
-        OCTEX_HIP(hipMemcpy(n2.data(), pl.n2.ptr, sizeof(int) * m, hipMemcpyDeviceToHost));
+        OCTEX_HIP(hipMemcpy(n2.data(), b.n2, sizeof(int) * m, hipMemcpyDeviceToHost));
         for (int v : n2) {
           cnt.distinct2[wv] += v;
-          cnt.reranked2[wv] += std::min(v, pl.sp.sketch_rank ? pl.KO : pl.R2);
+          cnt.reranked2[wv] += std::min(v, sh.sp.sketch_rank ? sh.KO : sh.R2);
         }
       }
     }

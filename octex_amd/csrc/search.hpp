@@ -1,31 +1,74 @@
-// Search plans of one MI355X: batch buffers and the hipGraph of one (batch, k, search parameters).
+// Search plans of one MI355X: the shape of one (batch, k, search parameters), its per-batch buffers and the
+// hipGraph of one batch.
 #pragma once
 
 #include "common.hpp"
 
 #include <cuvs/neighbors/octex.hpp>
 
+#include <hip/hip_fp16.h>
+
+#include <cstdint>
 #include <memory>
 #include <mutex>
 #include <string>
+#include <utility>
 #include <vector>
 
 namespace cuvs::neighbors::octex::detail {
 
 struct index_impl;
 
-struct plan {
+/** Batch size, k, parameters and the sizes derived from them (search.cu:619-655, 677-693). */
+struct plan_shape {
   search_params sp;
   int m = 0, k = 0, KO = 0, lr = 0, R1 = 0, R2 = 0, FR = 0;
   int W = 0, logW = 0, W2 = 0, logW2 = 0;  // hash-set / candidate capacity per query
-  // qbuf f32 [m, D] queries; qc f32 / qh f16 [m, D] centered; Y f16 [m, C 8b]; qs f32 [m, S];
-  // seg int2 [m, C]; cand i32 / dist f32 [m, W], nin [m]; si i64 / sd f32 [m, KO] kept list;
-  // done i64 [m, starts waves]; seg2 int2 [m, starts]; cand2 / dist2 [m, W2], n2 [m]; bi / bd [m, k]
-  dbuf qbuf, qc, qh, Y, qs, seg, cand, dist, nin, si, sd, done, seg2, cand2, dist2, n2, bi, bd;
+  int pool1 = 0, pool2 = 0;                // unfused merge (fused_merge = false): keys per query's pool
+  int Ep = 0;                              // unfused start points: sorted expanded ids per query
+};
+
+/**
+ * Where every per-batch array lies (device addresses): qbuf f32 [m, D] queries; qc f32 / qh f16 [m, D]
+ * centred; Y f16 [m, C 8b]; qs f32 [m, S]; seg int2 [m, C]; cand i32 / dist f32 [m, W], nin [m]; si i64 /
+ * sd f32 [m, KO] kept list; done i64 [m, starts waves]; seg2 int2 [m, starts]; cand2 / dist2 [m, W2], n2 [m];
+ * bi i64 / bd f32 [m, k]; with fused_merge = false also ukey u64 [m, max(W, W2)] candidate keys (sorted in
+ * place), upool u64 [m, max(pool1, pool2)] pools, dsort i64 [m, Ep] the ids earlier waves expanded, sorted
+ * (Ep the power of two >= starts (waves - 1)), and fresh u8 [m, KO].
+ */
+struct batch_buffers {
+  float *qbuf = nullptr, *qc = nullptr, *qs = nullptr, *dist = nullptr, *sd = nullptr, *dist2 = nullptr,
+        *bd = nullptr;
+  __half *qh = nullptr, *Y = nullptr;
+  int2 *seg = nullptr, *seg2 = nullptr;
+  int *cand = nullptr, *nin = nullptr, *cand2 = nullptr, *n2 = nullptr;
+  long long *si = nullptr, *done = nullptr, *bi = nullptr;
+  uint64_t *ukey = nullptr, *upool = nullptr, *dsort = nullptr;
+  unsigned char* fresh = nullptr;
+};
+
+/** The shape of a plan, with the reference's parameter limits checked (the same texts). */
+auto make_shape(index_impl const& ix, search_params const& sp, int m, int k) -> plan_shape;
+
+/**
+ * Lay the batch buffers of shape `sh` out in one block starting at `base` (each at a 256-byte boundary) and
+ * return the block's size in bytes; with base null only the size is computed.  Every buffer is written by a
+ * batch before it is read, so a block needs no clearing.
+ */
+auto carve_buffers(index_impl const& ix, plan_shape const& sh, void* base, batch_buffers* out) -> size_t;
+
+/** A named batch buffer ("queries", "Y", "seg", "cand", ..., as octexIndexCopyPlanBuffer lists) and its bytes. */
+auto named_buffer(index_impl const& ix, plan_shape const& sh, batch_buffers const& b, std::string const& name)
+  -> std::pair<const void*, size_t>;
+
+/** One plan: its shape, one block of batch buffers and the graph of a whole batch on the index's stream. */
+struct plan {
+  plan_shape shape;
+  dbuf block;
+  batch_buffers buf;
   hipGraphExec_t graph = nullptr;
   hipEvent_t ev_in = nullptr, ev_out = nullptr;
   hipStream_t stream = nullptr;  // the index's stream, where every batch of the plan runs
-  int64_t buffer_bytes = 0;
   plan() = default;
   plan(plan const&) = delete;
   ~plan();
@@ -35,6 +78,8 @@ auto plan_key(search_params const& sp, int m, int k) -> std::string;
 auto get_plan(index_impl& ix, search_params const& sp, int m, int k) -> std::shared_ptr<plan>;
 /** One batch of the plan on stream s (graph replay, or direct launches without a graph). */
 void run_batch(index_impl const& ix, plan const& pl, hipStream_t s);
+/** The launches of one batch over the buffers b on stream s, in order (direct launches, no graph). */
+void launch_batch(index_impl const& ix, plan_shape const& sh, batch_buffers const& b, hipStream_t s);
 /** Work counters of one profiled batch (summed over its m queries; per wave for the waves). */
 struct profile_counters {
   int64_t seg_hits = 0, entries1 = 0, distinct1 = 0, reranked1 = 0;

@@ -211,8 +211,8 @@ class Index:
             if given is None:
                 out.append(q.respond(got))
             else:
-                if tuple(given.shape) != (m, k):
-                    raise ValueError(f"octex: output arrays must have shape {(m, k)}, not {tuple(given.shape)}")
+                if _arrays.shape_of(given) != (m, k):
+                    raise ValueError(f"octex: output arrays must have shape {(m, k)}, not {_arrays.shape_of(given)}")
                 out.append(_arrays.write_into(given, got))
         return tuple(out)
 
