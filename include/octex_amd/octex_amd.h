@@ -96,6 +96,20 @@ cuvsError_t octexIndexPlaceOnHost(cuvsOctexIndex_t index, int32_t vectors, int32
  */
 cuvsError_t octexIndexCheckDirectory(const char* path, cuvsOctexLoadParams_t params, int64_t* info);
 
+/**
+ * No counterpart in the reference: for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  cuvsOctexSearch for device queries [nq, dim] (float32,
+ * row major) with every per-batch buffer in a file-scope device array of 256 MiB that each GPU holds until the
+ * process ends, instead of a cached plan's allocations; the batch's kernels run directly on `stream` (a
+ * hipStream_t, NULL the null stream; no graph) and write neighbors [nq, k] (int64) and distances [nq, k] (float32),
+ * device memory, ordered on that stream.  The queries are split into batches of min(params->batch, nq); a batch
+ * whose buffers exceed 256 MiB is an error that names the bytes it needs (lower params->batch).  No call allocates
+ * or frees device memory.  Every call on one GPU shares that GPU's array: calls that overlap on one GPU (other
+ * streams or threads) race, and the index must not change while one runs.
+ */
+cuvsError_t octexSearchNoAlloc(cuvsOctexSearchParams_t params, cuvsOctexIndex_t index, const float* queries,
+                               int64_t nq, int64_t dim, int64_t k, int64_t* neighbors, float* distances, void* stream);
+
 /* ---- stage entry points (fp16 arrays as raw 16-bit words) ---- */
 
 /** qc = q - mu, qh = fp16(qc) (search_kernels.cuh:57-69). */

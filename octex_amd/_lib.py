@@ -117,7 +117,7 @@ EXPORTS = (
     "cuvsOctexIndexGetCopies", "cuvsOctexIndexGetNumDevices", "cuvsOctexIndexGetDevices",
     "cuvsOctexIndexGetDeviceBytes", "cuvsOctexBuild", "cuvsOctexLoad", "cuvsOctexSearch",
     "octexIndexCopyPlanBuffer", "octexIndexPlanInfo", "octexBuildInMemory", "octexIndexProfileBatch", "octexIndexCopyArray",
-    "octexIndexCopyArrayRange", "octexIndexCopyArrayRanges", "octexIndexCheckDirectory",
+    "octexIndexCopyArrayRange", "octexIndexCopyArrayRanges", "octexIndexCheckDirectory", "octexSearchNoAlloc",
     "octexStageCenter", "octexStageProject", "octexStageSketchQuery", "octexStageE8", "octexStageProbe",
     "octexStageGather", "octexStageRerankKeep", "octexStageSketchKeep", "octexStagePickStarts",
     "octexStageFinalRerank", "octexStageTakeK",

@@ -375,6 +375,19 @@ extern "C" cuvsError_t cuvsOctexSearch(cuvsResources_t res, cuvsOctexSearchParam
   });
 }
 
+// ==================================================================== octex_amd.h
+
+extern "C" cuvsError_t octexSearchNoAlloc(cuvsOctexSearchParams_t params, cuvsOctexIndex_t index, const float* queries,
+                                          int64_t nq, int64_t dim, int64_t k, int64_t* neighbors, float* distances,
+                                          void* stream)
+{
+  return translate_exceptions([=] {
+    OCTEX_EXPECTS(params != nullptr && index != nullptr, "octex: NULL parameters or index");
+    octex::detail::search_no_alloc(to_cpp(*params), *as_index(*index), queries, nq, dim, k, neighbors, distances,
+                                   static_cast<hipStream_t>(stream));
+  });
+}
+
 // ==================================================================== introspection (octex_amd.h)
 
 extern "C" cuvsError_t octexIndexCheckDirectory(const char* path, cuvsOctexLoadParams_t params, int64_t* info)

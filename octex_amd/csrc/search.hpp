@@ -89,6 +89,13 @@ struct profile_counters {
 void profile_batch(index_impl& ix, plan& pl, int reps, std::vector<std::string>& names, std::vector<double>& ms,
                    profile_counters& cnt);
 /**
+ * The search of device queries [nq, dim] into device neighbors / distances [nq, k] on stream s with every batch
+ * buffer in the library's file-scope scratch array of the index's GPU (search_noalloc.cpp): no device allocation,
+ * direct launches, no graph.  A batch whose buffers exceed the array is an error.
+ */
+void search_no_alloc(search_params const& sp, index const& idx, const float* queries, int64_t nq, int64_t dim,
+                     int64_t k, int64_t* neighbors, float* distances, hipStream_t s);
+/**
  * The batch loop (search.cu:816-961).  resident: the queries of the previous call stay in place in
  * the plan's query buffer (one batch only) and nothing is copied in or out (the timing protocol).
  */
