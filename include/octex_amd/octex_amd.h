@@ -110,6 +110,16 @@ cuvsError_t octexIndexCheckDirectory(const char* path, cuvsOctexLoadParams_t par
 cuvsError_t octexSearchNoAlloc(cuvsOctexSearchParams_t params, cuvsOctexIndex_t index, const float* queries,
                                int64_t nq, int64_t dim, int64_t k, int64_t* neighbors, float* distances, void* stream);
 
+/**
+ * No counterpart in the reference (measurement): the random-row read ceiling that the search gathers are held
+ * against.  Reads n rows of row_bytes (a multiple of 16, at most 512) at uniformly random row numbers in
+ * [0, rows) of base (rows * pitch bytes of device memory), one 16-byte load per lane, in_flight (1, 2, 4 or 8)
+ * rows per lane group in flight, over `blocks` workgroups of 256 threads; out (device, blocks * 256 / G words,
+ * G = the next power of two >= row_bytes / 16) gets an XOR of the words read.  Asynchronous on `stream`.
+ */
+cuvsError_t octexMeasureRowReads(const void* base, int64_t rows, int32_t pitch, int32_t row_bytes, int64_t n,
+                                 int32_t in_flight, int32_t blocks, uint64_t seed, uint32_t* out, void* stream);
+
 /* ---- stage entry points (fp16 arrays as raw 16-bit words) ---- */
 
 /** qc = q - mu, qh = fp16(qc) (search_kernels.cuh:57-69). */

@@ -120,7 +120,7 @@ EXPORTS = (
     "octexIndexCopyArrayRange", "octexIndexCopyArrayRanges", "octexIndexCheckDirectory", "octexSearchNoAlloc",
     "octexStageCenter", "octexStageProject", "octexStageSketchQuery", "octexStageE8", "octexStageProbe",
     "octexStageGather", "octexStageRerankKeep", "octexStageSketchKeep", "octexStagePickStarts",
-    "octexStageFinalRerank", "octexStageTakeK",
+    "octexStageFinalRerank", "octexStageTakeK", "octexMeasureRowReads",
 )
 
 _lib = None

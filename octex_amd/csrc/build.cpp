@@ -508,6 +508,9 @@ auto build_in_memory(index_params const& params, dataset_view const& x, build_re
                       ? static_cast<int>(std::min<int64_t>(params.sketch_width, d))
                       : static_cast<int>(std::max<int64_t>(std::min<int64_t>(d / 16 * 16, 128), std::min<int64_t>(d, 16)));
   const int k = params.table_len;
+  // the loader's rule for a directory (load.cu:236): the sketch is scored in 16-code chunks
+  OCTEX_EXPECTS(S % 16 == 0 && S >= 16 && S <= 512,
+                "octex: sketch_width %d: the sketch width must be a multiple of 16 in [16, 512]", S);
   OCTEX_EXPECTS(C >= 1, "octex: at least one copy");
   OCTEX_EXPECTS(n >= 2 && d >= 1, "octex: empty dataset");
   OCTEX_EXPECTS(b >= 1 && b <= 8 && b != 7, "octex: blocks must be 1-6 or 8");

@@ -22,31 +22,32 @@ constexpr unsigned long long kMix = 0x9E3779B97F4A7C15ULL;  // e8.cuh:21
 
 // ------------------------------------------------------------------ E8 (e8.cuh:24-85)
 
-/** Nearest point of D8: round every coordinate, then fix the parity at the worst-rounded one. */
+/**
+ * Nearest point of D8: round every coordinate, then fix the parity at the worst-rounded one, the first index
+ * whose |x - rint(x)| is the largest (the reference's strict-greater scan from -1 picks the same one; a NaN error
+ * is never picked, and when every error is NaN the reference's fix lands on a coordinate that is NaN or infinite
+ * already).  The fix moves that coordinate one step towards x: copysign(1, e), e never being -0 here.
+ */
 __device__ __forceinline__ void d8(const float (&x)[8], float (&f)[8])
 {
-  float s  = 0.f;
-  int im   = 0;
-  float em = -1.f, ei = 0.f;
+  float s = 0.f, m = -1.f, e[8];
 #pragma unroll
   for (int i = 0; i < 8; i++) {
-    f[i]     = rintf(x[i]);
-    s        = s + f[i];
-    float e  = x[i] - f[i];
-    float ae = fabsf(e);
-    if (ae > em) {
-      em = ae;
-      im = i;
-      ei = e;
-    }
+    f[i] = rintf(x[i]);
+    s    = s + f[i];
+    e[i] = x[i] - f[i];
+    m    = fmaxf(m, fabsf(e[i]));
   }
   // fmodf(s, 2) != 0, with the integer parity for |s| < 2^24 (every such s here is an integer, and fmodf's
   // general reduction loop is costly); larger, infinite or NaN sums take fmodf itself
-  const bool odd   = fabsf(s) < 16777216.f ? (static_cast<int>(s) & 1) != 0 : fmodf(s, 2.f) != 0.f;
-  const float step = ei >= 0.f ? 1.f : -1.f;
+  const bool odd = fabsf(s) < 16777216.f ? (static_cast<int>(s) & 1) != 0 : fmodf(s, 2.f) != 0.f;
+  bool seen      = false;
 #pragma unroll
-  for (int i = 0; i < 8; i++)  // selects, not branches: the fixed coordinate differs between lanes
-    f[i] = (odd && i == im) ? f[i] + step : f[i];
+  for (int i = 0; i < 8; i++) {  // selects, not branches: the fixed coordinate differs between lanes
+    const bool pick = !seen && fabsf(e[i]) == m;
+    seen            = seen || pick;
+    f[i]            = (odd && pick) ? f[i] + copysignf(1.f, e[i]) : f[i];
+  }
 }
 
 /** Nearest point of E8 = D8 u (D8 + 1/2): the nearer of the two cosets' points (ties: D8). */
@@ -73,10 +74,26 @@ __device__ __forceinline__ void e8_point(const float (&x)[8], float (&p)[8])
     p[i] = useA ? a[i] : c[i];
 }
 
+/** The i-th prime as a signed low word and a high word with P = hi 2^32 + lo (mod 2^64), for 32 x 32 products. */
+struct prime_split {
+  int lo, hi;
+};
+constexpr auto split_prime(unsigned long long P) -> prime_split
+{
+  const unsigned lo = static_cast<unsigned>(P & 0xffffffffULL);
+  const unsigned hi = static_cast<unsigned>(P >> 32) + (lo >= 0x80000000u ? 1u : 0u);
+  return {static_cast<int>(lo), static_cast<int>(hi)};
+}
+constexpr prime_split kPrimeSplit[8] = {split_prime(1000003ULL),          split_prime(998244353ULL),
+                                        split_prime(1000000007ULL),       split_prime(2147483647ULL),
+                                        split_prime(1099511627791ULL),    split_prime(4398042316799ULL),
+                                        split_prime(70368744177643ULL),   split_prime(1125899906842597ULL)};
+
 /**
- * Block hash: sum of 2 p_i times the i-th prime (64-bit wraparound).  2 p_i is converted to int64 as a
- * 32-bit conversion sign-extended when every |2 p_i| < 2^31 (the same integer, and the float-to-int64
- * conversion has no single instruction); otherwise by the int64 conversion itself.
+ * Block hash: sum of 2 p_i times the i-th prime (64-bit wraparound).  When every |2 p_i| < 2^31, 2 p_i is a 32-bit
+ * integer q and q P = q lo + (q hi mod 2^32) 2^32 (mod 2^64) with lo, hi of kPrimeSplit: a 32 x 32 -> 64 signed
+ * multiply-add, plus a 32-bit product into the high word for the primes above 2^31.  Otherwise 2 p_i goes through
+ * the int64 conversion itself.
  */
 __device__ __forceinline__ unsigned long long block_hash(const float (&p)[8])
 {
@@ -86,11 +103,15 @@ __device__ __forceinline__ unsigned long long block_hash(const float (&p)[8])
     amax = fmaxf(amax, fabsf(2.f * p[i]));
   unsigned long long hb = 0;
   if (amax < 2147483648.f) {
+    unsigned long long lo = 0;  // each product fits in int64; their sum wraps mod 2^64
+    unsigned hi           = 0;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-      const long long p2 = static_cast<long long>(static_cast<int>(2.f * p[i]));
-      hb += static_cast<unsigned long long>(p2) * static_cast<unsigned long long>(kPrimes[i]);
+      const int q = static_cast<int>(2.f * p[i]);
+      lo += static_cast<unsigned long long>(static_cast<long long>(q) * static_cast<long long>(kPrimeSplit[i].lo));
+      if (kPrimeSplit[i].hi != 0) hi += static_cast<unsigned>(q) * static_cast<unsigned>(kPrimeSplit[i].hi);
     }
+    hb = lo + (static_cast<unsigned long long>(hi) << 32);
   } else {
 #pragma unroll
     for (int i = 0; i < 8; i++) {

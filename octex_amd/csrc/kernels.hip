@@ -293,9 +293,14 @@ __global__ __launch_bounds__(256) void probe_kernel(const __half* __restrict__ Y
   int lvl = 0, c = 0;
   int64_t u = 0;
   uint4 yv[B];
+  // item / m as (item + 1/2) * fl(1 / m), truncated: exact when item + 1/2 < 2^22 (the relative error of the
+  // product, at most 2^-23 (1 + 2^-24), stays under the 1/(2 m) between the quotient and an integer); larger
+  // batches divide in 64 bits
+  const bool by_recip = total < (int64_t{1} << 22);
+  const float inv_m   = 1.f / static_cast<float>(m);
   auto start = [&]() {  // a new item: its copy, its output slot, its fp16 row
-    c                 = static_cast<int>(item / m);
-    u                 = (item % m) * C + c;
+    c = by_recip ? static_cast<int>((static_cast<float>(item) + 0.5f) * inv_m) : static_cast<int>(item / m);
+    u = (item - static_cast<int64_t>(c) * m) * C + c;
     const uint4* yp   = reinterpret_cast<const uint4*>(Y + u * 8 * B);
 #pragma unroll
     for (int jb = 0; jb < B; jb++)
@@ -497,6 +502,11 @@ __device__ int collect_candidates(const int2* __restrict__ seg, int nseg, const 
     ht[i] = -1;
   __syncthreads();
   const int step = blockDim.x;
+  // i / len as (i + 1/2) * fl(1 / len), truncated: the product's relative error is at most 2^-23 (1 + 2^-24), under
+  // the 1/(2 len) between (i + 1/2) / len and an integer when i + 1/2 < 2^22 (a search reads at most kMaxHash
+  // entries per query); larger totals divide
+  const float inv_len = len > 0 ? 1.f / static_cast<float>(len) : 0.f;
+  const bool by_recip = total < (1 << 22);
   for (int i0 = 0; i0 < total; i0 += step * kUnroll) {
     int v[kUnroll];
 #pragma unroll
@@ -504,7 +514,7 @@ __device__ int collect_candidates(const int2* __restrict__ seg, int nseg, const 
       const int i = min(i0 + u * step + tid, total - 1);
       int sg;
       if (len > 0) {
-        sg = i / len;
+        sg = by_recip ? static_cast<int>((static_cast<float>(i) + 0.5f) * inv_len) : i / len;
       } else {
         int lo = 0, hi = ns - 1;
         while (lo < hi) {

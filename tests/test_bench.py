@@ -57,3 +57,17 @@ def test_distance_error():
 def test_one_gpu_only():
     out = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True, text=True)
     assert out.returncode != 0 and "one GPU" in (out.stdout + out.stderr)
+
+
+def test_every_workload_has_a_fixed_point():
+    for name, cfg in bench.CONFIGS.items():
+        if name == "small":
+            continue
+        p = cfg["point"]
+        assert {"read", "starts", "waves", "rerank", "wave_rerank"} <= set(p), name
+
+
+def test_host_cpu_record():
+    h = bench.host_cpu()
+    assert 1 <= h["threads"] <= 16 and h["threads"] <= h["affinity"] <= h["nproc"]
+    assert isinstance(h["model"], str) and "16" in h["rule"]

@@ -404,3 +404,46 @@ def test_stage_errors(L):
     with pytest.raises(OctexError, match="rerank in \\[1, 512\\]"):
         L.call("octexStageRerankKeep", P(x), P(x), P(x), i32(1), i32(2048), P(x), i32(64), P(x), i32(600), i32(10),
                P(x), P(x), i32(1), None)
+
+
+# ---------------------------------------------------------------- lane layouts of the row kernels
+
+# (D, S): the sketch scores put a row's S / 16 chunks on that many adjacent lanes (16 and 32 lanes per row at
+# S = 256 / 512, 6 at 96, 3 at 48, 1 at 16) and the exact distances a row's D / 8 chunks on D / 8 lanes up to 32
+# (12 lanes at D = 96, 25 at 200, 6 at 48); D = 960 takes several chunks per lane, D = 100 the unaligned path
+@pytest.mark.parametrize("D,S", [(960, 512), (960, 256), (100, 48), (200, 96), (96, 96), (48, 16)])
+def test_row_layouts_match_oracle(L, D, S):
+    import octex_amd
+
+    X, Q = clustered(n=1200, m=24, d=D, clusters=6, seed=D + S)
+    index, _ = octex_amd.build_in_memory(X, copies=3, blocks=2, pca_dims=min(D, 32), list_len=8, table_len=16,
+                                         log_buckets=8, sketch_width=S, member_lists=True, reverse_edges=False,
+                                         seed=3)
+    rix = O.Index(index)  # the GPU-built arrays, copied to the host
+    assert rix.sketch_width == S and rix.dim == D
+    rdix = dict(lists=dev(rix.lists), table=dev(rix.table), sketch=dev(rix.sketch), scale=dev(rix.scale),
+                vectors=dev(rix.vectors.view(np.int16)))
+    g = np.random.default_rng(D * 7 + S)
+    m, nst = len(Q), 24
+    seg2 = np.stack([g.integers(0, rix.n, (m, nst)), np.full((m, nst), rix.table_len)], -1).astype(np.int32)
+    seg2[:, -3:] = 0
+    qs = g.standard_normal((m, S)).astype(np.float32)
+    cand, dist, nout = gather_gpu(L, rix, rdix, dev(seg2), qs, rows=1, W=2048)
+    check_gather(rix, seg2, qs, cand, dist, nout, rows=True)
+    # exact rerank of these candidates into a fresh kept list, then into a kept list that holds entries
+    KO, R, W = 32, 48, 2048
+    si = np.full((m, KO), -1, np.int64)
+    sd = np.full((m, KO), np.inf, np.float32)
+    dsi, dsd = dev(si), dev(sd)
+    dc, dd, dn, dQ = dev(cand), dev(dist), dev(nout), dev(Q)
+    for fresh in (True, False):
+        L.call("octexStageRerankKeep", P(dc), P(dd), P(dn), i32(m), i32(W), P(rdix["vectors"]), i32(D), P(dQ),
+               i32(R), i32(KO), P(dsi), P(dsd), i32(fresh), None)
+        for q in range(m):
+            n = nout[q]
+            ri, rd = O.rerank_keep(rix, cand[q, :n], dist[q, :n], Q[q], R, si[q], sd[q], fresh)
+            assert np.array_equal(host(dsi)[q], ri), f"query {q} fresh {fresh}"
+            assert np.array_equal(host(dsd)[q], rd), f"query {q} fresh {fresh}"
+            si[q], sd[q] = ri, rd
+        dist = dist + g.uniform(0, 4, dist.shape).astype(np.float32)  # the second round: another sketch order
+        dd = dev(dist)
