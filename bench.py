@@ -28,12 +28,16 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor figure
 
+# Cell lists: the workloads of 1M rows and more build member lists (the reference's fast build mode, --member-lists /
+# octex_build --fast): its default IVF lists run k-means and a probed list search for every copy, too long for a
+# benchmark session at 100M rows.  cpu100k builds the reference's default index, IVF lists included.
 CONFIGS = {
     # configs[1] of BASELINE.json; the index as the reference's paper SIFT1M build (copies 200, lists of 32, no
     # reverse edges) with the reference's default sketch width for d = 128 (128), cells of >= 2 rows for lists
     "sift1m": dict(n=1_000_000, d=128, nq=10_000, clusters=1000, kind="sift", batch=10_000,
                    desc="seeded Gaussian mixture as BASELINE.json configs[1]",
-                   index=dict(copies=200, list_len=32, table_len=64, min_cell=2, reverse_edges=False, seed=0),
+                   index=dict(copies=200, list_len=32, table_len=64, min_cell=2, reverse_edges=False, member_lists=True,
+                              seed=0),
                    point=dict(read=4, starts=16, waves=1, rerank=16, wave_rerank=16)),
     # configs[3] of BASELINE.json: 100M L2-normalized rows, d = 96, of a 10,000-component mixture (centroids N(0, 1),
     # sigma 0.4) stored fp16; the index as the reference's paper Deep100M build (lists of 64, cells of >= 10 rows,
@@ -42,7 +46,7 @@ CONFIGS = {
     # the vectors, sketch, table and search buffers (1.3 GB of lists per copy on this data)
     "deep100m": dict(n=100_000_000, d=96, nq=10_000, clusters=10_000, kind="deep", batch=10_000,
                      desc="seeded normalized Gaussian mixture as BASELINE.json configs[3], fp16 rows",
-                     index=dict(copies=150, list_len=64, min_cell=10, table_len=64, seed=0),
+                     index=dict(copies=150, list_len=64, min_cell=10, table_len=64, member_lists=True, seed=0),
                      point=dict(read=12, starts=64, waves=2, rerank=128, wave_rerank=128)),
     # configs[4] of BASELINE.json (1B rows, fp16 vectors in pinned host memory, sketch-rank search) at a tenth of its
     # size: a 1B index does not build within one GPU session here.  The rows of deep100m; the index as configs[4]
@@ -52,7 +56,8 @@ CONFIGS = {
     "deep100m-host": dict(n=100_000_000, d=96, nq=10_000, clusters=10_000, kind="deep", batch=10_000,
                           desc="seeded normalized Gaussian mixture as BASELINE.json configs[3]/[4], fp16 rows, "
                                "vectors in pinned host memory",
-                          index=dict(copies=150, list_len=16, min_cell=10, table_len=32, seed=0), host=("vectors",),
+                          index=dict(copies=150, list_len=16, min_cell=10, table_len=32, member_lists=True, seed=0),
+                          host=("vectors",),
                           point=dict(read=16, starts=128, waves=3, rerank=128, wave_rerank=128, sketch_rank=True,
                                      final_rerank=32)),
     # configs[2] of BASELINE.json: 1M x 960 non-negative half-normal features (scale 0.05) plus per-cluster offsets
@@ -63,7 +68,7 @@ CONFIGS = {
     "gist1m": dict(n=1_000_000, d=960, nq=1_000, clusters=1000, kind="gist", batch=1_000,
                    desc="seeded half-normal mixture as BASELINE.json configs[2]",
                    index=dict(copies=150, list_len=64, min_cell=16, table_len=64, sketch_width=128, reverse_edges=False,
-                              seed=0),
+                              member_lists=True, seed=0),
                    point=dict(read=32, starts=64, waves=3, rerank=512, wave_rerank=512)),
     # configs[0] of BASELINE.json, the reference's CPU-runnable case: 100k rows, d = 128, of a 100-component
     # Gaussian mixture (centroids N(0, 1), sigma 0.3), 1,000 queries, the reference's default index (200 copies,
@@ -75,8 +80,8 @@ CONFIGS = {
                     point=dict(read=32, starts=128, waves=2, rerank=128, wave_rerank=128)),
     # a small stand-in for quick checks
     "small": dict(n=100_000, d=128, nq=10_000, clusters=100, kind="sift", batch=10_000, desc="small SIFT-like mixture",
-                  index=dict(copies=64, list_len=32, table_len=64, min_cell=2, reverse_edges=False, seed=0,
-                             log_buckets=18)),
+                  index=dict(copies=64, list_len=32, table_len=64, min_cell=2, reverse_edges=False, member_lists=True,
+                             seed=0, log_buckets=18)),
 }
 
 SWEEP_DEEP = [

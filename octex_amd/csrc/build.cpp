@@ -520,8 +520,12 @@ auto build_in_memory(index_params const& params, dataset_view const& x, build_re
   OCTEX_EXPECTS(params.log_buckets >= 1 && params.log_buckets <= 30, "octex: log_buckets in [1, 30]");
   OCTEX_EXPECTS(d % 2 == 0, "octex: the dimension must be even");
   OCTEX_EXPECTS(S % 16 == 0 && S <= 512, "octex: sketch width: a multiple of 16, <= 512");
-  const bool exact_lists = params.exact_lists && !params.member_lists;  // member lists first (build_cells.cuh:505)
+  // member lists first, then exact, else the IVF lists of the reference's default (build_cells.cuh:505-516)
+  const bool exact_lists = params.exact_lists && !params.member_lists;
+  const bool ivf_lists   = !params.exact_lists && !params.member_lists;
   OCTEX_EXPECTS(!exact_lists || l <= 128, "octex: exact lists take list_len <= 128");
+  OCTEX_EXPECTS(!ivf_lists || l <= 128, "octex: IVF lists take list_len <= 128");
+  OCTEX_EXPECTS(!ivf_lists || params.list_probes >= 1, "octex: list_probes must be positive");
   int cur = 0;
   OCTEX_HIP(hipGetDevice(&cur));
   auto impl = std::make_shared<index_impl>();
@@ -611,12 +615,18 @@ auto build_in_memory(index_params const& params, dataset_view const& x, build_re
   {
     cell_builder cb;
     cb.reserve(n, w, s);
+    ivf_index ivf;
+    // the reference's IVF parameters (build_cells.cuh:513-515): max(64, 4 sqrt(n)) lists, trained on half the rows
+    // up to 4M rows, a tenth above; 20 rounds of k-means (cuVS's default)
+    const int nlist = static_cast<int>(std::max<int64_t>(64, static_cast<int64_t>(4 * std::sqrt(static_cast<double>(n)))));
+    const double train_fraction = n <= 4000000 ? 0.5 : 0.1;
     dbuf y(static_cast<size_t>(n) * w * sizeof(float)), U(static_cast<size_t>(d) * w * sizeof(float)),
       sh(w * sizeof(float));
     for (int c = 0; c < C; c++) {
       upload(U.ptr, rec.proj.data() + static_cast<size_t>(c) * d * w, U.size, s);
       upload(sh.ptr, rec.shift.data() + static_cast<size_t>(c) * w, sh.size, s);
       project_rows(xd, n, static_cast<int>(d), ix.mean.as<float>(), U.as<float>(), sh.as<float>(), w, y.as<float>(), s);
+      if (ivf_lists) ivf.build(y.as<float>(), n, w, nlist, train_fraction, 20, s);
       std::vector<dbuf> level_lists(L);
       level_keys[c].resize(L);
       int64_t row = 0;
@@ -624,7 +634,7 @@ auto build_in_memory(index_params const& params, dataset_view const& x, build_re
         const int mc = (params.min_cell > 1 && j < L - 1) ? params.min_cell : 1;
         int* offs    = ix.offsets.as<int32_t>() + (static_cast<int64_t>(c) * L + j) * (T + 1);
         int64_t M    = cb.level(y.as<float>(), b, params.spacings[j], mc, l, params.log_buckets, exact_lists, offs,
-                                level_keys[c][j], level_lists[j]);
+                                level_keys[c][j], level_lists[j], ivf_lists ? &ivf : nullptr, params.list_probes);
         rec.base[static_cast<size_t>(c) * L + j]  = static_cast<int32_t>(row);
         rec.cells[static_cast<size_t>(c) * L + j] = M;
         row += M;

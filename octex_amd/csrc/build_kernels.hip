@@ -12,6 +12,7 @@
 #include <rocprim/device/device_radix_sort.hpp>
 #include <rocprim/device/device_scan.hpp>
 
+#include <algorithm>
 #include <cstdint>
 #include <type_traits>
 
@@ -563,6 +564,176 @@ __global__ __launch_bounds__(256) void knn_kernel(const T* __restrict__ Q, const
   }
 }
 
+// ------------------------------------------------------------------ IVF lists (build_cells.cuh:511-516, 584-596)
+
+/** ys [ns, w] = y [i * step] (the k-means sample). */
+__global__ void take_rows_kernel(const float* __restrict__ y, int64_t ns, int64_t step, int w, float* __restrict__ ys)
+{
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= ns * w) return;
+  const int64_t i = t / w, k = t - i * w;
+  ys[t] = y[i * step * w + k];
+}
+
+/** yc [n, w] = y [rows[i]] (the rows grouped by center). */
+__global__ void permute_rows_kernel(const float* __restrict__ y, const int* __restrict__ rows, int64_t n, int w,
+                                    float* __restrict__ yc)
+{
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= n * w) return;
+  const int64_t i = t / w, k = t - i * w;
+  yc[t] = y[static_cast<int64_t>(rows[i]) * w + k];
+}
+
+__global__ void iota_kernel(int* __restrict__ v, int64_t n)
+{
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t < n) v[t] = static_cast<int>(t);
+}
+
+__global__ void count_labels_kernel(const int* __restrict__ lab, int64_t n, int* __restrict__ cnt)
+{
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t < n) atomicAdd(&cnt[lab[t]], 1);
+}
+
+/**
+ * centers[c] = the mean of the sample rows sidx[off[c]] .. sidx[off[c + 1] - 1] (one workgroup per center; each of
+ * the 256 / w parts sums every parts-th member in order, the parts are added in order: the same floats on every
+ * run); a center without members keeps its place.
+ */
+__global__ __launch_bounds__(256) void kmeans_update_kernel(const float* __restrict__ ys, int w,
+                                                            const int* __restrict__ sidx, const int* __restrict__ off,
+                                                            float* __restrict__ centers)
+{
+  __shared__ float part[256];
+  const int c = blockIdx.x, t = threadIdx.x, parts = 256 / w;
+  const int k = t % w, pi = t / w;
+  const int a = off[c], b = off[c + 1];
+  float acc = 0.f;
+  if (pi < parts)
+    for (int r = a + pi; r < b; r += parts)
+      acc += ys[static_cast<int64_t>(sidx[r]) * w + k];
+  part[t] = acc;
+  __syncthreads();
+  if (t < w && b > a) {
+    float sum = 0.f;
+    for (int q = 0; q < parts; q++)
+      sum += part[q * w + t];
+    centers[static_cast<int64_t>(c) * w + t] = sum / static_cast<float>(b - a);
+  }
+}
+
+constexpr int kIvfBuf  = 512;   // candidate keys below the threshold, waiting to be merged
+constexpr int kIvfSort = 1024;  // the kept l (<= 128) and the waiting keys, sorted together
+
+/**
+ * The l rows nearest to center z of cell blockIdx.x among the rows of its P probed centers (probe [M, P]; rows of
+ * center c: rows[off[c] .. off[c + 1]), coordinates in yc): every candidate's key (fp32 squared distance, summed in
+ * coordinate order, then row) is computed by one thread; keys below the current l-th are appended to an LDS buffer,
+ * which is merged into the kept l by a bitonic sort whenever the next round could overflow it, and at the end.
+ */
+__global__ __launch_bounds__(256) void ivf_scan_kernel(const float* __restrict__ z, int w, const int* __restrict__ probe,
+                                                       int P, const int* __restrict__ off, const int* __restrict__ rows,
+                                                       const float* __restrict__ yc, int l, int* __restrict__ out)
+{
+  __shared__ float zs[kMaxW];
+  __shared__ int pre[129], pc[128];
+  __shared__ unsigned long long keys[kIvfSort];
+  __shared__ int nbuf, nkept;
+  __shared__ unsigned long long thr;
+  const int64_t cell = blockIdx.x;
+  const int t = threadIdx.x;
+  constexpr unsigned long long kNone = ~0ULL;
+  for (int k = t; k < w; k += blockDim.x)
+    zs[k] = z[cell * w + k];
+  if (t < 64) {  // wavefront 0: the probed centers and the exclusive prefix of their sizes
+    int carry = 0;
+    for (int p0 = 0; p0 < P; p0 += 64) {
+      const int p  = p0 + t;
+      const int c  = p < P ? probe[cell * P + p] : -1;
+      const int sz = c >= 0 ? off[c + 1] - off[c] : 0;
+      int v        = sz;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int u = __shfl_up(v, d);
+        if (t >= d) v += u;
+      }
+      if (p < P) {
+        pc[p]  = c;
+        pre[p] = carry + v - sz;
+      }
+      carry += __shfl(v, 63);
+    }
+    if (t == 0) {
+      pre[P] = carry;
+      nbuf   = 0;
+      nkept  = 0;
+      thr    = kNone;
+    }
+  }
+  __syncthreads();
+  const int total = pre[P];
+  auto merge = [&]() {  // keys[0, nkept) kept (sorted), keys[kIvfSort - kIvfBuf, + nbuf) waiting
+    const int nk = nkept, nb = nbuf;
+    for (int i = t; i < kIvfSort; i += blockDim.x)
+      if (i >= nk && i < kIvfSort - kIvfBuf) keys[i] = kNone;
+      else if (i >= kIvfSort - kIvfBuf + nb) keys[i] = kNone;
+    __syncthreads();
+    for (int size = 2; size <= kIvfSort; size <<= 1)
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        for (int i = t; i < kIvfSort / 2; i += blockDim.x) {
+          const int lo = 2 * i - (i & (stride - 1));  // the pair (lo, lo + stride)
+          const int hi = lo + stride;
+          const bool up = (lo & size) == 0;
+          const unsigned long long a = keys[lo], b = keys[hi];
+          if ((a > b) == up) {
+            keys[lo] = b;
+            keys[hi] = a;
+          }
+        }
+        __syncthreads();
+      }
+    if (t == 0) {
+      int m = 0;
+      while (m < l && keys[m] != kNone)
+        m++;
+      nkept = m;
+      nbuf  = 0;
+      thr   = m == l ? keys[l - 1] : kNone;
+    }
+    __syncthreads();
+  };
+  for (int base = 0; base < total; base += blockDim.x) {
+    const int i = base + t;
+    if (i < total) {
+      int lo = 0, hi = P - 1;  // the last probe whose prefix is <= i
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (pre[mid] <= i)
+          lo = mid;
+        else
+          hi = mid - 1;
+      }
+      const int64_t j = off[pc[lo]] + (i - pre[lo]);
+      const float* r  = yc + j * w;
+      float acc       = 0.f;
+      for (int k = 0; k < w; k++) {
+        const float u = r[k] - zs[k];
+        acc           = fmaf(u, u, acc);
+      }
+      const unsigned long long key =
+        (static_cast<unsigned long long>(__float_as_uint(acc)) << 32) | static_cast<unsigned>(rows[j]);
+      if (key < thr) keys[kIvfSort - kIvfBuf + atomicAdd(&nbuf, 1)] = key;
+    }
+    __syncthreads();
+    if (nbuf > kIvfBuf - static_cast<int>(blockDim.x)) merge();  // the next round could overflow the buffer
+  }
+  if (nbuf > 0) merge();
+  for (int k = t; k < l; k += blockDim.x)
+    out[cell * l + k] = k < nkept ? static_cast<int>(keys[k] & 0xffffffffULL) : -1;
+}
+
 template <typename T>
 void ensure(dbuf& b, int64_t count)
 {
@@ -720,8 +891,9 @@ void cell_builder::reserve(int64_t n_, int w_, hipStream_t s_)
 }
 
 auto cell_builder::level(const float* y, int B, float f, int min_cell, int l, int log_buckets, bool exact,
-                         int* offs_out, dbuf& keys_out, dbuf& lists_out) -> int64_t
+                         int* offs_out, dbuf& keys_out, dbuf& lists_out, ivf_index* ivf, int probes) -> int64_t
 {
+  const bool member = !exact && ivf == nullptr;
   const int64_t T = int64_t{1} << log_buckets;
   auto g          = grid_for(n, 256);
   switch (B) {
@@ -777,7 +949,7 @@ auto cell_builder::level(const float* y, int B, float f, int min_cell, int l, in
 #undef OCTEX_CENTER
     }
   }
-  if (!exact) {
+  if (member) {
     member_key_kernel<<<g, 256, 0, s>>>(y, w, sidx.as<int>(), rid.as<int>(), keep.as<int>(), kidx.as<int>(),
                                         z.as<float>(), n, mkey.as<unsigned long long>());
     with_tmp(tmp, [&](void* p, size_t& b) {
@@ -797,7 +969,11 @@ auto cell_builder::level(const float* y, int B, float f, int min_cell, int l, in
   keys_out  = dbuf(static_cast<size_t>(std::max(M, 1)) * sizeof(long long));
   lists_out = dbuf(static_cast<size_t>(std::max<int64_t>(int64_t{M} * l, 1)) * sizeof(int));
   if (M > 0) {
-    if (exact) {  // the l projected rows nearest to each center, by brute force (build_cells.cuh:506-510, 567-599)
+    if (ivf != nullptr) {  // the l rows nearest to each center among its probed IVF lists (build_cells.cuh:584-596)
+      ensure<float>(znorm, M);
+      row_norms<float>(z.as<float>(), M, w, znorm.as<float>(), s);
+      ivf->lists(z.as<float>(), znorm.as<float>(), M, probes, l, lists_tmp.as<int>(), s);
+    } else if (exact) {  // the l projected rows nearest to each center, by brute force (build_cells.cuh:506-510, 567-599)
       ensure<float>(ynorm, n);
       ensure<float>(znorm, M);
       ensure<float>(kdist, static_cast<int64_t>(M) * l);
@@ -823,6 +999,82 @@ auto cell_builder::level(const float* y, int B, float f, int min_cell, int l, in
   OCTEX_HIP(hipGetLastError());
   OCTEX_HIP(hipStreamSynchronize(s));
   return M;
+}
+
+void ivf_index::build(const float* y, int64_t n_, int w_, int nlist_, double train_fraction, int iters, hipStream_t s)
+{
+  n = n_, w = w_, nlist = static_cast<int>(std::min<int64_t>(nlist_, n_));
+  OCTEX_EXPECTS(nlist >= 1 && w >= 1 && w <= kMaxW, "octex: IVF lists need rows of at most %d coordinates", kMaxW);
+  // the sample: every step-th row, about train_fraction of them and at least nlist
+  const int64_t want = std::max<int64_t>(nlist, static_cast<int64_t>(static_cast<double>(n) * train_fraction));
+  const int64_t step = std::max<int64_t>(1, n / std::max<int64_t>(want, 1));
+  const int64_t ns   = (n + step - 1) / step;
+  ensure<float>(ys, ns * w);
+  ensure<float>(ysn, ns);
+  ensure<float>(centers, int64_t{nlist} * w);
+  ensure<float>(cnorm, nlist);
+  ensure<int>(off, nlist + 1);
+  ensure<int>(cnt, nlist + 1);
+  take_rows_kernel<<<grid_for(ns * w, 256), 256, 0, s>>>(y, ns, step, w, ys.as<float>());
+  row_norms<float>(ys.as<float>(), ns, w, ysn.as<float>(), s);
+  // the first centers: evenly spaced sample rows
+  take_rows_kernel<<<grid_for(int64_t{nlist} * w, 256), 256, 0, s>>>(ys.as<float>(), nlist, ns / nlist, w,
+                                                                      centers.as<float>());
+  const int bits = log2_ceil(nlist) + 1;
+  auto group = [&](int64_t m) {  // sidx: 0 .. m-1 ordered by lab (stable), off: CSR of the labels
+    ensure<int>(idx, m);
+    ensure<int>(sidx, m);
+    ensure<int>(slab, m);
+    iota_kernel<<<grid_for(m, 256), 256, 0, s>>>(idx.as<int>(), m);
+    with_tmp(tmp, [&](void* p, size_t& b) {
+      return rocprim::radix_sort_pairs(p, b, lab.as<int>(), slab.as<int>(), idx.as<int>(), sidx.as<int>(),
+                                       static_cast<unsigned>(m), 0, bits, s);
+    });
+    OCTEX_HIP(hipMemsetAsync(cnt.ptr, 0, static_cast<size_t>(nlist + 1) * sizeof(int), s));
+    count_labels_kernel<<<grid_for(m, 256), 256, 0, s>>>(lab.as<int>(), m, cnt.as<int>());
+    with_tmp(tmp, [&](void* p, size_t& b) {
+      return rocprim::exclusive_scan(p, b, cnt.as<int>(), off.as<int>(), 0, nlist + 1, rocprim::plus<int>(), s);
+    });
+  };
+  auto assign = [&](const float* q, const float* qn, int64_t m) {  // lab [m]: the nearest center of every row
+    ensure<int>(lab, m);
+    ensure<float>(dtmp, m);
+    row_norms<float>(centers.as<float>(), nlist, w, cnorm.as<float>(), s);
+    knn_rows<float>(q, qn, m, centers.as<float>(), cnorm.as<float>(), nlist, w, 1, dtmp.as<float>(), lab.as<int>(),
+                    s);
+  };
+  for (int it = 0; it < iters; it++) {
+    assign(ys.as<float>(), ysn.as<float>(), ns);
+    group(ns);
+    kmeans_update_kernel<<<nlist, 256, 0, s>>>(ys.as<float>(), w, sidx.as<int>(), off.as<int>(), centers.as<float>());
+    OCTEX_HIP(hipGetLastError());
+  }
+  // every row to its nearest center, the rows grouped by center
+  ensure<float>(yn, n);
+  row_norms<float>(y, n, w, yn.as<float>(), s);
+  assign(y, yn.as<float>(), n);
+  group(n);
+  rows = dbuf(static_cast<size_t>(n) * sizeof(int));
+  OCTEX_HIP(hipMemcpyAsync(rows.ptr, sidx.ptr, rows.size, hipMemcpyDeviceToDevice, s));
+  yc = dbuf(static_cast<size_t>(n) * w * sizeof(float));
+  permute_rows_kernel<<<grid_for(n * w, 256), 256, 0, s>>>(y, rows.as<int>(), n, w, yc.as<float>());
+  row_norms<float>(centers.as<float>(), nlist, w, cnorm.as<float>(), s);
+  OCTEX_HIP(hipGetLastError());
+  OCTEX_HIP(hipStreamSynchronize(s));
+}
+
+void ivf_index::lists(const float* z, const float* zn, int64_t M, int probes, int l, int* out, hipStream_t s)
+{
+  OCTEX_EXPECTS(l >= 1 && l <= 128, "octex: IVF lists take list_len <= 128");
+  if (M == 0) return;
+  const int P = std::max(1, std::min({probes, nlist, 128}));
+  ensure<float>(pd, M * P);
+  ensure<int>(pidx, M * P);
+  knn_rows<float>(z, zn, M, centers.as<float>(), cnorm.as<float>(), nlist, w, P, pd.as<float>(), pidx.as<int>(), s);
+  OCTEX_EXPECTS(M < (int64_t{1} << 31), "octex: too many cells for one launch");
+  ivf_scan_kernel<<<static_cast<unsigned>(M), 256, 0, s>>>(z, w, pidx.as<int>(), P, off.as<int>(), rows.as<int>(),
+                                                           yc.as<float>(), l, out);
+  OCTEX_HIP(hipGetLastError());
 }
 
 }  // namespace cuvs::neighbors::octex::detail

@@ -36,6 +36,30 @@ void float_to_half(const float* x, int64_t total, __half* out, hipStream_t s);
 void make_sketch(const __half* x, int64_t n, int d, const float* mean, const float* basis, int S, int pitch,
                  std::vector<float>& scale, signed char* codes, hipStream_t s);
 
+/**
+ * An IVF index of one copy's projected rows y [n, w], for the reference's default cell lists (build_cells.cuh:511-516,
+ * 584-596: cuVS ivf_flat with max(64, 4 sqrt(n)) lists trained on half the rows, a tenth above 4M, searched with
+ * list_probes probes).  cuVS is not part of this build: the centers here are Lloyd k-means over an evenly spaced
+ * sample (the first centers evenly spaced sample rows; a center keeps its place when no row is nearest to it), each
+ * row's nearest center by the exact k-NN kernel, the sums of a center's rows in row order (the same centers on every
+ * run).  The rows are kept grouped by center (yc, in the order rows[]).
+ */
+struct ivf_index {
+  int64_t n = 0;
+  int w = 0, nlist = 0;
+  dbuf centers, cnorm, off, rows, yc;
+  dbuf ys, ysn, yn, lab, slab, idx, sidx, cnt, dtmp, pd, pidx, tmp;
+
+  /** k-means of `iters` rounds over the rows y[i * step] (about train_fraction of them, at least nlist). */
+  void build(const float* y, int64_t n, int w, int nlist, double train_fraction, int iters, hipStream_t s);
+  /**
+   * out [M, l] (device): for each center z [M, w] (squared norms zn), the l rows nearest to it, by (fp32 squared
+   * distance summed in coordinate order, row), among the rows of its `probes` nearest centers (at most 128),
+   * -1 past the rows there are (l <= 128).
+   */
+  void lists(const float* z, const float* zn, int64_t M, int probes, int l, int* out, hipStream_t s);
+};
+
 /** Scratch of the cells of one level of one copy (reused across levels and copies). */
 struct cell_builder {
   int64_t n     = 0;
@@ -49,11 +73,12 @@ struct cell_builder {
   /**
    * The cells of the projected rows y [n, w] at spacing f: cells of at least min_cell rows, each with
    * the list of its l members nearest to its center (the nearest repeated when fewer), or with
-   * `exact` the l rows nearest to its center among all n (ties by row), in (bucket, id) order.  offs_out [T + 1] (device) receives the CSR over the buckets, keys_out / lists_out
-   * the ids and list rows.  Returns the number of cells.
+   * `exact` the l rows nearest to its center among all n (ties by row), or with `ivf` the l rows of ivf->lists
+   * (probes probes), in (bucket, id) order.  offs_out [T + 1] (device) receives the CSR over the buckets, keys_out /
+   * lists_out the ids and list rows.  Returns the number of cells.
    */
   auto level(const float* y, int B, float f, int min_cell, int l, int log_buckets, bool exact, int* offs_out,
-             dbuf& keys_out, dbuf& lists_out) -> int64_t;
+             dbuf& keys_out, dbuf& lists_out, ivf_index* ivf = nullptr, int probes = 0) -> int64_t;
 };
 
 }  // namespace cuvs::neighbors::octex::detail

@@ -1639,7 +1639,8 @@ void launch_probe(const __half* Y, int m, int C, int L, int B, const float* inv_
   if (tot == 0) return;
   OCTEX_EXPECTS(T1 == (int64_t{1} << logT) + 1, "octex: offsets rows must hold 2^log_buckets + 1 entries");
   OCTEX_EXPECTS(L >= 1, "octex: at least one spacing");
-  // items per wavefront: about 16 wavefronts per CU over the whole grid, at least one item per lane
+  // items per wavefront: about 24 wavefronts per CU over the whole grid (6 per SIMD, what the registers allow; 16
+  // and 32 measured slower), at least one item per lane
   static const int cus = [] {
     int dev = 0, n = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
@@ -1647,7 +1648,7 @@ void launch_probe(const __half* Y, int m, int C, int L, int B, const float* inv_
       n = 256;
     return n;
   }();
-  const int64_t chunk = std::max<int64_t>(64, (tot + int64_t{16} * cus - 1) / (int64_t{16} * cus));
+  const int64_t chunk = std::max<int64_t>(64, (tot + int64_t{24} * cus - 1) / (int64_t{24} * cus));
   const int64_t waves = (tot + chunk - 1) / chunk;
   auto g              = grid_for(waves * 64, 256);
 #define OCTEX_PROBE(b) \

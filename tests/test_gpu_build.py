@@ -56,17 +56,16 @@ def test_build_writes_directory(built, data):
     assert np.array_equal(np.load(os.path.join(path, "vectors.npy")), X.astype(np.float16))
 
 
-def test_cells_and_lists(built, data):
-    """Keys in (bucket, id) order with CSR offsets; every list entry a member of its cell (its projection hashes
-    to the cell's id), nearest to the cell center first; the table holds no self or out-of-range ids."""
-    _, path = built
+def check_cells_and_lists(path, X, copies, members):
+    """Keys in (bucket, id) order with CSR offsets, cells of at least min_cell (4) rows; list entries valid distinct
+    rows, and with `members` every entry a member of its cell (its projection hashes to the cell's id); the table
+    holds no self or out-of-range ids."""
     ix = O.Index(path)
-    X = data[0]
     T = 2 ** ix.log_buckets
     cells = np.load(os.path.join(path, "cells.npy"))
     Xh = X.astype(np.float16).astype(np.float32)
     hits = total = 0
-    for c in (0, 17, 63):
+    for c in copies:
         proj = np.load(os.path.join(path, "proj.npy"))[c]
         shift = np.load(os.path.join(path, "shift.npy"))[c]
         y = ((Xh - ix.mean) @ proj + shift).astype(np.float32)
@@ -79,14 +78,31 @@ def test_cells_and_lists(built, data):
             _, h = O.e8_batch(y / np.float32(f), ix.blocks, 1.0)
             r0 = ix.base[c, j]
             rows = ix.lists[c, r0 * ix.list_len : (r0 + M) * ix.list_len].reshape(M, ix.list_len)
+            assert (rows >= 0).all() and (rows < len(X)).all()
+            if not members:
+                assert all(len(set(r)) == ix.list_len for r in rows[:: max(1, M // 50)].tolist())
             hits += (h[rows] == keys[:, None]).sum()
             total += rows.size
             if j < len(ix.spacings) - 1:
                 counts = np.bincount(np.searchsorted(np.sort(keys), h[np.isin(h, keys)]), minlength=M)
                 assert counts.min() >= 4  # min_cell
-    assert hits / total > 0.99
+    if members:
+        assert hits / total > 0.99
     tab = ix.table
     assert (tab < len(X)).all() and (tab != np.arange(len(X))[:, None]).all()
+
+
+def test_cells_and_lists(built, data):
+    """The default build (IVF lists): cells, CSR and lists of valid distinct rows."""
+    check_cells_and_lists(built[1], data[0], (0, 17, 63), members=False)
+
+
+def test_member_lists_hold_members(octex, data, tmp_path):
+    """member_lists: every list entry a member of its cell, nearest to the cell center first."""
+    X = data[0]
+    path = str(tmp_path / "members")
+    octex.build(X, path, copies=8, seed=1, log_buckets=16, min_cell=4, member_lists=True)
+    check_cells_and_lists(path, X, (0, 3, 7), members=True)
 
 
 def test_build_recall(built, data):
@@ -225,6 +241,32 @@ def test_exact_lists(octex, tmp_path):
     path = str(tmp_path / "ex")
     octex.build(X, path, copies=2, list_len=16, table_len=8, log_buckets=10, exact_lists=True, seed=5)
     assert check_exact_lists(path, X) > 50
+
+
+def test_ivf_lists_probing_every_list_are_exact(octex, tmp_path):
+    """The default lists (IVF, build_cells.cuh:511-516, 584-596) with every k-means list probed: each cell's list is
+    the l rows nearest to its center among all rows (1,000 rows: max(64, 4 sqrt(n)) = 126 lists, list_probes 200)."""
+    from test_oracle import check_exact_lists
+
+    X, _ = clustered(n=1000, m=10, d=32, clusters=10, seed=9)
+    path = str(tmp_path / "ivf_all")
+    octex.build(X, path, copies=2, list_len=16, table_len=8, log_buckets=10, list_probes=200, seed=5)
+    assert check_exact_lists(path, X) > 50
+
+
+def test_ivf_lists_default_probes(octex, tmp_path):
+    """The default lists with the default 16 probes of 565 lists (20,000 rows): l distinct rows per cell, most of
+    them among the l nearest to the cell's center, and the same index on every build (the k-means sums and the list
+    merges run in a fixed order)."""
+    from test_oracle import check_exact_lists
+
+    X, Q = clustered(n=20_000, m=100, d=32, clusters=40, seed=10)
+    path = str(tmp_path / "ivf16")
+    octex.build(X, path, copies=2, list_len=16, table_len=16, log_buckets=12, seed=5)
+    assert check_exact_lists(path, X, stride=20, fraction=True) > 0.9
+    again = str(tmp_path / "ivf16b")
+    octex.build(X, again, copies=2, list_len=16, table_len=16, log_buckets=12, seed=5)
+    assert np.array_equal(np.load(os.path.join(path, "lists.npy")), np.load(os.path.join(again, "lists.npy")))
 
 
 def test_exact_table_reference_rule(octex, tmp_path):
