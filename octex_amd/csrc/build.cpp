@@ -375,7 +375,7 @@ void exact_table(index_impl& ix, int k, bool reverse_edges, std::vector<int32_t>
   OCTEX_EXPECTS(k + 1 <= 128, "octex: the exact neighbor table takes table_len <= 127");
   const int K = k + 1;
   hipStream_t s = ix.stream;
-  const __half* xd = ix.vectors.as<__half>();
+  const __half* xd = ix.vecs();
   dbuf norms(static_cast<size_t>(n) * sizeof(float));
   row_norms(xd, n, static_cast<int>(d), norms.as<float>(), s);
   const int64_t chunk = std::min<int64_t>(n, int64_t{1} << 18);
@@ -460,7 +460,7 @@ void searched_table(index_impl& ix, index const& idx, int k, bool reverse_edges,
     sp.waves  = plan[v].waves;
     for (int64_t r0 = 0; r0 < n; r0 += chunk) {
       const int64_t m = std::min(chunk, n - r0);
-      half_to_float(ix.vectors.as<__half>() + r0 * d, m * d, qf.as<float>(), ix.stream);
+      half_to_float(ix.vecs() + r0 * d, m * d, qf.as<float>(), ix.stream);
       search_impl(res, sp, idx, qf.as<float>(), m, d, nb.as<int64_t>(), nd.as<float>(), kq, false, false);
       OCTEX_HIP(hipStreamSynchronize(ix.stream));
       OCTEX_HIP(hipMemcpy(hnb.data(), nb.ptr, sizeof(int64_t) * m * kq, hipMemcpyDeviceToHost));
@@ -545,26 +545,53 @@ auto build_in_memory(index_params const& params, dataset_view const& x, build_re
     t = std::chrono::steady_clock::now();
   };
 
-  // the fp16 vectors: the index's own, read by every step of the build
-  ix.vectors = dbuf(static_cast<size_t>(n) * d * sizeof(__half));
-  ix.bytes += static_cast<int64_t>(ix.vectors.size);
+  // Streamed build (build_cells.cuh:756-1393; OCTEX_BUILD_STREAM=1 forces it): when the whole-projection build's
+  // device arrays (fp16 rows, one copy's fp32 projection, the cell sorts' scratch: about 2d + 4w + 64 bytes a row)
+  // would take more than half of the free device memory, the vectors stay in pinned host memory, every copy's
+  // projection is made in chunks and every level's cells come from each row's cell id and distance to its cell
+  // center (member lists only, like the reference's streamed copies)
+  size_t free_b = 0, total_b = 0;
+  OCTEX_HIP(hipMemGetInfo(&free_b, &total_b));
+  const char* stream_env = std::getenv("OCTEX_BUILD_STREAM");
+  const bool streamed    = (stream_env != nullptr && std::atoi(stream_env) != 0) ||
+                        static_cast<double>(n) * static_cast<double>(2 * d + 4 * w + 64) > 0.5 * static_cast<double>(free_b);
+  OCTEX_EXPECTS(!streamed || params.member_lists,
+                "octex: a dataset this large for the GPU's memory is built streamed, which builds member lists only "
+                "(set member_lists)");
+  if (streamed) build_log("streamed build: vectors in pinned host memory, projections in chunks\n");
+
+  // the fp16 vectors: the index's own, read by every step of the build (pinned host memory when streamed)
+  __half* vdst = nullptr;
+  if (streamed) {
+    ix.host_vectors = hbuf(static_cast<size_t>(n) * d * sizeof(__half));
+    vdst            = static_cast<__half*>(ix.host_vectors.dptr);
+  } else {
+    ix.vectors = dbuf(static_cast<size_t>(n) * d * sizeof(__half));
+    ix.bytes += static_cast<int64_t>(ix.vectors.size);
+    vdst = ix.vectors.as<__half>();
+  }
   if (!x.f32) {
-    OCTEX_HIP(hipMemcpyAsync(ix.vectors.ptr, x.data, ix.vectors.size,
-                             x.device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, s));
+    OCTEX_HIP(hipMemcpyAsync(vdst, x.data, static_cast<size_t>(n) * d * sizeof(__half), hipMemcpyDefault, s));
   } else if (x.device) {
-    float_to_half(static_cast<const float*>(x.data), n * d, ix.vectors.as<__half>(), s);
+    float_to_half(static_cast<const float*>(x.data), n * d, vdst, s);
   } else {  // fp32 rows from the host in pieces, rounded on the GPU
     const int64_t piece = std::min<int64_t>(n * d, int64_t{1} << 26);
     dbuf tmp(static_cast<size_t>(piece) * sizeof(float));
     for (int64_t o = 0; o < n * d; o += piece) {  // tmp is rewritten only after the previous piece's kernel
       const int64_t m = std::min(piece, n * d - o);
       upload(tmp.ptr, static_cast<const float*>(x.data) + o, m * sizeof(float), s);
-      float_to_half(tmp.as<float>(), m, ix.vectors.as<__half>() + o, s);
+      float_to_half(tmp.as<float>(), m, vdst + o, s);
       OCTEX_HIP(hipStreamSynchronize(s));
     }
   }
   OCTEX_HIP(hipStreamSynchronize(s));
-  const __half* xd = ix.vectors.as<__half>();
+  const __half* xd = ix.vecs();
+  row_source rsrc;
+  rsrc.d = static_cast<int>(d);
+  if (streamed)
+    rsrc.host = static_cast<const __half*>(ix.host_vectors.ptr);
+  else
+    rsrc.dev = xd;
 
   // PCA of a sample (build_setup.cuh:40-103): every step-th row
   const int64_t step = std::max<int64_t>(1, n / 200000), ns = (n + step - 1) / step;
@@ -614,30 +641,64 @@ auto build_in_memory(index_params const& params, dataset_view const& x, build_re
   ix.list_rows.resize(C);
   {
     cell_builder cb;
-    cb.reserve(n, w, s);
+    cb.reserve(n, w, s, !streamed);
     ivf_index ivf;
     // the reference's IVF parameters (build_cells.cuh:513-515): max(64, 4 sqrt(n)) lists, trained on half the rows
     // up to 4M rows, a tenth above; 20 rounds of k-means (cuVS's default)
     const int nlist = static_cast<int>(std::max<int64_t>(64, static_cast<int64_t>(4 * std::sqrt(static_cast<double>(n)))));
     const double train_fraction = n <= 4000000 ? 0.5 : 0.1;
-    dbuf y(static_cast<size_t>(n) * w * sizeof(float)), U(static_cast<size_t>(d) * w * sizeof(float)),
+    // streamed: rows per projected chunk, and levels per pass over the rows (12 bytes a row per level: cell id and
+    // distance), within a quarter of the free memory
+    const int64_t chunk = std::min<int64_t>(n, int64_t{1} << 22);
+    int lpp             = L;
+    if (streamed) {
+      size_t fr = 0, tot = 0;
+      OCTEX_HIP(hipMemGetInfo(&fr, &tot));
+      lpp = static_cast<int>(std::clamp<int64_t>(static_cast<int64_t>(fr / 4) / (n * 12), 1, L));
+      build_log("streamed build: %d levels per pass over the rows\n", lpp);
+    }
+    dbuf y(static_cast<size_t>(streamed ? chunk : n) * w * sizeof(float)), U(static_cast<size_t>(d) * w * sizeof(float)),
       sh(w * sizeof(float));
+    std::vector<dbuf> skey(streamed ? lpp : 0), sdist(streamed ? lpp : 0);
+    for (auto& v : skey)
+      v = dbuf(static_cast<size_t>(n) * sizeof(long long));
+    for (auto& v : sdist)
+      v = dbuf(static_cast<size_t>(n) * sizeof(float));
     for (int c = 0; c < C; c++) {
       upload(U.ptr, rec.proj.data() + static_cast<size_t>(c) * d * w, U.size, s);
       upload(sh.ptr, rec.shift.data() + static_cast<size_t>(c) * w, sh.size, s);
-      project_rows(xd, n, static_cast<int>(d), ix.mean.as<float>(), U.as<float>(), sh.as<float>(), w, y.as<float>(), s);
-      if (ivf_lists) ivf.build(y.as<float>(), n, w, nlist, train_fraction, 20, s);
+      if (!streamed) {
+        project_rows(xd, n, static_cast<int>(d), ix.mean.as<float>(), U.as<float>(), sh.as<float>(), w, y.as<float>(),
+                     s);
+        if (ivf_lists) ivf.build(y.as<float>(), n, w, nlist, train_fraction, 20, s);
+      }
       std::vector<dbuf> level_lists(L);
       level_keys[c].resize(L);
       int64_t row = 0;
-      for (int j = 0; j < L; j++) {
-        const int mc = (params.min_cell > 1 && j < L - 1) ? params.min_cell : 1;
-        int* offs    = ix.offsets.as<int32_t>() + (static_cast<int64_t>(c) * L + j) * (T + 1);
-        int64_t M    = cb.level(y.as<float>(), b, params.spacings[j], mc, l, params.log_buckets, exact_lists, offs,
-                                level_keys[c][j], level_lists[j], ivf_lists ? &ivf : nullptr, params.list_probes);
-        rec.base[static_cast<size_t>(c) * L + j]  = static_cast<int32_t>(row);
-        rec.cells[static_cast<size_t>(c) * L + j] = M;
-        row += M;
+      for (int j0 = 0; j0 < L; j0 += lpp) {
+        const int j1 = std::min(L, j0 + lpp);
+        if (streamed)  // one pass over the rows: every row's cell id and center distance at levels j0 .. j1 - 1
+          for (int64_t r0 = 0; r0 < n; r0 += chunk) {
+            const int64_t m = std::min(chunk, n - r0);
+            project_rows(rsrc.rows(r0, m, s), m, static_cast<int>(d), ix.mean.as<float>(), U.as<float>(),
+                         sh.as<float>(), w, y.as<float>(), s);
+            for (int j = j0; j < j1; j++)
+              stream_keys(y.as<float>(), m, b, params.spacings[j], skey[j - j0].as<long long>() + r0,
+                          sdist[j - j0].as<float>() + r0, s);
+          }
+        for (int j = j0; j < j1; j++) {
+          const int mc = (params.min_cell > 1 && j < L - 1) ? params.min_cell : 1;
+          int* offs    = ix.offsets.as<int32_t>() + (static_cast<int64_t>(c) * L + j) * (T + 1);
+          int64_t M    = streamed
+                           ? cb.level_streamed(skey[j - j0].as<long long>(), sdist[j - j0].as<float>(), mc, l,
+                                               params.log_buckets, offs, level_keys[c][j], level_lists[j])
+                           : cb.level(y.as<float>(), b, params.spacings[j], mc, l, params.log_buckets, exact_lists,
+                                      offs, level_keys[c][j], level_lists[j], ivf_lists ? &ivf : nullptr,
+                                      params.list_probes);
+          rec.base[static_cast<size_t>(c) * L + j]  = static_cast<int32_t>(row);
+          rec.cells[static_cast<size_t>(c) * L + j] = M;
+          row += M;
+        }
       }
       OCTEX_EXPECTS(row * l < (int64_t{1} << 31), "octex: a copy holds more than 2^31 list entries");
       ix.list_rows[c]     = row;
@@ -722,7 +783,7 @@ auto build_in_memory(index_params const& params, dataset_view const& x, build_re
   ix.sketch       = dbuf(static_cast<size_t>(n) * ix.sketch_pitch);
   ix.bytes += static_cast<int64_t>(ix.sketch.size);
   upload(ix.basis.ptr, rec.basis.data(), ix.basis.size, s);
-  make_sketch(xd, n, static_cast<int>(d), ix.mean.as<float>(), ix.basis.as<float>(), S, ix.sketch_pitch, rec.scale,
+  make_sketch(rsrc, n, static_cast<int>(d), ix.mean.as<float>(), ix.basis.as<float>(), S, ix.sketch_pitch, rec.scale,
               ix.sketch.as<signed char>(), s);
   ix.scale = dbuf(S * sizeof(float));
   upload(ix.scale.ptr, rec.scale.data(), ix.scale.size, s);
@@ -754,7 +815,7 @@ void put_device(npy_writer& w, const void* p, size_t bytes)
   std::vector<char> h(std::min(bytes, kChunk));
   for (size_t o = 0; o < bytes; o += kChunk) {
     const size_t m = std::min(kChunk, bytes - o);
-    OCTEX_HIP(hipMemcpy(h.data(), static_cast<const char*>(p) + o, m, hipMemcpyDeviceToHost));
+    OCTEX_HIP(hipMemcpy(h.data(), static_cast<const char*>(p) + o, m, hipMemcpyDefault));  // device or pinned host
     w.put(h.data(), m);
   }
 }
@@ -823,7 +884,8 @@ void write_index(index_impl const& ix, build_record const& rec, index_params con
   }
   {
     npy_writer v(file("vectors.npy"), "<f2", {n, d});
-    put_device(v, ix.vectors.ptr, static_cast<size_t>(n) * d * sizeof(__half));
+    put_device(v, ix.host_vectors.ptr != nullptr ? ix.host_vectors.ptr : ix.vectors.ptr,
+               static_cast<size_t>(n) * d * sizeof(__half));
     v.close();
   }
   if (ix.table_len > 0) {

@@ -109,6 +109,50 @@ __global__ void cell_hash_kernel(const float* __restrict__ y, int64_t n, float f
   idx[i]  = static_cast<int>(i);
 }
 
+/**
+ * The streamed build's per-row quantities at spacing f (build_cells.cuh stream_member_copy): key[i] = the cell id of
+ * y[i] / f, as cell_hash_kernel, and dist[i] = the squared distance of y[i] to its cell's center f * E8(y[i] / f),
+ * as member_key_kernel sums it (every member of a cell has that center).
+ */
+template <int B>
+__global__ void stream_keys_kernel(const float* __restrict__ y, int64_t m, float f, long long* __restrict__ key,
+                                   float* __restrict__ dist)
+{
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= m) return;
+  const float* r = y + i * 8 * B;
+  float x[8 * B], z[8 * B];
+#pragma unroll
+  for (int k = 0; k < 8 * B; k++)
+    x[k] = r[k] / f;
+  key[i] = e8b_hash64<B>(x, 1.0f);
+#pragma unroll
+  for (int j = 0; j < B; j++) {
+    float xb[8], p[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+      xb[k] = x[8 * j + k];
+    e8_point(xb, p);
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+      z[8 * j + k] = p[k] * f;
+  }
+  float dd = 0.f;
+  for (int k = 0; k < 8 * B; k++) {
+    const float e = r[k] - z[k];
+    dd            = fmaf(e, e, dd);
+  }
+  dist[i] = dd;
+}
+
+/** out[i] = key[idx[i]]. */
+__global__ void permute_keys_kernel(const long long* __restrict__ key, const int* __restrict__ idx, int64_t n,
+                                    long long* __restrict__ out)
+{
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = key[idx[i]];
+}
+
 /** flag[i] = 1 where a run of equal sorted keys starts. */
 __global__ void run_flag_kernel(const long long* __restrict__ k, int64_t n, int* __restrict__ flag)
 {
@@ -842,7 +886,16 @@ void float_to_half(const float* x, int64_t total, __half* out, hipStream_t s)
   }
 }
 
-void make_sketch(const __half* x, int64_t n, int d, const float* mean, const float* basis, int S, int pitch,
+auto row_source::rows(int64_t r0, int64_t m, hipStream_t s) -> const __half*
+{
+  if (dev != nullptr) return dev + r0 * d;
+  ensure<__half>(stage, m * d);
+  OCTEX_HIP(hipMemcpyAsync(stage.ptr, host + r0 * d, static_cast<size_t>(m) * d * sizeof(__half),
+                           hipMemcpyHostToDevice, s));
+  return stage.as<__half>();
+}
+
+void make_sketch(row_source& x, int64_t n, int d, const float* mean, const float* basis, int S, int pitch,
                  std::vector<float>& scale, signed char* codes, hipStream_t s)
 {
   const int64_t chunk = std::min<int64_t>(n, int64_t{1} << 22);
@@ -850,7 +903,7 @@ void make_sketch(const __half* x, int64_t n, int d, const float* mean, const flo
   OCTEX_HIP(hipMemsetAsync(amax.ptr, 0, amax.size, s));
   for (int64_t r0 = 0; r0 < n; r0 += chunk) {
     int64_t m = std::min(chunk, n - r0);
-    sketch_project_kernel<<<grid_for(m * S, 256), 256, 0, s>>>(x + r0 * d, m, d, mean, basis, S, v.as<float>(),
+    sketch_project_kernel<<<grid_for(m * S, 256), 256, 0, s>>>(x.rows(r0, m, s), m, d, mean, basis, S, v.as<float>(),
                                                               amax.as<unsigned>());
   }
   std::vector<unsigned> ha(S);
@@ -865,7 +918,7 @@ void make_sketch(const __half* x, int64_t n, int d, const float* mean, const flo
   OCTEX_HIP(hipMemcpyAsync(dscale.ptr, scale.data(), S * sizeof(float), hipMemcpyHostToDevice, s));
   for (int64_t r0 = 0; r0 < n; r0 += chunk) {
     int64_t m = std::min(chunk, n - r0);
-    sketch_project_kernel<<<grid_for(m * S, 256), 256, 0, s>>>(x + r0 * d, m, d, mean, basis, S, v.as<float>(),
+    sketch_project_kernel<<<grid_for(m * S, 256), 256, 0, s>>>(x.rows(r0, m, s), m, d, mean, basis, S, v.as<float>(),
                                                               amax.as<unsigned>());
     quantize_kernel<<<grid_for(m * pitch, 256), 256, 0, s>>>(v.as<float>(), dscale.as<float>(), m, S, pitch,
                                                              codes + r0 * pitch);
@@ -874,7 +927,7 @@ void make_sketch(const __half* x, int64_t n, int d, const float* mean, const flo
   OCTEX_HIP(hipStreamSynchronize(s));
 }
 
-void cell_builder::reserve(int64_t n_, int w_, hipStream_t s_)
+void cell_builder::reserve(int64_t n_, int w_, hipStream_t s_, bool member_keys)
 {
   n = n_;
   w = w_;
@@ -886,8 +939,10 @@ void cell_builder::reserve(int64_t n_, int w_, hipStream_t s_)
   ensure<int>(sidx2, n);
   ensure<int>(rid, n);
   ensure<int>(flag, n);
-  ensure<unsigned long long>(mkey, n);
-  ensure<unsigned long long>(mkey2, n);
+  if (member_keys) {
+    ensure<unsigned long long>(mkey, n);
+    ensure<unsigned long long>(mkey2, n);
+  }
 }
 
 auto cell_builder::level(const float* y, int B, float f, int min_cell, int l, int log_buckets, bool exact,
@@ -985,6 +1040,93 @@ auto cell_builder::level(const float* y, int B, float f, int min_cell, int l, in
       list_fill_kernel<<<grid_for(int64_t{M} * l, 256), 256, 0, s>>>(sidx2.as<int>(), cstart.as<int>(),
                                                                       cpop.as<int>(), M, l, lists_tmp.as<int>());
     }
+    bucket_kernel<<<grid_for(M, 256), 256, 0, s>>>(ckey.as<long long>(), M, T - 1, bucket.as<unsigned>(),
+                                                   seq.as<int>());
+    with_tmp(tmp, [&](void* p, size_t& b) {
+      return rocprim::radix_sort_pairs(p, b, bucket.as<unsigned>(), sbucket.as<unsigned>(), seq.as<int>(),
+                                       perm.as<int>(), M, 0, log_buckets, s);
+    });
+    level_gather_kernel<<<grid_for(int64_t{M} * l, 256), 256, 0, s>>>(ckey.as<long long>(), lists_tmp.as<int>(),
+                                                                       perm.as<int>(), M, l,
+                                                                       keys_out.as<long long>(), lists_out.as<int>());
+  }
+  offsets_kernel<<<grid_for(T + 1, 256), 256, 0, s>>>(sbucket.as<unsigned>(), M, T, offs_out);
+  OCTEX_HIP(hipGetLastError());
+  OCTEX_HIP(hipStreamSynchronize(s));
+  return M;
+}
+
+void stream_keys(const float* y, int64_t m, int B, float f, long long* key, float* dist, hipStream_t s)
+{
+  if (m == 0) return;
+  auto g = grid_for(m, 256);
+  switch (B) {
+#define OCTEX_SK(b) \
+  case b: stream_keys_kernel<b><<<g, 256, 0, s>>>(y, m, f, key, dist); break;
+    OCTEX_SK(1) OCTEX_SK(2) OCTEX_SK(3) OCTEX_SK(4) OCTEX_SK(5) OCTEX_SK(6) OCTEX_SK(8)
+#undef OCTEX_SK
+    default: fail("octex: blocks must be 1-6 or 8");
+  }
+  OCTEX_HIP(hipGetLastError());
+}
+
+auto cell_builder::level_streamed(const long long* key, const float* dist, int min_cell, int l, int log_buckets,
+                                  int* offs_out, dbuf& keys_out, dbuf& lists_out) -> int64_t
+{
+  const int64_t T = int64_t{1} << log_buckets;
+  auto g          = grid_for(n, 256);
+  // rows by distance (stable on the row order), then stably by cell id: each cell's run nearest first, ties by row
+  iota_kernel<<<g, 256, 0, s>>>(idx.as<int>(), n);
+  ensure<float>(kdist, n);
+  with_tmp(tmp, [&](void* p, size_t& b) {
+    return rocprim::radix_sort_pairs(p, b, reinterpret_cast<const unsigned*>(dist), kdist.as<unsigned>(),
+                                     idx.as<int>(), sidx.as<int>(), n, 0, 32, s);
+  });
+  permute_keys_kernel<<<g, 256, 0, s>>>(key, sidx.as<int>(), n, keys.as<long long>());
+  with_tmp(tmp, [&](void* p, size_t& b) {
+    return rocprim::radix_sort_pairs(p, b, keys.as<long long>(), skeys.as<long long>(), sidx.as<int>(),
+                                     sidx2.as<int>(), n, 0, 64, s);
+  });
+  run_flag_kernel<<<g, 256, 0, s>>>(skeys.as<long long>(), n, flag.as<int>());
+  with_tmp(tmp, [&](void* p, size_t& b) {
+    return rocprim::inclusive_scan(p, b, flag.as<int>(), rid.as<int>(), n, rocprim::plus<int>(), s);
+  });
+  int runs = 0;
+  OCTEX_HIP(hipMemcpyAsync(&runs, rid.as<int>() + n - 1, sizeof(int), hipMemcpyDeviceToHost, s));
+  OCTEX_HIP(hipStreamSynchronize(s));
+  ensure<int>(start, runs + 1);
+  ensure<long long>(ukey, runs);
+  ensure<int>(pop, runs);
+  ensure<int>(keep, runs);
+  ensure<int>(kidx, runs);
+  run_start_kernel<<<g, 256, 0, s>>>(skeys.as<long long>(), rid.as<int>(), n, start.as<int>(), ukey.as<long long>());
+  run_keep_kernel<<<grid_for(runs, 256), 256, 0, s>>>(start.as<int>(), runs, n, min_cell, pop.as<int>(),
+                                                      keep.as<int>());
+  with_tmp(tmp, [&](void* p, size_t& b) {
+    return rocprim::exclusive_scan(p, b, keep.as<int>(), kidx.as<int>(), 0, runs, rocprim::plus<int>(), s);
+  });
+  int last[2] = {0, 0};
+  OCTEX_HIP(hipMemcpyAsync(&last[0], kidx.as<int>() + runs - 1, sizeof(int), hipMemcpyDeviceToHost, s));
+  OCTEX_HIP(hipMemcpyAsync(&last[1], keep.as<int>() + runs - 1, sizeof(int), hipMemcpyDeviceToHost, s));
+  OCTEX_HIP(hipStreamSynchronize(s));
+  const int M = last[0] + last[1];
+  ensure<long long>(ckey, M);
+  ensure<int>(cfirst, M);
+  ensure<int>(cpop, M);
+  run_compact_kernel<<<grid_for(runs, 256), 256, 0, s>>>(ukey.as<long long>(), start.as<int>(), pop.as<int>(),
+                                                          keep.as<int>(), kidx.as<int>(), runs, ckey.as<long long>(),
+                                                          cfirst.as<int>(), cpop.as<int>());
+  ensure<int>(lists_tmp, static_cast<int64_t>(M) * l);
+  ensure<unsigned>(bucket, M);
+  ensure<unsigned>(sbucket, M);
+  ensure<int>(seq, M);
+  ensure<int>(perm, M);
+  keys_out  = dbuf(static_cast<size_t>(std::max(M, 1)) * sizeof(long long));
+  lists_out = dbuf(static_cast<size_t>(std::max<int64_t>(int64_t{M} * l, 1)) * sizeof(int));
+  if (M > 0) {
+    // a kept cell's run starts at cfirst in the sorted rows: its first l, the nearest repeated when fewer
+    list_fill_kernel<<<grid_for(int64_t{M} * l, 256), 256, 0, s>>>(sidx2.as<int>(), cfirst.as<int>(), cpop.as<int>(),
+                                                                    M, l, lists_tmp.as<int>());
     bucket_kernel<<<grid_for(M, 256), 256, 0, s>>>(ckey.as<long long>(), M, T - 1, bucket.as<unsigned>(),
                                                    seq.as<int>());
     with_tmp(tmp, [&](void* p, size_t& b) {

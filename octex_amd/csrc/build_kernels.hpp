@@ -32,8 +32,21 @@ void knn_rows(const T* Q, const float* qn, int64_t m, const T* X, const float* x
               float* out_d, int* out_i, hipStream_t s);
 /** out = fp16(x), round to nearest even (device arrays). */
 void float_to_half(const float* x, int64_t total, __half* out, hipStream_t s);
+/**
+ * The dataset's fp16 rows [n, d] for passes in chunks: device rows read in place, or pinned host rows copied chunk by
+ * chunk into a device staging buffer (a chunk's copy is ordered after the kernels of the previous one on s).
+ */
+struct row_source {
+  const __half* dev  = nullptr;
+  const __half* host = nullptr;
+  int d              = 0;
+  dbuf stage;
+  /** Device rows [r0, r0 + m). */
+  auto rows(int64_t r0, int64_t m, hipStream_t s) -> const __half*;
+};
+
 /** The int8 sketch: scale = amax / 127 per coordinate, codes [n, pitch] = round(((x - mean) @ basis) / scale). */
-void make_sketch(const __half* x, int64_t n, int d, const float* mean, const float* basis, int S, int pitch,
+void make_sketch(row_source& x, int64_t n, int d, const float* mean, const float* basis, int S, int pitch,
                  std::vector<float>& scale, signed char* codes, hipStream_t s);
 
 /**
@@ -60,6 +73,9 @@ struct ivf_index {
   void lists(const float* z, const float* zn, int64_t M, int probes, int l, int* out, hipStream_t s);
 };
 
+/** key / dist [m]: the cell id of each row of y [m, 8B] at spacing f and its squared distance to the cell's center. */
+void stream_keys(const float* y, int64_t m, int B, float f, long long* key, float* dist, hipStream_t s);
+
 /** Scratch of the cells of one level of one copy (reused across levels and copies). */
 struct cell_builder {
   int64_t n     = 0;
@@ -69,7 +85,8 @@ struct cell_builder {
   dbuf start, ukey, pop, keep, kidx, ckey, cfirst, cpop, cstart, z, lists_tmp, bucket, sbucket, seq, perm;
   dbuf ynorm, znorm, kdist;
 
-  void reserve(int64_t n, int w, hipStream_t s);
+  /** Scratch for n rows; without member_keys, none for level()'s member sort (the streamed build's levels). */
+  void reserve(int64_t n, int w, hipStream_t s, bool member_keys = true);
   /**
    * The cells of the projected rows y [n, w] at spacing f: cells of at least min_cell rows, each with
    * the list of its l members nearest to its center (the nearest repeated when fewer), or with
@@ -79,6 +96,13 @@ struct cell_builder {
    */
   auto level(const float* y, int B, float f, int min_cell, int l, int log_buckets, bool exact, int* offs_out,
              dbuf& keys_out, dbuf& lists_out, ivf_index* ivf = nullptr, int probes = 0) -> int64_t;
+  /**
+   * The member-list cells of one level from every row's cell id and squared distance to its cell center (key, dist
+   * [n], device; stream_keys): the same cells, keys, lists and offsets as level() with member lists, without the
+   * projected rows.
+   */
+  auto level_streamed(const long long* key, const float* dist, int min_cell, int l, int log_buckets, int* offs_out,
+                      dbuf& keys_out, dbuf& lists_out) -> int64_t;
 };
 
 }  // namespace cuvs::neighbors::octex::detail

@@ -299,3 +299,29 @@ def test_place_on_host_keeps_results(octex, data):
         assert np.array_equal(I0, I1) and np.array_equal(D0, D1)
     idx.place_on_host(vectors=True)  # a second call moves nothing
     assert idx.device_bytes[0] == dev0 - moved
+
+
+def test_streamed_build_equals_in_memory(octex, data, monkeypatch):
+    """The streamed build (build_cells.cuh:756-1393, forced by OCTEX_BUILD_STREAM=1 as in the reference): vectors in
+    pinned host memory, each copy's projection made in chunks, every level's member lists from each row's cell id
+    and distance to its cell center.  It gives the same arrays and search results as the whole-projection build, with
+    the vectors off the device; a streamed build needs member lists."""
+    from octex_amd._lib import OctexError
+
+    X, Q, _ = data
+    X = X[:6000]
+    args = dict(copies=12, seed=7, log_buckets=12, table_len=32, min_cell=3, member_lists=True)
+    mem, _ = octex.build_in_memory(X, **args)
+    monkeypatch.setenv("OCTEX_BUILD_STREAM", "1")
+    st, _ = octex.build_in_memory(X, **args)
+    for name, dt in (("keys", np.int64), ("offsets", np.int32), ("base", np.int32), ("sketch", np.int8),
+                     ("table", np.int32)):
+        assert np.array_equal(mem.array(name, dt), st.array(name, dt)), name
+    for c in range(12):
+        assert np.array_equal(mem.array("lists", np.int32, copy=c), st.array("lists", np.int32, copy=c)), c
+    assert st.device_bytes[0] == mem.device_bytes[0] - len(X) * X.shape[1] * 2
+    p = dict(read=16, starts=64, waves=2)
+    (D0, I0), (D1, I1) = mem.search(Q, k=10, **p), st.search(Q, k=10, **p)
+    assert np.array_equal(I0, I1) and np.array_equal(D0, D1)
+    with pytest.raises(OctexError, match="member lists only"):
+        octex.build_in_memory(X, **dict(args, member_lists=False))
