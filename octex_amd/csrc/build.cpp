@@ -11,6 +11,7 @@
 #include "build_kernels.hpp"
 #include "build.hpp"
 #include "common.hpp"
+#include "directory.hpp"
 #include "index_impl.hpp"
 #include "meta.hpp"
 #include "npy.hpp"
@@ -20,6 +21,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <exception>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
@@ -496,8 +498,8 @@ void searched_table(index_impl& ix, index const& idx, int k, bool reverse_edges,
   }
 }
 
-auto build_in_memory(index_params const& params, dataset_view const& x, build_record& rec)
-  -> std::shared_ptr<index_impl>
+auto build_in_memory(index_params const& params, dataset_view const& x, build_record& rec,
+                     std::function<void(index_impl const&)> const& before_table) -> std::shared_ptr<index_impl>
 {
   const int64_t n = x.n, d = x.d;
   const auto t_all = std::chrono::steady_clock::now();
@@ -789,6 +791,8 @@ auto build_in_memory(index_params const& params, dataset_view const& x, build_re
   upload(ix.scale.ptr, rec.scale.data(), ix.scale.size, s);
   phase("sketch");
 
+  if (before_table) before_table(ix);
+
   // neighbor table: exact up to exact_table_max rows (build.cu:354-360), else searched by this library's search
   if (k > 0) {
     std::vector<int32_t> table;
@@ -838,9 +842,8 @@ void put_device_rows(npy_writer& w, const void* p, int64_t rows, size_t row_byte
   }
 }
 
-}  // namespace
-
-void write_index(index_impl const& ix, build_record const& rec, index_params const& params, std::string const& path)
+/** Every array of the directory but table.npy and meta.json (the arrays final before the neighbor table). */
+void write_arrays(index_impl const& ix, build_record const& rec, index_params const& params, std::string const& path)
 {
   namespace fs = std::filesystem;
   fs::create_directories(path);
@@ -888,30 +891,148 @@ void write_index(index_impl const& ix, build_record const& rec, index_params con
                static_cast<size_t>(n) * d * sizeof(__half));
     v.close();
   }
-  if (ix.table_len > 0) {
-    npy_writer t(file("table.npy"), "<i4", {n, int64_t{ix.table_len}});
-    put_device(t, ix.table.ptr, static_cast<size_t>(n) * ix.table_len * sizeof(int32_t));
-    t.close();
-  }
-  // meta.json last: a directory without it is incomplete (build.cu:67-98, 423-424)
+}
+
+/** The format-1 meta.json text of an index with the given table_len (build.cu:67-98). */
+auto meta_text(index_impl const& ix, index_params const& params, int table_len,
+               std::vector<std::pair<std::string, double>> const& phases) -> std::string
+{
+  const int C = ix.copies, L = ix.levels(), l = ix.list_len, S = ix.sketch_width;
+  const int64_t n = ix.n, d = ix.dim;
   std::ostringstream m;
   m << "{\n \"format\": 1,\n \"n\": " << n << ",\n \"dim\": " << d << ",\n \"copies\": " << C
     << ",\n \"blocks\": " << ix.blocks << ",\n \"spacings\": [";
   for (int j = 0; j < L; j++)
     m << (j ? ", " : "") << json_float(params.spacings[j]);
   m << "],\n \"list_len\": " << l << ",\n \"log_buckets\": " << ix.log_buckets << ",\n \"sketch_width\": " << S
-    << ",\n \"table_len\": " << ix.table_len << ",\n \"metric\": \"sqeuclidean\",\n \"files\": {}";
-  if (!rec.phases.empty()) {
+    << ",\n \"table_len\": " << table_len << ",\n \"metric\": \"sqeuclidean\",\n \"files\": {}";
+  if (!phases.empty()) {
     m << ",\n \"build_seconds\": {";
-    for (size_t i = 0; i < rec.phases.size(); i++) {
+    for (size_t i = 0; i < phases.size(); i++) {
       char buf[64];
-      std::snprintf(buf, sizeof(buf), "%.3f", rec.phases[i].second);
-      m << (i ? ", " : "") << "\"" << rec.phases[i].first << "\": " << buf;
+      std::snprintf(buf, sizeof(buf), "%.3f", phases[i].second);
+      m << (i ? ", " : "") << "\"" << phases[i].first << "\": " << buf;
     }
     m << "}";
   }
   m << "\n}\n";
-  std::ofstream(file("meta.json")) << m.str();
+  return m.str();
+}
+
+/** table.npy, then meta.json last: a directory without meta.json is incomplete (build.cu:67-98, 423-424). */
+void write_table_meta(index_impl const& ix, index_params const& params,
+                      std::vector<std::pair<std::string, double>> const& phases, std::string const& path)
+{
+  namespace fs = std::filesystem;
+  OCTEX_HIP(hipSetDevice(ix.device));
+  if (ix.table_len > 0) {
+    npy_writer t((fs::path(path) / "table.npy").string(), "<i4", {ix.n, int64_t{ix.table_len}});
+    put_device(t, ix.table.ptr, static_cast<size_t>(ix.n) * ix.table_len * sizeof(int32_t));
+    t.close();
+  }
+  std::ofstream((fs::path(path) / "meta.json").string()) << meta_text(ix, params, ix.table_len, phases);
+}
+
+}  // namespace
+
+void write_index(index_impl const& ix, build_record const& rec, index_params const& params, std::string const& path)
+{
+  write_arrays(ix, rec, params, path);
+  write_table_meta(ix, params, rec.phases, path);
+}
+
+namespace {
+
+/** A writer thread that is joined whatever happens: its exception is rethrown by join(). */
+struct writer_thread {
+  std::thread t;
+  std::exception_ptr err;
+  template <typename F>
+  void start(F f)
+  {
+    t = std::thread([this, f] {
+      try {
+        f();
+      } catch (...) {
+        err = std::current_exception();
+      }
+    });
+  }
+  void join()
+  {
+    if (t.joinable()) t.join();
+    if (err) std::rethrow_exception(std::exchange(err, nullptr));
+  }
+  ~writer_thread()
+  {
+    if (t.joinable()) t.join();
+  }
+};
+
+/**
+ * The neighbor table of a directory holding every other array (OCTEX_TABLE_ONLY: build.cu:153-169): the arrays
+ * loaded under a meta.json text made in memory with no table, the table built over them as build_in_memory builds
+ * it, then table.npy and meta.json written.
+ */
+auto resume_table(index_params const& params, dataset_view const& x, std::string const& path, build_record& rec)
+  -> std::shared_ptr<index_impl>
+{
+  namespace fs = std::filesystem;
+  for (const char* f : {"mean.npy", "proj.npy", "shift.npy", "base.npy", "cells.npy", "keys.npy", "offsets.npy",
+                        "lists.npy", "sketch_basis.npy", "sketch_scale.npy", "sketch.npy", "vectors.npy"})
+    OCTEX_EXPECTS(fs::exists(fs::path(path) / f), "octex: OCTEX_TABLE_ONLY needs %s",
+                  (fs::path(path) / f).string().c_str());
+  const auto t0 = std::chrono::steady_clock::now();
+  npy_file basis((fs::path(path) / "sketch_basis.npy").string());
+  npy_file vec((fs::path(path) / "vectors.npy").string());
+  OCTEX_EXPECTS(vec.rank() == 2 && vec.dim(0) == x.n && vec.dim(1) == x.d,
+                "octex: OCTEX_TABLE_ONLY: vectors.npy does not hold the dataset's shape");
+  index_impl shape;  // the fields meta_text reads
+  shape.n = x.n, shape.dim = x.d, shape.copies = params.copies, shape.blocks = params.blocks;
+  shape.list_len = params.list_len, shape.log_buckets = params.log_buckets;
+  shape.sketch_width = static_cast<int>(basis.dim(1));
+  shape.spacings     = params.spacings;
+  load_params lp;
+  auto dir  = open_directory(path, lp, meta_text(shape, params, 0, {}));
+  auto impl = load_directory(dir, path, lp);
+  auto& ix  = *impl;
+  const int k = params.table_len;
+  if (k > 0) {
+    std::vector<int32_t> table;
+    if (x.n <= params.exact_table_max) {
+      exact_table(ix, k, params.reverse_edges, table);
+    } else {
+      index idx(impl);
+      searched_table(ix, idx, k, params.reverse_edges, params.table_passes, params.table_sketch_order, table);
+    }
+    set_table(ix, table, k);
+  }
+  rec.phases.emplace_back("table", seconds_since(t0));
+  build_log("table: %.2f s\n", rec.phases.back().second);
+  write_table_meta(ix, params, rec.phases, path);
+  return impl;
+}
+
+}  // namespace
+
+auto build_to_directory(index_params const& params, dataset_view const& x, std::string const& path,
+                        build_record& rec) -> std::shared_ptr<index_impl>
+{
+  if (const char* e = std::getenv("OCTEX_TABLE_ONLY"); e != nullptr && std::atoi(e) != 0)
+    return resume_table(params, x, path, rec);
+  if (!params.write_behind) {
+    auto impl = build_in_memory(params, x, rec);
+    write_index(*impl, rec, params, path);
+    return impl;
+  }
+  // write_behind (build.cu:146-178): the arrays final before the table go out while the table is built
+  writer_thread w;
+  auto impl = build_in_memory(params, x, rec, [&](index_impl const& ix) {
+    w.start([&ix, &rec, &params, &path] { write_arrays(ix, rec, params, path); });
+  });
+  w.join();
+  write_table_meta(*impl, params, rec.phases, path);
+  return impl;
 }
 
 }  // namespace detail
@@ -921,8 +1042,7 @@ namespace {
 void build_to(index_params const& params, detail::dataset_view const& x, std::string const& path)
 {
   detail::build_record rec;
-  auto impl = detail::build_in_memory(params, x, rec);
-  detail::write_index(*impl, rec, params, path);
+  detail::build_to_directory(params, x, path, rec);
 }
 
 }  // namespace

@@ -334,8 +334,7 @@ extern "C" cuvsError_t cuvsOctexBuild(cuvsResources_t res, cuvsOctexIndexParams_
     (void)as_res(res);
     const auto p = to_cpp(*params);
     octex::detail::build_record rec;
-    auto impl = octex::detail::build_in_memory(p, dataset_of(dataset), rec);
-    octex::detail::write_index(*impl, rec, p, std::string(path));
+    octex::detail::build_to_directory(p, dataset_of(dataset), std::string(path), rec);
   });
 }
 
@@ -449,8 +448,8 @@ extern "C" cuvsError_t octexBuildInMemory(cuvsResources_t res, cuvsOctexIndexPar
     OCTEX_EXPECTS(index->addr == 0, "octex: the index handle already holds an index");
     const auto p = to_cpp(*params);
     octex::detail::build_record rec;
-    auto impl = octex::detail::build_in_memory(p, dataset_of(dataset), rec);
-    if (path != nullptr) octex::detail::write_index(*impl, rec, p, std::string(path));
+    auto impl = path != nullptr ? octex::detail::build_to_directory(p, dataset_of(dataset), std::string(path), rec)
+                                : octex::detail::build_in_memory(p, dataset_of(dataset), rec);
     if (seconds != nullptr) *seconds = rec.phases.empty() ? 0.0 : rec.phases.back().second;
     index->addr = reinterpret_cast<uintptr_t>(new octex::index(impl));
   });

@@ -9,6 +9,7 @@
 
 #include <cstdint>
 #include <map>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -34,5 +35,10 @@ struct directory {
  * "octex: ..." error naming the file on any mismatch; makes no device call.
  */
 auto open_directory(std::string const& path, load_params const& params) -> directory;
+/** open_directory with the text of meta.json given (a build resumed before its meta.json is written). */
+auto open_directory(std::string const& path, load_params const& params, std::string const& meta_text) -> directory;
+/** The index of an opened directory on one GPU (the body of load()). */
+auto load_directory(directory const& dir, std::string const& path, load_params const& params)
+  -> std::shared_ptr<index_impl>;
 
 }  // namespace cuvs::neighbors::octex::detail

@@ -85,10 +85,14 @@ namespace detail {
 
 auto open_directory(std::string const& path, load_params const& params) -> directory
 {
+  return open_directory(path, params, read_text(path + "/meta.json"));
+}
+
+auto open_directory(std::string const& path, load_params const& params, std::string const& text) -> directory
+{
   directory dir;
-  dir.path               = path;
-  const std::string text = read_text(path + "/meta.json");
-  auto meta              = json_parser(text).parse();
+  dir.path  = path;
+  auto meta = json_parser(text).parse();
   OCTEX_EXPECTS(static_cast<int>(meta.number("format", 1)) == 1, "octex: unknown index format");
   auto count = [&](const char* key, double dflt) {
     const double v = meta.number(key, dflt);
@@ -194,6 +198,14 @@ auto load(raft::resources const& res, std::string const& path, load_params const
 {
   (void)res;
   detail::directory dir = detail::open_directory(path, params);  // every check, no device call
+  return index(detail::load_directory(dir, path, params));
+}
+
+namespace {
+
+auto load_opened(detail::directory const& dir, std::string const& path, load_params const& params)
+  -> std::shared_ptr<index_impl>
+{
   int cur = 0;
   OCTEX_HIP(hipGetDevice(&cur));
   auto impl = std::make_shared<index_impl>();
@@ -345,7 +357,15 @@ auto load(raft::resources const& res, std::string const& path, load_params const
   OCTEX_HIP(hipStreamSynchronize(ix.stream));
   ix.list_len = ll;
   OCTEX_HIP(hipSetDevice(cur));
-  return index(impl);
+  return impl;
+}
+
+}  // namespace
+
+auto detail::load_directory(directory const& dir, std::string const& path, load_params const& params)
+  -> std::shared_ptr<index_impl>
+{
+  return load_opened(dir, path, params);
 }
 
 }  // namespace cuvs::neighbors::octex

@@ -325,3 +325,32 @@ def test_streamed_build_equals_in_memory(octex, data, monkeypatch):
     assert np.array_equal(I0, I1) and np.array_equal(D0, D1)
     with pytest.raises(OctexError, match="member lists only"):
         octex.build_in_memory(X, **dict(args, member_lists=False))
+
+
+def test_write_behind_and_table_only_resume(octex, data, tmp_path, monkeypatch):
+    """write_behind (build.cu:146-178): the arrays final before the neighbor table are written while the table is
+    built: the same files as a build without it.  OCTEX_TABLE_ONLY=1 (build.cu:153-169) on a directory that stopped
+    in its table phase (every array but table.npy and meta.json): only the table is built and written, the same
+    table, and the directory loads with the same results."""
+    X, Q, _ = data
+    X = X[:5000]
+    args = dict(copies=8, seed=3, log_buckets=12, table_len=24, min_cell=3, member_lists=True)
+    plain, behind = str(tmp_path / "plain"), str(tmp_path / "behind")
+    octex.build(X, plain, **args)
+    octex.build(X, behind, write_behind=True, **args)
+    names = sorted(f for f in os.listdir(plain) if f.endswith(".npy"))
+    assert names == sorted(f for f in os.listdir(behind) if f.endswith(".npy")) and "table.npy" in names
+    for f in names:
+        assert open(os.path.join(plain, f), "rb").read() == open(os.path.join(behind, f), "rb").read(), f
+    table = np.load(os.path.join(plain, "table.npy"))
+    os.remove(os.path.join(behind, "table.npy"))
+    os.remove(os.path.join(behind, "meta.json"))
+    monkeypatch.setenv("OCTEX_TABLE_ONLY", "1")
+    octex.build(X, behind, **args)
+    monkeypatch.delenv("OCTEX_TABLE_ONLY")
+    assert np.array_equal(np.load(os.path.join(behind, "table.npy")), table)
+    meta = json.load(open(os.path.join(behind, "meta.json")))
+    assert meta["table_len"] == 24 and meta["n"] == len(X) and list(meta["build_seconds"]) == ["table"]
+    p = dict(read=16, starts=32, waves=2)
+    (D0, I0), (D1, I1) = octex.load(plain).search(Q, k=10, **p), octex.load(behind).search(Q, k=10, **p)
+    assert np.array_equal(I0, I1) and np.array_equal(D0, D1)
