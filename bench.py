@@ -428,6 +428,9 @@ def main():
     ap.add_argument("--params", default=None, help="JSON search parameters (skips the sweep)")
     ap.add_argument("--sweep", action="store_true",
                     help="time the fastest sweep point at recall >= 0.99 instead of the workload's fixed point")
+    ap.add_argument("--stream-build", action="store_true",
+                    help="build streamed (OCTEX_BUILD_STREAM=1): vectors in pinned host memory from the start, each "
+                         "copy's projection in chunks (the build a dataset beyond the GPU's memory takes)")
     ap.add_argument("--row-ceiling", action="store_true",
                     help="measure the random-row read ceiling of the GPU instead of a search (no index is built)")
     ap.add_argument("--save-index", default=None, help="also write the built index directory here")
@@ -446,6 +449,8 @@ def main():
 
     # the builder reports its phases on stderr (a 100M build runs for minutes)
     os.environ.setdefault("OCTEX_VERBOSE", "1")
+    if args.stream_build:
+        os.environ["OCTEX_BUILD_STREAM"] = "1"
     import torch
 
     import octex_amd
@@ -606,6 +611,7 @@ def main():
             "distance_max_rel_err": derr,
             "recall_target_met": rec >= 0.99,
             "build_seconds": round(build_s, 1) if build_s is not None else None,
+            "build_streamed": bool(args.stream_build),
             "index_gib": round(index.device_bytes[0] / 2**30, 2),
             "sweep": points,
             "stages": per_launch,

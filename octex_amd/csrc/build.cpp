@@ -781,7 +781,7 @@ auto build_in_memory(index_params const& params, dataset_view const& x, build_re
     for (int sI = 0; sI < S; sI++)
       rec.basis[r * S + sI] = pvec[r * d + sI];
   ix.basis  = dbuf(rec.basis.size() * sizeof(float));
-  ix.sketch_pitch = sketch_pitch_for(S);
+  ix.sketch_pitch = sketch_pitch_for(S, n, device_memory_bytes());
   ix.sketch       = dbuf(static_cast<size_t>(n) * ix.sketch_pitch);
   ix.bytes += static_cast<int64_t>(ix.sketch.size);
   upload(ix.basis.ptr, rec.basis.data(), ix.basis.size, s);

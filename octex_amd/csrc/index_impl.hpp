@@ -34,15 +34,28 @@ struct plan;  // buffers and graph of one (batch, k, search parameters); search.
 /**
  * Bytes between two sketch rows of S codes in memory: the next power of two for S <= 128, else a multiple
  * of 128, so that no row straddles a 128-byte cache line (a 96-byte row at a 96-byte stride touches 1.5
- * lines on average; padded to 128 it touches one).  The directory keeps rows of S bytes.
+ * lines on average; padded to 128 it touches one) -- while the padding of n rows costs at most 1/32 of the
+ * device memory (device_bytes; 0: no limit): a billion rows of 96 codes keep S-byte rows, since their padding
+ * alone would take 32 GB.  The directory keeps rows of S bytes.
  */
-inline auto sketch_pitch_for(int S) -> int
+inline auto sketch_pitch_for(int S, int64_t n = 0, size_t device_bytes = 0) -> int
 {
-  if (S > 128) return (S + 127) / 128 * 128;
   int p = 16;
-  while (p < S)
-    p <<= 1;
+  if (S > 128) {
+    p = (S + 127) / 128 * 128;
+  } else {
+    while (p < S)
+      p <<= 1;
+  }
+  if (device_bytes > 0 && static_cast<double>(n) * (p - S) > static_cast<double>(device_bytes) / 32) return S;
   return p;
+}
+
+/** The device's memory in bytes (0 if it cannot be read). */
+inline auto device_memory_bytes() -> size_t
+{
+  size_t fr = 0, tot = 0;
+  return hipMemGetInfo(&fr, &tot) == hipSuccess ? tot : 0;
 }
 
 struct index_impl {

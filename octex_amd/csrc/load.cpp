@@ -308,7 +308,7 @@ auto load_opened(detail::directory const& dir, std::string const& path, load_par
   ix.mean  = upload(ix, mean.as<float>(), D * sizeof(float));
   ix.basis = upload(ix, basis.as<float>(), D * S * sizeof(float));
   ix.scale = upload(ix, scale.as<float>(), S * sizeof(float));
-  ix.sketch_pitch = detail::sketch_pitch_for(S);
+  ix.sketch_pitch = detail::sketch_pitch_for(S, N, detail::device_memory_bytes());
   if (ix.sketch_pitch == S) {
     const size_t code_bytes = static_cast<size_t>(N * S);
     if (params.sketch == sketch_placement::host) {
