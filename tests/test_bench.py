@@ -35,9 +35,14 @@ def test_stage_bytes_cover_every_stage():
 
 
 def test_measured_traffic_from_the_committed_profile():
-    p = dict(read=12, starts=64, waves=2, rerank=128, wave_rerank=128)
+    """The committed counters are of the workload's fixed point: its line reads them as measured."""
+    import json
+
+    prof = json.load(open(os.path.join(ROOT, "profiles", "traffic_deep100m.json")))
+    p = bench.CONFIGS["deep100m"]["point"]
+    assert all(prof["params"][x] == p[x] for x in ("read", "starts", "waves", "rerank", "wave_rerank"))
     t, src = bench.measured_traffic("deep100m", p, "gather_rows", 100_000_000, 2.5e9)
-    assert t == 3_233_023_976 and "same parameters" in src
+    assert t == prof["kernels"]["gather_rows"]["hbm_bytes_per_launch"] and "same parameters" in src
     t2, src2 = bench.measured_traffic("deep100m", dict(p, read=16), "gather_rows", 100_000_000, 2.5e9)
     assert t2 is not None and "per algorithmic byte" in src2
     assert bench.measured_traffic("sift1m", p, "gather_rows", 1_000_000, 1e9) == (None, None)
