@@ -331,6 +331,132 @@ void merge_reverse(std::vector<int32_t> const& fwd, int64_t n, reverse_rule cons
   });
 }
 
+/** What one copy of a streamed build with exact or IVF lists works with (the projection of copy U, shift). */
+struct stream_copy {
+  row_source* rsrc    = nullptr;
+  const __half* xd    = nullptr;  // the same rows, device-readable (pinned host memory's device alias)
+  int64_t n           = 0;
+  int d = 0, b = 0, l = 0, log_buckets = 0, min_cell = 1, probes = 0, lpp = 1;
+  bool exact          = false;
+  const float *mean = nullptr, *U = nullptr, *shift = nullptr;
+  int64_t chunk       = 0;  // rows of y
+  float* y            = nullptr;
+  std::vector<dbuf>* skey  = nullptr;
+  std::vector<dbuf>* sdist = nullptr;
+};
+
+/**
+ * The exact or IVF lists of one copy without its whole projection on the device (build_cells.cuh:1074-1335).
+ * Every level's cells come from each row's cell id (lpp levels per pass over the rows), each cell's center from its
+ * first row, re-projected.  Then the rows go in ranges: each range is projected once, and the l nearest rows of every
+ * center are found among its rows (brute force, or the range's own IVF index searched with `probes` probes) and
+ * merged into the center's list.  Exact lists come out the same as from one search over all rows; IVF lists from one
+ * range the same as the whole-projection build's.  Level j's arrays go to keys_out[j] / lists_out[j] / offs + j (T + 1);
+ * returns the cells of every level.
+ */
+auto streamed_center_lists(cell_builder& cb, stream_copy const& sc, std::vector<float> const& spacings, int* offs,
+                           std::vector<dbuf>& keys_out, std::vector<dbuf>& lists_out, hipStream_t s)
+  -> std::vector<int64_t>
+{
+  const int L = static_cast<int>(spacings.size()), w = 8 * sc.b, l = sc.l;
+  const int64_t n = sc.n, T1 = (int64_t{1} << sc.log_buckets) + 1;
+  std::vector<dbuf> ck(L), z(L), zn(L), bd(L), bi(L);
+  std::vector<int64_t> M(L, 0);
+  dbuf stage;
+  for (int j0 = 0; j0 < L; j0 += sc.lpp) {
+    const int j1 = std::min(L, j0 + sc.lpp);
+    for (int64_t r0 = 0; r0 < n; r0 += sc.chunk) {  // one pass: every row's cell id at levels j0 .. j1 - 1
+      const int64_t m = std::min(sc.chunk, n - r0);
+      project_rows(sc.rsrc->rows(r0, m, s), m, sc.d, sc.mean, sc.U, sc.shift, w, sc.y, s);
+      for (int j = j0; j < j1; j++)
+        stream_keys(sc.y, m, sc.b, spacings[j], (*sc.skey)[j - j0].as<long long>() + r0,
+                    (*sc.sdist)[j - j0].as<float>() + r0, s);
+    }
+    for (int j = j0; j < j1; j++) {
+      const int mc = (sc.min_cell > 1 && j < L - 1) ? sc.min_cell : 1;  // the coarsest level keeps every cell
+      dbuf crow;
+      M[j]  = cb.cells_of_keys((*sc.skey)[j - j0].as<long long>(), mc, ck[j], crow);
+      z[j]  = dbuf(static_cast<size_t>(std::max<int64_t>(M[j], 1)) * w * sizeof(float));
+      zn[j] = dbuf(static_cast<size_t>(std::max<int64_t>(M[j], 1)) * sizeof(float));
+      bd[j] = dbuf(static_cast<size_t>(std::max<int64_t>(M[j] * l, 1)) * sizeof(float));
+      bi[j] = dbuf(static_cast<size_t>(std::max<int64_t>(M[j] * l, 1)) * sizeof(int));
+      if (M[j] > 0) {
+        cell_centers(sc.xd, crow.as<int>(), M[j], sc.d, sc.mean, sc.U, sc.shift, sc.b, spacings[j], sc.chunk, stage,
+                     sc.y, z[j].as<float>(), s);
+        row_norms<float>(z[j].as<float>(), M[j], w, zn[j].as<float>(), s);
+        init_lists(bd[j].as<float>(), bi[j].as<int>(), M[j] * l, s);
+      }
+      OCTEX_HIP(hipStreamSynchronize(s));
+    }
+  }
+  stage = dbuf();
+  // the row ranges (build_cells.cuh:1233-1245): OCTEX_BUILD_RANGES of them, else as many rows as 0.6 of the free
+  // memory holds at the range's bytes a row (its projection, and for IVF lists the index's copy of it, labels and
+  // sort scratch), at most 2^26; at least l rows a range; ranges over 2^18 rows end at multiples of 2^18 rows
+  int64_t K = 0;
+  if (const char* er = std::getenv("OCTEX_BUILD_RANGES"); er != nullptr && std::atoi(er) > 0) {
+    K = std::atoi(er);
+  } else {
+    size_t fr = 0, tot = 0;
+    OCTEX_HIP(hipMemGetInfo(&fr, &tot));
+    const double per_row = sc.exact ? 4.0 * w + 8 : 8.0 * w + 40;
+    const int64_t rmax   = std::clamp<int64_t>(static_cast<int64_t>(0.6 * static_cast<double>(fr) / per_row), 1,
+                                               int64_t{1} << 26);
+    K = (n + rmax - 1) / rmax;
+  }
+  K = std::clamp<int64_t>(K, 1, std::max<int64_t>(1, n / std::max(l, 1)));
+  constexpr int64_t kRangeStep = int64_t{1} << 18;
+  int64_t rlen = (n + K - 1) / K;
+  if (rlen > kRangeStep) rlen = std::min(n, (rlen + kRangeStep - 1) / kRangeStep * kRangeStep);
+  int64_t Mmax = 1;
+  for (auto m : M)
+    Mmax = std::max(Mmax, m);
+  const int64_t zc = std::min<int64_t>(int64_t{1} << 20, Mmax);  // centers per search
+  dbuf nd(static_cast<size_t>(zc) * l * sizeof(float)), ni(static_cast<size_t>(zc) * l * sizeof(int)),
+    od(static_cast<size_t>(zc) * l * sizeof(float)), oi(static_cast<size_t>(zc) * l * sizeof(int));
+  ivf_index ivf;
+  build_log("streamed lists: %lld row ranges of %lld rows\n", static_cast<long long>((n + rlen - 1) / rlen),
+            static_cast<long long>(rlen));
+  for (int64_t a = 0; a < n; a += rlen) {
+    const int64_t R = std::min(rlen, n - a);
+    dbuf yr(static_cast<size_t>(R) * w * sizeof(float)), yn;
+    for (int64_t r0 = 0; r0 < R; r0 += sc.chunk) {
+      const int64_t m = std::min(sc.chunk, R - r0);
+      project_rows(sc.rsrc->rows(a + r0, m, s), m, sc.d, sc.mean, sc.U, sc.shift, w, yr.as<float>() + r0 * w, s);
+    }
+    if (sc.exact) {
+      yn = dbuf(static_cast<size_t>(R) * sizeof(float));
+      row_norms<float>(yr.as<float>(), R, w, yn.as<float>(), s);
+    } else {  // the whole-projection build's IVF settings (build_cells.cuh:513-515, 1275-1279), for this range
+      const int nlist = static_cast<int>(std::max<int64_t>(64, static_cast<int64_t>(4 * std::sqrt(static_cast<double>(R)))));
+      ivf.build(yr.as<float>(), R, w, nlist, R <= 4000000 ? 0.5 : 0.1, 20, s);
+      yr = dbuf();  // the index holds its own copy of the rows
+    }
+    for (int j = 0; j < L; j++)
+      for (int64_t z0 = 0; z0 < M[j]; z0 += zc) {
+        const int64_t mz = std::min(zc, M[j] - z0);
+        const float* zj  = z[j].as<float>() + z0 * w;
+        if (sc.exact)
+          knn_rows<float>(zj, zn[j].as<float>() + z0, mz, yr.as<float>(), yn.as<float>(), R, w, l, nd.as<float>(),
+                          ni.as<int>(), s);
+        else
+          ivf.lists(zj, zn[j].as<float>() + z0, mz, sc.probes, l, ni.as<int>(), s, nd.as<float>());
+        float* bdj = bd[j].as<float>() + z0 * l;
+        int* bij   = bi[j].as<int>() + z0 * l;
+        merge_lists(bdj, bij, nd.as<float>(), ni.as<int>(), mz, l, a, od.as<float>(), oi.as<int>(), s);
+        OCTEX_HIP(hipMemcpyAsync(bdj, od.ptr, static_cast<size_t>(mz) * l * sizeof(float), hipMemcpyDeviceToDevice, s));
+        OCTEX_HIP(hipMemcpyAsync(bij, oi.ptr, static_cast<size_t>(mz) * l * sizeof(int), hipMemcpyDeviceToDevice, s));
+      }
+    OCTEX_HIP(hipStreamSynchronize(s));
+  }
+  for (int j = 0; j < L; j++) {
+    cb.finish_level(ck[j].as<long long>(), bi[j].as<int>(), M[j], l, sc.log_buckets, offs + j * T1, keys_out[j],
+                    lists_out[j]);
+    ck[j] = dbuf(), z[j] = dbuf(), zn[j] = dbuf(), bd[j] = dbuf(), bi[j] = dbuf();
+  }
+  return M;
+}
+
 }  // namespace
 
 /** The neighbor rows [n, k] of an in-memory index, replacing its table (the reference's set_table). */
@@ -547,19 +673,19 @@ auto build_in_memory(index_params const& params, dataset_view const& x, build_re
     t = std::chrono::steady_clock::now();
   };
 
-  // Streamed build (build_cells.cuh:756-1393; OCTEX_BUILD_STREAM=1 forces it): when the whole-projection build's
-  // device arrays (fp16 rows, one copy's fp32 projection, the cell sorts' scratch: about 2d + 4w + 64 bytes a row)
-  // would take more than half of the free device memory, the vectors stay in pinned host memory, every copy's
-  // projection is made in chunks and every level's cells come from each row's cell id and distance to its cell
-  // center (member lists only, like the reference's streamed copies)
+  // Streamed build (build_cells.cuh:756-1393, 1351-1393): when the whole-projection build's device arrays (fp16 rows,
+  // one copy's fp32 projection, the cell sorts' scratch, and for IVF lists the index's copy of the projection: about
+  // 2d + 4w + 64 bytes a row, 2d + 8w + 96 with IVF lists) would take more than half of the free device memory, the
+  // vectors stay in pinned host memory and every copy's projection is made in chunks.  Member lists come from each
+  // row's cell id and distance to its cell center; exact and IVF lists from row ranges, merged.  OCTEX_BUILD_STREAM=1
+  // forces the streamed build, =0 the whole-projection one.
   size_t free_b = 0, total_b = 0;
   OCTEX_HIP(hipMemGetInfo(&free_b, &total_b));
-  const char* stream_env = std::getenv("OCTEX_BUILD_STREAM");
-  const bool streamed    = (stream_env != nullptr && std::atoi(stream_env) != 0) ||
-                        static_cast<double>(n) * static_cast<double>(2 * d + 4 * w + 64) > 0.5 * static_cast<double>(free_b);
-  OCTEX_EXPECTS(!streamed || params.member_lists,
-                "octex: a dataset this large for the GPU's memory is built streamed, which builds member lists only "
-                "(set member_lists)");
+  const char* stream_env   = std::getenv("OCTEX_BUILD_STREAM");
+  const double whole_bytes = static_cast<double>(n) * (ivf_lists ? 2.0 * d + 8.0 * w + 96 : 2.0 * d + 4.0 * w + 64);
+  const bool streamed      = (stream_env != nullptr && *stream_env != '\0')
+                               ? std::atoi(stream_env) != 0
+                               : whole_bytes > 0.5 * static_cast<double>(free_b);
   if (streamed) build_log("streamed build: vectors in pinned host memory, projections in chunks\n");
 
   // the fp16 vectors: the index's own, read by every step of the build (pinned host memory when streamed)
@@ -677,7 +803,22 @@ auto build_in_memory(index_params const& params, dataset_view const& x, build_re
       std::vector<dbuf> level_lists(L);
       level_keys[c].resize(L);
       int64_t row = 0;
-      for (int j0 = 0; j0 < L; j0 += lpp) {
+      if (streamed && !params.member_lists) {
+        stream_copy sc;
+        sc.rsrc = &rsrc, sc.xd = xd, sc.n = n, sc.d = static_cast<int>(d), sc.b = b, sc.l = l;
+        sc.log_buckets = params.log_buckets, sc.min_cell = params.min_cell, sc.probes = params.list_probes;
+        sc.lpp = lpp, sc.exact = exact_lists, sc.mean = ix.mean.as<float>(), sc.U = U.as<float>();
+        sc.shift = sh.as<float>(), sc.chunk = chunk, sc.y = y.as<float>(), sc.skey = &skey, sc.sdist = &sdist;
+        const auto Ms = streamed_center_lists(cb, sc, params.spacings,
+                                              ix.offsets.as<int32_t>() + static_cast<int64_t>(c) * L * (T + 1),
+                                              level_keys[c], level_lists, s);
+        for (int j = 0; j < L; j++) {
+          rec.base[static_cast<size_t>(c) * L + j]  = static_cast<int32_t>(row);
+          rec.cells[static_cast<size_t>(c) * L + j] = Ms[j];
+          row += Ms[j];
+        }
+      }
+      for (int j0 = 0; j0 < L && !(streamed && !params.member_lists); j0 += lpp) {
         const int j1 = std::min(L, j0 + lpp);
         if (streamed)  // one pass over the rows: every row's cell id and center distance at levels j0 .. j1 - 1
           for (int64_t r0 = 0; r0 < n; r0 += chunk) {
@@ -1018,7 +1159,7 @@ auto resume_table(index_params const& params, dataset_view const& x, std::string
 auto build_to_directory(index_params const& params, dataset_view const& x, std::string const& path,
                         build_record& rec) -> std::shared_ptr<index_impl>
 {
-  if (const char* e = std::getenv("OCTEX_TABLE_ONLY"); e != nullptr && std::atoi(e) != 0)
+  if (std::getenv("OCTEX_TABLE_ONLY") != nullptr)  // set at all, as build.cu:148 reads it
     return resume_table(params, x, path, rec);
   if (!params.write_behind) {
     auto impl = build_in_memory(params, x, rec);

@@ -41,7 +41,7 @@ void write_index(index_impl const& ix, build_record const& rec, index_params con
 /**
  * Build the index of x into the directory `path` and return it (build.cu:104-454).  With params.write_behind the
  * arrays that are final before the neighbor table are written by a background thread while the table is built,
- * and joined before table.npy and meta.json (meta.json last).  With OCTEX_TABLE_ONLY=1 in the environment the
+ * and joined before table.npy and meta.json (meta.json last).  With OCTEX_TABLE_ONLY set in the environment the
  * directory already holds every array but table.npy and meta.json (a build that stopped in its table phase): only
  * the neighbor table is built, over those arrays, and table.npy and meta.json written.
  */

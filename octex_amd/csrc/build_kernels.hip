@@ -199,14 +199,18 @@ __global__ void run_compact_kernel(const long long* __restrict__ ukey, const int
   cpop[c]   = pop[r];
 }
 
-/** z[c] = f * E8 point of y[first member] / f: the center of kept cell c (build_cells.cuh:86-103). */
+/**
+ * z[c] = f * E8 point of y[first member] / f: the center of kept cell c (build_cells.cuh:86-103).  Without sidx, y
+ * holds the first members' projections themselves, y[c] for cell c.
+ */
 template <int B>
 __global__ void cell_center_kernel(const float* __restrict__ y, const int* __restrict__ sidx,
                                    const int* __restrict__ cfirst, int M, float f, float* __restrict__ z)
 {
   int c = blockIdx.x * blockDim.x + threadIdx.x;
   if (c >= M) return;
-  const float* r = y + static_cast<int64_t>(sidx[cfirst[c]]) * 8 * B;
+  const int64_t row = sidx != nullptr ? static_cast<int64_t>(sidx[cfirst[c]]) : c;
+  const float* r    = y + row * 8 * B;
 #pragma unroll
   for (int j = 0; j < B; j++) {
     float x[8], p[8];
@@ -256,6 +260,25 @@ __global__ void list_fill_kernel(const int* __restrict__ sidx2, const int* __res
   if (t >= static_cast<int64_t>(M) * l) return;
   int c = static_cast<int>(t / l), j = static_cast<int>(t % l);
   lists[t] = sidx2[cstart[c] + (j < cpop[c] ? j : 0)];
+}
+
+/** crow[c] = sidx[cfirst[c]]: the first row of kept cell c in the stable key sort, its smallest. */
+__global__ void first_row_kernel(const int* __restrict__ sidx, const int* __restrict__ cfirst, int M,
+                                 int* __restrict__ crow)
+{
+  int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c < M) crow[c] = sidx[cfirst[c]];
+}
+
+/** out [m, d] = x [at[i]]: fp16 rows (d even) by 4-byte words, consecutive threads on consecutive words of a row. */
+__global__ void gather_half_rows_kernel(const __half* __restrict__ x, const int* __restrict__ at, int64_t m, int d,
+                                        __half* __restrict__ out)
+{
+  const int64_t t  = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t hw = d / 2;
+  if (t >= m * hw) return;
+  const int64_t i = t / hw, k = t - i * hw;
+  reinterpret_cast<unsigned*>(out)[t] = reinterpret_cast<const unsigned*>(x + static_cast<int64_t>(at[i]) * d)[k];
 }
 
 __global__ void bucket_kernel(const long long* __restrict__ ckey, int M, long long mask,
@@ -679,7 +702,8 @@ constexpr int kIvfSort = 1024;  // the kept l (<= 128) and the waiting keys, sor
  */
 __global__ __launch_bounds__(256) void ivf_scan_kernel(const float* __restrict__ z, int w, const int* __restrict__ probe,
                                                        int P, const int* __restrict__ off, const int* __restrict__ rows,
-                                                       const float* __restrict__ yc, int l, int* __restrict__ out)
+                                                       const float* __restrict__ yc, int l, int* __restrict__ out,
+                                                       float* __restrict__ out_d)
 {
   __shared__ float zs[kMaxW];
   __shared__ int pre[129], pc[128];
@@ -774,8 +798,50 @@ __global__ __launch_bounds__(256) void ivf_scan_kernel(const float* __restrict__
     if (nbuf > kIvfBuf - static_cast<int>(blockDim.x)) merge();  // the next round could overflow the buffer
   }
   if (nbuf > 0) merge();
-  for (int k = t; k < l; k += blockDim.x)
+  for (int k = t; k < l; k += blockDim.x) {
     out[cell * l + k] = k < nkept ? static_cast<int>(keys[k] & 0xffffffffULL) : -1;
+    if (out_d != nullptr) out_d[cell * l + k] = k < nkept ? __uint_as_float(static_cast<unsigned>(keys[k] >> 32)) : INFINITY;
+  }
+}
+
+/** bd = +inf, bi = -1: empty lists before the first range's merge. */
+__global__ void list_init_kernel(float* __restrict__ bd, int* __restrict__ bi, int64_t total)
+{
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= total) return;
+  bd[t] = INFINITY;
+  bi[t] = -1;
+}
+
+/**
+ * The streamed lists' merge over row ranges (build_cells.cuh stream_merge_kernel): for each of M centers, the l first
+ * of its kept list (bd, bi) and of a range's list (nd, ni, rows numbered from a), both ascending by (distance, row;
+ * -1 entries last), into od, oi.  Distances order as the k-NN kernel orders them and rows as unsigned, so the lists
+ * merged over ranges are the lists of one search over all rows.
+ */
+__global__ void merge_lists_kernel(const float* __restrict__ bd, const int* __restrict__ bi,
+                                   const float* __restrict__ nd, const int* __restrict__ ni, int64_t M, int l,
+                                   int64_t a, float* __restrict__ od, int* __restrict__ oi)
+{
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (c >= M) return;
+  const int64_t o = c * l;
+  auto key        = [](float dd, int row) {
+    return (static_cast<unsigned long long>(knn_ord(dd)) << 32) | static_cast<unsigned>(row);
+  };
+  int p = 0, q = 0;  // p + q = j < l: both stay in their lists
+  for (int j = 0; j < l; j++) {
+    const int ry = ni[o + q] >= 0 ? static_cast<int>(ni[o + q] + a) : -1;
+    if (key(bd[o + p], bi[o + p]) <= key(nd[o + q], ry)) {
+      od[o + j] = bd[o + p];
+      oi[o + j] = bi[o + p];
+      p++;
+    } else {
+      od[o + j] = nd[o + q];
+      oi[o + j] = ry;
+      q++;
+    }
+  }
 }
 
 template <typename T>
@@ -945,23 +1011,9 @@ void cell_builder::reserve(int64_t n_, int w_, hipStream_t s_, bool member_keys)
   }
 }
 
-auto cell_builder::level(const float* y, int B, float f, int min_cell, int l, int log_buckets, bool exact,
-                         int* offs_out, dbuf& keys_out, dbuf& lists_out, ivf_index* ivf, int probes) -> int64_t
+auto cell_builder::compact_runs(int min_cell) -> int
 {
-  const bool member = !exact && ivf == nullptr;
-  const int64_t T = int64_t{1} << log_buckets;
-  auto g          = grid_for(n, 256);
-  switch (B) {
-#define OCTEX_HASH(b) \
-  case b: cell_hash_kernel<b><<<g, 256, 0, s>>>(y, n, f, keys.as<long long>(), idx.as<int>()); break;
-    OCTEX_HASH(1) OCTEX_HASH(2) OCTEX_HASH(3) OCTEX_HASH(4) OCTEX_HASH(5) OCTEX_HASH(6) OCTEX_HASH(8)
-#undef OCTEX_HASH
-    default: fail("octex: blocks must be 1-6 or 8");
-  }
-  with_tmp(tmp, [&](void* p, size_t& b) {
-    return rocprim::radix_sort_pairs(p, b, keys.as<long long>(), skeys.as<long long>(), idx.as<int>(), sidx.as<int>(),
-                                     n, 0, 64, s);
-  });
+  auto g = grid_for(n, 256);
   run_flag_kernel<<<g, 256, 0, s>>>(skeys.as<long long>(), n, flag.as<int>());
   with_tmp(tmp, [&](void* p, size_t& b) {
     return rocprim::inclusive_scan(p, b, flag.as<int>(), rid.as<int>(), n, rocprim::plus<int>(), s);
@@ -988,11 +1040,114 @@ auto cell_builder::level(const float* y, int B, float f, int min_cell, int l, in
   ensure<long long>(ckey, M);
   ensure<int>(cfirst, M);
   ensure<int>(cpop, M);
-  ensure<int>(cstart, M);
-  ensure<float>(z, static_cast<int64_t>(M) * w);
   run_compact_kernel<<<grid_for(runs, 256), 256, 0, s>>>(ukey.as<long long>(), start.as<int>(), pop.as<int>(),
                                                           keep.as<int>(), kidx.as<int>(), runs, ckey.as<long long>(),
                                                           cfirst.as<int>(), cpop.as<int>());
+  OCTEX_HIP(hipGetLastError());
+  return M;
+}
+
+void cell_builder::finish_level(const long long* ck, const int* lists, int64_t M64, int l, int log_buckets,
+                                int* offs_out, dbuf& keys_out, dbuf& lists_out)
+{
+  OCTEX_EXPECTS(M64 < (int64_t{1} << 31), "octex: more than 2^31 - 1 cells in a level");
+  const int M     = static_cast<int>(M64);
+  const int64_t T = int64_t{1} << log_buckets;
+  ensure<unsigned>(bucket, M);
+  ensure<unsigned>(sbucket, M);
+  ensure<int>(seq, M);
+  ensure<int>(perm, M);
+  keys_out  = dbuf(static_cast<size_t>(std::max(M, 1)) * sizeof(long long));
+  lists_out = dbuf(static_cast<size_t>(std::max<int64_t>(int64_t{M} * l, 1)) * sizeof(int));
+  if (M > 0) {
+    bucket_kernel<<<grid_for(M, 256), 256, 0, s>>>(ck, M, T - 1, bucket.as<unsigned>(), seq.as<int>());
+    with_tmp(tmp, [&](void* p, size_t& b) {
+      return rocprim::radix_sort_pairs(p, b, bucket.as<unsigned>(), sbucket.as<unsigned>(), seq.as<int>(),
+                                       perm.as<int>(), M, 0, log_buckets, s);
+    });
+    level_gather_kernel<<<grid_for(int64_t{M} * l, 256), 256, 0, s>>>(ck, lists, perm.as<int>(), M, l,
+                                                                       keys_out.as<long long>(), lists_out.as<int>());
+  }
+  offsets_kernel<<<grid_for(T + 1, 256), 256, 0, s>>>(sbucket.as<unsigned>(), M, T, offs_out);
+  OCTEX_HIP(hipGetLastError());
+  OCTEX_HIP(hipStreamSynchronize(s));
+}
+
+auto cell_builder::cells_of_keys(const long long* key, int min_cell, dbuf& ckey_out, dbuf& crow_out) -> int64_t
+{
+  auto g = grid_for(n, 256);
+  iota_kernel<<<g, 256, 0, s>>>(idx.as<int>(), n);
+  with_tmp(tmp, [&](void* p, size_t& b) {
+    return rocprim::radix_sort_pairs(p, b, key, skeys.as<long long>(), idx.as<int>(), sidx.as<int>(), n, 0, 64, s);
+  });
+  const int M = compact_runs(min_cell);
+  ckey_out    = dbuf(static_cast<size_t>(std::max(M, 1)) * sizeof(long long));
+  crow_out    = dbuf(static_cast<size_t>(std::max(M, 1)) * sizeof(int));
+  if (M > 0) {
+    OCTEX_HIP(hipMemcpyAsync(ckey_out.ptr, ckey.ptr, static_cast<size_t>(M) * sizeof(long long),
+                             hipMemcpyDeviceToDevice, s));
+    first_row_kernel<<<grid_for(M, 256), 256, 0, s>>>(sidx.as<int>(), cfirst.as<int>(), M, crow_out.as<int>());
+  }
+  OCTEX_HIP(hipGetLastError());
+  OCTEX_HIP(hipStreamSynchronize(s));
+  return M;
+}
+
+void cell_centers(const __half* x, const int* rows, int64_t M, int d, const float* mean, const float* U,
+                  const float* shift, int B, float f, int64_t chunk, dbuf& stage, float* y, float* z, hipStream_t s)
+{
+  OCTEX_EXPECTS(d % 2 == 0, "octex: the dimension must be even");
+  ensure<__half>(stage, std::min(chunk, M) * d);
+  for (int64_t z0 = 0; z0 < M; z0 += chunk) {
+    const int64_t m = std::min(chunk, M - z0);
+    gather_half_rows_kernel<<<grid_for(m * (d / 2), 256), 256, 0, s>>>(x, rows + z0, m, d, stage.as<__half>());
+    project_rows(stage.as<__half>(), m, d, mean, U, shift, 8 * B, y, s);
+    auto gm = grid_for(m, 256);
+    switch (B) {
+#define OCTEX_CC(b) \
+  case b: cell_center_kernel<b><<<gm, 256, 0, s>>>(y, nullptr, nullptr, static_cast<int>(m), f, z + z0 * 8 * B); break;
+      OCTEX_CC(1) OCTEX_CC(2) OCTEX_CC(3) OCTEX_CC(4) OCTEX_CC(5) OCTEX_CC(6) OCTEX_CC(8)
+#undef OCTEX_CC
+      default: fail("octex: blocks must be 1-6 or 8");
+    }
+    OCTEX_HIP(hipGetLastError());
+  }
+}
+
+void init_lists(float* bd, int* bi, int64_t total, hipStream_t s)
+{
+  if (total == 0) return;
+  list_init_kernel<<<grid_for(total, 256), 256, 0, s>>>(bd, bi, total);
+  OCTEX_HIP(hipGetLastError());
+}
+
+void merge_lists(const float* bd, const int* bi, const float* nd, const int* ni, int64_t M, int l, int64_t a,
+                 float* od, int* oi, hipStream_t s)
+{
+  if (M == 0) return;
+  merge_lists_kernel<<<grid_for(M, 128), 128, 0, s>>>(bd, bi, nd, ni, M, l, a, od, oi);
+  OCTEX_HIP(hipGetLastError());
+}
+
+auto cell_builder::level(const float* y, int B, float f, int min_cell, int l, int log_buckets, bool exact,
+                         int* offs_out, dbuf& keys_out, dbuf& lists_out, ivf_index* ivf, int probes) -> int64_t
+{
+  const bool member = !exact && ivf == nullptr;
+  auto g            = grid_for(n, 256);
+  switch (B) {
+#define OCTEX_HASH(b) \
+  case b: cell_hash_kernel<b><<<g, 256, 0, s>>>(y, n, f, keys.as<long long>(), idx.as<int>()); break;
+    OCTEX_HASH(1) OCTEX_HASH(2) OCTEX_HASH(3) OCTEX_HASH(4) OCTEX_HASH(5) OCTEX_HASH(6) OCTEX_HASH(8)
+#undef OCTEX_HASH
+    default: fail("octex: blocks must be 1-6 or 8");
+  }
+  with_tmp(tmp, [&](void* p, size_t& b) {
+    return rocprim::radix_sort_pairs(p, b, keys.as<long long>(), skeys.as<long long>(), idx.as<int>(), sidx.as<int>(),
+                                     n, 0, 64, s);
+  });
+  const int M = compact_runs(min_cell);
+  ensure<int>(cstart, M);
+  ensure<float>(z, static_cast<int64_t>(M) * w);
   if (M > 0) {
     auto gm = grid_for(M, 256);
     switch (B) {
@@ -1017,12 +1172,6 @@ auto cell_builder::level(const float* y, int B, float f, int min_cell, int l, in
       });
   }
   ensure<int>(lists_tmp, static_cast<int64_t>(M) * l);
-  ensure<unsigned>(bucket, M);
-  ensure<unsigned>(sbucket, M);
-  ensure<int>(seq, M);
-  ensure<int>(perm, M);
-  keys_out  = dbuf(static_cast<size_t>(std::max(M, 1)) * sizeof(long long));
-  lists_out = dbuf(static_cast<size_t>(std::max<int64_t>(int64_t{M} * l, 1)) * sizeof(int));
   if (M > 0) {
     if (ivf != nullptr) {  // the l rows nearest to each center among its probed IVF lists (build_cells.cuh:584-596)
       ensure<float>(znorm, M);
@@ -1040,19 +1189,8 @@ auto cell_builder::level(const float* y, int B, float f, int min_cell, int l, in
       list_fill_kernel<<<grid_for(int64_t{M} * l, 256), 256, 0, s>>>(sidx2.as<int>(), cstart.as<int>(),
                                                                       cpop.as<int>(), M, l, lists_tmp.as<int>());
     }
-    bucket_kernel<<<grid_for(M, 256), 256, 0, s>>>(ckey.as<long long>(), M, T - 1, bucket.as<unsigned>(),
-                                                   seq.as<int>());
-    with_tmp(tmp, [&](void* p, size_t& b) {
-      return rocprim::radix_sort_pairs(p, b, bucket.as<unsigned>(), sbucket.as<unsigned>(), seq.as<int>(),
-                                       perm.as<int>(), M, 0, log_buckets, s);
-    });
-    level_gather_kernel<<<grid_for(int64_t{M} * l, 256), 256, 0, s>>>(ckey.as<long long>(), lists_tmp.as<int>(),
-                                                                       perm.as<int>(), M, l,
-                                                                       keys_out.as<long long>(), lists_out.as<int>());
   }
-  offsets_kernel<<<grid_for(T + 1, 256), 256, 0, s>>>(sbucket.as<unsigned>(), M, T, offs_out);
-  OCTEX_HIP(hipGetLastError());
-  OCTEX_HIP(hipStreamSynchronize(s));
+  finish_level(ckey.as<long long>(), lists_tmp.as<int>(), M, l, log_buckets, offs_out, keys_out, lists_out);
   return M;
 }
 
@@ -1073,8 +1211,7 @@ void stream_keys(const float* y, int64_t m, int B, float f, long long* key, floa
 auto cell_builder::level_streamed(const long long* key, const float* dist, int min_cell, int l, int log_buckets,
                                   int* offs_out, dbuf& keys_out, dbuf& lists_out) -> int64_t
 {
-  const int64_t T = int64_t{1} << log_buckets;
-  auto g          = grid_for(n, 256);
+  auto g = grid_for(n, 256);
   // rows by distance (stable on the row order), then stably by cell id: each cell's run nearest first, ties by row
   iota_kernel<<<g, 256, 0, s>>>(idx.as<int>(), n);
   ensure<float>(kdist, n);
@@ -1087,59 +1224,14 @@ auto cell_builder::level_streamed(const long long* key, const float* dist, int m
     return rocprim::radix_sort_pairs(p, b, keys.as<long long>(), skeys.as<long long>(), sidx.as<int>(),
                                      sidx2.as<int>(), n, 0, 64, s);
   });
-  run_flag_kernel<<<g, 256, 0, s>>>(skeys.as<long long>(), n, flag.as<int>());
-  with_tmp(tmp, [&](void* p, size_t& b) {
-    return rocprim::inclusive_scan(p, b, flag.as<int>(), rid.as<int>(), n, rocprim::plus<int>(), s);
-  });
-  int runs = 0;
-  OCTEX_HIP(hipMemcpyAsync(&runs, rid.as<int>() + n - 1, sizeof(int), hipMemcpyDeviceToHost, s));
-  OCTEX_HIP(hipStreamSynchronize(s));
-  ensure<int>(start, runs + 1);
-  ensure<long long>(ukey, runs);
-  ensure<int>(pop, runs);
-  ensure<int>(keep, runs);
-  ensure<int>(kidx, runs);
-  run_start_kernel<<<g, 256, 0, s>>>(skeys.as<long long>(), rid.as<int>(), n, start.as<int>(), ukey.as<long long>());
-  run_keep_kernel<<<grid_for(runs, 256), 256, 0, s>>>(start.as<int>(), runs, n, min_cell, pop.as<int>(),
-                                                      keep.as<int>());
-  with_tmp(tmp, [&](void* p, size_t& b) {
-    return rocprim::exclusive_scan(p, b, keep.as<int>(), kidx.as<int>(), 0, runs, rocprim::plus<int>(), s);
-  });
-  int last[2] = {0, 0};
-  OCTEX_HIP(hipMemcpyAsync(&last[0], kidx.as<int>() + runs - 1, sizeof(int), hipMemcpyDeviceToHost, s));
-  OCTEX_HIP(hipMemcpyAsync(&last[1], keep.as<int>() + runs - 1, sizeof(int), hipMemcpyDeviceToHost, s));
-  OCTEX_HIP(hipStreamSynchronize(s));
-  const int M = last[0] + last[1];
-  ensure<long long>(ckey, M);
-  ensure<int>(cfirst, M);
-  ensure<int>(cpop, M);
-  run_compact_kernel<<<grid_for(runs, 256), 256, 0, s>>>(ukey.as<long long>(), start.as<int>(), pop.as<int>(),
-                                                          keep.as<int>(), kidx.as<int>(), runs, ckey.as<long long>(),
-                                                          cfirst.as<int>(), cpop.as<int>());
+  const int M = compact_runs(min_cell);
   ensure<int>(lists_tmp, static_cast<int64_t>(M) * l);
-  ensure<unsigned>(bucket, M);
-  ensure<unsigned>(sbucket, M);
-  ensure<int>(seq, M);
-  ensure<int>(perm, M);
-  keys_out  = dbuf(static_cast<size_t>(std::max(M, 1)) * sizeof(long long));
-  lists_out = dbuf(static_cast<size_t>(std::max<int64_t>(int64_t{M} * l, 1)) * sizeof(int));
   if (M > 0) {
     // a kept cell's run starts at cfirst in the sorted rows: its first l, the nearest repeated when fewer
     list_fill_kernel<<<grid_for(int64_t{M} * l, 256), 256, 0, s>>>(sidx2.as<int>(), cfirst.as<int>(), cpop.as<int>(),
                                                                     M, l, lists_tmp.as<int>());
-    bucket_kernel<<<grid_for(M, 256), 256, 0, s>>>(ckey.as<long long>(), M, T - 1, bucket.as<unsigned>(),
-                                                   seq.as<int>());
-    with_tmp(tmp, [&](void* p, size_t& b) {
-      return rocprim::radix_sort_pairs(p, b, bucket.as<unsigned>(), sbucket.as<unsigned>(), seq.as<int>(),
-                                       perm.as<int>(), M, 0, log_buckets, s);
-    });
-    level_gather_kernel<<<grid_for(int64_t{M} * l, 256), 256, 0, s>>>(ckey.as<long long>(), lists_tmp.as<int>(),
-                                                                       perm.as<int>(), M, l,
-                                                                       keys_out.as<long long>(), lists_out.as<int>());
   }
-  offsets_kernel<<<grid_for(T + 1, 256), 256, 0, s>>>(sbucket.as<unsigned>(), M, T, offs_out);
-  OCTEX_HIP(hipGetLastError());
-  OCTEX_HIP(hipStreamSynchronize(s));
+  finish_level(ckey.as<long long>(), lists_tmp.as<int>(), M, l, log_buckets, offs_out, keys_out, lists_out);
   return M;
 }
 
@@ -1205,7 +1297,8 @@ void ivf_index::build(const float* y, int64_t n_, int w_, int nlist_, double tra
   OCTEX_HIP(hipStreamSynchronize(s));
 }
 
-void ivf_index::lists(const float* z, const float* zn, int64_t M, int probes, int l, int* out, hipStream_t s)
+void ivf_index::lists(const float* z, const float* zn, int64_t M, int probes, int l, int* out, hipStream_t s,
+                      float* out_d)
 {
   OCTEX_EXPECTS(l >= 1 && l <= 128, "octex: IVF lists take list_len <= 128");
   if (M == 0) return;
@@ -1215,7 +1308,7 @@ void ivf_index::lists(const float* z, const float* zn, int64_t M, int probes, in
   knn_rows<float>(z, zn, M, centers.as<float>(), cnorm.as<float>(), nlist, w, P, pd.as<float>(), pidx.as<int>(), s);
   OCTEX_EXPECTS(M < (int64_t{1} << 31), "octex: too many cells for one launch");
   ivf_scan_kernel<<<static_cast<unsigned>(M), 256, 0, s>>>(z, w, pidx.as<int>(), P, off.as<int>(), rows.as<int>(),
-                                                           yc.as<float>(), l, out);
+                                                           yc.as<float>(), l, out, out_d);
   OCTEX_HIP(hipGetLastError());
 }
 

@@ -68,13 +68,28 @@ struct ivf_index {
   /**
    * out [M, l] (device): for each center z [M, w] (squared norms zn), the l rows nearest to it, by (fp32 squared
    * distance summed in coordinate order, row), among the rows of its `probes` nearest centers (at most 128),
-   * -1 past the rows there are (l <= 128).
+   * -1 past the rows there are (l <= 128); with out_d, their distances [M, l] (+inf past the rows there are).
    */
-  void lists(const float* z, const float* zn, int64_t M, int probes, int l, int* out, hipStream_t s);
+  void lists(const float* z, const float* zn, int64_t M, int probes, int l, int* out, hipStream_t s,
+             float* out_d = nullptr);
 };
 
 /** key / dist [m]: the cell id of each row of y [m, 8B] at spacing f and its squared distance to the cell's center. */
 void stream_keys(const float* y, int64_t m, int B, float f, long long* key, float* dist, hipStream_t s);
+/**
+ * z [M, 8B] = the centers f * E8(y / f) of cells from one member each: rows [M] of x (device-readable fp16 rows
+ * [*, d], d even), gathered `chunk` at a time into stage and projected into y [chunk, 8B].
+ */
+void cell_centers(const __half* x, const int* rows, int64_t M, int d, const float* mean, const float* U,
+                  const float* shift, int B, float f, int64_t chunk, dbuf& stage, float* y, float* z, hipStream_t s);
+/** bd = +inf, bi = -1 over total entries: empty lists. */
+void init_lists(float* bd, int* bi, int64_t total, hipStream_t s);
+/**
+ * od / oi [M, l] = for each center the l first of its kept list (bd, bi) and of one row range's list (nd, ni, rows
+ * numbered from a; -1 entries stay -1), by (distance as the k-NN kernel orders it, row).
+ */
+void merge_lists(const float* bd, const int* bi, const float* nd, const int* ni, int64_t M, int l, int64_t a,
+                 float* od, int* oi, hipStream_t s);
 
 /** Scratch of the cells of one level of one copy (reused across levels and copies). */
 struct cell_builder {
@@ -103,6 +118,22 @@ struct cell_builder {
    */
   auto level_streamed(const long long* key, const float* dist, int min_cell, int l, int log_buckets, int* offs_out,
                       dbuf& keys_out, dbuf& lists_out) -> int64_t;
+  /**
+   * The kept cells of one level from every row's cell id (key [n], device), as level() finds them: ckey_out [M]
+   * ascending, crow_out [M] the first row of each (its smallest, the member level() takes the center from).
+   * Returns M.
+   */
+  auto cells_of_keys(const long long* key, int min_cell, dbuf& ckey_out, dbuf& crow_out) -> int64_t;
+  /**
+   * The level arrays of cells ck [M] with lists [M, l] (both in ck's order): keys_out / lists_out in (bucket, id)
+   * order, offs_out [T + 1] their CSR over the buckets.
+   */
+  void finish_level(const long long* ck, const int* lists, int64_t M, int l, int log_buckets, int* offs_out,
+                    dbuf& keys_out, dbuf& lists_out);
+
+ private:
+  /** From the sorted ids skeys [n]: the runs, the kept ones (>= min_cell rows) compacted into ckey, cfirst, cpop. */
+  auto compact_runs(int min_cell) -> int;
 };
 
 }  // namespace cuvs::neighbors::octex::detail

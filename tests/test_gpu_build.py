@@ -301,13 +301,19 @@ def test_place_on_host_keeps_results(octex, data):
     assert idx.device_bytes[0] == dev0 - moved
 
 
+def same_cells(a, b, copies, lists=True):
+    """The two indexes hold the same cells: keys, offsets and bases, and with `lists` the same list of every cell."""
+    for name, dt in (("keys", np.int64), ("offsets", np.int32), ("base", np.int32)):
+        assert np.array_equal(a.array(name, dt), b.array(name, dt)), name
+    for c in range(copies if lists else 0):
+        assert np.array_equal(a.array("lists", np.int32, copy=c), b.array("lists", np.int32, copy=c)), c
+
+
 def test_streamed_build_equals_in_memory(octex, data, monkeypatch):
     """The streamed build (build_cells.cuh:756-1393, forced by OCTEX_BUILD_STREAM=1 as in the reference): vectors in
     pinned host memory, each copy's projection made in chunks, every level's member lists from each row's cell id
     and distance to its cell center.  It gives the same arrays and search results as the whole-projection build, with
-    the vectors off the device; a streamed build needs member lists."""
-    from octex_amd._lib import OctexError
-
+    the vectors off the device.  OCTEX_BUILD_STREAM=0 forces the whole-projection build."""
     X, Q, _ = data
     X = X[:6000]
     args = dict(copies=12, seed=7, log_buckets=12, table_len=32, min_cell=3, member_lists=True)
@@ -323,8 +329,55 @@ def test_streamed_build_equals_in_memory(octex, data, monkeypatch):
     p = dict(read=16, starts=64, waves=2)
     (D0, I0), (D1, I1) = mem.search(Q, k=10, **p), st.search(Q, k=10, **p)
     assert np.array_equal(I0, I1) and np.array_equal(D0, D1)
-    with pytest.raises(OctexError, match="member lists only"):
-        octex.build_in_memory(X, **dict(args, member_lists=False))
+    monkeypatch.setenv("OCTEX_BUILD_STREAM", "0")
+    whole, _ = octex.build_in_memory(X, **args)
+    assert whole.device_bytes[0] == mem.device_bytes[0]
+
+
+def test_streamed_exact_lists_over_ranges(octex, data, monkeypatch):
+    """Streamed exact lists (build_cells.cuh:1233-1335): each cell's center from its first row re-projected, the rows
+    in three ranges (OCTEX_BUILD_RANGES=3), each range's brute-force lists merged.  The lists are those of one search
+    over all rows: every array equals the whole-projection build's, and so do the search results (the reference's
+    streaming test allows differences at distance ties; here the two share one distance computation)."""
+    X, Q, _ = data
+    X = X[:6000]
+    args = dict(copies=6, seed=11, log_buckets=12, table_len=24, min_cell=3, exact_lists=True, list_len=32)
+    mem, _ = octex.build_in_memory(X, **args)
+    monkeypatch.setenv("OCTEX_BUILD_STREAM", "1")
+    monkeypatch.setenv("OCTEX_BUILD_RANGES", "3")
+    st, _ = octex.build_in_memory(X, **args)
+    same_cells(mem, st, 6)
+    assert st.device_bytes[0] == mem.device_bytes[0] - len(X) * X.shape[1] * 2
+    p = dict(read=16, starts=32, waves=2)
+    (D0, I0), (D1, I1) = mem.search(Q, k=10, **p), st.search(Q, k=10, **p)
+    assert np.array_equal(I0, I1) and np.array_equal(D0, D1)
+
+
+def test_streamed_ivf_lists(octex, data, tmp_path, monkeypatch):
+    """Streamed IVF lists (the reference's default, build_cells.cuh:1269-1300): each row range gets its own k-means
+    index, searched for every cell center with list_probes probes, the lists merged over the ranges.  One range gives
+    the whole-projection build's index exactly.  Over three ranges the cells are the same, with every k-means list
+    probed each list holds the l rows nearest to its center, and at the default 16 probes the search recall stays
+    within 0.005 of the whole-projection build's (the reference's streaming bar, test_build_stream.cu:9-11)."""
+    from test_oracle import check_exact_lists
+
+    X, Q, _ = data
+    X = X[:8000]
+    gt, _ = exact_knn(X.astype(np.float16).astype(np.float32), Q)
+    args = dict(copies=8, seed=13, log_buckets=12, table_len=24, min_cell=3, list_len=24)
+    mem, _ = octex.build_in_memory(X, **args)
+    monkeypatch.setenv("OCTEX_BUILD_STREAM", "1")
+    one, _ = octex.build_in_memory(X, **args)
+    same_cells(mem, one, 8)
+    monkeypatch.setenv("OCTEX_BUILD_RANGES", "3")
+    three, _ = octex.build_in_memory(X, **args)
+    same_cells(mem, three, 8, lists=False)
+    p = dict(read=8, starts=32, waves=2)
+    r_mem, r_three = recall(mem.search(Q, k=10, **p)[1], gt), recall(three.search(Q, k=10, **p)[1], gt)
+    assert r_three >= r_mem - 0.005, (r_mem, r_three)
+    path = str(tmp_path / "ivf3")  # 3 ranges of 1,000 rows: 126 k-means lists each, all probed
+    octex.build(X[:3000], path, **dict(args, copies=2, list_len=16, list_probes=200))
+    assert check_exact_lists(path, X[:3000]) > 50
 
 
 def test_write_behind_and_table_only_resume(octex, data, tmp_path, monkeypatch):
