@@ -702,8 +702,10 @@ struct bin_select_state {
   int wtot[16];
 };
 
+static_assert(kMaxHash <= 65535, "a selection's bin counts are 16-bit");
+
 struct bin_select_lds {
-  unsigned hist[kBins];
+  unsigned hist[kBins / 2];  // two 16-bit bin counts a word (a query has at most 2^15 candidates: no carry)
   unsigned tkey[kTieCap];
   int tid[kTieCap];
   bin_select_state bs;
@@ -762,7 +764,7 @@ __device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, c
     lo = min(lo, static_cast<unsigned>(__shfl_xor(static_cast<int>(lo), o)));
     hi = max(hi, static_cast<unsigned>(__shfl_xor(static_cast<int>(hi), o)));
   }
-  for (int i = tid; i < kBins; i += nthr)
+  for (int i = tid; i < kBins / 2; i += nthr)
     sh.hist[i] = 0;
   __syncthreads();
   if (lane == 0) {
@@ -783,14 +785,18 @@ __device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, c
     }
   };
   for_keys([&](unsigned k, int, bool ok) {
-    if (ok) atomicAdd(&sh.hist[(k - kmin) >> shift], 1u);
+    if (ok) {
+      const unsigned b = (k - kmin) >> shift;
+      atomicAdd(&sh.hist[b >> 1], 1u << (16 * (b & 1)));
+    }
   });
   __syncthreads();
+  auto count = [&](int b) { return (sh.hist[b >> 1] >> (16 * (b & 1))) & 0xffffu; };
   // the bin where the running count reaches R: thread t scans bins [t per, (t + 1) per)
   const int per = kBins / nthr;
   unsigned s    = 0;
   for (int b = 0; b < per; b++)
-    s += sh.hist[tid * per + b];
+    s += count(tid * per + b);
   unsigned incl = s;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
@@ -805,7 +811,7 @@ __device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, c
   if (excl < static_cast<unsigned>(R) && static_cast<unsigned>(R) <= excl + s) {
     unsigned cum = excl;
     for (int b = 0; b < per; b++) {
-      const unsigned h = sh.hist[tid * per + b];
+      const unsigned h = count(tid * per + b);
       if (cum + h >= static_cast<unsigned>(R)) {
         bs.bstar = tid * per + b;
         bs.below = static_cast<int>(cum);
@@ -1065,6 +1071,25 @@ struct merge_lds {
   uint64_t last[16];
 };
 
+/** Where a merge's LDS lives: the exchange of C blockDim keys, and 16 words of each per-wavefront scratch. */
+struct merge_view {
+  uint64_t* xch;
+  int* wsum;
+  uint64_t* last;
+};
+
+template <int KEYS>
+__device__ __forceinline__ auto view(merge_lds<KEYS>& m) -> merge_view
+{
+  return {m.xch, m.wsum, m.last};
+}
+
+/** LDS bytes of merge_view over `keys` exchange keys (8-byte aligned). */
+__host__ __device__ constexpr auto merge_bytes(int keys) -> size_t
+{
+  return static_cast<size_t>(keys) * 8 + 16 * 8 + 16 * 4;
+}
+
 /**
  * The kept list merged with new keys (search_kernels.cuh:379-415): the keys of the kept list (pb, pd: KO entries,
  * ignored when `fresh`, -1 entries empty) and the ns new (sdv[i], sid[i]) pairs, sorted together in registers,
@@ -1073,9 +1098,9 @@ struct merge_lds {
  * key is kept when it differs from its predecessor, and its place is the number of kept keys before it (a
  * workgroup prefix sum).  ns <= C blockDim - KO.  Every thread of the workgroup calls it.
  */
-template <int C, int KEYS>
+template <int C>
 __device__ void merge_keep(long long* pb, float* pd, int KO, bool fresh, const int* sid, const float* sdv, int ns,
-                           long long* ob, float* od, int KOout, merge_lds<KEYS>& sh)
+                           long long* ob, float* od, int KOout, merge_view sh)
 {
   const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
   uint64_t k[C];
@@ -1121,47 +1146,77 @@ __device__ void merge_keep(long long* pb, float* pd, int KO, bool fresh, const i
   }
 }
 
-/** f(std::integral_constant<int, C>) with C the keys per thread that hold `keys` keys over `threads` threads. */
-template <typename F>
+/**
+ * f(std::integral_constant<int, C>) with C the keys per thread that hold `keys` keys over `threads` threads, C a power
+ * of two up to MAXC (the callers' limits keep keys <= MAXC threads).
+ */
+template <int MAXC = 4, typename F>
 __device__ __forceinline__ void with_keys_per_thread(int keys, int threads, F&& f)
 {
   if (keys <= threads)
     f(std::integral_constant<int, 1>{});
-  else if (keys <= 2 * threads)
+  else if (keys <= 2 * threads || MAXC <= 2)
     f(std::integral_constant<int, 2>{});
-  else
+  else if (keys <= 4 * threads || MAXC <= 4)
     f(std::integral_constant<int, 4>{});
+  else
+    f(std::integral_constant<int, MAXC <= 8 ? MAXC : 8>{});
+}
+
+/** The keys per thread of a kept-list merge of `keys` keys over `threads` threads (with_keys_per_thread's C). */
+__host__ __device__ constexpr auto keys_per_thread(int keys, int threads) -> int
+{
+  return keys <= threads ? 1 : keys <= 2 * threads ? 2 : keys <= 4 * threads ? 4 : 8;
+}
+
+/**
+ * LDS of rerank_keep_kernel for R reranked keys, KO kept and D coordinates, carved from its dynamic LDS in this
+ * order: the region shared by the selection and the merge (8-byte aligned), the selected ids and their distances,
+ * the query.  Sized per launch, so small R and KO leave room for more workgroups per CU.
+ */
+__host__ __device__ constexpr auto rerank_region_bytes(int R, int KO, int threads) -> size_t
+{
+  const size_t merge = merge_bytes(keys_per_thread(KO + R, threads) * threads);
+  return ((sizeof(bin_select_lds) > merge ? sizeof(bin_select_lds) : merge) + 7) / 8 * 8;
+}
+__host__ __device__ constexpr auto rerank_lds_bytes(int R, int KO, int D, int threads) -> size_t
+{
+  return rerank_region_bytes(R, KO, threads) + static_cast<size_t>(R) * 8 + static_cast<size_t>(D) * 4;
 }
 
 /**
  * Exact rerank of the R sketch-nearest candidates of a query, merged into its kept list of the best
- * KO (search_kernels.cuh:421-467).  fresh: the kept list starts empty.
+ * KO (search_kernels.cuh:421-467).  fresh: the kept list starts empty.  One workgroup of kRerankThreads per query.
  */
 template <int LX>
-__global__ __launch_bounds__(kKeepThreads) void rerank_keep_kernel(
+__global__ __launch_bounds__(kRerankThreads) void rerank_keep_kernel(
   const int* __restrict__ cand, const float* __restrict__ dist, const int* __restrict__ nin, int W,
   const __half* __restrict__ vectors, int D, const float* __restrict__ Q, int R, int KO,
   long long* __restrict__ bi, float* __restrict__ bd, bool fresh)
 {
   const int q = blockIdx.x;
-  extern __shared__ float sq[];
-  __shared__ union {
-    bin_select_lds sel;
-    merge_lds<kMaxKeepSort> merge;
-  } u;
-  __shared__ int sid[kMaxRerank];
-  __shared__ float sd[kMaxRerank];
+  extern __shared__ uint64_t rk_lds[];
+  const size_t region = rerank_region_bytes(R, KO, kRerankThreads);
+  auto* base          = reinterpret_cast<unsigned char*>(rk_lds);
+  auto& sel           = *reinterpret_cast<bin_select_lds*>(base);
+  const int keys      = keys_per_thread(KO + R, kRerankThreads) * kRerankThreads;
+  merge_view mv{reinterpret_cast<uint64_t*>(base), reinterpret_cast<int*>(base + static_cast<size_t>(keys) * 8 + 16 * 8),
+                reinterpret_cast<uint64_t*>(base + static_cast<size_t>(keys) * 8)};
+  int* sid  = reinterpret_cast<int*>(base + region);
+  float* sd = reinterpret_cast<float*>(sid + R);
+  float* sq = sd + R;
   const int n = min(nin[q], W);
   for (int i = threadIdx.x; i < D; i += blockDim.x)
     sq[i] = Q[static_cast<int64_t>(q) * D + i];
   const int ns = select_by_bins(reinterpret_cast<const unsigned*>(dist + static_cast<int64_t>(q) * W),
-                                cand + static_cast<int64_t>(q) * W, n, R, sid, nullptr, u.sel);
+                                cand + static_cast<int64_t>(q) * W, n, R, sid, nullptr, sel);
   exact_distances<LX>(sid, ns, vectors, D, sq, sd);
   long long* pb = bi + static_cast<int64_t>(q) * KO;
   float* pd     = bd + static_cast<int64_t>(q) * KO;
-  with_keys_per_thread(KO + ns, blockDim.x, [&](auto c) {
+  // exact_distances ended with a barrier: the selection's LDS is free for the merge
+  with_keys_per_thread<kMaxKeepSort / kRerankThreads>(KO + ns, blockDim.x, [&](auto c) {
     constexpr int C = decltype(c)::value;
-    merge_keep<C>(pb, pd, KO, fresh, sid, sd, ns, pb, pd, KO, u.merge);
+    merge_keep<C>(pb, pd, KO, fresh, sid, sd, ns, pb, pd, KO, mv);
   });
 }
 
@@ -1186,7 +1241,7 @@ __global__ __launch_bounds__(512) void sketch_keep_kernel(const int* __restrict_
   float* pd     = sd + static_cast<int64_t>(q) * KO;
   with_keys_per_thread(KO + ns, blockDim.x, [&](auto c) {
     constexpr int C = decltype(c)::value;
-    merge_keep<C>(pb, pd, KO, fresh, sid, sdv, ns, pb, pd, KO, u.merge);
+    merge_keep<C>(pb, pd, KO, fresh, sid, sdv, ns, pb, pd, KO, view(u.merge));
   });
 }
 
@@ -1319,7 +1374,7 @@ __global__ __launch_bounds__(kKeepThreads) void final_rerank_kernel(
   with_keys_per_thread(ns, blockDim.x, [&](auto c) {
     constexpr int C = decltype(c)::value < 2 ? decltype(c)::value : 2;
     merge_keep<C>(nullptr, nullptr, 0, true, sid, sd, ns, bi + static_cast<int64_t>(q) * k,
-                  bd + static_cast<int64_t>(q) * k, k, m2);
+                  bd + static_cast<int64_t>(q) * k, k, view(m2));
   });
 }
 
@@ -1814,9 +1869,12 @@ void launch_rerank_keep(const int* cand, const float* dist, const int* nin, int 
   OCTEX_EXPECTS(R >= 1 && R <= kMaxRerank && KO + R <= kMaxKeepSort && KO >= 1,
                 "octex: rerank in [1, 512] and max(starts, k) + rerank <= 1024");
   OCTEX_EXPECTS(D % 2 == 0, "octex: the dimension must be even");
+  const size_t smem = rerank_lds_bytes(R, KO, D, kRerankThreads);
   with_lx(D, [&](auto lx) {
-    rerank_keep_kernel<decltype(lx)::value>
-      <<<m, kKeepThreads, D * sizeof(float), s>>>(cand, dist, nin, W, vectors, D, Q, R, KO, si, sd, fresh);
+    auto kernel = &rerank_keep_kernel<decltype(lx)::value>;
+    OCTEX_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  static_cast<int>(smem)));
+    kernel<<<m, kRerankThreads, smem, s>>>(cand, dist, nin, W, vectors, D, Q, R, KO, si, sd, fresh);
   });
   OCTEX_HIP(hipGetLastError());
 }

@@ -20,6 +20,7 @@ constexpr int kPickHash       = 8192;   // hash set of the expanded start points
 constexpr int kMaxExpanded    = 6144;   // start points expanded by earlier waves
 constexpr int kGatherThreads  = 512;
 constexpr int kKeepThreads    = 256;
+constexpr int kRerankThreads  = 128;    // rerank_keep: one workgroup per query
 
 /** log2 of the hash set of a query reading `total` entries: ceil(log2(1.5 total)) in [11, log_cap]. */
 inline auto hash_log_host(int total, int log_cap) -> int
