@@ -641,10 +641,12 @@ __device__ int collect_segments_whole(const int2* __restrict__ seg, int nseg, co
  * sketch_scores with LR = the reference's lanes per candidate for this S), written to the query's rows of
  * cand / dist and their count to nout.  The candidates are kept as hash-set slot numbers: 16-bit in LDS
  * (kLdsSlots), or, when they do not fit in LDS beside a large hash set, in the query's own row of cand,
- * where candidate j's slot is read and then overwritten by its id by the one lane group that scores it.
+ * where candidate j's slot is read and then overwritten by its id by the one lane group that scores it.  A list
+ * gather runs on kGatherListThreads, a row gather on kGatherRowThreads: the row gather's larger hash set leaves room
+ * for fewer workgroups per CU, so each gets more threads.
  */
 template <bool kRows, int LR, bool kLdsSlots, bool kBalanced>
-__global__ __launch_bounds__(kGatherThreads) void gather_kernel(
+__global__ __launch_bounds__(kRows ? kGatherRowThreads : kGatherListThreads) void gather_kernel(
   const int2* __restrict__ seg, int nseg, const long long* __restrict__ list_ptr,
   const int* __restrict__ table, int table_len, int64_t N, const signed char* __restrict__ code,
   const float* __restrict__ scale, const float* __restrict__ qs, int S, int pitch, int W, int logW, int cap,
@@ -1760,8 +1762,8 @@ void gather_impl(bool rows, const int2* seg, int nseg, int max_len, int m, const
     auto launch      = [&](auto kernel) {
       OCTEX_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                                     static_cast<int>(smem)));
-      kernel<<<m, kGatherThreads, smem, s>>>(seg, nseg, list_ptr, table, table_len, n, code, scale, qs, S, pitch, W,
-                                             logW, cap, cand, dist, nout);
+      kernel<<<m, R ? kGatherRowThreads : kGatherListThreads, smem, s>>>(
+        seg, nseg, list_ptr, table, table_len, n, code, scale, qs, S, pitch, W, logW, cap, cand, dist, nout);
     };
     if (lds_slots)
       launch(&gather_kernel<R, LR, true, kBalanced>);

@@ -18,7 +18,8 @@ constexpr int kMaxKeepSort    = 1024;   // kept + reranked keys sorted together
 constexpr int kMaxSketchKO    = 1024;   // kept entries of the sketch merge
 constexpr int kPickHash       = 8192;   // hash set of the expanded start points
 constexpr int kMaxExpanded    = 6144;   // start points expanded by earlier waves
-constexpr int kGatherThreads  = 512;
+constexpr int kGatherListThreads = 256;  // gathers of cell lists (first round): small hash sets, many per CU
+constexpr int kGatherRowThreads  = 512;  // gathers of neighbor-table rows (waves)
 constexpr int kKeepThreads    = 256;
 constexpr int kRerankThreads  = 128;    // rerank_keep: one workgroup per query
 
