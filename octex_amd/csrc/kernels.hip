@@ -349,22 +349,13 @@ __global__ __launch_bounds__(256) void probe_kernel(const __half* __restrict__ Y
 
 // ------------------------------------------------------------------ gather (search_kernels.cuh:138-253)
 
-/**
- * Slots of a query's hash set for `total` entries: 1.5 total rounded up to 64, at least 64 and at most hmax (the
- * LDS the launch reserved, itself at least 1.5 times any query's entries or the candidate row width W).  Which slots
- * a set has changes only the speed of the dedup, never the distinct ids.
- */
-__device__ __forceinline__ int hash_slots(int total, int hmax)
+__device__ __forceinline__ int hash_log_dev(int total, int log_cap)
 {
-  const int64_t want = (3 * static_cast<int64_t>(total) + 1) / 2;
-  const int64_t hs   = (want + 63) / 64 * 64;
-  return static_cast<int>(hs < 64 ? 64 : (hs > hmax ? hmax : hs));
-}
-
-/** The home slot of id v in a set of HT slots (a multiplicative hash, then a multiply-shift into [0, HT)). */
-__device__ __forceinline__ unsigned hash_home(int v, int HT)
-{
-  return __umulhi(static_cast<unsigned>(v) * kIdHash, static_cast<unsigned>(HT));
+  if (total <= 0) return kMinLogHash;
+  int want = static_cast<int>((3 * static_cast<int64_t>(total) + 1) / 2);
+  int e    = 32 - __clz(want - 1);  // smallest e with 2^e >= want (want >= 1)
+  if (want == 1) e = 0;
+  return e < kMinLogHash ? kMinLogHash : (e > log_cap ? log_cap : e);
 }
 
 /**
@@ -376,10 +367,11 @@ __device__ __forceinline__ unsigned hash_home(int v, int HT)
  * lie anywhere in a sketch of many GB), and every group has kRows candidates' loads in flight before it
  * computes.
  */
-template <int LR, int kRows, typename IdOf, typename Put>
+template <int LR, typename IdOf, typename Put>
 __device__ __forceinline__ void sketch_scores(int n, IdOf const& id_of, const signed char* __restrict__ code, int S,
                                               int pitch, const float2* sq, Put const& put)
 {
+  constexpr int kRows = 4;        // candidates per group in flight
   constexpr int GPW   = 64 / LR;  // groups per wavefront
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
   const int sub = lane & (LR - 1), grp = lane / LR;
@@ -457,7 +449,7 @@ struct collect_state {
  */
 template <bool kRows, typename Add>
 __device__ int collect_candidates(const int2* __restrict__ seg, int nseg, const long long* __restrict__ list_ptr,
-                                  const int* __restrict__ table, int table_len, int64_t N, int hmax, int cap,
+                                  const int* __restrict__ table, int table_len, int64_t N, int logW, int cap,
                                   const int** sp, int* pre, int* ht, collect_state& cs, Add const& add)
 {
   constexpr int kUnroll = 4;
@@ -505,7 +497,7 @@ __device__ int collect_candidates(const int2* __restrict__ seg, int nseg, const 
   __syncthreads();
   const int ns = cs.nsp, len = cs.ulen;
   const int total = pre[ns];
-  const int HT    = hash_slots(total, hmax);
+  const int HT    = 1 << hash_log_dev(total, logW);
   for (int i = tid; i < HT; i += blockDim.x)
     ht[i] = -1;
   __syncthreads();
@@ -544,7 +536,7 @@ __device__ int collect_candidates(const int2* __restrict__ seg, int nseg, const 
       bool fresh = false;
       unsigned h = 0;
       if (v[u] >= 0 && v[u] < N) {  // -1: padding of a table row (search_kernels.cuh:213)
-        h = hash_home(v[u], HT);
+        h = (static_cast<unsigned>(v[u]) * kIdHash) & (HT - 1);
         for (int p = 0; p < HT; p++) {
           int prev = atomicCAS(&ht[h], -1, v[u]);
           if (prev == -1) {
@@ -552,7 +544,7 @@ __device__ int collect_candidates(const int2* __restrict__ seg, int nseg, const 
             break;
           }
           if (prev == v[u]) break;
-          h = h + 1 == static_cast<unsigned>(HT) ? 0u : h + 1;
+          h = (h + 1) & (HT - 1);
         }
       }
       const unsigned long long mask = __ballot(fresh);
@@ -597,7 +589,7 @@ __device__ __forceinline__ int wave_append(bool pred, int* count)
  */
 template <bool kRows, typename Add>
 __device__ int collect_segments_whole(const int2* __restrict__ seg, int nseg, const long long* __restrict__ list_ptr,
-                                      const int* __restrict__ table, int table_len, int64_t N, int hmax, int cap,
+                                      const int* __restrict__ table, int table_len, int64_t N, int logW, int cap,
                                       int* ht, collect_state& cs, Add const& add)
 {
   const int q = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6, nw = blockDim.x >> 6;
@@ -611,7 +603,7 @@ __device__ int collect_segments_whole(const int2* __restrict__ seg, int nseg, co
     part += max(seg[static_cast<int64_t>(q) * nseg + c].y, 0);
   if (part > 0) atomicAdd(&cs.ulen, part);
   __syncthreads();
-  const int HT = hash_slots(cs.ulen, hmax);
+  const int HT = 1 << hash_log_dev(cs.ulen, logW);
   for (int i = tid; i < HT; i += blockDim.x)
     ht[i] = -1;
   __syncthreads();
@@ -625,7 +617,7 @@ __device__ int collect_segments_whole(const int2* __restrict__ seg, int nseg, co
       bool fresh  = false;
       unsigned h  = 0;
       if (v >= 0 && v < N) {
-        h = hash_home(v, HT);
+        h = (static_cast<unsigned>(v) * kIdHash) & (HT - 1);
         for (int p = 0; p < HT; p++) {
           const int prev = atomicCAS(&ht[h], -1, v);
           if (prev == -1) {
@@ -633,7 +625,7 @@ __device__ int collect_segments_whole(const int2* __restrict__ seg, int nseg, co
             break;
           }
           if (prev == v) break;
-          h = h + 1 == static_cast<unsigned>(HT) ? 0u : h + 1;
+          h = (h + 1) & (HT - 1);
         }
       }
       const int slot = wave_append(fresh, &cs.cnt);
@@ -657,7 +649,7 @@ template <bool kRows, int LR, bool kLdsSlots, bool kBalanced>
 __global__ __launch_bounds__(kRows ? kGatherRowThreads : kGatherListThreads) void gather_kernel(
   const int2* __restrict__ seg, int nseg, const long long* __restrict__ list_ptr,
   const int* __restrict__ table, int table_len, int64_t N, const signed char* __restrict__ code,
-  const float* __restrict__ scale, const float* __restrict__ qs, int S, int pitch, int W, int hmax, int cap,
+  const float* __restrict__ scale, const float* __restrict__ qs, int S, int pitch, int W, int logW, int cap,
   int* __restrict__ cand, float* __restrict__ dist, int* __restrict__ nout)
 {
   const int q = blockIdx.x;
@@ -665,8 +657,8 @@ __global__ __launch_bounds__(kRows ? kGatherRowThreads : kGatherListThreads) voi
   const int** sp = reinterpret_cast<const int**>(smq);  // [nseg] first entry of every non-empty segment
   float2* sq     = reinterpret_cast<float2*>(smq + nseg);  // [S] (scale, query sketch) per coordinate
   int* pre       = reinterpret_cast<int*>(sq + S);  // [nseg + 1] exclusive prefix of the compacted lengths
-  int* ht        = pre + nseg + 1;                  // [hmax] hash set
-  auto* cl       = reinterpret_cast<unsigned short*>(ht + hmax);  // [cap] slots of the candidates (kLdsSlots)
+  int* ht        = pre + nseg + 1;                  // [W] hash set
+  auto* cl       = reinterpret_cast<unsigned short*>(ht + W);  // [cap] slots of the candidates (kLdsSlots)
   __shared__ collect_state cs;
   int* crow   = cand + static_cast<int64_t>(q) * W;
   float* drow = dist + static_cast<int64_t>(q) * W;
@@ -680,10 +672,10 @@ __global__ __launch_bounds__(kRows ? kGatherRowThreads : kGatherListThreads) voi
   };
   int n = 0;
   if constexpr (kBalanced)
-    n = collect_candidates<kRows>(seg, nseg, list_ptr, table, table_len, N, hmax, cap, sp, pre, ht, cs, keep_slot);
+    n = collect_candidates<kRows>(seg, nseg, list_ptr, table, table_len, N, logW, cap, sp, pre, ht, cs, keep_slot);
   else
-    n = collect_segments_whole<kRows>(seg, nseg, list_ptr, table, table_len, N, hmax, cap, ht, cs, keep_slot);
-  sketch_scores<LR, kRows ? kGatherRowRows : kGatherListRows>(
+    n = collect_segments_whole<kRows>(seg, nseg, list_ptr, table, table_len, N, logW, cap, ht, cs, keep_slot);
+  sketch_scores<LR>(
     n,
     [&](int j) {
       if constexpr (kLdsSlots)
@@ -1737,16 +1729,9 @@ auto gather_cap(int W, int nseg, int max_len) -> int
   return static_cast<int>(std::min<int64_t>(W, static_cast<int64_t>(nseg) * std::max(max_len, 1)));
 }
 
-auto gather_hash_slots(int W, int nseg, int max_len) -> int
-{
-  const int64_t want = (3 * static_cast<int64_t>(nseg) * std::max(max_len, 1) + 1) / 2;
-  return static_cast<int>(std::clamp<int64_t>((want + 63) / 64 * 64, 64, W));
-}
-
 auto gather_smem(int W, int S, int nseg, int max_len, bool lds_slots) -> size_t
 {
-  return static_cast<size_t>(nseg) * sizeof(long long) +
-         static_cast<size_t>(gather_hash_slots(W, nseg, max_len) + 2 * S + nseg + 1) * sizeof(int) +
+  return static_cast<size_t>(nseg) * sizeof(long long) + static_cast<size_t>(W + 2 * S + nseg + 1) * sizeof(int) +
          (lds_slots ? static_cast<size_t>(gather_cap(W, nseg, max_len)) * sizeof(unsigned short) : 0);
 }
 
@@ -1767,8 +1752,7 @@ void gather_impl(bool rows, const int2* seg, int nseg, int max_len, int m, const
   const bool lds_slots  = gather_smem(W, S, nseg, max_len, true) <= kLds;  // else the slots go to cand
   const size_t smem     = gather_smem(W, S, nseg, max_len, lds_slots);
   OCTEX_EXPECTS(smem <= kLds, "octex: gather needs %zu bytes of LDS (max 160 KiB)", smem);
-  const int cap  = gather_cap(W, nseg, max_len);
-  const int hmax = gather_hash_slots(W, nseg, max_len);
+  const int cap = gather_cap(W, nseg, max_len);
   int Lr = 1;  // the reference's lanes per candidate: the next power of two >= S / 16, at most 32
   while (Lr < S / 16 && Lr < 32)
     Lr <<= 1;
@@ -1779,7 +1763,7 @@ void gather_impl(bool rows, const int2* seg, int nseg, int max_len, int m, const
       OCTEX_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                                     static_cast<int>(smem)));
       kernel<<<m, R ? kGatherRowThreads : kGatherListThreads, smem, s>>>(
-        seg, nseg, list_ptr, table, table_len, n, code, scale, qs, S, pitch, W, hmax, cap, cand, dist, nout);
+        seg, nseg, list_ptr, table, table_len, n, code, scale, qs, S, pitch, W, logW, cap, cand, dist, nout);
     };
     if (lds_slots)
       launch(&gather_kernel<R, LR, true, kBalanced>);

@@ -20,10 +20,6 @@ constexpr int kPickHash       = 8192;   // hash set of the expanded start points
 constexpr int kMaxExpanded    = 6144;   // start points expanded by earlier waves
 constexpr int kGatherListThreads = 256;  // gathers of cell lists (first round): small hash sets, many per CU
 constexpr int kGatherRowThreads  = 512;  // gathers of neighbor-table rows (waves)
-// sketch rows in flight per lane group: 4 in list gathers; 2 in row gathers, whose 62 VGPRs and 1.5x hash sets fit
-// 4 workgroups of 512 threads per CU (4 rows: 72 VGPRs, 3 workgroups; measured 4 % slower at 10M rows)
-constexpr int kGatherListRows = 4;
-constexpr int kGatherRowRows  = 2;
 constexpr int kKeepThreads    = 256;
 constexpr int kRerankThreads  = 128;    // rerank_keep: one workgroup per query
 
