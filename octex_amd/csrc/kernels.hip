@@ -1188,20 +1188,20 @@ __host__ __device__ constexpr auto rerank_lds_bytes(int R, int KO, int D, int th
 
 /**
  * Exact rerank of the R sketch-nearest candidates of a query, merged into its kept list of the best
- * KO (search_kernels.cuh:421-467).  fresh: the kept list starts empty.  One workgroup of kRerankThreads per query.
+ * KO (search_kernels.cuh:421-467).  fresh: the kept list starts empty.  One workgroup of NT threads per query.
  */
-template <int LX>
-__global__ __launch_bounds__(kRerankThreads) void rerank_keep_kernel(
+template <int LX, int NT>
+__global__ __launch_bounds__(NT) void rerank_keep_kernel(
   const int* __restrict__ cand, const float* __restrict__ dist, const int* __restrict__ nin, int W,
   const __half* __restrict__ vectors, int D, const float* __restrict__ Q, int R, int KO,
   long long* __restrict__ bi, float* __restrict__ bd, bool fresh)
 {
   const int q = blockIdx.x;
   extern __shared__ uint64_t rk_lds[];
-  const size_t region = rerank_region_bytes(R, KO, kRerankThreads);
+  const size_t region = rerank_region_bytes(R, KO, NT);
   auto* base          = reinterpret_cast<unsigned char*>(rk_lds);
   auto& sel           = *reinterpret_cast<bin_select_lds*>(base);
-  const int keys      = keys_per_thread(KO + R, kRerankThreads) * kRerankThreads;
+  const int keys      = keys_per_thread(KO + R, NT) * NT;
   merge_view mv{reinterpret_cast<uint64_t*>(base), reinterpret_cast<int*>(base + static_cast<size_t>(keys) * 8 + 16 * 8),
                 reinterpret_cast<uint64_t*>(base + static_cast<size_t>(keys) * 8)};
   int* sid  = reinterpret_cast<int*>(base + region);
@@ -1216,7 +1216,7 @@ __global__ __launch_bounds__(kRerankThreads) void rerank_keep_kernel(
   long long* pb = bi + static_cast<int64_t>(q) * KO;
   float* pd     = bd + static_cast<int64_t>(q) * KO;
   // exact_distances ended with a barrier: the selection's LDS is free for the merge
-  with_keys_per_thread<kMaxKeepSort / kRerankThreads>(KO + ns, blockDim.x, [&](auto c) {
+  with_keys_per_thread<kMaxKeepSort / NT>(KO + ns, blockDim.x, [&](auto c) {
     constexpr int C = decltype(c)::value;
     merge_keep<C>(pb, pd, KO, fresh, sid, sd, ns, pb, pd, KO, mv);
   });
@@ -1871,12 +1871,20 @@ void launch_rerank_keep(const int* cand, const float* dist, const int* nin, int 
   OCTEX_EXPECTS(R >= 1 && R <= kMaxRerank && KO + R <= kMaxKeepSort && KO >= 1,
                 "octex: rerank in [1, 512] and max(starts, k) + rerank <= 1024");
   OCTEX_EXPECTS(D % 2 == 0, "octex: the dimension must be even");
-  const size_t smem = rerank_lds_bytes(R, KO, D, kRerankThreads);
+  // 128 threads a query while its candidate rows are at most 4096 wide (the first round: more queries in flight per
+  // CU), 256 above (the waves: more of the candidates' keys held in registers); measured at 100M rows
+  const int nt      = W > 4096 ? 256 : 128;
+  const size_t smem = rerank_lds_bytes(R, KO, D, nt);
   with_lx(D, [&](auto lx) {
-    auto kernel = &rerank_keep_kernel<decltype(lx)::value>;
-    OCTEX_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  static_cast<int>(smem)));
-    kernel<<<m, kRerankThreads, smem, s>>>(cand, dist, nin, W, vectors, D, Q, R, KO, si, sd, fresh);
+    auto go = [&](auto kernel) {
+      OCTEX_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    static_cast<int>(smem)));
+      kernel<<<m, nt, smem, s>>>(cand, dist, nin, W, vectors, D, Q, R, KO, si, sd, fresh);
+    };
+    if (nt == 256)
+      go(&rerank_keep_kernel<decltype(lx)::value, 256>);
+    else
+      go(&rerank_keep_kernel<decltype(lx)::value, 128>);
   });
   OCTEX_HIP(hipGetLastError());
 }

@@ -21,7 +21,6 @@ constexpr int kMaxExpanded    = 6144;   // start points expanded by earlier wave
 constexpr int kGatherListThreads = 256;  // gathers of cell lists (first round): small hash sets, many per CU
 constexpr int kGatherRowThreads  = 512;  // gathers of neighbor-table rows (waves)
 constexpr int kKeepThreads    = 256;
-constexpr int kRerankThreads  = 128;    // rerank_keep: one workgroup per query
 
 /** log2 of the hash set of a query reading `total` entries: ceil(log2(1.5 total)) in [11, log_cap]. */
 inline auto hash_log_host(int total, int log_cap) -> int
