@@ -47,7 +47,7 @@ CONFIGS = {
     "deep100m": dict(n=100_000_000, d=96, nq=10_000, clusters=10_000, kind="deep", batch=10_000,
                      desc="seeded normalized Gaussian mixture as BASELINE.json configs[3], fp16 rows",
                      index=dict(copies=150, list_len=64, min_cell=10, table_len=64, member_lists=True, seed=0),
-                     point=dict(read=12, starts=64, waves=2, rerank=96, wave_rerank=96)),
+                     point=dict(read=12, starts=64, waves=2, rerank=64, wave_rerank=64)),
     # configs[4] of BASELINE.json (1B rows, fp16 vectors in pinned host memory, sketch-rank search) at a tenth of its
     # size: a 1B index does not build within one GPU session here.  The rows of deep100m; the index as configs[4]
     # (lists of 16, searched table of 32, sketch 96 in HBM) with the vectors moved to pinned host memory after the
@@ -93,6 +93,8 @@ SWEEP_DEEP = [
     dict(read=12, starts=64, waves=2, rerank=128, wave_rerank=128),
     dict(read=12, starts=64, waves=2, rerank=64, wave_rerank=128),
     dict(read=12, starts=64, waves=2, rerank=96, wave_rerank=96),
+    dict(read=12, starts=64, waves=2, rerank=64, wave_rerank=64),
+    dict(read=10, starts=64, waves=2, rerank=64, wave_rerank=64),
     dict(read=12, starts=64, waves=2, rerank=128, wave_rerank=96),
     dict(read=10, starts=64, waves=2, rerank=128, wave_rerank=128),
     dict(read=12, starts=56, waves=2, rerank=112, wave_rerank=112),
