@@ -587,8 +587,18 @@ def main():
         t0 = time.time()
         Dc, Ic = O.search(oix, Q[:n_s], k=k, threads=threads, **params)
         cs = time.time() - t0
-        cpu = dict(value=round(n_s / cs, 1), unit="queries/s", cores=threads, kind="port",
-                   sample=f"first {n_s} of the {len(Q)} queries, same index and parameters, {cs:.1f} s"
+        # the whole batch in less than half the target: it is searched again, so that about cpu_seconds are timed
+        passes = 1
+        if n_s == pool and cs < 0.5 * args.cpu_seconds:
+            passes = max(2, int(round(args.cpu_seconds / max(cs, 1e-3))))
+            t0 = time.time()
+            for _ in range(passes):
+                O.search(oix, Q[:n_s], k=k, threads=threads, **params)
+            cs = time.time() - t0
+        cpu = dict(value=round(passes * n_s / cs, 1), unit="queries/s", cores=threads, kind="port",
+                   sample=(f"first {n_s} of the {len(Q)} queries" if passes == 1 else
+                           f"the {len(Q)} queries searched {passes} times")
+                          + f", same index and parameters, {cs:.1f} s"
                           + (" (list rows copied for these queries only)" if big else ""),
                    recall=round(recall(Ic, gt[:n_s]), 4), nproc=host["nproc"], affinity=host["affinity"],
                    cpu_model=host["model"], threads_rule=host["rule"])
