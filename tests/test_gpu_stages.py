@@ -287,14 +287,16 @@ def random_candidates(g, m, W, n_max, N, ties=True, kind=None):
     return cand, dist, nin
 
 
-# (KO, R): the kept list and the reranked rows sort together in P = pow2 >= KO + R keys: P = 32 sorts in LDS,
-# P = 128 holds one key in half the threads, P = 512 two keys per thread, P = 1024 four
+# (KO, R): the kept list and the reranked rows sort together, C keys a thread for the smallest C that holds KO + R:
+# candidate rows of W = 2048 run on 128 threads a query (C = 1, 2, 4 and 8 below), W = 8192 on 256 (C = 1, 2, 4)
 @pytest.mark.parametrize("KO,R", [(64, 16), (64, 48), (10, 20), (256, 256), (512, 512)])
 @pytest.mark.parametrize("fresh", [True, False])
-def test_rerank_keep_matches_oracle(L, ix, dix, small_index, fresh, KO, R):
+@pytest.mark.parametrize("W", [2048, 8192])
+def test_rerank_keep_matches_oracle(L, ix, dix, small_index, fresh, KO, R, W):
     g = np.random.default_rng(4 + fresh)
-    m, W = 40, 2048
-    cand, dist, nin = random_candidates(g, m, W, 1500, ix.n)
+    m = 40
+    # more candidates than a workgroup holds in registers (8 keys a thread), so the selection also streams keys
+    cand, dist, nin = random_candidates(g, m, W, 1500 if W == 2048 else 3000, ix.n)
     Q = small_index["Q"][:m]
     si = np.full((m, KO), -1, np.int64)
     sd = np.full((m, KO), np.inf, np.float32)
