@@ -81,11 +81,12 @@ __device__ __forceinline__ half4_t load_h4(const __half* __restrict__ row, bool 
  * accumulation over k in steps of 16, the fp16 shift added in fp32 and one rounding to fp16.  Lane l
  * holds D[4 (l / 16) + r][l % 16]: 4 consecutive outputs of one query, written to an LDS tile and
  * stored by rows, 16 bytes per lane.  A workgroup is 4 waves along the outputs (64 queries x 256
- * outputs).  The fragments of 4 k steps are loaded before their MFMAs and the shift before the
- * products, so a wave's loads overlap.
+ * outputs), held to 3 waves per SIMD (the registers allow it without spills; measured faster than 2).  The
+ * fragments of 2 k steps are loaded before their MFMAs, so a wave's loads overlap; the shift is read after the
+ * products.
  */
 template <bool FULL>
-__global__ __launch_bounds__(256) void project_kernel(const __half* __restrict__ qh,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void project_kernel(const __half* __restrict__ qh,
                                                       const __half* __restrict__ ucatT,
                                                       const __half* __restrict__ shift, int m, int K,
                                                       int N, __half* __restrict__ Y)
@@ -96,16 +97,6 @@ __global__ __launch_bounds__(256) void project_kernel(const __half* __restrict__
   const int n0   = (blockIdx.y * 4 + wid) * 64;
   const bool active = n0 < N;  // a wave past the outputs computes nothing but meets the barrier
   const int kq      = (lane >> 4) * 4;
-  // the shift of this lane's 16 outputs, read once and in flight during the products
-  float sh[4][4];
-#pragma unroll
-  for (int t = 0; t < 4; t++)
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int nb  = n0 + t * 16 + kq + r;
-      const float v = __half2float(shift[nb < N ? nb : 0]);  // unconditional load, then a select
-      sh[t][r]      = nb < N ? v : 0.f;
-    }
   // this lane's rows of qh and ucatT: pointers (row 0 past the end) and validity, the same for every k step
   const __half* qrow[4];
   const __half* urow[4];
@@ -128,9 +119,9 @@ __global__ __launch_bounds__(256) void project_kernel(const __half* __restrict__
 #pragma unroll
     for (int t = 0; t < 4; t++)
       acc[i][t] = float4_t{0.f, 0.f, 0.f, 0.f};
-  // k in chunks of 4 steps of 16: a chunk's 32 fragment loads are issued back to back, so a wave waits
-  // for memory once per chunk rather than once per step
-  constexpr int kChunk = 4;
+  // k in chunks of 2 steps of 16: a chunk's 16 fragment loads are issued back to back, so a wave waits
+  // for memory once per chunk rather than once per step (2, not 4: the registers of 3 waves per SIMD)
+  constexpr int kChunk = 2;
   for (int c0 = 0; active && c0 < K; c0 += 16 * kChunk) {
     half4_t a[kChunk][4], b[kChunk][4];
 #pragma unroll
@@ -158,6 +149,15 @@ __global__ __launch_bounds__(256) void project_kernel(const __half* __restrict__
   // stores would write every 128-byte line of Y in four 32-byte pieces; read back by rows, a lane
   // stores 16 bytes and 8 lanes a whole line
   if (active) {
+    float sh[4][4];  // the shift of this lane's 16 outputs
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int nb  = n0 + t * 16 + kq + r;
+        const float v = __half2float(shift[nb < N ? nb : 0]);  // unconditional load, then a select
+        sh[t][r]      = nb < N ? v : 0.f;
+      }
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
