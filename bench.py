@@ -346,6 +346,14 @@ def measured_traffic(config, params, stage, n, algorithmic):
     return None, None
 
 
+def cpu_passes(n, pool, seconds, target):
+    """Searches of the CPU baseline's sample: one, or when the sample is the whole batch (n == pool) and one pass
+    took less than half the target time, as many as fill about `target` seconds (at least two)."""
+    if n < pool or seconds >= 0.5 * target:
+        return 1
+    return max(2, int(round(target / max(seconds, 1e-3))))
+
+
 def host_cpu():
     """The host's CPU model, its logical CPU count, the CPUs this process may run on, and the threads the CPU
     baseline uses: every CPU it may run on, at most 16 (the host share of one GPU on the GPU boxes here, whatever
@@ -587,10 +595,8 @@ def main():
         t0 = time.time()
         Dc, Ic = O.search(oix, Q[:n_s], k=k, threads=threads, **params)
         cs = time.time() - t0
-        # the whole batch in less than half the target: it is searched again, so that about cpu_seconds are timed
-        passes = 1
-        if n_s == pool and cs < 0.5 * args.cpu_seconds:
-            passes = max(2, int(round(args.cpu_seconds / max(cs, 1e-3))))
+        passes = cpu_passes(n_s, pool, cs, args.cpu_seconds)
+        if passes > 1:
             t0 = time.time()
             for _ in range(passes):
                 O.search(oix, Q[:n_s], k=k, threads=threads, **params)

@@ -76,3 +76,12 @@ def test_host_cpu_record():
     h = bench.host_cpu()
     assert 1 <= h["threads"] <= 16 and h["threads"] <= h["affinity"] <= h["nproc"]
     assert isinstance(h["model"], str) and "16" in h["rule"]
+
+
+def test_cpu_passes():
+    """The CPU baseline repeats a whole batch that takes under half the target time, to about the target."""
+    assert bench.cpu_passes(500, 1000, 1.0, 15.0) == 1  # a partial sample: one pass
+    assert bench.cpu_passes(1000, 1000, 9.0, 15.0) == 1  # the whole batch, long enough
+    assert bench.cpu_passes(1000, 1000, 2.4, 15.0) == 6
+    assert bench.cpu_passes(1000, 1000, 7.4, 15.0) == 2
+    assert bench.cpu_passes(1000, 1000, 0.0, 15.0) > 1000
