@@ -295,6 +295,19 @@ class Index:
         self._struct(L)
         return self
 
+    @classmethod
+    def from_vectors(cls, vectors):
+        """An index holding only fp16 vectors [N, D] (uint16 bits): the input of the exact reranks
+        (rerank_keep, final_rerank), for rule tests such as test_search.cu:293-412; no cell tables."""
+        vectors = _c(vectors, np.uint16)
+        n, dim = vectors.shape
+        self = cls.from_arrays(inv_f=np.ones(1, np.float32), offsets=np.zeros((1, 1, 3), np.int32),
+                               keys=np.zeros((1, 1, 1), np.int64), base=np.zeros((1, 1), np.int32), list_len=1,
+                               blocks=1, n=n, dim=dim)
+        self.vectors = vectors
+        self._struct(1)
+        return self
+
     def _from_live(self, live, queries=None, read=32):
         """The arrays of a loaded or built octex_amd index, copied to the host (the same index the GPU searches)."""
         meta = live.array("meta", np.int64)

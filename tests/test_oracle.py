@@ -219,6 +219,135 @@ def test_pick_starts_rule():
     assert np.array_equal(seg2, exp)
 
 
+def rerank_rule_case(m=16, N=5000, D=32, KO=40, seed=11):
+    """The inputs of the reference's rule test (test_search.cu:293-343): fp16 rows, fp32 queries; query q holds
+    300 + 400 (q % 4) candidates of distinct sketch distances (a random rank times 0.01f, so the sketch order is
+    unrelated to the exact one) and a kept list of KO / 2 other ids with their exact distances, sorted, padded
+    with (-1, +inf).  The reference runs 4 queries; 16 here, so each planted mistake below changes some query."""
+    g = np.random.default_rng(seed)
+    X = g.standard_normal((N, D)).astype(np.float16)
+    Q = g.standard_normal((m, D)).astype(np.float32)
+    X64 = X.astype(np.float64)
+    exact = lambda q, ids: ((X64[np.asarray(ids)] - Q[q].astype(np.float64)) ** 2).sum(-1)  # noqa: E731
+    cands, dists, si, sd = [], [], np.full((m, KO), -1, np.int64), np.full((m, KO), np.inf, np.float32)
+    for q in range(m):
+        n = 300 + 400 * (q % 4)
+        ids = g.permutation(N).astype(np.int32)
+        rank = g.permutation(np.arange(1, n + 1))
+        cands.append(ids[:n])
+        dists.append(rank.astype(np.float32) * np.float32(0.01))
+        kept = ids[n : n + KO // 2]
+        order = np.argsort(exact(q, kept), kind="stable")
+        si[q, : KO // 2] = kept[order]
+        sd[q, : KO // 2] = exact(q, kept[order]).astype(np.float32)
+    return O.Index.from_vectors(X.view(np.uint16)), Q, exact, cands, dists, si, sd
+
+
+def same_up_to_near_ties(got_ids, got_d, want_ids, want_d64, exact_of):
+    """Ids equal position by position, except where the fp64 distances of the two ids agree within 1e-5 relative
+    (a near tie that fp32 and fp64 may order differently); distances within 1e-3 relative (the north star's bar)."""
+    for j, (a, b) in enumerate(zip(got_ids, want_ids)):
+        if a == b:
+            continue
+        assert a >= 0 and b >= 0, f"position {j}: {a} vs {b}"
+        da, db = exact_of(a), exact_of(b)
+        assert abs(da - db) <= 1e-5 * (1 + db), f"position {j}: {a} ({da}) vs {b} ({db})"
+    valid = np.asarray(want_ids) >= 0
+    assert np.all(np.abs(np.asarray(got_d)[valid] - np.asarray(want_d64)[valid]) <= 1e-3 * (1 + np.asarray(want_d64)[valid]))
+
+
+def check_rerank_rule(cand, dist, si, sd, out_i, out_d, R, KO, exact_q):
+    """test_search.cu:350-375: the pool of the R sketch-nearest candidates and the kept ids, exact (fp64) distances,
+    the best KO distinct, padded with -1."""
+    sk = sorted(zip(dist.tolist(), cand.tolist()))[: min(R, len(cand))]
+    pool = {int(i) for _, i in sk} | {int(i) for i in si if i >= 0}
+    ids = np.array(sorted(pool), np.int64)
+    d64 = exact_q(ids)
+    order = np.lexsort((ids, d64))[:KO]
+    want_i = np.full(KO, -1, np.int64)
+    want_d = np.full(KO, np.inf)
+    want_i[: len(order)], want_d[: len(order)] = ids[order], d64[order]
+    same_up_to_near_ties(out_i, out_d, want_i, want_d, lambda i: float(exact_q([i])[0]))
+
+
+def check_sketch_keep_rule(cand, dist, out_i, out_d, KO):
+    """test_search.cu:381-396: the KO sketch-nearest, by sketch distance, into an empty list (distinct distances
+    here, so the ids are fixed too)."""
+    sk = sorted(zip(dist.tolist(), cand.tolist()))[:KO]
+    assert np.array_equal(out_d[: len(sk)], np.array([d for d, _ in sk], np.float32))
+    assert np.array_equal(out_i[: len(sk)], np.array([i for _, i in sk], np.int64))
+
+
+def check_final_rule(si, out_i, out_d, FR, k, exact_q):
+    """test_search.cu:398-410: the first FR kept entries reranked exactly (fp64) into the best k."""
+    ids = np.asarray(si[:FR], np.int64)
+    ids = ids[ids >= 0]
+    d64 = exact_q(ids)
+    order = np.lexsort((ids, d64))[:k]
+    same_up_to_near_ties(out_i, out_d, ids[order], d64[order], lambda i: float(exact_q([i])[0]))
+
+
+def test_rerank_sketch_keep_final_rerank_rules():
+    """The reference's rule test of rerank_keep, sketch_keep and final_rerank (test_search.cu:293-412) against the
+    oracle's functions: exact rerank of the R sketch-nearest merged into the kept KO, the sketch merge into an
+    empty list, then the final exact rerank of the first 24 kept entries into the best 10."""
+    ix, Q, exact, cands, dists, si, sd = rerank_rule_case()
+    R, KO, k, FR = 64, 40, 10, 24
+    for q in range(len(Q)):
+        ex = lambda ids, q=q: exact(q, ids)  # noqa: E731
+        oi, od = O.rerank_keep(ix, cands[q], dists[q], Q[q], R, si[q], sd[q], fresh=False)
+        check_rerank_rule(cands[q], dists[q], si[q], sd[q], oi, od, R, KO, ex)
+        ki, kd = O.sketch_keep(cands[q], dists[q], si[q], sd[q], fresh=True)
+        check_sketch_keep_rule(cands[q], dists[q], ki, kd, KO)
+        bi, bd = O.final_rerank(ix, ki, FR, Q[q], k)
+        check_final_rule(ki, bi, bd, FR, k, ex)
+
+
+def test_rerank_rules_catch_plausible_mistakes():
+    """Each plausible mistake in the composition fails the rules above on some query (planted on the CPU by
+    feeding the oracle's own functions the wrong arguments)."""
+    ix, Q, exact, cands, dists, si, sd = rerank_rule_case()
+    R, KO, k, FR = 64, 40, 10, 24
+
+    def fails(run):
+        for q in range(len(Q)):
+            try:
+                run(q, lambda ids, q=q: exact(q, ids))
+            except AssertionError:
+                return True
+        return False
+
+    def rerank(R_used, fresh):
+        def run(q, ex):
+            oi, od = O.rerank_keep(ix, cands[q], dists[q], Q[q], R_used, si[q], sd[q], fresh=fresh)
+            check_rerank_rule(cands[q], dists[q], si[q], sd[q], oi, od, R, KO, ex)
+        return run
+
+    assert not fails(rerank(R, False))
+    assert fails(rerank(R + 1, False))  # one candidate too many reranked
+    assert fails(rerank(R - 1, False))  # one too few
+    assert fails(rerank(R, True))  # the kept list ignored when not fresh
+
+    def sketch_keep_not_fresh(q, ex):  # the previous kept list merged into what should start empty
+        ki, kd = O.sketch_keep(cands[q], dists[q], si[q], np.zeros_like(sd[q]), fresh=False)
+        check_sketch_keep_rule(cands[q], dists[q], ki, kd, KO)
+
+    assert fails(sketch_keep_not_fresh)
+
+    def final(kind):
+        def run(q, ex):
+            ki, _ = O.sketch_keep(cands[q], dists[q], si[q], sd[q], fresh=True)
+            if kind == "sketch":  # the first k kept entries with their sketch distances, not reranked
+                bi, bd = ki[:k], O.sketch_keep(cands[q], dists[q], si[q], sd[q], fresh=True)[1][:k]
+            else:  # reranked over every kept entry instead of the first FR
+                bi, bd = O.final_rerank(ix, ki, KO, Q[q], k)
+            check_final_rule(ki, bi, bd, FR, k, ex)
+        return run
+
+    assert fails(final("sketch"))
+    assert fails(final("all"))
+
+
 # ---------------------------------------------------------------- index-level stages
 
 
@@ -445,10 +574,20 @@ def test_search_recall(small_index):
 
 
 def test_search_sketch_rank(small_index):
+    """Sketch-rank mode (search_kernels.cuh:471-508, 634-669): the returned distances are the exact ones of the
+    returned ids (fp64 over the fp16 rows, within fp32 accumulation error), sorted; with final_rerank 0 they are
+    the sketch distances, which that check rejects."""
     ix = O.Index(small_index["path"])
-    D, I = O.search(ix, small_index["Q"], k=10, read=32, starts=64, waves=2, sketch_rank=True, final_rerank=64)
+    Q = small_index["Q"]
+    Xh = small_index["X"].astype(np.float16).astype(np.float64)
+    D, I = O.search(ix, Q, k=10, read=32, starts=64, waves=2, sketch_rank=True, final_rerank=64)
     assert recall(I, small_index["gt"]) >= 0.8
     assert (np.diff(D, axis=1) >= 0).all()
+    exact = ((Xh[I] - Q[:, None, :].astype(np.float64)) ** 2).sum(-1)
+    assert np.allclose(D, exact, rtol=1e-4)
+    Ds, Is = O.search(ix, Q, k=10, read=32, starts=64, waves=2, sketch_rank=True, final_rerank=0)
+    exact_s = ((Xh[Is] - Q[:, None, :].astype(np.float64)) ** 2).sum(-1)
+    assert not np.allclose(Ds, exact_s, rtol=1e-4)
 
 
 def test_search_limits(small_index):
