@@ -385,14 +385,21 @@ __device__ __forceinline__ void sketch_scores(int n, IdOf const& id_of, const si
     q16[e]         = v.y;
   }
   const int per_wave = GPW * kRows;
-  // Loads are unconditional (past-the-end candidates read the last one, chunkless lanes chunk 0) so
-  // that every row of the group is requested before the first one is used.
+  // Loads are unconditional (past-the-end candidates read row 0, chunkless lanes chunk 0) so that every row of
+  // the group is requested before the first one is used.  A past-the-end candidate's id is row 0 whatever id_of
+  // returns for the clamped index n - 1: that entry belongs to another group, which may already have replaced
+  // what id_of reads there (the slot list kept in `cand` is overwritten by ids as candidates are scored), so its
+  // value is no row id.
   const int stride = nw * per_wave;
+  auto id_at = [&](int j) {
+    const int v = id_of(min(j, n - 1));
+    return j < n ? v : 0;
+  };
   int id[kRows];
   if (wid * per_wave < n) {
 #pragma unroll
     for (int r = 0; r < kRows; r++)  // candidate j0 + r * GPW + grp
-      id[r] = id_of(min(wid * per_wave + r * GPW + grp, n - 1));
+      id[r] = id_at(wid * per_wave + r * GPW + grp);
   }
   for (int j0 = wid * per_wave; j0 < n; j0 += stride) {
     int4 w[kRows];
@@ -402,7 +409,7 @@ __device__ __forceinline__ void sketch_scores(int n, IdOf const& id_of, const si
     int idn[kRows];  // the next rows' ids, read while these rows are in flight
 #pragma unroll
     for (int r = 0; r < kRows; r++)
-      idn[r] = j0 + stride < n ? id_of(min(j0 + stride + r * GPW + grp, n - 1)) : 0;
+      idn[r] = j0 + stride < n ? id_at(j0 + stride + r * GPW + grp) : 0;
     float d[kRows];
 #pragma unroll
     for (int r = 0; r < kRows; r++) {
@@ -681,7 +688,7 @@ __global__ __launch_bounds__(kRows ? kGatherRowThreads : kGatherListThreads) voi
       if constexpr (kLdsSlots)
         return ht[cl[j]];
       else
-        return ht[crow[j]];
+        return ht[crow[j] & (W - 1)];  // a slot (< W), or an id when another group has scored j: kept inside ht
     },
     code, S, pitch, sq,
     [&](int j, int id, float d) {
@@ -1760,8 +1767,7 @@ void gather_impl(bool rows, const int2* seg, int nseg, int max_len, int m, const
     constexpr bool R = decltype(rows_tag)::value;
     constexpr int LR = decltype(lr_tag)::value;
     auto launch      = [&](auto kernel) {
-      OCTEX_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    static_cast<int>(smem)));
+      allow_max_lds(reinterpret_cast<const void*>(kernel));
       kernel<<<m, R ? kGatherRowThreads : kGatherListThreads, smem, s>>>(
         seg, nseg, list_ptr, table, table_len, n, code, scale, qs, S, pitch, W, logW, cap, cand, dist, nout);
     };
@@ -1877,8 +1883,7 @@ void launch_rerank_keep(const int* cand, const float* dist, const int* nin, int 
   const size_t smem = rerank_lds_bytes(R, KO, D, nt);
   with_lx(D, [&](auto lx) {
     auto go = [&](auto kernel) {
-      OCTEX_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    static_cast<int>(smem)));
+      allow_max_lds(reinterpret_cast<const void*>(kernel));
       kernel<<<m, nt, smem, s>>>(cand, dist, nin, W, vectors, D, Q, R, KO, si, sd, fresh);
     };
     if (nt == 256)
