@@ -177,18 +177,39 @@ auto open_directory(std::string const& path, load_params const& params, std::str
   if (dir.table_len > 0) dir.table = open("table", "<i4", {N, dir.table_len});
   OCTEX_EXPECTS(dir.lists.dim(1) % dir.list_len == 0, "octex: lists rows hold %lld entries, not a multiple of list_len %d",
                 static_cast<long long>(dir.lists.dim(1)), dir.list_len);
-  // the cell tables stay inside their arrays: every bucket run inside keys, every level's rows inside lists
+  // the cell tables stay inside their arrays: every bucket run [o[i], o[i + 1]) inside keys (0 = o[0] <= o[1] <= ...
+  // <= o[T1 - 1] <= mmax: the probe reads keys o[i] .. o[i + 1] - 1 of any bucket), every level's rows inside lists.
+  // Every entry of every selected copy and level is checked, the copies spread over host threads.
   const int64_t mmax = dir.keys.dim(2), rows = dir.lists.dim(1) / dir.list_len;
   const int32_t* off = dir.offsets.as<int32_t>();
   const int32_t* bs  = dir.base.as<int32_t>();
-  for (int c : dir.copy_list)
-    for (int64_t j = 0; j < L; j++) {
-      const int32_t* o  = off + (c * L + j) * T1;
-      const int64_t end = o[T1 - 1];
-      OCTEX_EXPECTS(o[0] == 0 && end <= mmax && bs[c * L + j] >= 0 && bs[c * L + j] + end <= rows,
-                    "octex: copy %d level %lld: its cells run past keys (%lld) or lists (%lld rows)", c,
-                    static_cast<long long>(j), static_cast<long long>(mmax), static_cast<long long>(rows));
+  std::vector<int> const& sel = dir.copy_list;
+  std::vector<int64_t> bad(sel.size(), -1);  // per selected copy: the first bad level, or -1
+  auto check_copy = [&](size_t s) {
+    const int c = sel[s];
+    for (int64_t j = 0; j < L && bad[s] < 0; j++) {
+      const int32_t* o = off + (c * L + j) * T1;
+      bool ok          = o[0] == 0 && o[T1 - 1] <= mmax && bs[c * L + j] >= 0 && bs[c * L + j] + o[T1 - 1] <= rows;
+      bool down        = false;
+      for (int64_t i = 0; i + 1 < T1; i++)
+        down |= o[i + 1] < o[i];
+      if (!ok || down) bad[s] = j;
     }
+  };
+  const int nth = static_cast<int>(std::min<size_t>(sel.size(), std::max(1u, std::min(16u, std::thread::hardware_concurrency()))));
+  std::vector<std::thread> th;
+  for (int t = 0; t < nth; t++)
+    th.emplace_back([&, t] {
+      for (size_t s = t; s < sel.size(); s += nth)
+        check_copy(s);
+    });
+  for (auto& t : th)
+    t.join();
+  for (size_t s = 0; s < sel.size(); s++)
+    OCTEX_EXPECTS(bad[s] < 0,
+                  "octex: copy %d level %lld: its cells run past keys (%lld) or lists (%lld rows), or its bucket "
+                  "offsets decrease",
+                  sel[s], static_cast<long long>(bad[s]), static_cast<long long>(mmax), static_cast<long long>(rows));
   return dir;
 }
 

@@ -18,6 +18,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <limits>
 #include <string>
 #include <type_traits>
 #include <utility>
@@ -46,19 +47,22 @@ struct npy_header {
   std::vector<int64_t> shape;  // () for a scalar
   size_t data_offset = 0;      // bytes before the data
 
+  /** Elements of the shape, or -1 when their count does not fit in int64. */
   [[nodiscard]] auto count() const -> int64_t
   {
     int64_t n = 1;
     for (int64_t v : shape)
-      n *= v;
+      if (__builtin_mul_overflow(n, v, &n)) return -1;
     return n;
   }
   /** Bytes per element from the descr's size digits ("<f4" -> 4). */
   [[nodiscard]] auto item_bytes() const -> int64_t
   {
     int64_t b = 0;
-    for (size_t i = 2; i < descr.size() && descr[i] >= '0' && descr[i] <= '9'; i++)  // after byte order, kind
+    for (size_t i = 2; i < descr.size() && descr[i] >= '0' && descr[i] <= '9'; i++) {  // after byte order, kind
       b = b * 10 + (descr[i] - '0');
+      if (b > (int64_t{1} << 20)) return -1;  // no element type is this wide
+    }
     return b;
   }
 };
@@ -156,8 +160,10 @@ class npy_header_parser {
       if (peek() == ')') break;
       if (peek() < '0' || peek() > '9') bad("expected a dimension");
       int64_t x = 0;
-      while (peek() >= '0' && peek() <= '9')
+      while (peek() >= '0' && peek() <= '9') {  // every dimension below 2^62: no overflow here or in count()'s checks
         x = x * 10 + (t_[i_++] - '0');
+        if (x >= (int64_t{1} << 62)) bad("a dimension of 2^62 or more");
+      }
       if (peek() == 'L') i_++;
       v.push_back(x);
       skip();
@@ -238,7 +244,11 @@ class npy_file {
   {
     hdr  = read_npy_header(map_.bytes(), map_.size(), path);
     data = reinterpret_cast<const char*>(map_.bytes()) + hdr.data_offset;
-    const int64_t need = hdr.count() * hdr.item_bytes();
+    int64_t need       = 0;
+    const int64_t cnt  = hdr.count();
+    OCTEX_EXPECTS(cnt >= 0 && hdr.item_bytes() >= 0 && !__builtin_mul_overflow(cnt, hdr.item_bytes(), &need) &&
+                    need <= std::numeric_limits<int64_t>::max() - static_cast<int64_t>(hdr.data_offset),
+                  "octex: %s: the shape's byte count overflows", path.c_str());
     OCTEX_EXPECTS(hdr.data_offset + static_cast<size_t>(need) <= map_.size(),
                   "octex: %s holds %zu data bytes, its shape needs %lld", path.c_str(),
                   map_.size() - hdr.data_offset, static_cast<long long>(need));

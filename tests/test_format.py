@@ -125,6 +125,14 @@ def rewrite(path, name, array):
     ("lists", lambda a: a[:, :-3], r"lists rows hold \d+ entries, not a multiple of list_len 8"),
     ("offsets", lambda a: np.where(np.arange(a.shape[2]) == a.shape[2] - 1, a + 10**6, a),
      r"its cells run past keys"),
+    # a middle entry past the end of keys (first and last entries intact): the probe would read keys out of bounds
+    ("offsets", lambda a: np.where((np.arange(a.shape[2]) == 3)[None, None, :] & (np.arange(a.shape[0]) == 2)[:, None, None],
+                                   a[:, :, -1:] + 10**6, a).astype(np.int32),
+     r"copy 2 level 0: .*bucket offsets decrease"),
+    # a middle entry below its predecessor
+    ("offsets", lambda a: np.where((np.arange(a.shape[2]) == a.shape[2] // 2)[None, None, :]
+                                   & (np.arange(a.shape[1]) == 1)[None, :, None], -5, a).astype(np.int32),
+     r"copy 0 level 1: .*bucket offsets decrease"),
 ])
 def test_mismatched_directory_is_refused(L, tmp_path, name, bad, match):
     from octex_amd._lib import OctexError
@@ -172,4 +180,30 @@ def test_meta_json_errors(L, tmp_path):
         check_directory(L, d)
     open(meta, "w").write(text.replace('"copies": 6', '"copies": 0'))
     with pytest.raises(OctexError, match="a device holds no copies"):
+        check_directory(L, d)
+
+
+def npy_bytes(header, data=b"\0" * 64):
+    """A version-1.0 .npy file with the given header dictionary text (padded as numpy pads it)."""
+    h = header.encode() + b" "
+    h += b" " * ((-(10 + len(h) + 1)) % 64) + b"\n"
+    return b"\x93NUMPY\x01\x00" + len(h).to_bytes(2, "little") + h + data
+
+
+@pytest.mark.parametrize("shape,match", [
+    ("(4611686018427387904, 16)", r"malformed .npy header \(a dimension of 2\^62 or more\)"),
+    ("(99999999999999999999999, 16)", r"malformed .npy header \(a dimension of 2\^62 or more\)"),
+    ("(4294967296, 4294967296, 16)", r"the shape's byte count overflows"),  # 2^68 elements: the count wraps
+    ("(2305843009213693952, 4)", r"the shape's byte count overflows"),  # 2^63 elements x 1 byte
+    ("(1152921504606846976, 16)", r"the shape's byte count overflows"),  # 2^64 bytes: wraps to zero
+    ("(4000000000, 16)", r"sketch.npy holds \d+ data bytes, its shape needs 64000000000"),
+])
+def test_crafted_npy_shapes_are_refused(L, tmp_path, shape, match):
+    """A header whose shape overflows int64 (elements or bytes) cannot pass the data-size check by wrapping."""
+    from octex_amd._lib import OctexError
+
+    d = refdir_copy(tmp_path, absolute=())
+    with open(os.path.join(d, "sketch.npy"), "wb") as f:
+        f.write(npy_bytes("{'descr': '|i1', 'fortran_order': False, 'shape': %s, }" % shape))
+    with pytest.raises(OctexError, match=match):
         check_directory(L, d)
