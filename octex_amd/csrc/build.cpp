@@ -625,7 +625,8 @@ void searched_table(index_impl& ix, index const& idx, int k, bool reverse_edges,
 }
 
 auto build_in_memory(index_params const& params, dataset_view const& x, build_record& rec,
-                     std::function<void(index_impl const&)> const& before_table) -> std::shared_ptr<index_impl>
+                     std::function<void(std::shared_ptr<index_impl> const&)> const& before_table)
+  -> std::shared_ptr<index_impl>
 {
   const int64_t n = x.n, d = x.d;
   const auto t_all = std::chrono::steady_clock::now();
@@ -932,7 +933,7 @@ auto build_in_memory(index_params const& params, dataset_view const& x, build_re
   upload(ix.scale.ptr, rec.scale.data(), ix.scale.size, s);
   phase("sketch");
 
-  if (before_table) before_table(ix);
+  if (before_table) before_table(impl);  // a hook that outlives this call (a writer thread) keeps its own reference
 
   // neighbor table: exact up to exact_table_max rows (build.cu:354-360), else searched by this library's search
   if (k > 0) {
@@ -1167,9 +1168,12 @@ auto build_to_directory(index_params const& params, dataset_view const& x, std::
     return impl;
   }
   // write_behind (build.cu:146-178): the arrays final before the table go out while the table is built
+  // The writer holds its own reference to the index: when the table phase throws, build_in_memory drops its
+  // reference while the writer may still copy from the index's device buffers, and `w` is joined only as this
+  // frame unwinds (rec, params and path outlive it).
   writer_thread w;
-  auto impl = build_in_memory(params, x, rec, [&](index_impl const& ix) {
-    w.start([&ix, &rec, &params, &path] { write_arrays(ix, rec, params, path); });
+  auto impl = build_in_memory(params, x, rec, [&](std::shared_ptr<index_impl> const& ixp) {
+    w.start([ixp, &rec, &params, &path] { write_arrays(*ixp, rec, params, path); });
   });
   w.join();
   write_table_meta(*impl, params, rec.phases, path);

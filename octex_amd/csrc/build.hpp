@@ -35,7 +35,8 @@ struct dataset_view {
  * fp16 (round to nearest) whatever their type; a device dataset is read in place.
  */
 auto build_in_memory(index_params const& params, dataset_view const& x, build_record& rec,
-                     std::function<void(index_impl const&)> const& before_table = {}) -> std::shared_ptr<index_impl>;
+                     std::function<void(std::shared_ptr<index_impl> const&)> const& before_table = {})
+  -> std::shared_ptr<index_impl>;
 /** Write the format-1 directory of a built index (meta.json last). */
 void write_index(index_impl const& ix, build_record const& rec, index_params const& params, std::string const& path);
 /**

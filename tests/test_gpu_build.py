@@ -407,3 +407,27 @@ def test_write_behind_and_table_only_resume(octex, data, tmp_path, monkeypatch):
     p = dict(read=16, starts=32, waves=2)
     (D0, I0), (D1, I1) = octex.load(plain).search(Q, k=10, **p), octex.load(behind).search(Q, k=10, **p)
     assert np.array_equal(I0, I1) and np.array_equal(D0, D1)
+
+
+def test_write_behind_survives_a_table_phase_error(octex, data, tmp_path):
+    """A table phase that throws (here the exact table's table_len limit, checked only in that phase) while the
+    write-behind thread is still copying the index's arrays: the error reaches the caller, the writer finishes with
+    its own reference to the index (no use of freed buffers), the arrays final before the table are on disk, and the
+    next build and search work."""
+    from octex_amd._lib import OctexError
+
+    X, Q, _ = data
+    X = X[:3000]
+    bad = str(tmp_path / "bad")
+    with pytest.raises(OctexError, match="table_len <= 127"):
+        octex.build(X, bad, write_behind=True, copies=8, seed=3, log_buckets=12, list_len=8, table_len=128,
+                    member_lists=True)
+    assert not os.path.exists(os.path.join(bad, "meta.json"))  # incomplete: meta.json is written last
+    for f in ("lists.npy", "keys.npy", "offsets.npy", "sketch.npy", "vectors.npy"):
+        assert os.path.getsize(os.path.join(bad, f)) > 0, f
+    assert np.load(os.path.join(bad, "vectors.npy")).shape == X.shape
+    good = str(tmp_path / "good")
+    index = octex.build(X, good, write_behind=True, copies=8, seed=3, log_buckets=12, list_len=8, table_len=16,
+                        member_lists=True)
+    D, I = index.search(Q, k=10, read=8, starts=32, waves=1)
+    assert (I >= 0).all() and (np.diff(D, axis=1) >= 0).all()
