@@ -6,6 +6,8 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <mutex>
+#include <set>
 #include <stdexcept>
 #include <string>
 #include <utility>
@@ -109,6 +111,22 @@ inline void upload(void* dst, const void* src, size_t bytes, hipStream_t s)
   if (bytes == 0) return;
   OCTEX_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s));
   OCTEX_HIP(hipStreamSynchronize(s));
+}
+
+/**
+ * Allow a kernel the CU's whole LDS (160 KiB) as dynamic shared memory, once per kernel and device: later launches,
+ * including launches under stream capture, make no other runtime call than the launch itself.
+ */
+inline void allow_max_lds(const void* kernel)
+{
+  static std::mutex mu;
+  static std::set<std::pair<const void*, int>> done;
+  int dev = 0;
+  OCTEX_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(mu);
+  if (done.count({kernel, dev}) != 0) return;
+  OCTEX_HIP(hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+  done.insert({kernel, dev});
 }
 
 inline auto grid_for(int64_t total, int threads) -> unsigned

@@ -51,7 +51,7 @@ void search_no_alloc(search_params const& sp, index const& idx, const float* que
 {
   auto& ix = idx.impl();
   OCTEX_EXPECTS(dim == ix.dim, "octex: query dimension differs from the index");
-  OCTEX_EXPECTS(k >= 1 && k <= kMaxSketchKO, "octex: k >= 1");
+  OCTEX_EXPECTS(k >= 1 && k <= kMaxSketchKO, "octex: k in [1, %d] for a search without allocations", kMaxSketchKO);
   OCTEX_EXPECTS(nq >= 0, "octex: a negative number of queries");
   if (nq == 0) return;
   OCTEX_EXPECTS(queries != nullptr && neighbors != nullptr && distances != nullptr, "octex: NULL tensor");

@@ -25,23 +25,30 @@ def octex():
     return octex_amd
 
 
-def no_alloc(index, q, k, **params):
-    """octexSearchNoAlloc through the C ABI on torch's current stream; device outputs."""
+def call_no_alloc(index, q, I, D, **params):
+    """octexSearchNoAlloc through the C ABI on torch's current stream, into the device outputs I, D; no sync."""
     from octex_amd import _lib
     from octex_amd import index as octex_index
 
     p = octex_index.search_params(**params)
     n, d = q.shape
-    I = torch.full((n, k), -7, dtype=torch.int64, device="cuda")
-    D = torch.full((n, k), float("nan"), dtype=torch.float32, device="cuda")
     stream = ct.c_void_p(torch.cuda.current_stream().cuda_stream)
     _lib.call("octexSearchNoAlloc", ct.byref(p), index.handle, ct.c_void_p(q.data_ptr()), ct.c_int64(n),
-              ct.c_int64(d), ct.c_int64(k), ct.c_void_p(I.data_ptr()), ct.c_void_p(D.data_ptr()), stream)
+              ct.c_int64(d), ct.c_int64(I.shape[1]), ct.c_void_p(I.data_ptr()), ct.c_void_p(D.data_ptr()), stream)
+
+
+def no_alloc(index, q, k, **params):
+    """octexSearchNoAlloc on torch's current stream; results on the host."""
+    n = q.shape[0]
+    I = torch.full((n, k), -7, dtype=torch.int64, device="cuda")
+    D = torch.full((n, k), float("nan"), dtype=torch.float32, device="cuda")
+    call_no_alloc(index, q, I, D, **params)
     torch.cuda.synchronize()
     return D.cpu().numpy(), I.cpu().numpy()
 
 
-@pytest.mark.parametrize("extra", [dict(), dict(sketch_rank=True, final_rerank=32), dict(batch=37)])
+@pytest.mark.parametrize("extra", [dict(), dict(sketch_rank=True, final_rerank=32), dict(batch=37),
+                                   dict(fused_merge=False, balanced_gather=False)])
 def test_no_alloc_equals_search(octex, small_index, extra):
     index = octex.load(small_index["path"])
     Q = small_index["Q"]
@@ -66,3 +73,40 @@ def test_no_alloc_refuses_a_batch_beyond_the_scratch(octex, small_index):
     D, I = no_alloc(index, q[:300], 10, batch=100, **PARAMS)
     Dr, Ir = index.search(q[:300].cpu().numpy(), k=10, batch=100, **PARAMS)
     assert np.array_equal(I, Ir) and np.array_equal(D, Dr)
+
+
+def test_no_alloc_allocates_nothing_and_runs_under_capture(octex, small_index):
+    """The defining property: after a warm-up call, a call leaves the device's free memory unchanged; and the call
+    can be captured into a graph (torch's stream capture), whose replays, with new queries copied into the captured
+    input and eager work and synchronizations between them, each give the eager search's results."""
+    index = octex.load(small_index["path"])
+    Q = np.ascontiguousarray(small_index["Q"][:60])
+    q = torch.from_numpy(Q).cuda()
+    I = torch.full((len(Q), 10), -7, dtype=torch.int64, device="cuda")
+    D = torch.full((len(Q), 10), float("nan"), dtype=torch.float32, device="cuda")
+    call_no_alloc(index, q, I, D, **PARAMS)  # warm-up: code objects loaded, the scratch's address looked up
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info()
+    call_no_alloc(index, q, I, D, **PARAMS)
+    torch.cuda.synchronize()
+    free1, _ = torch.cuda.mem_get_info()
+    print(f"no-alloc: free device memory {free0} before, {free1} after a call", flush=True)
+    assert free1 == free0
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            call_no_alloc(index, q, I, D, **PARAMS)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = np.random.default_rng(5)
+    for rep in range(3):
+        Qr = np.ascontiguousarray(Q[g.permutation(len(Q))]) if rep else Q
+        q.copy_(torch.from_numpy(Qr).cuda())
+        Dr, Ir = index.search(Qr, k=10, **PARAMS)  # eager work between the replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        print(f"no-alloc graph replay {rep}", flush=True)
+        assert np.array_equal(I.cpu().numpy(), Ir) and np.array_equal(D.cpu().numpy(), Dr)
