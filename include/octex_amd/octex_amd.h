@@ -145,10 +145,27 @@ cuvsError_t octexStageGather(int32_t rows, const int32_t* seg, int32_t nseg, int
                              int64_t stride, const int32_t* table, int32_t table_len, int64_t n, const int8_t* code,
                              const float* scale, const float* qs, int32_t S, int32_t W, int32_t* cand,
                              float* dist, int32_t* nout, void* stream);
-/** rerank_keep_kernel (search_kernels.cuh:421-467). */
-cuvsError_t octexStageRerankKeep(const int32_t* cand, const float* dist, const int32_t* nin, int32_t m,
+/** octexStageGather with n_old earlier rounds' candidate rows (device pointers in host arrays: ids, scores, counts
+ * and row widths, as a wave gather of a search reuses them; at most 4): a candidate found there takes its score
+ * from there, the same score; such candidates come last in the row and their count goes to nknown [m] (may be
+ * NULL).  Reuse happens only when the gather keeps its slot lists in LDS; the results are the same either way. */
+cuvsError_t octexStageGatherReuse(int32_t rows, const int32_t* seg, int32_t nseg, int32_t m, const int32_t* lists,
+                                  int64_t stride, const int32_t* table, int32_t table_len, int64_t n,
+                                  const int8_t* code, const float* scale, const float* qs, int32_t S, int32_t W,
+                                  int32_t* cand, float* dist, int32_t* nout, int32_t n_old,
+                                  const int32_t* const* old_cand, const float* const* old_dist,
+                                  const int32_t* const* old_n, const int32_t* old_W, int32_t* nknown, void* stream);
+/** rerank_keep_kernel (search_kernels.cuh:421-467).  Selected candidates with bit 31 set are taken as reranked by an
+ * earlier round of the same kept list (not fresh): they are not reranked or merged again. */
+cuvsError_t octexStageRerankKeep(int32_t* cand, const float* dist, const int32_t* nin, int32_t m,
                                  int32_t W, const void* vectors, int32_t D, const float* Q, int32_t R,
                                  int32_t KO, int64_t* si, float* sd, int32_t fresh, void* stream);
+/** octexStageRerankKeep that also sets bit 31 of every selected candidate in cand (mark) and writes the selected
+ * candidates it did not rerank again to nskip [m] (may be NULL). */
+cuvsError_t octexStageRerankKeepMarked(int32_t* cand, const float* dist, const int32_t* nin, int32_t m, int32_t W,
+                                       const void* vectors, int32_t D, const float* Q, int32_t R, int32_t KO,
+                                       int64_t* si, float* sd, int32_t fresh, int32_t mark, int32_t* nskip,
+                                       void* stream);
 /** sketch_keep_kernel (search_kernels.cuh:471-508). */
 cuvsError_t octexStageSketchKeep(const int32_t* cand, const float* dist, const int32_t* nin, int32_t m,
                                  int32_t W, int32_t KO, int64_t* si, float* sd, int32_t fresh, void* stream);

@@ -6,8 +6,8 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <map>
 #include <mutex>
-#include <set>
 #include <stdexcept>
 #include <string>
 #include <utility>
@@ -114,19 +114,21 @@ inline void upload(void* dst, const void* src, size_t bytes, hipStream_t s)
 }
 
 /**
- * Allow a kernel the CU's whole LDS (160 KiB) as dynamic shared memory, once per kernel and device: later launches,
- * including launches under stream capture, make no other runtime call than the launch itself.
+ * Allow a kernel `bytes` of dynamic LDS on the current device.  The attribute is set only when a launch needs more
+ * than any earlier one of the same kernel on that device, so repeated launches of a plan (including launches under
+ * stream capture) make no other runtime call than the launch itself.
  */
-inline void allow_max_lds(const void* kernel)
+inline void allow_lds(const void* kernel, size_t bytes)
 {
   static std::mutex mu;
-  static std::set<std::pair<const void*, int>> done;
+  static std::map<std::pair<const void*, int>, size_t> set_to;
   int dev = 0;
   OCTEX_HIP(hipGetDevice(&dev));
   std::lock_guard<std::mutex> lock(mu);
-  if (done.count({kernel, dev}) != 0) return;
-  OCTEX_HIP(hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-  done.insert({kernel, dev});
+  auto& cur = set_to[{kernel, dev}];
+  if (bytes <= cur) return;
+  OCTEX_HIP(hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes)));
+  cur = bytes;
 }
 
 inline auto grid_for(int64_t total, int threads) -> unsigned

@@ -440,6 +440,8 @@ __device__ __forceinline__ void sketch_scores(int n, IdOf const& id_of, const si
 /** Per-query state of collect_candidates (LDS). */
 struct collect_state {
   int cnt, nsp, ulen;
+  int hts;  // the hash set's slots
+  int nk;   // candidates whose scores an earlier round's row holds
 };
 
 /**
@@ -507,6 +509,7 @@ __device__ int collect_candidates(const int2* __restrict__ seg, int nseg, const 
   const int HT    = 1 << hash_log_dev(total, logW);
   for (int i = tid; i < HT; i += blockDim.x)
     ht[i] = -1;
+  if (tid == 0) cs.hts = HT;
   __syncthreads();
   const int step = blockDim.x;
   // i / len as (i + 1/2) * fl(1 / len), truncated: the product's relative error is at most 2^-23 (1 + 2^-24), under
@@ -588,6 +591,28 @@ __device__ __forceinline__ int wave_append(bool pred, int* count)
   return pred ? base + __popcll(mask & ((1ULL << lane) - 1ULL)) : -1;
 }
 
+/** Exclusive prefix sum of one int per thread over the workgroup (<= 16 wavefronts); *total gets the sum. */
+__device__ __forceinline__ int block_exclusive_sum(int v, int* wsum, int* total)
+{
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+  int incl = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int u = __shfl_up(incl, d);
+    if (lane >= d) incl += u;
+  }
+  if (lane == 63) wsum[wid] = incl;
+  __syncthreads();
+  int before = 0, all = 0;
+  for (int w = 0; w < nw; w++) {
+    before += w < wid ? wsum[w] : 0;
+    all += wsum[w];
+  }
+  *total = all;
+  __syncthreads();  // wsum may be reused by the caller
+  return before + incl - v;
+}
+
 /**
  * collect_candidates without the load balance (the reference's ablation, gather_warp_kernel of
  * search_kernels.cuh:687-760): wavefront w reads the segments w, w + wavefronts, ... whole, one entry per
@@ -613,6 +638,7 @@ __device__ int collect_segments_whole(const int2* __restrict__ seg, int nseg, co
   const int HT = 1 << hash_log_dev(cs.ulen, logW);
   for (int i = tid; i < HT; i += blockDim.x)
     ht[i] = -1;
+  if (tid == 0) cs.hts = HT;
   __syncthreads();
   for (int c = wid; c < nseg; c += nw) {
     const int2 sl = seg[static_cast<int64_t>(q) * nseg + c];
@@ -644,12 +670,92 @@ __device__ int collect_segments_whole(const int2* __restrict__ seg, int nseg, co
 }
 
 /**
+ * The candidates of query q that earlier rounds scored, taken from their rows instead of scored again.  After
+ * collect_* (the hash set ht of cs.hts slots holds this round's n distinct ids, cl their slots): every id of the old
+ * rows is looked up in ht; the first lookup that finds it sets the entry's kSeenBit and writes the old (id, score) -
+ * the id with its rerank bit - to the end of the query's rows, position n - 1 - k for the k-th one.  The slots of
+ * those candidates are then dropped from cl, in place and in order, so that cl[0, n - nk) lists the candidates left
+ * to score.  Returns n - nk; cs.nk = nk.  The old rows are read whole, with coalesced loads.  Every thread calls it.
+ */
+__device__ int take_known(old_lists const& ol, int q, int n, int* ht, unsigned short* cl, collect_state& cs,
+                          int* wsum, int* crow, float* drow)
+{
+  constexpr int U = 4;  // old entries per thread with their loads in flight together
+  constexpr int E = 8;  // slots per thread per compaction step
+  const int tid = threadIdx.x, nthr = blockDim.x, HT = cs.hts;
+  if (tid == 0) cs.nk = 0;
+  __syncthreads();
+  for (int o = 0; o < ol.count; o++) {  // uniform: every thread walks the same rows
+    const int no      = min(ol.n[o][q], ol.W[o]);
+    const int* oc     = ol.cand[o] + static_cast<int64_t>(q) * ol.W[o];
+    const float* od   = ol.dist[o] + static_cast<int64_t>(q) * ol.W[o];
+    for (int i0 = 0; i0 < no; i0 += nthr * U) {
+      int raw[U];
+      float sc[U];
+#pragma unroll
+      for (int u = 0; u < U; u++) {  // past the end: the last entry (results dropped)
+        const int i = min(i0 + u * nthr + tid, no - 1);
+        raw[u]      = oc[i];
+        sc[u]       = od[i];
+      }
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        const int id = static_cast<int>(static_cast<unsigned>(raw[u]) & ~kSeenBit);
+        bool claim   = false;
+        if (i0 + u * nthr + tid < no) {
+          unsigned h = (static_cast<unsigned>(id) * kIdHash) & (HT - 1);
+          for (int p = 0; p < HT; p++) {
+            const int e = ht[h];
+            if (e == -1) break;  // not a candidate of this round
+            if ((static_cast<unsigned>(e) & ~kSeenBit) == static_cast<unsigned>(id)) {
+              claim = (static_cast<unsigned>(atomicOr(&ht[h], static_cast<int>(kSeenBit))) & kSeenBit) == 0;
+              break;
+            }
+            h = (h + 1) & (HT - 1);
+          }
+        }
+        const int k = wave_append(claim, &cs.nk);
+        if (claim) {
+          crow[n - 1 - k] = raw[u];
+          drow[n - 1 - k] = sc[u];
+        }
+      }
+    }
+  }
+  __syncthreads();
+  const int nk = cs.nk;
+  if (nk == 0) return n;
+  int ubase = 0;  // slots kept so far (uniform)
+  for (int c0 = 0; c0 < n; c0 += nthr * E) {
+    unsigned short sl[E];
+    bool keep[E];
+    int mine = 0;
+#pragma unroll
+    for (int e = 0; e < E; e++) {  // every slot of the step is read before any is written (the sum's barriers)
+      const int j = c0 + tid * E + e;
+      sl[e]       = cl[min(j, n - 1)];
+      keep[e]     = j < n && (static_cast<unsigned>(ht[sl[e]]) & kSeenBit) == 0;
+      mine += keep[e] ? 1 : 0;
+    }
+    int total = 0;
+    int at    = ubase + block_exclusive_sum(mine, wsum, &total);
+#pragma unroll
+    for (int e = 0; e < E; e++)  // at <= the slot's own position: no unread slot is overwritten
+      if (keep[e]) cl[at++] = sl[e];
+    ubase += total;
+  }
+  __syncthreads();
+  return n - nk;
+}
+
+/**
  * Distinct ids of all segments of a query with their sketch scores (collect_candidates, then
  * sketch_scores with LR = the reference's lanes per candidate for this S), written to the query's rows of
  * cand / dist and their count to nout.  The candidates are kept as hash-set slot numbers: 16-bit in LDS
  * (kLdsSlots), or, when they do not fit in LDS beside a large hash set, in the query's own row of cand,
- * where candidate j's slot is read and then overwritten by its id by the one lane group that scores it.  A list
- * gather runs on kGatherListThreads, a row gather on kGatherRowThreads: the row gather's larger hash set leaves room
+ * where candidate j's slot is read and then overwritten by its id by the one lane group that scores it.  With LDS
+ * slots, candidates found in earlier rounds' rows (ol) take their scores from there (take_known) and only the rest
+ * are scored; their count goes to nknown.  A list gather runs on kGatherListThreads, a row gather on kGatherRowThreads: the row gather's larger hash set leaves room
  * for fewer workgroups per CU, so each gets more threads.
  */
 template <bool kRows, int LR, bool kLdsSlots, bool kBalanced>
@@ -657,10 +763,11 @@ __global__ __launch_bounds__(kRows ? kGatherRowThreads : kGatherListThreads) voi
   const int2* __restrict__ seg, int nseg, const long long* __restrict__ list_ptr,
   const int* __restrict__ table, int table_len, int64_t N, const signed char* __restrict__ code,
   const float* __restrict__ scale, const float* __restrict__ qs, int S, int pitch, int W, int logW, int cap,
-  int* __restrict__ cand, float* __restrict__ dist, int* __restrict__ nout)
+  int* __restrict__ cand, float* __restrict__ dist, int* __restrict__ nout, old_lists ol, int* __restrict__ nknown)
 {
   const int q = blockIdx.x;
   extern __shared__ long long smq[];
+  __shared__ int wsum[16];
   const int** sp = reinterpret_cast<const int**>(smq);  // [nseg] first entry of every non-empty segment
   float2* sq     = reinterpret_cast<float2*>(smq + nseg);  // [S] (scale, query sketch) per coordinate
   int* pre       = reinterpret_cast<int*>(sq + S);  // [nseg + 1] exclusive prefix of the compacted lengths
@@ -682,8 +789,12 @@ __global__ __launch_bounds__(kRows ? kGatherRowThreads : kGatherListThreads) voi
     n = collect_candidates<kRows>(seg, nseg, list_ptr, table, table_len, N, logW, cap, sp, pre, ht, cs, keep_slot);
   else
     n = collect_segments_whole<kRows>(seg, nseg, list_ptr, table, table_len, N, logW, cap, ht, cs, keep_slot);
+  int nu = n;  // candidates to score here: the first nu of the row (the rest come from earlier rounds' rows)
+  if constexpr (kLdsSlots) {
+    if (ol.count > 0 && cs.cnt <= cap) nu = take_known(ol, q, n, ht, cl, cs, wsum, crow, drow);
+  }
   sketch_scores<LR>(
-    n,
+    nu,
     [&](int j) {
       if constexpr (kLdsSlots)
         return ht[cl[j]];
@@ -695,13 +806,16 @@ __global__ __launch_bounds__(kRows ? kGatherRowThreads : kGatherListThreads) voi
       crow[j] = id;
       drow[j] = d;
     });
-  if (threadIdx.x == 0) nout[q] = n;
+  if (threadIdx.x == 0) {
+    nout[q] = n;
+    if (nknown != nullptr) nknown[q] = n - nu;
+  }
 }
 
 // ------------------------------------------------------------------ selection and merges
 
 
-constexpr int kBins     = 2048;  // histogram of the two-pass selection
+constexpr int kBins     = 2048;  // histogram of the selection's passes
 constexpr int kTieCap   = 256;   // keys of the threshold bin ranked directly
 constexpr int kSelCache = 8;     // keys per thread held in registers
 
@@ -717,29 +831,82 @@ struct bin_select_lds {
   unsigned hist[kBins / 2];  // two 16-bit bin counts a word (a query has at most 2^15 candidates: no carry)
   unsigned tkey[kTieCap];
   int tid[kTieCap];
+  int tpos[kTieCap];
   bin_select_state bs;
 };
 
+/** An id without its rerank bit (kSeenBit), as the selections order ids. */
+__device__ __forceinline__ unsigned plain_id(int v) { return static_cast<unsigned>(v) & ~kSeenBit; }
+
+/** Bin b's count in the packed histogram. */
+__device__ __forceinline__ unsigned bin_count(bin_select_lds const& sh, int b)
+{
+  return (sh.hist[b >> 1] >> (16 * (b & 1))) & 0xffffu;
+}
+
 /**
- * The R smallest of n (distance, id) pairs of a query by (distance bits, id) (search_kernels.cuh
- * :259-322 with a deterministic tie rule) in two passes over the keys, kSelCache per thread held in
- * registers (the rest are read again): a kBins-bin histogram of (key - kmin) >> shift,
- * shift fitting the keys' range into the bins, gives the bin b* where the count reaches R; keys of
- * lower bins are taken, and the keys of bin b* are ranked by (key, id) among themselves, the
- * R - (count below b*) smallest taken.  The keys of b* are ranked from a buffer of kTieCap entries; when
- * b* holds more (many equal or nearly equal distances), each of them is ranked by a scan over all the
- * keys instead, with the same result.  Selected ids (and keys when skey is set) go to sid / skey in any
- * order; their count is returned in every thread.  All threads of the workgroup call it.
+ * The bin where the running count of the histogram reaches `need` (1 <= need <= the total count): bs.bstar, and in
+ * bs.below the count of the bins before it.  Thread t scans bins [t per, (t + 1) per) after a 64-lane scan of the
+ * per-thread sums.  Every thread calls it; it ends with a barrier.
  */
-__device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, const int* __restrict__ cid, int n,
-                                              int R, int* sid, float* skey, bin_select_lds& sh)
+__device__ __forceinline__ void threshold_bin(bin_select_lds& sh, unsigned need)
 {
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, nthr = blockDim.x;
+  auto& bs      = sh.bs;
+  const int per = kBins / nthr;
+  unsigned s    = 0;
+  for (int b = 0; b < per; b++)
+    s += bin_count(sh, tid * per + b);
+  unsigned incl = s;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const unsigned u = __shfl_up(incl, o);
+    if (lane >= o) incl += u;
+  }
+  if (lane == 63) bs.wtot[wid] = static_cast<int>(incl);
+  __syncthreads();
+  unsigned excl = incl - s;
+  for (int w = 0; w < wid; w++)
+    excl += static_cast<unsigned>(bs.wtot[w]);
+  if (excl < need && need <= excl + s) {
+    unsigned cum = excl;
+    for (int b = 0; b < per; b++) {
+      const unsigned h = bin_count(sh, tid * per + b);
+      if (cum + h >= need) {
+        bs.bstar = tid * per + b;
+        bs.below = static_cast<int>(cum);
+        break;
+      }
+      cum += h;
+    }
+  }
+  __syncthreads();
+}
+
+/**
+ * The R smallest of n (distance, id) pairs of a query by (distance bits, id) (search_kernels.cuh:259-322 with a
+ * deterministic tie rule; ids are compared without their rerank bit) in passes over the keys, kSelCache per thread
+ * held in registers (the rest are read again).
+ * - First pass: a kBins-bin histogram of (key - kmin) >> shift, shift fitting the keys' range into the bins, gives
+ *   the bin b* where the count reaches R.  Keys of lower bins are taken.
+ * - When b* holds at most kTieCap keys, they are ranked by (key, id) among themselves and the R - (count below b*)
+ *   smallest taken.
+ * - Otherwise (many equal or nearly equal distances) the (key, id) pairs of b* are narrowed by further histogram
+ *   passes over the 64-bit values key 2^32 + id, each over a range 2^11 times smaller, until the threshold bin holds
+ *   at most kTieCap pairs (ids being distinct, at most 6 passes): linear in n, as the reference's radix passes.
+ * Selected ids (with their rerank bits), their keys (skey) and their positions in the row (spos) go to sid / skey /
+ * spos in any order; their count (at most R) is returned in every thread.  All threads of the workgroup call it.
+ */
+__device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, const int* __restrict__ cid, int n,
+                                              int R, int* sid, float* skey, int* spos, bin_select_lds& sh)
+{
+  const int tid = threadIdx.x, lane = tid & 63, nthr = blockDim.x;
   auto& bs = sh.bs;
   if (n <= R) {
     for (int i = tid; i < n; i += nthr) {
       sid[i] = cid[i];
       if (skey) skey[i] = __uint_as_float(kd[i]);
+      if (spos) spos[i] = i;
     }
     __syncthreads();
     return n;
@@ -781,57 +948,38 @@ __device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, c
     atomicMax(&bs.kmax, hi);
   }
   __syncthreads();
-  const unsigned kmin = bs.kmin, range = bs.kmax - bs.kmin;
+  const unsigned kmin = bs.kmin, kmax = bs.kmax, range = kmax - kmin;
   const int shift = range < static_cast<unsigned>(kBins) ? 0 : (32 - __clz(static_cast<int>(range))) - 11;
-  // every key with its index, registers first (uniform trip counts: the appends below use ballots)
-  auto for_keys = [&](auto&& f) {
-#pragma unroll
-    for (int j = 0; j < kCache; j++)
-      f(kr[j], tid + j * nthr, kr[j] != kNone);
-    for (int i0 = kCache * nthr; i0 < n; i0 += nthr) {
-      const int i = i0 + tid;
-      f(i < n ? kd[i] : kNone, i, i < n);
-    }
-  };
-  for_keys([&](unsigned k, int, bool ok) {
-    if (ok) {
-      const unsigned b = (k - kmin) >> shift;
+  for (int j = 0; j < kCache; j++) {  // the histogram: register-held keys, then the rest
+    if (kr[j] != kNone) {
+      const unsigned b = (kr[j] - kmin) >> shift;
       atomicAdd(&sh.hist[b >> 1], 1u << (16 * (b & 1)));
     }
-  });
-  __syncthreads();
-  auto count = [&](int b) { return (sh.hist[b >> 1] >> (16 * (b & 1))) & 0xffffu; };
-  // the bin where the running count reaches R: thread t scans bins [t per, (t + 1) per)
-  const int per = kBins / nthr;
-  unsigned s    = 0;
-  for (int b = 0; b < per; b++)
-    s += count(tid * per + b);
-  unsigned incl = s;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const unsigned u = __shfl_up(incl, o);
-    if (lane >= o) incl += u;
   }
-  if (lane == 63) bs.wtot[wid] = static_cast<int>(incl);
-  __syncthreads();
-  unsigned excl = incl - s;
-  for (int w = 0; w < wid; w++)
-    excl += static_cast<unsigned>(bs.wtot[w]);
-  if (excl < static_cast<unsigned>(R) && static_cast<unsigned>(R) <= excl + s) {
-    unsigned cum = excl;
-    for (int b = 0; b < per; b++) {
-      const unsigned h = count(tid * per + b);
-      if (cum + h >= static_cast<unsigned>(R)) {
-        bs.bstar = tid * per + b;
-        bs.below = static_cast<int>(cum);
-        break;
-      }
-      cum += h;
-    }
+  for (int i = tid + kCache * nthr; i < n; i += nthr) {
+    const unsigned b = (kd[i] - kmin) >> shift;
+    atomicAdd(&sh.hist[b >> 1], 1u << (16 * (b & 1)));
   }
   __syncthreads();
+  threshold_bin(sh, static_cast<unsigned>(R));
   const unsigned bstar = static_cast<unsigned>(bs.bstar);
-  const int need       = R - bs.below;
+  int need             = R - bs.below;
+  auto take = [&](bool pred, int id, unsigned key, int pos) {  // append to the selection (every lane calls it)
+    const int at = wave_append(pred, &bs.nsel);
+    if (pred && at < R) {
+      sid[at] = id;
+      if (skey) skey[at] = __uint_as_float(key);
+      if (spos) spos[at] = pos;
+    }
+  };
+  auto to_tie = [&](bool pred, int id, unsigned key, int pos) {  // into the ranked buffer (every lane calls it)
+    const int t = wave_append(pred, &bs.ntb);
+    if (pred && t < kTieCap) {
+      sh.tkey[t] = key;
+      sh.tid[t]  = id;
+      sh.tpos[t] = pos;
+    }
+  };
   // the candidate ids of the cached keys, loaded together before they are placed (unconditional loads of
   // clamped indices: an id read under the per-lane "selected" branch waited for the previous one)
   int ci[kCache];
@@ -840,67 +988,88 @@ __device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, c
     const int i = tid + j * nthr;
     ci[j]       = cid[i < n ? i : 0];
   }
-  auto place = [&](unsigned k, int id, bool ok) {
-    const unsigned b = (k - kmin) >> shift;
-    const int at     = wave_append(ok && b < bstar, &bs.nsel);
-    if (at >= 0) {
-      sid[at] = id;
-      if (skey) skey[at] = __uint_as_float(k);
-    }
-    const int t = wave_append(ok && b == bstar, &bs.ntb);
-    if (t >= 0 && t < kTieCap) {
-      sh.tkey[t] = k;
-      sh.tid[t]  = id;
-    }
-  };
 #pragma unroll
-  for (int j = 0; j < kCache; j++)
-    place(kr[j], ci[j], kr[j] != kNone);
+  for (int j = 0; j < kCache; j++) {
+    const bool ok    = kr[j] != kNone;
+    const unsigned b = (kr[j] - kmin) >> shift;
+    take(ok && b < bstar, ci[j], kr[j], tid + j * nthr);
+    to_tie(ok && b == bstar, ci[j], kr[j], tid + j * nthr);
+  }
   for (int i0 = kCache * nthr; i0 < n; i0 += nthr) {  // keys past the cache: key and id read together
-    const int i  = i0 + tid;
-    const int ii = i < n ? i : 0;
+    const int i       = i0 + tid;
+    const int ii      = i < n ? i : 0;
     const unsigned kv = kd[ii];
     const int id      = cid[ii];
-    place(i < n ? kv : kNone, id, i < n);
+    const unsigned b  = (kv - kmin) >> shift;
+    take(i < n && b < bstar, id, kv, i);
+    to_tie(i < n && b == bstar, id, kv, i);
   }
   __syncthreads();
-  const int ntb = bs.ntb;
-  if (ntb > kTieCap) {  // more keys in bin b* than the buffer holds: rank each against every key of b*
-    for (int i = tid; i < n; i += nthr) {
-      const unsigned ki = kd[i];
-      if (((ki - kmin) >> shift) != bstar) continue;
-      const unsigned ii = static_cast<unsigned>(cid[i]);
-      int rank          = 0;
-      for (int j = 0; j < n; j++) {
-        const unsigned kj = kd[j];
-        if (((kj - kmin) >> shift) == bstar && (kj < ki || (kj == ki && static_cast<unsigned>(cid[j]) < ii))) rank++;
+  // every thread reads the count before the passes below reset it (a wave that read it after thread 0's reset would
+  // skip the passes, and its barriers would pair with the other waves' barriers inside them)
+  const bool many = bs.ntb > kTieCap;
+  __syncthreads();
+  if (many) {
+    // more keys in bin b* than the ranked buffer holds: narrow the (key, id) values of b* by histogram passes
+    const uint64_t blo = static_cast<uint64_t>(kmin) + (static_cast<uint64_t>(bstar) << shift);
+    const uint64_t bhi = min(static_cast<uint64_t>(kmax), blo + ((uint64_t{1} << shift) - 1));
+    uint64_t vlo = blo << 32, vhi = (bhi << 32) | ~kSeenBit;
+    for (;;) {  // uniform: every bound comes from LDS after a barrier
+      const uint64_t vr = vhi - vlo;
+      const int sh2     = vr < static_cast<uint64_t>(kBins) ? 0 : (64 - __clzll(static_cast<long long>(vr))) - 11;
+      for (int i = tid; i < kBins / 2; i += nthr)
+        sh.hist[i] = 0;
+      if (tid == 0) bs.ntb = 0;
+      __syncthreads();
+      for (int i = tid; i < n; i += nthr) {
+        const uint64_t v = (static_cast<uint64_t>(kd[i]) << 32) | plain_id(cid[i]);
+        if (v >= vlo && v <= vhi) {
+          const unsigned b = static_cast<unsigned>((v - vlo) >> sh2);
+          atomicAdd(&sh.hist[b >> 1], 1u << (16 * (b & 1)));
+        }
       }
-      if (rank < need) {
-        const int at = atomicAdd(&bs.nsel, 1);
-        sid[at]      = static_cast<int>(ii);
-        if (skey) skey[at] = __uint_as_float(ki);
+      __syncthreads();
+      threshold_bin(sh, static_cast<unsigned>(need));
+      const int b2        = bs.bstar;
+      const int below2    = bs.below;
+      const bool last     = bin_count(sh, b2) <= static_cast<unsigned>(kTieCap) || sh2 == 0;
+      const uint64_t nlo  = vlo + (static_cast<uint64_t>(b2) << sh2);
+      const uint64_t nhi  = min(vhi, nlo + ((uint64_t{1} << sh2) - 1));
+      for (int i0 = 0; i0 < n; i0 += nthr) {  // uniform trip count: the appends use ballots
+        const int i      = i0 + tid;
+        const int ii     = i < n ? i : 0;
+        const unsigned k = kd[ii];
+        const int id     = cid[ii];
+        const uint64_t v = (static_cast<uint64_t>(k) << 32) | plain_id(id);
+        take(i < n && v >= vlo && v < nlo, id, k, i);
+        to_tie(last && i < n && v >= nlo && v <= nhi, id, k, i);
       }
+      __syncthreads();
+      need -= below2;
+      vlo = nlo;
+      vhi = nhi;
+      if (last) break;
     }
-    __syncthreads();
-    const int ns = bs.nsel;
-    __syncthreads();
-    return ns;
   }
-  for (int i = tid; i < ntb; i += nthr) {  // rank of each tie-bin key by (key, id) among them
-    const unsigned ki = sh.tkey[i], ii = static_cast<unsigned>(sh.tid[i]);
+  const int ntb = min(bs.ntb, kTieCap);
+  for (int i = tid; i < ntb; i += nthr) {  // rank of each ranked-buffer key by (key, id) among them
+    const unsigned ki = sh.tkey[i], ii = plain_id(sh.tid[i]);
     int rank          = 0;
     for (int j = 0; j < ntb; j++) {
-      const unsigned kj = sh.tkey[j], ij = static_cast<unsigned>(sh.tid[j]);
+      const unsigned kj = sh.tkey[j], ij = plain_id(sh.tid[j]);
       rank += (kj < ki || (kj == ki && ij < ii)) ? 1 : 0;
     }
     if (rank < need) {
       const int at = atomicAdd(&bs.nsel, 1);
-      sid[at]      = static_cast<int>(ii);
-      if (skey) skey[at] = __uint_as_float(ki);
+      if (at < R) {
+        sid[at] = sh.tid[i];
+        if (skey) skey[at] = __uint_as_float(ki);
+        if (spos) spos[at] = sh.tpos[i];
+      }
     }
   }
   __syncthreads();
-  const int ns = bs.nsel;
+  const int ns = min(bs.nsel, R);
   __syncthreads();
   return ns;
 }
@@ -1050,28 +1219,6 @@ __device__ __forceinline__ void block_sort(uint64_t (&k)[C], uint64_t* xch)
       bitonic_step<C>(k, xch, 0, size, stride);
 }
 
-/** Exclusive prefix sum of one int per thread over the workgroup (<= 16 wavefronts); *total gets the sum. */
-__device__ __forceinline__ int block_exclusive_sum(int v, int* wsum, int* total)
-{
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
-  int incl = v;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int u = __shfl_up(incl, d);
-    if (lane >= d) incl += u;
-  }
-  if (lane == 63) wsum[wid] = incl;
-  __syncthreads();
-  int before = 0, all = 0;
-  for (int w = 0; w < nw; w++) {
-    before += w < wid ? wsum[w] : 0;
-    all += wsum[w];
-  }
-  *total = all;
-  __syncthreads();  // wsum may be reused by the caller
-  return before + incl - v;
-}
-
 /** LDS of a kept-list merge of up to KEYS keys (C blockDim for the largest C a kernel uses). */
 template <int KEYS>
 struct merge_lds {
@@ -1121,7 +1268,7 @@ __device__ void merge_keep(long long* pb, float* pd, int KO, bool fresh, const i
       const long long id = (!fresh && pb != nullptr) ? pb[i] : -1;
       if (id >= 0) v = dist_key(pd[i], id);
     } else if (i - KO < ns) {
-      v = dist_key(sdv[i - KO], sid[i - KO]);
+      v = dist_key(sdv[i - KO], plain_id(sid[i - KO]));
     }
     k[j] = v;
   }
@@ -1196,12 +1343,18 @@ __host__ __device__ constexpr auto rerank_lds_bytes(int R, int KO, int D, int th
 /**
  * Exact rerank of the R sketch-nearest candidates of a query, merged into its kept list of the best
  * KO (search_kernels.cuh:421-467).  fresh: the kept list starts empty.  One workgroup of NT threads per query.
+ *
+ * Rounds after the first skip what an earlier round reranked.  Whenever the kept list is merged, it becomes the KO
+ * smallest distinct keys of every key merged so far. A selected candidate with kSeenBit was reranked and merged by an
+ * earlier round, so its exact key is either in the kept list already (merging it again changes nothing) or larger than
+ * all KO kept keys (it cannot enter). Dropping it leaves the merge's result unchanged. It is neither read nor merged.
+ * mark: every selected candidate gets kSeenBit in its row of cand, for the rounds after this one.
  */
 template <int LX, int NT>
 __global__ __launch_bounds__(NT) void rerank_keep_kernel(
-  const int* __restrict__ cand, const float* __restrict__ dist, const int* __restrict__ nin, int W,
+  int* __restrict__ cand, const float* __restrict__ dist, const int* __restrict__ nin, int W,
   const __half* __restrict__ vectors, int D, const float* __restrict__ Q, int R, int KO,
-  long long* __restrict__ bi, float* __restrict__ bd, bool fresh)
+  long long* __restrict__ bi, float* __restrict__ bd, bool fresh, bool mark, int* __restrict__ nskip)
 {
   const int q = blockIdx.x;
   extern __shared__ uint64_t rk_lds[];
@@ -1217,15 +1370,41 @@ __global__ __launch_bounds__(NT) void rerank_keep_kernel(
   const int n = min(nin[q], W);
   for (int i = threadIdx.x; i < D; i += blockDim.x)
     sq[i] = Q[static_cast<int64_t>(q) * D + i];
-  const int ns = select_by_bins(reinterpret_cast<const unsigned*>(dist + static_cast<int64_t>(q) * W),
-                                cand + static_cast<int64_t>(q) * W, n, R, sid, nullptr, sel);
-  exact_distances<LX>(sid, ns, vectors, D, sq, sd);
+  int* crow  = cand + static_cast<int64_t>(q) * W;
+  int* spos  = reinterpret_cast<int*>(sd);  // the selected positions, while sd is not yet written
+  const int ns = select_by_bins(reinterpret_cast<const unsigned*>(dist + static_cast<int64_t>(q) * W), crow, n, R,
+                                sid, nullptr, mark ? spos : nullptr, sel);
+  if (mark) {
+    for (int t = threadIdx.x; t < ns; t += NT)
+      crow[spos[t]] = static_cast<int>(static_cast<unsigned>(sid[t]) | kSeenBit);
+    __syncthreads();  // spos (sd) is read before the distances overwrite it
+  }
+  int nr = ns;  // the selected candidates reranked here: those no earlier round reranked (all when fresh)
+  if (!fresh) {
+    constexpr int E = (kMaxRerank + NT - 1) / NT;
+    int v[E], mine = 0;
+    bool keep[E];
+#pragma unroll
+    for (int e = 0; e < E; e++) {  // read before the prefix sum's barriers, written after: in place
+      const int i = threadIdx.x * E + e;
+      v[e]        = i < ns ? sid[i] : 0;
+      keep[e]     = i < ns && (static_cast<unsigned>(v[e]) & kSeenBit) == 0;
+      mine += keep[e] ? 1 : 0;
+    }
+    int at = block_exclusive_sum(mine, mv.wsum, &nr);  // the selection's LDS is free: it ended with a barrier
+#pragma unroll
+    for (int e = 0; e < E; e++)
+      if (keep[e]) sid[at++] = v[e];
+    __syncthreads();
+  }
+  if (nskip != nullptr && threadIdx.x == 0) nskip[q] = ns - nr;
+  exact_distances<LX>(sid, nr, vectors, D, sq, sd);
   long long* pb = bi + static_cast<int64_t>(q) * KO;
   float* pd     = bd + static_cast<int64_t>(q) * KO;
   // exact_distances ended with a barrier: the selection's LDS is free for the merge
-  with_keys_per_thread<kMaxKeepSort / NT>(KO + ns, blockDim.x, [&](auto c) {
+  with_keys_per_thread<kMaxKeepSort / NT>(KO + nr, blockDim.x, [&](auto c) {
     constexpr int C = decltype(c)::value;
-    merge_keep<C>(pb, pd, KO, fresh, sid, sd, ns, pb, pd, KO, mv);
+    merge_keep<C>(pb, pd, KO, fresh, sid, sd, nr, pb, pd, KO, mv);
   });
 }
 
@@ -1245,7 +1424,7 @@ __global__ __launch_bounds__(512) void sketch_keep_kernel(const int* __restrict_
   __shared__ float sdv[kMaxSketchKO];
   const int n  = min(nin[q], W);
   const int ns = select_by_bins(reinterpret_cast<const unsigned*>(dist + static_cast<int64_t>(q) * W),
-                                cand + static_cast<int64_t>(q) * W, n, KO, sid, sdv, u.sel);
+                                cand + static_cast<int64_t>(q) * W, n, KO, sid, sdv, nullptr, u.sel);
   long long* pb = si + static_cast<int64_t>(q) * KO;
   float* pd     = sd + static_cast<int64_t>(q) * KO;
   with_keys_per_thread(KO + ns, blockDim.x, [&](auto c) {
@@ -1744,10 +1923,22 @@ auto gather_smem(int W, int S, int nseg, int max_len, bool lds_slots) -> size_t
 
 namespace {
 
+constexpr size_t kGatherLds = 160 * 1024 - 256;  // the CU's LDS less the kernel's static LDS (state, prefix sums)
+
+}  // namespace
+
+auto gather_lds_slots(int W, int S, int nseg, int max_len) -> bool
+{
+  return gather_smem(W, S, nseg, max_len, true) <= kGatherLds;
+}
+
+namespace {
+
 template <bool kBalanced>
 void gather_impl(bool rows, const int2* seg, int nseg, int max_len, int m, const long long* list_ptr,
                  const int* table, int table_len, int64_t n, const signed char* code, int pitch, const float* scale,
-                 const float* qs, int S, int W, int logW, int* cand, float* dist, int* nout, hipStream_t s)
+                 const float* qs, int S, int W, int logW, int* cand, float* dist, int* nout, old_lists const& old,
+                 int* nknown, hipStream_t s)
 {
   OCTEX_EXPECTS(pitch >= S && pitch % 16 == 0, "octex: sketch rows are at least S bytes apart, 16-byte aligned");
   if (m == 0) return;
@@ -1755,11 +1946,17 @@ void gather_impl(bool rows, const int2* seg, int nseg, int max_len, int m, const
   OCTEX_EXPECTS(max_len >= 0, "octex: segment lengths are non-negative");
   OCTEX_EXPECTS(W == (1 << logW) && W <= kMaxHash, "octex: hash set size");
   OCTEX_EXPECTS(S % 16 == 0 && S >= 16 && S <= 512, "octex: sketch width: a multiple of 16, <= 512");
-  constexpr size_t kLds = 160 * 1024;
-  const bool lds_slots  = gather_smem(W, S, nseg, max_len, true) <= kLds;  // else the slots go to cand
-  const size_t smem     = gather_smem(W, S, nseg, max_len, lds_slots);
-  OCTEX_EXPECTS(smem <= kLds, "octex: gather needs %zu bytes of LDS (max 160 KiB)", smem);
+  const bool lds_slots = gather_lds_slots(W, S, nseg, max_len);  // else the slots go to cand
+  const size_t smem    = gather_smem(W, S, nseg, max_len, lds_slots);
+  OCTEX_EXPECTS(smem <= kGatherLds, "octex: gather needs %zu bytes of LDS (max 160 KiB)", smem);
   const int cap = gather_cap(W, nseg, max_len);
+  OCTEX_EXPECTS(old.count >= 0 && old.count <= kMaxOld, "octex: at most %d earlier candidate rows", kMaxOld);
+  for (int o = 0; o < old.count; o++)
+    OCTEX_EXPECTS(old.cand[o] != nullptr && old.dist[o] != nullptr && old.n[o] != nullptr && old.W[o] >= 1 &&
+                    old.cand[o] != cand,
+                  "octex: an earlier candidate row list is incomplete or is this gather's own output");
+  old_lists ol = old;
+  if (!lds_slots) ol.count = 0;  // the slot list in cand leaves no room for the reused candidates
   int Lr = 1;  // the reference's lanes per candidate: the next power of two >= S / 16, at most 32
   while (Lr < S / 16 && Lr < 32)
     Lr <<= 1;
@@ -1767,9 +1964,10 @@ void gather_impl(bool rows, const int2* seg, int nseg, int max_len, int m, const
     constexpr bool R = decltype(rows_tag)::value;
     constexpr int LR = decltype(lr_tag)::value;
     auto launch      = [&](auto kernel) {
-      allow_max_lds(reinterpret_cast<const void*>(kernel));
+      allow_lds(reinterpret_cast<const void*>(kernel), smem);
       kernel<<<m, R ? kGatherRowThreads : kGatherListThreads, smem, s>>>(
-        seg, nseg, list_ptr, table, table_len, n, code, scale, qs, S, pitch, W, logW, cap, cand, dist, nout);
+        seg, nseg, list_ptr, table, table_len, n, code, scale, qs, S, pitch, W, logW, cap, cand, dist, nout, ol,
+        nknown);
     };
     if (lds_slots)
       launch(&gather_kernel<R, LR, true, kBalanced>);
@@ -1815,19 +2013,19 @@ void sort_rows(uint64_t* keys, int rows, int width, hipStream_t s)
 void launch_gather(bool rows, const int2* seg, int nseg, int max_len, int m, const long long* list_ptr,
                    const int* table, int table_len, int64_t n, const signed char* code, int pitch,
                    const float* scale, const float* qs, int S, int W, int logW, int* cand, float* dist,
-                   int* nout, hipStream_t s)
+                   int* nout, old_lists const& old, int* nknown, hipStream_t s)
 {
   gather_impl<true>(rows, seg, nseg, max_len, m, list_ptr, table, table_len, n, code, pitch, scale, qs, S, W, logW,
-                    cand, dist, nout, s);
+                    cand, dist, nout, old, nknown, s);
 }
 
 void launch_gather_segments(bool rows, const int2* seg, int nseg, int max_len, int m, const long long* list_ptr,
                             const int* table, int table_len, int64_t n, const signed char* code, int pitch,
                             const float* scale, const float* qs, int S, int W, int logW, int* cand, float* dist,
-                            int* nout, hipStream_t s)
+                            int* nout, old_lists const& old, int* nknown, hipStream_t s)
 {
   gather_impl<false>(rows, seg, nseg, max_len, m, list_ptr, table, table_len, n, code, pitch, scale, qs, S, W, logW,
-                     cand, dist, nout, s);
+                     cand, dist, nout, old, nknown, s);
 }
 
 void launch_unfused_keep(const int* cand, const float* dist, const int* nin, int m, int W, const __half* vectors,
@@ -1869,9 +2067,9 @@ void launch_unfused_pick(const long long* si, int m, int KO, long long* done, in
   OCTEX_HIP(hipGetLastError());
 }
 
-void launch_rerank_keep(const int* cand, const float* dist, const int* nin, int m, int W,
+void launch_rerank_keep(int* cand, const float* dist, const int* nin, int m, int W,
                         const __half* vectors, int D, const float* Q, int R, int KO, long long* si,
-                        float* sd, bool fresh, hipStream_t s)
+                        float* sd, bool fresh, bool mark, int* nskip, hipStream_t s)
 {
   if (m == 0) return;
   OCTEX_EXPECTS(R >= 1 && R <= kMaxRerank && KO + R <= kMaxKeepSort && KO >= 1,
@@ -1883,8 +2081,8 @@ void launch_rerank_keep(const int* cand, const float* dist, const int* nin, int 
   const size_t smem = rerank_lds_bytes(R, KO, D, nt);
   with_lx(D, [&](auto lx) {
     auto go = [&](auto kernel) {
-      allow_max_lds(reinterpret_cast<const void*>(kernel));
-      kernel<<<m, nt, smem, s>>>(cand, dist, nin, W, vectors, D, Q, R, KO, si, sd, fresh);
+      allow_lds(reinterpret_cast<const void*>(kernel), smem);
+      kernel<<<m, nt, smem, s>>>(cand, dist, nin, W, vectors, D, Q, R, KO, si, sd, fresh, mark, nskip);
     };
     if (nt == 256)
       go(&rerank_keep_kernel<decltype(lx)::value, 256>);

@@ -91,13 +91,25 @@ extern "C" cuvsError_t octexStageProbe(const void* Y, int32_t m, int32_t C, int3
   });
 }
 
-extern "C" cuvsError_t octexStageGather(int32_t rows, const int32_t* seg, int32_t nseg, int32_t m,
-                                        const int32_t* lists, int64_t stride, const int32_t* table,
-                                        int32_t table_len, int64_t n, const int8_t* code, const float* scale, const float* qs,
-                                        int32_t S, int32_t W, int32_t* cand, float* dist, int32_t* nout,
-                                        void* stream)
+extern "C" cuvsError_t octexStageGatherReuse(int32_t rows, const int32_t* seg, int32_t nseg, int32_t m,
+                                             const int32_t* lists, int64_t stride, const int32_t* table,
+                                             int32_t table_len, int64_t n, const int8_t* code, const float* scale,
+                                             const float* qs, int32_t S, int32_t W, int32_t* cand, float* dist,
+                                             int32_t* nout, int32_t n_old, const int32_t* const* old_cand,
+                                             const float* const* old_dist, const int32_t* const* old_n,
+                                             const int32_t* old_W, int32_t* nknown, void* stream)
 {
   return run(stream, [&](hipStream_t s) {
+    OCTEX_EXPECTS(n_old >= 0 && n_old <= kMaxOld, "octex: at most %d earlier candidate rows", kMaxOld);
+    old_lists ol;
+    for (int o = 0; o < n_old; o++) {
+      need(old_cand, "old_cand"), need(old_dist, "old_dist"), need(old_n, "old_n"), need(old_W, "old_W");
+      ol.cand[o] = old_cand[o];
+      ol.dist[o] = old_dist[o];
+      ol.n[o]    = old_n[o];
+      ol.W[o]    = old_W[o];
+    }
+    ol.count = n_old;
     need(seg, "seg"), need(code, "code"), need(scale, "scale"), need(qs, "qs");
     need(cand, "cand"), need(dist, "dist"), need(nout, "nout");
     if (rows)
@@ -122,22 +134,40 @@ extern "C" cuvsError_t octexStageGather(int32_t rows, const int32_t* seg, int32_
     }
     launch_gather(rows != 0, reinterpret_cast<const int2*>(seg), nseg, max_len, m, ptrs.as<long long>(), table, table_len,
                   n, reinterpret_cast<const signed char*>(code), S, scale, qs, S, W, log2_ceil(W), cand, dist,
-                  nout, s);
+                  nout, ol, nknown, s);
     OCTEX_HIP(hipStreamSynchronize(s));
   });
 }
 
-extern "C" cuvsError_t octexStageRerankKeep(const int32_t* cand, const float* dist, const int32_t* nin,
-                                            int32_t m, int32_t W, const void* vectors, int32_t D, const float* Q,
-                                            int32_t R, int32_t KO, int64_t* si, float* sd, int32_t fresh,
-                                            void* stream)
+extern "C" cuvsError_t octexStageGather(int32_t rows, const int32_t* seg, int32_t nseg, int32_t m,
+                                        const int32_t* lists, int64_t stride, const int32_t* table,
+                                        int32_t table_len, int64_t n, const int8_t* code, const float* scale, const float* qs,
+                                        int32_t S, int32_t W, int32_t* cand, float* dist, int32_t* nout,
+                                        void* stream)
+{
+  return octexStageGatherReuse(rows, seg, nseg, m, lists, stride, table, table_len, n, code, scale, qs, S, W, cand,
+                               dist, nout, 0, nullptr, nullptr, nullptr, nullptr, nullptr, stream);
+}
+
+extern "C" cuvsError_t octexStageRerankKeepMarked(int32_t* cand, const float* dist, const int32_t* nin, int32_t m,
+                                                  int32_t W, const void* vectors, int32_t D, const float* Q, int32_t R,
+                                                  int32_t KO, int64_t* si, float* sd, int32_t fresh, int32_t mark,
+                                                  int32_t* nskip, void* stream)
 {
   return run(stream, [&](hipStream_t s) {
     need(cand, "cand"), need(dist, "dist"), need(nin, "nin"), need(vectors, "vectors"), need(Q, "Q");
     need(si, "si"), need(sd, "sd");
     launch_rerank_keep(cand, dist, nin, m, W, static_cast<const __half*>(vectors), D, Q, R, KO,
-                       reinterpret_cast<long long*>(si), sd, fresh != 0, s);
+                       reinterpret_cast<long long*>(si), sd, fresh != 0, mark != 0, nskip, s);
   });
+}
+
+extern "C" cuvsError_t octexStageRerankKeep(int32_t* cand, const float* dist, const int32_t* nin,
+                                            int32_t m, int32_t W, const void* vectors, int32_t D, const float* Q,
+                                            int32_t R, int32_t KO, int64_t* si, float* sd, int32_t fresh,
+                                            void* stream)
+{
+  return octexStageRerankKeepMarked(cand, dist, nin, m, W, vectors, D, Q, R, KO, si, sd, fresh, 0, nullptr, stream);
 }
 
 extern "C" cuvsError_t octexStageSketchKeep(const int32_t* cand, const float* dist, const int32_t* nin,

@@ -449,3 +449,171 @@ def test_row_layouts_match_oracle(L, D, S):
             si[q], sd[q] = ri, rd
         dist = dist + g.uniform(0, 4, dist.shape).astype(np.float32)  # the second round: another sketch order
         dd = dev(dist)
+
+
+# ---------------------------------------------------------------- reuse of earlier rounds' rows
+
+SEEN = np.int32(-(2**31))  # bit 31 of an id: "an earlier round's exact rerank took it"
+
+
+def plain(a):
+    return np.asarray(a) & np.int32(0x7FFFFFFF)
+
+
+def gather_reuse_gpu(L, ix, dix, seg, qs, old, W=4096):
+    """octexStageGatherReuse over table rows with the earlier rows `old` [(cand, dist, n, W)] (device tensors)."""
+    m, nseg = seg.shape[0], seg.shape[1]
+    cand = torch.full((m, W), -5, dtype=torch.int32, device="cuda")
+    dist = torch.zeros((m, W), dtype=torch.float32, device="cuda")
+    nout = torch.zeros(m, dtype=torch.int32, device="cuda")
+    nk = torch.full((m,), -1, dtype=torch.int32, device="cuda")
+    dqs, dseg = dev(qs), dev(seg)
+    k = len(old)
+    oc = (ct.c_void_p * max(k, 1))(*[o[0].data_ptr() for o in old])
+    od = (ct.c_void_p * max(k, 1))(*[o[1].data_ptr() for o in old])
+    on = (ct.c_void_p * max(k, 1))(*[o[2].data_ptr() for o in old])
+    ow = (ct.c_int32 * max(k, 1))(*[o[3] for o in old])
+    L.call("octexStageGatherReuse", i32(1), P(dseg), i32(nseg), i32(m), P(dix["lists"]), i64(ix.lists.shape[1]),
+           P(dix["table"]), i32(ix.table_len), i64(ix.n), P(dix["sketch"]), P(dix["scale"]), P(dqs),
+           i32(ix.sketch_width), i32(W), P(cand), P(dist), P(nout), i32(k), oc, od, on, ow, P(nk), None)
+    return cand, dist, nout, nk
+
+
+def test_gather_reuses_earlier_rows(L, ix, dix):
+    """A wave gather given earlier rounds' rows: the same candidate set and bit-identical scores as the oracle's
+    gather (which scores every candidate); the candidates found in the earlier rows are counted in nknown and keep
+    those rows' rerank bits; an id in two earlier rows is taken once."""
+    g = np.random.default_rng(21)
+    m, S, W = 40, 64, 4096
+    qs = g.standard_normal((m, ix.sketch_width)).astype(np.float32)
+    starts_a = g.integers(0, ix.n, (m, S))
+    seg_a = np.stack([starts_a, np.full((m, S), ix.table_len)], -1).astype(np.int32)
+    seg_a[:, -5:] = 0
+    ca, da, na = gather_gpu(L, ix, dix, dev(seg_a), qs, rows=1, W=W)
+    # rerank bits on a third of the first row's candidates, as a marked rerank leaves them
+    marked = g.random(ca.shape) < 0.33
+    ca_m = np.where(marked & (np.arange(W)[None, :] < na[:, None]), ca | SEEN, ca).astype(np.int32)
+    # a second earlier row: other starts, partly the same
+    starts_b = np.where(g.random((m, S)) < 0.5, starts_a, g.integers(0, ix.n, (m, S)))
+    seg_b = np.stack([starts_b, np.full((m, S), ix.table_len)], -1).astype(np.int32)
+    cb, db, nb = gather_gpu(L, ix, dix, dev(seg_b), qs, rows=1, W=W)
+    # this wave: half its starts from the first row's starts
+    starts_c = np.where(g.random((m, S)) < 0.5, starts_a, g.integers(0, ix.n, (m, S)))
+    seg_c = np.stack([starts_c, np.full((m, S), ix.table_len)], -1).astype(np.int32)
+    seg_c[:, :3] = 0
+    seg_c[1] = 0  # a query without starts
+    old = [(dev(ca_m), dev(da), dev(na), W), (dev(cb), dev(db), dev(nb), W)]
+    cand, dist, nout, nk = (host(t) for t in gather_reuse_gpu(L, ix, dix, seg_c, qs, old, W=W))
+    check_gather(ix, seg_c, qs, plain(cand), dist, nout, rows=True)
+    for q in range(m):
+        n = nout[q]
+        ids = plain(cand[q, :n])
+        seen_a = {int(v) for v in ca[q, : na[q]]}
+        seen = seen_a | {int(v) for v in cb[q, : nb[q]]}
+        known = [int(v) in seen for v in ids]
+        assert nk[q] == sum(known), f"query {q}"
+        assert not any(known[: n - nk[q]]) and all(known[n - nk[q] :]), f"query {q}: known candidates come last"
+        bit_a = {int(v) for v, mk in zip(ca[q, : na[q]], marked[q, : na[q]]) if mk}
+        want_bit = np.array([int(v) in bit_a for v in ids])
+        assert np.array_equal(cand[q, :n] < 0, want_bit), f"query {q}: rerank bits"
+    assert nout[1] == 0 and nk[1] == 0
+    assert nk.sum() > 0.2 * nout.sum()  # half the starts repeat: many candidates come from the earlier rows
+
+
+def test_marked_rerank_rounds_match_oracle(L, ix, dix, small_index):
+    """Two rounds of the fused rerank as a search runs them: the first (fresh) marks what it selects; the second, over
+    candidate rows that hold some of those marked ids with the same sketch scores (a query's scores do not change),
+    skips them and still gives the oracle's kept list exactly (the oracle reranks everything)."""
+    g = np.random.default_rng(22)
+    m, W, KO, R = 32, 4096, 64, 96
+    Q = small_index["Q"][:m]
+    score = g.uniform(0, 100, ix.n).astype(np.float32)  # one sketch score per id, as within one query's search
+    n1 = g.integers(200, 2000, m).astype(np.int32)
+    n1[0] = 50  # fewer candidates than R: all selected
+    c1 = np.full((m, W), -9, np.int32)
+    d1 = np.zeros((m, W), np.float32)
+    for q in range(m):
+        c1[q, : n1[q]] = g.choice(ix.n, n1[q], replace=False)
+        d1[q, : n1[q]] = score[c1[q, : n1[q]]]
+    si = np.full((m, KO), -1, np.int64)
+    sd = np.full((m, KO), np.inf, np.float32)
+    dc1, dd1, dn1, dQ, dsi, dsd = dev(c1), dev(d1), dev(n1), dev(Q), dev(si), dev(sd)
+    nskip = torch.full((m,), -1, dtype=torch.int32, device="cuda")
+    L.call("octexStageRerankKeepMarked", P(dc1), P(dd1), P(dn1), i32(m), i32(W), P(dix["vectors"]), i32(ix.dim),
+           P(dQ), i32(R), i32(KO), P(dsi), P(dsd), i32(1), i32(1), P(nskip), None)
+    gc1 = host(dc1)
+    for q in range(m):
+        sel, _ = O.select(c1[q, : n1[q]], d1[q, : n1[q]], R)
+        ri, rd = O.rerank_keep(ix, c1[q, : n1[q]], d1[q, : n1[q]], Q[q], R, si[q], sd[q], True)
+        assert np.array_equal(host(dsi)[q], ri) and np.array_equal(host(dsd)[q], rd), f"query {q}"
+        si[q], sd[q] = ri, rd
+        got = {int(v) for v in plain(gc1[q, : n1[q]][gc1[q, : n1[q]] < 0])}
+        assert got == {int(v) for v in sel}, f"query {q}: marked ids"
+        assert np.array_equal(plain(gc1[q, : n1[q]]), c1[q, : n1[q]])
+    # the second round: about half of each row from the first round's candidates (with their marks), half new
+    n2 = g.integers(300, 2500, m).astype(np.int32)
+    c2 = np.full((m, W), -9, np.int32)
+    d2 = np.zeros((m, W), np.float32)
+    for q in range(m):
+        old = gc1[q, : n1[q]]
+        k_old = min(len(old), n2[q] // 2)
+        pick = old[g.choice(len(old), k_old, replace=False)]
+        fresh_ids = np.setdiff1d(np.arange(ix.n), plain(old))
+        new = g.choice(fresh_ids, n2[q] - k_old, replace=False).astype(np.int32)
+        row = np.concatenate([pick, new])[g.permutation(n2[q])]
+        c2[q, : n2[q]] = row
+        d2[q, : n2[q]] = score[plain(row)]
+    dc2, dd2, dn2 = dev(c2), dev(d2), dev(n2)
+    L.call("octexStageRerankKeepMarked", P(dc2), P(dd2), P(dn2), i32(m), i32(W), P(dix["vectors"]), i32(ix.dim),
+           P(dQ), i32(R), i32(KO), P(dsi), P(dsd), i32(0), i32(1), P(nskip), None)
+    sk = host(nskip)
+    for q in range(m):
+        ids = plain(c2[q, : n2[q]])
+        ri, rd = O.rerank_keep(ix, ids, d2[q, : n2[q]], Q[q], R, si[q], sd[q], False)
+        assert np.array_equal(host(dsi)[q], ri) and np.array_equal(host(dsd)[q], rd), f"query {q}"
+        sel, _ = O.select(ids, d2[q, : n2[q]], R)
+        was = {int(v) for v in plain(gc1[q, : n1[q]][gc1[q, : n1[q]] < 0])}
+        assert sk[q] == sum(int(v) in was for v in sel), f"query {q}: skipped reranks"
+    assert sk.sum() > 0
+
+
+@pytest.mark.parametrize("kind", ["equal", "few"])
+def test_selection_of_many_equal_keys_at_the_largest_width(L, ix, dix, small_index, kind):
+    """Candidate rows of 2^15 slots whose threshold bin holds thousands of keys (all equal, or three values): the
+    selection narrows them by further histogram passes over (key, id) and takes the smallest ids, as the oracle;
+    through the sketch merge (up to 30,000 candidates, KO 1000) and the exact rerank (every id of the index)."""
+    g = np.random.default_rng(23)
+    m, W = 12, 1 << 15
+
+    def rows(n_max, N):
+        cand = np.full((m, W), -9, np.int32)
+        dist = np.zeros((m, W), np.float32)
+        nin = g.integers(n_max // 2, n_max, m).astype(np.int32)
+        nin[0] = n_max
+        for q in range(m):
+            n = nin[q]
+            cand[q, :n] = g.choice(N, n, replace=False)
+            dist[q, :n] = 7.25 if kind == "equal" else g.integers(0, 3, n).astype(np.float32)
+        return cand, dist, nin
+
+    cand, dist, nin = rows(30_000, 1_000_000)
+    KO = 1000
+    si = torch.full((m, KO), -1, dtype=torch.int64, device="cuda")
+    sd = torch.full((m, KO), float("inf"), dtype=torch.float32, device="cuda")
+    dc, dd, dn = dev(cand), dev(dist), dev(nin)
+    L.call("octexStageSketchKeep", P(dc), P(dd), P(dn), i32(m), i32(W), i32(KO), P(si), P(sd), i32(1), None)
+    for q in range(m):
+        ri, rd = O.sketch_keep(cand[q, : nin[q]], dist[q, : nin[q]], np.full(KO, -1, np.int64),
+                               np.full(KO, np.inf, np.float32), True)
+        assert np.array_equal(host(si)[q], ri) and np.array_equal(host(sd)[q], rd), f"sketch_keep query {q}"
+    cand, dist, nin = rows(ix.n, ix.n)
+    KO, R = 64, 512
+    Q = small_index["Q"][:m]
+    si = np.full((m, KO), -1, np.int64)
+    sd = np.full((m, KO), np.inf, np.float32)
+    dsi, dsd, dc, dd, dn, dQ = dev(si), dev(sd), dev(cand), dev(dist), dev(nin), dev(Q)
+    L.call("octexStageRerankKeep", P(dc), P(dd), P(dn), i32(m), i32(W), P(dix["vectors"]), i32(ix.dim), P(dQ),
+           i32(R), i32(KO), P(dsi), P(dsd), i32(1), None)
+    for q in range(m):
+        ri, rd = O.rerank_keep(ix, cand[q, : nin[q]], dist[q, : nin[q]], Q[q], R, si[q], sd[q], True)
+        assert np.array_equal(host(dsi)[q], ri) and np.array_equal(host(dsd)[q], rd), f"rerank_keep query {q}"
