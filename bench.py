@@ -28,22 +28,25 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor figure
 
-# Cell lists: the workloads of 1M rows and more build member lists (the reference's fast build mode, --member-lists /
-# octex_build --fast): its default IVF lists run k-means and a probed list search for every copy, too long for a
-# benchmark session at 100M rows.  cpu100k builds the reference's default index, IVF lists included.
+# Cell lists, per workload (every BENCH line records its index parameters in config.index):
+# - sift1m and gist1m: exact lists, as the reference's paper builds (bench/paper_build.sh:29-30, --exact-lists);
+# - deep100m and deep100m-host: member lists, the reference's fast build mode (--member-lists).  The paper's Deep100M
+#   build uses the default IVF lists (bench/paper_build.sh:36), whose k-means and probed list search over 100M rows for
+#   every copy do not fit a GPU session here; member lists hold members of the query's cell instead of the rows
+#   nearest to its center, so this index is not the paper's;
+# - cpu100k: the reference's default index, IVF lists included.
 CONFIGS = {
-    # configs[1] of BASELINE.json; the index as the reference's paper SIFT1M build (copies 200, lists of 32, no
-    # reverse edges) with the reference's default sketch width for d = 128 (128), cells of >= 2 rows for lists
+    # configs[1] of BASELINE.json; the index as the reference's paper SIFT1M build (copies 200, lists of 32, exact
+    # lists, table 64, no reverse edges) with the reference's default sketch width for d = 128 (128; the paper's 64)
     "sift1m": dict(n=1_000_000, d=128, nq=10_000, clusters=1000, kind="sift", batch=10_000,
                    desc="seeded Gaussian mixture as BASELINE.json configs[1]",
-                   index=dict(copies=200, list_len=32, table_len=64, min_cell=2, reverse_edges=False, member_lists=True,
-                              seed=0),
+                   index=dict(copies=200, list_len=32, table_len=64, reverse_edges=False, exact_lists=True, seed=0),
                    point=dict(read=4, starts=16, waves=1, rerank=16, wave_rerank=16)),
     # configs[3] of BASELINE.json: 100M L2-normalized rows, d = 96, of a 10,000-component mixture (centroids N(0, 1),
-    # sigma 0.4) stored fp16; the index as the reference's paper Deep100M build (lists of 64, cells of >= 10 rows,
-    # table 64) with the reference's default sketch width for d = 96 (96: this mixture's variance is spread over
-    # all 96 PCA axes, so a 64-wide sketch ranks poorly), and as many copies as fit one MI355X's 288 GB next to
-    # the vectors, sketch, table and search buffers (1.3 GB of lists per copy on this data)
+    # sigma 0.4) stored fp16; the index shaped as the reference's paper Deep100M build (lists of 64, cells of >= 10
+    # rows, table 64) but with member lists (see above), the reference's default sketch width for d = 96 (96: this
+    # mixture's variance is spread over all 96 PCA axes, so a 64-wide sketch ranks poorly), and as many copies as fit
+    # one MI355X's 288 GB next to the vectors, sketch, table and search buffers (1.3 GB of lists per copy here)
     "deep100m": dict(n=100_000_000, d=96, nq=10_000, clusters=10_000, kind="deep", batch=10_000,
                      desc="seeded normalized Gaussian mixture as BASELINE.json configs[3], fp16 rows",
                      index=dict(copies=150, list_len=64, min_cell=10, table_len=64, member_lists=True, seed=0),
@@ -62,13 +65,12 @@ CONFIGS = {
                                      final_rerank=32)),
     # configs[2] of BASELINE.json: 1M x 960 non-negative half-normal features (scale 0.05) plus per-cluster offsets
     # U[0, 0.1] of a 1,000-component mixture, 1,000 queries, batch 1,000; the index as the reference's paper GIST
-    # build (lists of 64, sketch 128, exact table of 64, no reverse edges) with 150 copies and member lists of cells
-    # of >= 16 rows (the paper's exact lists, --index-params '{"exact_lists": true}', cost 80 s more to build here
-    # and give the same recall on this data)
+    # build (lists of 64, exact lists, sketch 128, exact table of 64, no reverse edges) with 150 copies (the paper's
+    # 400 do not fit next to this index's arrays: 0.70 GB a copy)
     "gist1m": dict(n=1_000_000, d=960, nq=1_000, clusters=1000, kind="gist", batch=1_000,
                    desc="seeded half-normal mixture as BASELINE.json configs[2]",
-                   index=dict(copies=150, list_len=64, min_cell=16, table_len=64, sketch_width=128, reverse_edges=False,
-                              member_lists=True, seed=0),
+                   index=dict(copies=150, list_len=64, table_len=64, sketch_width=128, reverse_edges=False,
+                              exact_lists=True, seed=0),
                    point=dict(read=32, starts=64, waves=3, rerank=512, wave_rerank=512)),
     # configs[0] of BASELINE.json, the reference's CPU-runnable case: 100k rows, d = 128, of a 100-component
     # Gaussian mixture (centroids N(0, 1), sigma 0.3), 1,000 queries, the reference's default index (200 copies,
@@ -308,14 +310,22 @@ def stage_bytes(name, wave, cnt, m, C, S, D, KO, table_len, starts, w, L, FR=0, 
         return cnt["distinct2"][wave] * 8 + m * 24 * KO
     if name == "final_rerank":  # FR rows per query (from host memory when the vectors are there)
         return m * (FR * 2 * D + 12 * KO + 4 * D + 12 * k)
+    # the fused search: each gather ends by selecting its round's R candidates from the row it wrote (read back, 8
+    # bytes a candidate; the ids out, 4 bytes each) and the exact rerank reads those ids
     if name == "gather_lists":
-        return m * C * 8 + cnt["entries1"] * 4 + cnt["distinct1"] * (S + 8) + m * (S * 4 + 4)
-    if name == "gather_rows":
-        return m * starts * 8 + cnt["starts2"][wave] * table_len * 4 + cnt["distinct2"][wave] * (S + 8) + m * (S * 4 + 4)
+        return (m * C * 8 + cnt["entries1"] * 4 + cnt["distinct1"] * (S + 8) + m * (S * 4 + 4)
+                + cnt["distinct1"] * 8 + cnt["reranked1"] * 4)
+    if name == "gather_rows":  # sketch rows of the candidates no earlier round scored; 8 bytes per earlier-row entry
+        known = cnt.get("known2", [0] * 16)[wave]
+        old = cnt.get("oldread2", [0] * 16)[wave]
+        return (m * starts * 8 + cnt["starts2"][wave] * table_len * 4 + (cnt["distinct2"][wave] - known) * S
+                + cnt["distinct2"][wave] * 8 + old * 8 + m * (S * 4 + 4)
+                + cnt["distinct2"][wave] * 8 + cnt["reranked2"][wave] * 4)
     if name == "rerank_keep":
-        return cnt["distinct1"] * 8 + cnt["reranked1"] * 2 * D + m * (12 * KO + 4 * D + 4)
-    if name == "rerank_keep_wave":
-        return cnt["distinct2"][wave] * 8 + cnt["reranked2"][wave] * 2 * D + m * (24 * KO + 4 * D + 4)
+        return cnt["reranked1"] * (4 + 2 * D) + m * (12 * KO + 4 * D + 4)
+    if name == "rerank_keep_wave":  # rows of the selected candidates no earlier round reranked
+        skipped = cnt.get("skipped2", [0] * 16)[wave]
+        return cnt["reranked2"][wave] * 4 + (cnt["reranked2"][wave] - skipped) * 2 * D + m * (24 * KO + 4 * D + 4)
     if name == "probe":  # Y rows and segments out; an offsets pair and a key per level tried (finest first)
         tried = sum((j + 1) * h for j, h in enumerate(cnt["hit_level"])) + L * (m * C - cnt["seg_hits"])
         return m * C * (2 * w + 8) + tried * (8 + 8)
@@ -571,6 +581,12 @@ def main():
     achieved = avg_bytes / (avg_ms * 1e-3) / 1e9
     traffic, traffic_source = measured_traffic(args.config, params, dominant, X.shape[0], avg_bytes)
     log(f"probe hits by level {cnt['hit_level'][:int(meta[4])]}, misses {len(Q) * C - cnt['seg_hits']}")
+    nw = params.get("waves", 0)
+    if nw:
+        log("waves: distinct " + str(cnt["distinct2"][:nw]) + ", scored in earlier rounds " + str(cnt["known2"][:nw])
+            + f" ({', '.join(f'{k / max(d, 1):.3f}' for k, d in zip(cnt['known2'][:nw], cnt['distinct2'][:nw]))})"
+            + ", earlier-row entries read " + str(cnt["oldread2"][:nw]) + ", reranked " + str(cnt["reranked2"][:nw])
+            + ", of them not reranked again " + str(cnt["skipped2"][:nw]))
     log("stages: " + ", ".join(f"{x['stage']}[{x['wave']}] {x['ms']:.3f} ms {x['gbs']} GB/s" for x in per_launch))
 
     # CPU baseline: the oracle (C++ restatement of the search) on the same index, a bounded query sample
@@ -638,6 +654,10 @@ def main():
             "index_gib": round(index.device_bytes[0] / 2**30, 2),
             "sweep": points,
             "stages": per_launch,
+            # per wave: distinct candidates, those whose sketch scores came from earlier rounds' rows (no sketch row
+            # read), earlier-row entries read, selected for the exact rerank, and of those reranked by an earlier round
+            "wave_reuse": {key: cnt[key][: params.get("waves", 0)]
+                           for key in ("distinct2", "known2", "oldread2", "reranked2", "skipped2")},
         },
         "roofline": {
             "bound": "hbm",

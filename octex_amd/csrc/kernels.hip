@@ -191,11 +191,11 @@ __global__ __launch_bounds__(256) void sketch_query_kernel(const float* __restri
                                                            const float* __restrict__ basis, int m, int D,
                                                            int S, float* __restrict__ qs)
 {
-  extern __shared__ float rows[];  // [16, D]
+  extern __shared__ float qrows[];  // [16, D]
   const int q0 = blockIdx.y * 16, s = blockIdx.x * 64 + (threadIdx.x & 63), ty = threadIdx.x >> 6;
   for (int i = threadIdx.x; i < 16 * D; i += blockDim.x) {
     const int q = q0 + i / D;
-    rows[i]     = q < m ? qc[static_cast<int64_t>(q) * D + i % D] : 0.f;
+    qrows[i]     = q < m ? qc[static_cast<int64_t>(q) * D + i % D] : 0.f;
   }
   __syncthreads();
   if (s >= S) return;
@@ -204,7 +204,7 @@ __global__ __launch_bounds__(256) void sketch_query_kernel(const float* __restri
     const float b = basis[static_cast<int64_t>(d) * S + s];
 #pragma unroll
     for (int r = 0; r < 4; r++)
-      acc[r] = fmaf(rows[(4 * ty + r) * D + d], b, acc[r]);
+      acc[r] = fmaf(qrows[(4 * ty + r) * D + d], b, acc[r]);
   }
 #pragma unroll
   for (int r = 0; r < 4; r++) {
@@ -669,151 +669,7 @@ __device__ int collect_segments_whole(const int2* __restrict__ seg, int nseg, co
   return min(cs.cnt, cap);
 }
 
-/**
- * The candidates of query q that earlier rounds scored, taken from their rows instead of scored again.  After
- * collect_* (the hash set ht of cs.hts slots holds this round's n distinct ids, cl their slots): every id of the old
- * rows is looked up in ht; the first lookup that finds it sets the entry's kSeenBit and writes the old (id, score) -
- * the id with its rerank bit - to the end of the query's rows, position n - 1 - k for the k-th one.  The slots of
- * those candidates are then dropped from cl, in place and in order, so that cl[0, n - nk) lists the candidates left
- * to score.  Returns n - nk; cs.nk = nk.  The old rows are read whole, with coalesced loads.  Every thread calls it.
- */
-__device__ int take_known(old_lists const& ol, int q, int n, int* ht, unsigned short* cl, collect_state& cs,
-                          int* wsum, int* crow, float* drow)
-{
-  constexpr int U = 4;  // old entries per thread with their loads in flight together
-  constexpr int E = 8;  // slots per thread per compaction step
-  const int tid = threadIdx.x, nthr = blockDim.x, HT = cs.hts;
-  if (tid == 0) cs.nk = 0;
-  __syncthreads();
-  for (int o = 0; o < ol.count; o++) {  // uniform: every thread walks the same rows
-    const int no      = min(ol.n[o][q], ol.W[o]);
-    const int* oc     = ol.cand[o] + static_cast<int64_t>(q) * ol.W[o];
-    const float* od   = ol.dist[o] + static_cast<int64_t>(q) * ol.W[o];
-    for (int i0 = 0; i0 < no; i0 += nthr * U) {
-      int raw[U];
-      float sc[U];
-#pragma unroll
-      for (int u = 0; u < U; u++) {  // past the end: the last entry (results dropped)
-        const int i = min(i0 + u * nthr + tid, no - 1);
-        raw[u]      = oc[i];
-        sc[u]       = od[i];
-      }
-#pragma unroll
-      for (int u = 0; u < U; u++) {
-        const int id = static_cast<int>(static_cast<unsigned>(raw[u]) & ~kSeenBit);
-        bool claim   = false;
-        if (i0 + u * nthr + tid < no) {
-          unsigned h = (static_cast<unsigned>(id) * kIdHash) & (HT - 1);
-          for (int p = 0; p < HT; p++) {
-            const int e = ht[h];
-            if (e == -1) break;  // not a candidate of this round
-            if ((static_cast<unsigned>(e) & ~kSeenBit) == static_cast<unsigned>(id)) {
-              claim = (static_cast<unsigned>(atomicOr(&ht[h], static_cast<int>(kSeenBit))) & kSeenBit) == 0;
-              break;
-            }
-            h = (h + 1) & (HT - 1);
-          }
-        }
-        const int k = wave_append(claim, &cs.nk);
-        if (claim) {
-          crow[n - 1 - k] = raw[u];
-          drow[n - 1 - k] = sc[u];
-        }
-      }
-    }
-  }
-  __syncthreads();
-  const int nk = cs.nk;
-  if (nk == 0) return n;
-  int ubase = 0;  // slots kept so far (uniform)
-  for (int c0 = 0; c0 < n; c0 += nthr * E) {
-    unsigned short sl[E];
-    bool keep[E];
-    int mine = 0;
-#pragma unroll
-    for (int e = 0; e < E; e++) {  // every slot of the step is read before any is written (the sum's barriers)
-      const int j = c0 + tid * E + e;
-      sl[e]       = cl[min(j, n - 1)];
-      keep[e]     = j < n && (static_cast<unsigned>(ht[sl[e]]) & kSeenBit) == 0;
-      mine += keep[e] ? 1 : 0;
-    }
-    int total = 0;
-    int at    = ubase + block_exclusive_sum(mine, wsum, &total);
-#pragma unroll
-    for (int e = 0; e < E; e++)  // at <= the slot's own position: no unread slot is overwritten
-      if (keep[e]) cl[at++] = sl[e];
-    ubase += total;
-  }
-  __syncthreads();
-  return n - nk;
-}
-
-/**
- * Distinct ids of all segments of a query with their sketch scores (collect_candidates, then
- * sketch_scores with LR = the reference's lanes per candidate for this S), written to the query's rows of
- * cand / dist and their count to nout.  The candidates are kept as hash-set slot numbers: 16-bit in LDS
- * (kLdsSlots), or, when they do not fit in LDS beside a large hash set, in the query's own row of cand,
- * where candidate j's slot is read and then overwritten by its id by the one lane group that scores it.  With LDS
- * slots, candidates found in earlier rounds' rows (ol) take their scores from there (take_known) and only the rest
- * are scored; their count goes to nknown.  A list gather runs on kGatherListThreads, a row gather on kGatherRowThreads: the row gather's larger hash set leaves room
- * for fewer workgroups per CU, so each gets more threads.
- */
-template <bool kRows, int LR, bool kLdsSlots, bool kBalanced>
-__global__ __launch_bounds__(kRows ? kGatherRowThreads : kGatherListThreads) void gather_kernel(
-  const int2* __restrict__ seg, int nseg, const long long* __restrict__ list_ptr,
-  const int* __restrict__ table, int table_len, int64_t N, const signed char* __restrict__ code,
-  const float* __restrict__ scale, const float* __restrict__ qs, int S, int pitch, int W, int logW, int cap,
-  int* __restrict__ cand, float* __restrict__ dist, int* __restrict__ nout, old_lists ol, int* __restrict__ nknown)
-{
-  const int q = blockIdx.x;
-  extern __shared__ long long smq[];
-  __shared__ int wsum[16];
-  const int** sp = reinterpret_cast<const int**>(smq);  // [nseg] first entry of every non-empty segment
-  float2* sq     = reinterpret_cast<float2*>(smq + nseg);  // [S] (scale, query sketch) per coordinate
-  int* pre       = reinterpret_cast<int*>(sq + S);  // [nseg + 1] exclusive prefix of the compacted lengths
-  int* ht        = pre + nseg + 1;                  // [W] hash set
-  auto* cl       = reinterpret_cast<unsigned short*>(ht + W);  // [cap] slots of the candidates (kLdsSlots)
-  __shared__ collect_state cs;
-  int* crow   = cand + static_cast<int64_t>(q) * W;
-  float* drow = dist + static_cast<int64_t>(q) * W;
-  for (int i = threadIdx.x; i < S; i += blockDim.x)
-    sq[i] = make_float2(scale[i], qs[static_cast<int64_t>(q) * S + i]);
-  auto keep_slot = [&](int slot, int, unsigned h) {
-    if constexpr (kLdsSlots)
-      cl[slot] = static_cast<unsigned short>(h);
-    else
-      crow[slot] = static_cast<int>(h);
-  };
-  int n = 0;
-  if constexpr (kBalanced)
-    n = collect_candidates<kRows>(seg, nseg, list_ptr, table, table_len, N, logW, cap, sp, pre, ht, cs, keep_slot);
-  else
-    n = collect_segments_whole<kRows>(seg, nseg, list_ptr, table, table_len, N, logW, cap, ht, cs, keep_slot);
-  int nu = n;  // candidates to score here: the first nu of the row (the rest come from earlier rounds' rows)
-  if constexpr (kLdsSlots) {
-    if (ol.count > 0 && cs.cnt <= cap) nu = take_known(ol, q, n, ht, cl, cs, wsum, crow, drow);
-  }
-  sketch_scores<LR>(
-    nu,
-    [&](int j) {
-      if constexpr (kLdsSlots)
-        return ht[cl[j]];
-      else
-        return ht[crow[j] & (W - 1)];  // a slot (< W), or an id when another group has scored j: kept inside ht
-    },
-    code, S, pitch, sq,
-    [&](int j, int id, float d) {
-      crow[j] = id;
-      drow[j] = d;
-    });
-  if (threadIdx.x == 0) {
-    nout[q] = n;
-    if (nknown != nullptr) nknown[q] = n - nu;
-  }
-}
-
-// ------------------------------------------------------------------ selection and merges
-
+// ------------------------------------------------------------------ selection (search_kernels.cuh:259-322)
 
 constexpr int kBins     = 2048;  // histogram of the selection's passes
 constexpr int kTieCap   = 256;   // keys of the threshold bin ranked directly
@@ -894,19 +750,24 @@ __device__ __forceinline__ void threshold_bin(bin_select_lds& sh, unsigned need)
  * - Otherwise (many equal or nearly equal distances) the (key, id) pairs of b* are narrowed by further histogram
  *   passes over the 64-bit values key 2^32 + id, each over a range 2^11 times smaller, until the threshold bin holds
  *   at most kTieCap pairs (ids being distinct, at most 6 passes): linear in n, as the reference's radix passes.
- * Selected ids (with their rerank bits), their keys (skey) and their positions in the row (spos) go to sid / skey /
- * spos in any order; their count (at most R) is returned in every thread.  All threads of the workgroup call it.
+ * Selected ids (with their rerank bits as read), their keys (skey) and their positions in the row (spos) go to sid /
+ * skey / spos in any order; their count (at most R) is returned in every thread.  mark (the row cid itself, or null):
+ * every selected position gets its id with kSeenBit, as the row's later readers take it (the passes read ids
+ * without that bit, and a position is selected once).  All threads of the workgroup call it.
  */
-__device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, const int* __restrict__ cid, int n,
-                                              int R, int* sid, float* skey, int* spos, bin_select_lds& sh)
+template <int kCache = kSelCache>
+__device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, const int* cid, int n, int R, int* sid,
+                                              float* skey, int* spos, int* mark, bin_select_lds& sh)
 {
   const int tid = threadIdx.x, lane = tid & 63, nthr = blockDim.x;
   auto& bs = sh.bs;
   if (n <= R) {
     for (int i = tid; i < n; i += nthr) {
-      sid[i] = cid[i];
+      const int id = cid[i];
+      sid[i]       = id;
       if (skey) skey[i] = __uint_as_float(kd[i]);
       if (spos) spos[i] = i;
+      if (mark) mark[i] = static_cast<int>(static_cast<unsigned>(id) | kSeenBit);
     }
     __syncthreads();
     return n;
@@ -918,7 +779,6 @@ __device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, c
     bs.nsel = 0;
   }
   constexpr unsigned kNone = ~0u;  // an empty register slot (valid keys are finite non-negative floats)
-  constexpr int kCache = kSelCache;
   unsigned kr[kCache];
   unsigned lo = ~0u, hi = 0u;
 #pragma unroll
@@ -970,6 +830,7 @@ __device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, c
       sid[at] = id;
       if (skey) skey[at] = __uint_as_float(key);
       if (spos) spos[at] = pos;
+      if (mark) mark[pos] = static_cast<int>(static_cast<unsigned>(id) | kSeenBit);
     }
   };
   auto to_tie = [&](bool pred, int id, unsigned key, int pos) {  // into the ranked buffer (every lane calls it)
@@ -1065,6 +926,7 @@ __device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, c
         sid[at] = sh.tid[i];
         if (skey) skey[at] = __uint_as_float(ki);
         if (spos) spos[at] = sh.tpos[i];
+        if (mark) mark[sh.tpos[i]] = static_cast<int>(static_cast<unsigned>(sh.tid[i]) | kSeenBit);
       }
     }
   }
@@ -1073,6 +935,216 @@ __device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, c
   __syncthreads();
   return ns;
 }
+
+constexpr int kOldU  = 4;  // old entries per thread with their loads in flight together
+constexpr int kOldPf = 2;  // old rows whose first kOldU entries per thread are loaded at the start of the gather
+
+/**
+ * The first kOldU entries per thread of the first kOldPf earlier-round rows of query q (the entries tid + u blockDim),
+ * loaded when the gather starts, so that their latency passes while the round's own segments are collected.
+ */
+struct old_prefetch {
+  int raw[kOldPf][kOldU];
+  float sc[kOldPf][kOldU];
+  int no[kOldPf];
+};
+
+__device__ __forceinline__ void prefetch_old(old_lists const& ol, int q, old_prefetch& pf)
+{
+  const int tid = threadIdx.x, nthr = blockDim.x;
+#pragma unroll
+  for (int o = 0; o < kOldPf; o++) {
+    pf.no[o] = o < ol.count ? min(ol.n[o][q], ol.W[o]) : 0;
+    const int* oc   = ol.cand[o < ol.count ? o : 0] + static_cast<int64_t>(q) * ol.W[o < ol.count ? o : 0];
+    const float* od = ol.dist[o < ol.count ? o : 0] + static_cast<int64_t>(q) * ol.W[o < ol.count ? o : 0];
+#pragma unroll
+    for (int u = 0; u < kOldU; u++) {  // clamped into the row (past its end: its first entry, results dropped)
+      const int i = min(u * nthr + tid, max(pf.no[o] - 1, 0));
+      pf.raw[o][u] = pf.no[o] > 0 ? oc[i] : 0;
+      pf.sc[o][u]  = pf.no[o] > 0 ? od[i] : 0.f;
+    }
+  }
+}
+
+/**
+ * The candidates of query q that earlier rounds scored, taken from their rows instead of scored again.  After
+ * collect_* (the hash set ht of cs.hts slots holds this round's n distinct ids, cl their slots): every id of the old
+ * rows is looked up in ht; the first lookup that finds it sets the entry's kSeenBit and writes the old (id, score) -
+ * the id with its rerank bit - to the end of the query's rows, position n - 1 - k for the k-th one.  The slots of
+ * those candidates are then dropped from cl, in place and in order, so that cl[0, n - nk) lists the candidates left
+ * to score.  Returns n - nk; cs.nk = nk.  The old rows are read whole, with coalesced loads, the first entries of
+ * each from pf.  Every thread calls it.
+ */
+__device__ int take_known(old_lists const& ol, old_prefetch const& pf, int q, int n, int* ht, unsigned short* cl,
+                          collect_state& cs, int* wsum, int* crow, float* drow)
+{
+  constexpr int U = kOldU;
+  constexpr int E = 8;  // slots per thread per compaction step
+  const int tid = threadIdx.x, nthr = blockDim.x, HT = cs.hts;
+  if (tid == 0) cs.nk = 0;
+  __syncthreads();
+  auto look = [&](int raw, float sc, bool in) {  // every lane calls it (the append uses a ballot)
+    const int id = static_cast<int>(static_cast<unsigned>(raw) & ~kSeenBit);
+    bool claim   = false;
+    if (in) {
+      unsigned h = (static_cast<unsigned>(id) * kIdHash) & (HT - 1);
+      for (int p = 0; p < HT; p++) {
+        const int e = ht[h];
+        if (e == -1) break;  // not a candidate of this round
+        if ((static_cast<unsigned>(e) & ~kSeenBit) == static_cast<unsigned>(id)) {
+          claim = (static_cast<unsigned>(atomicOr(&ht[h], static_cast<int>(kSeenBit))) & kSeenBit) == 0;
+          break;
+        }
+        h = (h + 1) & (HT - 1);
+      }
+    }
+    const int k = wave_append(claim, &cs.nk);
+    if (claim) {
+      crow[n - 1 - k] = raw;
+      drow[n - 1 - k] = sc;
+    }
+  };
+  auto walk = [&](int o, int no, int i0) {  // entries i0, i0 + 1, ... of old row o (uniform: every thread walks it)
+    const int* oc   = ol.cand[o] + static_cast<int64_t>(q) * ol.W[o];
+    const float* od = ol.dist[o] + static_cast<int64_t>(q) * ol.W[o];
+    for (; i0 < no; i0 += nthr * U) {
+      int raw[U];
+      float sc[U];
+#pragma unroll
+      for (int u = 0; u < U; u++) {  // past the end: the last entry (results dropped)
+        const int i = min(i0 + u * nthr + tid, no - 1);
+        raw[u]      = oc[i];
+        sc[u]       = od[i];
+      }
+#pragma unroll
+      for (int u = 0; u < U; u++)
+        look(raw[u], sc[u], i0 + u * nthr + tid < no);
+    }
+  };
+#pragma unroll
+  for (int o = 0; o < kOldPf; o++) {  // the prefetched rows (compile-time indices into pf), then the rest of them
+    if (o < ol.count) {
+#pragma unroll
+      for (int u = 0; u < U; u++)
+        look(pf.raw[o][u], pf.sc[o][u], u * nthr + tid < pf.no[o]);
+      walk(o, pf.no[o], nthr * U);
+    }
+  }
+  for (int o = kOldPf; o < ol.count; o++)
+    walk(o, min(ol.n[o][q], ol.W[o]), 0);
+  __syncthreads();
+  const int nk = cs.nk;
+  if (nk == 0) return n;
+  int ubase = 0;  // slots kept so far (uniform)
+  for (int c0 = 0; c0 < n; c0 += nthr * E) {
+    unsigned short sl[E];
+    bool keep[E];
+    int mine = 0;
+#pragma unroll
+    for (int e = 0; e < E; e++) {  // every slot of the step is read before any is written (the sum's barriers)
+      const int j = c0 + tid * E + e;
+      sl[e]       = cl[min(j, n - 1)];
+      keep[e]     = j < n && (static_cast<unsigned>(ht[sl[e]]) & kSeenBit) == 0;
+      mine += keep[e] ? 1 : 0;
+    }
+    int total = 0;
+    int at    = ubase + block_exclusive_sum(mine, wsum, &total);
+#pragma unroll
+    for (int e = 0; e < E; e++)  // at <= the slot's own position: no unread slot is overwritten
+      if (keep[e]) cl[at++] = sl[e];
+    ubase += total;
+  }
+  __syncthreads();
+  return n - nk;
+}
+
+/**
+ * Distinct ids of all segments of a query with their sketch scores (collect_candidates, then
+ * sketch_scores with LR = the reference's lanes per candidate for this S), written to the query's rows of
+ * cand / dist and their count to nout.  The candidates are kept as hash-set slot numbers: 16-bit in LDS
+ * (kLdsSlots), or, when they do not fit in LDS beside a large hash set, in the query's own row of cand,
+ * where candidate j's slot is read and then overwritten by its id by the one lane group that scores it.  With LDS
+ * slots, candidates found in earlier rounds' rows (ol) take their scores from there (take_known) and only the rest
+ * are scored; their count goes to nknown.  A list gather runs on kGatherListThreads, a row gather on kGatherRowThreads: the row gather's larger hash set leaves room
+ * for fewer workgroups per CU, so each gets more threads.
+ */
+// 7 wavefronts per SIMD (72 registers: the epilogue's selection would take 74, one wavefront fewer) where that needs
+// no spills: the balanced gathers of sketch widths 32 to 256
+template <bool kRows, int LR, bool kLdsSlots, bool kBalanced>
+__global__ __launch_bounds__(kRows ? kGatherRowThreads : kGatherListThreads)
+__attribute__((amdgpu_waves_per_eu((kBalanced && LR >= 2 && LR <= 16) ? 7 : 1))) void gather_kernel(
+  const int2* __restrict__ seg, int nseg, const long long* __restrict__ list_ptr,
+  const int* __restrict__ table, int table_len, int64_t N, const signed char* __restrict__ code,
+  const float* __restrict__ scale, const float* __restrict__ qs, int S, int pitch, int W, int logW, int cap,
+  int* __restrict__ cand, float* __restrict__ dist, int* __restrict__ nout, old_lists ol, int* __restrict__ nknown,
+  int R, int* __restrict__ sel, int* __restrict__ nsel)
+{
+  const int q = blockIdx.x;
+  extern __shared__ long long smq[];
+  __shared__ int wsum[16];
+  old_prefetch pf;
+  if constexpr (kLdsSlots) {
+    if (ol.count > 0) prefetch_old(ol, q, pf);  // in flight while the segments are collected
+  }
+  const int** sp = reinterpret_cast<const int**>(smq);  // [nseg] first entry of every non-empty segment
+  float2* sq     = reinterpret_cast<float2*>(smq + nseg);  // [S] (scale, query sketch) per coordinate
+  int* pre       = reinterpret_cast<int*>(sq + S);  // [nseg + 1] exclusive prefix of the compacted lengths
+  int* ht        = pre + nseg + 1;                  // [W] hash set
+  auto* cl       = reinterpret_cast<unsigned short*>(ht + W);  // [cap] slots of the candidates (kLdsSlots)
+  __shared__ collect_state cs;
+  int* crow   = cand + static_cast<int64_t>(q) * W;
+  float* drow = dist + static_cast<int64_t>(q) * W;
+  for (int i = threadIdx.x; i < S; i += blockDim.x)
+    sq[i] = make_float2(scale[i], qs[static_cast<int64_t>(q) * S + i]);
+  auto keep_slot = [&](int slot, int, unsigned h) {
+    if constexpr (kLdsSlots)
+      cl[slot] = static_cast<unsigned short>(h);
+    else
+      crow[slot] = static_cast<int>(h);
+  };
+  int n = 0;
+  if constexpr (kBalanced)
+    n = collect_candidates<kRows>(seg, nseg, list_ptr, table, table_len, N, logW, cap, sp, pre, ht, cs, keep_slot);
+  else
+    n = collect_segments_whole<kRows>(seg, nseg, list_ptr, table, table_len, N, logW, cap, ht, cs, keep_slot);
+  int nu = n;  // candidates to score here: the first nu of the row (the rest come from earlier rounds' rows)
+  if constexpr (kLdsSlots) {
+    if (ol.count > 0 && cs.cnt <= cap) nu = take_known(ol, pf, q, n, ht, cl, cs, wsum, crow, drow);
+  }
+  sketch_scores<LR>(
+    nu,
+    [&](int j) {
+      if constexpr (kLdsSlots)
+        return ht[cl[j]];
+      else
+        return ht[crow[j] & (W - 1)];  // a slot (< W), or an id when another group has scored j: kept inside ht
+    },
+    code, S, pitch, sq,
+    [&](int j, int id, float d) {
+      crow[j] = id;
+      drow[j] = d;
+    });
+  if (threadIdx.x == 0) {
+    nout[q] = n;
+    if (nknown != nullptr) nknown[q] = n - nu;
+  }
+  if (sel != nullptr) {
+    // the R smallest of the row just written (still in the L2) for the exact rerank: ids to sel [m, R] and their
+    // count to nsel, each selected entry of the row marked as reranked for the rounds after this one.  The hash set
+    // and the slot list are no longer read: the selection's LDS takes their place (W >= 2048 slots hold it).
+    __syncthreads();
+    const int ns = select_by_bins<4>(reinterpret_cast<const unsigned*>(drow), crow, n, R,
+                                     sel + static_cast<int64_t>(q) * R, nullptr, nullptr, crow,
+                                     *reinterpret_cast<bin_select_lds*>(ht));
+    if (threadIdx.x == 0) nsel[q] = ns;
+  }
+}
+
+static_assert(sizeof(bin_select_lds) <= sizeof(int) * (1 << kMinLogHash),
+              "the gather's smallest hash set holds the selection's LDS");
+
+// ------------------------------------------------------------------ selection and merges
+
 
 /**
  * Squared distances of the fp16 rows sid[0, ns) to the fp32 query sq (search_kernels.cuh:325-342 with
@@ -1326,14 +1398,12 @@ __host__ __device__ constexpr auto keys_per_thread(int keys, int threads) -> int
 }
 
 /**
- * LDS of rerank_keep_kernel for R reranked keys, KO kept and D coordinates, carved from its dynamic LDS in this
- * order: the region shared by the selection and the merge (8-byte aligned), the selected ids and their distances,
- * the query.  Sized per launch, so small R and KO leave room for more workgroups per CU.
+ * LDS of rerank_given_kernel for up to R reranked keys, KO kept and D coordinates, carved from its dynamic LDS in this
+ * order: the merge's exchange (8-byte aligned), the ids and their distances, the query.  Sized per launch.
  */
 __host__ __device__ constexpr auto rerank_region_bytes(int R, int KO, int threads) -> size_t
 {
-  const size_t merge = merge_bytes(keys_per_thread(KO + R, threads) * threads);
-  return ((sizeof(bin_select_lds) > merge ? sizeof(bin_select_lds) : merge) + 7) / 8 * 8;
+  return (merge_bytes(keys_per_thread(KO + R, threads) * threads) + 7) / 8 * 8;
 }
 __host__ __device__ constexpr auto rerank_lds_bytes(int R, int KO, int D, int threads) -> size_t
 {
@@ -1341,71 +1411,79 @@ __host__ __device__ constexpr auto rerank_lds_bytes(int R, int KO, int D, int th
 }
 
 /**
- * Exact rerank of the R sketch-nearest candidates of a query, merged into its kept list of the best
- * KO (search_kernels.cuh:421-467).  fresh: the kept list starts empty.  One workgroup of NT threads per query.
+ * The R sketch-nearest candidates of every query's row of cand / dist (select_by_bins; search_kernels.cuh:259-322) into
+ * sel [m, R] and their count into nsel [m]; with mark, each selected entry of the row gets kSeenBit.  One workgroup of
+ * NT threads per query (NT kSelCache keys held in registers).
+ */
+template <int NT>
+__global__ __launch_bounds__(NT) void select_rows_kernel(int* __restrict__ cand, const float* __restrict__ dist,
+                                                         const int* __restrict__ nin, int W, int R, int* __restrict__ sel,
+                                                         int* __restrict__ nsel, bool mark)
+{
+  const int q = blockIdx.x;
+  __shared__ bin_select_lds sh;
+  int* crow    = cand + static_cast<int64_t>(q) * W;
+  const int n  = min(nin[q], W);
+  const int ns = select_by_bins(reinterpret_cast<const unsigned*>(dist + static_cast<int64_t>(q) * W), crow, n, R,
+                                sel + static_cast<int64_t>(q) * R, nullptr, nullptr, mark ? crow : nullptr, sh);
+  if (threadIdx.x == 0) nsel[q] = ns;
+}
+
+/**
+ * Exact rerank of each query's selected candidates sel[q, 0 .. nsel[q]) (the R sketch-nearest, selected by the gather
+ * or select_rows_kernel), merged into its kept list of the best KO (search_kernels.cuh:421-467).  fresh: the kept list
+ * starts empty.  One workgroup of NT threads per query.
  *
  * Rounds after the first skip what an earlier round reranked.  Whenever the kept list is merged, it becomes the KO
  * smallest distinct keys of every key merged so far. A selected candidate with kSeenBit was reranked and merged by an
  * earlier round, so its exact key is either in the kept list already (merging it again changes nothing) or larger than
  * all KO kept keys (it cannot enter). Dropping it leaves the merge's result unchanged. It is neither read nor merged.
- * mark: every selected candidate gets kSeenBit in its row of cand, for the rounds after this one.
+ * Their count goes to nskip [m] (when not null).
  */
-template <int LX, int NT>
-__global__ __launch_bounds__(NT) void rerank_keep_kernel(
-  int* __restrict__ cand, const float* __restrict__ dist, const int* __restrict__ nin, int W,
-  const __half* __restrict__ vectors, int D, const float* __restrict__ Q, int R, int KO,
-  long long* __restrict__ bi, float* __restrict__ bd, bool fresh, bool mark, int* __restrict__ nskip)
+template <int LX, int NT, int C>
+__global__ __launch_bounds__(NT) void rerank_given_kernel(const int* __restrict__ sel, const int* __restrict__ nsel, int R,
+                                                          const __half* __restrict__ vectors, int64_t N, int D,
+                                                          const float* __restrict__ Q, int KO, long long* __restrict__ bi,
+                                                          float* __restrict__ bd, bool fresh, int* __restrict__ nskip)
 {
   const int q = blockIdx.x;
   extern __shared__ uint64_t rk_lds[];
   const size_t region = rerank_region_bytes(R, KO, NT);
   auto* base          = reinterpret_cast<unsigned char*>(rk_lds);
-  auto& sel           = *reinterpret_cast<bin_select_lds*>(base);
   const int keys      = keys_per_thread(KO + R, NT) * NT;
   merge_view mv{reinterpret_cast<uint64_t*>(base), reinterpret_cast<int*>(base + static_cast<size_t>(keys) * 8 + 16 * 8),
                 reinterpret_cast<uint64_t*>(base + static_cast<size_t>(keys) * 8)};
   int* sid  = reinterpret_cast<int*>(base + region);
   float* sd = reinterpret_cast<float*>(sid + R);
   float* sq = sd + R;
-  const int n = min(nin[q], W);
   for (int i = threadIdx.x; i < D; i += blockDim.x)
     sq[i] = Q[static_cast<int64_t>(q) * D + i];
-  int* crow  = cand + static_cast<int64_t>(q) * W;
-  int* spos  = reinterpret_cast<int*>(sd);  // the selected positions, while sd is not yet written
-  const int ns = select_by_bins(reinterpret_cast<const unsigned*>(dist + static_cast<int64_t>(q) * W), crow, n, R,
-                                sid, nullptr, mark ? spos : nullptr, sel);
-  if (mark) {
-    for (int t = threadIdx.x; t < ns; t += NT)
-      crow[spos[t]] = static_cast<int>(static_cast<unsigned>(sid[t]) | kSeenBit);
-    __syncthreads();  // spos (sd) is read before the distances overwrite it
-  }
-  int nr = ns;  // the selected candidates reranked here: those no earlier round reranked (all when fresh)
-  if (!fresh) {
-    constexpr int E = (kMaxRerank + NT - 1) / NT;
-    int v[E], mine = 0;
-    bool keep[E];
+  const int ns     = min(nsel[q], R);
+  const int* srow  = sel + static_cast<int64_t>(q) * R;
+  // the ids to rerank into LDS, in order, without the rerank bit: all of them when fresh, else those no earlier round
+  // reranked; an id at or above N (no row of the index) is dropped, as the gathers drop them
+  constexpr int E = (kMaxRerank + NT - 1) / NT;
+  int v[E], mine = 0;
+  bool keep[E];
 #pragma unroll
-    for (int e = 0; e < E; e++) {  // read before the prefix sum's barriers, written after: in place
-      const int i = threadIdx.x * E + e;
-      v[e]        = i < ns ? sid[i] : 0;
-      keep[e]     = i < ns && (static_cast<unsigned>(v[e]) & kSeenBit) == 0;
-      mine += keep[e] ? 1 : 0;
-    }
-    int at = block_exclusive_sum(mine, mv.wsum, &nr);  // the selection's LDS is free: it ended with a barrier
-#pragma unroll
-    for (int e = 0; e < E; e++)
-      if (keep[e]) sid[at++] = v[e];
-    __syncthreads();
+  for (int e = 0; e < E; e++) {
+    const int i = threadIdx.x * E + e;
+    v[e]        = srow[i < ns ? i : 0];
+    keep[e]     = i < ns && (fresh || (static_cast<unsigned>(v[e]) & kSeenBit) == 0) &&
+              static_cast<int64_t>(static_cast<unsigned>(v[e]) & ~kSeenBit) < N;
+    mine += keep[e] ? 1 : 0;
   }
+  int nr = 0;
+  int at = block_exclusive_sum(mine, mv.wsum, &nr);
+#pragma unroll
+  for (int e = 0; e < E; e++)
+    if (keep[e]) sid[at++] = static_cast<int>(static_cast<unsigned>(v[e]) & ~kSeenBit);
+  __syncthreads();
   if (nskip != nullptr && threadIdx.x == 0) nskip[q] = ns - nr;
   exact_distances<LX>(sid, nr, vectors, D, sq, sd);
-  long long* pb = bi + static_cast<int64_t>(q) * KO;
-  float* pd     = bd + static_cast<int64_t>(q) * KO;
-  // exact_distances ended with a barrier: the selection's LDS is free for the merge
-  with_keys_per_thread<kMaxKeepSort / NT>(KO + nr, blockDim.x, [&](auto c) {
-    constexpr int C = decltype(c)::value;
-    merge_keep<C>(pb, pd, KO, fresh, sid, sd, nr, pb, pd, KO, mv);
-  });
+  // C keys a thread hold KO + R (the host's choice): the merge's registers are sized for this launch, not the largest
+  merge_keep<C>(bi + static_cast<int64_t>(q) * KO, bd + static_cast<int64_t>(q) * KO, KO, fresh, sid, sd, nr,
+                bi + static_cast<int64_t>(q) * KO, bd + static_cast<int64_t>(q) * KO, KO, mv);
 }
 
 /** The KO sketch-nearest candidates merged into the kept list by sketch distance (:471-508). */
@@ -1424,7 +1502,7 @@ __global__ __launch_bounds__(512) void sketch_keep_kernel(const int* __restrict_
   __shared__ float sdv[kMaxSketchKO];
   const int n  = min(nin[q], W);
   const int ns = select_by_bins(reinterpret_cast<const unsigned*>(dist + static_cast<int64_t>(q) * W),
-                                cand + static_cast<int64_t>(q) * W, n, KO, sid, sdv, nullptr, u.sel);
+                                cand + static_cast<int64_t>(q) * W, n, KO, sid, sdv, nullptr, nullptr, u.sel);
   long long* pb = si + static_cast<int64_t>(q) * KO;
   float* pd     = sd + static_cast<int64_t>(q) * KO;
   with_keys_per_thread(KO + ns, blockDim.x, [&](auto c) {
@@ -1938,7 +2016,7 @@ template <bool kBalanced>
 void gather_impl(bool rows, const int2* seg, int nseg, int max_len, int m, const long long* list_ptr,
                  const int* table, int table_len, int64_t n, const signed char* code, int pitch, const float* scale,
                  const float* qs, int S, int W, int logW, int* cand, float* dist, int* nout, old_lists const& old,
-                 int* nknown, hipStream_t s)
+                 int* nknown, int R, int* sel, int* nsel, hipStream_t s)
 {
   OCTEX_EXPECTS(pitch >= S && pitch % 16 == 0, "octex: sketch rows are at least S bytes apart, 16-byte aligned");
   if (m == 0) return;
@@ -1957,22 +2035,24 @@ void gather_impl(bool rows, const int2* seg, int nseg, int max_len, int m, const
                   "octex: an earlier candidate row list is incomplete or is this gather's own output");
   old_lists ol = old;
   if (!lds_slots) ol.count = 0;  // the slot list in cand leaves no room for the reused candidates
+  OCTEX_EXPECTS(sel == nullptr || (nsel != nullptr && R >= 1 && R <= kMaxSketchKO),
+                "octex: a gather's selection takes 1 to 1024 candidates");
   int Lr = 1;  // the reference's lanes per candidate: the next power of two >= S / 16, at most 32
   while (Lr < S / 16 && Lr < 32)
     Lr <<= 1;
   auto go = [&](auto rows_tag, auto lr_tag) {
-    constexpr bool R = decltype(rows_tag)::value;
-    constexpr int LR = decltype(lr_tag)::value;
-    auto launch      = [&](auto kernel) {
+    constexpr bool kRowsTag = decltype(rows_tag)::value;
+    constexpr int LR        = decltype(lr_tag)::value;
+    auto launch             = [&](auto kernel) {
       allow_lds(reinterpret_cast<const void*>(kernel), smem);
-      kernel<<<m, R ? kGatherRowThreads : kGatherListThreads, smem, s>>>(
+      kernel<<<m, kRowsTag ? kGatherRowThreads : kGatherListThreads, smem, s>>>(
         seg, nseg, list_ptr, table, table_len, n, code, scale, qs, S, pitch, W, logW, cap, cand, dist, nout, ol,
-        nknown);
+        nknown, R, sel, nsel);
     };
     if (lds_slots)
-      launch(&gather_kernel<R, LR, true, kBalanced>);
+      launch(&gather_kernel<kRowsTag, LR, true, kBalanced>);
     else
-      launch(&gather_kernel<R, LR, false, kBalanced>);
+      launch(&gather_kernel<kRowsTag, LR, false, kBalanced>);
   };
   auto by_lr = [&](auto rows_tag) {
     switch (Lr) {
@@ -2013,19 +2093,19 @@ void sort_rows(uint64_t* keys, int rows, int width, hipStream_t s)
 void launch_gather(bool rows, const int2* seg, int nseg, int max_len, int m, const long long* list_ptr,
                    const int* table, int table_len, int64_t n, const signed char* code, int pitch,
                    const float* scale, const float* qs, int S, int W, int logW, int* cand, float* dist,
-                   int* nout, old_lists const& old, int* nknown, hipStream_t s)
+                   int* nout, old_lists const& old, int* nknown, int R, int* sel, int* nsel, hipStream_t s)
 {
   gather_impl<true>(rows, seg, nseg, max_len, m, list_ptr, table, table_len, n, code, pitch, scale, qs, S, W, logW,
-                    cand, dist, nout, old, nknown, s);
+                    cand, dist, nout, old, nknown, R, sel, nsel, s);
 }
 
 void launch_gather_segments(bool rows, const int2* seg, int nseg, int max_len, int m, const long long* list_ptr,
                             const int* table, int table_len, int64_t n, const signed char* code, int pitch,
                             const float* scale, const float* qs, int S, int W, int logW, int* cand, float* dist,
-                            int* nout, old_lists const& old, int* nknown, hipStream_t s)
+                            int* nout, old_lists const& old, int* nknown, int R, int* sel, int* nsel, hipStream_t s)
 {
   gather_impl<false>(rows, seg, nseg, max_len, m, list_ptr, table, table_len, n, code, pitch, scale, qs, S, W, logW,
-                     cand, dist, nout, old, nknown, s);
+                     cand, dist, nout, old, nknown, R, sel, nsel, s);
 }
 
 void launch_unfused_keep(const int* cand, const float* dist, const int* nin, int m, int W, const __half* vectors,
@@ -2067,27 +2147,41 @@ void launch_unfused_pick(const long long* si, int m, int KO, long long* done, in
   OCTEX_HIP(hipGetLastError());
 }
 
-void launch_rerank_keep(int* cand, const float* dist, const int* nin, int m, int W,
-                        const __half* vectors, int D, const float* Q, int R, int KO, long long* si,
-                        float* sd, bool fresh, bool mark, int* nskip, hipStream_t s)
+void launch_select_rows(int* cand, const float* dist, const int* nin, int m, int W, int R, int* sel, int* nsel,
+                        bool mark, hipStream_t s)
+{
+  if (m == 0) return;
+  OCTEX_EXPECTS(R >= 1 && R <= kMaxSketchKO, "octex: a selection of 1 to 1024 candidates");
+  // 128 threads a query while the rows are at most 4096 wide, 256 above (more keys held in registers)
+  if (W > 4096)
+    select_rows_kernel<256><<<m, 256, 0, s>>>(cand, dist, nin, W, R, sel, nsel, mark);
+  else
+    select_rows_kernel<128><<<m, 128, 0, s>>>(cand, dist, nin, W, R, sel, nsel, mark);
+  OCTEX_HIP(hipGetLastError());
+}
+
+void launch_rerank_given(const int* sel, const int* nsel, int m, int R, const __half* vectors, int64_t N, int D,
+                         const float* Q, int KO, long long* si, float* sd, bool fresh, int* nskip, hipStream_t s)
 {
   if (m == 0) return;
   OCTEX_EXPECTS(R >= 1 && R <= kMaxRerank && KO + R <= kMaxKeepSort && KO >= 1,
                 "octex: rerank in [1, 512] and max(starts, k) + rerank <= 1024");
   OCTEX_EXPECTS(D % 2 == 0, "octex: the dimension must be even");
-  // 128 threads a query while its candidate rows are at most 4096 wide (the first round: more queries in flight per
-  // CU), 256 above (the waves: more of the candidates' keys held in registers); measured at 100M rows
-  const int nt      = W > 4096 ? 256 : 128;
+  constexpr int nt  = 128;
   const size_t smem = rerank_lds_bytes(R, KO, D, nt);
+  const int c       = keys_per_thread(KO + R, nt);
   with_lx(D, [&](auto lx) {
     auto go = [&](auto kernel) {
       allow_lds(reinterpret_cast<const void*>(kernel), smem);
-      kernel<<<m, nt, smem, s>>>(cand, dist, nin, W, vectors, D, Q, R, KO, si, sd, fresh, mark, nskip);
+      kernel<<<m, nt, smem, s>>>(sel, nsel, R, vectors, N, D, Q, KO, si, sd, fresh, nskip);
     };
-    if (nt == 256)
-      go(&rerank_keep_kernel<decltype(lx)::value, 256>);
-    else
-      go(&rerank_keep_kernel<decltype(lx)::value, 128>);
+    constexpr int LX = decltype(lx)::value;
+    switch (c) {
+      case 1: go(&rerank_given_kernel<LX, nt, 1>); break;
+      case 2: go(&rerank_given_kernel<LX, nt, 2>); break;
+      case 4: go(&rerank_given_kernel<LX, nt, 4>); break;
+      default: go(&rerank_given_kernel<LX, nt, 8>); break;
+    }
   });
   OCTEX_HIP(hipGetLastError());
 }

@@ -81,17 +81,19 @@ auto gather_lds_slots(int W, int S, int nseg, int max_len) -> bool;
  * old: earlier rounds' candidate rows.  An id found there takes its score (and its rerank bit) from there instead of
  * reading its sketch row: the same score, since a query's scores do not change between rounds.  Those candidates
  * come last in the row, and their count goes to nknown [m] (when not null).  Used only when gather_lds_slots.
+ * sel (when not null): the R sketch-nearest candidates of each row (launch_select_rows' selection, with mark) are
+ * selected as the gather ends, while the row is in the L2, into sel [m, R] and their count into nsel [m].
  */
 void launch_gather(bool rows, const int2* seg, int nseg, int max_len, int m, const long long* list_ptr,
                    const int* table, int table_len, int64_t n, const signed char* code, int pitch,
                    const float* scale, const float* qs, int S, int W, int logW, int* cand, float* dist,
-                   int* nout, old_lists const& old, int* nknown, hipStream_t s);
+                   int* nout, old_lists const& old, int* nknown, int R, int* sel, int* nsel, hipStream_t s);
 /** launch_gather without the load balance (balanced_gather = false): a wavefront reads each segment whole
  * (search_kernels.cuh:687-792).  Same arguments and results. */
 void launch_gather_segments(bool rows, const int2* seg, int nseg, int max_len, int m, const long long* list_ptr,
                             const int* table, int table_len, int64_t n, const signed char* code, int pitch,
                             const float* scale, const float* qs, int S, int W, int logW, int* cand, float* dist,
-                            int* nout, old_lists const& old, int* nknown, hipStream_t s);
+                            int* nout, old_lists const& old, int* nknown, int R, int* sel, int* nsel, hipStream_t s);
 /**
  * The kept list merged with a round's candidates without the fused kernels (fused_merge = false,
  * search.cu:213-253): every candidate's key into ukey [m, W] and each row sorted, the pool of the kept list
@@ -106,15 +108,21 @@ void launch_unfused_keep(const int* cand, const float* dist, const int* nin, int
 void launch_unfused_pick(const long long* si, int m, int KO, long long* done, int E, int off, int S, int rowlen,
                          uint64_t* dsort, int Ep, unsigned char* fresh, int2* seg2, hipStream_t s);
 /**
- * Exact rerank of each query's R sketch-nearest candidates merged into its kept list si / sd [m, KO]
- * (search_kernels.cuh:421-467).  Candidates with bit 31 set were reranked by an earlier round of the batch: their
- * exact keys are already merged into this kept list, so they are neither read nor merged again (the kept list of the
- * KO smallest keys comes out the same).  mark: set bit 31 of every selected candidate in its row of cand, for the
- * later rounds that reuse these rows.  nskip [m] (when not null): selected candidates not reranked again.
+ * The R sketch-nearest candidates of every query's row of cand / dist [m, W] (nin [m] of them; by (distance bits,
+ * id), ids compared without bit 31) into sel [m, R], their count into nsel [m].  mark: set bit 31 of every selected
+ * candidate in its row of cand, for the later rounds that reuse these rows.
  */
-void launch_rerank_keep(int* cand, const float* dist, const int* nin, int m, int W,
-                        const __half* vectors, int D, const float* Q, int R, int KO, long long* si,
-                        float* sd, bool fresh, bool mark, int* nskip, hipStream_t s);
+void launch_select_rows(int* cand, const float* dist, const int* nin, int m, int W, int R, int* sel, int* nsel,
+                        bool mark, hipStream_t s);
+/**
+ * Exact rerank of each query's selected candidates sel[q, 0 .. nsel[q]) (at most R) merged into its kept list si / sd
+ * [m, KO] (search_kernels.cuh:421-467).  Candidates with bit 31 set were reranked by an earlier round of the batch:
+ * unless fresh, their exact keys are already merged into this kept list, so they are neither read nor merged again
+ * (the kept list of the KO smallest keys comes out the same); nskip [m] (when not null) gets their count.  vectors
+ * [N, D]: ids at or above N are dropped.
+ */
+void launch_rerank_given(const int* sel, const int* nsel, int m, int R, const __half* vectors, int64_t N, int D,
+                         const float* Q, int KO, long long* si, float* sd, bool fresh, int* nskip, hipStream_t s);
 void launch_sketch_keep(const int* cand, const float* dist, const int* nin, int m, int W, int KO,
                         long long* si, float* sd, bool fresh, hipStream_t s);
 void launch_pick_starts(const long long* si, int m, int KO, long long* done, int E, int off, int S,

@@ -122,6 +122,10 @@ auto carve_buffers(index_impl const& ix, plan_shape const& sh, void* base, batch
     take(b.nknown, m);
     take(b.nskip, m);
   }
+  if (sh.sp.fused_merge && !sh.sp.sketch_rank) {
+    take(b.sel, m * std::max(sh.R1, sh.sp.waves > 0 ? sh.R2 : 0));
+    take(b.nsel, m);
+  }
   take(b.bi, m * sh.k);
   take(b.bd, m * sh.k);
   if (!sh.sp.fused_merge) {
@@ -190,20 +194,21 @@ auto batch_stages(index_impl const& ix, plan_shape const& sh, batch_buffers cons
   });
   // stage names as profiled: the ablation paths are marked, so a profile shows which kernels ran
   const std::string whole = balanced ? "" : "_whole", unfused = fused ? "" : "_unfused";
+  // the fused exact rerank takes its R candidates from the gather, which selects them as it ends
+  const bool given = fused && !sketch_rank;
   auto gather = [&](std::string const& name, bool rows, const int2* seg, int nseg, int max_len, int W, int logW,
-                    int* cand, float* dist, int* n, old_lists const& ol, int* nknown) {
+                    int* cand, float* dist, int* n, old_lists const& ol, int* nknown, int R) {
     add((name + whole).c_str(), [&ix, b, s, m, S, rows, seg, nseg, max_len, W, logW, cand, dist, n, balanced, ol,
-                                 nknown] {
+                                 nknown, R, given] {
       (balanced ? launch_gather : launch_gather_segments)(
         rows, seg, nseg, max_len, m, rows ? nullptr : ix.list_ptr.as<long long>(), rows ? ix.rows() : nullptr,
         ix.table_len, ix.n, ix.code(), ix.sketch_pitch, ix.scale.as<float>(), b.qs, S, W, logW, cand, dist, n, ol,
-        nknown, s);
+        nknown, R, given ? b.sel : nullptr, given ? b.nsel : nullptr, s);
     });
   };
-  // the wave gathers reuse earlier rounds' scores when their slot lists fit in LDS; the fused exact rerank then marks
-  // what it reranks, and skips what earlier rounds reranked
+  // the wave gathers reuse earlier rounds' scores when their slot lists fit in LDS; the gathers' selections mark what
+  // the exact rerank takes, and the rerank skips what earlier rounds took
   const bool reuse = sh.sp.waves > 0 && gather_lds_slots(sh.W2, S, sh.sp.starts, ix.table_len);
-  const bool mark  = reuse;
   // the kept list merged with a round's candidates: fused (one kernel) or through global-memory sorts
   auto keep = [&](std::string const& base_name, int* cand, const float* dist, const int* n, int W, int R,
                   int pool, bool fresh) {
@@ -214,9 +219,9 @@ auto batch_stages(index_impl const& ix, plan_shape const& sh, batch_buffers cons
         launch_sketch_keep(cand, dist, n, m, W, sh.KO, b.si, b.sd, fresh, s);
       });
     else if (fused)
-      add(name, [&ix, b, sh, s, m, D, cand, dist, n, W, R, fresh, mark] {
-        launch_rerank_keep(cand, dist, n, m, W, ix.vecs(), D, b.qbuf, R, sh.KO, b.si, b.sd, fresh, mark,
-                           fresh ? nullptr : b.nskip, s);
+      add(name, [&ix, b, sh, s, m, D, R, fresh] {
+        launch_rerank_given(b.sel, b.nsel, m, R, ix.vecs(), ix.n, D, b.qbuf, sh.KO, b.si, b.sd, fresh,
+                            fresh ? nullptr : b.nskip, s);
       });
     else
       add(name, [&ix, b, sh, s, m, D, cand, dist, n, W, R, pool, fresh, sketch_rank] {
@@ -224,7 +229,7 @@ auto batch_stages(index_impl const& ix, plan_shape const& sh, batch_buffers cons
                             sketch_rank ? sh.KO : R, sh.KO, pool, fresh, b.ukey, b.upool, b.si, b.sd, s);
       });
   };
-  gather("gather_lists", false, b.seg, C, sh.lr, sh.W, sh.logW, b.cand, b.dist, b.nin, old_lists{}, nullptr);
+  gather("gather_lists", false, b.seg, C, sh.lr, sh.W, sh.logW, b.cand, b.dist, b.nin, old_lists{}, nullptr, sh.R1);
   keep(sketch_rank ? "sketch_keep" : "rerank_keep", b.cand, b.dist, b.nin, sh.W, sh.R1, sh.pool1, true);
   const int st = sh.sp.starts, nw = sh.sp.waves;
   for (int wv = 0; wv < nw; wv++) {
@@ -252,7 +257,7 @@ auto batch_stages(index_impl const& ix, plan_shape const& sh, batch_buffers cons
                             b.seg2, s);
     });
     gather("gather_rows", true, b.seg2, st, ix.table_len, sh.W2, sh.logW2, b.cand2[r], b.dist2[r], b.n2[r], ol,
-           b.nknown);
+           b.nknown, sh.R2);
     keep(sketch_rank ? "sketch_keep_wave" : "rerank_keep_wave", b.cand2[r], b.dist2[r], b.n2[r], sh.W2, sh.R2,
          sh.pool2, false);
   }
@@ -443,8 +448,8 @@ void profile_batch(index_impl& ix, plan& pl, int reps, std::vector<std::string>&
         for (int64_t j = 0; j < int64_t{m} * st; j++)
           cnt.starts2[wv] += segh[j].y > 0;
       } else if (nm == "gather_rows") {
-        const int r = wv % sh.ring;
-        OCTEX_HIP(hipMemcpy(n2.data(), b.n2[r], sizeof(int) * m, hipMemcpyDeviceToHost));
+        const int slot = wv % sh.ring;
+        OCTEX_HIP(hipMemcpy(n2.data(), b.n2[slot], sizeof(int) * m, hipMemcpyDeviceToHost));
         OCTEX_HIP(hipMemcpy(nk.data(), b.nknown, sizeof(int) * m, hipMemcpyDeviceToHost));
         for (int q = 0; q < m; q++) {
           cnt.distinct2[wv] += n2[q];

@@ -37,7 +37,9 @@ constexpr int kMaxRing = 3;  // wave candidate row sets kept for reuse
  * centred; Y f16 [m, C 8b]; qs f32 [m, S]; seg int2 [m, C]; cand i32 / dist f32 [m, W], nin [m]; si i64 /
  * sd f32 [m, KO] kept list; done i64 [m, starts waves]; seg2 int2 [m, starts]; cand2 / dist2 [m, W2], n2 [m],
  * one set per ring slot; nknown [m] (candidates of the last wave gather whose scores came from earlier rows), nskip
- * [m] (selected candidates the last rerank did not rerank again); bi i64 / bd f32 [m, k]; with fused_merge = false also ukey u64 [m, max(W, W2)] candidate keys (sorted in
+ * [m] (selected candidates the last rerank did not rerank again); with fused_merge, sel i32 [m, max(rerank,
+ * wave_rerank)] and nsel [m] (a round's selected candidates, from its gather to its rerank); bi i64 / bd f32 [m, k];
+ * with fused_merge = false also ukey u64 [m, max(W, W2)] candidate keys (sorted in
  * place), upool u64 [m, max(pool1, pool2)] pools, dsort i64 [m, Ep] the ids earlier waves expanded, sorted
  * (Ep the power of two >= starts (waves - 1)), and fresh u8 [m, KO].
  */
@@ -46,7 +48,7 @@ struct batch_buffers {
   float* dist2[kMaxRing] = {};
   __half *qh = nullptr, *Y = nullptr;
   int2 *seg = nullptr, *seg2 = nullptr;
-  int *cand = nullptr, *nin = nullptr, *nknown = nullptr, *nskip = nullptr;
+  int *cand = nullptr, *nin = nullptr, *nknown = nullptr, *nskip = nullptr, *sel = nullptr, *nsel = nullptr;
   int* cand2[kMaxRing] = {};
   int* n2[kMaxRing]    = {};
   long long *si = nullptr, *done = nullptr, *bi = nullptr;

@@ -1,7 +1,8 @@
 """The reference's end-to-end recall contracts at its own search settings, on BASELINE.json configs[1]'s workload at
-full size: 1M SIFT-like integer-valued rows x 128 (bench.py's generator, exact in fp16) and bench.py's sift1m index
-(200 copies, member lists of 32, exact neighbor table of 64, no reverse edges), with the first 2,000 of its queries
-(the reference's end-to-end test takes at most 2,000).
+full size: 1M SIFT-like integer-valued rows x 128 (bench.py's generator, exact in fp16) and an index of bench.py's
+sift1m shape built with member lists, the fast build (200 copies, lists of 32 of cells of >= 2 rows, exact neighbor
+table of 64, no reverse edges), with the first 2,000 of its queries (the reference's end-to-end test takes at most
+2,000).
 
 - tests/test_recall.py:31-45: recall@10 >= 0.99 at read 8, starts 32, waves 1, and at the default search
   parameters, where the returned distances are the squared distances of the returned rows.
@@ -22,7 +23,7 @@ pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
 
 NQ = 2000
-INDEX = bench.CONFIGS["sift1m"]["index"]
+INDEX = dict(copies=200, list_len=32, table_len=64, min_cell=2, reverse_edges=False, member_lists=True, seed=0)
 
 
 @pytest.fixture(scope="module")

@@ -460,13 +460,16 @@ def plain(a):
     return np.asarray(a) & np.int32(0x7FFFFFFF)
 
 
-def gather_reuse_gpu(L, ix, dix, seg, qs, old, W=4096):
-    """octexStageGatherReuse over table rows with the earlier rows `old` [(cand, dist, n, W)] (device tensors)."""
+def gather_reuse_gpu(L, ix, dix, seg, qs, old, W=4096, R=0):
+    """octexStageGatherReuse over table rows with the earlier rows `old` [(cand, dist, n, W)] (device tensors); with
+    R > 0 also the gather's selection of the R sketch-nearest (returned as sel, nsel)."""
     m, nseg = seg.shape[0], seg.shape[1]
     cand = torch.full((m, W), -5, dtype=torch.int32, device="cuda")
     dist = torch.zeros((m, W), dtype=torch.float32, device="cuda")
     nout = torch.zeros(m, dtype=torch.int32, device="cuda")
     nk = torch.full((m,), -1, dtype=torch.int32, device="cuda")
+    sel = torch.full((m, max(R, 1)), -3, dtype=torch.int32, device="cuda")
+    nsel = torch.full((m,), -1, dtype=torch.int32, device="cuda")
     dqs, dseg = dev(qs), dev(seg)
     k = len(old)
     oc = (ct.c_void_p * max(k, 1))(*[o[0].data_ptr() for o in old])
@@ -475,8 +478,9 @@ def gather_reuse_gpu(L, ix, dix, seg, qs, old, W=4096):
     ow = (ct.c_int32 * max(k, 1))(*[o[3] for o in old])
     L.call("octexStageGatherReuse", i32(1), P(dseg), i32(nseg), i32(m), P(dix["lists"]), i64(ix.lists.shape[1]),
            P(dix["table"]), i32(ix.table_len), i64(ix.n), P(dix["sketch"]), P(dix["scale"]), P(dqs),
-           i32(ix.sketch_width), i32(W), P(cand), P(dist), P(nout), i32(k), oc, od, on, ow, P(nk), None)
-    return cand, dist, nout, nk
+           i32(ix.sketch_width), i32(W), P(cand), P(dist), P(nout), i32(k), oc, od, on, ow, P(nk), i32(R),
+           P(sel) if R else None, P(nsel) if R else None, None)
+    return (cand, dist, nout, nk, sel, nsel) if R else (cand, dist, nout, nk)
 
 
 def test_gather_reuses_earlier_rows(L, ix, dix):
@@ -617,3 +621,54 @@ def test_selection_of_many_equal_keys_at_the_largest_width(L, ix, dix, small_ind
     for q in range(m):
         ri, rd = O.rerank_keep(ix, cand[q, : nin[q]], dist[q, : nin[q]], Q[q], R, si[q], sd[q], True)
         assert np.array_equal(host(dsi)[q], ri) and np.array_equal(host(dsd)[q], rd), f"rerank_keep query {q}"
+
+
+def test_gather_selection_and_given_rerank_match_oracle(L, ix, dix, small_index):
+    """The search's fused path: a wave gather (reusing an earlier row) that selects its R sketch-nearest as it ends,
+    then the exact rerank of those ids.  The selection is the oracle's (the R smallest by (distance, id)), each
+    selected entry of the row is marked, sel keeps the earlier rounds' rerank bits, and the kept lists equal the
+    oracle's rerank_keep on the same rows, first fresh, then merged into that kept list with the marked ids skipped."""
+    g = np.random.default_rng(24)
+    m, S, W, KO, R = 32, 64, 4096, 64, 96
+    Q = small_index["Q"][:m]
+    qs = g.standard_normal((m, ix.sketch_width)).astype(np.float32)
+    starts_a = g.integers(0, ix.n, (m, S))
+    seg_a = np.stack([starts_a, np.full((m, S), ix.table_len)], -1).astype(np.int32)
+    ca, da, na, _, sa, nsa = gather_reuse_gpu(L, ix, dix, seg_a, qs, [], W=W, R=R)
+    si = torch.full((m, KO), -1, dtype=torch.int64, device="cuda")
+    sd = torch.full((m, KO), float("inf"), dtype=torch.float32, device="cuda")
+    dQ = dev(Q)
+    L.call("octexStageRerankGiven", P(sa), P(nsa), i32(m), i32(R), P(dix["vectors"]), i64(ix.n), i32(ix.dim), P(dQ),
+           i32(KO), P(si), P(sd), i32(1), None, None)
+    hca, hda, hna, hsa, hnsa = host(ca), host(da), host(na), host(sa), host(nsa)
+    si_h = np.full((m, KO), -1, np.int64)
+    sd_h = np.full((m, KO), np.inf, np.float32)
+    for q in range(m):
+        n = hna[q]
+        ids = plain(hca[q, :n])
+        want, _ = O.select(ids, hda[q, :n], R)
+        assert hnsa[q] == len(want) and set(plain(hsa[q, : hnsa[q]]).tolist()) == set(want.tolist()), f"query {q}"
+        assert set(ids[hca[q, :n] < 0].tolist()) == set(want.tolist()), f"query {q}: marked entries"
+        ri, rd = O.rerank_keep(ix, ids, hda[q, :n], Q[q], R, si_h[q], sd_h[q], True)
+        assert np.array_equal(host(si)[q], ri) and np.array_equal(host(sd)[q], rd), f"query {q}"
+        si_h[q], sd_h[q] = ri, rd
+    # the next wave, half its starts shared: reuses the marked row, selects, reranks without the marked ids
+    starts_b = np.where(g.random((m, S)) < 0.5, starts_a, g.integers(0, ix.n, (m, S)))
+    seg_b = np.stack([starts_b, np.full((m, S), ix.table_len)], -1).astype(np.int32)
+    cb, db, nb, nkb, sb, nsb = gather_reuse_gpu(L, ix, dix, seg_b, qs, [(ca, da, na, W)], W=W, R=R)
+    nskip = torch.full((m,), -1, dtype=torch.int32, device="cuda")
+    L.call("octexStageRerankGiven", P(sb), P(nsb), i32(m), i32(R), P(dix["vectors"]), i64(ix.n), i32(ix.dim), P(dQ),
+           i32(KO), P(si), P(sd), i32(0), P(nskip), None)
+    hcb, hdb, hnb, hsb, hnsb, hsk = host(cb), host(db), host(nb), host(sb), host(nsb), host(nskip)
+    for q in range(m):
+        n = hnb[q]
+        ids = plain(hcb[q, :n])
+        want, _ = O.select(ids, hdb[q, :n], R)
+        got = hsb[q, : hnsb[q]]
+        assert set(plain(got).tolist()) == set(want.tolist()), f"query {q}"
+        was = {int(v) for v in plain(hca[q, : hna[q]][hca[q, : hna[q]] < 0])}  # marked by the first selection
+        assert {int(v) for v in plain(got[got < 0])} == {int(v) for v in want if int(v) in was}, f"query {q}: bits"
+        assert hsk[q] == int((got < 0).sum()), f"query {q}: skipped"
+        ri, rd = O.rerank_keep(ix, ids, hdb[q, :n], Q[q], R, si_h[q], sd_h[q], False)
+        assert np.array_equal(host(si)[q], ri) and np.array_equal(host(sd)[q], rd), f"query {q}"
+    assert hsk.sum() > 0 and host(nkb).sum() > 0
