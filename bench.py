@@ -310,22 +310,16 @@ def stage_bytes(name, wave, cnt, m, C, S, D, KO, table_len, starts, w, L, FR=0, 
         return cnt["distinct2"][wave] * 8 + m * 24 * KO
     if name == "final_rerank":  # FR rows per query (from host memory when the vectors are there)
         return m * (FR * 2 * D + 12 * KO + 4 * D + 12 * k)
-    # the fused search: each gather ends by selecting its round's R candidates from the row it wrote (read back, 8
-    # bytes a candidate; the ids out, 4 bytes each) and the exact rerank reads those ids
     if name == "gather_lists":
-        return (m * C * 8 + cnt["entries1"] * 4 + cnt["distinct1"] * (S + 8) + m * (S * 4 + 4)
-                + cnt["distinct1"] * 8 + cnt["reranked1"] * 4)
-    if name == "gather_rows":  # sketch rows of the candidates no earlier round scored; 8 bytes per earlier-row entry
-        known = cnt.get("known2", [0] * 16)[wave]
-        old = cnt.get("oldread2", [0] * 16)[wave]
-        return (m * starts * 8 + cnt["starts2"][wave] * table_len * 4 + (cnt["distinct2"][wave] - known) * S
-                + cnt["distinct2"][wave] * 8 + old * 8 + m * (S * 4 + 4)
-                + cnt["distinct2"][wave] * 8 + cnt["reranked2"][wave] * 4)
+        return m * C * 8 + cnt["entries1"] * 4 + cnt["distinct1"] * (S + 8) + m * (S * 4 + 4)
+    if name == "gather_rows":
+        return m * starts * 8 + cnt["starts2"][wave] * table_len * 4 + cnt["distinct2"][wave] * (S + 8) + m * (S * 4 + 4)
     if name == "rerank_keep":
-        return cnt["reranked1"] * (4 + 2 * D) + m * (12 * KO + 4 * D + 4)
-    if name == "rerank_keep_wave":  # rows of the selected candidates no earlier round reranked
+        return cnt["distinct1"] * 8 + cnt["reranked1"] * 2 * D + m * (12 * KO + 4 * D + 4)
+    if name == "rerank_keep_wave":  # the selected candidates' rows, less those an earlier round reranked
         skipped = cnt.get("skipped2", [0] * 16)[wave]
-        return cnt["reranked2"][wave] * 4 + (cnt["reranked2"][wave] - skipped) * 2 * D + m * (24 * KO + 4 * D + 4)
+        return (cnt["distinct2"][wave] * 8 + (cnt["reranked2"][wave] - skipped) * 2 * D
+                + m * (24 * KO + 4 * D + 4))
     if name == "probe":  # Y rows and segments out; an offsets pair and a key per level tried (finest first)
         tried = sum((j + 1) * h for j, h in enumerate(cnt["hit_level"])) + L * (m * C - cnt["seg_hits"])
         return m * C * (2 * w + 8) + tried * (8 + 8)
@@ -583,10 +577,8 @@ def main():
     log(f"probe hits by level {cnt['hit_level'][:int(meta[4])]}, misses {len(Q) * C - cnt['seg_hits']}")
     nw = params.get("waves", 0)
     if nw:
-        log("waves: distinct " + str(cnt["distinct2"][:nw]) + ", scored in earlier rounds " + str(cnt["known2"][:nw])
-            + f" ({', '.join(f'{k / max(d, 1):.3f}' for k, d in zip(cnt['known2'][:nw], cnt['distinct2'][:nw]))})"
-            + ", earlier-row entries read " + str(cnt["oldread2"][:nw]) + ", reranked " + str(cnt["reranked2"][:nw])
-            + ", of them not reranked again " + str(cnt["skipped2"][:nw]))
+        log("waves: distinct " + str(cnt["distinct2"][:nw]) + ", selected " + str(cnt["reranked2"][:nw])
+            + ", of them reranked by an earlier round " + str(cnt["skipped2"][:nw]))
     log("stages: " + ", ".join(f"{x['stage']}[{x['wave']}] {x['ms']:.3f} ms {x['gbs']} GB/s" for x in per_launch))
 
     # CPU baseline: the oracle (C++ restatement of the search) on the same index, a bounded query sample
@@ -654,10 +646,9 @@ def main():
             "index_gib": round(index.device_bytes[0] / 2**30, 2),
             "sweep": points,
             "stages": per_launch,
-            # per wave: distinct candidates, those whose sketch scores came from earlier rounds' rows (no sketch row
-            # read), earlier-row entries read, selected for the exact rerank, and of those reranked by an earlier round
-            "wave_reuse": {key: cnt[key][: params.get("waves", 0)]
-                           for key in ("distinct2", "known2", "oldread2", "reranked2", "skipped2")},
+            # per wave: distinct candidates, those selected for the exact rerank, and of those the ones an earlier
+            # round reranked (their rows not read again)
+            "wave_reuse": {key: cnt[key][: params.get("waves", 0)] for key in ("distinct2", "reranked2", "skipped2")},
         },
         "roofline": {
             "bound": "hbm",

@@ -38,11 +38,11 @@ cuvsError_t octexBuildInMemory(cuvsResources_t res, cuvsOctexIndexParams_t param
  * Profile one batch of queries [m <= batch, dim] (float32, host or device): a normal search, then the
  * same batch launched kernel by kernel `reps` times with HIP events around every launch on the index's
  * stream.  names (64 x 32 chars) and ms receive the stages in launch order with their average
- * milliseconds, *nstages their count; counters (108 int64, optional): probe hits, list entries read,
+ * milliseconds, *nstages their count; counters (76 int64, optional): probe hits, list entries read,
  * distinct first-round candidates, first-round reranked, then per wave (16 each) valid start points,
  * distinct candidates and reranked entries, then probe hits by level (8, the finest first), then per wave
- * (16 each) candidates whose scores came from earlier rounds' rows, entries of earlier rows read, and
- * selected candidates not reranked again; all summed over the batch's m rows.
+ * (16) the selected candidates not reranked again (an earlier round reranked them); all summed over the batch's
+ * m rows.
  */
 cuvsError_t octexIndexProfileBatch(cuvsOctexIndex_t index, cuvsOctexSearchParams_t params, DLManagedTensor* queries,
                                    int64_t k, int32_t reps, char* names, double* ms, int32_t* nstages,
@@ -146,39 +146,18 @@ cuvsError_t octexStageGather(int32_t rows, const int32_t* seg, int32_t nseg, int
                              int64_t stride, const int32_t* table, int32_t table_len, int64_t n, const int8_t* code,
                              const float* scale, const float* qs, int32_t S, int32_t W, int32_t* cand,
                              float* dist, int32_t* nout, void* stream);
-/** octexStageGather with n_old earlier rounds' candidate rows (device pointers in host arrays: ids, scores, counts
- * and row widths, as a wave gather of a search reuses them; at most 4): a candidate found there takes its score
- * from there, the same score; such candidates come last in the row and their count goes to nknown [m] (may be
- * NULL).  Reuse happens only when the gather keeps its slot lists in LDS; the results are the same either way.
- * sel (may be NULL): the R sketch-nearest of each row are selected as the gather ends, as the search's rerank takes
- * them (octexStageRerankGiven): ids (bit 31 kept) into sel [m, R], count into nsel [m], and each selected entry of
- * cand marked with bit 31. */
-cuvsError_t octexStageGatherReuse(int32_t rows, const int32_t* seg, int32_t nseg, int32_t m, const int32_t* lists,
-                                  int64_t stride, const int32_t* table, int32_t table_len, int64_t n,
-                                  const int8_t* code, const float* scale, const float* qs, int32_t S, int32_t W,
-                                  int32_t* cand, float* dist, int32_t* nout, int32_t n_old,
-                                  const int32_t* const* old_cand, const float* const* old_dist,
-                                  const int32_t* const* old_n, const int32_t* old_W, int32_t* nknown, int32_t R,
-                                  int32_t* sel, int32_t* nsel, void* stream);
-/** The exact rerank of the search (search_kernels.cuh:421-467) given each query's selected ids sel[q, 0 .. nsel[q])
- * (row stride R) over vectors [n, D]: exact distances merged into si / sd [m, KO]; unless fresh, ids with bit 31
- * (reranked by an earlier round of the same kept list) are skipped and counted in nskip [m] (may be NULL); ids at or
- * above n are dropped. */
-cuvsError_t octexStageRerankGiven(const int32_t* sel, const int32_t* nsel, int32_t m, int32_t R, const void* vectors,
-                                  int64_t n, int32_t D, const float* Q, int32_t KO, int64_t* si, float* sd,
-                                  int32_t fresh, int32_t* nskip, void* stream);
-/** rerank_keep_kernel (search_kernels.cuh:421-467) as two steps: the selection of the R sketch-nearest, then the
- * exact rerank (octexStageRerankGiven).  Selected candidates with bit 31 set are taken as reranked by an earlier round
- * of the same kept list (not fresh): they are not reranked or merged again. */
-cuvsError_t octexStageRerankKeep(int32_t* cand, const float* dist, const int32_t* nin, int32_t m,
+/** rerank_keep_kernel (search_kernels.cuh:421-467). */
+cuvsError_t octexStageRerankKeep(const int32_t* cand, const float* dist, const int32_t* nin, int32_t m,
                                  int32_t W, const void* vectors, int32_t D, const float* Q, int32_t R,
                                  int32_t KO, int64_t* si, float* sd, int32_t fresh, void* stream);
-/** octexStageRerankKeep that also sets bit 31 of every selected candidate in cand (mark) and writes the selected
- * candidates it did not rerank again to nskip [m] (may be NULL). */
-cuvsError_t octexStageRerankKeepMarked(int32_t* cand, const float* dist, const int32_t* nin, int32_t m, int32_t W,
-                                       const void* vectors, int32_t D, const float* Q, int32_t R, int32_t KO,
-                                       int64_t* si, float* sd, int32_t fresh, int32_t mark, int32_t* nskip,
-                                       void* stream);
+/** octexStageRerankKeep with the history of a batch's selected ids, as the search's rounds run it: hist [m, H] holds
+ * each round's R selected ids (-1 padded); with hstore this round's go to hist[q, hoff .. hoff + R); unless fresh, the
+ * ids of hist[q, 0 .. hoff) were reranked into this kept list by earlier rounds, and those of its last 256 entries are
+ * skipped when selected again (counted in nskip [m], may be NULL). */
+cuvsError_t octexStageRerankKeepHistory(const int32_t* cand, const float* dist, const int32_t* nin, int32_t m,
+                                        int32_t W, const void* vectors, int32_t D, const float* Q, int32_t R,
+                                        int32_t KO, int64_t* si, float* sd, int32_t fresh, int32_t* hist, int32_t H,
+                                        int32_t hoff, int32_t hstore, int32_t* nskip, void* stream);
 /** sketch_keep_kernel (search_kernels.cuh:471-508). */
 cuvsError_t octexStageSketchKeep(const int32_t* cand, const float* dist, const int32_t* nin, int32_t m,
                                  int32_t W, int32_t KO, int64_t* si, float* sd, int32_t fresh, void* stream);

@@ -441,7 +441,6 @@ __device__ __forceinline__ void sketch_scores(int n, IdOf const& id_of, const si
 struct collect_state {
   int cnt, nsp, ulen;
   int hts;  // the hash set's slots
-  int nk;   // candidates whose scores an earlier round's row holds
 };
 
 /**
@@ -687,12 +686,11 @@ struct bin_select_lds {
   unsigned hist[kBins / 2];  // two 16-bit bin counts a word (a query has at most 2^15 candidates: no carry)
   unsigned tkey[kTieCap];
   int tid[kTieCap];
-  int tpos[kTieCap];
   bin_select_state bs;
 };
 
-/** An id without its rerank bit (kSeenBit), as the selections order ids. */
-__device__ __forceinline__ unsigned plain_id(int v) { return static_cast<unsigned>(v) & ~kSeenBit; }
+/** An id as the selections order it (ids are non-negative). */
+__device__ __forceinline__ unsigned plain_id(int v) { return static_cast<unsigned>(v); }
 
 /** Bin b's count in the packed histogram. */
 __device__ __forceinline__ unsigned bin_count(bin_select_lds const& sh, int b)
@@ -741,7 +739,7 @@ __device__ __forceinline__ void threshold_bin(bin_select_lds& sh, unsigned need)
 
 /**
  * The R smallest of n (distance, id) pairs of a query by (distance bits, id) (search_kernels.cuh:259-322 with a
- * deterministic tie rule; ids are compared without their rerank bit) in passes over the keys, kSelCache per thread
+ * deterministic tie rule) in passes over the keys, kSelCache per thread
  * held in registers (the rest are read again).
  * - First pass: a kBins-bin histogram of (key - kmin) >> shift, shift fitting the keys' range into the bins, gives
  *   the bin b* where the count reaches R.  Keys of lower bins are taken.
@@ -750,24 +748,19 @@ __device__ __forceinline__ void threshold_bin(bin_select_lds& sh, unsigned need)
  * - Otherwise (many equal or nearly equal distances) the (key, id) pairs of b* are narrowed by further histogram
  *   passes over the 64-bit values key 2^32 + id, each over a range 2^11 times smaller, until the threshold bin holds
  *   at most kTieCap pairs (ids being distinct, at most 6 passes): linear in n, as the reference's radix passes.
- * Selected ids (with their rerank bits as read), their keys (skey) and their positions in the row (spos) go to sid /
- * skey / spos in any order; their count (at most R) is returned in every thread.  mark (the row cid itself, or null):
- * every selected position gets its id with kSeenBit, as the row's later readers take it (the passes read ids
- * without that bit, and a position is selected once).  All threads of the workgroup call it.
+ * Selected ids and their keys (skey, when not null) go to sid / skey in any order; their count (at most R) is returned
+ * in every thread.  All threads of the workgroup call it.
  */
 template <int kCache = kSelCache>
 __device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, const int* cid, int n, int R, int* sid,
-                                              float* skey, int* spos, int* mark, bin_select_lds& sh)
+                                              float* skey, bin_select_lds& sh)
 {
   const int tid = threadIdx.x, lane = tid & 63, nthr = blockDim.x;
   auto& bs = sh.bs;
   if (n <= R) {
     for (int i = tid; i < n; i += nthr) {
-      const int id = cid[i];
-      sid[i]       = id;
+      sid[i] = cid[i];
       if (skey) skey[i] = __uint_as_float(kd[i]);
-      if (spos) spos[i] = i;
-      if (mark) mark[i] = static_cast<int>(static_cast<unsigned>(id) | kSeenBit);
     }
     __syncthreads();
     return n;
@@ -824,21 +817,18 @@ __device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, c
   threshold_bin(sh, static_cast<unsigned>(R));
   const unsigned bstar = static_cast<unsigned>(bs.bstar);
   int need             = R - bs.below;
-  auto take = [&](bool pred, int id, unsigned key, int pos) {  // append to the selection (every lane calls it)
+  auto take = [&](bool pred, int id, unsigned key) {  // append to the selection (every lane calls it)
     const int at = wave_append(pred, &bs.nsel);
     if (pred && at < R) {
       sid[at] = id;
       if (skey) skey[at] = __uint_as_float(key);
-      if (spos) spos[at] = pos;
-      if (mark) mark[pos] = static_cast<int>(static_cast<unsigned>(id) | kSeenBit);
     }
   };
-  auto to_tie = [&](bool pred, int id, unsigned key, int pos) {  // into the ranked buffer (every lane calls it)
+  auto to_tie = [&](bool pred, int id, unsigned key) {  // into the ranked buffer (every lane calls it)
     const int t = wave_append(pred, &bs.ntb);
     if (pred && t < kTieCap) {
       sh.tkey[t] = key;
       sh.tid[t]  = id;
-      sh.tpos[t] = pos;
     }
   };
   // the candidate ids of the cached keys, loaded together before they are placed (unconditional loads of
@@ -853,8 +843,8 @@ __device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, c
   for (int j = 0; j < kCache; j++) {
     const bool ok    = kr[j] != kNone;
     const unsigned b = (kr[j] - kmin) >> shift;
-    take(ok && b < bstar, ci[j], kr[j], tid + j * nthr);
-    to_tie(ok && b == bstar, ci[j], kr[j], tid + j * nthr);
+    take(ok && b < bstar, ci[j], kr[j]);
+    to_tie(ok && b == bstar, ci[j], kr[j]);
   }
   for (int i0 = kCache * nthr; i0 < n; i0 += nthr) {  // keys past the cache: key and id read together
     const int i       = i0 + tid;
@@ -862,8 +852,8 @@ __device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, c
     const unsigned kv = kd[ii];
     const int id      = cid[ii];
     const unsigned b  = (kv - kmin) >> shift;
-    take(i < n && b < bstar, id, kv, i);
-    to_tie(i < n && b == bstar, id, kv, i);
+    take(i < n && b < bstar, id, kv);
+    to_tie(i < n && b == bstar, id, kv);
   }
   __syncthreads();
   // every thread reads the count before the passes below reset it (a wave that read it after thread 0's reset would
@@ -874,7 +864,7 @@ __device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, c
     // more keys in bin b* than the ranked buffer holds: narrow the (key, id) values of b* by histogram passes
     const uint64_t blo = static_cast<uint64_t>(kmin) + (static_cast<uint64_t>(bstar) << shift);
     const uint64_t bhi = min(static_cast<uint64_t>(kmax), blo + ((uint64_t{1} << shift) - 1));
-    uint64_t vlo = blo << 32, vhi = (bhi << 32) | ~kSeenBit;
+    uint64_t vlo = blo << 32, vhi = (bhi << 32) | 0x7fffffffu;
     for (;;) {  // uniform: every bound comes from LDS after a barrier
       const uint64_t vr = vhi - vlo;
       const int sh2     = vr < static_cast<uint64_t>(kBins) ? 0 : (64 - __clzll(static_cast<long long>(vr))) - 11;
@@ -902,8 +892,8 @@ __device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, c
         const unsigned k = kd[ii];
         const int id     = cid[ii];
         const uint64_t v = (static_cast<uint64_t>(k) << 32) | plain_id(id);
-        take(i < n && v >= vlo && v < nlo, id, k, i);
-        to_tie(last && i < n && v >= nlo && v <= nhi, id, k, i);
+        take(i < n && v >= vlo && v < nlo, id, k);
+        to_tie(last && i < n && v >= nlo && v <= nhi, id, k);
       }
       __syncthreads();
       need -= below2;
@@ -925,8 +915,6 @@ __device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, c
       if (at < R) {
         sid[at] = sh.tid[i];
         if (skey) skey[at] = __uint_as_float(ki);
-        if (spos) spos[at] = sh.tpos[i];
-        if (mark) mark[sh.tpos[i]] = static_cast<int>(static_cast<unsigned>(sh.tid[i]) | kSeenBit);
       }
     }
   }
@@ -936,156 +924,24 @@ __device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, c
   return ns;
 }
 
-constexpr int kOldU  = 4;  // old entries per thread with their loads in flight together
-constexpr int kOldPf = 2;  // old rows whose first kOldU entries per thread are loaded at the start of the gather
-
-/**
- * The first kOldU entries per thread of the first kOldPf earlier-round rows of query q (the entries tid + u blockDim),
- * loaded when the gather starts, so that their latency passes while the round's own segments are collected.
- */
-struct old_prefetch {
-  int raw[kOldPf][kOldU];
-  float sc[kOldPf][kOldU];
-  int no[kOldPf];
-};
-
-__device__ __forceinline__ void prefetch_old(old_lists const& ol, int q, old_prefetch& pf)
-{
-  const int tid = threadIdx.x, nthr = blockDim.x;
-#pragma unroll
-  for (int o = 0; o < kOldPf; o++) {
-    pf.no[o] = o < ol.count ? min(ol.n[o][q], ol.W[o]) : 0;
-    const int* oc   = ol.cand[o < ol.count ? o : 0] + static_cast<int64_t>(q) * ol.W[o < ol.count ? o : 0];
-    const float* od = ol.dist[o < ol.count ? o : 0] + static_cast<int64_t>(q) * ol.W[o < ol.count ? o : 0];
-#pragma unroll
-    for (int u = 0; u < kOldU; u++) {  // clamped into the row (past its end: its first entry, results dropped)
-      const int i = min(u * nthr + tid, max(pf.no[o] - 1, 0));
-      pf.raw[o][u] = pf.no[o] > 0 ? oc[i] : 0;
-      pf.sc[o][u]  = pf.no[o] > 0 ? od[i] : 0.f;
-    }
-  }
-}
-
-/**
- * The candidates of query q that earlier rounds scored, taken from their rows instead of scored again.  After
- * collect_* (the hash set ht of cs.hts slots holds this round's n distinct ids, cl their slots): every id of the old
- * rows is looked up in ht; the first lookup that finds it sets the entry's kSeenBit and writes the old (id, score) -
- * the id with its rerank bit - to the end of the query's rows, position n - 1 - k for the k-th one.  The slots of
- * those candidates are then dropped from cl, in place and in order, so that cl[0, n - nk) lists the candidates left
- * to score.  Returns n - nk; cs.nk = nk.  The old rows are read whole, with coalesced loads, the first entries of
- * each from pf.  Every thread calls it.
- */
-__device__ int take_known(old_lists const& ol, old_prefetch const& pf, int q, int n, int* ht, unsigned short* cl,
-                          collect_state& cs, int* wsum, int* crow, float* drow)
-{
-  constexpr int U = kOldU;
-  constexpr int E = 8;  // slots per thread per compaction step
-  const int tid = threadIdx.x, nthr = blockDim.x, HT = cs.hts;
-  if (tid == 0) cs.nk = 0;
-  __syncthreads();
-  auto look = [&](int raw, float sc, bool in) {  // every lane calls it (the append uses a ballot)
-    const int id = static_cast<int>(static_cast<unsigned>(raw) & ~kSeenBit);
-    bool claim   = false;
-    if (in) {
-      unsigned h = (static_cast<unsigned>(id) * kIdHash) & (HT - 1);
-      for (int p = 0; p < HT; p++) {
-        const int e = ht[h];
-        if (e == -1) break;  // not a candidate of this round
-        if ((static_cast<unsigned>(e) & ~kSeenBit) == static_cast<unsigned>(id)) {
-          claim = (static_cast<unsigned>(atomicOr(&ht[h], static_cast<int>(kSeenBit))) & kSeenBit) == 0;
-          break;
-        }
-        h = (h + 1) & (HT - 1);
-      }
-    }
-    const int k = wave_append(claim, &cs.nk);
-    if (claim) {
-      crow[n - 1 - k] = raw;
-      drow[n - 1 - k] = sc;
-    }
-  };
-  auto walk = [&](int o, int no, int i0) {  // entries i0, i0 + 1, ... of old row o (uniform: every thread walks it)
-    const int* oc   = ol.cand[o] + static_cast<int64_t>(q) * ol.W[o];
-    const float* od = ol.dist[o] + static_cast<int64_t>(q) * ol.W[o];
-    for (; i0 < no; i0 += nthr * U) {
-      int raw[U];
-      float sc[U];
-#pragma unroll
-      for (int u = 0; u < U; u++) {  // past the end: the last entry (results dropped)
-        const int i = min(i0 + u * nthr + tid, no - 1);
-        raw[u]      = oc[i];
-        sc[u]       = od[i];
-      }
-#pragma unroll
-      for (int u = 0; u < U; u++)
-        look(raw[u], sc[u], i0 + u * nthr + tid < no);
-    }
-  };
-#pragma unroll
-  for (int o = 0; o < kOldPf; o++) {  // the prefetched rows (compile-time indices into pf), then the rest of them
-    if (o < ol.count) {
-#pragma unroll
-      for (int u = 0; u < U; u++)
-        look(pf.raw[o][u], pf.sc[o][u], u * nthr + tid < pf.no[o]);
-      walk(o, pf.no[o], nthr * U);
-    }
-  }
-  for (int o = kOldPf; o < ol.count; o++)
-    walk(o, min(ol.n[o][q], ol.W[o]), 0);
-  __syncthreads();
-  const int nk = cs.nk;
-  if (nk == 0) return n;
-  int ubase = 0;  // slots kept so far (uniform)
-  for (int c0 = 0; c0 < n; c0 += nthr * E) {
-    unsigned short sl[E];
-    bool keep[E];
-    int mine = 0;
-#pragma unroll
-    for (int e = 0; e < E; e++) {  // every slot of the step is read before any is written (the sum's barriers)
-      const int j = c0 + tid * E + e;
-      sl[e]       = cl[min(j, n - 1)];
-      keep[e]     = j < n && (static_cast<unsigned>(ht[sl[e]]) & kSeenBit) == 0;
-      mine += keep[e] ? 1 : 0;
-    }
-    int total = 0;
-    int at    = ubase + block_exclusive_sum(mine, wsum, &total);
-#pragma unroll
-    for (int e = 0; e < E; e++)  // at <= the slot's own position: no unread slot is overwritten
-      if (keep[e]) cl[at++] = sl[e];
-    ubase += total;
-  }
-  __syncthreads();
-  return n - nk;
-}
-
 /**
  * Distinct ids of all segments of a query with their sketch scores (collect_candidates, then
  * sketch_scores with LR = the reference's lanes per candidate for this S), written to the query's rows of
  * cand / dist and their count to nout.  The candidates are kept as hash-set slot numbers: 16-bit in LDS
  * (kLdsSlots), or, when they do not fit in LDS beside a large hash set, in the query's own row of cand,
- * where candidate j's slot is read and then overwritten by its id by the one lane group that scores it.  With LDS
- * slots, candidates found in earlier rounds' rows (ol) take their scores from there (take_known) and only the rest
- * are scored; their count goes to nknown.  A list gather runs on kGatherListThreads, a row gather on kGatherRowThreads: the row gather's larger hash set leaves room
+ * where candidate j's slot is read and then overwritten by its id by the one lane group that scores it.  A list
+ * gather runs on kGatherListThreads, a row gather on kGatherRowThreads: the row gather's larger hash set leaves room
  * for fewer workgroups per CU, so each gets more threads.
  */
-// 7 wavefronts per SIMD (72 registers: the epilogue's selection would take 74, one wavefront fewer) where that needs
-// no spills: the balanced gathers of sketch widths 32 to 256
 template <bool kRows, int LR, bool kLdsSlots, bool kBalanced>
-__global__ __launch_bounds__(kRows ? kGatherRowThreads : kGatherListThreads)
-__attribute__((amdgpu_waves_per_eu((kBalanced && LR >= 2 && LR <= 16) ? 7 : 1))) void gather_kernel(
+__global__ __launch_bounds__(kRows ? kGatherRowThreads : kGatherListThreads) void gather_kernel(
   const int2* __restrict__ seg, int nseg, const long long* __restrict__ list_ptr,
   const int* __restrict__ table, int table_len, int64_t N, const signed char* __restrict__ code,
   const float* __restrict__ scale, const float* __restrict__ qs, int S, int pitch, int W, int logW, int cap,
-  int* __restrict__ cand, float* __restrict__ dist, int* __restrict__ nout, old_lists ol, int* __restrict__ nknown,
-  int R, int* __restrict__ sel, int* __restrict__ nsel)
+  int* __restrict__ cand, float* __restrict__ dist, int* __restrict__ nout)
 {
   const int q = blockIdx.x;
   extern __shared__ long long smq[];
-  __shared__ int wsum[16];
-  old_prefetch pf;
-  if constexpr (kLdsSlots) {
-    if (ol.count > 0) prefetch_old(ol, q, pf);  // in flight while the segments are collected
-  }
   const int** sp = reinterpret_cast<const int**>(smq);  // [nseg] first entry of every non-empty segment
   float2* sq     = reinterpret_cast<float2*>(smq + nseg);  // [S] (scale, query sketch) per coordinate
   int* pre       = reinterpret_cast<int*>(sq + S);  // [nseg + 1] exclusive prefix of the compacted lengths
@@ -1107,12 +963,8 @@ __attribute__((amdgpu_waves_per_eu((kBalanced && LR >= 2 && LR <= 16) ? 7 : 1)))
     n = collect_candidates<kRows>(seg, nseg, list_ptr, table, table_len, N, logW, cap, sp, pre, ht, cs, keep_slot);
   else
     n = collect_segments_whole<kRows>(seg, nseg, list_ptr, table, table_len, N, logW, cap, ht, cs, keep_slot);
-  int nu = n;  // candidates to score here: the first nu of the row (the rest come from earlier rounds' rows)
-  if constexpr (kLdsSlots) {
-    if (ol.count > 0 && cs.cnt <= cap) nu = take_known(ol, pf, q, n, ht, cl, cs, wsum, crow, drow);
-  }
   sketch_scores<LR>(
-    nu,
+    n,
     [&](int j) {
       if constexpr (kLdsSlots)
         return ht[cl[j]];
@@ -1124,24 +976,8 @@ __attribute__((amdgpu_waves_per_eu((kBalanced && LR >= 2 && LR <= 16) ? 7 : 1)))
       crow[j] = id;
       drow[j] = d;
     });
-  if (threadIdx.x == 0) {
-    nout[q] = n;
-    if (nknown != nullptr) nknown[q] = n - nu;
-  }
-  if (sel != nullptr) {
-    // the R smallest of the row just written (still in the L2) for the exact rerank: ids to sel [m, R] and their
-    // count to nsel, each selected entry of the row marked as reranked for the rounds after this one.  The hash set
-    // and the slot list are no longer read: the selection's LDS takes their place (W >= 2048 slots hold it).
-    __syncthreads();
-    const int ns = select_by_bins<4>(reinterpret_cast<const unsigned*>(drow), crow, n, R,
-                                     sel + static_cast<int64_t>(q) * R, nullptr, nullptr, crow,
-                                     *reinterpret_cast<bin_select_lds*>(ht));
-    if (threadIdx.x == 0) nsel[q] = ns;
-  }
+  if (threadIdx.x == 0) nout[q] = n;
 }
-
-static_assert(sizeof(bin_select_lds) <= sizeof(int) * (1 << kMinLogHash),
-              "the gather's smallest hash set holds the selection's LDS");
 
 // ------------------------------------------------------------------ selection and merges
 
@@ -1340,7 +1176,7 @@ __device__ void merge_keep(long long* pb, float* pd, int KO, bool fresh, const i
       const long long id = (!fresh && pb != nullptr) ? pb[i] : -1;
       if (id >= 0) v = dist_key(pd[i], id);
     } else if (i - KO < ns) {
-      v = dist_key(sdv[i - KO], plain_id(sid[i - KO]));
+      v = dist_key(sdv[i - KO], sid[i - KO]);
     }
     k[j] = v;
   }
@@ -1397,92 +1233,137 @@ __host__ __device__ constexpr auto keys_per_thread(int keys, int threads) -> int
   return keys <= threads ? 1 : keys <= 2 * threads ? 2 : keys <= 4 * threads ? 4 : 8;
 }
 
+constexpr int kRerankThreads = 128;  // rerank_keep_kernel's workgroup: one query
+constexpr int kHistWindow    = 256;  // the most recent history entries a round skips (earlier ones are reranked again)
+
+/** Slots of the set of a round's history window (hoff entries before it): a power of two at least twice the window,
+ * 0 for a round without one. */
+__host__ __device__ constexpr auto hist_slots(int hoff) -> int
+{
+  const int w = hoff < kHistWindow ? hoff : kHistWindow;
+  int s       = 64;
+  while (s < 2 * w)
+    s <<= 1;
+  return w > 0 ? s : 0;
+}
+
 /**
- * LDS of rerank_given_kernel for up to R reranked keys, KO kept and D coordinates, carved from its dynamic LDS in this
- * order: the merge's exchange (8-byte aligned), the ids and their distances, the query.  Sized per launch.
+ * LDS of rerank_keep_kernel for R reranked keys, KO kept, D coordinates and a history set of `slots`, carved from its
+ * dynamic LDS in this order: the region the selection and the merge use in turn (8-byte aligned), the selected ids,
+ * their distances, the ids left to rerank, the query, the history set.  Sized per launch, so small R and KO leave room
+ * for more workgroups per CU.
  */
 __host__ __device__ constexpr auto rerank_region_bytes(int R, int KO, int threads) -> size_t
 {
-  return (merge_bytes(keys_per_thread(KO + R, threads) * threads) + 7) / 8 * 8;
+  const size_t merge = merge_bytes(keys_per_thread(KO + R, threads) * threads);
+  return ((sizeof(bin_select_lds) > merge ? sizeof(bin_select_lds) : merge) + 7) / 8 * 8;
 }
-__host__ __device__ constexpr auto rerank_lds_bytes(int R, int KO, int D, int threads) -> size_t
+__host__ __device__ constexpr auto rerank_lds_bytes(int R, int KO, int D, int threads, int slots) -> size_t
 {
-  return rerank_region_bytes(R, KO, threads) + static_cast<size_t>(R) * 8 + static_cast<size_t>(D) * 4;
+  return rerank_region_bytes(R, KO, threads) + static_cast<size_t>(R) * 12 + static_cast<size_t>(D) * 4 +
+         static_cast<size_t>(slots) * 4;
+}
+
+/** Slot of id v in the set hs of `slots` slots (a power of two; -1 empty, linear probing), inserting it when
+ * `insert`; -1 when it is absent (a lookup) or the set is full. */
+__device__ __forceinline__ int hist_slot(int* hs, int slots, int v, bool insert)
+{
+  unsigned h = (static_cast<unsigned>(v) * kIdHash) & static_cast<unsigned>(slots - 1);
+  for (int p = 0; p < slots; p++) {
+    const int e = insert ? atomicCAS(&hs[h], -1, v) : hs[h];
+    if (e == v || (insert && e == -1)) return static_cast<int>(h);
+    if (e == -1) return -1;
+    h = (h + 1) & static_cast<unsigned>(slots - 1);
+  }
+  return -1;
 }
 
 /**
- * The R sketch-nearest candidates of every query's row of cand / dist (select_by_bins; search_kernels.cuh:259-322) into
- * sel [m, R] and their count into nsel [m]; with mark, each selected entry of the row gets kSeenBit.  One workgroup of
- * NT threads per query (NT kSelCache keys held in registers).
- */
-template <int NT>
-__global__ __launch_bounds__(NT) void select_rows_kernel(int* __restrict__ cand, const float* __restrict__ dist,
-                                                         const int* __restrict__ nin, int W, int R, int* __restrict__ sel,
-                                                         int* __restrict__ nsel, bool mark)
-{
-  const int q = blockIdx.x;
-  __shared__ bin_select_lds sh;
-  int* crow    = cand + static_cast<int64_t>(q) * W;
-  const int n  = min(nin[q], W);
-  const int ns = select_by_bins(reinterpret_cast<const unsigned*>(dist + static_cast<int64_t>(q) * W), crow, n, R,
-                                sel + static_cast<int64_t>(q) * R, nullptr, nullptr, mark ? crow : nullptr, sh);
-  if (threadIdx.x == 0) nsel[q] = ns;
-}
-
-/**
- * Exact rerank of each query's selected candidates sel[q, 0 .. nsel[q]) (the R sketch-nearest, selected by the gather
- * or select_rows_kernel), merged into its kept list of the best KO (search_kernels.cuh:421-467).  fresh: the kept list
- * starts empty.  One workgroup of NT threads per query.
+ * Exact rerank of the R sketch-nearest candidates of a query, merged into its kept list of the best
+ * KO (search_kernels.cuh:421-467).  fresh: the kept list starts empty.  One workgroup of NT threads per query, C keys a
+ * thread in the merge (the host's choice for KO + R).
  *
- * Rounds after the first skip what an earlier round reranked.  Whenever the kept list is merged, it becomes the KO
- * smallest distinct keys of every key merged so far. A selected candidate with kSeenBit was reranked and merged by an
- * earlier round, so its exact key is either in the kept list already (merging it again changes nothing) or larger than
- * all KO kept keys (it cannot enter). Dropping it leaves the merge's result unchanged. It is neither read nor merged.
- * Their count goes to nskip [m] (when not null).
+ * Rounds after the first skip what an earlier round reranked.  hist [m, H] holds every round's selected ids (each round
+ * R entries, -1 padded): this round's go to hist[q, hoff .. hoff + R) when hstore, and unless fresh the ids at
+ * hist[q, 0 .. hoff) (the last kHistWindow of them) are the earlier rounds'.  Whenever the kept list is merged, it
+ * becomes the KO smallest distinct keys of every key merged so far, so an id an earlier round reranked has its exact key
+ * either in the kept list already (merging it again changes nothing) or above all KO kept keys (it cannot enter):
+ * dropping it leaves the merge's result unchanged.  It is neither read nor merged; nskip [m] (when not null) gets the
+ * count.  The window's ids are loaded as the kernel starts and their set (hslots slots, at least twice the window)
+ * cleared, so neither waits after the selection.
  */
+// Eight waves a SIMD: the selection's 64-bit tie bounds took the kernel to about 100 SGPRs, which allow seven (the
+// excess spills to VGPR lanes); measured at 10M rows, the first round's launch went from 94 to 84 us.  Merges of 8
+// keys a thread (KO + R above 512 on 128 threads) need more than the 64 VGPRs of eight waves: seven.
 template <int LX, int NT, int C>
-__global__ __launch_bounds__(NT) void rerank_given_kernel(const int* __restrict__ sel, const int* __restrict__ nsel, int R,
-                                                          const __half* __restrict__ vectors, int64_t N, int D,
-                                                          const float* __restrict__ Q, int KO, long long* __restrict__ bi,
-                                                          float* __restrict__ bd, bool fresh, int* __restrict__ nskip)
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(C <= 4 ? 8 : 7, C <= 4 ? 8 : 7))) void
+rerank_keep_kernel(
+  const int* __restrict__ cand, const float* __restrict__ dist, const int* __restrict__ nin, int W,
+  const __half* __restrict__ vectors, int D, const float* __restrict__ Q, int R, int KO,
+  long long* __restrict__ bi, float* __restrict__ bd, bool fresh, int* __restrict__ hist, int H, int hoff, bool hstore,
+  int hslots, int* __restrict__ nskip)
 {
   const int q = blockIdx.x;
   extern __shared__ uint64_t rk_lds[];
+  __shared__ int nfresh;  // selected ids no earlier round reranked
   const size_t region = rerank_region_bytes(R, KO, NT);
   auto* base          = reinterpret_cast<unsigned char*>(rk_lds);
+  auto& sel           = *reinterpret_cast<bin_select_lds*>(base);
   const int keys      = keys_per_thread(KO + R, NT) * NT;
   merge_view mv{reinterpret_cast<uint64_t*>(base), reinterpret_cast<int*>(base + static_cast<size_t>(keys) * 8 + 16 * 8),
                 reinterpret_cast<uint64_t*>(base + static_cast<size_t>(keys) * 8)};
   int* sid  = reinterpret_cast<int*>(base + region);
   float* sd = reinterpret_cast<float*>(sid + R);
-  float* sq = sd + R;
+  int* rid  = reinterpret_cast<int*>(sd + R);  // the selected ids left to rerank (filtered rounds)
+  float* sq = reinterpret_cast<float*>(rid + R);
+  int* hs   = reinterpret_cast<int*>(sq + D);  // the history window's set
+  int* hrow = hist != nullptr ? hist + static_cast<int64_t>(q) * H : nullptr;
+  const bool filter = !fresh && hoff > 0;  // the host passes hist and hslots >= 2 min(hoff, kHistWindow) then
+  constexpr int kPer = (kHistWindow + NT - 1) / NT;
+  int hv[kPer];
+  if (filter) {
+    const int h0 = hoff > kHistWindow ? hoff - kHistWindow : 0;
+#pragma unroll
+    for (int e = 0; e < kPer; e++) {  // unconditional loads of clamped in-bounds entries, then a select
+      const int i = h0 + threadIdx.x + e * NT;
+      const int v = hrow[i < hoff ? i : hoff - 1];
+      hv[e]       = i < hoff ? v : -1;
+    }
+    for (int i = threadIdx.x; i < hslots; i += NT)
+      hs[i] = -1;
+    if (threadIdx.x == 0) nfresh = 0;
+  }
+  const int n = min(nin[q], W);
   for (int i = threadIdx.x; i < D; i += blockDim.x)
     sq[i] = Q[static_cast<int64_t>(q) * D + i];
-  const int ns     = min(nsel[q], R);
-  const int* srow  = sel + static_cast<int64_t>(q) * R;
-  // the ids to rerank into LDS, in order, without the rerank bit: all of them when fresh, else those no earlier round
-  // reranked; an id at or above N (no row of the index) is dropped, as the gathers drop them
-  constexpr int E = (kMaxRerank + NT - 1) / NT;
-  int v[E], mine = 0;
-  bool keep[E];
+  // the selection's barriers order the set's clearing before its inserts below
+  const int ns = select_by_bins(reinterpret_cast<const unsigned*>(dist + static_cast<int64_t>(q) * W),
+                                cand + static_cast<int64_t>(q) * W, n, R, sid, nullptr, sel);
+  if (hstore)
+    for (int t = threadIdx.x; t < R; t += NT)
+      hrow[hoff + t] = t < ns ? sid[t] : -1;
+  int nr        = ns;  // the selected ids reranked here
+  const int* rr = sid;
+  if (filter) {
 #pragma unroll
-  for (int e = 0; e < E; e++) {
-    const int i = threadIdx.x * E + e;
-    v[e]        = srow[i < ns ? i : 0];
-    keep[e]     = i < ns && (fresh || (static_cast<unsigned>(v[e]) & kSeenBit) == 0) &&
-              static_cast<int64_t>(static_cast<unsigned>(v[e]) & ~kSeenBit) < N;
-    mine += keep[e] ? 1 : 0;
+    for (int e = 0; e < kPer; e++)
+      if (hv[e] >= 0) hist_slot(hs, hslots, hv[e], true);
+    __syncthreads();
+    for (int i0 = 0; i0 < ns; i0 += NT) {  // uniform trip count: the appends use ballots
+      const int i     = i0 + threadIdx.x;
+      const int v     = sid[i < ns ? i : 0];
+      const bool keep = i < ns && hist_slot(hs, hslots, v, false) < 0;
+      const int at    = wave_append(keep, &nfresh);
+      if (keep) rid[at] = v;
+    }
+    __syncthreads();
+    nr = nfresh;
+    rr = rid;
   }
-  int nr = 0;
-  int at = block_exclusive_sum(mine, mv.wsum, &nr);
-#pragma unroll
-  for (int e = 0; e < E; e++)
-    if (keep[e]) sid[at++] = static_cast<int>(static_cast<unsigned>(v[e]) & ~kSeenBit);
-  __syncthreads();
   if (nskip != nullptr && threadIdx.x == 0) nskip[q] = ns - nr;
-  exact_distances<LX>(sid, nr, vectors, D, sq, sd);
-  // C keys a thread hold KO + R (the host's choice): the merge's registers are sized for this launch, not the largest
-  merge_keep<C>(bi + static_cast<int64_t>(q) * KO, bd + static_cast<int64_t>(q) * KO, KO, fresh, sid, sd, nr,
+  exact_distances<LX>(rr, nr, vectors, D, sq, sd);
+  // exact_distances ended with a barrier: the region is free for the merge
+  merge_keep<C>(bi + static_cast<int64_t>(q) * KO, bd + static_cast<int64_t>(q) * KO, KO, fresh, rr, sd, nr,
                 bi + static_cast<int64_t>(q) * KO, bd + static_cast<int64_t>(q) * KO, KO, mv);
 }
 
@@ -1502,7 +1383,7 @@ __global__ __launch_bounds__(512) void sketch_keep_kernel(const int* __restrict_
   __shared__ float sdv[kMaxSketchKO];
   const int n  = min(nin[q], W);
   const int ns = select_by_bins(reinterpret_cast<const unsigned*>(dist + static_cast<int64_t>(q) * W),
-                                cand + static_cast<int64_t>(q) * W, n, KO, sid, sdv, nullptr, nullptr, u.sel);
+                                cand + static_cast<int64_t>(q) * W, n, KO, sid, sdv, u.sel);
   long long* pb = si + static_cast<int64_t>(q) * KO;
   float* pd     = sd + static_cast<int64_t>(q) * KO;
   with_keys_per_thread(KO + ns, blockDim.x, [&](auto c) {
@@ -2001,22 +1882,12 @@ auto gather_smem(int W, int S, int nseg, int max_len, bool lds_slots) -> size_t
 
 namespace {
 
-constexpr size_t kGatherLds = 160 * 1024 - 256;  // the CU's LDS less the kernel's static LDS (state, prefix sums)
-
-}  // namespace
-
-auto gather_lds_slots(int W, int S, int nseg, int max_len) -> bool
-{
-  return gather_smem(W, S, nseg, max_len, true) <= kGatherLds;
-}
-
-namespace {
+constexpr size_t kGatherLds = 160 * 1024 - 256;  // the CU's LDS less the kernel's static LDS (its state)
 
 template <bool kBalanced>
 void gather_impl(bool rows, const int2* seg, int nseg, int max_len, int m, const long long* list_ptr,
                  const int* table, int table_len, int64_t n, const signed char* code, int pitch, const float* scale,
-                 const float* qs, int S, int W, int logW, int* cand, float* dist, int* nout, old_lists const& old,
-                 int* nknown, int R, int* sel, int* nsel, hipStream_t s)
+                 const float* qs, int S, int W, int logW, int* cand, float* dist, int* nout, hipStream_t s)
 {
   OCTEX_EXPECTS(pitch >= S && pitch % 16 == 0, "octex: sketch rows are at least S bytes apart, 16-byte aligned");
   if (m == 0) return;
@@ -2024,19 +1895,10 @@ void gather_impl(bool rows, const int2* seg, int nseg, int max_len, int m, const
   OCTEX_EXPECTS(max_len >= 0, "octex: segment lengths are non-negative");
   OCTEX_EXPECTS(W == (1 << logW) && W <= kMaxHash, "octex: hash set size");
   OCTEX_EXPECTS(S % 16 == 0 && S >= 16 && S <= 512, "octex: sketch width: a multiple of 16, <= 512");
-  const bool lds_slots = gather_lds_slots(W, S, nseg, max_len);  // else the slots go to cand
+  const bool lds_slots = gather_smem(W, S, nseg, max_len, true) <= kGatherLds;  // else the slots go to cand
   const size_t smem    = gather_smem(W, S, nseg, max_len, lds_slots);
   OCTEX_EXPECTS(smem <= kGatherLds, "octex: gather needs %zu bytes of LDS (max 160 KiB)", smem);
   const int cap = gather_cap(W, nseg, max_len);
-  OCTEX_EXPECTS(old.count >= 0 && old.count <= kMaxOld, "octex: at most %d earlier candidate rows", kMaxOld);
-  for (int o = 0; o < old.count; o++)
-    OCTEX_EXPECTS(old.cand[o] != nullptr && old.dist[o] != nullptr && old.n[o] != nullptr && old.W[o] >= 1 &&
-                    old.cand[o] != cand,
-                  "octex: an earlier candidate row list is incomplete or is this gather's own output");
-  old_lists ol = old;
-  if (!lds_slots) ol.count = 0;  // the slot list in cand leaves no room for the reused candidates
-  OCTEX_EXPECTS(sel == nullptr || (nsel != nullptr && R >= 1 && R <= kMaxSketchKO),
-                "octex: a gather's selection takes 1 to 1024 candidates");
   int Lr = 1;  // the reference's lanes per candidate: the next power of two >= S / 16, at most 32
   while (Lr < S / 16 && Lr < 32)
     Lr <<= 1;
@@ -2046,8 +1908,7 @@ void gather_impl(bool rows, const int2* seg, int nseg, int max_len, int m, const
     auto launch             = [&](auto kernel) {
       allow_lds(reinterpret_cast<const void*>(kernel), smem);
       kernel<<<m, kRowsTag ? kGatherRowThreads : kGatherListThreads, smem, s>>>(
-        seg, nseg, list_ptr, table, table_len, n, code, scale, qs, S, pitch, W, logW, cap, cand, dist, nout, ol,
-        nknown, R, sel, nsel);
+        seg, nseg, list_ptr, table, table_len, n, code, scale, qs, S, pitch, W, logW, cap, cand, dist, nout);
     };
     if (lds_slots)
       launch(&gather_kernel<kRowsTag, LR, true, kBalanced>);
@@ -2093,19 +1954,19 @@ void sort_rows(uint64_t* keys, int rows, int width, hipStream_t s)
 void launch_gather(bool rows, const int2* seg, int nseg, int max_len, int m, const long long* list_ptr,
                    const int* table, int table_len, int64_t n, const signed char* code, int pitch,
                    const float* scale, const float* qs, int S, int W, int logW, int* cand, float* dist,
-                   int* nout, old_lists const& old, int* nknown, int R, int* sel, int* nsel, hipStream_t s)
+                   int* nout, hipStream_t s)
 {
   gather_impl<true>(rows, seg, nseg, max_len, m, list_ptr, table, table_len, n, code, pitch, scale, qs, S, W, logW,
-                    cand, dist, nout, old, nknown, R, sel, nsel, s);
+                    cand, dist, nout, s);
 }
 
 void launch_gather_segments(bool rows, const int2* seg, int nseg, int max_len, int m, const long long* list_ptr,
                             const int* table, int table_len, int64_t n, const signed char* code, int pitch,
                             const float* scale, const float* qs, int S, int W, int logW, int* cand, float* dist,
-                            int* nout, old_lists const& old, int* nknown, int R, int* sel, int* nsel, hipStream_t s)
+                            int* nout, hipStream_t s)
 {
   gather_impl<false>(rows, seg, nseg, max_len, m, list_ptr, table, table_len, n, code, pitch, scale, qs, S, W, logW,
-                     cand, dist, nout, old, nknown, R, sel, nsel, s);
+                     cand, dist, nout, s);
 }
 
 void launch_unfused_keep(const int* cand, const float* dist, const int* nin, int m, int W, const __half* vectors,
@@ -2147,40 +2008,34 @@ void launch_unfused_pick(const long long* si, int m, int KO, long long* done, in
   OCTEX_HIP(hipGetLastError());
 }
 
-void launch_select_rows(int* cand, const float* dist, const int* nin, int m, int W, int R, int* sel, int* nsel,
-                        bool mark, hipStream_t s)
-{
-  if (m == 0) return;
-  OCTEX_EXPECTS(R >= 1 && R <= kMaxSketchKO, "octex: a selection of 1 to 1024 candidates");
-  // 128 threads a query while the rows are at most 4096 wide, 256 above (more keys held in registers)
-  if (W > 4096)
-    select_rows_kernel<256><<<m, 256, 0, s>>>(cand, dist, nin, W, R, sel, nsel, mark);
-  else
-    select_rows_kernel<128><<<m, 128, 0, s>>>(cand, dist, nin, W, R, sel, nsel, mark);
-  OCTEX_HIP(hipGetLastError());
-}
-
-void launch_rerank_given(const int* sel, const int* nsel, int m, int R, const __half* vectors, int64_t N, int D,
-                         const float* Q, int KO, long long* si, float* sd, bool fresh, int* nskip, hipStream_t s)
+void launch_rerank_keep(const int* cand, const float* dist, const int* nin, int m, int W, const __half* vectors, int D,
+                        const float* Q, int R, int KO, long long* si, float* sd, bool fresh, int* hist, int H, int hoff,
+                        bool hstore, int* nskip, hipStream_t s)
 {
   if (m == 0) return;
   OCTEX_EXPECTS(R >= 1 && R <= kMaxRerank && KO + R <= kMaxKeepSort && KO >= 1,
                 "octex: rerank in [1, 512] and max(starts, k) + rerank <= 1024");
   OCTEX_EXPECTS(D % 2 == 0, "octex: the dimension must be even");
-  constexpr int nt  = 128;
-  const size_t smem = rerank_lds_bytes(R, KO, D, nt);
-  const int c       = keys_per_thread(KO + R, nt);
+  OCTEX_EXPECTS(hoff >= 0 && (hist != nullptr || (hoff == 0 && !hstore)) && (!hstore || hoff + R <= H) && hoff <= H,
+                "octex: the selected-id history must hold this round's offset and ids");
+  // 128 threads a query (16 queries in flight per CU).  Measured at 100M rows with the history skip: the waves'
+  // launches 0.155 / 0.125 ms on 256 threads (twice the keys held in registers), 0.141 / 0.096 ms on 128
+  constexpr int NT  = kRerankThreads;
+  const int hslots  = !fresh && hoff > 0 ? hist_slots(hoff) : 0;
+  const size_t smem = rerank_lds_bytes(R, KO, D, NT, hslots);
+  const int c       = keys_per_thread(KO + R, NT);
   with_lx(D, [&](auto lx) {
-    auto go = [&](auto kernel) {
-      allow_lds(reinterpret_cast<const void*>(kernel), smem);
-      kernel<<<m, nt, smem, s>>>(sel, nsel, R, vectors, N, D, Q, KO, si, sd, fresh, nskip);
-    };
     constexpr int LX = decltype(lx)::value;
+    auto go          = [&](auto kernel) {
+      allow_lds(reinterpret_cast<const void*>(kernel), smem);
+      kernel<<<m, NT, smem, s>>>(cand, dist, nin, W, vectors, D, Q, R, KO, si, sd, fresh, hist, H, hoff, hstore, hslots,
+                                 nskip);
+    };
     switch (c) {
-      case 1: go(&rerank_given_kernel<LX, nt, 1>); break;
-      case 2: go(&rerank_given_kernel<LX, nt, 2>); break;
-      case 4: go(&rerank_given_kernel<LX, nt, 4>); break;
-      default: go(&rerank_given_kernel<LX, nt, 8>); break;
+      case 1: go(&rerank_keep_kernel<LX, NT, 1>); break;
+      case 2: go(&rerank_keep_kernel<LX, NT, 2>); break;
+      case 4: go(&rerank_keep_kernel<LX, NT, 4>); break;
+      default: go(&rerank_keep_kernel<LX, NT, 8>); break;
     }
   });
   OCTEX_HIP(hipGetLastError());

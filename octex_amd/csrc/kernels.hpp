@@ -22,24 +22,6 @@ constexpr int kGatherListThreads = 256;  // gathers of cell lists (first round):
 constexpr int kGatherRowThreads  = 512;  // gathers of neighbor-table rows (waves)
 constexpr int kKeepThreads    = 256;
 
-/** Bit 31 of an id: in a hash-set entry, "an earlier round scored this id"; in a row of `cand`, "an earlier round's
- * exact rerank took this id" (ids are below 2^31 - 1, so the bit is free in both). */
-constexpr unsigned kSeenBit = 0x80000000u;
-constexpr int kMaxOld       = 4;  // earlier rounds' candidate rows a wave gather takes scores from
-
-/**
- * Candidate rows of earlier rounds of the same batch, whose sketch scores a wave gather reuses: list o holds query q's
- * n[o][q] (at most W[o]) distinct candidates at cand[o] + q W[o] (ids, bit 31 set for ids an exact rerank took) with
- * their scores at dist[o] + q W[o].  count = 0: none.
- */
-struct old_lists {
-  const int* cand[kMaxOld]   = {};
-  const float* dist[kMaxOld] = {};
-  const int* n[kMaxOld]      = {};
-  int W[kMaxOld]             = {};
-  int count                  = 0;
-};
-
 /** log2 of the hash set of a query reading `total` entries: ceil(log2(1.5 total)) in [11, log_cap]. */
 inline auto hash_log_host(int total, int log_cap) -> int
 {
@@ -68,9 +50,6 @@ void launch_probe(const __half* Y, int m, int C, int L, int B, const float* inv_
 /** LDS bytes of a gather over `nseg` segments per query with hash sets up to W slots; lds_slots: with the
  * candidates' 16-bit slot list in LDS too (else it is kept in the query's row of cand). */
 auto gather_smem(int W, int S, int nseg, int max_len, bool lds_slots) -> size_t;
-/** Whether a gather of these sizes keeps its candidates' slot list in LDS, the layout that can reuse earlier
- * rounds' scores (a 2^15-slot hash set leaves no room for it: the list then lives in `cand`). */
-auto gather_lds_slots(int W, int S, int nseg, int max_len) -> bool;
 /**
  * The distinct ids of every query's segments with their sketch scores into cand / dist [m, W] (ids in any order,
  * count in nout [m]).
@@ -78,22 +57,17 @@ auto gather_lds_slots(int W, int S, int nseg, int max_len) -> bool;
  * Lists: segment c of a query reads copy c's lists at list_ptr[c] (a device pointer per copy).
  * code [n, pitch]: the S sketch codes of row v start at code + v * pitch.
  * max_len: no segment is longer (a query keeps at most min(W, nseg * max_len) candidates).
- * old: earlier rounds' candidate rows.  An id found there takes its score (and its rerank bit) from there instead of
- * reading its sketch row: the same score, since a query's scores do not change between rounds.  Those candidates
- * come last in the row, and their count goes to nknown [m] (when not null).  Used only when gather_lds_slots.
- * sel (when not null): the R sketch-nearest candidates of each row (launch_select_rows' selection, with mark) are
- * selected as the gather ends, while the row is in the L2, into sel [m, R] and their count into nsel [m].
  */
 void launch_gather(bool rows, const int2* seg, int nseg, int max_len, int m, const long long* list_ptr,
                    const int* table, int table_len, int64_t n, const signed char* code, int pitch,
                    const float* scale, const float* qs, int S, int W, int logW, int* cand, float* dist,
-                   int* nout, old_lists const& old, int* nknown, int R, int* sel, int* nsel, hipStream_t s);
+                   int* nout, hipStream_t s);
 /** launch_gather without the load balance (balanced_gather = false): a wavefront reads each segment whole
  * (search_kernels.cuh:687-792).  Same arguments and results. */
 void launch_gather_segments(bool rows, const int2* seg, int nseg, int max_len, int m, const long long* list_ptr,
                             const int* table, int table_len, int64_t n, const signed char* code, int pitch,
                             const float* scale, const float* qs, int S, int W, int logW, int* cand, float* dist,
-                            int* nout, old_lists const& old, int* nknown, int R, int* sel, int* nsel, hipStream_t s);
+                            int* nout, hipStream_t s);
 /**
  * The kept list merged with a round's candidates without the fused kernels (fused_merge = false,
  * search.cu:213-253): every candidate's key into ukey [m, W] and each row sorted, the pool of the kept list
@@ -108,21 +82,16 @@ void launch_unfused_keep(const int* cand, const float* dist, const int* nin, int
 void launch_unfused_pick(const long long* si, int m, int KO, long long* done, int E, int off, int S, int rowlen,
                          uint64_t* dsort, int Ep, unsigned char* fresh, int2* seg2, hipStream_t s);
 /**
- * The R sketch-nearest candidates of every query's row of cand / dist [m, W] (nin [m] of them; by (distance bits,
- * id), ids compared without bit 31) into sel [m, R], their count into nsel [m].  mark: set bit 31 of every selected
- * candidate in its row of cand, for the later rounds that reuse these rows.
+ * Exact rerank of each query's R sketch-nearest candidates (of its nin [m] in cand / dist [m, W]) merged into its kept
+ * list si / sd [m, KO] (search_kernels.cuh:421-467).
+ * hist [m, H] (may be null with hoff 0 and no store): the selected ids of a batch's rounds, R entries each, -1 padded;
+ * with hstore this round's go to hist[q, hoff .. hoff + R).  Unless fresh, the ids of hist[q, 0 .. hoff) are those the
+ * earlier rounds reranked into this kept list; those of its last 256 entries, selected again, are neither read nor
+ * merged (the kept list of the KO smallest keys comes out the same), and nskip [m] (when not null) gets their count.
  */
-void launch_select_rows(int* cand, const float* dist, const int* nin, int m, int W, int R, int* sel, int* nsel,
-                        bool mark, hipStream_t s);
-/**
- * Exact rerank of each query's selected candidates sel[q, 0 .. nsel[q]) (at most R) merged into its kept list si / sd
- * [m, KO] (search_kernels.cuh:421-467).  Candidates with bit 31 set were reranked by an earlier round of the batch:
- * unless fresh, their exact keys are already merged into this kept list, so they are neither read nor merged again
- * (the kept list of the KO smallest keys comes out the same); nskip [m] (when not null) gets their count.  vectors
- * [N, D]: ids at or above N are dropped.
- */
-void launch_rerank_given(const int* sel, const int* nsel, int m, int R, const __half* vectors, int64_t N, int D,
-                         const float* Q, int KO, long long* si, float* sd, bool fresh, int* nskip, hipStream_t s);
+void launch_rerank_keep(const int* cand, const float* dist, const int* nin, int m, int W, const __half* vectors, int D,
+                        const float* Q, int R, int KO, long long* si, float* sd, bool fresh, int* hist, int H, int hoff,
+                        bool hstore, int* nskip, hipStream_t s);
 void launch_sketch_keep(const int* cand, const float* dist, const int* nin, int m, int W, int KO,
                         long long* si, float* sd, bool fresh, hipStream_t s);
 void launch_pick_starts(const long long* si, int m, int KO, long long* done, int E, int off, int S,

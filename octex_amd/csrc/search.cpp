@@ -76,8 +76,8 @@ auto make_shape(index_impl const& ix, search_params const& sp, int m, int k) -> 
                   "octex: starts x table_len too large for the shared-memory hash set");
     sh.logW2 = std::clamp(log2_ceil(static_cast<int64_t>(std::ceil(S * ix.table_len * 1.5f))), kMinLogHash, log_max);
     sh.W2    = 1 << sh.logW2;
-    // wave gathers reuse earlier rounds' scores when their slot lists fit in LDS
-    if (gather_lds_slots(sh.W2, ix.sketch_width, S, ix.table_len)) sh.ring = std::min(sp.waves, kMaxRing);
+    // the fused exact rerank keeps the ids every round but the last selects, to skip them when selected again
+    if (sp.fused_merge && !sp.sketch_rank) sh.H = sh.R1 + sh.R2 * (sp.waves - 1);
   }
   if (!sp.fused_merge) {  // the pools of the unfused merge: the kept list and the R best candidates
     auto pool = [&](int R) { return 1 << log2_ceil(sh.KO + (sp.sketch_rank ? sh.KO : R)); };
@@ -114,17 +114,11 @@ auto carve_buffers(index_impl const& ix, plan_shape const& sh, void* base, batch
   if (sh.sp.waves > 0) {
     take(b.done, m * st * sh.sp.waves);
     take(b.seg2, m * st);
-    for (int r = 0; r < sh.ring; r++) {
-      take(b.cand2[r], m * sh.W2);
-      take(b.dist2[r], m * sh.W2);
-      take(b.n2[r], m);
-    }
-    take(b.nknown, m);
+    take(b.cand2, m * sh.W2);
+    take(b.dist2, m * sh.W2);
+    take(b.n2, m);
     take(b.nskip, m);
-  }
-  if (sh.sp.fused_merge && !sh.sp.sketch_rank) {
-    take(b.sel, m * std::max(sh.R1, sh.sp.waves > 0 ? sh.R2 : 0));
-    take(b.nsel, m);
+    take(b.hist, m * sh.H);
   }
   take(b.bi, m * sh.k);
   take(b.bd, m * sh.k);
@@ -146,15 +140,14 @@ auto named_buffer(index_impl const& ix, plan_shape const& sh, batch_buffers cons
   const size_t wv = static_cast<size_t>(sh.sp.waves), W = static_cast<size_t>(sh.W), W2 = static_cast<size_t>(sh.W2);
   const size_t KO = static_cast<size_t>(sh.KO), k = static_cast<size_t>(sh.k);
   const size_t wdt = size_t{8} * static_cast<size_t>(ix.blocks) * C;
-  const int last   = wv > 0 ? static_cast<int>((wv - 1) % static_cast<size_t>(sh.ring)) : 0;  // the last wave's rows
   const std::pair<const char*, std::pair<const void*, size_t>> all[] = {
     {"queries", {b.qbuf, m * D * 4}}, {"qc", {b.qc, m * D * 4}},     {"qh", {b.qh, m * D * 2}},
     {"Y", {b.Y, m * wdt * 2}},        {"qs", {b.qs, m * S * 4}},     {"seg", {b.seg, m * C * 8}},
     {"cand", {b.cand, m * W * 4}},    {"dist", {b.dist, m * W * 4}}, {"nin", {b.nin, m * 4}},
     {"si", {b.si, m * KO * 8}},       {"sd", {b.sd, m * KO * 4}},    {"done", {b.done, m * st * wv * 8}},
-    {"seg2", {b.seg2, m * st * 8}},   {"cand2", {b.cand2[last], m * W2 * 4}}, {"dist2", {b.dist2[last], m * W2 * 4}},
-    {"n2", {b.n2[last], wv > 0 ? m * 4 : 0}}, {"nknown", {b.nknown, wv > 0 ? m * 4 : 0}},
-    {"nskip", {b.nskip, wv > 0 ? m * 4 : 0}}, {"bi", {b.bi, m * k * 8}},  {"bd", {b.bd, m * k * 4}},
+    {"seg2", {b.seg2, m * st * 8}},   {"cand2", {b.cand2, m * W2 * 4}}, {"dist2", {b.dist2, m * W2 * 4}},
+    {"n2", {b.n2, wv > 0 ? m * 4 : 0}}, {"nskip", {b.nskip, wv > 0 ? m * 4 : 0}},
+    {"hist", {b.hist, m * static_cast<size_t>(sh.H) * 4}}, {"bi", {b.bi, m * k * 8}},  {"bd", {b.bd, m * k * 4}},
   };
   for (auto const& [name, where] : all)
     if (n == name) return where.first != nullptr ? where : std::pair<const void*, size_t>(nullptr, 0);
@@ -194,24 +187,22 @@ auto batch_stages(index_impl const& ix, plan_shape const& sh, batch_buffers cons
   });
   // stage names as profiled: the ablation paths are marked, so a profile shows which kernels ran
   const std::string whole = balanced ? "" : "_whole", unfused = fused ? "" : "_unfused";
-  // the fused exact rerank takes its R candidates from the gather, which selects them as it ends
-  const bool given = fused && !sketch_rank;
   auto gather = [&](std::string const& name, bool rows, const int2* seg, int nseg, int max_len, int W, int logW,
-                    int* cand, float* dist, int* n, old_lists const& ol, int* nknown, int R) {
-    add((name + whole).c_str(), [&ix, b, s, m, S, rows, seg, nseg, max_len, W, logW, cand, dist, n, balanced, ol,
-                                 nknown, R, given] {
+                    int* cand, float* dist, int* n) {
+    add((name + whole).c_str(), [&ix, b, s, m, S, rows, seg, nseg, max_len, W, logW, cand, dist, n, balanced] {
       (balanced ? launch_gather : launch_gather_segments)(
         rows, seg, nseg, max_len, m, rows ? nullptr : ix.list_ptr.as<long long>(), rows ? ix.rows() : nullptr,
-        ix.table_len, ix.n, ix.code(), ix.sketch_pitch, ix.scale.as<float>(), b.qs, S, W, logW, cand, dist, n, ol,
-        nknown, R, given ? b.sel : nullptr, given ? b.nsel : nullptr, s);
+        ix.table_len, ix.n, ix.code(), ix.sketch_pitch, ix.scale.as<float>(), b.qs, S, W, logW, cand, dist, n, s);
     });
   };
-  // the wave gathers reuse earlier rounds' scores when their slot lists fit in LDS; the gathers' selections mark what
-  // the exact rerank takes, and the rerank skips what earlier rounds took
-  const bool reuse = sh.sp.waves > 0 && gather_lds_slots(sh.W2, S, sh.sp.starts, ix.table_len);
-  // the kept list merged with a round's candidates: fused (one kernel) or through global-memory sorts
-  auto keep = [&](std::string const& base_name, int* cand, const float* dist, const int* n, int W, int R,
-                  int pool, bool fresh) {
+  // the kept list merged with a round's candidates: fused (one kernel) or through global-memory sorts.  The fused
+  // rerank of round r (0 the first) keeps its selected ids at hist[:, off(r) ..) for the later rounds, which skip them:
+  // off(0) = 0, off(r) = rerank + (r - 1) wave_rerank
+  auto keep = [&](std::string const& base_name, const int* cand, const float* dist, const int* n, int W, int R,
+                  int pool, int round) {
+    const bool fresh = round == 0;
+    const int hoff   = round == 0 ? 0 : sh.R1 + (round - 1) * sh.R2;
+    const bool store = sh.H > 0 && round < sh.sp.waves;
     const std::string nm = base_name + unfused;
     const char* name     = nm.c_str();
     if (fused && sketch_rank)
@@ -219,9 +210,9 @@ auto batch_stages(index_impl const& ix, plan_shape const& sh, batch_buffers cons
         launch_sketch_keep(cand, dist, n, m, W, sh.KO, b.si, b.sd, fresh, s);
       });
     else if (fused)
-      add(name, [&ix, b, sh, s, m, D, R, fresh] {
-        launch_rerank_given(b.sel, b.nsel, m, R, ix.vecs(), ix.n, D, b.qbuf, sh.KO, b.si, b.sd, fresh,
-                            fresh ? nullptr : b.nskip, s);
+      add(name, [&ix, b, sh, s, m, D, cand, dist, n, W, R, fresh, hoff, store] {
+        launch_rerank_keep(cand, dist, n, m, W, ix.vecs(), D, b.qbuf, R, sh.KO, b.si, b.sd, fresh,
+                           sh.H > 0 ? b.hist : nullptr, sh.H, sh.H > 0 ? hoff : 0, store, fresh ? nullptr : b.nskip, s);
       });
     else
       add(name, [&ix, b, sh, s, m, D, cand, dist, n, W, R, pool, fresh, sketch_rank] {
@@ -229,26 +220,10 @@ auto batch_stages(index_impl const& ix, plan_shape const& sh, batch_buffers cons
                             sketch_rank ? sh.KO : R, sh.KO, pool, fresh, b.ukey, b.upool, b.si, b.sd, s);
       });
   };
-  gather("gather_lists", false, b.seg, C, sh.lr, sh.W, sh.logW, b.cand, b.dist, b.nin, old_lists{}, nullptr, sh.R1);
-  keep(sketch_rank ? "sketch_keep" : "rerank_keep", b.cand, b.dist, b.nin, sh.W, sh.R1, sh.pool1, true);
+  gather("gather_lists", false, b.seg, C, sh.lr, sh.W, sh.logW, b.cand, b.dist, b.nin);
+  keep(sketch_rank ? "sketch_keep" : "rerank_keep", b.cand, b.dist, b.nin, sh.W, sh.R1, sh.pool1, 0);
   const int st = sh.sp.starts, nw = sh.sp.waves;
   for (int wv = 0; wv < nw; wv++) {
-    const int r = wv % sh.ring;
-    old_lists ol;  // the rows whose scores this wave reuses: the first round's, then the ring's earlier waves
-    auto add_old = [&](int* c, float* d, int* n, int W) {
-      ol.cand[ol.count] = c;
-      ol.dist[ol.count] = d;
-      ol.n[ol.count]    = n;
-      ol.W[ol.count]    = W;
-      ol.count++;
-    };
-    if (reuse) {
-      add_old(b.cand, b.dist, b.nin, sh.W);
-      for (int back = 1; back < sh.ring && wv - back >= 0; back++) {
-        const int rb = (wv - back) % sh.ring;
-        add_old(b.cand2[rb], b.dist2[rb], b.n2[rb], sh.W2);
-      }
-    }
     add(("pick_starts" + unfused).c_str(), [&ix, b, sh, s, m, st, nw, wv, fused] {
       if (fused)
         launch_pick_starts(b.si, m, sh.KO, b.done, st * nw, wv * st, st, ix.table_len, b.seg2, s);
@@ -256,10 +231,9 @@ auto batch_stages(index_impl const& ix, plan_shape const& sh, batch_buffers cons
         launch_unfused_pick(b.si, m, sh.KO, b.done, st * nw, wv * st, st, ix.table_len, b.dsort, sh.Ep, b.fresh,
                             b.seg2, s);
     });
-    gather("gather_rows", true, b.seg2, st, ix.table_len, sh.W2, sh.logW2, b.cand2[r], b.dist2[r], b.n2[r], ol,
-           b.nknown, sh.R2);
-    keep(sketch_rank ? "sketch_keep_wave" : "rerank_keep_wave", b.cand2[r], b.dist2[r], b.n2[r], sh.W2, sh.R2,
-         sh.pool2, false);
+    gather("gather_rows", true, b.seg2, st, ix.table_len, sh.W2, sh.logW2, b.cand2, b.dist2, b.n2);
+    keep(sketch_rank ? "sketch_keep_wave" : "rerank_keep_wave", b.cand2, b.dist2, b.n2, sh.W2, sh.R2, sh.pool2,
+         wv + 1);
   }
   if (sketch_rank && sh.FR > 0)
     add("final_rerank", [&ix, b, sh, s, m, D] {
@@ -403,9 +377,7 @@ void profile_batch(index_impl& ix, plan& pl, int reps, std::vector<std::string>&
   for (auto& st2 : steps)
     names.push_back(st2.name);
   cnt = profile_counters{};
-  const bool reuse = sh.sp.waves > 0 && gather_lds_slots(sh.W2, ix.sketch_width, st, ix.table_len);
   std::vector<int> nin(m), n2(m), nk(m);
-  std::vector<std::vector<int>> n2w;  // every wave's distinct counts (the old rows of the later waves)
   std::vector<int2> segh(static_cast<size_t>(m) * std::max(C, st));
   for (int r = 0; r < reps; r++) {
     const bool last = r + 1 == reps;
@@ -448,19 +420,11 @@ void profile_batch(index_impl& ix, plan& pl, int reps, std::vector<std::string>&
         for (int64_t j = 0; j < int64_t{m} * st; j++)
           cnt.starts2[wv] += segh[j].y > 0;
       } else if (nm == "gather_rows") {
-        const int slot = wv % sh.ring;
-        OCTEX_HIP(hipMemcpy(n2.data(), b.n2[slot], sizeof(int) * m, hipMemcpyDeviceToHost));
-        OCTEX_HIP(hipMemcpy(nk.data(), b.nknown, sizeof(int) * m, hipMemcpyDeviceToHost));
-        for (int q = 0; q < m; q++) {
-          cnt.distinct2[wv] += n2[q];
-          cnt.reranked2[wv] += std::min(n2[q], sh.sp.sketch_rank ? sh.KO : sh.R2);
-          cnt.known2[wv] += nk[q];
-          if (!reuse) continue;
-          cnt.oldread2[wv] += std::min(nin[q], sh.W);  // the old rows: the first round's and the ring's earlier waves
-          for (int back = 1; back < sh.ring && wv - back >= 0; back++)
-            cnt.oldread2[wv] += std::min(n2w[wv - back][q], sh.W2);
+        OCTEX_HIP(hipMemcpy(n2.data(), b.n2, sizeof(int) * m, hipMemcpyDeviceToHost));
+        for (int v : n2) {
+          cnt.distinct2[wv] += v;
+          cnt.reranked2[wv] += std::min(v, sh.sp.sketch_rank ? sh.KO : sh.R2);
         }
-        n2w.push_back(n2);
       } else if (nm == "rerank_keep_wave") {
         OCTEX_HIP(hipMemcpy(nk.data(), b.nskip, sizeof(int) * m, hipMemcpyDeviceToHost));
         for (int v : nk)

@@ -26,31 +26,24 @@ struct plan_shape {
   int W = 0, logW = 0, W2 = 0, logW2 = 0;  // hash-set / candidate capacity per query
   int pool1 = 0, pool2 = 0;                // unfused merge (fused_merge = false): keys per query's pool
   int Ep = 0;                              // unfused start points: sorted expanded ids per query
-  int ring = 1;  // waves' candidate rows kept: wave w writes row set w % ring and reuses the scores of the first round
-                 // and of the ring - 1 waves before it (1: no reuse, the row gathers keep their slot lists in cand)
+  int H = 0;  // the fused rerank's history of selected ids per query: rerank + wave_rerank (waves - 1)
 };
-
-constexpr int kMaxRing = 3;  // wave candidate row sets kept for reuse
 
 /**
  * Where every per-batch array lies (device addresses): qbuf f32 [m, D] queries; qc f32 / qh f16 [m, D]
  * centred; Y f16 [m, C 8b]; qs f32 [m, S]; seg int2 [m, C]; cand i32 / dist f32 [m, W], nin [m]; si i64 /
- * sd f32 [m, KO] kept list; done i64 [m, starts waves]; seg2 int2 [m, starts]; cand2 / dist2 [m, W2], n2 [m],
- * one set per ring slot; nknown [m] (candidates of the last wave gather whose scores came from earlier rows), nskip
- * [m] (selected candidates the last rerank did not rerank again); with fused_merge, sel i32 [m, max(rerank,
- * wave_rerank)] and nsel [m] (a round's selected candidates, from its gather to its rerank); bi i64 / bd f32 [m, k];
- * with fused_merge = false also ukey u64 [m, max(W, W2)] candidate keys (sorted in
- * place), upool u64 [m, max(pool1, pool2)] pools, dsort i64 [m, Ep] the ids earlier waves expanded, sorted
- * (Ep the power of two >= starts (waves - 1)), and fresh u8 [m, KO].
+ * sd f32 [m, KO] kept list; done i64 [m, starts waves]; seg2 int2 [m, starts]; cand2 / dist2 [m, W2], n2 [m];
+ * nskip [m] (selected candidates the last wave's rerank did not rerank again); hist i32 [m, H] (the fused rerank's
+ * selected ids of every round but the last); bi i64 / bd f32 [m, k]; with fused_merge = false also ukey u64
+ * [m, max(W, W2)] candidate keys (sorted in place), upool u64 [m, max(pool1, pool2)] pools, dsort i64 [m, Ep] the ids
+ * earlier waves expanded, sorted (Ep the power of two >= starts (waves - 1)), and fresh u8 [m, KO].
  */
 struct batch_buffers {
-  float *qbuf = nullptr, *qc = nullptr, *qs = nullptr, *dist = nullptr, *sd = nullptr, *bd = nullptr;
-  float* dist2[kMaxRing] = {};
+  float *qbuf = nullptr, *qc = nullptr, *qs = nullptr, *dist = nullptr, *sd = nullptr, *dist2 = nullptr,
+        *bd = nullptr;
   __half *qh = nullptr, *Y = nullptr;
   int2 *seg = nullptr, *seg2 = nullptr;
-  int *cand = nullptr, *nin = nullptr, *nknown = nullptr, *nskip = nullptr, *sel = nullptr, *nsel = nullptr;
-  int* cand2[kMaxRing] = {};
-  int* n2[kMaxRing]    = {};
+  int *cand = nullptr, *nin = nullptr, *cand2 = nullptr, *n2 = nullptr, *nskip = nullptr, *hist = nullptr;
   long long *si = nullptr, *done = nullptr, *bi = nullptr;
   uint64_t *ukey = nullptr, *upool = nullptr, *dsort = nullptr;
   unsigned char* fresh = nullptr;
@@ -93,9 +86,7 @@ void launch_batch(index_impl const& ix, plan_shape const& sh, batch_buffers cons
 struct profile_counters {
   int64_t seg_hits = 0, entries1 = 0, distinct1 = 0, reranked1 = 0;
   int64_t starts2[16] = {}, distinct2[16] = {}, reranked2[16] = {};
-  int64_t known2[16] = {};    // wave candidates whose scores came from earlier rounds' rows
-  int64_t oldread2[16] = {};  // entries of earlier rounds' rows each wave gather read
-  int64_t skipped2[16] = {};  // selected wave candidates not reranked again
+  int64_t skipped2[16] = {};  // selected wave candidates not reranked again (an earlier round reranked them)
   int64_t hit_level[8] = {};  // probe hits by level (0 the finest); misses are m C - seg_hits
 };
 void profile_batch(index_impl& ix, plan& pl, int reps, std::vector<std::string>& names, std::vector<double>& ms,

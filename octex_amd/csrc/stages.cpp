@@ -92,26 +92,13 @@ extern "C" cuvsError_t octexStageProbe(const void* Y, int32_t m, int32_t C, int3
   });
 }
 
-extern "C" cuvsError_t octexStageGatherReuse(int32_t rows, const int32_t* seg, int32_t nseg, int32_t m,
-                                             const int32_t* lists, int64_t stride, const int32_t* table,
-                                             int32_t table_len, int64_t n, const int8_t* code, const float* scale,
-                                             const float* qs, int32_t S, int32_t W, int32_t* cand, float* dist,
-                                             int32_t* nout, int32_t n_old, const int32_t* const* old_cand,
-                                             const float* const* old_dist, const int32_t* const* old_n,
-                                             const int32_t* old_W, int32_t* nknown, int32_t R, int32_t* sel,
-                                             int32_t* nsel, void* stream)
+extern "C" cuvsError_t octexStageGather(int32_t rows, const int32_t* seg, int32_t nseg, int32_t m,
+                                        const int32_t* lists, int64_t stride, const int32_t* table,
+                                        int32_t table_len, int64_t n, const int8_t* code, const float* scale, const float* qs,
+                                        int32_t S, int32_t W, int32_t* cand, float* dist, int32_t* nout,
+                                        void* stream)
 {
   return run(stream, [&](hipStream_t s) {
-    OCTEX_EXPECTS(n_old >= 0 && n_old <= kMaxOld, "octex: at most %d earlier candidate rows", kMaxOld);
-    old_lists ol;
-    for (int o = 0; o < n_old; o++) {
-      need(old_cand, "old_cand"), need(old_dist, "old_dist"), need(old_n, "old_n"), need(old_W, "old_W");
-      ol.cand[o] = old_cand[o];
-      ol.dist[o] = old_dist[o];
-      ol.n[o]    = old_n[o];
-      ol.W[o]    = old_W[o];
-    }
-    ol.count = n_old;
     need(seg, "seg"), need(code, "code"), need(scale, "scale"), need(qs, "qs");
     need(cand, "cand"), need(dist, "dist"), need(nout, "nout");
     if (rows)
@@ -136,58 +123,32 @@ extern "C" cuvsError_t octexStageGatherReuse(int32_t rows, const int32_t* seg, i
     }
     launch_gather(rows != 0, reinterpret_cast<const int2*>(seg), nseg, max_len, m, ptrs.as<long long>(), table, table_len,
                   n, reinterpret_cast<const signed char*>(code), S, scale, qs, S, W, log2_ceil(W), cand, dist,
-                  nout, ol, nknown, R, sel, nsel, s);
+                  nout, s);
     OCTEX_HIP(hipStreamSynchronize(s));
   });
 }
 
-extern "C" cuvsError_t octexStageGather(int32_t rows, const int32_t* seg, int32_t nseg, int32_t m,
-                                        const int32_t* lists, int64_t stride, const int32_t* table,
-                                        int32_t table_len, int64_t n, const int8_t* code, const float* scale, const float* qs,
-                                        int32_t S, int32_t W, int32_t* cand, float* dist, int32_t* nout,
-                                        void* stream)
-{
-  return octexStageGatherReuse(rows, seg, nseg, m, lists, stride, table, table_len, n, code, scale, qs, S, W, cand,
-                               dist, nout, 0, nullptr, nullptr, nullptr, nullptr, nullptr, 0, nullptr, nullptr, stream);
-}
-
-extern "C" cuvsError_t octexStageRerankKeepMarked(int32_t* cand, const float* dist, const int32_t* nin, int32_t m,
-                                                  int32_t W, const void* vectors, int32_t D, const float* Q, int32_t R,
-                                                  int32_t KO, int64_t* si, float* sd, int32_t fresh, int32_t mark,
-                                                  int32_t* nskip, void* stream)
+extern "C" cuvsError_t octexStageRerankKeepHistory(const int32_t* cand, const float* dist, const int32_t* nin,
+                                                   int32_t m, int32_t W, const void* vectors, int32_t D, const float* Q,
+                                                   int32_t R, int32_t KO, int64_t* si, float* sd, int32_t fresh,
+                                                   int32_t* hist, int32_t H, int32_t hoff, int32_t hstore,
+                                                   int32_t* nskip, void* stream)
 {
   return run(stream, [&](hipStream_t s) {
     need(cand, "cand"), need(dist, "dist"), need(nin, "nin"), need(vectors, "vectors"), need(Q, "Q");
     need(si, "si"), need(sd, "sd");
-    OCTEX_EXPECTS(R >= 1 && R <= kMaxRerank && KO + R <= kMaxKeepSort && KO >= 1,
-                  "octex: rerank in [1, 512] and max(starts, k) + rerank <= 1024");
-    OCTEX_EXPECTS(m >= 0 && W >= 1, "octex: rerank shape");
-    // the search's two steps: the selection of the R sketch-nearest (as the gather ends it), then the exact rerank
-    dbuf sel(static_cast<size_t>(std::max(m, 1)) * R * sizeof(int32_t)), nsel(static_cast<size_t>(std::max(m, 1)) * sizeof(int32_t));
-    launch_select_rows(cand, dist, nin, m, W, R, sel.as<int>(), nsel.as<int>(), mark != 0, s);
-    launch_rerank_given(sel.as<int>(), nsel.as<int>(), m, R, static_cast<const __half*>(vectors), int64_t{1} << 31, D,
-                        Q, KO, reinterpret_cast<long long*>(si), sd, fresh != 0, nskip, s);
-    OCTEX_HIP(hipStreamSynchronize(s));
+    launch_rerank_keep(cand, dist, nin, m, W, static_cast<const __half*>(vectors), D, Q, R, KO,
+                       reinterpret_cast<long long*>(si), sd, fresh != 0, hist, H, hoff, hstore != 0, nskip, s);
   });
 }
 
-extern "C" cuvsError_t octexStageRerankGiven(const int32_t* sel, const int32_t* nsel, int32_t m, int32_t R,
-                                             const void* vectors, int64_t n, int32_t D, const float* Q, int32_t KO,
-                                             int64_t* si, float* sd, int32_t fresh, int32_t* nskip, void* stream)
-{
-  return run(stream, [&](hipStream_t s) {
-    need(sel, "sel"), need(nsel, "nsel"), need(vectors, "vectors"), need(Q, "Q"), need(si, "si"), need(sd, "sd");
-    launch_rerank_given(sel, nsel, m, R, static_cast<const __half*>(vectors), n, D, Q, KO,
-                        reinterpret_cast<long long*>(si), sd, fresh != 0, nskip, s);
-  });
-}
-
-extern "C" cuvsError_t octexStageRerankKeep(int32_t* cand, const float* dist, const int32_t* nin,
+extern "C" cuvsError_t octexStageRerankKeep(const int32_t* cand, const float* dist, const int32_t* nin,
                                             int32_t m, int32_t W, const void* vectors, int32_t D, const float* Q,
                                             int32_t R, int32_t KO, int64_t* si, float* sd, int32_t fresh,
                                             void* stream)
 {
-  return octexStageRerankKeepMarked(cand, dist, nin, m, W, vectors, D, Q, R, KO, si, sd, fresh, 0, nullptr, stream);
+  return octexStageRerankKeepHistory(cand, dist, nin, m, W, vectors, D, Q, R, KO, si, sd, fresh, nullptr, 0, 0, 0,
+                                     nullptr, stream);
 }
 
 extern "C" cuvsError_t octexStageSketchKeep(const int32_t* cand, const float* dist, const int32_t* nin,

@@ -29,18 +29,13 @@ def test_stage_bytes_cover_every_stage():
         b = bench.stage_bytes(name, 0, COUNTERS, **args)
         assert isinstance(b, int) and b > 0, name
     assert bench.stage_bytes("center", 0, COUNTERS, **args) is None
-    # gather_rows: starts + table rows + every distinct sketch row at S + 8 bytes + the query's sketch, then the
-    # selection's read of the row it wrote and its ids out
-    reranked = COUNTERS["reranked2"][0]
-    want = (10_000 * 64 * 8 + 10_000 * 64 * 64 * 4 + 10_000 * 3000 * (96 + 8) + 10_000 * (96 * 4 + 4)
-            + 10_000 * 3000 * 8 + reranked * 4)
+    # gather_rows: starts + table rows + every distinct sketch row at S + 8 bytes + the query's sketch
+    want = 10_000 * 64 * 8 + 10_000 * 64 * 64 * 4 + 10_000 * 3000 * (96 + 8) + 10_000 * (96 * 4 + 4)
     assert bench.stage_bytes("gather_rows", 0, COUNTERS, **args) == want
-    # with earlier rounds' scores: the known candidates' sketch rows are not read; the earlier rows are, 8 bytes an
-    # entry; the wave rerank reads the rows of the candidates no earlier round reranked
-    reuse = dict(COUNTERS, known2=[1000] + [0] * 15, oldread2=[2500] + [0] * 15, skipped2=[300] + [0] * 15)
-    assert bench.stage_bytes("gather_rows", 0, reuse, **args) == want - 1000 * 96 + 2500 * 8
+    # the wave rerank does not read the rows of the selected candidates an earlier round reranked
+    skip = dict(COUNTERS, skipped2=[300] + [0] * 15)
     assert (bench.stage_bytes("rerank_keep_wave", 0, COUNTERS, **args)
-            - bench.stage_bytes("rerank_keep_wave", 0, reuse, **args)) == 300 * 2 * 96
+            - bench.stage_bytes("rerank_keep_wave", 0, skip, **args)) == 300 * 2 * 96
 
 
 def test_measured_traffic_from_the_committed_profile():

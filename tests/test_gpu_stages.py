@@ -451,134 +451,119 @@ def test_row_layouts_match_oracle(L, D, S):
         dd = dev(dist)
 
 
-# ---------------------------------------------------------------- reuse of earlier rounds' rows
-
-SEEN = np.int32(-(2**31))  # bit 31 of an id: "an earlier round's exact rerank took it"
+# ---------------------------------------------------------------- the rerank's history of selected ids
 
 
-def plain(a):
-    return np.asarray(a) & np.int32(0x7FFFFFFF)
+def rerank_history(L, dix, ix, cand, dist, nin, W, Q, R, KO, si, sd, fresh, hist, H, hoff, hstore):
+    """One octexStageRerankKeepHistory call on host arrays (si, sd, hist device tensors, updated in place); the
+    per-query count of selected ids not reranked again."""
+    m = cand.shape[0]
+    nskip = torch.full((m,), -7, dtype=torch.int32, device="cuda")
+    dc, dd, dn, dQ = dev(cand), dev(dist), dev(nin), dev(Q)  # alive until the kernel has run
+    L.call("octexStageRerankKeepHistory", P(dc), P(dd), P(dn), i32(m), i32(W), P(dix["vectors"]), i32(ix.dim), P(dQ),
+           i32(R), i32(KO), P(si), P(sd), i32(fresh), P(hist) if hist is not None else None, i32(H), i32(hoff),
+           i32(hstore), P(nskip), None)
+    return host(nskip)
 
 
-def gather_reuse_gpu(L, ix, dix, seg, qs, old, W=4096, R=0):
-    """octexStageGatherReuse over table rows with the earlier rows `old` [(cand, dist, n, W)] (device tensors); with
-    R > 0 also the gather's selection of the R sketch-nearest (returned as sel, nsel)."""
-    m, nseg = seg.shape[0], seg.shape[1]
-    cand = torch.full((m, W), -5, dtype=torch.int32, device="cuda")
-    dist = torch.zeros((m, W), dtype=torch.float32, device="cuda")
-    nout = torch.zeros(m, dtype=torch.int32, device="cuda")
-    nk = torch.full((m,), -1, dtype=torch.int32, device="cuda")
-    sel = torch.full((m, max(R, 1)), -3, dtype=torch.int32, device="cuda")
-    nsel = torch.full((m,), -1, dtype=torch.int32, device="cuda")
-    dqs, dseg = dev(qs), dev(seg)
-    k = len(old)
-    oc = (ct.c_void_p * max(k, 1))(*[o[0].data_ptr() for o in old])
-    od = (ct.c_void_p * max(k, 1))(*[o[1].data_ptr() for o in old])
-    on = (ct.c_void_p * max(k, 1))(*[o[2].data_ptr() for o in old])
-    ow = (ct.c_int32 * max(k, 1))(*[o[3] for o in old])
-    L.call("octexStageGatherReuse", i32(1), P(dseg), i32(nseg), i32(m), P(dix["lists"]), i64(ix.lists.shape[1]),
-           P(dix["table"]), i32(ix.table_len), i64(ix.n), P(dix["sketch"]), P(dix["scale"]), P(dqs),
-           i32(ix.sketch_width), i32(W), P(cand), P(dist), P(nout), i32(k), oc, od, on, ow, P(nk), i32(R),
-           P(sel) if R else None, P(nsel) if R else None, None)
-    return (cand, dist, nout, nk, sel, nsel) if R else (cand, dist, nout, nk)
-
-
-def test_gather_reuses_earlier_rows(L, ix, dix):
-    """A wave gather given earlier rounds' rows: the same candidate set and bit-identical scores as the oracle's
-    gather (which scores every candidate); the candidates found in the earlier rows are counted in nknown and keep
-    those rows' rerank bits; an id in two earlier rows is taken once."""
-    g = np.random.default_rng(21)
-    m, S, W = 40, 64, 4096
-    qs = g.standard_normal((m, ix.sketch_width)).astype(np.float32)
-    starts_a = g.integers(0, ix.n, (m, S))
-    seg_a = np.stack([starts_a, np.full((m, S), ix.table_len)], -1).astype(np.int32)
-    seg_a[:, -5:] = 0
-    ca, da, na = gather_gpu(L, ix, dix, dev(seg_a), qs, rows=1, W=W)
-    # rerank bits on a third of the first row's candidates, as a marked rerank leaves them
-    marked = g.random(ca.shape) < 0.33
-    ca_m = np.where(marked & (np.arange(W)[None, :] < na[:, None]), ca | SEEN, ca).astype(np.int32)
-    # a second earlier row: other starts, partly the same
-    starts_b = np.where(g.random((m, S)) < 0.5, starts_a, g.integers(0, ix.n, (m, S)))
-    seg_b = np.stack([starts_b, np.full((m, S), ix.table_len)], -1).astype(np.int32)
-    cb, db, nb = gather_gpu(L, ix, dix, dev(seg_b), qs, rows=1, W=W)
-    # this wave: half its starts from the first row's starts
-    starts_c = np.where(g.random((m, S)) < 0.5, starts_a, g.integers(0, ix.n, (m, S)))
-    seg_c = np.stack([starts_c, np.full((m, S), ix.table_len)], -1).astype(np.int32)
-    seg_c[:, :3] = 0
-    seg_c[1] = 0  # a query without starts
-    old = [(dev(ca_m), dev(da), dev(na), W), (dev(cb), dev(db), dev(nb), W)]
-    cand, dist, nout, nk = (host(t) for t in gather_reuse_gpu(L, ix, dix, seg_c, qs, old, W=W))
-    check_gather(ix, seg_c, qs, plain(cand), dist, nout, rows=True)
-    for q in range(m):
-        n = nout[q]
-        ids = plain(cand[q, :n])
-        seen_a = {int(v) for v in ca[q, : na[q]]}
-        seen = seen_a | {int(v) for v in cb[q, : nb[q]]}
-        known = [int(v) in seen for v in ids]
-        assert nk[q] == sum(known), f"query {q}"
-        assert not any(known[: n - nk[q]]) and all(known[n - nk[q] :]), f"query {q}: known candidates come last"
-        bit_a = {int(v) for v, mk in zip(ca[q, : na[q]], marked[q, : na[q]]) if mk}
-        want_bit = np.array([int(v) in bit_a for v in ids])
-        assert np.array_equal(cand[q, :n] < 0, want_bit), f"query {q}: rerank bits"
-    assert nout[1] == 0 and nk[1] == 0
-    assert nk.sum() > 0.2 * nout.sum()  # half the starts repeat: many candidates come from the earlier rows
-
-
-def test_marked_rerank_rounds_match_oracle(L, ix, dix, small_index):
-    """Two rounds of the fused rerank as a search runs them: the first (fresh) marks what it selects; the second, over
-    candidate rows that hold some of those marked ids with the same sketch scores (a query's scores do not change),
-    skips them and still gives the oracle's kept list exactly (the oracle reranks everything)."""
+def test_rerank_history_rounds_match_oracle(L, ix, dix, small_index):
+    """The rounds of the fused rerank as a search runs them (a first round of R1, three waves of R2): each round but
+    the last stores its selected ids in the history, and each later round skips the selected ids found there.  The
+    kept lists equal the oracle's rerank_keep (which reranks every selected id) after every round; the history holds
+    each round's selection (-1 padded); the skip counts are the selected ids an earlier round selected."""
     g = np.random.default_rng(22)
-    m, W, KO, R = 32, 4096, 64, 96
+    m, W, KO, R1, R2, waves = 32, 4096, 64, 96, 64, 3
+    H = R1 + R2 * (waves - 1)
     Q = small_index["Q"][:m]
     score = g.uniform(0, 100, ix.n).astype(np.float32)  # one sketch score per id, as within one query's search
-    n1 = g.integers(200, 2000, m).astype(np.int32)
-    n1[0] = 50  # fewer candidates than R: all selected
-    c1 = np.full((m, W), -9, np.int32)
-    d1 = np.zeros((m, W), np.float32)
+    si = torch.full((m, KO), -3, dtype=torch.int64, device="cuda")  # stale contents: the first round is fresh
+    sd = torch.full((m, KO), -1.0, dtype=torch.float32, device="cuda")
+    hist = torch.full((m, H), -5, dtype=torch.int32, device="cuda")
+    si_h = np.full((m, KO), -1, np.int64)
+    sd_h = np.full((m, KO), np.inf, np.float32)
+    earlier = [set() for _ in range(m)]  # ids selected by earlier rounds, per query
+    skipped, before = 0, None
+    for rnd in range(waves + 1):
+        R = R1 if rnd == 0 else R2
+        hoff = 0 if rnd == 0 else R1 + (rnd - 1) * R2
+        store = rnd < waves
+        nin = g.integers(200, 2000, m).astype(np.int32)
+        nin[0] = 40 + rnd  # fewer candidates than R: all selected
+        nin[1] = 0 if rnd == 2 else nin[1]  # a round without candidates
+        cand = np.full((m, W), -9, np.int32)
+        dist = np.zeros((m, W), np.float32)
+        for q in range(m):
+            old = np.array(sorted(earlier[q]), np.int64)
+            k_old = min(len(old), nin[q] // 3)
+            pick = g.choice(old, k_old, replace=False) if k_old else np.zeros(0, np.int64)
+            others = g.permutation(np.setdiff1d(np.arange(ix.n), old))[: nin[q] - k_old]
+            row = np.concatenate([pick, others])[g.permutation(nin[q])].astype(np.int32)
+            cand[q, : nin[q]] = row
+            dist[q, : nin[q]] = score[row]
+        sk = rerank_history(L, dix, ix, cand, dist, nin, W, Q, R, KO, si, sd, rnd == 0, hist, H, hoff, store)
+        gsi, gsd, gh = host(si), host(sd), host(hist)
+        for q in range(m):
+            n = nin[q]
+            ri, rd = O.rerank_keep(ix, cand[q, :n], dist[q, :n], Q[q], R, si_h[q], sd_h[q], rnd == 0)
+            assert np.array_equal(gsi[q], ri) and np.array_equal(gsd[q], rd), f"round {rnd} query {q}"
+            si_h[q], sd_h[q] = ri, rd
+            sel, _ = O.select(cand[q, :n], dist[q, :n], R)
+            sel = {int(v) for v in sel}
+            want_skip = 0 if rnd == 0 else len(sel & earlier[q])
+            assert sk[q] == want_skip, f"round {rnd} query {q}: skipped reranks"
+            skipped += want_skip
+            if store:
+                row = gh[q, hoff : hoff + R]
+                assert {int(v) for v in row[row >= 0]} == sel and (row < 0).sum() == R - len(sel), f"round {rnd} {q}"
+                assert np.all(row[: len(sel)] >= 0), f"round {rnd} query {q}: selected ids first"
+            earlier[q] |= sel
+        if not store:  # the last round leaves the history as it was
+            assert np.array_equal(gh, before)
+        before = gh
+    assert skipped > 0
+
+
+def test_rerank_history_uses_its_last_256_entries(L, ix, dix, small_index):
+    """Only the ids of the history's last 256 entries are skipped: ids stored before them are reranked again.  Here the
+    history's early entries name ids never merged (skipping them would lose them from the kept list, which then
+    differs from the oracle's) and its last 256 entries ids that were merged."""
+    g = np.random.default_rng(25)
+    m, W, KO, R, H, hoff = 16, 4096, 64, 512, 1024, 1000
+    Q = small_index["Q"][:m]
+    score = g.uniform(0, 100, ix.n).astype(np.float32)
+    si = torch.full((m, KO), -1, dtype=torch.int64, device="cuda")
+    sd = torch.full((m, KO), float("inf"), dtype=torch.float32, device="cuda")
+    si_h = np.full((m, KO), -1, np.int64)
+    sd_h = np.full((m, KO), np.inf, np.float32)
+    A = [g.choice(ix.n, 200, replace=False).astype(np.int32) for _ in range(m)]
+    cand = np.full((m, W), -9, np.int32)
+    dist = np.zeros((m, W), np.float32)
+    nin = np.full(m, 200, np.int32)
     for q in range(m):
-        c1[q, : n1[q]] = g.choice(ix.n, n1[q], replace=False)
-        d1[q, : n1[q]] = score[c1[q, : n1[q]]]
-    si = np.full((m, KO), -1, np.int64)
-    sd = np.full((m, KO), np.inf, np.float32)
-    dc1, dd1, dn1, dQ, dsi, dsd = dev(c1), dev(d1), dev(n1), dev(Q), dev(si), dev(sd)
-    nskip = torch.full((m,), -1, dtype=torch.int32, device="cuda")
-    L.call("octexStageRerankKeepMarked", P(dc1), P(dd1), P(dn1), i32(m), i32(W), P(dix["vectors"]), i32(ix.dim),
-           P(dQ), i32(R), i32(KO), P(dsi), P(dsd), i32(1), i32(1), P(nskip), None)
-    gc1 = host(dc1)
+        cand[q, :200], dist[q, :200] = A[q], score[A[q]]
+    assert rerank_history(L, dix, ix, cand, dist, nin, W, Q, R, KO, si, sd, True, None, 0, 0, False).sum() == 0
+    hist = np.full((m, H), -1, np.int32)
+    B = []
     for q in range(m):
-        sel, _ = O.select(c1[q, : n1[q]], d1[q, : n1[q]], R)
-        ri, rd = O.rerank_keep(ix, c1[q, : n1[q]], d1[q, : n1[q]], Q[q], R, si[q], sd[q], True)
-        assert np.array_equal(host(dsi)[q], ri) and np.array_equal(host(dsd)[q], rd), f"query {q}"
-        si[q], sd[q] = ri, rd
-        got = {int(v) for v in plain(gc1[q, : n1[q]][gc1[q, : n1[q]] < 0])}
-        assert got == {int(v) for v in sel}, f"query {q}: marked ids"
-        assert np.array_equal(plain(gc1[q, : n1[q]]), c1[q, : n1[q]])
-    # the second round: about half of each row from the first round's candidates (with their marks), half new
-    n2 = g.integers(300, 2500, m).astype(np.int32)
-    c2 = np.full((m, W), -9, np.int32)
-    d2 = np.zeros((m, W), np.float32)
+        ri, rd = O.rerank_keep(ix, cand[q, :200], dist[q, :200], Q[q], R, si_h[q], sd_h[q], True)
+        si_h[q], sd_h[q] = ri, rd
+        b = np.setdiff1d(g.choice(ix.n, 900, replace=False), A[q])[:400].astype(np.int32)
+        B.append(b)
+        hist[q, : len(b)] = b  # outside the window: never merged
+        hist[q, hoff - 256 : hoff - 256 + 200] = A[q]  # inside the window: merged above
+        hist[q, hoff - 257] = b[0]  # just outside the window
+    dh = dev(hist)
+    nin = np.full(m, 600, np.int32)
     for q in range(m):
-        old = gc1[q, : n1[q]]
-        k_old = min(len(old), n2[q] // 2)
-        pick = old[g.choice(len(old), k_old, replace=False)]
-        fresh_ids = np.setdiff1d(np.arange(ix.n), plain(old))
-        new = g.choice(fresh_ids, n2[q] - k_old, replace=False).astype(np.int32)
-        row = np.concatenate([pick, new])[g.permutation(n2[q])]
-        c2[q, : n2[q]] = row
-        d2[q, : n2[q]] = score[plain(row)]
-    dc2, dd2, dn2 = dev(c2), dev(d2), dev(n2)
-    L.call("octexStageRerankKeepMarked", P(dc2), P(dd2), P(dn2), i32(m), i32(W), P(dix["vectors"]), i32(ix.dim),
-           P(dQ), i32(R), i32(KO), P(dsi), P(dsd), i32(0), i32(1), P(nskip), None)
-    sk = host(nskip)
+        row = np.concatenate([A[q], B[q]])[g.permutation(600)]
+        cand[q, :600], dist[q, :600] = row, score[row]
+    sk = rerank_history(L, dix, ix, cand, dist, nin, W, Q, R, KO, si, sd, False, dh, H, hoff, False)
     for q in range(m):
-        ids = plain(c2[q, : n2[q]])
-        ri, rd = O.rerank_keep(ix, ids, d2[q, : n2[q]], Q[q], R, si[q], sd[q], False)
-        assert np.array_equal(host(dsi)[q], ri) and np.array_equal(host(dsd)[q], rd), f"query {q}"
-        sel, _ = O.select(ids, d2[q, : n2[q]], R)
-        was = {int(v) for v in plain(gc1[q, : n1[q]][gc1[q, : n1[q]] < 0])}
-        assert sk[q] == sum(int(v) in was for v in sel), f"query {q}: skipped reranks"
-    assert sk.sum() > 0
+        ri, rd = O.rerank_keep(ix, cand[q, :600], dist[q, :600], Q[q], R, si_h[q], sd_h[q], False)
+        assert np.array_equal(host(si)[q], ri) and np.array_equal(host(sd)[q], rd), f"query {q}"
+        sel, _ = O.select(cand[q, :600], dist[q, :600], R)
+        assert sk[q] == len({int(v) for v in sel} & {int(v) for v in A[q]}), f"query {q}"
+    assert np.array_equal(host(dh), hist)  # not stored: the history is unchanged
 
 
 @pytest.mark.parametrize("kind", ["equal", "few"])
@@ -621,54 +606,3 @@ def test_selection_of_many_equal_keys_at_the_largest_width(L, ix, dix, small_ind
     for q in range(m):
         ri, rd = O.rerank_keep(ix, cand[q, : nin[q]], dist[q, : nin[q]], Q[q], R, si[q], sd[q], True)
         assert np.array_equal(host(dsi)[q], ri) and np.array_equal(host(dsd)[q], rd), f"rerank_keep query {q}"
-
-
-def test_gather_selection_and_given_rerank_match_oracle(L, ix, dix, small_index):
-    """The search's fused path: a wave gather (reusing an earlier row) that selects its R sketch-nearest as it ends,
-    then the exact rerank of those ids.  The selection is the oracle's (the R smallest by (distance, id)), each
-    selected entry of the row is marked, sel keeps the earlier rounds' rerank bits, and the kept lists equal the
-    oracle's rerank_keep on the same rows, first fresh, then merged into that kept list with the marked ids skipped."""
-    g = np.random.default_rng(24)
-    m, S, W, KO, R = 32, 64, 4096, 64, 96
-    Q = small_index["Q"][:m]
-    qs = g.standard_normal((m, ix.sketch_width)).astype(np.float32)
-    starts_a = g.integers(0, ix.n, (m, S))
-    seg_a = np.stack([starts_a, np.full((m, S), ix.table_len)], -1).astype(np.int32)
-    ca, da, na, _, sa, nsa = gather_reuse_gpu(L, ix, dix, seg_a, qs, [], W=W, R=R)
-    si = torch.full((m, KO), -1, dtype=torch.int64, device="cuda")
-    sd = torch.full((m, KO), float("inf"), dtype=torch.float32, device="cuda")
-    dQ = dev(Q)
-    L.call("octexStageRerankGiven", P(sa), P(nsa), i32(m), i32(R), P(dix["vectors"]), i64(ix.n), i32(ix.dim), P(dQ),
-           i32(KO), P(si), P(sd), i32(1), None, None)
-    hca, hda, hna, hsa, hnsa = host(ca), host(da), host(na), host(sa), host(nsa)
-    si_h = np.full((m, KO), -1, np.int64)
-    sd_h = np.full((m, KO), np.inf, np.float32)
-    for q in range(m):
-        n = hna[q]
-        ids = plain(hca[q, :n])
-        want, _ = O.select(ids, hda[q, :n], R)
-        assert hnsa[q] == len(want) and set(plain(hsa[q, : hnsa[q]]).tolist()) == set(want.tolist()), f"query {q}"
-        assert set(ids[hca[q, :n] < 0].tolist()) == set(want.tolist()), f"query {q}: marked entries"
-        ri, rd = O.rerank_keep(ix, ids, hda[q, :n], Q[q], R, si_h[q], sd_h[q], True)
-        assert np.array_equal(host(si)[q], ri) and np.array_equal(host(sd)[q], rd), f"query {q}"
-        si_h[q], sd_h[q] = ri, rd
-    # the next wave, half its starts shared: reuses the marked row, selects, reranks without the marked ids
-    starts_b = np.where(g.random((m, S)) < 0.5, starts_a, g.integers(0, ix.n, (m, S)))
-    seg_b = np.stack([starts_b, np.full((m, S), ix.table_len)], -1).astype(np.int32)
-    cb, db, nb, nkb, sb, nsb = gather_reuse_gpu(L, ix, dix, seg_b, qs, [(ca, da, na, W)], W=W, R=R)
-    nskip = torch.full((m,), -1, dtype=torch.int32, device="cuda")
-    L.call("octexStageRerankGiven", P(sb), P(nsb), i32(m), i32(R), P(dix["vectors"]), i64(ix.n), i32(ix.dim), P(dQ),
-           i32(KO), P(si), P(sd), i32(0), P(nskip), None)
-    hcb, hdb, hnb, hsb, hnsb, hsk = host(cb), host(db), host(nb), host(sb), host(nsb), host(nskip)
-    for q in range(m):
-        n = hnb[q]
-        ids = plain(hcb[q, :n])
-        want, _ = O.select(ids, hdb[q, :n], R)
-        got = hsb[q, : hnsb[q]]
-        assert set(plain(got).tolist()) == set(want.tolist()), f"query {q}"
-        was = {int(v) for v in plain(hca[q, : hna[q]][hca[q, : hna[q]] < 0])}  # marked by the first selection
-        assert {int(v) for v in plain(got[got < 0])} == {int(v) for v in want if int(v) in was}, f"query {q}: bits"
-        assert hsk[q] == int((got < 0).sum()), f"query {q}: skipped"
-        ri, rd = O.rerank_keep(ix, ids, hdb[q, :n], Q[q], R, si_h[q], sd_h[q], False)
-        assert np.array_equal(host(si)[q], ri) and np.array_equal(host(sd)[q], rd), f"query {q}"
-    assert hsk.sum() > 0 and host(nkb).sum() > 0
