@@ -140,6 +140,12 @@ cuvsError_t octexStageProbe(const void* Y, int32_t m, int32_t C, int32_t L, int3
                             const int32_t* off, int64_t T1, const int64_t* keys, int64_t Mmax,
                             const int32_t* base, int32_t l, int32_t lr, int32_t logT, int32_t* seg,
                             void* stream);
+/** octexStageProbe reading the buckets from bucket lines (first key and key range of every bucket, 16 bytes) built
+ * from off and keys, as the search does when they fit in HBM; the same segments. */
+cuvsError_t octexStageProbeLines(const void* Y, int32_t m, int32_t C, int32_t L, int32_t B, const float* inv_f,
+                                 const int32_t* off, int64_t T1, const int64_t* keys, int64_t Mmax,
+                                 const int32_t* base, int32_t l, int32_t lr, int32_t logT, int32_t* seg,
+                                 void* stream);
 /** gather_kernel (search_kernels.cuh:138-253): rows = 0 lists, 1 table rows; W a power of two; ids at or
  * above n are skipped like the -1 padding. */
 cuvsError_t octexStageGather(int32_t rows, const int32_t* seg, int32_t nseg, int32_t m, const int32_t* lists,

@@ -933,6 +933,10 @@ auto build_in_memory(index_params const& params, dataset_view const& x, build_re
   upload(ix.scale.ptr, rec.scale.data(), ix.scale.size, s);
   phase("sketch");
 
+  // the probe's bucket lines, before the table phase's searches, keeping room for the table and the searches
+  make_bucket_lines(ix, kSearchReserve + (k > 0 ? static_cast<size_t>(n) * k * sizeof(int32_t) : 0));
+  build_log("bucket lines: %s\n", ix.lines.ptr != nullptr ? "in HBM" : "left out (memory)");
+
   if (before_table) before_table(impl);  // a hook that outlives this call (a writer thread) keeps its own reference
 
   // neighbor table: exact up to exact_table_max rows (build.cu:354-360), else searched by this library's search

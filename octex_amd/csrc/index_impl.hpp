@@ -6,6 +6,8 @@
 //                                   allocation per copy; list_ptr i64 [C] holds each copy's address
 //   keys     i64 [C, L, mmax]       cell ids per (copy, level) in (bucket, id) order
 //   offsets  i32 [C, L, 2^logT + 1] CSR of the buckets into keys
+//   lines    16 B [C, L, 2^logT]   the probe's bucket lines: first key and key range of every bucket
+//                                   (make_bucket_lines; absent when the device lacks the memory)
 //   base     i32 [C, L]             first cell row of every level
 //   ucatT    f16 [C * 8b, D]        projections of all copies, one row per projected coordinate
 //                                   (the transpose of the reference's ucat [D, C * 8b]) so that the
@@ -76,6 +78,7 @@ struct index_impl {
   dbuf list_ptr;                  // i64 [C]: device address of every copy's lists
   std::vector<int64_t> list_rows; // cell rows of every copy (builder)
   dbuf keys, offsets, base, ucatT, shift, inv_f, mean, basis, scale;
+  dbuf lines;  // bucket_line [C, L, T1 - 1], or empty
   dbuf sketch, vectors, table;
   hbuf host_sketch, host_vectors, host_table;
   int64_t stride = 0, mmax = 0, T1 = 0;
@@ -108,5 +111,13 @@ struct index_impl {
   index_impl(index_impl const&) = delete;
   ~index_impl();
 };
+
+/**
+ * The probe's bucket lines of a loaded or built index (keys and offsets in HBM), when the device keeps keep_free
+ * bytes free beside them; without them the probe reads the offsets.  OCTEX_PROBE_LINES=0 leaves them out.
+ */
+void make_bucket_lines(index_impl& ix, size_t keep_free);
+/** Device memory left free for the search's batch buffers when the bucket lines are added. */
+constexpr size_t kSearchReserve = size_t{8} << 30;
 
 }  // namespace cuvs::neighbors::octex::detail

@@ -264,18 +264,40 @@ __device__ __forceinline__ long long probe_cell_id(const uint4 (&yv)[B], float i
 }
 
 /**
+ * The bucket lines of the CSR offsets off [CL, T1] into keys [CL, Mmax] (one thread a bucket): the first key and the
+ * range of every bucket.  The loader has checked that the offsets of a level rise to at most its cell count.
+ */
+__global__ __launch_bounds__(256) void bucket_lines_kernel(const int* __restrict__ off, int64_t T1,
+                                                           const long long* __restrict__ keys, int64_t Mmax,
+                                                           int64_t total, bucket_line* __restrict__ lines)
+{
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int64_t T = T1 - 1, cl = i / T, b = i - cl * T;
+  const int* o    = off + cl * T1 + b;
+  bucket_line e;
+  e.p0   = o[0];
+  e.p1   = o[1];
+  e.key0 = e.p1 > e.p0 ? keys[cl * Mmax + e.p0] : 0;
+  lines[i] = e;
+}
+
+/**
  * Levels fine to coarse for every (query, copy) item, stopping at the first level whose bucket holds
  * the cell id (search_kernels.cuh:84-127).  A wavefront owns `chunk` consecutive items (item t: copy
  * t / m, query t % m, so a wavefront's lookups stay in one copy's tables); each lane holds one item and
  * its next level, and runs one level per step: the cell id of y * inv_f[level], the bucket's bounds,
- * its keys four loads at a time.  A lane whose item is decided (a hit: seg = ((base + p) * l, lr); no
- * level left: (0, 0)) takes the wavefront's next item, so lanes stay busy until the chunk runs out
- * instead of every item paying for all L levels.  The loop ends for the whole wavefront together.
+ * its keys four loads at a time.  With kLines the bucket's line (its first key and bounds, one 16-byte load)
+ * replaces the bounds, and the keys are read only past a first key that is not the cell's.  A lane whose item is
+ * decided (a hit: seg = ((base + p) * l, lr); no level left: (0, 0)) takes the wavefront's next item, so lanes stay
+ * busy until the chunk runs out instead of every item paying for all L levels.  The loop ends for the whole
+ * wavefront together.
  */
-template <int B>
+template <int B, bool kLines>
 __global__ __launch_bounds__(256) void probe_kernel(const __half* __restrict__ Y, int m, int C,
                                                     int L, const float* __restrict__ inv_f,
-                                                    const int* __restrict__ off, int64_t T1,
+                                                    const int* __restrict__ off,
+                                                    const bucket_line* __restrict__ lines, int64_t T1,
                                                     const long long* __restrict__ keys,
                                                     int64_t Mmax, const int* __restrict__ base,
                                                     int l, int lr, int logT, int64_t chunk,
@@ -313,10 +335,18 @@ __global__ __launch_bounds__(256) void probe_kernel(const __half* __restrict__ Y
     if (item >= 0) {
       const long long h   = probe_cell_id<B>(yv, inv_f[lvl]);
       const int bk        = static_cast<int>(h & ((1LL << logT) - 1));
-      const int* o        = off + (static_cast<int64_t>(c) * L + lvl) * T1 + bk;
       const long long* kk = keys + (static_cast<int64_t>(c) * L + lvl) * Mmax;
-      const int p0 = o[0], p1 = o[1];
-      int hit      = -1;
+      int p0 = 0, p1 = 0, hit = -1;
+      if constexpr (kLines) {
+        const bucket_line e = lines[(static_cast<int64_t>(c) * L + lvl) * (T1 - 1) + bk];
+        p1                  = e.p1;
+        if (e.p1 > e.p0 && e.key0 == h) hit = e.p0;
+        p0 = e.p0 + 1;  // the first key is checked
+      } else {
+        const int* o = off + (static_cast<int64_t>(c) * L + lvl) * T1 + bk;
+        p0           = o[0];
+        p1           = o[1];
+      }
       for (int p = p0; p < p1 && hit < 0; p += 4) {  // keys of the bucket, four loads in flight
         long long k4[4];
 #pragma unroll
@@ -1833,9 +1863,19 @@ void launch_e8(const float* y, int64_t n, int b, float inv_f, float* p, long lon
   OCTEX_HIP(hipGetLastError());
 }
 
+void launch_bucket_lines(const int* off, int64_t T1, const long long* keys, int64_t Mmax, int64_t CL,
+                         bucket_line* lines, hipStream_t s)
+{
+  OCTEX_EXPECTS(T1 >= 2 && CL >= 0, "octex: bucket lines of offsets rows of at least 2 entries");
+  const int64_t total = CL * (T1 - 1);
+  if (total == 0) return;
+  bucket_lines_kernel<<<grid_for(total, 256), 256, 0, s>>>(off, T1, keys, Mmax, total, lines);
+  OCTEX_HIP(hipGetLastError());
+}
+
 void launch_probe(const __half* Y, int m, int C, int L, int B, const float* inv_f, const int* off,
-                  int64_t T1, const long long* keys, int64_t Mmax, const int* base, int l, int lr,
-                  int logT, int2* seg, hipStream_t s)
+                  const bucket_line* lines, int64_t T1, const long long* keys, int64_t Mmax, const int* base, int l,
+                  int lr, int logT, int2* seg, hipStream_t s)
 {
   const int64_t tot = static_cast<int64_t>(m) * C;
   if (tot == 0) return;
@@ -1853,8 +1893,11 @@ void launch_probe(const __half* Y, int m, int C, int L, int B, const float* inv_
   const int64_t chunk = std::max<int64_t>(64, (tot + int64_t{24} * cus - 1) / (int64_t{24} * cus));
   const int64_t waves = (tot + chunk - 1) / chunk;
   auto g              = grid_for(waves * 64, 256);
-#define OCTEX_PROBE(b) \
-  probe_kernel<b><<<g, 256, 0, s>>>(Y, m, C, L, inv_f, off, T1, keys, Mmax, base, l, lr, logT, chunk, seg)
+#define OCTEX_PROBE(b)                                                                                          \
+  (lines != nullptr ? probe_kernel<b, true><<<g, 256, 0, s>>>(Y, m, C, L, inv_f, off, lines, T1, keys, Mmax, base, \
+                                                              l, lr, logT, chunk, seg)                             \
+                    : probe_kernel<b, false><<<g, 256, 0, s>>>(Y, m, C, L, inv_f, off, lines, T1, keys, Mmax,      \
+                                                               base, l, lr, logT, chunk, seg))
   switch (B) {
     case 1: OCTEX_PROBE(1); break;
     case 2: OCTEX_PROBE(2); break;

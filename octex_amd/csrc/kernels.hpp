@@ -44,9 +44,26 @@ void launch_sketch_query(const float* qc, const float* basis, int m, int D, int 
                          hipStream_t s);
 /** E8^b points and hashes of y [n, 8b] * inv_f (the E8 decode of the probe, for tests). */
 void launch_e8(const float* y, int64_t n, int b, float inv_f, float* p, long long* h, hipStream_t s);
+/**
+ * One bucket of a (copy, level) cell table as the probe reads it: its first key and the range [p0, p1) of its keys in
+ * the level's keys (the CSR offsets off[b], off[b + 1]).  A level's probe is then one 16-byte load, and a second read
+ * of the keys only when the bucket holds more than one key and the first is not the cell's.
+ */
+struct alignas(16) bucket_line {
+  long long key0;  // keys[p0] when p1 > p0
+  int p0, p1;
+};
+/** lines [CL, T1 - 1] of the CSR offsets off [CL, T1] into keys [CL, Mmax]. */
+void launch_bucket_lines(const int* off, int64_t T1, const long long* keys, int64_t Mmax, int64_t CL,
+                         bucket_line* lines, hipStream_t s);
+/**
+ * Segments seg [m, C] of every (query, copy): the finest level whose bucket (h & (T1 - 2), T1 - 1 = 2^logT) holds the
+ * cell id h of the query's E8 point, as (first list row, lr), or (0, 0) (search_kernels.cuh:84-127).  With lines (may
+ * be null) the buckets are read from them, else from off.
+ */
 void launch_probe(const __half* Y, int m, int C, int L, int B, const float* inv_f, const int* off,
-                  int64_t T1, const long long* keys, int64_t Mmax, const int* base, int l, int lr,
-                  int logT, int2* seg, hipStream_t s);
+                  const bucket_line* lines, int64_t T1, const long long* keys, int64_t Mmax, const int* base, int l,
+                  int lr, int logT, int2* seg, hipStream_t s);
 /** LDS bytes of a gather over `nseg` segments per query with hash sets up to W slots; lds_slots: with the
  * candidates' 16-bit slot list in LDS too (else it is kept in the query's row of cand). */
 auto gather_smem(int W, int S, int nseg, int max_len, bool lds_slots) -> size_t;

@@ -5,6 +5,7 @@
 #include "common.hpp"
 #include "directory.hpp"
 #include "index_impl.hpp"
+#include "kernels.hpp"
 #include "meta.hpp"
 #include "npy.hpp"
 
@@ -82,6 +83,22 @@ auto to_pinned(npy_file const& f, size_t bytes) -> hbuf
 }  // namespace
 
 namespace detail {
+
+void make_bucket_lines(index_impl& ix, size_t keep_free)
+{
+  if (const char* e = std::getenv("OCTEX_PROBE_LINES"); e != nullptr && std::string(e) == "0") return;
+  const int64_t CL = static_cast<int64_t>(ix.offsets.size / sizeof(int32_t)) / std::max<int64_t>(ix.T1, 1);
+  if (CL == 0 || ix.T1 < 2 || ix.keys.ptr == nullptr) return;
+  const size_t bytes = static_cast<size_t>(CL) * static_cast<size_t>(ix.T1 - 1) * sizeof(bucket_line);
+  size_t fr = 0, tot = 0;
+  OCTEX_HIP(hipMemGetInfo(&fr, &tot));
+  if (fr < bytes + keep_free) return;  // the probe reads the offsets
+  ix.lines = dbuf(bytes);
+  ix.bytes += static_cast<int64_t>(bytes);
+  launch_bucket_lines(ix.offsets.as<int32_t>(), ix.T1, ix.keys.as<long long>(), ix.mmax, CL,
+                      ix.lines.as<bucket_line>(), ix.stream);
+  OCTEX_HIP(hipStreamSynchronize(ix.stream));
+}
 
 auto open_directory(std::string const& path, load_params const& params) -> directory
 {
@@ -376,6 +393,7 @@ auto load_opened(detail::directory const& dir, std::string const& path, load_par
       ix.table = upload(ix, table->as<int32_t>(), tb);
   }
   OCTEX_HIP(hipStreamSynchronize(ix.stream));
+  detail::make_bucket_lines(ix, detail::kSearchReserve);
   ix.list_len = ll;
   OCTEX_HIP(hipSetDevice(cur));
   return impl;

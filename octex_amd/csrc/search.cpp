@@ -182,8 +182,9 @@ auto batch_stages(index_impl const& ix, plan_shape const& sh, batch_buffers cons
   });
   add("sketch_query", [&ix, b, s, m, D, S] { launch_sketch_query(b.qc, ix.basis.as<float>(), m, D, S, b.qs, s); });
   add("probe", [&ix, b, sh, s, m, C] {
-    launch_probe(b.Y, m, C, ix.levels(), ix.blocks, ix.inv_f.as<float>(), ix.offsets.as<int>(), ix.T1,
-                 ix.keys.as<long long>(), ix.mmax, ix.base.as<int>(), ix.list_len, sh.lr, ix.log_buckets, b.seg, s);
+    launch_probe(b.Y, m, C, ix.levels(), ix.blocks, ix.inv_f.as<float>(), ix.offsets.as<int>(),
+                 ix.lines.as<bucket_line>(), ix.T1, ix.keys.as<long long>(), ix.mmax, ix.base.as<int>(), ix.list_len,
+                 sh.lr, ix.log_buckets, b.seg, s);
   });
   // stage names as profiled: the ablation paths are marked, so a profile shows which kernels ran
   const std::string whole = balanced ? "" : "_whole", unfused = fused ? "" : "_unfused";

@@ -86,9 +86,29 @@ extern "C" cuvsError_t octexStageProbe(const void* Y, int32_t m, int32_t C, int3
     need(Y, "Y"), need(inv_f, "inv_f"), need(off, "offsets"), need(keys, "keys"), need(base, "base");
     need(seg, "seg");
     OCTEX_EXPECTS(m >= 0 && C >= 1 && L >= 1 && logT >= 1 && logT <= 30, "octex: probe shape");
-    launch_probe(static_cast<const __half*>(Y), m, C, L, B, inv_f, off, T1,
+    launch_probe(static_cast<const __half*>(Y), m, C, L, B, inv_f, off, nullptr, T1,
                  reinterpret_cast<const long long*>(keys), Mmax, base, l, lr, logT, reinterpret_cast<int2*>(seg),
                  s);
+  });
+}
+
+extern "C" cuvsError_t octexStageProbeLines(const void* Y, int32_t m, int32_t C, int32_t L, int32_t B,
+                                            const float* inv_f, const int32_t* off, int64_t T1, const int64_t* keys,
+                                            int64_t Mmax, const int32_t* base, int32_t l, int32_t lr, int32_t logT,
+                                            int32_t* seg, void* stream)
+{
+  return run(stream, [&](hipStream_t s) {
+    need(Y, "Y"), need(inv_f, "inv_f"), need(off, "offsets"), need(keys, "keys"), need(base, "base");
+    need(seg, "seg");
+    OCTEX_EXPECTS(m >= 0 && C >= 1 && L >= 1 && logT >= 1 && logT <= 30 && T1 == (int64_t{1} << logT) + 1,
+                  "octex: probe shape");
+    dbuf lines(static_cast<size_t>(C) * L * (T1 - 1) * sizeof(bucket_line));
+    launch_bucket_lines(off, T1, reinterpret_cast<const long long*>(keys), Mmax, int64_t{C} * L,
+                        lines.as<bucket_line>(), s);
+    launch_probe(static_cast<const __half*>(Y), m, C, L, B, inv_f, off, lines.as<bucket_line>(), T1,
+                 reinterpret_cast<const long long*>(keys), Mmax, base, l, lr, logT, reinterpret_cast<int2*>(seg),
+                 s);
+    OCTEX_HIP(hipStreamSynchronize(s));  // before the lines are freed
   });
 }
 

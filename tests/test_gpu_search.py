@@ -264,6 +264,24 @@ def test_load_limits_match_oracle(octex, small_index):
     assert_same_results(D, I, Do, Io)
 
 
+def test_probe_without_bucket_lines(octex, small_index, monkeypatch):
+    """The search's probe reads each bucket's line (first key and key range) when the index has its bucket lines,
+    the offsets and keys otherwise (OCTEX_PROBE_LINES=0 at load): the same segments and results, and the lines are
+    C L 2^log_buckets 16-byte entries of device memory."""
+    oix = O.Index(small_index["path"])
+    Q = small_index["Q"][:60]
+    a = octex.load(small_index["path"])
+    Da, Ia = a.search(Q, k=10, **PARAMS)
+    seg_a = a.plan_buffer("seg", np.int32)[: len(Q) * oix.copies * 2].copy()
+    monkeypatch.setenv("OCTEX_PROBE_LINES", "0")
+    b = octex.load(small_index["path"])
+    Db, Ib = b.search(Q, k=10, **PARAMS)
+    seg_b = b.plan_buffer("seg", np.int32)[: len(Q) * oix.copies * 2]
+    assert np.array_equal(seg_a, seg_b) and np.array_equal(Ia, Ib) and np.array_equal(Da, Db)
+    lines = oix.copies * len(oix.spacings) * 2**oix.log_buckets * 16
+    assert a.device_bytes[0] - b.device_bytes[0] == lines
+
+
 def test_placements_on_host(octex, small_index):
     """Vectors, table and sketch in pinned host memory give the same results."""
     Q = small_index["Q"][:40]

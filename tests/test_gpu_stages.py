@@ -163,11 +163,14 @@ def queries_Y(ix, X, extra_random=64, seed=0):
     return np.concatenate([Y, R])
 
 
-def run_probe(L, ix, dix, Y, lr):
+PROBES = ["octexStageProbe", "octexStageProbeLines"]  # buckets read from the offsets, or from bucket lines
+
+
+def run_probe(L, ix, dix, Y, lr, stage="octexStageProbe"):
     m, C = Y.shape[0], ix.copies
     seg = torch.empty((m, C, 2), dtype=torch.int32, device="cuda")
     dY = dev(Y.view(np.int16))
-    L.call("octexStageProbe", P(dY), i32(m), i32(C), i32(len(ix.spacings)), i32(ix.blocks),
+    L.call(stage, P(dY), i32(m), i32(C), i32(len(ix.spacings)), i32(ix.blocks),
            P(dix["inv_f"]), P(dix["offsets"]), i64(ix.offsets.shape[2]), P(dix["keys"]), i64(ix.keys.shape[2]),
            P(dix["base"]), i32(ix.list_len), i32(lr), i32(ix.log_buckets), P(seg), None)
     return seg
@@ -178,22 +181,24 @@ def run_probe(L, ix, dix, Y, lr):
     dict(m=60, C=5, spacing=(0.5, 1.0, 2.0, 4.0, 8.0), logT=3, l=16, lr=9, seed=3, absent=(5, 6, 17)),
     dict(m=300, C=7, spacing=(1.0, 2.0, 4.0), b=2, logT=5, l=8, lr=8, seed=4, absent=tuple(range(0, 300, 13))),
 ])
-def test_probe_construction_matches_reference(L, case):
+@pytest.mark.parametrize("stage", PROBES)
+def test_probe_construction_matches_reference(L, case, stage):
     """The probe over hand-built cell tables: exactly (row * l, lr) at the finest level holding each query's
     cell, (0, 0) when none does; the oracle gives the same segments."""
     arrays, Y, want = probe_construction(**case)
     pix = O.Index.from_arrays(**arrays)
     pdix = dict(inv_f=dev(pix.inv_f), offsets=dev(pix.offsets), keys=dev(pix.keys), base=dev(pix.base))
     lr = int(want[:, :, 1].max())
-    seg = host(run_probe(L, pix, pdix, Y, lr))
+    seg = host(run_probe(L, pix, pdix, Y, lr, stage))
     check_probe(seg, want)
     check_probe(O.probe(pix, Y, read=lr), want)
 
 
-def test_probe_matches_oracle(L, ix, dix, small_index):
+@pytest.mark.parametrize("stage", PROBES)
+def test_probe_matches_oracle(L, ix, dix, small_index, stage):
     Y = queries_Y(ix, small_index["X"][:200])
     for lr in (ix.list_len, 5):
-        seg = run_probe(L, ix, dix, Y, lr)
+        seg = run_probe(L, ix, dix, Y, lr, stage)
         ref = O.probe(ix, Y, read=lr)
         assert np.array_equal(host(seg), ref)
     assert (ref[:200, :, 1] > 0).mean() > 0.9 and (ref[200:, :, 1] == 0).mean() > 0.5
@@ -204,7 +209,8 @@ def test_probe_matches_oracle(L, ix, dix, small_index):
     (3, [2.5], 6, 1),                                # one level
     (1, [1.0, 1.4, 2.0, 2.8, 4.0, 5.6, 8.0, 11.0, 16.0, 22.0, 32.0], 8, 4),  # 11 levels: 5 groups per wavefront
 ])
-def test_probe_level_and_bucket_shapes(L, tmp_path, blocks, spacings, log_buckets, min_cell):
+@pytest.mark.parametrize("stage", PROBES)
+def test_probe_level_and_bucket_shapes(L, tmp_path, blocks, spacings, log_buckets, min_cell, stage):
     X, _ = clustered(n=1500, m=10, d=32, clusters=8, seed=11)
     path = str(tmp_path / "probe")
     O.build(X, path, copies=6, blocks=blocks, pca_dims=32, spacings=spacings, list_len=8, table_len=0,
@@ -212,7 +218,7 @@ def test_probe_level_and_bucket_shapes(L, tmp_path, blocks, spacings, log_bucket
     pix = O.Index(path)
     pdix = dict(inv_f=dev(pix.inv_f), offsets=dev(pix.offsets), keys=dev(pix.keys), base=dev(pix.base))
     Y = queries_Y(pix, X[:300], extra_random=100)
-    seg = run_probe(L, pix, pdix, Y, pix.list_len)
+    seg = run_probe(L, pix, pdix, Y, pix.list_len, stage)
     ref = O.probe(pix, Y, read=pix.list_len)
     assert np.array_equal(host(seg), ref)
     rows = ref[:, :, 0] // pix.list_len
