@@ -813,11 +813,6 @@ __device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, c
       hi = max(hi, kr[j]);
     }
   }
-  for (int i = tid + kCache * nthr; i < n; i += nthr) {
-    const unsigned k = kd[i];
-    lo               = min(lo, k);
-    hi               = max(hi, k);
-  }
 #pragma unroll
   for (int o = 32; o; o >>= 1) {
     lo = min(lo, static_cast<unsigned>(__shfl_xor(static_cast<int>(lo), o)));
@@ -831,16 +826,21 @@ __device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, c
     atomicMax(&bs.kmax, hi);
   }
   __syncthreads();
+  // the range of the register-held keys (all keys when n <= kCache nthr): keys past the cache outside it fall into
+  // the first or the last bin, which keeps the bins in key order
   const unsigned kmin = bs.kmin, kmax = bs.kmax, range = kmax - kmin;
   const int shift = range < static_cast<unsigned>(kBins) ? 0 : (32 - __clz(static_cast<int>(range))) - 11;
+  auto bin_of     = [&](unsigned k) {
+    return k < kmin ? 0u : min((k - kmin) >> shift, static_cast<unsigned>(kBins - 1));
+  };
   for (int j = 0; j < kCache; j++) {  // the histogram: register-held keys, then the rest
     if (kr[j] != kNone) {
-      const unsigned b = (kr[j] - kmin) >> shift;
+      const unsigned b = bin_of(kr[j]);
       atomicAdd(&sh.hist[b >> 1], 1u << (16 * (b & 1)));
     }
   }
   for (int i = tid + kCache * nthr; i < n; i += nthr) {
-    const unsigned b = (kd[i] - kmin) >> shift;
+    const unsigned b = bin_of(kd[i]);
     atomicAdd(&sh.hist[b >> 1], 1u << (16 * (b & 1)));
   }
   __syncthreads();
@@ -872,7 +872,7 @@ __device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, c
 #pragma unroll
   for (int j = 0; j < kCache; j++) {
     const bool ok    = kr[j] != kNone;
-    const unsigned b = (kr[j] - kmin) >> shift;
+    const unsigned b = bin_of(kr[j]);
     take(ok && b < bstar, ci[j], kr[j]);
     to_tie(ok && b == bstar, ci[j], kr[j]);
   }
@@ -881,7 +881,7 @@ __device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, c
     const int ii      = i < n ? i : 0;
     const unsigned kv = kd[ii];
     const int id      = cid[ii];
-    const unsigned b  = (kv - kmin) >> shift;
+    const unsigned b  = bin_of(kv);
     take(i < n && b < bstar, id, kv);
     to_tie(i < n && b == bstar, id, kv);
   }
@@ -892,8 +892,11 @@ __device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, c
   __syncthreads();
   if (many) {
     // more keys in bin b* than the ranked buffer holds: narrow the (key, id) values of b* by histogram passes
-    const uint64_t blo = static_cast<uint64_t>(kmin) + (static_cast<uint64_t>(bstar) << shift);
-    const uint64_t bhi = min(static_cast<uint64_t>(kmax), blo + ((uint64_t{1} << shift) - 1));
+    // the key range of bin b*: the first bin also holds the keys below kmin, the last those above kmax
+    const uint64_t blo = bstar == 0 ? 0 : static_cast<uint64_t>(kmin) + (static_cast<uint64_t>(bstar) << shift);
+    const uint64_t bhi = bstar == kBins - 1
+                           ? uint64_t{0xffffffffu}
+                           : static_cast<uint64_t>(kmin) + ((static_cast<uint64_t>(bstar) + 1) << shift) - 1;
     uint64_t vlo = blo << 32, vhi = (bhi << 32) | 0x7fffffffu;
     for (;;) {  // uniform: every bound comes from LDS after a barrier
       const uint64_t vr = vhi - vlo;

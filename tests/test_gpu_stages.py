@@ -273,8 +273,18 @@ def test_gather_rows_matches_oracle(L, ix, dix):
 # ---------------------------------------------------------------- keep, pick, final
 
 
+CACHED = 1024  # the selection's register-held keys on 128 threads (8 a thread): the first 1024 of a row
+
+
+def key_bits(bits):
+    return np.asarray(bits, np.uint32).view(np.float32)
+
+
 def random_candidates(g, m, W, n_max, N, ties=True, kind=None):
-    """Candidate rows of m queries: integer distances in [0, 40) (ties), uniform ones, or all equal."""
+    """Candidate rows of m queries: integer distances in [0, 40) (ties), uniform ones, or all equal; or rows whose keys
+    past the first CACHED lie outside the range of the first CACHED (the selection's bins come from those): spread on
+    both sides (tails), all equal below it (low_ties), or a last bin of thousands of keys at and above its top
+    (last_bin: keys of bits K and K + 2^24 - 1 in the cache, K + 2^25 past it)."""
     kind = kind or ("ties" if ties else "uniform")
     cand = np.full((m, W), -9, np.int32)
     dist = np.zeros((m, W), np.float32)
@@ -288,13 +298,21 @@ def random_candidates(g, m, W, n_max, N, ties=True, kind=None):
             dist[q, :n] = g.integers(0, 40, n)
         elif kind == "uniform":
             dist[q, :n] = g.uniform(0, 100, n)
+        elif kind == "tails":
+            dist[q, :n] = np.where(np.arange(n) < CACHED, g.uniform(40, 60, n), g.uniform(0, 100, n))
+        elif kind == "low_ties":
+            dist[q, :n] = np.where(np.arange(n) < CACHED, g.uniform(40, 60, n), 5.0)
+        elif kind == "last_bin":
+            K = 0x41000000
+            bits = np.where(np.arange(n) < 24, K, np.where(np.arange(n) < CACHED, K + 0xFFFFFF, K + 0x2000000))
+            dist[q, :n] = key_bits(bits)
         else:
             dist[q, :n] = 7.25
     return cand, dist, nin
 
 
-# (KO, R): the kept list and the reranked rows sort together, C keys a thread for the smallest C that holds KO + R:
-# candidate rows of W = 2048 run on 128 threads a query (C = 1, 2, 4 and 8 below), W = 8192 on 256 (C = 1, 2, 4)
+# (KO, R): the kept list and the reranked rows sort together on 128 threads a query, C keys a thread for the smallest C
+# that holds KO + R (C = 1, 2, 4 and 8 below)
 @pytest.mark.parametrize("KO,R", [(64, 16), (64, 48), (10, 20), (256, 256), (512, 512)])
 @pytest.mark.parametrize("fresh", [True, False])
 @pytest.mark.parametrize("W", [2048, 8192])
@@ -321,9 +339,10 @@ def test_rerank_keep_matches_oracle(L, ix, dix, small_index, fresh, KO, R, W):
         assert np.array_equal(host(dsd)[q], rd), f"query {q}"
 
 
-# the selection's paths: a threshold bin of a few keys (uniform), of many equal keys ranked by id (ties), and
-# of more keys than the ranked buffer holds (equal: every key in one bin, selected by radix passes)
-@pytest.mark.parametrize("kind", ["uniform", "ties", "equal"])
+# the selection's paths: a threshold bin of a few keys (uniform), of many equal keys ranked by id (ties), of more keys
+# than the ranked buffer holds (equal: every key in one bin, narrowed by histogram passes over (key, id)), and keys past
+# the register cache outside its range, in the first bin (tails, low_ties) or the last (last_bin)
+@pytest.mark.parametrize("kind", ["uniform", "ties", "equal", "tails", "low_ties", "last_bin"])
 def test_rerank_keep_selection_paths(L, ix, dix, small_index, kind):
     g = np.random.default_rng(9)
     m, W, KO, R = 24, 4096, 64, 128
@@ -572,7 +591,7 @@ def test_rerank_history_uses_its_last_256_entries(L, ix, dix, small_index):
     assert np.array_equal(host(dh), hist)  # not stored: the history is unchanged
 
 
-@pytest.mark.parametrize("kind", ["equal", "few"])
+@pytest.mark.parametrize("kind", ["equal", "few", "tails"])
 def test_selection_of_many_equal_keys_at_the_largest_width(L, ix, dix, small_index, kind):
     """Candidate rows of 2^15 slots whose threshold bin holds thousands of keys (all equal, or three values): the
     selection narrows them by further histogram passes over (key, id) and takes the smallest ids, as the oracle;
@@ -588,7 +607,10 @@ def test_selection_of_many_equal_keys_at_the_largest_width(L, ix, dix, small_ind
         for q in range(m):
             n = nin[q]
             cand[q, :n] = g.choice(N, n, replace=False)
-            dist[q, :n] = 7.25 if kind == "equal" else g.integers(0, 3, n).astype(np.float32)
+            if kind == "tails":  # keys past the first 4096 (the sketch merge's register cache) on both sides
+                dist[q, :n] = np.where(np.arange(n) < 4096, g.uniform(40, 60, n), g.integers(0, 100, n))
+            else:
+                dist[q, :n] = 7.25 if kind == "equal" else g.integers(0, 3, n).astype(np.float32)
         return cand, dist, nin
 
     cand, dist, nin = rows(30_000, 1_000_000)
