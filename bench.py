@@ -312,8 +312,11 @@ def stage_bytes(name, wave, cnt, m, C, S, D, KO, table_len, starts, w, L, FR=0, 
         return m * (FR * 2 * D + 12 * KO + 4 * D + 12 * k)
     if name == "gather_lists":
         return m * C * 8 + cnt["entries1"] * 4 + cnt["distinct1"] * (S + 8) + m * (S * 4 + 4)
-    if name == "gather_rows":
-        return m * starts * 8 + cnt["starts2"][wave] * table_len * 4 + cnt["distinct2"][wave] * (S + 8) + m * (S * 4 + 4)
+    if name == "gather_rows":  # the sketch rows of candidates no earlier row scored; 8 bytes an earlier-row entry read
+        known = cnt.get("known2", [0] * 16)[wave]
+        old = cnt.get("oldread2", [0] * 16)[wave]
+        return (m * starts * 8 + cnt["starts2"][wave] * table_len * 4 + (cnt["distinct2"][wave] - known) * S
+                + cnt["distinct2"][wave] * 8 + old * 8 + m * (S * 4 + 4))
     if name == "rerank_keep":
         return cnt["distinct1"] * 8 + cnt["reranked1"] * 2 * D + m * (12 * KO + 4 * D + 4)
     if name == "rerank_keep_wave":  # the selected candidates' rows, less those an earlier round reranked
@@ -577,7 +580,8 @@ def main():
     log(f"probe hits by level {cnt['hit_level'][:int(meta[4])]}, misses {len(Q) * C - cnt['seg_hits']}")
     nw = params.get("waves", 0)
     if nw:
-        log("waves: distinct " + str(cnt["distinct2"][:nw]) + ", selected " + str(cnt["reranked2"][:nw])
+        log("waves: distinct " + str(cnt["distinct2"][:nw]) + ", scored in earlier rows " + str(cnt["known2"][:nw])
+            + ", earlier-row entries read " + str(cnt["oldread2"][:nw]) + ", selected " + str(cnt["reranked2"][:nw])
             + ", of them reranked by an earlier round " + str(cnt["skipped2"][:nw]))
     log("stages: " + ", ".join(f"{x['stage']}[{x['wave']}] {x['ms']:.3f} ms {x['gbs']} GB/s" for x in per_launch))
 
@@ -646,9 +650,11 @@ def main():
             "index_gib": round(index.device_bytes[0] / 2**30, 2),
             "sweep": points,
             "stages": per_launch,
-            # per wave: distinct candidates, those selected for the exact rerank, and of those the ones an earlier
+            # per wave: distinct candidates, those whose scores came from earlier rows (no sketch row read), the
+            # earlier rows' entries read, the candidates selected for the exact rerank, and of those the ones an earlier
             # round reranked (their rows not read again)
-            "wave_reuse": {key: cnt[key][: params.get("waves", 0)] for key in ("distinct2", "reranked2", "skipped2")},
+            "wave_reuse": {key: cnt[key][: params.get("waves", 0)]
+                           for key in ("distinct2", "known2", "oldread2", "reranked2", "skipped2")},
         },
         "roofline": {
             "bound": "hbm",

@@ -38,11 +38,11 @@ cuvsError_t octexBuildInMemory(cuvsResources_t res, cuvsOctexIndexParams_t param
  * Profile one batch of queries [m <= batch, dim] (float32, host or device): a normal search, then the
  * same batch launched kernel by kernel `reps` times with HIP events around every launch on the index's
  * stream.  names (64 x 32 chars) and ms receive the stages in launch order with their average
- * milliseconds, *nstages their count; counters (76 int64, optional): probe hits, list entries read,
+ * milliseconds, *nstages their count; counters (108 int64, optional): probe hits, list entries read,
  * distinct first-round candidates, first-round reranked, then per wave (16 each) valid start points,
- * distinct candidates and reranked entries, then probe hits by level (8, the finest first), then per wave
- * (16) the selected candidates not reranked again (an earlier round reranked them); all summed over the batch's
- * m rows.
+ * distinct candidates and reranked entries, then probe hits by level (8, the finest first), then per wave (16 each)
+ * the selected candidates not reranked again (an earlier round reranked them), the candidates whose scores came from
+ * earlier rows, and the earlier rows' entries read; all summed over the batch's m rows.
  */
 cuvsError_t octexIndexProfileBatch(cuvsOctexIndex_t index, cuvsOctexSearchParams_t params, DLManagedTensor* queries,
                                    int64_t k, int32_t reps, char* names, double* ms, int32_t* nstages,
@@ -152,6 +152,14 @@ cuvsError_t octexStageGather(int32_t rows, const int32_t* seg, int32_t nseg, int
                              int64_t stride, const int32_t* table, int32_t table_len, int64_t n, const int8_t* code,
                              const float* scale, const float* qs, int32_t S, int32_t W, int32_t* cand,
                              float* dist, int32_t* nout, void* stream);
+/** octexStageGather over table rows taking the scores of candidates found in up to two earlier candidate rows
+ * (old_cand / old_dist [m, old_W[r]], counts old_n [m]; host arrays of device pointers), as the search's wave
+ * gathers do: those candidates come last in each row, copied, and nknown [m] (may be NULL) gets their count. */
+cuvsError_t octexStageGatherReuse(const int32_t* seg, int32_t nseg, int32_t m, const int32_t* table,
+                                  int32_t table_len, int64_t n, const int8_t* code, const float* scale,
+                                  const float* qs, int32_t S, int32_t W, int32_t* cand, float* dist, int32_t* nout,
+                                  int32_t nold, const int32_t* const* old_cand, const float* const* old_dist,
+                                  const int32_t* const* old_n, const int32_t* old_W, int32_t* nknown, void* stream);
 /** rerank_keep_kernel (search_kernels.cuh:421-467). */
 cuvsError_t octexStageRerankKeep(const int32_t* cand, const float* dist, const int32_t* nin, int32_t m,
                                  int32_t W, const void* vectors, int32_t D, const float* Q, int32_t R,

@@ -503,12 +503,14 @@ extern "C" cuvsError_t octexIndexProfileBatch(cuvsOctexIndex_t index, cuvsOctexS
     }
     *nstages = static_cast<int32_t>(nm.size());
     if (counters != nullptr) {
-      int64_t v[4 + 48 + 8 + 16] = {cnt.seg_hits, cnt.entries1, cnt.distinct1, cnt.reranked1};
+      int64_t v[4 + 48 + 8 + 48] = {cnt.seg_hits, cnt.entries1, cnt.distinct1, cnt.reranked1};
       for (int w = 0; w < 16; w++) {
-        v[4 + w]      = cnt.starts2[w];
-        v[4 + 16 + w] = cnt.distinct2[w];
-        v[4 + 32 + w] = cnt.reranked2[w];
-        v[60 + w]     = cnt.skipped2[w];
+        v[4 + w]       = cnt.starts2[w];
+        v[4 + 16 + w]  = cnt.distinct2[w];
+        v[4 + 32 + w]  = cnt.reranked2[w];
+        v[60 + w]      = cnt.skipped2[w];
+        v[60 + 16 + w] = cnt.known2[w];
+        v[60 + 32 + w] = cnt.oldread2[w];
       }
       for (int j = 0; j < 8; j++)
         v[52 + j] = cnt.hit_level[j];

@@ -470,7 +470,9 @@ __device__ __forceinline__ void sketch_scores(int n, IdOf const& id_of, const si
 /** Per-query state of collect_candidates (LDS). */
 struct collect_state {
   int cnt, nsp, ulen;
-  int hts;  // the hash set's slots
+  int hts;       // the hash set's slots
+  int known;     // candidates whose scores came from earlier rows (row gathers)
+  int wsum[16];  // a prefix sum's per-wavefront totals
 };
 
 /**
@@ -966,12 +968,134 @@ __device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, c
  * gather runs on kGatherListThreads, a row gather on kGatherRowThreads: the row gather's larger hash set leaves room
  * for fewer workgroups per CU, so each gets more threads.
  */
+constexpr int kKnown = static_cast<int>(0x80000000u);  // a hash-set entry whose id's score came from an earlier row
+
+/**
+ * The entries of a query's earlier rows (earlier_rows, at most two) as one sequence: entry e is row 0's e-th while
+ * e < no0, then row 1's.  load() reads entry e, or marks it absent (id -1) past the end, always from an in-bounds
+ * address (a row's W slots exist whatever its count), so the loads can be issued without branches.
+ */
+struct earlier_entries {
+  const int* c0;
+  const int* c1;
+  const float* d0;
+  const float* d1;
+  int W0, W1, no0, no1;
+
+  __device__ earlier_entries(earlier_rows const& er, int q)
+  {
+    const int r1 = er.count > 1 ? 1 : 0;  // one row: row 1 is row 0, never taken (no1 = 0)
+    c0  = er.cand[0] + static_cast<int64_t>(q) * er.W[0];
+    d0  = er.dist[0] + static_cast<int64_t>(q) * er.W[0];
+    c1  = er.cand[r1] + static_cast<int64_t>(q) * er.W[r1];
+    d1  = er.dist[r1] + static_cast<int64_t>(q) * er.W[r1];
+    W0  = er.W[0];
+    W1  = er.W[r1];
+    no0 = min(er.n[0][q], W0);
+    no1 = er.count > 1 ? min(er.n[1][q], W1) : 0;
+  }
+  [[nodiscard]] __device__ int total() const { return no0 + no1; }
+  __device__ void load(int e, int& id, float& sc) const
+  {
+    const bool first = e < no0;
+    const int Wr     = first ? W0 : W1;
+    const int i      = min(max(first ? e : e - no0, 0), Wr - 1);
+    id               = (first ? c0 : c1)[i];
+    sc               = (first ? d0 : d1)[i];
+    if (e >= no0 + no1) id = -1;
+  }
+};
+
+constexpr int kKnownPre = 4;  // earlier entries a row-gather thread loads before collecting
+
+/**
+ * Looks up an earlier entry (id, score) in a row gather's hash set ht (HT slots) after collecting; the first lookup to
+ * find an id marks its slot kKnown and writes (id, score) to crow / drow from position n - 1 down.
+ */
+__device__ __forceinline__ void take_entry(int id, float sc, int64_t N, int n, int* ht, int HT, int* crow,
+                                           float* drow, collect_state& cs)
+{
+  if (id < 0 || id >= N) return;
+  unsigned h = (static_cast<unsigned>(id) * kIdHash) & (HT - 1);
+  int at     = -1;
+  for (int p = 0; p < HT; p++) {
+    const int v = ht[h];
+    if (v == -1) break;
+    if ((v & ~kKnown) == id) {
+      at = static_cast<int>(h);
+      break;
+    }
+    h = (h + 1) & (HT - 1);
+  }
+  if (at >= 0 && (atomicOr(&ht[at], kKnown) & kKnown) == 0) {
+    const int pos = n - 1 - atomicAdd(&cs.known, 1);
+    if (pos >= 0) {
+      crow[pos] = id;
+      drow[pos] = sc;
+    }
+  }
+}
+
+/**
+ * A row gather's candidates found in earlier rows of the batch (the same query's, so the same scores), after
+ * collecting: the entries the thread loaded before collecting (pid / psc, entries tid + u NT), then the rest, are
+ * looked up (take_entry).  Then the slot list cl keeps only the unmarked candidates, in order, at its front.  Returns
+ * their count: candidates 0 .. returned - 1 are scored, the others are the copied ones.  Requires every inserted id
+ * listed (cnt <= cap).  Every thread calls it; it ends with a barrier.
+ */
+template <int NT>
+__device__ int take_known(earlier_entries const& ee, int const (&pid)[kKnownPre], float const (&psc)[kKnownPre],
+                          int64_t N, int n, int* ht, int HT, unsigned short* cl, int* crow, float* drow,
+                          collect_state& cs)
+{
+  constexpr int kU = 4;  // entries past the preloaded ones a thread loads together
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int u = 0; u < kKnownPre; u++)
+    take_entry(pid[u], psc[u], N, n, ht, HT, crow, drow, cs);
+  const int total = ee.total();
+  for (int e0 = kKnownPre * NT; e0 < total; e0 += NT * kU) {
+    int id[kU];
+    float sc[kU];
+#pragma unroll
+    for (int u = 0; u < kU; u++)
+      ee.load(e0 + u * NT + tid, id[u], sc[u]);
+#pragma unroll
+    for (int u = 0; u < kU; u++)
+      take_entry(id[u], sc[u], N, n, ht, HT, crow, drow, cs);
+  }
+  __syncthreads();
+  // the unmarked candidates' slots to the front of cl, in order: each chunk read whole before any of it is written
+  constexpr int kE = 8;
+  int kept = 0;
+  for (int j0 = 0; j0 < n; j0 += NT * kE) {
+    unsigned short sl[kE];
+    bool keep[kE];
+    int mine = 0;
+#pragma unroll
+    for (int e = 0; e < kE; e++) {
+      const int j = j0 + tid * kE + e;
+      sl[e]       = cl[j < n ? j : 0];
+      keep[e]     = j < n && (ht[sl[e]] & kKnown) == 0;
+      mine += keep[e] ? 1 : 0;
+    }
+    int tot = 0;
+    int at  = kept + block_exclusive_sum(mine, cs.wsum, &tot);
+#pragma unroll
+    for (int e = 0; e < kE; e++)
+      if (keep[e]) cl[at++] = sl[e];
+    kept += tot;
+  }
+  __syncthreads();
+  return kept;
+}
+
 template <bool kRows, int LR, bool kLdsSlots, bool kBalanced>
 __global__ __launch_bounds__(kRows ? kGatherRowThreads : kGatherListThreads) void gather_kernel(
   const int2* __restrict__ seg, int nseg, const long long* __restrict__ list_ptr,
   const int* __restrict__ table, int table_len, int64_t N, const signed char* __restrict__ code,
   const float* __restrict__ scale, const float* __restrict__ qs, int S, int pitch, int W, int logW, int cap,
-  int* __restrict__ cand, float* __restrict__ dist, int* __restrict__ nout)
+  int* __restrict__ cand, float* __restrict__ dist, int* __restrict__ nout, earlier_rows er, int* __restrict__ nknown)
 {
   const int q = blockIdx.x;
   extern __shared__ long long smq[];
@@ -991,13 +1115,35 @@ __global__ __launch_bounds__(kRows ? kGatherRowThreads : kGatherListThreads) voi
     else
       crow[slot] = static_cast<int>(h);
   };
+  if (threadIdx.x == 0) cs.known = 0;  // the collection's barriers order this before take_known
+  // the earlier rows' first entries, loaded now: their latency passes under the collection's
+  const bool reuse = kRows && kLdsSlots && er.count > 0;
+  int pid[kKnownPre];
+  float psc[kKnownPre];
+#pragma unroll
+  for (int u = 0; u < kKnownPre; u++)
+    pid[u] = -1;
+  if constexpr (kRows && kLdsSlots) {
+    if (reuse) {
+      const earlier_entries ee(er, q);
+#pragma unroll
+      for (int u = 0; u < kKnownPre; u++)
+        ee.load(threadIdx.x + u * kGatherRowThreads, pid[u], psc[u]);
+    }
+  }
   int n = 0;
   if constexpr (kBalanced)
     n = collect_candidates<kRows>(seg, nseg, list_ptr, table, table_len, N, logW, cap, sp, pre, ht, cs, keep_slot);
   else
     n = collect_segments_whole<kRows>(seg, nseg, list_ptr, table, table_len, N, logW, cap, ht, cs, keep_slot);
+  int nu = n;  // the candidates scored here
+  if constexpr (kRows && kLdsSlots) {
+    if (reuse && cs.cnt <= cap)  // uniform (read after the collection's last barrier)
+      nu = take_known<kGatherRowThreads>(earlier_entries(er, q), pid, psc, N, n, ht, cs.hts, cl, crow, drow, cs);
+  }
+  if (nknown != nullptr && threadIdx.x == 0) nknown[q] = n - nu;
   sketch_scores<LR>(
-    n,
+    nu,
     [&](int j) {
       if constexpr (kLdsSlots)
         return ht[cl[j]];
@@ -1933,7 +2079,8 @@ constexpr size_t kGatherLds = 160 * 1024 - 256;  // the CU's LDS less the kernel
 template <bool kBalanced>
 void gather_impl(bool rows, const int2* seg, int nseg, int max_len, int m, const long long* list_ptr,
                  const int* table, int table_len, int64_t n, const signed char* code, int pitch, const float* scale,
-                 const float* qs, int S, int W, int logW, int* cand, float* dist, int* nout, hipStream_t s)
+                 const float* qs, int S, int W, int logW, int* cand, float* dist, int* nout, earlier_rows er,
+                 int* nknown, hipStream_t s)
 {
   OCTEX_EXPECTS(pitch >= S && pitch % 16 == 0, "octex: sketch rows are at least S bytes apart, 16-byte aligned");
   if (m == 0) return;
@@ -1945,6 +2092,11 @@ void gather_impl(bool rows, const int2* seg, int nseg, int max_len, int m, const
   const size_t smem    = gather_smem(W, S, nseg, max_len, lds_slots);
   OCTEX_EXPECTS(smem <= kGatherLds, "octex: gather needs %zu bytes of LDS (max 160 KiB)", smem);
   const int cap = gather_cap(W, nseg, max_len);
+  OCTEX_EXPECTS(er.count >= 0 && er.count <= 2 && (er.count == 0 || rows), "octex: earlier rows of a row gather");
+  for (int r = 0; r < er.count; r++)
+    OCTEX_EXPECTS(er.cand[r] != nullptr && er.dist[r] != nullptr && er.n[r] != nullptr && er.W[r] >= 1 &&
+                    er.cand[r] != cand && er.dist[r] != dist,
+                  "octex: an earlier row set is another batch row set");
   int Lr = 1;  // the reference's lanes per candidate: the next power of two >= S / 16, at most 32
   while (Lr < S / 16 && Lr < 32)
     Lr <<= 1;
@@ -1954,7 +2106,8 @@ void gather_impl(bool rows, const int2* seg, int nseg, int max_len, int m, const
     auto launch             = [&](auto kernel) {
       allow_lds(reinterpret_cast<const void*>(kernel), smem);
       kernel<<<m, kRowsTag ? kGatherRowThreads : kGatherListThreads, smem, s>>>(
-        seg, nseg, list_ptr, table, table_len, n, code, scale, qs, S, pitch, W, logW, cap, cand, dist, nout);
+        seg, nseg, list_ptr, table, table_len, n, code, scale, qs, S, pitch, W, logW, cap, cand, dist, nout, er,
+        nknown);
     };
     if (lds_slots)
       launch(&gather_kernel<kRowsTag, LR, true, kBalanced>);
@@ -2003,7 +2156,16 @@ void launch_gather(bool rows, const int2* seg, int nseg, int max_len, int m, con
                    int* nout, hipStream_t s)
 {
   gather_impl<true>(rows, seg, nseg, max_len, m, list_ptr, table, table_len, n, code, pitch, scale, qs, S, W, logW,
-                    cand, dist, nout, s);
+                    cand, dist, nout, earlier_rows{}, nullptr, s);
+}
+
+void launch_gather_reuse(const int2* seg, int nseg, int max_len, int m, const int* table, int table_len, int64_t n,
+                         const signed char* code, int pitch, const float* scale, const float* qs, int S, int W,
+                         int logW, int* cand, float* dist, int* nout, earlier_rows const& er, int* nknown,
+                         bool balanced, hipStream_t s)
+{
+  (balanced ? gather_impl<true> : gather_impl<false>)(true, seg, nseg, max_len, m, nullptr, table, table_len, n, code,
+                                                      pitch, scale, qs, S, W, logW, cand, dist, nout, er, nknown, s);
 }
 
 void launch_gather_segments(bool rows, const int2* seg, int nseg, int max_len, int m, const long long* list_ptr,
@@ -2012,7 +2174,7 @@ void launch_gather_segments(bool rows, const int2* seg, int nseg, int max_len, i
                             int* nout, hipStream_t s)
 {
   gather_impl<false>(rows, seg, nseg, max_len, m, list_ptr, table, table_len, n, code, pitch, scale, qs, S, W, logW,
-                     cand, dist, nout, s);
+                     cand, dist, nout, earlier_rows{}, nullptr, s);
 }
 
 void launch_unfused_keep(const int* cand, const float* dist, const int* nin, int m, int W, const __half* vectors,

@@ -75,10 +75,32 @@ auto gather_smem(int W, int S, int nseg, int max_len, bool lds_slots) -> size_t;
  * code [n, pitch]: the S sketch codes of row v start at code + v * pitch.
  * max_len: no segment is longer (a query keeps at most min(W, nseg * max_len) candidates).
  */
+/**
+ * Up to two earlier candidate rows of a batch: ids and sketch scores cand / dist [m, W[r]], counts n [m].  A query's
+ * sketch score of an id is the same in every round, so a row gather takes the scores of the candidates found there
+ * instead of reading their sketch rows again.
+ */
+struct earlier_rows {
+  const int* cand[2]    = {};
+  const float* dist[2]  = {};
+  const int* n[2]       = {};
+  int W[2]              = {};
+  int count             = 0;
+};
 void launch_gather(bool rows, const int2* seg, int nseg, int max_len, int m, const long long* list_ptr,
                    const int* table, int table_len, int64_t n, const signed char* code, int pitch,
                    const float* scale, const float* qs, int S, int W, int logW, int* cand, float* dist,
                    int* nout, hipStream_t s);
+/**
+ * launch_gather over table rows (rows = true) taking the scores of candidates found in the earlier rows `er`: those
+ * candidates come last in each query's row (positions nout - nknown .. nout - 1), copied, and the others are scored as
+ * launch_gather scores them.  nknown [m] (may be null) gets their count.  The earlier rows are used only when the
+ * candidates' slot list fits in LDS beside the hash set (else nknown is 0).
+ */
+void launch_gather_reuse(const int2* seg, int nseg, int max_len, int m, const int* table, int table_len, int64_t n,
+                         const signed char* code, int pitch, const float* scale, const float* qs, int S, int W,
+                         int logW, int* cand, float* dist, int* nout, earlier_rows const& er, int* nknown,
+                         bool balanced, hipStream_t s);
 /** launch_gather without the load balance (balanced_gather = false): a wavefront reads each segment whole
  * (search_kernels.cuh:687-792).  Same arguments and results. */
 void launch_gather_segments(bool rows, const int2* seg, int nseg, int max_len, int m, const long long* list_ptr,

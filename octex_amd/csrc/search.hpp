@@ -27,23 +27,33 @@ struct plan_shape {
   int pool1 = 0, pool2 = 0;                // unfused merge (fused_merge = false): keys per query's pool
   int Ep = 0;                              // unfused start points: sorted expanded ids per query
   int H = 0;  // the fused rerank's history of selected ids per query: rerank + wave_rerank (waves - 1)
+  // wave row sets: wave w writes set w % ring and takes the scores its candidates have in the previous round's row
+  // (the first round's for wave 0, set (w - 1) % ring after; reuse, ring 2 from two waves on)
+  int ring = 1;
+  bool reuse = false;
+  bool reuse_first = false;  // waves after the first also take scores from the first round's row
 };
 
 /**
  * Where every per-batch array lies (device addresses): qbuf f32 [m, D] queries; qc f32 / qh f16 [m, D]
  * centred; Y f16 [m, C 8b]; qs f32 [m, S]; seg int2 [m, C]; cand i32 / dist f32 [m, W], nin [m]; si i64 /
- * sd f32 [m, KO] kept list; done i64 [m, starts waves]; seg2 int2 [m, starts]; cand2 / dist2 [m, W2], n2 [m];
- * nskip [m] (selected candidates the last wave's rerank did not rerank again); hist i32 [m, H] (the fused rerank's
+ * sd f32 [m, KO] kept list; done i64 [m, starts waves]; seg2 int2 [m, starts]; cand2 / dist2 [m, W2], n2 [m], one
+ * set per ring slot; nknown [m] (candidates of the last wave gather whose scores came from earlier rows); nskip [m]
+ * (selected candidates the last wave's rerank did not rerank again); hist i32 [m, H] (the fused rerank's
  * selected ids of every round but the last); bi i64 / bd f32 [m, k]; with fused_merge = false also ukey u64
  * [m, max(W, W2)] candidate keys (sorted in place), upool u64 [m, max(pool1, pool2)] pools, dsort i64 [m, Ep] the ids
  * earlier waves expanded, sorted (Ep the power of two >= starts (waves - 1)), and fresh u8 [m, KO].
  */
+constexpr int kRing = 2;  // wave row sets at most
+
 struct batch_buffers {
-  float *qbuf = nullptr, *qc = nullptr, *qs = nullptr, *dist = nullptr, *sd = nullptr, *dist2 = nullptr,
-        *bd = nullptr;
+  float *qbuf = nullptr, *qc = nullptr, *qs = nullptr, *dist = nullptr, *sd = nullptr, *bd = nullptr;
+  float* dist2[kRing] = {};
   __half *qh = nullptr, *Y = nullptr;
   int2 *seg = nullptr, *seg2 = nullptr;
-  int *cand = nullptr, *nin = nullptr, *cand2 = nullptr, *n2 = nullptr, *nskip = nullptr, *hist = nullptr;
+  int *cand = nullptr, *nin = nullptr, *nknown = nullptr, *nskip = nullptr, *hist = nullptr;
+  int* cand2[kRing] = {};
+  int* n2[kRing]    = {};
   long long *si = nullptr, *done = nullptr, *bi = nullptr;
   uint64_t *ukey = nullptr, *upool = nullptr, *dsort = nullptr;
   unsigned char* fresh = nullptr;
@@ -86,6 +96,8 @@ void launch_batch(index_impl const& ix, plan_shape const& sh, batch_buffers cons
 struct profile_counters {
   int64_t seg_hits = 0, entries1 = 0, distinct1 = 0, reranked1 = 0;
   int64_t starts2[16] = {}, distinct2[16] = {}, reranked2[16] = {};
+  int64_t known2[16] = {};    // wave candidates whose scores came from earlier rows
+  int64_t oldread2[16] = {};  // entries of earlier rows each wave gather read
   int64_t skipped2[16] = {};  // selected wave candidates not reranked again (an earlier round reranked them)
   int64_t hit_level[8] = {};  // probe hits by level (0 the finest); misses are m C - seg_hits
 };

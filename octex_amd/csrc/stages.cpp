@@ -148,6 +148,41 @@ extern "C" cuvsError_t octexStageGather(int32_t rows, const int32_t* seg, int32_
   });
 }
 
+extern "C" cuvsError_t octexStageGatherReuse(const int32_t* seg, int32_t nseg, int32_t m, const int32_t* table,
+                                             int32_t table_len, int64_t n, const int8_t* code, const float* scale,
+                                             const float* qs, int32_t S, int32_t W, int32_t* cand, float* dist,
+                                             int32_t* nout, int32_t nold, const int32_t* const* old_cand,
+                                             const float* const* old_dist, const int32_t* const* old_n,
+                                             const int32_t* old_W, int32_t* nknown, void* stream)
+{
+  return run(stream, [&](hipStream_t s) {
+    need(seg, "seg"), need(table, "table"), need(code, "code"), need(scale, "scale"), need(qs, "qs");
+    need(cand, "cand"), need(dist, "dist"), need(nout, "nout");
+    OCTEX_EXPECTS(W >= (1 << kMinLogHash) && (W & (W - 1)) == 0, "octex: W must be a power of two >= 2048");
+    OCTEX_EXPECTS(nold >= 0 && nold <= 2 && (nold == 0 || (old_cand && old_dist && old_n && old_W)),
+                  "octex: at most two earlier rows");
+    earlier_rows er;
+    for (int r = 0; r < nold; r++) {
+      er.cand[r] = old_cand[r];
+      er.dist[r] = old_dist[r];
+      er.n[r]    = old_n[r];
+      er.W[r]    = old_W[r];
+    }
+    er.count = nold;
+    int max_len = 0;  // the longest segment (sizes the candidate list)
+    {
+      std::vector<int2> hs(static_cast<size_t>(m) * nseg);
+      if (!hs.empty()) OCTEX_HIP(hipMemcpy(hs.data(), seg, hs.size() * sizeof(int2), hipMemcpyDefault));
+      for (auto const& v : hs)
+        max_len = std::max(max_len, v.y);
+    }
+    launch_gather_reuse(reinterpret_cast<const int2*>(seg), nseg, max_len, m, table, table_len, n,
+                        reinterpret_cast<const signed char*>(code), S, scale, qs, S, W, log2_ceil(W), cand, dist,
+                        nout, er, nknown, true, s);
+    OCTEX_HIP(hipStreamSynchronize(s));
+  });
+}
+
 extern "C" cuvsError_t octexStageRerankKeepHistory(const int32_t* cand, const float* dist, const int32_t* nin,
                                                    int32_t m, int32_t W, const void* vectors, int32_t D, const float* Q,
                                                    int32_t R, int32_t KO, int64_t* si, float* sd, int32_t fresh,

@@ -266,13 +266,14 @@ class Index:
         names = ct.create_string_buffer(64 * 32)
         ms = (ct.c_double * 64)()
         ns = ct.c_int32(0)
-        cnt = (ct.c_int64 * 76)()
+        cnt = (ct.c_int64 * 108)()
         _lib.call("octexIndexProfileBatch", self._handle, ct.byref(p), dq.ptr, ct.c_int64(k), ct.c_int32(reps), names,
                   ms, ct.byref(ns), cnt)
         stages = [(names.raw[32 * i : 32 * (i + 1)].split(b"\0")[0].decode(), ms[i]) for i in range(ns.value)]
         c = list(cnt)
         counters = dict(seg_hits=c[0], entries1=c[1], distinct1=c[2], reranked1=c[3], starts2=c[4:20],
-                        distinct2=c[20:36], reranked2=c[36:52], hit_level=c[52:60], skipped2=c[60:76])
+                        distinct2=c[20:36], reranked2=c[36:52], hit_level=c[52:60], skipped2=c[60:76],
+                        known2=c[76:92], oldread2=c[92:108])
         return stages, counters
 
     def place_on_host(self, vectors=True, table=False, sketch=False):

@@ -32,6 +32,9 @@ def test_stage_bytes_cover_every_stage():
     # gather_rows: starts + table rows + every distinct sketch row at S + 8 bytes + the query's sketch
     want = 10_000 * 64 * 8 + 10_000 * 64 * 64 * 4 + 10_000 * 3000 * (96 + 8) + 10_000 * (96 * 4 + 4)
     assert bench.stage_bytes("gather_rows", 0, COUNTERS, **args) == want
+    # candidates whose scores came from earlier rows: no sketch row, 8 bytes per earlier-row entry read
+    reuse = dict(COUNTERS, known2=[1000] + [0] * 15, oldread2=[2500] + [0] * 15)
+    assert bench.stage_bytes("gather_rows", 0, reuse, **args) == want - 1000 * 96 + 2500 * 8
     # the wave rerank does not read the rows of the selected candidates an earlier round reranked
     skip = dict(COUNTERS, skipped2=[300] + [0] * 15)
     assert (bench.stage_bytes("rerank_keep_wave", 0, COUNTERS, **args)

@@ -282,6 +282,27 @@ def test_probe_without_bucket_lines(octex, small_index, monkeypatch):
     assert a.device_bytes[0] - b.device_bytes[0] == lines
 
 
+@pytest.mark.parametrize("mode", ["1", "all"])
+def test_wave_gathers_with_and_without_earlier_scores(octex, small_index, monkeypatch, mode):
+    """Wave gathers take the scores of candidates found in the previous round's row (all: also in the first round's);
+    with OCTEX_GATHER_REUSE=0 (read when a plan is made) they score every candidate: the same results, and the profile
+    counts the candidates found (three waves)."""
+    Q = small_index["Q"][:60]
+    params = dict(PARAMS, waves=3)
+    monkeypatch.setenv("OCTEX_GATHER_REUSE", mode)
+    a = octex.load(small_index["path"])
+    Da, Ia = a.search(Q, k=10, **params)
+    _, cnt = a.profile_batch(Q, k=10, reps=1, **params)
+    monkeypatch.setenv("OCTEX_GATHER_REUSE", "0")
+    b = octex.load(small_index["path"])
+    Db, Ib = b.search(Q, k=10, **params)
+    _, cnt0 = b.profile_batch(Q, k=10, reps=1, **params)
+    assert np.array_equal(Ia, Ib) and np.array_equal(Da, Db)
+    assert all(k > 0 for k in cnt["known2"][:3]) and all(o > 0 for o in cnt["oldread2"][:3])
+    assert sum(cnt0["known2"]) == 0 and sum(cnt0["oldread2"]) == 0
+    assert cnt["distinct2"][:3] == cnt0["distinct2"][:3]
+
+
 def test_placements_on_host(octex, small_index):
     """Vectors, table and sketch in pinned host memory give the same results."""
     Q = small_index["Q"][:40]

@@ -270,6 +270,65 @@ def test_gather_rows_matches_oracle(L, ix, dix):
     assert nout[0] == 0
 
 
+def gather_reuse_gpu(L, ix, dix, seg, qs, old, W=4096):
+    """octexStageGatherReuse over table rows with the earlier rows `old` [(cand, dist, n, W)] (device tensors)."""
+    m, nseg = seg.shape[0], seg.shape[1]
+    cand = torch.full((m, W), -5, dtype=torch.int32, device="cuda")
+    dist = torch.zeros((m, W), dtype=torch.float32, device="cuda")
+    nout = torch.zeros(m, dtype=torch.int32, device="cuda")
+    nk = torch.full((m,), -1, dtype=torch.int32, device="cuda")
+    dqs, dseg = dev(qs), dev(seg)
+    k = len(old)
+    oc = (ct.c_void_p * max(k, 1))(*[o[0].data_ptr() for o in old])
+    od = (ct.c_void_p * max(k, 1))(*[o[1].data_ptr() for o in old])
+    on = (ct.c_void_p * max(k, 1))(*[o[2].data_ptr() for o in old])
+    ow = (ct.c_int32 * max(k, 1))(*[o[3] for o in old])
+    L.call("octexStageGatherReuse", P(dseg), i32(nseg), i32(m), P(dix["table"]), i32(ix.table_len), i64(ix.n),
+           P(dix["sketch"]), P(dix["scale"]), P(dqs), i32(ix.sketch_width), i32(W), P(cand), P(dist), P(nout), i32(k),
+           oc, od, on, ow, P(nk), None)
+    return host(cand), host(dist), host(nout), host(nk)
+
+
+def test_gather_takes_scores_from_earlier_rows(L, ix, dix):
+    """A wave gather given two earlier rows (of another width, with repeated ids between them, one query's rows
+    empty): the oracle's candidate set with bit-identical scores; the candidates found in an earlier row come last
+    and number nknown; a query without starts has none."""
+    g = np.random.default_rng(21)
+    m, S = 40, 64
+
+    def rows_of(starts, dead=0):
+        seg = np.stack([starts, np.full(starts.shape, ix.table_len)], -1).astype(np.int32)
+        if dead:
+            seg[:, -dead:] = 0
+        return seg
+
+    qs = g.standard_normal((m, ix.sketch_width)).astype(np.float32)
+    starts_a = g.integers(0, ix.n, (m, S))
+    seg_a = rows_of(starts_a, dead=5)
+    seg_a[2] = 0  # an earlier row without candidates
+    ca, da, na = gather_gpu(L, ix, dix, dev(seg_a), qs, rows=1, W=2048)
+    starts_b = np.where(g.random((m, S)) < 0.5, starts_a, g.integers(0, ix.n, (m, S)))
+    cb, db, nb = gather_gpu(L, ix, dix, dev(rows_of(starts_b)), qs, rows=1, W=4096)
+    starts_c = np.where(g.random((m, S)) < 0.5, starts_b, g.integers(0, ix.n, (m, S)))
+    seg_c = rows_of(starts_c, dead=3)
+    seg_c[1] = 0  # a query without starts
+    old = [(dev(ca), dev(da), dev(na), 2048), (dev(cb), dev(db), dev(nb), 4096)]
+    cand, dist, nout, nk = gather_reuse_gpu(L, ix, dix, seg_c, qs, old)
+    check_gather(ix, seg_c, qs, cand, dist, nout, rows=True)
+    for q in range(m):
+        n = nout[q]
+        seen = {int(v) for v in ca[q, : na[q]]} | {int(v) for v in cb[q, : nb[q]]}
+        known = np.array([int(v) in seen for v in cand[q, :n]], bool)
+        assert nk[q] == known.sum(), f"query {q}"
+        assert not known[: n - nk[q]].any() and known[n - nk[q] :].all(), f"query {q}: the found candidates come last"
+    assert nout[1] == 0 and nk[1] == 0
+    assert nk.sum() > 0.3 * nout.sum()  # half the starts repeat: many candidates come from the earlier rows
+    # no earlier rows: the plain gather's result
+    cand0, dist0, nout0, nk0 = gather_reuse_gpu(L, ix, dix, seg_c, qs, [])
+    check_gather(ix, seg_c, qs, cand0, dist0, nout0, rows=True)
+    assert (nk0 == 0).all()
+
+
 # ---------------------------------------------------------------- keep, pick, final
 
 
