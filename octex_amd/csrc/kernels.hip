@@ -972,8 +972,9 @@ constexpr int kKnown = static_cast<int>(0x80000000u);  // a hash-set entry whose
 
 /**
  * The entries of a query's earlier rows (earlier_rows, at most two) as one sequence: entry e is row 0's e-th while
- * e < no0, then row 1's.  load() reads entry e, or marks it absent (id -1) past the end, always from an in-bounds
- * address (a row's W slots exist whatever its count), so the loads can be issued without branches.
+ * e < no0, then row 1's.  load() reads entry e from an in-bounds address whatever e is (a row's W slots exist whatever
+ * its count; without earlier rows, the fallback row) and returns whether the entry exists; the loaded values are not
+ * used before the caller uses them, so the loads stay in flight.
  */
 struct earlier_entries {
   const int* c0;
@@ -982,8 +983,15 @@ struct earlier_entries {
   const float* d1;
   int W0, W1, no0, no1;
 
-  __device__ earlier_entries(earlier_rows const& er, int q)
+  __device__ earlier_entries(earlier_rows const& er, int q, const int* fc, const float* fd, int fW)
   {
+    if (er.count == 0) {  // no rows: the fallback row (the query's own), never taken
+      c0 = c1 = fc;
+      d0 = d1 = fd;
+      W0 = W1 = fW;
+      no0 = no1 = 0;
+      return;
+    }
     const int r1 = er.count > 1 ? 1 : 0;  // one row: row 1 is row 0, never taken (no1 = 0)
     c0  = er.cand[0] + static_cast<int64_t>(q) * er.W[0];
     d0  = er.dist[0] + static_cast<int64_t>(q) * er.W[0];
@@ -995,14 +1003,14 @@ struct earlier_entries {
     no1 = er.count > 1 ? min(er.n[1][q], W1) : 0;
   }
   [[nodiscard]] __device__ int total() const { return no0 + no1; }
-  __device__ void load(int e, int& id, float& sc) const
+  __device__ bool load(int e, int& id, float& sc) const
   {
     const bool first = e < no0;
     const int Wr     = first ? W0 : W1;
     const int i      = min(max(first ? e : e - no0, 0), Wr - 1);
     id               = (first ? c0 : c1)[i];
     sc               = (first ? d0 : d1)[i];
-    if (e >= no0 + no1) id = -1;
+    return e < no0 + no1;
   }
 };
 
@@ -1045,24 +1053,25 @@ __device__ __forceinline__ void take_entry(int id, float sc, int64_t N, int n, i
  */
 template <int NT>
 __device__ int take_known(earlier_entries const& ee, int const (&pid)[kKnownPre], float const (&psc)[kKnownPre],
-                          int64_t N, int n, int* ht, int HT, unsigned short* cl, int* crow, float* drow,
-                          collect_state& cs)
+                          bool const (&pok)[kKnownPre], int64_t N, int n, int* ht, int HT, unsigned short* cl,
+                          int* crow, float* drow, collect_state& cs)
 {
   constexpr int kU = 4;  // entries past the preloaded ones a thread loads together
   const int tid = threadIdx.x;
 #pragma unroll
   for (int u = 0; u < kKnownPre; u++)
-    take_entry(pid[u], psc[u], N, n, ht, HT, crow, drow, cs);
+    take_entry(pok[u] ? pid[u] : -1, psc[u], N, n, ht, HT, crow, drow, cs);
   const int total = ee.total();
   for (int e0 = kKnownPre * NT; e0 < total; e0 += NT * kU) {
     int id[kU];
     float sc[kU];
+    bool ok[kU];
 #pragma unroll
     for (int u = 0; u < kU; u++)
-      ee.load(e0 + u * NT + tid, id[u], sc[u]);
+      ok[u] = ee.load(e0 + u * NT + tid, id[u], sc[u]);
 #pragma unroll
     for (int u = 0; u < kU; u++)
-      take_entry(id[u], sc[u], N, n, ht, HT, crow, drow, cs);
+      take_entry(ok[u] ? id[u] : -1, sc[u], N, n, ht, HT, crow, drow, cs);
   }
   __syncthreads();
   // the unmarked candidates' slots to the front of cl, in order: each chunk read whole before any of it is written
@@ -1116,19 +1125,18 @@ __global__ __launch_bounds__(kRows ? kGatherRowThreads : kGatherListThreads) voi
       crow[slot] = static_cast<int>(h);
   };
   if (threadIdx.x == 0) cs.known = 0;  // the collection's barriers order this before take_known
-  // the earlier rows' first entries, loaded now: their latency passes under the collection's
+  // the earlier rows' first entries, loaded now and not used before the collection ends: their latency passes under
+  // the collection's (pid / psc are left unset without earlier rows, so that no value of them waits for the loads)
   const bool reuse = kRows && kLdsSlots && er.count > 0;
   int pid[kKnownPre];
   float psc[kKnownPre];
-#pragma unroll
-  for (int u = 0; u < kKnownPre; u++)
-    pid[u] = -1;
+  bool pok[kKnownPre] = {};
   if constexpr (kRows && kLdsSlots) {
-    if (reuse) {
-      const earlier_entries ee(er, q);
+    if (reuse) {  // uniform
+      const earlier_entries ee(er, q, crow, drow, W);
 #pragma unroll
       for (int u = 0; u < kKnownPre; u++)
-        ee.load(threadIdx.x + u * kGatherRowThreads, pid[u], psc[u]);
+        pok[u] = ee.load(threadIdx.x + u * kGatherRowThreads, pid[u], psc[u]);
     }
   }
   int n = 0;
@@ -1139,7 +1147,8 @@ __global__ __launch_bounds__(kRows ? kGatherRowThreads : kGatherListThreads) voi
   int nu = n;  // the candidates scored here
   if constexpr (kRows && kLdsSlots) {
     if (reuse && cs.cnt <= cap)  // uniform (read after the collection's last barrier)
-      nu = take_known<kGatherRowThreads>(earlier_entries(er, q), pid, psc, N, n, ht, cs.hts, cl, crow, drow, cs);
+      nu = take_known<kGatherRowThreads>(earlier_entries(er, q, crow, drow, W), pid, psc, pok, N, n, ht, cs.hts, cl,
+                                         crow, drow, cs);
   }
   if (nknown != nullptr && threadIdx.x == 0) nknown[q] = n - nu;
   sketch_scores<LR>(

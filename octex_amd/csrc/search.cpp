@@ -79,13 +79,17 @@ auto make_shape(index_impl const& ix, search_params const& sp, int m, int k) -> 
     sh.W2    = 1 << sh.logW2;
     // the fused exact rerank keeps the ids every round but the last selects, to skip them when selected again
     if (sp.fused_merge && !sp.sketch_rank) sh.H = sh.R1 + sh.R2 * (sp.waves - 1);
-    // wave gathers take the scores of their candidates found in the previous round's row (OCTEX_GATHER_REUSE=0: they
-    // score every candidate; =all: from the first round's row too).  Measured at 10M rows: the second wave found 345
-    // of its 359 candidates in the first wave's row, and 352 in both rows, for a 2.3 times longer scan
-    const char* e  = std::getenv("OCTEX_GATHER_REUSE");
-    sh.reuse       = e == nullptr || std::string(e) != "0";
-    sh.reuse_first = e != nullptr && std::string(e) == "all";
-    sh.ring        = sh.reuse && sp.waves > 1 ? 2 : 1;
+    // the first wave's gather takes the scores of its candidates found in the first round's row.  OCTEX_GATHER_REUSE
+    // (read when a plan is made): 0, no wave does; prev, every wave from the previous round's row; all, later waves
+    // from the first round's and the previous wave's rows.  Measured at 100M rows (no graphs): the first wave
+    // 0.737 -> 0.690 ms; the second, from the first wave's row, 0.474 -> 0.485 ms although 43 % of its candidates are
+    // found there (the scan of 2,858 entries a query costs what the 729 rows it saves do)
+    const char* e          = std::getenv("OCTEX_GATHER_REUSE");
+    const std::string mode = e != nullptr ? e : "1";
+    sh.reuse               = mode != "0";
+    sh.reuse_later         = mode == "prev" || mode == "all";
+    sh.reuse_first         = mode == "all";
+    sh.ring                = sh.reuse_later && sp.waves > 1 ? 2 : 1;
   }
   if (!sp.fused_merge) {  // the pools of the unfused merge: the kept list and the R best candidates
     auto pool = [&](int R) { return 1 << log2_ceil(sh.KO + (sp.sketch_rank ? sh.KO : R)); };
@@ -246,7 +250,7 @@ auto batch_stages(index_impl const& ix, plan_shape const& sh, batch_buffers cons
                             b.seg2, s);
     });
     const int r = wv % sh.ring;
-    if (sh.reuse) {
+    if (sh.reuse && (wv == 0 || sh.reuse_later)) {
       earlier_rows er;  // the first round's row, and the previous wave's
       auto add_row = [&er](const int* c, const float* d, const int* n, int W) {
         er.cand[er.count] = c;
@@ -462,7 +466,7 @@ void profile_batch(index_impl& ix, plan& pl, int reps, std::vector<std::string>&
         for (int q = 0; q < m; q++) {
           cnt.distinct2[wv] += n2[q];
           cnt.reranked2[wv] += std::min(n2[q], sh.sp.sketch_rank ? sh.KO : sh.R2);
-          if (!sh.reuse) continue;
+          if (!sh.reuse || (wv > 0 && !sh.reuse_later)) continue;
           cnt.known2[wv] += nk[q];
           cnt.oldread2[wv] += (wv == 0 || sh.reuse_first ? std::min(nin[q], sh.W) : 0) +
                               (wv > 0 ? std::min(prev2[q], sh.W2) : 0);

@@ -27,11 +27,13 @@ struct plan_shape {
   int pool1 = 0, pool2 = 0;                // unfused merge (fused_merge = false): keys per query's pool
   int Ep = 0;                              // unfused start points: sorted expanded ids per query
   int H = 0;  // the fused rerank's history of selected ids per query: rerank + wave_rerank (waves - 1)
-  // wave row sets: wave w writes set w % ring and takes the scores its candidates have in the previous round's row
-  // (the first round's for wave 0, set (w - 1) % ring after; reuse, ring 2 from two waves on)
-  int ring = 1;
-  bool reuse = false;
-  bool reuse_first = false;  // waves after the first also take scores from the first round's row
+  // wave row sets: wave w writes set w % ring.  With reuse the first wave takes the scores its candidates have in the
+  // first round's row; with reuse_later the later waves too, from set (w - 1) % ring (ring 2) and, with reuse_first,
+  // from the first round's row
+  int ring         = 1;
+  bool reuse       = false;
+  bool reuse_later = false;
+  bool reuse_first = false;
 };
 
 /**

@@ -282,11 +282,12 @@ def test_probe_without_bucket_lines(octex, small_index, monkeypatch):
     assert a.device_bytes[0] - b.device_bytes[0] == lines
 
 
-@pytest.mark.parametrize("mode", ["1", "all"])
+@pytest.mark.parametrize("mode", ["1", "prev", "all"])
 def test_wave_gathers_with_and_without_earlier_scores(octex, small_index, monkeypatch, mode):
-    """Wave gathers take the scores of candidates found in the previous round's row (all: also in the first round's);
-    with OCTEX_GATHER_REUSE=0 (read when a plan is made) they score every candidate: the same results, and the profile
-    counts the candidates found (three waves)."""
+    """The first wave's gather takes the scores of candidates found in the first round's row; with prev every wave from
+    the previous round's row, with all the later waves also from the first round's.  With OCTEX_GATHER_REUSE=0 (read
+    when a plan is made) they score every candidate: the same results, and the profile counts the candidates found
+    (three waves)."""
     Q = small_index["Q"][:60]
     params = dict(PARAMS, waves=3)
     monkeypatch.setenv("OCTEX_GATHER_REUSE", mode)
@@ -298,7 +299,9 @@ def test_wave_gathers_with_and_without_earlier_scores(octex, small_index, monkey
     Db, Ib = b.search(Q, k=10, **params)
     _, cnt0 = b.profile_batch(Q, k=10, reps=1, **params)
     assert np.array_equal(Ia, Ib) and np.array_equal(Da, Db)
-    assert all(k > 0 for k in cnt["known2"][:3]) and all(o > 0 for o in cnt["oldread2"][:3])
+    used = 3 if mode != "1" else 1  # the waves that read earlier rows
+    assert all(k > 0 for k in cnt["known2"][:used]) and all(o > 0 for o in cnt["oldread2"][:used])
+    assert sum(cnt["known2"][used:]) == 0 and sum(cnt["oldread2"][used:]) == 0
     assert sum(cnt0["known2"]) == 0 and sum(cnt0["oldread2"]) == 0
     assert cnt["distinct2"][:3] == cnt0["distinct2"][:3]
 
