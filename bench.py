@@ -29,7 +29,9 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor figure
 
 # Cell lists, per workload (every BENCH line records its index parameters in config.index):
-# - sift1m and gist1m: exact lists, as the reference's paper builds (bench/paper_build.sh:29-30, --exact-lists);
+# - sift1m: exact lists, as the reference's paper builds (bench/paper_build.sh:29, --exact-lists): 818 s to build here;
+# - gist1m: member lists.  The paper's exact lists (bench/paper_build.sh:30) took 850 s for 80 of the 150 copies here,
+#   about 27 minutes in all, more than one GPU session allows; member lists hold members of the query's cell;
 # - deep100m and deep100m-host: member lists, the reference's fast build mode (--member-lists).  The paper's Deep100M
 #   build uses the default IVF lists (bench/paper_build.sh:36), whose k-means and probed list search over 100M rows for
 #   every copy do not fit a GPU session here; member lists hold members of the query's cell instead of the rows
@@ -64,13 +66,13 @@ CONFIGS = {
                           point=dict(read=16, starts=128, waves=3, rerank=128, wave_rerank=128, sketch_rank=True,
                                      final_rerank=32)),
     # configs[2] of BASELINE.json: 1M x 960 non-negative half-normal features (scale 0.05) plus per-cluster offsets
-    # U[0, 0.1] of a 1,000-component mixture, 1,000 queries, batch 1,000; the index as the reference's paper GIST
-    # build (lists of 64, exact lists, sketch 128, exact table of 64, no reverse edges) with 150 copies (the paper's
-    # 400 do not fit next to this index's arrays: 0.70 GB a copy)
+    # U[0, 0.1] of a 1,000-component mixture, 1,000 queries, batch 1,000; the index shaped as the reference's paper
+    # GIST build (lists of 64, sketch 128, exact table of 64, no reverse edges) with member lists of cells of >= 16
+    # rows (see above) and 150 copies (the paper's 400 do not fit next to this index's arrays: 0.70 GB a copy)
     "gist1m": dict(n=1_000_000, d=960, nq=1_000, clusters=1000, kind="gist", batch=1_000,
                    desc="seeded half-normal mixture as BASELINE.json configs[2]",
-                   index=dict(copies=150, list_len=64, table_len=64, sketch_width=128, reverse_edges=False,
-                              exact_lists=True, seed=0),
+                   index=dict(copies=150, list_len=64, min_cell=16, table_len=64, sketch_width=128,
+                              reverse_edges=False, member_lists=True, seed=0),
                    point=dict(read=32, starts=64, waves=3, rerank=512, wave_rerank=512)),
     # configs[0] of BASELINE.json, the reference's CPU-runnable case: 100k rows, d = 128, of a 100-component
     # Gaussian mixture (centroids N(0, 1), sigma 0.3), 1,000 queries, the reference's default index (200 copies,

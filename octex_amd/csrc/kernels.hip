@@ -971,10 +971,10 @@ __device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, c
 constexpr int kKnown = static_cast<int>(0x80000000u);  // a hash-set entry whose id's score came from an earlier row
 
 /**
- * The entries of a query's earlier rows (earlier_rows, at most two) as one sequence: entry e is row 0's e-th while
+ * The entries of a query's earlier rows (earlier_rows, one or two) as one sequence: entry e is row 0's e-th while
  * e < no0, then row 1's.  load() reads entry e from an in-bounds address whatever e is (a row's W slots exist whatever
- * its count; without earlier rows, the fallback row) and returns whether the entry exists; the loaded values are not
- * used before the caller uses them, so the loads stay in flight.
+ * its count) and returns whether the entry exists; nothing derived from the loaded values is computed before the
+ * caller uses them, so the loads stay in flight.
  */
 struct earlier_entries {
   const int* c0;
@@ -983,15 +983,8 @@ struct earlier_entries {
   const float* d1;
   int W0, W1, no0, no1;
 
-  __device__ earlier_entries(earlier_rows const& er, int q, const int* fc, const float* fd, int fW)
+  __device__ earlier_entries(earlier_rows const& er, int q)
   {
-    if (er.count == 0) {  // no rows: the fallback row (the query's own), never taken
-      c0 = c1 = fc;
-      d0 = d1 = fd;
-      W0 = W1 = fW;
-      no0 = no1 = 0;
-      return;
-    }
     const int r1 = er.count > 1 ? 1 : 0;  // one row: row 1 is row 0, never taken (no1 = 0)
     c0  = er.cand[0] + static_cast<int64_t>(q) * er.W[0];
     d0  = er.dist[0] + static_cast<int64_t>(q) * er.W[0];
@@ -1133,7 +1126,7 @@ __global__ __launch_bounds__(kRows ? kGatherRowThreads : kGatherListThreads) voi
   bool pok[kKnownPre] = {};
   if constexpr (kRows && kLdsSlots) {
     if (reuse) {  // uniform
-      const earlier_entries ee(er, q, crow, drow, W);
+      const earlier_entries ee(er, q);
 #pragma unroll
       for (int u = 0; u < kKnownPre; u++)
         pok[u] = ee.load(threadIdx.x + u * kGatherRowThreads, pid[u], psc[u]);
@@ -1147,8 +1140,7 @@ __global__ __launch_bounds__(kRows ? kGatherRowThreads : kGatherListThreads) voi
   int nu = n;  // the candidates scored here
   if constexpr (kRows && kLdsSlots) {
     if (reuse && cs.cnt <= cap)  // uniform (read after the collection's last barrier)
-      nu = take_known<kGatherRowThreads>(earlier_entries(er, q, crow, drow, W), pid, psc, pok, N, n, ht, cs.hts, cl,
-                                         crow, drow, cs);
+      nu = take_known<kGatherRowThreads>(earlier_entries(er, q), pid, psc, pok, N, n, ht, cs.hts, cl, crow, drow, cs);
   }
   if (nknown != nullptr && threadIdx.x == 0) nknown[q] = n - nu;
   sketch_scores<LR>(
@@ -1421,7 +1413,8 @@ __host__ __device__ constexpr auto keys_per_thread(int keys, int threads) -> int
   return keys <= threads ? 1 : keys <= 2 * threads ? 2 : keys <= 4 * threads ? 4 : 8;
 }
 
-constexpr int kRerankThreads = 128;  // rerank_keep_kernel's workgroup: one query
+constexpr int kRerankThreads = 128;         // rerank_keep_kernel's workgroup: one query
+constexpr int64_t kWideRerank = int64_t{1} << 15;  // R D from which a query takes 256 threads
 constexpr int kHistWindow    = 256;  // the most recent history entries a round skips (earlier ones are reranked again)
 
 /** Slots of the set of a round's history window (hoff entries before it): a power of two at least twice the window,
@@ -2235,25 +2228,33 @@ void launch_rerank_keep(const int* cand, const float* dist, const int* nin, int 
   OCTEX_EXPECTS(D % 2 == 0, "octex: the dimension must be even");
   OCTEX_EXPECTS(hoff >= 0 && (hist != nullptr || (hoff == 0 && !hstore)) && (!hstore || hoff + R <= H) && hoff <= H,
                 "octex: the selected-id history must hold this round's offset and ids");
-  // 128 threads a query (16 queries in flight per CU).  Measured at 100M rows with the history skip: the waves'
-  // launches 0.155 / 0.125 ms on 256 threads (twice the keys held in registers), 0.141 / 0.096 ms on 128
-  constexpr int NT  = kRerankThreads;
+  // 128 threads a query (16 queries in flight per CU): measured at 100M rows with the history skip, the waves'
+  // launches 0.155 / 0.125 ms on 256 threads, 0.141 / 0.096 ms on 128.  Rounds of many long rows (R D >= 2^15: 512
+  // rows of 960 at gist1m) take 256, twice the rows in flight
+  const int nt      = static_cast<int64_t>(R) * D >= kWideRerank ? 256 : kRerankThreads;
   const int hslots  = !fresh && hoff > 0 ? hist_slots(hoff) : 0;
-  const size_t smem = rerank_lds_bytes(R, KO, D, NT, hslots);
-  const int c       = keys_per_thread(KO + R, NT);
+  const size_t smem = rerank_lds_bytes(R, KO, D, nt, hslots);
+  const int c       = keys_per_thread(KO + R, nt);
   with_lx(D, [&](auto lx) {
     constexpr int LX = decltype(lx)::value;
     auto go          = [&](auto kernel) {
       allow_lds(reinterpret_cast<const void*>(kernel), smem);
-      kernel<<<m, NT, smem, s>>>(cand, dist, nin, W, vectors, D, Q, R, KO, si, sd, fresh, hist, H, hoff, hstore, hslots,
+      kernel<<<m, nt, smem, s>>>(cand, dist, nin, W, vectors, D, Q, R, KO, si, sd, fresh, hist, H, hoff, hstore, hslots,
                                  nskip);
     };
-    switch (c) {
-      case 1: go(&rerank_keep_kernel<LX, NT, 1>); break;
-      case 2: go(&rerank_keep_kernel<LX, NT, 2>); break;
-      case 4: go(&rerank_keep_kernel<LX, NT, 4>); break;
-      default: go(&rerank_keep_kernel<LX, NT, 8>); break;
-    }
+    auto by_c = [&](auto nt_tag) {
+      constexpr int NT = decltype(nt_tag)::value;
+      switch (c) {
+        case 1: go(&rerank_keep_kernel<LX, NT, 1>); break;
+        case 2: go(&rerank_keep_kernel<LX, NT, 2>); break;
+        case 4: go(&rerank_keep_kernel<LX, NT, 4>); break;
+        default: go(&rerank_keep_kernel<LX, NT, 8>); break;
+      }
+    };
+    if (nt == 256)
+      by_c(std::integral_constant<int, 256>{});
+    else
+      by_c(std::integral_constant<int, kRerankThreads>{});
   });
   OCTEX_HIP(hipGetLastError());
 }
