@@ -1574,25 +1574,27 @@ __global__ __launch_bounds__(512) void sketch_keep_kernel(const int* __restrict_
 }
 
 /**
- * A set of up to kPickHash ids in LDS, in buckets of four slots: an id lives in its home bucket (a multiplicative
- * hash) or, when that is full, in the next buckets.  A lookup reads a whole bucket with one 16-byte load.
+ * A set of ids in LDS, in nb buckets of four slots (nb a power of two): an id lives in its home bucket (a
+ * multiplicative hash) or, when that is full, in the next buckets.  A lookup reads a whole bucket with one 16-byte
+ * load.  The set is sized per launch to at least twice the ids it takes (at most kPickHash slots).
  */
 struct id_buckets {
-  static constexpr int kSlots = 4, kBuckets = kPickHash / kSlots;
-  int4 b[kBuckets];
+  static constexpr int kSlots = 4;
+  int4* b;
+  int nb;
 
-  __device__ static unsigned home(long long v)
+  [[nodiscard]] __device__ unsigned home(long long v) const
   {
-    return ((static_cast<unsigned>(v) * kIdHash) >> 7) & (kBuckets - 1);
+    return ((static_cast<unsigned>(v) * kIdHash) >> 7) & static_cast<unsigned>(nb - 1);
   }
-  __device__ void clear()
+  __device__ void clear() const
   {
-    for (int i = threadIdx.x; i < kBuckets; i += blockDim.x)
+    for (int i = threadIdx.x; i < nb; i += blockDim.x)
       b[i] = make_int4(-1, -1, -1, -1);
   }
-  __device__ void insert(int v)
+  __device__ void insert(int v) const
   {
-    for (unsigned h = home(v), p = 0; p < kBuckets; p++, h = (h + 1) & (kBuckets - 1)) {
+    for (unsigned h = home(v), p = 0; p < static_cast<unsigned>(nb); p++, h = (h + 1) & (nb - 1)) {
       int* slot = reinterpret_cast<int*>(&b[h]);
       for (int j = 0; j < kSlots; j++) {
         const int prev = atomicCAS(&slot[j], -1, v);
@@ -1600,9 +1602,9 @@ struct id_buckets {
       }
     }
   }
-  __device__ bool contains(int v) const
+  [[nodiscard]] __device__ bool contains(int v) const
   {
-    for (unsigned h = home(v), p = 0; p < kBuckets; p++, h = (h + 1) & (kBuckets - 1)) {
+    for (unsigned h = home(v), p = 0; p < static_cast<unsigned>(nb); p++, h = (h + 1) & (nb - 1)) {
       const int4 w = b[h];
       if (w.x == v || w.y == v || w.z == v || w.w == v) return true;
       if (w.w == -1) return false;  // a bucket with a free slot ends the run
@@ -1610,6 +1612,15 @@ struct id_buckets {
     return false;
   }
 };
+
+/** Buckets of pick_starts_kernel's set for `off` expanded ids: at least 2 off slots, at most kPickHash. */
+__host__ __device__ constexpr auto pick_buckets(int off) -> int
+{
+  int nb = 4;
+  while (nb * id_buckets::kSlots < 2 * off && nb * id_buckets::kSlots < kPickHash)
+    nb <<= 1;
+  return nb;
+}
 
 /**
  * Start points of a wave (search_kernels.cuh:571-631): the first S kept entries (best first) that no
@@ -1620,10 +1631,11 @@ struct id_buckets {
 __global__ __launch_bounds__(256) void pick_starts_kernel(const long long* __restrict__ si, int KO,
                                                           long long* __restrict__ done, int E,
                                                           int off, int S, int rowlen,
-                                                          int2* __restrict__ seg2)
+                                                          int2* __restrict__ seg2, int nb)
 {
   const int q = blockIdx.x;
-  __shared__ id_buckets seen;
+  extern __shared__ int4 pick_lds[];  // the set's nb buckets (none when off is 0)
+  const id_buckets seen{pick_lds, nb};
   __shared__ unsigned char fresh[kMaxSketchKO];
   const long long* ps = si + static_cast<int64_t>(q) * KO;
   long long* pd       = done + static_cast<int64_t>(q) * E;
@@ -2274,7 +2286,10 @@ void launch_pick_starts(const long long* si, int m, int KO, long long* done, int
   if (m == 0) return;
   OCTEX_EXPECTS(KO <= kMaxSketchKO && off <= kMaxExpanded && off + S <= E,
                 "octex: starts * (waves - 1) <= 6144");
-  pick_starts_kernel<<<m, 256, 0, s>>>(si, KO, done, E, off, S, rowlen, seg2);
+  // the set of the off ids earlier waves expanded, sized to them (a wave's own LDS, so more workgroups per CU)
+  const int nb      = pick_buckets(off);
+  const size_t smem = off > 0 ? static_cast<size_t>(nb) * sizeof(int4) : 0;
+  pick_starts_kernel<<<m, 256, smem, s>>>(si, KO, done, E, off, S, rowlen, seg2, nb);
   OCTEX_HIP(hipGetLastError());
 }
 
