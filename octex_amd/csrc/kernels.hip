@@ -841,9 +841,21 @@ __device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, c
       atomicAdd(&sh.hist[b >> 1], 1u << (16 * (b & 1)));
     }
   }
-  for (int i = tid + kCache * nthr; i < n; i += nthr) {
-    const unsigned b = bin_of(kd[i]);
-    atomicAdd(&sh.hist[b >> 1], 1u << (16 * (b & 1)));
+  // keys past the cache, kPast a thread in flight together (unconditional loads of clamped indices, then a select:
+  // one key at a time waited for each load in turn)
+  constexpr int kPast = 4;
+  for (int i0 = tid + kCache * nthr; i0 < n; i0 += kPast * nthr) {
+    unsigned kv[kPast];
+#pragma unroll
+    for (int u = 0; u < kPast; u++)
+      kv[u] = kd[min(i0 + u * nthr, n - 1)];
+#pragma unroll
+    for (int u = 0; u < kPast; u++) {
+      if (i0 + u * nthr < n) {
+        const unsigned b = bin_of(kv[u]);
+        atomicAdd(&sh.hist[b >> 1], 1u << (16 * (b & 1)));
+      }
+    }
   }
   __syncthreads();
   threshold_bin(sh, static_cast<unsigned>(R));
@@ -878,14 +890,22 @@ __device__ __forceinline__ int select_by_bins(const unsigned* __restrict__ kd, c
     take(ok && b < bstar, ci[j], kr[j]);
     to_tie(ok && b == bstar, ci[j], kr[j]);
   }
-  for (int i0 = kCache * nthr; i0 < n; i0 += nthr) {  // keys past the cache: key and id read together
-    const int i       = i0 + tid;
-    const int ii      = i < n ? i : 0;
-    const unsigned kv = kd[ii];
-    const int id      = cid[ii];
-    const unsigned b  = bin_of(kv);
-    take(i < n && b < bstar, id, kv);
-    to_tie(i < n && b == bstar, id, kv);
+  for (int i0 = kCache * nthr; i0 < n; i0 += kPast * nthr) {  // keys past the cache: kPast keys and ids in flight
+    unsigned kv[kPast];
+    int id[kPast];
+#pragma unroll
+    for (int u = 0; u < kPast; u++) {
+      const int ii = min(i0 + u * nthr + tid, n - 1);
+      kv[u]        = kd[ii];
+      id[u]        = cid[ii];
+    }
+#pragma unroll
+    for (int u = 0; u < kPast; u++) {  // uniform trip counts: the appends use ballots
+      const bool in    = i0 + u * nthr + tid < n;
+      const unsigned b = bin_of(kv[u]);
+      take(in && b < bstar, id[u], kv[u]);
+      to_tie(in && b == bstar, id[u], kv[u]);
+    }
   }
   __syncthreads();
   // every thread reads the count before the passes below reset it (a wave that read it after thread 0's reset would
