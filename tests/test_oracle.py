@@ -348,6 +348,47 @@ def test_rerank_rules_catch_plausible_mistakes():
     assert fails(final("all"))
 
 
+def test_rerank_history_skip_keeps_the_same_lists():
+    """The rule the HIP rerank's history skip rests on, checked with the oracle's functions over four rounds: merging
+    only the selected ids no earlier round selected gives the kept list that reranking every selected id gives (the
+    kept list is the KO smallest distinct keys of every key merged so far, so an id merged before is either in it
+    already or above all KO of it).  Rows repeat earlier rounds' ids with the same sketch scores, as a query's do.
+    Skipping ids selected for the first time (a planted mistake: ids never merged) changes some query's list."""
+    ix, Q, exact, cands, dists, si0, sd0 = rerank_rule_case(m=24, seed=13)
+    g = np.random.default_rng(14)
+    KO, R = 40, 48
+    N = ix.n
+    score = g.permutation(N).astype(np.float32) * np.float32(0.01)  # one sketch score per id and query
+    planted_differs = False
+    for q in range(len(Q)):
+        full_i, full_d = si0[q].copy(), sd0[q].copy()
+        skip_i, skip_d = si0[q].copy(), sd0[q].copy()
+        bad_i, bad_d = si0[q].copy(), sd0[q].copy()
+        seen, never_merged = set(), set()
+        for rnd in range(4):
+            old = np.array(sorted(seen), np.int32)
+            k_old = min(len(old), 150)
+            row = np.concatenate([g.choice(old, k_old, replace=False) if k_old else np.zeros(0, np.int32),
+                                  g.choice(N, 400, replace=False).astype(np.int32)])
+            row = np.unique(row)[g.permutation(len(np.unique(row)))]
+            d = score[row]
+            full_i, full_d = O.rerank_keep(ix, row, d, Q[q], R, full_i, full_d, fresh=False)
+            sel, seld = O.select(row, d, R)
+            keep = np.array([int(v) not in seen for v in sel], bool)
+            skip_i, skip_d = O.rerank_keep(ix, sel[keep], seld[keep], Q[q], max(1, int(keep.sum())), skip_i, skip_d,
+                                           fresh=False)
+            assert np.array_equal(skip_i, full_i) and np.array_equal(skip_d, full_d), f"query {q} round {rnd}"
+            # planted: four of the ids selected for the first time are treated as seen too
+            new_ids = [int(v) for v in sel if int(v) not in seen][:4]
+            never_merged |= set(new_ids)
+            bkeep = np.array([int(v) not in seen and int(v) not in never_merged for v in sel], bool)
+            bad_i, bad_d = O.rerank_keep(ix, sel[bkeep], seld[bkeep], Q[q], max(1, int(bkeep.sum())), bad_i, bad_d,
+                                         fresh=False)
+            planted_differs |= not np.array_equal(bad_i, full_i)
+            seen |= {int(v) for v in sel}
+    assert planted_differs
+
+
 # ---------------------------------------------------------------- index-level stages
 
 
