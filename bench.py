@@ -77,10 +77,11 @@ CONFIGS = {
     # configs[0] of BASELINE.json, the reference's CPU-runnable case: 100k rows, d = 128, of a 100-component
     # Gaussian mixture (centroids N(0, 1), sigma 0.3), 1,000 queries, the reference's default index (200 copies,
     # lists of 64, exact table of 64 with reverse edges) but for log_buckets 16; the search sweep ends at the
-    # default read 32 / starts 128 / waves 2
+    # default read 32 / starts 128 / waves 2.  Its CPU baseline also times the host path the configuration names
+    # (host_path): the CPU oracle builds the index and searches it on the host
     "cpu100k": dict(n=100_000, d=128, nq=1_000, clusters=100, kind="gauss", batch=1_000,
                     desc="seeded Gaussian mixture as BASELINE.json configs[0]",
-                    index=dict(log_buckets=16, seed=0),
+                    index=dict(log_buckets=16, seed=0), host_path=True,
                     point=dict(read=32, starts=128, waves=2, rerank=128, wave_rerank=128)),
     # a small stand-in for quick checks
     "small": dict(n=100_000, d=128, nq=10_000, clusters=100, kind="sift", batch=10_000, desc="small SIFT-like mixture",
@@ -363,6 +364,38 @@ def cpu_passes(n, pool, seconds, target):
     return max(2, int(round(target / max(seconds, 1e-3))))
 
 
+def host_path(X, Q, k, index, params, threads, log=lambda *a: None):
+    """configs[0]'s CPU path, build and search both on the host: the oracle's builder writes an index of X (member
+    lists: the CPU builder has no k-means lists; every other parameter as `index`, the workload's), the oracle
+    searches all of Q with `params`, and I and D are checked against fp64 brute force over the fp16 rows."""
+    import shutil
+    import tempfile
+
+    from oracle import oracle as O
+
+    kw = dict(copies=200, list_len=64, table_len=64, log_buckets=20, reverse_edges=True, seed=0)
+    kw.update({key: v for key, v in index.items() if key in kw or key in ("min_cell", "sketch_width", "blocks")})
+    kw.update(member_lists=True, exact_lists=False)
+    tmp = tempfile.mkdtemp(prefix="octex_host_")
+    try:
+        t0 = time.time()
+        O.build(X, tmp, threads=threads, **kw)
+        build_s = time.time() - t0
+        log(f"host build: {build_s:.1f} s on {threads} threads")
+        oix = O.Index(tmp)
+        t0 = time.time()
+        D, I = O.search(oix, Q, k=k, threads=threads, **params)
+        search_s = time.time() - t0
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    x16 = np.asarray(X, np.float16).astype(np.float32)
+    _, gt = O.bruteforce(x16, Q, k, threads=threads)
+    return dict(build_seconds=round(build_s, 1), search_seconds=round(search_s, 3),
+                value=round(len(Q) / search_s, 1), unit="queries/s", threads=threads, index=kw, search=params,
+                recall=round(recall(I, gt, k), 4), distance_max_rel_err=distance_error(X, Q, D, I),
+                truth="fp64 brute force over the fp16 rows")
+
+
 def host_cpu():
     """The host's CPU model, its logical CPU count, the CPUs this process may run on, and the threads the CPU
     baseline uses: every CPU it may run on, at most 16 (the host share of one GPU on the GPU boxes here, whatever
@@ -446,6 +479,9 @@ def main():
     ap.add_argument("--config", default="deep100m", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU time of the CPU-baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--host-path", action="store_true",
+                    help="also build the index with the CPU oracle and search it on the host (cpu_baseline.host_path; "
+                         "the default of --config cpu100k, configs[0]'s CPU path)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also copy 1 GiB device to device inside the profiled region (the known-size kernel that "
                          "scales rocprof's FETCH_SIZE / WRITE_SIZE counters to bytes)")
@@ -622,6 +658,8 @@ def main():
                           + (" (list rows copied for these queries only)" if big else ""),
                    recall=round(recall(Ic, gt[:n_s]), 4), nproc=host["nproc"], affinity=host["affinity"],
                    cpu_model=host["model"], threads_rule=host["rule"])
+        if cfg.get("host_path") or args.host_path:  # configs[0]: build and search both on the host
+            cpu["host_path"] = host_path(X, Q, k, cfg["index"], params, threads, log=log)
         log(f"cpu baseline: {cpu}")
 
     out = {

@@ -11,7 +11,9 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <exception>
 #include <fstream>
+#include <immintrin.h>
 #include <numeric>
 #include <random>
 #include <sstream>
@@ -814,22 +816,66 @@ int orc_search(const orc_index* ix, const orc_search_params* sp, const float* q,
 void orc_bruteforce(const float* x, int64_t n, const float* q, int64_t m, int64_t d, int k,
                     int64_t* I, float* D, int threads)
 {
-  parallel_rows(m, threads, [&](int64_t r0, int64_t r1, int) {
-    std::vector<std::pair<double, int64_t>> all(n);
-    for (int64_t r = r0; r < r1; r++) {
-      for (int64_t i = 0; i < n; i++) {
-        double acc = 0;
-        for (int64_t j = 0; j < d; j++) {
-          double t = double(x[i * d + j]) - double(q[r * d + j]);
-          acc += t * t;
-        }
-        all[i] = {acc, i};
+  // blocks of kQ queries share each pass over the rows, their fp64 sums four to an AVX register (a multiply, then
+  // an add: the same roundings as one query at a time); every query keeps its k smallest (distance, id) pairs in a
+  // max-heap, which holds what a partial sort of all n pairs puts first (the pairs are distinct by id)
+  constexpr int kQ     = 16;
+  const int kk         = static_cast<int>(std::min<int64_t>(k, n));
+  const int64_t blocks = (m + kQ - 1) / kQ;
+  parallel_rows(blocks, threads, [&](int64_t b0, int64_t b1, int) {
+    std::vector<std::pair<double, int64_t>> best[kQ];
+    std::vector<double> qb(static_cast<size_t>(d) * kQ);  // [d][kQ]
+    alignas(32) double acc[kQ];
+    for (int64_t bq = b0; bq < b1; bq++) {
+      const int64_t r0 = bq * kQ;
+      const int nr     = static_cast<int>(std::min<int64_t>(kQ, m - r0));
+      for (int t = 0; t < kQ; t++) {
+        const float* qt = q + (r0 + std::min(t, nr - 1)) * d;
+        for (int64_t j = 0; j < d; j++)
+          qb[j * kQ + t] = double(qt[j]);
+        best[t].clear();
       }
-      int kk = static_cast<int>(std::min<int64_t>(k, n));
-      std::partial_sort(all.begin(), all.begin() + kk, all.end());
-      for (int j = 0; j < k; j++) {
-        I[r * k + j] = j < kk ? all[j].second : -1;
-        D[r * k + j] = j < kk ? static_cast<float>(all[j].first) : INFINITY;
+      for (int64_t i = 0; i < n; i++) {
+        const float* xi = x + i * d;
+        __m256d a0 = _mm256_setzero_pd(), a1 = _mm256_setzero_pd();
+        __m256d a2 = _mm256_setzero_pd(), a3 = _mm256_setzero_pd();
+        for (int64_t j = 0; j < d; j++) {
+          const __m256d xj = _mm256_set1_pd(double(xi[j]));
+          const double* qj = qb.data() + j * kQ;
+          const __m256d u0 = _mm256_sub_pd(xj, _mm256_loadu_pd(qj));
+          const __m256d u1 = _mm256_sub_pd(xj, _mm256_loadu_pd(qj + 4));
+          const __m256d u2 = _mm256_sub_pd(xj, _mm256_loadu_pd(qj + 8));
+          const __m256d u3 = _mm256_sub_pd(xj, _mm256_loadu_pd(qj + 12));
+          a0 = _mm256_add_pd(a0, _mm256_mul_pd(u0, u0));
+          a1 = _mm256_add_pd(a1, _mm256_mul_pd(u1, u1));
+          a2 = _mm256_add_pd(a2, _mm256_mul_pd(u2, u2));
+          a3 = _mm256_add_pd(a3, _mm256_mul_pd(u3, u3));
+        }
+        _mm256_store_pd(acc, a0);
+        _mm256_store_pd(acc + 4, a1);
+        _mm256_store_pd(acc + 8, a2);
+        _mm256_store_pd(acc + 12, a3);
+        for (int t = 0; t < nr; t++) {
+          auto& h = best[t];
+          const std::pair<double, int64_t> e{acc[t], i};
+          if (static_cast<int>(h.size()) < kk) {
+            h.push_back(e);
+            std::push_heap(h.begin(), h.end());
+          } else if (kk > 0 && e < h.front()) {
+            std::pop_heap(h.begin(), h.end());
+            h.back() = e;
+            std::push_heap(h.begin(), h.end());
+          }
+        }
+      }
+      for (int t = 0; t < nr; t++) {
+        auto& h = best[t];
+        std::sort_heap(h.begin(), h.end());
+        const int64_t r = r0 + t;
+        for (int j = 0; j < k; j++) {
+          I[r * k + j] = j < kk ? h[j].second : -1;
+          D[r * k + j] = j < kk ? static_cast<float>(h[j].first) : INFINITY;
+        }
       }
     }
   });
@@ -837,7 +883,8 @@ void orc_bruteforce(const float* x, int64_t n, const float* q, int64_t m, int64_
 
 /*
  * The small builder (build.cu:104-426; build_setup.cuh:40-175; build_cells.cuh:61-613;
- * build_table.cuh:157-554), single threaded, for test indexes of a few thousand vectors.
+ * build_table.cuh:157-554), its copies and table rows over host threads, for test indexes and the host build of
+ * the 100k-row CPU workload.
  * Lists: exact (brute force in the projection) or from cell members (build_cells.cuh:176-250); the
  * reference's IVF-Flat default is approximate, exact lists stand in for it here.
  */
@@ -933,107 +980,119 @@ int orc_build(const float* xin, int64_t n, int64_t d, const orc_build_params* p,
     std::vector<std::vector<int32_t>> offs(C);
     std::vector<int32_t> base(static_cast<size_t>(C) * L);
     std::vector<int64_t> ncells(static_cast<size_t>(C) * L);
-    std::vector<float> y(static_cast<size_t>(n) * w);
-    std::vector<float> xc(d);
-    for (int c = 0; c < C; c++) {
-      const float* u = proj.data() + static_cast<size_t>(c) * d * w;
-      for (int64_t i = 0; i < n; i++) {
-        for (int64_t j = 0; j < d; j++)
-          xc[j] = x[i * d + j] - mean[j];
-        for (int s = 0; s < w; s++) {
-          float acc = 0.f;
-          for (int64_t j = 0; j < d; j++)
-            acc = std::fma(xc[j], u[j * w + s], acc);
-          y[i * w + s] = acc + shift[static_cast<size_t>(c) * w + s];
-        }
-      }
-      int64_t row = 0;
-      offs[c].assign(static_cast<size_t>(L) * (T + 1), 0);
-      for (int j = 0; j < L; j++) {
-        const float f = spac[j];
-        std::vector<std::pair<int64_t, int32_t>> hv(n);
-        std::vector<float> yf(w);
-        for (int64_t i = 0; i < n; i++) {
-          for (int s = 0; s < w; s++)
-            yf[s] = y[i * w + s] / f;  // division, as build_cells.cuh:69-71
-          hv[i] = {e8b_hash64(yf.data(), b, 1.0f), static_cast<int32_t>(i)};
-        }
-        std::sort(hv.begin(), hv.end());
-        struct cell {
-          int64_t key;
-          int32_t start, pop;
-        };
-        std::vector<cell> cells;
-        for (int64_t i = 0; i < n;) {
-          int64_t e = i;
-          while (e < n && hv[e].first == hv[i].first)
-            e++;
-          int32_t pop = static_cast<int32_t>(e - i);
-          if (!(p->min_cell > 1 && j < L - 1 && pop < p->min_cell))
-            cells.push_back({hv[i].first, static_cast<int32_t>(i), pop});
-          i = e;
-        }
-        const int64_t M = static_cast<int64_t>(cells.size());
-        std::vector<int32_t> lst(static_cast<size_t>(M) * l);
-        std::vector<float> z(w);
-        std::vector<std::pair<float, int32_t>> cand;
-        for (int64_t ci = 0; ci < M; ci++) {
-          // center: f times the E8 point of the first member / f (build_cells.cuh:86-103)
-          const float* r0 = y.data() + int64_t{hv[cells[ci].start].second} * w;
-          for (int jb = 0; jb < b; jb++) {
-            float xx[8], pp[8];
-            for (int kk = 0; kk < 8; kk++)
-              xx[kk] = r0[8 * jb + kk] / f;
-            e8_point(xx, pp);
-            for (int kk = 0; kk < 8; kk++)
-              z[8 * jb + kk] = pp[kk] * f;
-          }
-          cand.clear();
-          auto dist_to = [&](int32_t r) {
-            float dd = 0.f;
+    // the copies are independent (each writes its own lists, keys, offsets, bases and counts): threads take
+    // contiguous ranges of them, and the files are the same for any thread count
+    const int nth = std::max(1, p->threads);
+    std::vector<std::exception_ptr> fail(nth);
+    parallel_rows(C, nth, [&](int64_t c0, int64_t c1, int th) {
+      try {
+        std::vector<float> y(static_cast<size_t>(n) * w);
+        std::vector<float> xc(d);
+        for (int c = static_cast<int>(c0); c < c1; c++) {
+          const float* u = proj.data() + static_cast<size_t>(c) * d * w;
+          for (int64_t i = 0; i < n; i++) {
+            for (int64_t j = 0; j < d; j++)
+              xc[j] = x[i * d + j] - mean[j];
             for (int s = 0; s < w; s++) {
-              float e = y[int64_t{r} * w + s] - z[s];
-              dd      = std::fma(e, e, dd);
+              float acc = 0.f;
+              for (int64_t j = 0; j < d; j++)
+                acc = std::fma(xc[j], u[j * w + s], acc);
+              y[i * w + s] = acc + shift[static_cast<size_t>(c) * w + s];
             }
-            return dd;
-          };
-          if (p->member_lists || !p->exact_lists) {
-            for (int32_t t = 0; t < cells[ci].pop; t++) {
-              int32_t r = hv[cells[ci].start + t].second;
-              cand.push_back({dist_to(r), r});
-            }
-          } else {
-            for (int32_t r = 0; r < n; r++)
-              cand.push_back({dist_to(r), r});
           }
-          int kk = std::min<int>(l, static_cast<int>(cand.size()));
-          std::partial_sort(cand.begin(), cand.begin() + kk, cand.end());
-          for (int t = 0; t < l; t++)  // fewer than l members: the nearest repeats (octex.hpp:62-68)
-            lst[ci * l + t] = cand[t < kk ? t : 0].second;
+          int64_t row = 0;
+          offs[c].assign(static_cast<size_t>(L) * (T + 1), 0);
+          for (int j = 0; j < L; j++) {
+            const float f = spac[j];
+            std::vector<std::pair<int64_t, int32_t>> hv(n);
+            std::vector<float> yf(w);
+            for (int64_t i = 0; i < n; i++) {
+              for (int s = 0; s < w; s++)
+                yf[s] = y[i * w + s] / f;  // division, as build_cells.cuh:69-71
+              hv[i] = {e8b_hash64(yf.data(), b, 1.0f), static_cast<int32_t>(i)};
+            }
+            std::sort(hv.begin(), hv.end());
+            struct cell {
+              int64_t key;
+              int32_t start, pop;
+            };
+            std::vector<cell> cells;
+            for (int64_t i = 0; i < n;) {
+              int64_t e = i;
+              while (e < n && hv[e].first == hv[i].first)
+                e++;
+              int32_t pop = static_cast<int32_t>(e - i);
+              if (!(p->min_cell > 1 && j < L - 1 && pop < p->min_cell))
+                cells.push_back({hv[i].first, static_cast<int32_t>(i), pop});
+              i = e;
+            }
+            const int64_t M = static_cast<int64_t>(cells.size());
+            std::vector<int32_t> lst(static_cast<size_t>(M) * l);
+            std::vector<float> z(w);
+            std::vector<std::pair<float, int32_t>> cand;
+            for (int64_t ci = 0; ci < M; ci++) {
+              // center: f times the E8 point of the first member / f (build_cells.cuh:86-103)
+              const float* r0 = y.data() + int64_t{hv[cells[ci].start].second} * w;
+              for (int jb = 0; jb < b; jb++) {
+                float xx[8], pp[8];
+                for (int kk = 0; kk < 8; kk++)
+                  xx[kk] = r0[8 * jb + kk] / f;
+                e8_point(xx, pp);
+                for (int kk = 0; kk < 8; kk++)
+                  z[8 * jb + kk] = pp[kk] * f;
+              }
+              cand.clear();
+              auto dist_to = [&](int32_t r) {
+                float dd = 0.f;
+                for (int s = 0; s < w; s++) {
+                  float e = y[int64_t{r} * w + s] - z[s];
+                  dd      = std::fma(e, e, dd);
+                }
+                return dd;
+              };
+              if (p->member_lists || !p->exact_lists) {
+                for (int32_t t = 0; t < cells[ci].pop; t++) {
+                  int32_t r = hv[cells[ci].start + t].second;
+                  cand.push_back({dist_to(r), r});
+                }
+              } else {
+                for (int32_t r = 0; r < n; r++)
+                  cand.push_back({dist_to(r), r});
+              }
+              int kk = std::min<int>(l, static_cast<int>(cand.size()));
+              std::partial_sort(cand.begin(), cand.begin() + kk, cand.end());
+              for (int t = 0; t < l; t++)  // fewer than l members: the nearest repeats (octex.hpp:62-68)
+                lst[ci * l + t] = cand[t < kk ? t : 0].second;
+            }
+            // (bucket, hash) order, CSR over buckets (build_cells.cuh:387-448)
+            std::vector<int64_t> order(M);
+            std::iota(order.begin(), order.end(), 0);
+            std::stable_sort(order.begin(), order.end(), [&](int64_t a2, int64_t b2) {
+              return (cells[a2].key & (T - 1)) < (cells[b2].key & (T - 1));
+            });
+            int32_t* o = offs[c].data() + static_cast<size_t>(j) * (T + 1);
+            std::vector<int64_t> cnt(T + 1, 0);
+            for (int64_t ci = 0; ci < M; ci++) {
+              keys[c].push_back(cells[order[ci]].key);
+              for (int t = 0; t < l; t++)
+                lists[c].push_back(lst[order[ci] * l + t]);
+              cnt[(cells[order[ci]].key & (T - 1)) + 1]++;
+            }
+            for (int64_t t = 0; t < T; t++)
+              cnt[t + 1] += cnt[t];
+            for (int64_t t = 0; t <= T; t++)
+              o[t] = static_cast<int32_t>(cnt[t]);
+            base[static_cast<size_t>(c) * L + j]   = static_cast<int32_t>(row);
+            ncells[static_cast<size_t>(c) * L + j] = M;
+            row += M;
+          }
         }
-        // (bucket, hash) order, CSR over buckets (build_cells.cuh:387-448)
-        std::vector<int64_t> order(M);
-        std::iota(order.begin(), order.end(), 0);
-        std::stable_sort(order.begin(), order.end(), [&](int64_t a2, int64_t b2) {
-          return (cells[a2].key & (T - 1)) < (cells[b2].key & (T - 1));
-        });
-        int32_t* o = offs[c].data() + static_cast<size_t>(j) * (T + 1);
-        std::vector<int64_t> cnt(T + 1, 0);
-        for (int64_t ci = 0; ci < M; ci++) {
-          keys[c].push_back(cells[order[ci]].key);
-          for (int t = 0; t < l; t++)
-            lists[c].push_back(lst[order[ci] * l + t]);
-          cnt[(cells[order[ci]].key & (T - 1)) + 1]++;
-        }
-        for (int64_t t = 0; t < T; t++)
-          cnt[t + 1] += cnt[t];
-        for (int64_t t = 0; t <= T; t++)
-          o[t] = static_cast<int32_t>(cnt[t]);
-        base[static_cast<size_t>(c) * L + j]   = static_cast<int32_t>(row);
-        ncells[static_cast<size_t>(c) * L + j] = M;
-        row += M;
+      } catch (...) {
+        fail[th] = std::current_exception();
       }
-    }
+    });
+    for (auto& e : fail)
+      if (e) std::rethrow_exception(e);
     int64_t lmax = 0, mmax = 0;
     for (int c = 0; c < C; c++) {
       lmax = std::max<int64_t>(lmax, lists[c].size());
@@ -1096,7 +1155,7 @@ int orc_build(const float* xin, int64_t n, int64_t d, const orc_build_params* p,
       std::vector<float> fd(static_cast<size_t>(n) * k);
       std::vector<int64_t> I(static_cast<size_t>(n) * (k + 1));
       std::vector<float> Dd(static_cast<size_t>(n) * (k + 1));
-      orc_bruteforce(x.data(), n, x.data(), n, d, k + 1, I.data(), Dd.data(), 8);
+      orc_bruteforce(x.data(), n, x.data(), n, d, k + 1, I.data(), Dd.data(), nth);
       for (int64_t i = 0; i < n; i++) {  // drop_self_kernel (build_table.cuh:60-74)
         int t = 0;
         for (int j = 0; j <= k && t < k; j++) {

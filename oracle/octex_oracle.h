@@ -128,6 +128,7 @@ typedef struct {
   int32_t list_len, min_cell, log_buckets, sketch_width, table_len;
   int32_t reverse_edges, exact_lists, member_lists;
   uint64_t seed;
+  int32_t threads; /* host threads over copies and table rows (< 1: one); the files do not depend on it */
 } orc_build_params;
 
 /** Build an index of x [n, d] (fp32, rounded to fp16 first as build.cu:434-441) into `path`. */

@@ -82,6 +82,7 @@ class OrcBuildParams(ct.Structure):
         ("exact_lists", ct.c_int32),
         ("member_lists", ct.c_int32),
         ("seed", ct.c_uint64),
+        ("threads", ct.c_int32),
     ]
 
 
@@ -488,8 +489,9 @@ def bruteforce(x, q, k, threads=8):
 
 
 def build(x, path, copies=8, blocks=4, pca_dims=64, spacings=None, list_len=64, min_cell=1, log_buckets=20,
-          sketch_width=0, table_len=64, reverse_edges=True, exact_lists=False, member_lists=False, seed=0):
-    """The oracle's small CPU builder: writes a format-1 index directory at `path`."""
+          sketch_width=0, table_len=64, reverse_edges=True, exact_lists=False, member_lists=False, seed=0, threads=8):
+    """The oracle's small CPU builder: writes a format-1 index directory at `path` (copies and table rows over
+    `threads` host threads; the files do not depend on the count)."""
     x = _c(x, np.float32)
     sp = np.array(spacings if spacings is not None else [2.0, 2.5, 3.2, 4.0, 5.0], np.float32)
     p = OrcBuildParams()
@@ -497,6 +499,7 @@ def build(x, path, copies=8, blocks=4, pca_dims=64, spacings=None, list_len=64, 
     p.spacings, p.n_spacings = sp.ctypes.data, len(sp)
     p.list_len, p.min_cell, p.log_buckets, p.sketch_width, p.table_len = list_len, min_cell, log_buckets, sketch_width, table_len
     p.reverse_edges, p.exact_lists, p.member_lists, p.seed = int(reverse_edges), int(exact_lists), int(member_lists), seed
+    p.threads = threads
     os.makedirs(path, exist_ok=True)
     rc = lib().orc_build(_p(x), ct.c_int64(x.shape[0]), ct.c_int64(x.shape[1]), ct.byref(p), os.fsencode(path))
     if rc != 0:

@@ -92,3 +92,18 @@ def test_cpu_passes():
     assert bench.cpu_passes(1000, 1000, 2.4, 15.0) == 6
     assert bench.cpu_passes(1000, 1000, 7.4, 15.0) == 2
     assert bench.cpu_passes(1000, 1000, 0.0, 15.0) > 1000
+
+
+def test_host_path():
+    """configs[0]'s CPU path on a small mixture: the oracle builds with the workload's index parameters (member
+    lists), searches every query on the host, and the result is checked against fp64 brute force."""
+    cfg = dict(bench.CONFIGS["cpu100k"], n=4000, nq=64)
+    assert cfg["host_path"]
+    X, Q = bench.make_gauss(cfg)
+    index = dict(cfg["index"], copies=16, list_len=32, table_len=32, log_buckets=12)
+    point = dict(cfg["point"], batch=64)
+    r = bench.host_path(X, Q, 10, index, point, threads=4)
+    assert r["index"]["member_lists"] and not r["index"]["exact_lists"] and r["index"]["copies"] == 16
+    assert r["index"]["log_buckets"] == 12 and r["search"] == point and r["threads"] == 4
+    assert r["build_seconds"] >= 0 and r["value"] > 0 and r["unit"] == "queries/s"
+    assert r["recall"] >= 0.95 and r["distance_max_rel_err"] < 1e-3

@@ -790,3 +790,34 @@ def test_exact_list_check_catches_member_lists(tmp_path):
     O.build(X, str(tmp_path / "m"), copies=2, list_len=16, table_len=8, log_buckets=10, member_lists=True, seed=5)
     with pytest.raises(AssertionError):
         check_exact_lists(str(tmp_path / "m"), X)
+
+
+@pytest.mark.parametrize("lists", ["member_lists", "exact_lists"])
+def test_oracle_build_files_do_not_depend_on_threads(tmp_path, lists):
+    """The CPU builder splits its copies and table rows over threads: one thread and three threads over seven
+    copies (uneven ranges) write byte-identical files."""
+    X, _ = clustered(n=1200, m=10, d=32, clusters=10, seed=4)
+    kw = dict(copies=7, list_len=16, table_len=12, log_buckets=10, min_cell=2, seed=3, **{lists: True})
+    O.build(X, str(tmp_path / "one"), threads=1, **kw)
+    O.build(X, str(tmp_path / "three"), threads=3, **kw)
+    names = sorted(os.listdir(tmp_path / "one"))
+    assert names == sorted(os.listdir(tmp_path / "three")) and "lists.npy" in names and "table.npy" in names
+    for name in names:
+        assert (tmp_path / "one" / name).read_bytes() == (tmp_path / "three" / name).read_bytes(), name
+
+
+@pytest.mark.parametrize("n,m,k,d", [(50, 37, 70, 8), (1000, 33, 17, 5), (2000, 100, 64, 128), (16, 1, 16, 1)])
+def test_bruteforce_matches_a_sort_of_all_distances(n, m, k, d):
+    """The brute force (16 queries a pass, heaps of the k smallest) equals a lexicographic sort of all (distance,
+    id) pairs: integer rows (exact fp64 sums, many ties broken by id), fewer rows than k (padded with -1 and inf),
+    query counts that are not multiples of 16."""
+    g = np.random.default_rng(n + m)
+    X = g.integers(-2, 3, (n, d)).astype(np.float32)
+    Q = g.integers(-2, 3, (m, d)).astype(np.float32)
+    D, I = O.bruteforce(X, Q, k, threads=3)
+    d2 = ((Q[:, None, :].astype(np.float64) - X[None, :, :]) ** 2).sum(-1)
+    kk = min(k, n)
+    for r in range(m):
+        order = np.lexsort((np.arange(n), d2[r]))[:kk]
+        assert (I[r, :kk] == order).all() and (D[r, :kk] == d2[r, order].astype(np.float32)).all()
+        assert (I[r, kk:] == -1).all() and np.isinf(D[r, kk:]).all()
