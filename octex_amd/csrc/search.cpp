@@ -293,9 +293,11 @@ auto make_plan(index_impl& ix, search_params const& sp, int m, int k) -> std::sh
   carve_buffers(ix, pl->shape, pl->block.ptr, &pl->buf);
   OCTEX_HIP(hipEventCreateWithFlags(&pl->ev_in, hipEventDisableTiming));
   OCTEX_HIP(hipEventCreateWithFlags(&pl->ev_out, hipEventDisableTiming));
-  // one eager run on zeroed buffers (code objects loaded, LDS limits set), then the capture of the whole batch
+  // one eager run on zeroed buffers (code objects loaded, LDS limits set), then the capture of the whole batch.
+  // Only the index's own stream is drained first: the index arrays were complete when its load or build returned,
+  // and other streams (another index's searches) are not waited for
   hipStream_t s = ix.stream;
-  OCTEX_HIP(hipDeviceSynchronize());
+  OCTEX_HIP(hipStreamSynchronize(s));
   OCTEX_HIP(hipMemsetAsync(pl->block.ptr, 0, pl->block.size, s));
   launch_batch(ix, pl->shape, pl->buf, s);
   OCTEX_HIP(hipStreamSynchronize(s));
