@@ -74,20 +74,31 @@ auto to_cpp(cuvsOctexIndexParams const& p) -> octex::index_params
   return out;
 }
 
+// A C caller can store any int in an enum field; reading it as the C++ enum type is undefined for values outside
+// the enumeration, so the fields are read as the ints they are
+template <typename E>
+auto enum_value(E const& field) -> int
+{
+  static_assert(sizeof(E) == sizeof(int), "C enums are int-sized");
+  int v = 0;
+  std::memcpy(&v, &field, sizeof v);
+  return v;
+}
+
 auto to_cpp(cuvsOctexLoadParams const& p) -> octex::load_params
 {
-  OCTEX_EXPECTS(p.placement == OCTEX_PLACEMENT_REPLICATE || p.placement == OCTEX_PLACEMENT_SHARD,
+  const int placement = enum_value(p.placement), sketch = enum_value(p.sketch);
+  OCTEX_EXPECTS(placement == OCTEX_PLACEMENT_REPLICATE || placement == OCTEX_PLACEMENT_SHARD,
                 "octex: unknown placement");
-  OCTEX_EXPECTS(p.sketch == OCTEX_SKETCH_REPLICATE || p.sketch == OCTEX_SKETCH_SHARD ||
-                  p.sketch == OCTEX_SKETCH_HOST,
+  OCTEX_EXPECTS(sketch == OCTEX_SKETCH_REPLICATE || sketch == OCTEX_SKETCH_SHARD || sketch == OCTEX_SKETCH_HOST,
                 "octex: unknown sketch placement");
   octex::load_params out;
   if (p.devices != nullptr && p.n_devices > 0) out.devices.assign(p.devices, p.devices + p.n_devices);
-  out.mode            = static_cast<octex::placement>(static_cast<int>(p.placement));
+  out.mode            = static_cast<octex::placement>(placement);
   out.vectors_on_host = p.vectors_on_host;
   out.shard_vectors   = p.shard_vectors;
   out.table_on_host   = p.table_on_host;
-  out.sketch          = static_cast<octex::sketch_placement>(static_cast<int>(p.sketch));
+  out.sketch          = static_cast<octex::sketch_placement>(sketch);
   out.parts           = p.parts;
   out.copies_per_part = p.copies_per_part;
   out.copies_limit    = p.copies_limit;

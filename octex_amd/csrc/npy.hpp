@@ -161,8 +161,9 @@ class npy_header_parser {
       if (peek() < '0' || peek() > '9') bad("expected a dimension");
       int64_t x = 0;
       while (peek() >= '0' && peek() <= '9') {  // every dimension below 2^62: no overflow here or in count()'s checks
-        x = x * 10 + (t_[i_++] - '0');
-        if (x >= (int64_t{1} << 62)) bad("a dimension of 2^62 or more");
+        const int digit = t_[i_++] - '0';
+        if (x > ((int64_t{1} << 62) - 1 - digit) / 10) bad("a dimension of 2^62 or more");  // checked before the step
+        x = x * 10 + digit;
       }
       if (peek() == 'L') i_++;
       v.push_back(x);

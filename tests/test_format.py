@@ -193,6 +193,8 @@ def npy_bytes(header, data=b"\0" * 64):
 @pytest.mark.parametrize("shape,match", [
     ("(4611686018427387904, 16)", r"malformed .npy header \(a dimension of 2\^62 or more\)"),
     ("(99999999999999999999999, 16)", r"malformed .npy header \(a dimension of 2\^62 or more\)"),
+    ("(9999999999999999999, 16)", r"malformed .npy header \(a dimension of 2\^62 or more\)"),  # 19 digits
+    ("(4611686018427387903, 1)", r"sketch.npy holds \d+ data bytes, its shape needs 4611686018427387903"),  # 2^62 - 1
     ("(4294967296, 4294967296, 16)", r"the shape's byte count overflows"),  # 2^68 elements: the count wraps
     ("(2305843009213693952, 4)", r"the shape's byte count overflows"),  # 2^63 elements x 1 byte
     ("(1152921504606846976, 16)", r"the shape's byte count overflows"),  # 2^64 bytes: wraps to zero
