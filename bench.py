@@ -27,6 +27,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor figure
+HOST_PATH_MAX_ROWS = 2_000_000  # the CPU oracle's build holds every copy's projection and an n^2 exact table pass
 
 # Cell lists, per workload (every BENCH line records its index parameters in config.index):
 # - sift1m: exact lists, as the reference's paper builds (bench/paper_build.sh:29, --exact-lists): 818 s to build here;
@@ -501,6 +502,11 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build searches on one GPU; runs on several GPUs are not part of it", file=sys.stderr)
+        sys.exit(2)
+    n_rows = args.n or CONFIGS[args.config]["n"]
+    if args.host_path and n_rows > HOST_PATH_MAX_ROWS:
+        print(f"bench.py: --host-path builds with the CPU oracle's builder, for at most {HOST_PATH_MAX_ROWS:,} rows "
+              f"(configs[0] has 100,000); this workload has {n_rows:,}", file=sys.stderr)
         sys.exit(2)
 
     if args.row_ceiling:

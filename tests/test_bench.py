@@ -71,6 +71,11 @@ def test_one_gpu_only():
     assert out.returncode != 0 and "one GPU" in (out.stdout + out.stderr)
 
 
+def test_host_path_refuses_large_workloads():
+    out = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--host-path"], capture_output=True, text=True)
+    assert out.returncode == 2 and "at most 2,000,000 rows" in out.stderr and "100,000,000" in out.stderr
+
+
 def test_every_workload_has_a_fixed_point():
     for name, cfg in bench.CONFIGS.items():
         if name == "small":
