@@ -3,8 +3,8 @@
  *
  * A plain C++ restatement of the reference's search arithmetic (cpp/src/neighbors/octex/detail/e8.cuh,
  * detail/search_kernels.cuh and search.cu) used only by tests/, __graft_entry__.smoke() and the
- * cpu_baseline leg of bench.py, as the checker of the HIP library and as the CPU baseline.  The
- * product (octex_amd/) never links, loads or calls it.
+ * cpu_baseline leg of bench.py, as the checker of the HIP library and as the CPU baseline (for the 100k-row
+ * CPU workload also its host build, orc_build).  The product (octex_amd/) never links, loads or calls it.
  *
  * Arithmetic pins (both here and in the HIP kernels), where the reference leaves the order to nvcc:
  *   - E8 distances da/dc:   t = x - a; acc = fma(t, t, acc)                 (e8.cuh:56-57)
