@@ -126,6 +126,9 @@ SWEEP_GIST = [
 
 SWEEP_HOST = [  # sketch-rank mode: the exact distances only in the final rerank, over the host link
     dict(read=16, starts=128, waves=3, rerank=128, wave_rerank=128, sketch_rank=True, final_rerank=32),
+    dict(read=16, starts=128, waves=4, rerank=128, wave_rerank=128, sketch_rank=True, final_rerank=32),
+    dict(read=16, starts=192, waves=3, rerank=128, wave_rerank=128, sketch_rank=True, final_rerank=32),
+    dict(read=16, starts=192, waves=4, rerank=128, wave_rerank=128, sketch_rank=True, final_rerank=32),
     dict(read=16, starts=256, waves=4, rerank=128, wave_rerank=128, sketch_rank=True, final_rerank=32),
     dict(read=16, starts=512, waves=5, rerank=128, wave_rerank=128, sketch_rank=True, final_rerank=32),
     dict(read=32, starts=512, waves=5, rerank=128, wave_rerank=128, sketch_rank=True, final_rerank=64),
